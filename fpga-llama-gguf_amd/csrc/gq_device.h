@@ -1,0 +1,181 @@
+// Device-side arithmetic shared by the gfx950 kernels: fp16 conversion, exp/log, reductions, fixed-point terms.
+// Every function here evaluates exactly the formula documented next to it, with no fused multiply-add except
+// where fmaf is written (the sources are compiled with -ffp-contract=off), so results are reproducible bit for bit.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gq {
+
+constexpr int WAVE = 64;
+
+// IEEE binary16 <-> binary32, round to nearest even; overflow gives infinity (gemvq_ref.h:16-52).
+__device__ __forceinline__ float h2f(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu, bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {
+            const int lz = __builtin_clz(m) - 21;  // shifts that bring the leading bit to position 10
+            m <<= lz;
+            bits = sign | (uint32_t(113 - lz) << 23) | ((m & 0x3ffu) << 13);
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7f800000u | (m << 13);
+    } else {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    return __uint_as_float(bits);
+}
+
+__device__ __forceinline__ uint32_t f2h(float f) {
+    const uint32_t bits = __float_as_uint(f);
+    const uint32_t sign = (bits >> 16) & 0x8000u;
+    const int e = int((bits >> 23) & 0xff) - 127 + 15;
+    uint32_t m = bits & 0x7fffffu;
+    if (e >= 31) return sign | 0x7c00u;
+    if (e <= 0) {
+        if (e < -10) return sign;
+        m |= 0x800000u;
+        const int sh = 14 - e;
+        uint32_t r = m >> sh;
+        const uint32_t rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1);
+        if (rem > half || (rem == half && (r & 1u))) ++r;
+        return sign | r;
+    }
+    uint32_t out = (uint32_t(e) << 10) | (m >> 13);
+    const uint32_t rem = m & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (out & 1u))) ++out;
+    return sign | out;
+}
+
+// exp: Cody-Waite reduction x = n ln2 + r (ln2 in a 15-bit and a low part), Taylor series of e^r to r^7/7! by
+// Horner with fused multiply-adds, exact scaling by 2^n; results below the normal range flush to +0.
+__device__ __forceinline__ float pow2i(int n) { return __uint_as_float(uint32_t(n + 127) << 23); }
+
+__device__ __forceinline__ float expf_(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return __builtin_inff();
+    if (x < -87.0f) return 0.0f;
+    const float n = __builtin_rintf(x * 1.44269504088896341f);
+    float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+    r = __builtin_fmaf(-n, 1.42860682030941723212e-6f, r);
+    float p = 1.0f / 5040.0f;
+    p = __builtin_fmaf(p, r, 1.0f / 720.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 120.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 24.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 6.0f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const int ni = int(n);
+    if (ni > 127) return (p * 2.0f) * pow2i(ni - 1);
+    return p * pow2i(ni);
+}
+
+// log for x > 0: x = m 2^e, m in [sqrt(1/2), sqrt(2)), log m = 2 atanh((m - 1) / (m + 1)) to s^9 / 9.
+__device__ __forceinline__ float logf_(float x) {
+    if (x != x || x < 0.0f) return __builtin_nanf("");
+    if (x == 0.0f) return -__builtin_inff();
+    if (x == __builtin_inff()) return x;
+    uint32_t b = __float_as_uint(x);
+    int e;
+    if ((b >> 23) == 0) {
+        b = __float_as_uint(x * 8388608.0f);
+        e = int(b >> 23) - 150;
+    } else {
+        e = int(b >> 23) - 127;
+    }
+    float m = __uint_as_float((b & 0x7fffffu) | 0x3f800000u);
+    if (m > 1.41421353816986083984f) {
+        m = m * 0.5f;
+        e += 1;
+    }
+    const float f = m - 1.0f;
+    const float s = f / (2.0f + f);
+    const float s2 = s * s;
+    float p = 1.0f / 9.0f;
+    p = __builtin_fmaf(p, s2, 1.0f / 7.0f);
+    p = __builtin_fmaf(p, s2, 1.0f / 5.0f);
+    p = __builtin_fmaf(p, s2, 1.0f / 3.0f);
+    p = p * s2;
+    const float two_s = 2.0f * s;
+    const float logm = __builtin_fmaf(two_s, p, two_s);
+    const float ef = float(e);
+    return __builtin_fmaf(ef, 0.693145751953125f, __builtin_fmaf(ef, 1.42860682030941723212e-6f, logm));
+}
+
+// ggml forms (gemvqc_ops.h:64-99): SiLU x / (1 + e^-x), sigmoid 1 / (1 + e^-x), softplus x > 20 ? x : log(1 + e^x).
+__device__ __forceinline__ float silu_(float x) { return x / (1.0f + expf_(-x)); }
+__device__ __forceinline__ float sigmoid_(float x) { return 1.0f / (1.0f + expf_(-x)); }
+__device__ __forceinline__ float softplus_(float x) { return x > 20.0f ? x : logf_(1.0f + expf_(x)); }
+
+// Pairwise (adjacent-pair tree) sums. Lane l holds element l of an aligned group of `width` lanes: after the xor
+// steps 1, 2, 4, .. every lane of the group holds the tree sum (a + b == b + a bitwise, so both lanes of a pair agree).
+template <int WIDTH>
+__device__ __forceinline__ float pair_sum_lanes(float v) {
+#pragma unroll
+    for (int s = 1; s < WIDTH; s <<= 1) v = v + __shfl_xor(v, s, WAVE);
+    return v;
+}
+
+// In-register adjacent tree of N (power of two) consecutive elements.
+template <int N>
+__device__ __forceinline__ float tree(float * v) {
+#pragma unroll
+    for (int s = 1; s < N; s <<= 1)
+#pragma unroll
+        for (int i = 0; i < N; i += 2 * s) v[i] = v[i] + v[i + s];
+    return v[0];
+}
+
+__device__ __forceinline__ long long wave_sum_i64(long long v) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) v += __shfl_xor(v, s, WAVE);
+    return v;
+}
+
+__device__ __forceinline__ int sum_lanes4_i32(int v) {
+    v += __shfl_xor(v, 1, WAVE);
+    v += __shfl_xor(v, 2, WAVE);
+    return v;
+}
+
+// Fixed-point term of the reference kernel (gemvqw_engine.h:352-445): floor(s * m * 2^(e + 40)) for the signed
+// integer s times the significand product m and the power of two e; LSB of the accumulator is 2^-40.
+__device__ __forceinline__ long long fixed_term(long long p, int e) {
+    const int sh = e + 40;
+    return sh >= 0 ? (long long)((unsigned long long)p << (sh < 63 ? sh : 63)) : (p >> (-sh < 63 ? -sh : 63));
+}
+
+// fp16 bits -> (significand, exponent): value = m * 2^e (subnormals: raw fraction, e = -24).
+__device__ __forceinline__ void half_parts(uint32_t h, int & m, int & e) {
+    const int ex = (h >> 10) & 31, f = h & 1023;
+    m = ex == 0 ? f : (f | 1024);
+    e = ex == 0 ? -24 : ex - 25;
+}
+
+// FP32 -> (significand, exponent); FP32 subnormals count as zero (gemvqw_engine.h:385-394).
+__device__ __forceinline__ void float_parts(float v, int & m, int & e) {
+    const uint32_t b = __float_as_uint(v);
+    const int ex = (b >> 23) & 255;
+    m = ex == 0 ? 0 : int((b & 0x7fffffu) | 0x800000u);
+    e = ex - 150;
+}
+
+// The accumulator (LSB 2^-40) rounded to FP32 once (int64 -> FP32 rounds to nearest even; the scaling is exact).
+__device__ __forceinline__ float fixed_to_float(long long acc) { return float(acc) * 9.094947017729282379e-13f; }
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4(int(a), int(b), c, false);
+}
+
+// Orderable key of (value, index): larger value wins, then the smaller index (ggml argmax keeps the first).
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
+    uint32_t b = __float_as_uint(v);
+    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)b << 32) | (0xffffffffu - idx);
+}
+
+}  // namespace gq

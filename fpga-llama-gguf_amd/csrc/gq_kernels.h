@@ -1,0 +1,208 @@
+// Launch descriptors of the gfx950 kernels (shared by the kernels and the host command processor).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gq {
+
+enum : int { T_Q4_0 = 2, T_Q8_0 = 8, T_Q5_K = 13, T_Q6_K = 14 };
+
+// Repacked weight layout (layout only, original bits): the GGUF block fields of all rows split into
+// field-major regions, each row-major, so that lane l of a wave reads unit l of a row from consecutive bytes.
+//   Q4_0: qs[rows][nb][16], d[rows][nb] (u16)
+//   Q8_0: qs_lo[rows][nb][16] (bytes 0..15 of each block's quants), qs_hi[rows][nb][16], d[rows][nb]
+//   Q5_K: qs[rows][nsb][128], qh[rows][nsb][32], meta[rows][nsb][16] (d, dmin, 12 scale bytes)
+//   Q6_K: ql[rows][nsb][128], qh[rows][nsb][64], sc[rows][nsb][16], d[rows][nsb] (u16)
+struct WeightView {
+    const uint8_t * a;  // first region
+    const uint8_t * b;
+    const uint8_t * c;
+    const uint8_t * d;
+};
+
+enum : int { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_ADD = 2, EPI_CONV = 3 };
+enum : int { XSRC_RAW = 0, XSRC_NORM = 1 };
+
+struct GemvMember {
+    WeightView w;    // matrix (g of a SwiGLU pair)
+    WeightView w2;   // u of a SwiGLU pair
+    float * y;
+    const float * res;        // ADD residual
+    const float * conv_src;   // CONV state [rows][3]
+    float * conv_dst;
+    const float * conv_w;     // CONV kernel [rows][4]
+    int rows;
+    int task_begin;
+    int epi;
+    int conv_silu;
+};
+
+struct GemvArgs {
+    const float * x;          // activation (act + x_off)
+    const float * norm_w;     // deferred norm weight (NULL: no weight)
+    float norm_eps;
+    int xsrc;                 // XSRC_RAW or XSRC_NORM
+    int norm_l2;
+    int cols;
+    int n_members;
+    int total_tasks;
+    GemvMember m[4];
+    unsigned long long * argmax_key;  // non-NULL: argmax over member 0's y
+    int32_t * dbg;                    // non-NULL: integer block sums of member 0
+};
+
+struct NormArgs {
+    const float * x;
+    const float * w;
+    float * y;
+    int n, rows, stride;  // stride in floats
+    float eps;
+    int flags;
+};
+
+enum : int { EW_ADD = 0, EW_MUL = 1, EW_SILU_MUL = 2, EW_SIGMOID_MUL = 3, EW_SILU = 4, EW_SIGMOID = 5,
+             EW_SOFTPLUS = 6, EW_COPY = 7, EW_FILL = 8 };
+
+struct EwArgs {
+    const float * a;   // first operand (g for SILU_MUL, x for UNARY)
+    const float * b;   // second operand (u for SILU_MUL)
+    float * y;
+    int n;
+    int row, stride;   // a is rows of `row` floats every `stride` floats (row 0: contiguous)
+    int op;
+    float value;       // FILL
+};
+
+struct ConvArgs {
+    const float * x;
+    const float * w;
+    const float * s_src;
+    float * s_dst;
+    float * y;
+    int ch;
+    int silu;
+};
+
+struct RopeArgs {
+    const float * x;
+    const float * cs;     // n_dims floats, or a table with n_dims floats per position
+    const int32_t * pos;  // non-NULL: row of the table
+    float * y;
+    int n_dims, ne0, rows;
+};
+
+struct GdnArgs {
+    const float * q;
+    const float * k;
+    const float * v;
+    const float * g;      // log decay, or alpha raw with gates
+    const float * beta;   // beta, or beta raw with gates
+    const float * dt;
+    const float * a;
+    float * y;
+    const float * src;    // state rows (128 floats each), head h row j at (h * 128 + j) * 128
+    float * dst;
+    int hv, hk;
+    float scale, l2_eps;
+    int flags;
+};
+
+struct GatedNormArgs {    // per head of 128: y = silu(z) * ((y * s) * w), s = 1 / sqrt(mean(y^2) + eps)
+    float * y;
+    const float * z;
+    const float * w;
+    int heads;
+    float eps;
+};
+
+struct AttnArgs {
+    const float * q;      // q rows
+    const float * k;      // new key rows (n_head_kv x head_dim)
+    const float * v;
+    const float * qn;     // q norm weight (head_dim)
+    const float * kn;
+    const float * cs;     // cos/sin table, n_rot floats per position
+    const int32_t * pos;
+    const float * gate;   // NULL or gate rows (stride 2 * head_dim)
+    float * y;
+    uint16_t * kc;        // [n_ctx][n_head_kv][head_dim]
+    uint16_t * vc;
+    float * part;         // partials: [n_head][max_chunks][2 + head_dim]
+    unsigned int * counter;  // [n_head_kv]
+    int n_head, n_head_kv, head_dim, n_rot, q_stride, n_ctx;
+    float scale, eps;
+};
+
+struct GetRowsArgs {
+    WeightView w;
+    const int32_t * id;
+    float * y;
+    int rows, cols, type;
+};
+
+struct NextTokenArgs {
+    unsigned long long * key;
+    int32_t * tok;
+    int32_t * pos;
+    const int32_t * prompt;
+    int n_prompt;
+    int32_t * out;
+    int max_pos;
+};
+
+constexpr int ATTN_CHUNK = 64;
+
+hipError_t launch_gemv(const GemvArgs & a, int type, hipStream_t s);
+hipError_t launch_norm(const NormArgs & a, hipStream_t s);
+hipError_t launch_ew(const EwArgs & a, hipStream_t s);
+hipError_t launch_conv(const ConvArgs & a, hipStream_t s);
+hipError_t launch_rope(const RopeArgs & a, hipStream_t s);
+hipError_t launch_gdn(const GdnArgs & a, hipStream_t s);
+hipError_t launch_gated_norm(const GatedNormArgs & a, hipStream_t s);
+hipError_t launch_attn(const AttnArgs & a, hipStream_t s);
+hipError_t launch_get_rows(const GetRowsArgs & a, hipStream_t s);
+hipError_t launch_argmax(const float * x, int n, unsigned long long * key, hipStream_t s);
+hipError_t launch_next_token(const NextTokenArgs & a, hipStream_t s);
+
+// Layout helpers (host and device).
+__host__ __device__ inline size_t gguf_row_bytes(int type, int cols) {
+    switch (type) {
+    case T_Q4_0: return size_t(cols / 32) * 18;
+    case T_Q8_0: return size_t(cols / 32) * 34;
+    case T_Q5_K: return size_t(cols / 256) * 176;
+    case T_Q6_K: return size_t(cols / 256) * 210;
+    default: return 0;
+    }
+}
+
+__host__ __device__ inline WeightView weight_view(const uint8_t * base, int type, int rows, int cols) {
+    WeightView v;
+    const size_t R = size_t(rows);
+    if (type == T_Q4_0) {
+        const size_t nb = size_t(cols / 32);
+        v.a = base;
+        v.b = base + R * nb * 16;
+        v.c = v.d = nullptr;
+    } else if (type == T_Q8_0) {
+        const size_t nb = size_t(cols / 32);
+        v.a = base;
+        v.b = base + R * nb * 16;
+        v.c = base + R * nb * 32;
+        v.d = nullptr;
+    } else if (type == T_Q5_K) {
+        const size_t ns = size_t(cols / 256);
+        v.a = base;
+        v.b = base + R * ns * 128;
+        v.c = base + R * ns * 160;
+        v.d = nullptr;
+    } else {
+        const size_t ns = size_t(cols / 256);
+        v.a = base;
+        v.b = base + R * ns * 128;
+        v.c = base + R * ns * 192;
+        v.d = base + R * ns * 208;
+    }
+    return v;
+}
+
+}  // namespace gq

@@ -1,0 +1,455 @@
+// Non-GEMV kernels of the decode command stream for gfx950: row norms, element-wise ops, conv, RoPE, the Gated
+// DeltaNet step, its gated output norm, the attention core, embedding rows, argmax and the greedy token step.
+// Reductions follow the pairwise tree over element indices; see gq_device.h for the scalar arithmetic.
+#include "gq_device.h"
+#include "gq_kernels.h"
+
+namespace gq {
+namespace {
+
+// ---- RMSNORM opcode (gemvqc_ops.h:169-234): one workgroup of 256 per row ----
+__global__ __launch_bounds__(256) void norm_kernel(NormArgs a) {
+    __shared__ float red[4];
+    const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float * x = a.x + size_t(r) * a.stride;
+    const int nw = a.n / 16, rounds = (nw + 255) / 256;  // n <= 16384: at most 4 rounds
+    float rs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        if (g >= rounds) break;
+        const int w = g * 256 + tid;
+        float ws = 0.0f;
+        if (w < nw) {
+            float sq[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float v = x[16 * w + i];
+                sq[i] = v * v;
+            }
+            ws = tree<16>(sq);
+        }
+        ws = pair_sum_lanes<64>(ws);
+        if (lane == 0) red[wave] = ws;
+        __syncthreads();
+        rs[g] = (red[0] + red[1]) + (red[2] + red[3]);
+        __syncthreads();
+    }
+    const float sum = (rs[0] + rs[1]) + (rs[2] + rs[3]);
+    const float s = (a.flags & 1) ? 1.0f / fmaxf(sqrtf(sum), a.eps) : 1.0f / sqrtf(sum / float(a.n) + a.eps);
+    float * y = a.y + size_t(r) * a.n;
+    for (int i = tid; i < a.n; i += 256) y[i] = (a.flags & 2) ? x[i] * s : (x[i] * s) * a.w[i];
+}
+
+// ---- element-wise (gemvqc_ops.h:314-385) ----
+__global__ void ew_kernel(EwArgs a) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += gridDim.x * blockDim.x) {
+        const float av = a.op == EW_FILL ? 0.0f
+                       : a.row ? a.a[size_t(i / a.row) * a.stride + i % a.row] : a.a[i];
+        float r;
+        switch (a.op) {
+        case EW_ADD: r = av + a.b[i]; break;
+        case EW_MUL: r = av * a.b[i]; break;
+        case EW_SILU_MUL: r = (av / (1.0f + expf_(-av))) * a.b[i]; break;
+        case EW_SIGMOID_MUL: r = (1.0f / (1.0f + expf_(-av))) * a.b[i]; break;
+        case EW_SILU: r = silu_(av); break;
+        case EW_SIGMOID: r = sigmoid_(av); break;
+        case EW_SOFTPLUS: r = softplus_(av); break;
+        case EW_COPY: r = av; break;
+        default: r = a.value; break;
+        }
+        a.y[i] = r;
+    }
+}
+
+// ---- CONV opcode (gemvqc_ops.h:387-431): window [state (3), x], summed from t = 0 ----
+__global__ void conv_kernel(ConvArgs a) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= a.ch) return;
+    const float s0 = a.s_src[3 * c], s1 = a.s_src[3 * c + 1], s2 = a.s_src[3 * c + 2], x = a.x[c];
+    float sum = 0.0f;
+    sum += s0 * a.w[4 * c];
+    sum += s1 * a.w[4 * c + 1];
+    sum += s2 * a.w[4 * c + 2];
+    sum += x * a.w[4 * c + 3];
+    a.y[c] = a.silu ? silu_(sum) : sum;
+    a.s_dst[3 * c] = s1;
+    a.s_dst[3 * c + 1] = s2;
+    a.s_dst[3 * c + 2] = x;
+}
+
+// ---- ROPE opcode (gemvqc_ops.h:275-312): NEOX pairs (i, i + n_dims / 2) ----
+__global__ void rope_kernel(RopeArgs a) {
+    const int r = blockIdx.x;
+    const float * cs = a.pos ? a.cs + size_t(*a.pos) * a.n_dims : a.cs;
+    const float * x = a.x + size_t(r) * a.ne0;
+    float * y = a.y + size_t(r) * a.ne0;
+    const int half = a.n_dims / 2, i = threadIdx.x;  // blockDim.x >= ne0
+    float out = 0.0f;
+    if (i < a.ne0) {
+        if (i < half) {
+            out = x[i] * cs[2 * i] - x[i + half] * cs[2 * i + 1];
+        } else if (i < a.n_dims) {
+            const int j = i - half;
+            out = x[j] * cs[2 * j + 1] + x[i] * cs[2 * j];
+        } else {
+            out = x[i];
+        }
+    }
+    __syncthreads();  // y may be x
+    if (i < a.ne0) y[i] = out;
+}
+
+// ---- GDN step (gemvqc_gdn.h:73-187 with the input load of :223-281) ----
+// Workgroup (value head h, chunk of 32 state rows), 128 threads: 16 lanes per row, 8 consecutive floats per lane.
+constexpr int GDN_ROWS = 32;
+__global__ __launch_bounds__(128) void gdn_kernel(GdnArgs a) {
+    const int chunks = 128 / GDN_ROWS;
+    const int h = blockIdx.x / chunks, chunk = blockIdx.x % chunks, kh = h % a.hk;
+    const int l16 = threadIdx.x & 15, grp = threadIdx.x >> 4;  // 8 row groups
+    float q[8], k[8];
+    {
+        const float4 * qp = reinterpret_cast<const float4 *>(a.q + kh * 128 + 8 * l16);
+        const float4 * kp = reinterpret_cast<const float4 *>(a.k + kh * 128 + 8 * l16);
+        const float4 q0 = qp[0], q1 = qp[1], k0 = kp[0], k1 = kp[1];
+        q[0] = q0.x; q[1] = q0.y; q[2] = q0.z; q[3] = q0.w; q[4] = q1.x; q[5] = q1.y; q[6] = q1.z; q[7] = q1.w;
+        k[0] = k0.x; k[1] = k0.y; k[2] = k0.z; k[3] = k0.w; k[4] = k1.x; k[5] = k1.y; k[6] = k1.z; k[7] = k1.w;
+    }
+    if (a.flags & 2) {  // L2 norm of q and k per key head (ggml_l2_norm)
+        float sq[8], sk[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            sq[i] = q[i] * q[i];
+            sk[i] = k[i] * k[i];
+        }
+        const float tq = pair_sum_lanes<16>(tree<8>(sq)), tk = pair_sum_lanes<16>(tree<8>(sk));
+        const float fq = 1.0f / fmaxf(sqrtf(tq), a.l2_eps), fk = 1.0f / fmaxf(sqrtf(tk), a.l2_eps);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            q[i] = q[i] * fq;
+            k[i] = k[i] * fk;
+        }
+    }
+    float gv = a.g[h], bt = a.beta[h];
+    if (a.flags & 8) {  // gates from the raw projections: beta = sigmoid(b), g = softplus(a_raw + dt) * a
+        gv = softplus_(a.g[h] + a.dt[h]) * a.a[h];
+        bt = sigmoid_(a.beta[h]);
+    }
+    const float decay = expf_(gv);
+    for (int it = 0; it < GDN_ROWS / 8; ++it) {
+        const int j = chunk * GDN_ROWS + it * 8 + grp;
+        const size_t row = (size_t(h) * 128 + j) * 128 + 8 * l16;
+        const float4 s0 = *reinterpret_cast<const float4 *>(a.src + row);
+        const float4 s1 = *reinterpret_cast<const float4 *>(a.src + row + 4);
+        float x[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        float pr[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            x[i] = x[i] * decay;
+            pr[i] = x[i] * k[i];
+        }
+        const float dot = pair_sum_lanes<16>(tree<8>(pr));
+        const float delta = (a.v[h * 128 + j] - dot) * bt;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            x[i] = x[i] + k[i] * delta;
+            pr[i] = x[i] * q[i];
+        }
+        const float out = pair_sum_lanes<16>(tree<8>(pr));
+        *reinterpret_cast<float4 *>(a.dst + row) = make_float4(x[0], x[1], x[2], x[3]);
+        *reinterpret_cast<float4 *>(a.dst + row + 4) = make_float4(x[4], x[5], x[6], x[7]);
+        if (l16 == 0) a.y[h * 128 + j] = out * a.scale;
+    }
+}
+
+// ---- gated output norm (gemvqc_gdn.h:284-346): one wave per head, lane l holds elements 2l, 2l + 1 ----
+__global__ __launch_bounds__(64) void gated_norm_kernel(GatedNormArgs a) {
+    const int h = blockIdx.x, l = threadIdx.x;
+    float * y = a.y + h * 128;
+    const float y0 = y[2 * l], y1 = y[2 * l + 1];
+    const float sum = pair_sum_lanes<64>(y0 * y0 + y1 * y1);
+    const float s = 1.0f / sqrtf(sum / 128.0f + a.eps);
+    const float z0 = a.z[h * 128 + 2 * l], z1 = a.z[h * 128 + 2 * l + 1];
+    const float o0 = silu_(z0) * ((y0 * s) * a.w[2 * l]);
+    const float o1 = silu_(z1) * ((y1 * s) * a.w[2 * l + 1]);
+    y[2 * l] = o0;
+    y[2 * l + 1] = o1;
+}
+
+// ---- attention core (one token, GQA, fp16 KV) ----
+// Workgroup (KV head, chunk of 64 positions), 256 threads. Each workgroup normalizes and rotates its q heads and
+// the new key, scores its positions (pairwise over head_dim, 4 dims per lane), runs the chunk's softmax part
+// (max, e^(s - max), sequential sums over positions), writes the partials; the last workgroup of a KV head
+// combines the chunks in order and applies the sigmoid output gate.
+constexpr int ATT_T = 256;
+constexpr int MAXHD = 256;
+constexpr int MAXG = 8;
+
+__device__ float head_norm_scale(const float * v, int hd, float eps, float * red) {
+    // pairwise over hd (<= 256): lane l of wave 0..3 holds element tid (one element per thread)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float e = tid < hd ? v[tid] : 0.0f;
+    const float t = pair_sum_lanes<64>(e * e);
+    if (lane == 0) red[wave] = t;
+    __syncthreads();
+    const float sum = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return 1.0f / sqrtf(sum / float(hd) + eps);
+}
+
+__global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
+    __shared__ float qs[MAXG][MAXHD];      // fp16-rounded q of the group's heads
+    __shared__ float kcur[MAXHD], vcur[MAXHD];
+    __shared__ float tmp[MAXHD];
+    __shared__ float sc[MAXG][ATTN_CHUNK];
+    __shared__ float red[4];
+    __shared__ float mx[MAXG], lsum[MAXG];
+    __shared__ int last;
+    const int kvh = blockIdx.x % a.n_head_kv, chunk = blockIdx.x / a.n_head_kv;
+    const int pos = *a.pos, nc = (pos + ATTN_CHUNK) / ATTN_CHUNK;
+    if (chunk >= nc) return;
+    const int tid = threadIdx.x, hd = a.head_dim, G = a.n_head / a.n_head_kv, half = a.n_rot / 2;
+    const float * cs = a.cs + size_t(pos) * a.n_rot;
+    // q heads of the group: RMS norm with weight, NEOX RoPE on the first n_rot dims, fp16 rounding.
+    for (int g = 0; g < G; ++g) {
+        const int h = kvh * G + g;
+        const float * qr = a.q + size_t(h) * a.q_stride;
+        const float s = head_norm_scale(qr, hd, a.eps, red);
+        if (tid < hd) tmp[tid] = (qr[tid] * s) * a.qn[tid];
+        __syncthreads();
+        if (tid < hd) {
+            float o = tmp[tid];
+            if (tid < half) o = tmp[tid] * cs[2 * tid] - tmp[tid + half] * cs[2 * tid + 1];
+            else if (tid < a.n_rot) o = tmp[tid - half] * cs[2 * (tid - half) + 1] + tmp[tid] * cs[2 * (tid - half)];
+            qs[g][tid] = h2f(f2h(o));
+        }
+        __syncthreads();
+    }
+    // the new key and value of this KV head
+    {
+        const float * kr = a.k + size_t(kvh) * hd;
+        const float s = head_norm_scale(kr, hd, a.eps, red);
+        if (tid < hd) tmp[tid] = (kr[tid] * s) * a.kn[tid];
+        __syncthreads();
+        if (tid < hd) {
+            float o = tmp[tid];
+            if (tid < half) o = tmp[tid] * cs[2 * tid] - tmp[tid + half] * cs[2 * tid + 1];
+            else if (tid < a.n_rot) o = tmp[tid - half] * cs[2 * (tid - half) + 1] + tmp[tid] * cs[2 * (tid - half)];
+            const uint32_t kb = f2h(o), vb = f2h(a.v[size_t(kvh) * hd + tid]);
+            kcur[tid] = h2f(kb);
+            vcur[tid] = h2f(vb);
+            if (chunk == nc - 1) {
+                const size_t off = (size_t(pos) * a.n_head_kv + kvh) * hd + tid;
+                a.kc[off] = uint16_t(kb);
+                a.vc[off] = uint16_t(vb);
+            }
+        }
+        __syncthreads();
+    }
+    // scores: wave w takes positions t0 + w, t0 + w + 4, ...; lane l holds dims 4l .. 4l + 3
+    const int t0 = chunk * ATTN_CHUNK, t1 = min(t0 + ATTN_CHUNK, pos + 1), nt = t1 - t0;
+    const int lane = tid & 63, wave = tid >> 6;
+    for (int ti = wave; ti < nt; ti += 4) {
+        const int t = t0 + ti;
+        float kv4[4];
+        if (t == pos) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) kv4[i] = 4 * lane + i < hd ? kcur[4 * lane + i] : 0.0f;
+        } else {
+            const uint16_t * kp = a.kc + (size_t(t) * a.n_head_kv + kvh) * hd;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) kv4[i] = 4 * lane + i < hd ? h2f(kp[4 * lane + i]) : 0.0f;
+        }
+        for (int g = 0; g < G; ++g) {
+            float pr[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pr[i] = 4 * lane + i < hd ? qs[g][4 * lane + i] * kv4[i] : 0.0f;
+            const float dot = pair_sum_lanes<64>(tree<4>(pr));
+            if (lane == 0) sc[g][ti] = dot * a.scale;
+        }
+    }
+    __syncthreads();
+    // chunk max and e^(s - max), sum over positions in order
+    if (tid < G) {
+        float m = sc[tid][0];
+        for (int i = 1; i < nt; ++i) m = fmaxf(m, sc[tid][i]);
+        float l = 0.0f;
+        for (int i = 0; i < nt; ++i) {
+            const float p = expf_(sc[tid][i] - m);
+            sc[tid][i] = p;
+            l += p;
+        }
+        mx[tid] = m;
+        lsum[tid] = l;
+    }
+    __syncthreads();
+    // o[g][d] = sum over positions in order of p * v
+    const int pstride = 2 + hd, nchmax = (a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
+    for (int od = tid; od < G * hd; od += ATT_T) {
+        const int g = od / hd, d = od % hd;
+        float o = 0.0f;
+        for (int i = 0; i < nt; ++i) {
+            const int t = t0 + i;
+            const float vv = t == pos ? vcur[d] : h2f(a.vc[(size_t(t) * a.n_head_kv + kvh) * hd + d]);
+            o += sc[g][i] * vv;
+        }
+        float * pp = a.part + (size_t(kvh * G + g) * nchmax + chunk) * pstride;
+        pp[2 + d] = o;
+        if (d == 0) {
+            pp[0] = mx[g];
+            pp[1] = lsum[g];
+        }
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last = atomicAdd(a.counter + kvh, 1u) == unsigned(nc - 1);
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    for (int od = tid; od < G * hd; od += ATT_T) {
+        const int g = od / hd, d = od % hd, h = kvh * G + g;
+        const float * pp = a.part + size_t(h) * nchmax * pstride;
+        float M = __builtin_nontemporal_load(pp);
+        for (int c = 1; c < nc; ++c) M = fmaxf(M, __builtin_nontemporal_load(pp + size_t(c) * pstride));
+        float L = 0.0f, O = 0.0f;
+        for (int c = 0; c < nc; ++c) {
+            const float * pc = pp + size_t(c) * pstride;
+            const float f = expf_(__builtin_nontemporal_load(pc) - M);
+            L += __builtin_nontemporal_load(pc + 1) * f;
+            O += __builtin_nontemporal_load(pc + 2 + d) * f;
+        }
+        float out = O / L;
+        if (a.gate) {
+            const float gt = a.gate[size_t(h) * 2 * hd + d];
+            out = (1.0f / (1.0f + expf_(-gt))) * out;
+        }
+        a.y[size_t(h) * hd + d] = out;
+    }
+    if (tid == 0) a.counter[kvh] = 0u;
+}
+
+// ---- embedding rows (ggml dequantize_row_*) ----
+__global__ void get_rows_kernel(GetRowsArgs a) {
+    const int id = *a.id;
+    if (id < 0 || id >= a.rows) return;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < a.cols; i += gridDim.x * blockDim.x) {
+        float y;
+        if (a.type == T_Q6_K) {
+            const int nsb = a.cols / 256, sb = i / 256, e = i % 256;
+            const size_t sbi = size_t(id) * nsb + sb;
+            const int n = e / 128, r = e % 128, quarter = r / 32, l = r % 32;
+            const uint8_t ql = a.w.a[sbi * 128 + 64 * n + l + 32 * (quarter & 1)];
+            const uint8_t qh = a.w.b[sbi * 64 + 32 * n + l];
+            const int lo = quarter < 2 ? (ql & 0xF) : (ql >> 4);
+            const int q = (lo | (((qh >> (2 * quarter)) & 3) << 4)) - 32;
+            const int8_t scv = int8_t(a.w.c[sbi * 16 + e / 16]);
+            const float d = h2f(*reinterpret_cast<const uint16_t *>(a.w.d + sbi * 2));
+            y = (d * float(scv)) * float(q);
+        } else if (a.type == T_Q4_0) {
+            const int nb = a.cols / 32, b = i / 32, j = i % 32;
+            const size_t bi = size_t(id) * nb + b;
+            const uint8_t byte = a.w.a[bi * 16 + (j & 15)];
+            const int q = (j < 16 ? (byte & 15) : (byte >> 4)) - 8;
+            y = float(q) * h2f(*reinterpret_cast<const uint16_t *>(a.w.b + bi * 2));
+        } else {  // Q8_0
+            const int nb = a.cols / 32, b = i / 32, j = i % 32;
+            const size_t bi = size_t(id) * nb + b;
+            const int8_t q = int8_t(j < 16 ? a.w.a[bi * 16 + j] : a.w.b[bi * 16 + j - 16]);
+            y = float(q) * h2f(*reinterpret_cast<const uint16_t *>(a.w.c + bi * 2));
+        }
+        a.y[i] = y;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(const float * x, int n, unsigned long long * key) {
+    __shared__ unsigned long long red[4];
+    unsigned long long best = 0;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+        const unsigned long long k = argmax_key(x[i], uint32_t(i));
+        best = k > best ? k : best;
+    }
+    for (int s = 32; s >= 1; s >>= 1) {
+        const unsigned long long o = __shfl_xor(best, s, WAVE);
+        best = o > best ? o : best;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long b = red[0];
+        for (int i = 1; i < 4; ++i) b = red[i] > b ? red[i] : b;
+        atomicMax(key, b);
+    }
+}
+
+__global__ void next_token_kernel(NextTokenArgs a) {
+    const int pos = *a.pos;
+    const unsigned long long k = *a.key;
+    int tok = int(0xffffffffu - uint32_t(k & 0xffffffffu));
+    if (pos + 1 < a.n_prompt) tok = a.prompt[pos + 1];
+    if (pos + 1 < a.max_pos) a.out[pos + 1] = tok;
+    *a.tok = tok;
+    *a.pos = pos + 1;
+    *a.key = 0ull;
+}
+
+}  // namespace
+
+hipError_t launch_norm(const NormArgs & a, hipStream_t s) {
+    hipLaunchKernelGGL(norm_kernel, dim3(a.rows), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_ew(const EwArgs & a, hipStream_t s) {
+    int grid = (a.n + 255) / 256;
+    grid = grid < 1024 ? grid : 1024;
+    hipLaunchKernelGGL(ew_kernel, dim3(grid), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv(const ConvArgs & a, hipStream_t s) {
+    hipLaunchKernelGGL(conv_kernel, dim3((a.ch + 255) / 256), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(const RopeArgs & a, hipStream_t s) {
+    if (a.ne0 > 1024) return hipErrorInvalidValue;
+    const int t = ((a.ne0 + 63) / 64) * 64;
+    hipLaunchKernelGGL(rope_kernel, dim3(a.rows), dim3(t), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn(const GdnArgs & a, hipStream_t s) {
+    hipLaunchKernelGGL(gdn_kernel, dim3(a.hv * (128 / GDN_ROWS)), dim3(128), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gated_norm(const GatedNormArgs & a, hipStream_t s) {
+    hipLaunchKernelGGL(gated_norm_kernel, dim3(a.heads), dim3(64), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn(const AttnArgs & a, hipStream_t s) {
+    if (a.head_dim > MAXHD || a.head_dim % 4 || a.n_head % a.n_head_kv || a.n_head / a.n_head_kv > MAXG)
+        return hipErrorInvalidValue;
+    const int nch = (a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
+    hipLaunchKernelGGL(attn_kernel, dim3(a.n_head_kv * nch), dim3(ATT_T), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_get_rows(const GetRowsArgs & a, hipStream_t s) {
+    hipLaunchKernelGGL(get_rows_kernel, dim3((a.cols + 255) / 256), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float * x, int n, unsigned long long * key, hipStream_t s) {
+    int grid = (n + 255) / 256;
+    grid = grid < 256 ? grid : 256;
+    hipLaunchKernelGGL(argmax_kernel, dim3(grid), dim3(256), 0, s, x, n, key);
+    return hipGetLastError();
+}
+
+hipError_t launch_next_token(const NextTokenArgs & a, hipStream_t s) {
+    hipLaunchKernelGGL(next_token_kernel, dim3(1), dim3(1), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace gq

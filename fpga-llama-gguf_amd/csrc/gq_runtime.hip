@@ -1,0 +1,853 @@
+// Host side of the MI355X decode backend: device buffers, the load-time weight repack, the command processor that
+// validates a command list and fuses it into kernel launches (the role of gemvqc16's run_list,
+// fpga/src/gemvqc16.cpp:552-958, moved to the host because a GPU launch sequence can be captured once), and the
+// hipGraph capture and replay of per-token lists. C ABI in include/gemvq_hip.h.
+#include "gemvq_hip.h"
+#include "gq_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <variant>
+#include <vector>
+
+using namespace gq;
+
+namespace {
+
+struct Weight {
+    int type, rows, cols;
+    size_t bytes;
+};
+
+struct KvBuf {
+    uint16_t * k = nullptr;
+    uint16_t * v = nullptr;
+    float * part = nullptr;
+    unsigned * counter = nullptr;
+    int n_ctx = 0, n_head_kv = 0, head_dim = 0;
+};
+
+struct LGemv { GemvArgs a; int type; };
+struct LNorm { NormArgs a; };
+struct LEw { EwArgs a; };
+struct LConv { ConvArgs a; };
+struct LRope { RopeArgs a; };
+struct LGdn { GdnArgs a; };
+struct LGated { GatedNormArgs a; };
+struct LAttn { AttnArgs a; };
+struct LRows { GetRowsArgs a; };
+struct LArgmax { const float * x; int n; unsigned long long * key; };
+struct LNext { NextTokenArgs a; };
+using Launch = std::variant<LGemv, LNorm, LEw, LConv, LRope, LGdn, LGated, LAttn, LRows, LArgmax, LNext>;
+
+}  // namespace
+
+struct gemvq_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    float * act = nullptr;
+    size_t act_floats = 0;
+    uint8_t * warena = nullptr;
+    size_t wbytes = 0, wused = 0;
+    float * state = nullptr;
+    size_t state_rows = 0;
+    std::map<uint64_t, Weight> weights;
+    std::vector<KvBuf> kvs;
+    std::vector<hipGraphExec_t> graphs;
+    std::vector<hipGraph_t> graph_defs;
+    int32_t * dbg = nullptr;      // device buffer of the armed block-sum dump
+    size_t dbg_n = 0;
+    int32_t * dbg_dst = nullptr;  // host destination; non-NULL while armed
+    bool dbg_used = false;        // the list being compiled writes the dump
+    int last_launches = 0;
+    std::string err;
+};
+
+static std::string g_create_error;
+
+namespace {
+
+int fail(gemvq_ctx * c, hipError_t e, const char * what) {
+    if (c) c->err = std::string(what) + ": " + hipGetErrorString(e);
+    return -int(e);
+}
+
+int einval(gemvq_ctx * c, const std::string & what) {
+    if (c) c->err = what;
+    return GEMVQ_EINVAL;
+}
+
+float bits_f(uint32_t b) {
+    float f;
+    std::memcpy(&f, &b, 4);
+    return f;
+}
+
+// ---- layout-only repack (gq_kernels.h: the GGUF block fields split into field-major regions) ----
+void repack_rows(int type, int rows, int cols, const uint8_t * src, uint8_t * dst, bool inverse) {
+    const size_t R = size_t(rows);
+    if (type == T_Q4_0 || type == T_Q8_0) {
+        const size_t nb = size_t(cols / 32), bb = type == T_Q4_0 ? 18 : 34;
+        uint8_t * qa = dst;
+        uint8_t * qb = dst + R * nb * 16;
+        uint8_t * dd = type == T_Q4_0 ? qb : dst + R * nb * 32;
+        for (size_t i = 0; i < R * nb; ++i) {
+            uint8_t * blk = const_cast<uint8_t *>(src) + i * bb;
+            if (!inverse) {
+                std::memcpy(dd + 2 * i, blk, 2);
+                std::memcpy(qa + 16 * i, blk + 2, 16);
+                if (type == T_Q8_0) std::memcpy(qb + 16 * i, blk + 18, 16);
+            } else {
+                std::memcpy(blk, dd + 2 * i, 2);
+                std::memcpy(blk + 2, qa + 16 * i, 16);
+                if (type == T_Q8_0) std::memcpy(blk + 18, qb + 16 * i, 16);
+            }
+        }
+    } else if (type == T_Q5_K) {
+        const size_t ns = size_t(cols / 256);
+        uint8_t * qs = dst, * qh = dst + R * ns * 128, * meta = dst + R * ns * 160;
+        for (size_t i = 0; i < R * ns; ++i) {
+            uint8_t * blk = const_cast<uint8_t *>(src) + i * 176;
+            if (!inverse) {
+                std::memcpy(meta + 16 * i, blk, 16);
+                std::memcpy(qh + 32 * i, blk + 16, 32);
+                std::memcpy(qs + 128 * i, blk + 48, 128);
+            } else {
+                std::memcpy(blk, meta + 16 * i, 16);
+                std::memcpy(blk + 16, qh + 32 * i, 32);
+                std::memcpy(blk + 48, qs + 128 * i, 128);
+            }
+        }
+    } else if (type == T_Q6_K) {
+        const size_t ns = size_t(cols / 256);
+        uint8_t * ql = dst, * qh = dst + R * ns * 128, * sc = dst + R * ns * 192, * dd = dst + R * ns * 208;
+        for (size_t i = 0; i < R * ns; ++i) {
+            uint8_t * blk = const_cast<uint8_t *>(src) + i * 210;
+            if (!inverse) {
+                std::memcpy(ql + 128 * i, blk, 128);
+                std::memcpy(qh + 64 * i, blk + 128, 64);
+                std::memcpy(sc + 16 * i, blk + 192, 16);
+                std::memcpy(dd + 2 * i, blk + 208, 2);
+            } else {
+                std::memcpy(blk, ql + 128 * i, 128);
+                std::memcpy(blk + 128, qh + 64 * i, 64);
+                std::memcpy(blk + 192, sc + 16 * i, 16);
+                std::memcpy(blk + 208, dd + 2 * i, 2);
+            }
+        }
+    }
+}
+
+bool type_ok(int t) { return t == T_Q4_0 || t == T_Q8_0 || t == T_Q5_K || t == T_Q6_K; }
+
+bool shape_ok(int t, int rows, int cols) {
+    if (rows <= 0 || cols <= 0 || cols > int(GEMVQ_MAX_COLS)) return false;
+    return (t == T_Q5_K || t == T_Q6_K) ? cols % 256 == 0 : cols % 32 == 0;
+}
+
+// ---- command processor ----
+struct Compiler {
+    gemvq_ctx * c;
+    std::vector<Launch> out;
+    int bad = 0;  // 1-based index of the first invalid command
+    std::string why;
+
+    bool range(uint32_t off, uint64_t n) const { return off % 16 == 0 && uint64_t(off) + n <= c->act_floats; }
+    float * A(uint32_t off) const { return c->act + off; }
+
+    bool reject(unsigned i, const std::string & w) {
+        bad = int(i) + 1;
+        why = "command " + std::to_string(i + 1) + ": " + w;
+        return false;
+    }
+
+    const Weight * weight(uint64_t off, int type, int rows, int cols) const {
+        auto it = c->weights.find(off);
+        if (it == c->weights.end()) return nullptr;
+        const Weight & w = it->second;
+        return (w.type == type && w.rows == rows && w.cols == cols) ? &w : nullptr;
+    }
+
+    bool compile(const uint32_t * cmds, unsigned n) {
+        struct Deferred { bool on = false; uint32_t n, x, w, y; float eps; uint32_t flags; } defer;
+        for (unsigned i = 0; i < n;) {
+            const uint32_t * k = cmds + size_t(i) * GEMVQ_CMD_WORDS;
+            const uint32_t op = k[0];
+            switch (op) {
+            case GEMVQ_OP_GEMV: {
+                unsigned used = 0;
+                if (!gemv_group(cmds, n, i, defer.on ? &defer.n : nullptr, defer, used)) return false;
+                i += used;
+                continue;
+            }
+            case GEMVQ_OP_RMSNORM: {
+                const uint32_t nn = k[1], rows = k[6] ? k[6] : 1, flags = k[7], stride = ((flags >> 8) & 0xffffu) * 16;
+                const uint32_t st = stride ? stride : nn;
+                if (nn == 0 || nn % 16 || nn > GEMVQ_MAX_COLS || stride % 16) return reject(i, "RMSNORM n");
+                if (stride && stride < nn) return reject(i, "RMSNORM stride");
+                if (!range(k[2], uint64_t(st) * (rows - 1) + nn) || !range(k[4], uint64_t(nn) * rows)) return reject(i, "RMSNORM range");
+                if (!(flags & GEMVQ_NORM_NO_WEIGHT) && !range(k[3], nn)) return reject(i, "RMSNORM weight");
+                if (flags & GEMVQ_NORM_DEFER) {
+                    if (rows != 1 || stride) return reject(i, "deferred RMSNORM needs one packed row");
+                    defer.on = true;
+                    defer.n = nn;
+                    defer.x = k[2];
+                    defer.w = k[3];
+                    defer.y = k[4];
+                    defer.eps = bits_f(k[5]);
+                    defer.flags = flags;
+                } else {
+                    NormArgs a{A(k[2]), (flags & GEMVQ_NORM_NO_WEIGHT) ? nullptr : A(k[3]), A(k[4]), int(nn), int(rows),
+                               int(st), bits_f(k[5]), int(flags & 3)};
+                    out.push_back(LNorm{a});
+                }
+                break;
+            }
+            case GEMVQ_OP_ADD:
+            case GEMVQ_OP_MUL: {
+                const uint32_t nn = k[1];
+                if (nn == 0 || !range(k[2], nn) || !range(k[3], nn) || !range(k[4], nn)) return reject(i, "ADD/MUL range");
+                EwArgs a{A(k[2]), A(k[3]), A(k[4]), int(nn), 0, 0, op == GEMVQ_OP_ADD ? EW_ADD : EW_MUL, 0.0f};
+                out.push_back(LEw{a});
+                break;
+            }
+            case GEMVQ_OP_SILU_MUL: {
+                const uint32_t nn = k[1], row = k[6], stride = k[7];
+                if (nn == 0 || !range(k[3], nn) || !range(k[4], nn)) return reject(i, "SILU_MUL range");
+                if (row) {
+                    if (nn % row || row % 16 || stride % 16 || stride < row || !range(k[2], uint64_t(stride) * (nn / row - 1) + row))
+                        return reject(i, "SILU_MUL rows");
+                } else if (!range(k[2], nn)) {
+                    return reject(i, "SILU_MUL range");
+                }
+                EwArgs a{A(k[2]), A(k[3]), A(k[4]), int(nn), int(row), int(stride),
+                         (k[5] & GEMVQ_SILU_MUL_SIGMOID) ? EW_SIGMOID_MUL : EW_SILU_MUL, 0.0f};
+                out.push_back(LEw{a});
+                break;
+            }
+            case GEMVQ_OP_UNARY: {
+                const uint32_t nn = k[1], kind = k[3], row = k[5], stride = k[6];
+                if (nn == 0 || kind < 1 || kind > 4 || !range(k[4], nn)) return reject(i, "UNARY");
+                if (row) {
+                    if (nn % row || row % 16 || stride % 16 || stride < row || !range(k[2], uint64_t(stride) * (nn / row - 1) + row))
+                        return reject(i, "UNARY rows");
+                } else if (!range(k[2], nn)) {
+                    return reject(i, "UNARY range");
+                }
+                const int ops[5] = {0, EW_SILU, EW_SIGMOID, EW_SOFTPLUS, EW_COPY};
+                EwArgs a{A(k[2]), nullptr, A(k[4]), int(nn), int(row), int(stride), ops[kind], 0.0f};
+                out.push_back(LEw{a});
+                break;
+            }
+            case GEMVQ_OP_GDN: {
+                if (i + 1 >= n) return reject(i, "GDN needs its second slot");
+                const uint32_t * k2 = k + GEMVQ_CMD_WORDS;
+                const uint32_t hv = k[1] & 0xffffu, hk = k[1] >> 16, flags = k2[3];
+                const bool gates = flags & GEMVQ_GDN_GATES;
+                if (gates && i + 2 >= n) return reject(i, "GDN needs its gates slot");
+                const uint32_t * k3 = gates ? k2 + GEMVQ_CMD_WORDS : nullptr;
+                if (hv == 0 || hk == 0 || hv > 64 || hv % hk) return reject(i, "GDN heads");
+                if (!range(k[2], hk * 128) || !range(k[3], hk * 128) || !range(k[4], hv * 128) || !range(k[5], hv) ||
+                    !range(k[6], hv) || !range(k[7], hv * 128))
+                    return reject(i, "GDN range");
+                const uint64_t src = k2[0], dst = k2[1];
+                if (src + uint64_t(hv) * 128 > c->state_rows || dst + uint64_t(hv) * 128 > c->state_rows)
+                    return reject(i, "GDN state rows");
+                if (src != dst && (src < dst + hv * 128ull && dst < src + hv * 128ull)) return reject(i, "GDN state overlap");
+                if (gates && (!range(k3[0], hv) || !range(k3[1], hv))) return reject(i, "GDN gates range");
+                if ((flags & GEMVQ_GDN_GATED) && (!range(k2[6], 128) || !range(k2[7], hv * 128))) return reject(i, "GDN gated range");
+                GdnArgs a{};
+                a.q = A(k[2]);
+                a.k = A(k[3]);
+                a.v = A(k[4]);
+                a.g = A(k[5]);
+                a.beta = A(k[6]);
+                a.y = A(k[7]);
+                a.dt = gates ? A(k3[0]) : nullptr;
+                a.a = gates ? A(k3[1]) : nullptr;
+                a.src = c->state + src * 128;
+                a.dst = c->state + dst * 128;
+                a.hv = int(hv);
+                a.hk = int(hk);
+                a.scale = bits_f(k2[2]);
+                a.l2_eps = bits_f(k2[4]);
+                a.flags = int(flags);
+                out.push_back(LGdn{a});
+                if (flags & GEMVQ_GDN_GATED) {
+                    GatedNormArgs g{A(k[7]), A(k2[7]), A(k2[6]), int(hv), bits_f(k2[5])};
+                    out.push_back(LGated{g});
+                }
+                i += gates ? 3 : 2;
+                continue;
+            }
+            case GEMVQ_OP_CONV: {
+                const uint32_t ch = k[1];
+                if (ch == 0 || ch % 16 || !range(k[2], ch) || !range(k[3], 4ull * ch) || !range(k[4], ch) ||
+                    !range(k[5], 3ull * ch) || !range(k[6], 3ull * ch))
+                    return reject(i, "CONV range");
+                ConvArgs a{A(k[2]), A(k[3]), A(k[5]), A(k[6]), A(k[4]), int(ch), int(k[7] & 1)};
+                out.push_back(LConv{a});
+                break;
+            }
+            case GEMVQ_OP_STATE_LOAD:
+            case GEMVQ_OP_TRACE:
+                break;
+            case GEMVQ_OP_ROPE: {
+                const uint32_t nd = k[1], ne0 = k[5], rows = k[6], pos_off = k[7];
+                if (nd == 0 || nd % 2 || nd > ne0 || ne0 % 16 || ne0 > 1024 || rows == 0) return reject(i, "ROPE shape");
+                if (!range(k[2], uint64_t(ne0) * rows) || !range(k[4], uint64_t(ne0) * rows)) return reject(i, "ROPE range");
+                if (pos_off && !range(pos_off, 1)) return reject(i, "ROPE pos");
+                if (!pos_off && k[3] + uint64_t(nd) > c->act_floats) return reject(i, "ROPE cache");
+                RopeArgs a{A(k[2]), A(k[3]), pos_off ? reinterpret_cast<const int32_t *>(A(pos_off)) : nullptr, A(k[4]),
+                           int(nd), int(ne0), int(rows)};
+                out.push_back(LRope{a});
+                break;
+            }
+            case GEMVQ_OP_ATTN: {
+                if (i + 1 >= n) return reject(i, "ATTN needs its second slot");
+                const uint32_t * k2 = k + GEMVQ_CMD_WORDS;
+                const uint32_t nh = k[1] & 0xffffu, nkv = k[1] >> 16, hd = k[5] & 0xffffu, nrot = k[5] >> 16;
+                const uint32_t kv = k[3], flags = k[7];
+                if (kv >= c->kvs.size()) return reject(i, "ATTN kv buffer");
+                const KvBuf & b = c->kvs[kv];
+                if (nkv == 0 || nh % nkv || nh / nkv > 8 || int(nkv) != b.n_head_kv || int(hd) != b.head_dim || hd > 256 ||
+                    hd % 16 || nrot > hd || nrot % 2)
+                    return reject(i, "ATTN shape");
+                const uint32_t qstride = (flags & 1) ? 2 * hd : hd;
+                if (!range(k[2], uint64_t(qstride) * (nh - 1) + hd) || !range(k[4], uint64_t(nh) * hd) || !range(k[6], 1) ||
+                    !range(k2[0], uint64_t(nkv) * hd) || !range(k2[1], uint64_t(nkv) * hd) || !range(k2[4], hd) ||
+                    !range(k2[5], hd) || k2[6] + uint64_t(b.n_ctx) * nrot > c->act_floats)
+                    return reject(i, "ATTN range");
+                if ((flags & 1) && !range(k2[7], uint64_t(2 * hd) * (nh - 1) + hd)) return reject(i, "ATTN gate range");
+                AttnArgs a{};
+                a.q = A(k[2]);
+                a.k = A(k2[0]);
+                a.v = A(k2[1]);
+                a.qn = A(k2[4]);
+                a.kn = A(k2[5]);
+                a.cs = A(k2[6]);
+                a.pos = reinterpret_cast<const int32_t *>(A(k[6]));
+                a.gate = (flags & 1) ? A(k2[7]) : nullptr;
+                a.y = A(k[4]);
+                a.kc = b.k;
+                a.vc = b.v;
+                a.part = b.part;
+                a.counter = b.counter;
+                a.n_head = int(nh);
+                a.n_head_kv = int(nkv);
+                a.head_dim = int(hd);
+                a.n_rot = int(nrot);
+                a.q_stride = int(qstride);
+                a.n_ctx = b.n_ctx;
+                a.scale = bits_f(k2[2]);
+                a.eps = bits_f(k2[3]);
+                out.push_back(LAttn{a});
+                i += 2;
+                continue;
+            }
+            case GEMVQ_OP_GET_ROWS: {
+                const int type = int(k[1] & 0xffu), rows = int(k[2]), cols = int(k[3]);
+                const uint64_t woff = uint64_t(k[4]) | (uint64_t(k[5]) << 32);
+                if (type != T_Q6_K && type != T_Q4_0 && type != T_Q8_0) return reject(i, "GET_ROWS type");
+                if (!weight(woff, type, rows, cols)) return reject(i, "GET_ROWS weight");
+                if (!range(k[6], 1) || !range(k[7], uint64_t(cols))) return reject(i, "GET_ROWS range");
+                GetRowsArgs a{weight_view(c->warena + woff, type, rows, cols), reinterpret_cast<const int32_t *>(A(k[6])),
+                              A(k[7]), rows, cols, type};
+                out.push_back(LRows{a});
+                break;
+            }
+            case GEMVQ_OP_ARGMAX: {
+                if (k[1] == 0 || !range(k[2], k[1]) || !range(k[3], 2)) return reject(i, "ARGMAX range");
+                out.push_back(LArgmax{A(k[2]), int(k[1]), reinterpret_cast<unsigned long long *>(A(k[3]))});
+                break;
+            }
+            case GEMVQ_OP_NEXT_TOKEN: {
+                if (!range(k[1], 2) || !range(k[2], 1) || !range(k[3], 1) || (k[5] && !range(k[4], k[5])) ||
+                    !range(k[6], 1))
+                    return reject(i, "NEXT_TOKEN range");
+                NextTokenArgs a{};
+                a.key = reinterpret_cast<unsigned long long *>(A(k[1]));
+                a.tok = reinterpret_cast<int32_t *>(A(k[2]));
+                a.pos = reinterpret_cast<int32_t *>(A(k[3]));
+                a.prompt = reinterpret_cast<const int32_t *>(A(k[4]));
+                a.n_prompt = int(k[5]);
+                a.out = reinterpret_cast<int32_t *>(A(k[6]));
+                a.max_pos = int(c->act_floats - k[6]);
+                out.push_back(LNext{a});
+                break;
+            }
+            case GEMVQ_OP_FILL: {
+                if (k[1] == 0 || !range(k[2], k[1])) return reject(i, "FILL range");
+                EwArgs a{nullptr, nullptr, A(k[2]), int(k[1]), 0, 0, EW_FILL, bits_f(k[3])};
+                out.push_back(LEw{a});
+                break;
+            }
+            default:
+                return reject(i, "unknown opcode " + std::to_string(op));
+            }
+            ++i;
+        }
+        return true;
+    }
+
+    // A GEMV group starting at command i (gemvqc16.h:26-45, gemvqc16.cpp:646-733).
+    template <typename D>
+    bool gemv_group(const uint32_t * cmds, unsigned n, unsigned i0, const uint32_t *, const D & defer, unsigned & used) {
+        GemvArgs a{};
+        int type = -1;
+        uint32_t x_off = 0, cols = 0;
+        unsigned i = i0, gemvs = 0;
+        int tasks = 0;
+        while (i < n && a.n_members < 4) {
+            const uint32_t * k = cmds + size_t(i) * GEMVQ_CMD_WORDS;
+            if (k[0] != GEMVQ_OP_GEMV) break;
+            const int t = int(k[1] & 0xffu);
+            const uint32_t flags = k[1] & ~0xffu;
+            const int rows = int(k[2]);
+            if (gemvs > 0 && (k[6] != x_off || k[3] != cols || t != type)) break;
+            if (!type_ok(t) || !shape_ok(t, rows, int(k[3]))) return reject(i, "GEMV format or shape");
+            if (flags & ~(GEMVQ_GEMV_SWIGLU | GEMVQ_GEMV_CONV | GEMVQ_GEMV_ADD | GEMVQ_GEMV_ARGMAX))
+                return reject(i, "GEMV flags");
+            if (__builtin_popcount(flags) > 1) return reject(i, "GEMV: at most one epilog bit");
+            const uint64_t woff = uint64_t(k[4]) | (uint64_t(k[5]) << 32);
+            const Weight * w = weight(woff, t, rows, int(k[3]));
+            if (!w) return reject(i, "GEMV weight offset, format or shape does not match an uploaded weight");
+            if (!range(k[6], k[3]) || !range(k[7], uint64_t(rows))) return reject(i, "GEMV range");
+            if (gemvs + ((flags & GEMVQ_GEMV_SWIGLU) ? 2 : 1) > GEMVQ_GROUP) break;
+            if (gemvs == 0) {
+                type = t;
+                x_off = k[6];
+                cols = k[3];
+            }
+            GemvMember m{};
+            m.w = weight_view(c->warena + woff, t, rows, int(cols));
+            m.rows = rows;
+            m.task_begin = tasks;
+            m.epi = EPI_PLAIN;
+            m.y = A(k[7]);
+            uint32_t y_off = k[7], y_len = uint32_t(rows);
+            unsigned step = 1;
+            if (flags & GEMVQ_GEMV_SWIGLU) {
+                if (i + 1 >= n) return reject(i, "SwiGLU GEMV without its u GEMV");
+                const uint32_t * u = k + GEMVQ_CMD_WORDS;
+                const uint64_t uoff = uint64_t(u[4]) | (uint64_t(u[5]) << 32);
+                if (u[0] != GEMVQ_OP_GEMV || int(u[1] & 0xffu) != t || (u[1] & ~0xffu) || int(u[2]) != rows || u[3] != cols ||
+                    u[6] != x_off)
+                    return reject(i + 1, "SwiGLU u GEMV must match its g GEMV");
+                if (!weight(uoff, t, rows, int(cols)) || !range(u[7], uint64_t(rows))) return reject(i + 1, "SwiGLU u weight or range");
+                m.epi = EPI_SWIGLU;
+                m.w2 = weight_view(c->warena + uoff, t, rows, int(cols));
+                m.y = A(u[7]);
+                y_off = u[7];
+                step = 2;
+            } else if (flags & (GEMVQ_GEMV_CONV | GEMVQ_GEMV_ADD | GEMVQ_GEMV_ARGMAX)) {
+                if (i + 1 >= n) return reject(i, "GEMV epilog without its command");
+                const uint32_t * e = k + GEMVQ_CMD_WORDS;
+                if (flags & GEMVQ_GEMV_CONV) {
+                    if (e[0] != GEMVQ_OP_CONV || e[1] != uint32_t(rows) || e[2] != k[7] || rows % 16) return reject(i + 1, "CONV epilog");
+                    if (!range(e[3], 4ull * rows) || !range(e[4], uint64_t(rows)) || !range(e[5], 3ull * rows) ||
+                        !range(e[6], 3ull * rows))
+                        return reject(i + 1, "CONV epilog range");
+                    m.epi = EPI_CONV;
+                    m.conv_w = A(e[3]);
+                    m.conv_src = A(e[5]);
+                    m.conv_dst = A(e[6]);
+                    m.conv_silu = int(e[7] & 1);
+                    m.y = A(e[4]);
+                    y_off = e[4];
+                } else if (flags & GEMVQ_GEMV_ADD) {
+                    if (e[0] != GEMVQ_OP_ADD || e[1] != uint32_t(rows) || (e[2] != k[7] && e[3] != k[7]))
+                        return reject(i + 1, "ADD epilog");
+                    const uint32_t r_off = e[2] == k[7] ? e[3] : e[2];
+                    if (!range(r_off, uint64_t(rows)) || !range(e[4], uint64_t(rows))) return reject(i + 1, "ADD epilog range");
+                    m.epi = EPI_ADD;
+                    m.res = A(r_off);
+                    m.y = A(e[4]);
+                    y_off = e[4];
+                } else {
+                    if (e[0] != GEMVQ_OP_ARGMAX || e[1] != uint32_t(rows) || e[2] != k[7] || !range(e[3], 2))
+                        return reject(i + 1, "ARGMAX epilog");
+                    if (a.n_members != 0) return reject(i, "ARGMAX epilog must be on the first GEMV of a group");
+                    a.argmax_key = reinterpret_cast<unsigned long long *>(A(e[3]));
+                }
+                step = 2;
+            }
+            a.m[a.n_members++] = m;
+            tasks += rows;
+            gemvs += (flags & GEMVQ_GEMV_SWIGLU) ? 2 : 1;
+            i += step;
+            // a group ends after a GEMV whose y overlaps x (gemvqc16.cpp:468-474)
+            if (y_off < x_off + cols && x_off < y_off + y_len) break;
+        }
+        if (a.n_members == 0) return reject(i0, "GEMV");
+        a.cols = int(cols);
+        a.total_tasks = tasks;
+        a.x = A(x_off);
+        a.xsrc = XSRC_RAW;
+        if (defer.on && defer.y == x_off && defer.n == cols) {
+            a.xsrc = XSRC_NORM;
+            a.x = A(defer.x);
+            a.norm_w = (defer.flags & GEMVQ_NORM_NO_WEIGHT) ? nullptr : A(defer.w);
+            a.norm_eps = defer.eps;
+            a.norm_l2 = int(defer.flags & GEMVQ_NORM_L2);
+        }
+        if (c->dbg_dst && !c->dbg_used) {
+            const Weight * w0 = &c->weights[uint64_t(cmds[size_t(i0) * GEMVQ_CMD_WORDS + 4]) |
+                                            (uint64_t(cmds[size_t(i0) * GEMVQ_CMD_WORDS + 5]) << 32)];
+            const size_t need = (type == T_Q5_K || type == T_Q6_K) ? size_t(w0->rows) * (cols / 256) * 2
+                                                                   : size_t(w0->rows) * (cols / 32);
+            if (need > c->dbg_n) return reject(i0, "debug block-sum buffer too small for this GEMV");
+            a.dbg = c->dbg;
+            c->dbg_used = true;
+        }
+        out.push_back(LGemv{a, type});
+        used = i - i0;
+        return true;
+    }
+};
+
+hipError_t issue(const std::vector<Launch> & ls, hipStream_t s) {
+    for (const Launch & l : ls) {
+        hipError_t e = hipSuccess;
+        if (auto * g = std::get_if<LGemv>(&l)) e = launch_gemv(g->a, g->type, s);
+        else if (auto * x = std::get_if<LNorm>(&l)) e = launch_norm(x->a, s);
+        else if (auto * x = std::get_if<LEw>(&l)) e = launch_ew(x->a, s);
+        else if (auto * x = std::get_if<LConv>(&l)) e = launch_conv(x->a, s);
+        else if (auto * x = std::get_if<LRope>(&l)) e = launch_rope(x->a, s);
+        else if (auto * x = std::get_if<LGdn>(&l)) e = launch_gdn(x->a, s);
+        else if (auto * x = std::get_if<LGated>(&l)) e = launch_gated_norm(x->a, s);
+        else if (auto * x = std::get_if<LAttn>(&l)) e = launch_attn(x->a, s);
+        else if (auto * x = std::get_if<LRows>(&l)) e = launch_get_rows(x->a, s);
+        else if (auto * x = std::get_if<LArgmax>(&l)) e = launch_argmax(x->x, x->n, x->key, s);
+        else if (auto * x = std::get_if<LNext>(&l)) e = launch_next_token(x->a, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+int compile_list(gemvq_ctx * c, const uint32_t * cmds, unsigned n, std::vector<Launch> & out) {
+    if (n > GEMVQ_MAX_CMDS) {
+        c->err = "command list too long";
+        return int(GEMVQ_MAX_CMDS) + 1;
+    }
+    Compiler cp{c, {}, 0, {}};
+    if (!cp.compile(cmds, n)) {
+        c->err = cp.why;
+        return cp.bad;
+    }
+    out = std::move(cp.out);
+    c->last_launches = int(out.size());
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+gemvq_ctx * gemvq_ctx_create(int device, size_t act_floats, size_t weight_bytes, size_t state_rows) {
+    auto * c = new gemvq_ctx();
+    c->device = device;
+    hipError_t e = hipSetDevice(device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipMalloc(&c->act, std::max<size_t>(act_floats, 16) * sizeof(float));
+    if (e == hipSuccess) e = hipMemset(c->act, 0, std::max<size_t>(act_floats, 16) * sizeof(float));
+    if (e == hipSuccess && weight_bytes) e = hipMalloc(&c->warena, weight_bytes);
+    if (e == hipSuccess && state_rows) e = hipMalloc(&c->state, state_rows * 128 * sizeof(float));
+    if (e == hipSuccess && state_rows) e = hipMemset(c->state, 0, state_rows * 128 * sizeof(float));
+    if (e != hipSuccess) {
+        g_create_error = std::string("gemvq_ctx_create: ") + hipGetErrorString(e);
+        gemvq_ctx_destroy(c);
+        return nullptr;
+    }
+    c->act_floats = act_floats;
+    c->wbytes = weight_bytes;
+    c->state_rows = state_rows;
+    return c;
+}
+
+void gemvq_ctx_destroy(gemvq_ctx * c) {
+    if (!c) return;
+    hipSetDevice(c->device);
+    if (c->stream) hipStreamSynchronize(c->stream);
+    for (auto g : c->graphs)
+        if (g) hipGraphExecDestroy(g);
+    for (auto g : c->graph_defs)
+        if (g) hipGraphDestroy(g);
+    for (auto & b : c->kvs) {
+        hipFree(b.k);
+        hipFree(b.v);
+        hipFree(b.part);
+        hipFree(b.counter);
+    }
+    hipFree(c->act);
+    hipFree(c->warena);
+    hipFree(c->state);
+    hipFree(c->dbg);
+    if (c->stream) hipStreamDestroy(c->stream);
+    delete c;
+}
+
+const char * gemvq_last_error(const gemvq_ctx * c) { return c ? c->err.c_str() : g_create_error.c_str(); }
+
+void gemvq_features(gemvq_ctx *, uint32_t out[2]) {
+    out[0] = GEMVQ_FEATURES;
+    out[1] = GEMVQ_FEATURES2;
+}
+
+int gemvq_repack(int type, int rows, int cols, const void * gguf_rows, void * dst) {
+    if (!type_ok(type) || !shape_ok(type, rows, cols) || !gguf_rows || !dst) return GEMVQ_EINVAL;
+    repack_rows(type, rows, cols, static_cast<const uint8_t *>(gguf_rows), static_cast<uint8_t *>(dst), false);
+    return 0;
+}
+
+int gemvq_unpack(int type, int rows, int cols, const void * packed, void * gguf_rows) {
+    if (!type_ok(type) || !shape_ok(type, rows, cols) || !gguf_rows || !packed) return GEMVQ_EINVAL;
+    repack_rows(type, rows, cols, static_cast<uint8_t *>(gguf_rows), const_cast<uint8_t *>(static_cast<const uint8_t *>(packed)),
+                true);
+    return 0;
+}
+
+int gemvq_upload_weight(gemvq_ctx * c, int type, int rows, int cols, const void * gguf_rows, uint64_t * w_off) {
+    if (!c || !w_off || !gguf_rows) return einval(c, "gemvq_upload_weight: null argument");
+    if (!type_ok(type) || !shape_ok(type, rows, cols)) return einval(c, "gemvq_upload_weight: unsupported type or shape");
+    const size_t bytes = gguf_row_bytes(type, cols) * size_t(rows);
+    const size_t off = (c->wused + 255) & ~size_t(255);
+    if (off + bytes > c->wbytes) return einval(c, "gemvq_upload_weight: weight arena full");
+    hipSetDevice(c->device);
+    void * host = nullptr;
+    hipError_t e = hipHostMalloc(&host, bytes, hipHostMallocDefault);
+    if (e != hipSuccess) return fail(c, e, "hipHostMalloc");
+    repack_rows(type, rows, cols, static_cast<const uint8_t *>(gguf_rows), static_cast<uint8_t *>(host), false);
+    e = hipMemcpyAsync(c->warena + off, host, bytes, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    hipHostFree(host);
+    if (e != hipSuccess) return fail(c, e, "weight upload");
+    c->weights[off] = Weight{type, rows, cols, bytes};
+    c->wused = off + bytes;
+    *w_off = off;
+    return 0;
+}
+
+uint64_t gemvq_weight_bytes_used(const gemvq_ctx * c) { return c ? c->wused : 0; }
+
+int gemvq_act_write(gemvq_ctx * c, size_t off, const void * src, size_t n) {
+    if (!c || !src || off + n > c->act_floats) return einval(c, "gemvq_act_write: range");
+    hipSetDevice(c->device);
+    hipError_t e = hipMemcpyAsync(c->act + off, src, n * 4, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return e == hipSuccess ? 0 : fail(c, e, "act write");
+}
+
+int gemvq_act_read(gemvq_ctx * c, size_t off, void * dst, size_t n) {
+    if (!c || !dst || off + n > c->act_floats) return einval(c, "gemvq_act_read: range");
+    hipSetDevice(c->device);
+    hipError_t e = hipMemcpyAsync(dst, c->act + off, n * 4, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return e == hipSuccess ? 0 : fail(c, e, "act read");
+}
+
+int gemvq_state_write(gemvq_ctx * c, size_t row, const float * src, size_t rows) {
+    if (!c || !src || row + rows > c->state_rows) return einval(c, "gemvq_state_write: range");
+    hipSetDevice(c->device);
+    hipError_t e = hipMemcpyAsync(c->state + row * 128, src, rows * 512, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return e == hipSuccess ? 0 : fail(c, e, "state write");
+}
+
+int gemvq_state_read(gemvq_ctx * c, size_t row, float * dst, size_t rows) {
+    if (!c || !dst || row + rows > c->state_rows) return einval(c, "gemvq_state_read: range");
+    hipSetDevice(c->device);
+    hipError_t e = hipMemcpyAsync(dst, c->state + row * 128, rows * 512, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return e == hipSuccess ? 0 : fail(c, e, "state read");
+}
+
+int gemvq_state_clear(gemvq_ctx * c) {
+    if (!c) return GEMVQ_EINVAL;
+    if (!c->state_rows) return 0;
+    hipSetDevice(c->device);
+    hipError_t e = hipMemsetAsync(c->state, 0, c->state_rows * 512, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return e == hipSuccess ? 0 : fail(c, e, "state clear");
+}
+
+int gemvq_kv_create(gemvq_ctx * c, int n_ctx, int n_head_kv, int head_dim) {
+    if (!c || n_ctx <= 0 || n_head_kv <= 0 || head_dim <= 0 || head_dim > 256 || head_dim % 16)
+        return einval(c, "gemvq_kv_create: shape");
+    hipSetDevice(c->device);
+    KvBuf b;
+    b.n_ctx = n_ctx;
+    b.n_head_kv = n_head_kv;
+    b.head_dim = head_dim;
+    const size_t kvn = size_t(n_ctx) * n_head_kv * head_dim;
+    const size_t nch = size_t(n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
+    const size_t partn = size_t(8) * n_head_kv * nch * (2 + head_dim);
+    hipError_t e = hipMalloc(&b.k, kvn * 2);
+    if (e == hipSuccess) e = hipMalloc(&b.v, kvn * 2);
+    if (e == hipSuccess) e = hipMalloc(&b.part, partn * 4);
+    if (e == hipSuccess) e = hipMalloc(&b.counter, size_t(n_head_kv) * 4);
+    if (e == hipSuccess) e = hipMemset(b.k, 0, kvn * 2);
+    if (e == hipSuccess) e = hipMemset(b.v, 0, kvn * 2);
+    if (e == hipSuccess) e = hipMemset(b.counter, 0, size_t(n_head_kv) * 4);
+    if (e != hipSuccess) {
+        hipFree(b.k);
+        hipFree(b.v);
+        hipFree(b.part);
+        hipFree(b.counter);
+        return fail(c, e, "kv create");
+    }
+    c->kvs.push_back(b);
+    return int(c->kvs.size()) - 1;
+}
+
+int gemvq_kv_read(gemvq_ctx * c, int kv, int pos0, int npos, uint16_t * k, uint16_t * v) {
+    if (!c || kv < 0 || size_t(kv) >= c->kvs.size()) return einval(c, "gemvq_kv_read: buffer");
+    const KvBuf & b = c->kvs[kv];
+    if (pos0 < 0 || npos < 0 || pos0 + npos > b.n_ctx) return einval(c, "gemvq_kv_read: range");
+    hipSetDevice(c->device);
+    const size_t row = size_t(b.n_head_kv) * b.head_dim, off = size_t(pos0) * row, n = size_t(npos) * row;
+    hipError_t e = hipSuccess;
+    if (k) e = hipMemcpyAsync(k, b.k + off, n * 2, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess && v) e = hipMemcpyAsync(v, b.v + off, n * 2, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return e == hipSuccess ? 0 : fail(c, e, "kv read");
+}
+
+int gemvq_kv_clear(gemvq_ctx * c) {
+    if (!c) return GEMVQ_EINVAL;
+    hipSetDevice(c->device);
+    hipError_t e = hipSuccess;
+    for (auto & b : c->kvs) {
+        const size_t kvn = size_t(b.n_ctx) * b.n_head_kv * b.head_dim;
+        if (e == hipSuccess) e = hipMemsetAsync(b.k, 0, kvn * 2, c->stream);
+        if (e == hipSuccess) e = hipMemsetAsync(b.v, 0, kvn * 2, c->stream);
+        if (e == hipSuccess) e = hipMemsetAsync(b.counter, 0, size_t(b.n_head_kv) * 4, c->stream);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return e == hipSuccess ? 0 : fail(c, e, "kv clear");
+}
+
+int gemvq_run(gemvq_ctx * c, const uint32_t * cmds, unsigned n) {
+    if (!c || (n && !cmds)) return einval(c, "gemvq_run: null argument");
+    hipSetDevice(c->device);
+    if (n == 0) {  // feature probe (gemvqc16.cpp:1076-1082)
+        const uint32_t f[2] = {GEMVQ_FEATURES, GEMVQ_FEATURES2};
+        return gemvq_act_write(c, 0, f, 2);
+    }
+    std::vector<Launch> ls;
+    c->dbg_used = false;
+    const int st = compile_list(c, cmds, n, ls);
+    if (st) {
+        c->dbg_used = false;
+        return st;
+    }
+    hipError_t e = issue(ls, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e == hipSuccess && c->dbg_used) {
+        e = hipMemcpy(c->dbg_dst, c->dbg, c->dbg_n * 4, hipMemcpyDeviceToHost);
+        c->dbg_dst = nullptr;
+        c->dbg_used = false;
+    }
+    return e == hipSuccess ? 0 : fail(c, e, "run");
+}
+
+int gemvq_graph_create(gemvq_ctx * c, const uint32_t * cmds, unsigned n, int * graph) {
+    if (!c || !cmds || !graph || n == 0) return einval(c, "gemvq_graph_create: arguments");
+    hipSetDevice(c->device);
+    std::vector<Launch> ls;
+    int32_t * const armed = c->dbg_dst;
+    c->dbg_dst = nullptr;  // block-sum dumps are for gemvq_run only
+    const int st = compile_list(c, cmds, n, ls);
+    c->dbg_dst = armed;
+    c->dbg_used = false;
+    if (st) return st;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return fail(c, e, "begin capture");
+    hipError_t le = issue(ls, c->stream);
+    e = hipStreamEndCapture(c->stream, &g);
+    if (le != hipSuccess) {
+        if (g) hipGraphDestroy(g);
+        return fail(c, le, "launch during capture");
+    }
+    if (e != hipSuccess) return fail(c, e, "end capture");
+    e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        hipGraphDestroy(g);
+        return fail(c, e, "graph instantiate");
+    }
+    c->graphs.push_back(ge);
+    c->graph_defs.push_back(g);
+    *graph = int(c->graphs.size()) - 1;
+    return 0;
+}
+
+int gemvq_graph_replay(gemvq_ctx * c, int graph, int times) {
+    if (!c || graph < 0 || size_t(graph) >= c->graphs.size() || !c->graphs[graph] || times < 0)
+        return einval(c, "gemvq_graph_replay: graph");
+    hipSetDevice(c->device);
+    for (int t = 0; t < times; ++t) {
+        const hipError_t e = hipGraphLaunch(c->graphs[graph], c->stream);
+        if (e != hipSuccess) return fail(c, e, "graph launch");
+    }
+    return 0;
+}
+
+int gemvq_graph_destroy(gemvq_ctx * c, int graph) {
+    if (!c || graph < 0 || size_t(graph) >= c->graphs.size()) return einval(c, "gemvq_graph_destroy: graph");
+    hipSetDevice(c->device);
+    hipStreamSynchronize(c->stream);
+    if (c->graphs[graph]) hipGraphExecDestroy(c->graphs[graph]);
+    if (c->graph_defs[graph]) hipGraphDestroy(c->graph_defs[graph]);
+    c->graphs[graph] = nullptr;
+    c->graph_defs[graph] = nullptr;
+    return 0;
+}
+
+int gemvq_sync(gemvq_ctx * c) {
+    if (!c) return GEMVQ_EINVAL;
+    hipSetDevice(c->device);
+    const hipError_t e = hipStreamSynchronize(c->stream);
+    return e == hipSuccess ? 0 : fail(c, e, "sync");
+}
+
+int gemvq_last_launch_count(const gemvq_ctx * c) { return c ? c->last_launches : -1; }
+
+int gemvq_debug_blocksums(gemvq_ctx * c, int32_t * dst, size_t n) {
+    if (!c || !dst || n == 0) return einval(c, "gemvq_debug_blocksums: arguments");
+    hipSetDevice(c->device);
+    hipFree(c->dbg);
+    hipError_t e = hipMalloc(&c->dbg, n * 4);
+    if (e != hipSuccess) return fail(c, e, "debug buffer");
+    c->dbg_n = n;
+    c->dbg_dst = dst;
+    c->dbg_used = false;
+    return 0;
+}
+
+int gemvq_graph_time(gemvq_ctx * c, int graph, int times, double * us) {
+    if (!c || !us || times <= 0 || graph < 0 || size_t(graph) >= c->graphs.size() || !c->graphs[graph])
+        return einval(c, "gemvq_graph_time: arguments");
+    hipSetDevice(c->device);
+    hipEvent_t a, b;
+    hipEventCreate(&a);
+    hipEventCreate(&b);
+    hipError_t e = hipEventRecord(a, c->stream);
+    for (int t = 0; t < times && e == hipSuccess; ++t) e = hipGraphLaunch(c->graphs[graph], c->stream);
+    if (e == hipSuccess) e = hipEventRecord(b, c->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(b);
+    float ms = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    if (e != hipSuccess) return fail(c, e, "graph time");
+    *us = double(ms) * 1000.0 / times;
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,159 @@
+/* MI355X (gfx950) batch-1 decode backend: the C ABI between the C++ host side and the HIP kernels.
+ *
+ * It replaces the boundary between the reference's ggml backend and its FPGA kernel:
+ *   - gemvq_run()            replaces the kernel call gemvqc16(w0..w19, act, cmds, n_cmds, st..., act_rd)
+ *                            (fpga/src/gemvqc16.h:136-149) and its launch by xrt_qc_launch (ggml-xrt.cpp:1241-1280);
+ *   - gemvq_upload_weight()  replaces xrt_qc_weight_offset + gemvqw_layout::repack (ggml-xrt.cpp:735-765,
+ *                            fpga/src/gemvqw_layout.h:137-157): one layout-only repack at load;
+ *   - gemvq_act_write/read() replace the act BO syncs of xrt_qc_flush (ggml-xrt.cpp:1399-1478);
+ *   - gemvq_state_*()        replace the XRT_RS buffer I/O (ggml-xrt.cpp:439-475, 535-552);
+ *   - gemvq_graph_*()        a per-token command list captured once as a hipGraph and replayed per token (the
+ *                            reference starts the kernel once per list, ggml-xrt.cpp:1241-1280);
+ *   - gemvq_features()       the n_cmds == 0 feature probe (gemvqc16.cpp:1076-1082, ggml-xrt.cpp:1284-1300).
+ * Plain C types only; a context is not re-entrant (one host thread at a time, as the reference's backend mutex).
+ *
+ * Command list: GEMVQ_CMD_WORDS uint32 words per command, the opcodes and word layouts of gemvqc16.h:26-98 with
+ * these differences: act offsets and lengths count floats and must be multiples of 16; a GEMV's w_off lo/hi is the
+ * weight offset returned by gemvq_upload_weight (the matrix keeps its rows/cols/format from the upload and the
+ * command must repeat them); GDN state rows index the state buffer (128 floats per row); there is no STATE_LOAD
+ * prefetch need (the opcode is accepted and does nothing) and TRACE is accepted and does nothing. Opcodes added for
+ * the parts the reference leaves on the CPU (attention core, embedding rows, greedy sampling) are listed below.
+ *
+ *   GEMV      [1, format | flags, rows, cols, w_off lo, w_off hi, x_off, y_off]
+ *             format 2 Q4_0, 8 Q8_0, 13 Q5_K, 14 Q6_K; flags GEMVQ_GEMV_SWIGLU (0x100), GEMVQ_GEMV_CONV (0x200),
+ *             GEMVQ_GEMV_ADD (0x400) as gemvqc16.h:31-45, and GEMVQ_GEMV_ARGMAX (0x800): the next command is an
+ *             ARGMAX over this GEMV's y (consumed; y is written). Groups of up to 4 GEMVs with the same x_off, cols
+ *             and format run as one pass; a group ends after a GEMV whose y overlaps x.
+ *   RMSNORM   [2, n, x_off, w_off, y_off, eps bits, rows, flags]  flags bit0 L2, bit1 no weight, bit2 deferred
+ *             (the following GEMVs with x_off == y_off and cols == n quantize the normalized row), bits 23:8 row
+ *             stride in 16-float words (0: packed).
+ *   ADD 3, SILU_MUL 4, MUL 5, UNARY 6, CONV 8, ROPE 10 as gemvqc16.h:52-59, 85-91; ROPE word 7 (pos_off): if
+ *             nonzero, cs_off is a table of n_dims floats per position and the row is selected by the int32
+ *             position stored at act[pos_off].
+ *   GDN       [7, H_v | H_k << 16, q_off, k_off, v_off, g_off, beta_off, y_off]
+ *             + [src_row, dst_row, scale bits, flags, l2_eps bits, rms_eps bits, w_off, z_off]
+ *             (+ [dt_off, a_off, 0...] with GEMVQ_GDN_GATES) as gemvqc16.h:60-81; GEMVQ_GDN_WITH_GEMV and
+ *             GEMVQ_GDN_WITH_OUT are accepted (the results are those of the commands run one by one).
+ *   ATTN      [12, n_head | n_head_kv << 16, q_off, kv, y_off, head_dim | n_rot << 16, pos_off, flags]
+ *             + [k_off, v_off, scale bits, eps bits, qn_off, kn_off, cs_off, gate_off]
+ *             One token of GQA attention (q head h reads KV head h / (n_head / n_head_kv)). q rows (head_dim floats)
+ *             start every 2 * head_dim floats when flags bit0 (gate interleaved, Qwen3.5 Q+gate projection), else
+ *             every head_dim floats. Per head: RMS norm with weight (qn_off / kn_off, eps), NEOX RoPE on the first
+ *             n_rot floats with the cos/sin table at cs_off (n_rot floats per position), K and V stored as fp16 in
+ *             KV buffer kv at the position act[pos_off], softmax(q k^T * scale) V over positions 0..pos, then
+ *             flags bit0: y = sigmoid(gate) * y with the gate rows at gate_off (stride 2 * head_dim).
+ *   GET_ROWS  [13, format, rows, cols, w_off lo, w_off hi, id_off, y_off]  y = dequantized row act_i32[id_off].
+ *   ARGMAX    [14, n, x_off, key_off, 0, 0, 0, 0]  max(packed key at act[key_off..+1]) with the first index of the
+ *             maximum of x; the key must be cleared (NEXT_TOKEN does it).
+ *   NEXT_TOKEN [15, key_off, tok_off, pos_off, prompt_off, n_prompt, out_off, 0]  token = argmax of the key, or
+ *             the prompt token act_i32[prompt_off + pos + 1] while pos + 1 < n_prompt; act_i32[out_off + pos + 1]
+ *             = token; act_i32[tok_off] = token; act_i32[pos_off] = pos + 1; the key is cleared.
+ *   FILL      [16, n, y_off, value bits, 0, 0, 0, 0]  y = value.
+ */
+#ifndef GEMVQ_HIP_H
+#define GEMVQ_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GEMVQ_CMD_WORDS 8u
+#define GEMVQ_OP_GEMV 1u
+#define GEMVQ_OP_RMSNORM 2u
+#define GEMVQ_OP_ADD 3u
+#define GEMVQ_OP_SILU_MUL 4u
+#define GEMVQ_OP_MUL 5u
+#define GEMVQ_OP_UNARY 6u
+#define GEMVQ_OP_GDN 7u
+#define GEMVQ_OP_CONV 8u
+#define GEMVQ_OP_STATE_LOAD 9u
+#define GEMVQ_OP_ROPE 10u
+#define GEMVQ_OP_TRACE 11u
+#define GEMVQ_OP_ATTN 12u
+#define GEMVQ_OP_GET_ROWS 13u
+#define GEMVQ_OP_ARGMAX 14u
+#define GEMVQ_OP_NEXT_TOKEN 15u
+#define GEMVQ_OP_FILL 16u
+#define GEMVQ_GEMV_SWIGLU 0x100u
+#define GEMVQ_GEMV_CONV 0x200u
+#define GEMVQ_GEMV_ADD 0x400u
+#define GEMVQ_GEMV_ARGMAX 0x800u
+#define GEMVQ_GROUP 4u
+#define GEMVQ_GDN_WITH_GEMV 1u
+#define GEMVQ_GDN_L2_QK 2u
+#define GEMVQ_GDN_GATED 4u
+#define GEMVQ_GDN_GATES 8u
+#define GEMVQ_GDN_WITH_OUT 16u
+#define GEMVQ_NORM_L2 1u
+#define GEMVQ_NORM_NO_WEIGHT 2u
+#define GEMVQ_NORM_DEFER 4u
+#define GEMVQ_SILU_MUL_SIGMOID 1u
+#define GEMVQ_MAX_COLS 16384u
+#define GEMVQ_MAX_CMDS 4096u
+/* Feature words (gemvqc16.h:126-134 layout, marker 0x6B51 / 0x6B52). */
+#define GEMVQ_FEATURES 0x6B51FFFBu
+#define GEMVQ_FEATURES2 0x6B520003u /* bit0 SILU_MUL sigmoid + strided g, bit1 ATTN/GET_ROWS/ARGMAX/NEXT_TOKEN */
+
+typedef struct gemvq_ctx gemvq_ctx;
+
+/* Status: 0 ok; > 0 the 1-based index of the first invalid command (nothing ran); GEMVQ_MAX_CMDS + 1 for a list
+ * that is too long; < 0 a HIP error (negated hipError_t) or an argument error (GEMVQ_EINVAL). */
+#define GEMVQ_EINVAL (-10000)
+
+/* Creates a context on HIP device `device` with an activation buffer of act_floats floats, a weight arena of
+ * weight_bytes, and state_rows GDN state rows of 128 floats. Returns NULL on failure. */
+gemvq_ctx * gemvq_ctx_create(int device, size_t act_floats, size_t weight_bytes, size_t state_rows);
+void gemvq_ctx_destroy(gemvq_ctx * ctx);
+/* Last error message of the context (or of the last failed create when ctx is NULL). */
+const char * gemvq_last_error(const gemvq_ctx * ctx);
+void gemvq_features(gemvq_ctx * ctx, uint32_t out[2]);
+
+/* Repacks rows x cols GGUF rows of ggml type `type` (2, 8, 13, 14) into the weight arena and returns the weight
+ * offset for GEMV / GET_ROWS commands in *w_off. The bits are the original ones; only their order changes. */
+int gemvq_upload_weight(gemvq_ctx * ctx, int type, int rows, int cols, const void * gguf_rows, uint64_t * w_off);
+/* Bytes of the arena in use (weights uploaded so far, with alignment). */
+uint64_t gemvq_weight_bytes_used(const gemvq_ctx * ctx);
+/* The load-time layout on the host (no GPU call): gemvq_repack writes the device layout of rows x cols GGUF rows
+ * into dst (the same number of bytes); gemvq_unpack is its inverse. Returns 0 or GEMVQ_EINVAL. */
+int gemvq_repack(int type, int rows, int cols, const void * gguf_rows, void * dst);
+int gemvq_unpack(int type, int rows, int cols, const void * packed, void * gguf_rows);
+
+/* Activation buffer I/O (offsets and counts in floats; int32 data may be written through the same calls). */
+int gemvq_act_write(gemvq_ctx * ctx, size_t off, const void * src, size_t n);
+int gemvq_act_read(gemvq_ctx * ctx, size_t off, void * dst, size_t n);
+/* GDN state rows (128 floats each). */
+int gemvq_state_write(gemvq_ctx * ctx, size_t row, const float * src, size_t rows);
+int gemvq_state_read(gemvq_ctx * ctx, size_t row, float * dst, size_t rows);
+int gemvq_state_clear(gemvq_ctx * ctx);
+
+/* KV buffer for ATTN: n_ctx positions of n_head_kv x head_dim fp16 keys and values. Returns its id (>= 0). */
+int gemvq_kv_create(gemvq_ctx * ctx, int n_ctx, int n_head_kv, int head_dim);
+int gemvq_kv_read(gemvq_ctx * ctx, int kv, int pos0, int npos, uint16_t * k, uint16_t * v);
+int gemvq_kv_clear(gemvq_ctx * ctx);
+
+/* Runs a command list now (validated first; synchronous). */
+int gemvq_run(gemvq_ctx * ctx, const uint32_t * cmds, unsigned n_cmds);
+/* Validates and captures a command list as a hipGraph; *graph receives its id. */
+int gemvq_graph_create(gemvq_ctx * ctx, const uint32_t * cmds, unsigned n_cmds, int * graph);
+/* Launches a captured graph `times` times back to back (asynchronous; gemvq_sync waits). */
+int gemvq_graph_replay(gemvq_ctx * ctx, int graph, int times);
+int gemvq_graph_destroy(gemvq_ctx * ctx, int graph);
+int gemvq_sync(gemvq_ctx * ctx);
+
+/* Number of kernel launches the last validated list compiled to (after fusion). */
+int gemvq_last_launch_count(const gemvq_ctx * ctx);
+
+/* Debug: the integer block sums of the next GEMV pass's first matrix are written to dst (int32 per 32-block for
+ * Q4_0 / Q8_0, two int32 S, M per super-block for Q5_K / Q6_K); cleared after that pass. */
+int gemvq_debug_blocksums(gemvq_ctx * ctx, int32_t * dst, size_t n);
+
+/* Timing: average device time in microseconds of the kernels of `graph` over `times` replays, measured with
+ * HIP events on the context stream (the replays run back to back between the events). */
+int gemvq_graph_time(gemvq_ctx * ctx, int graph, int times, double * us_per_replay);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,235 @@
+"""ctypes bindings of the CPU oracle (liborc_gemvq.so) and of the reference's own CPU path compiled into
+_ref/libgemvq_ref.so. TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg, never by the product path."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORC_PATH = os.path.join(HERE, "liborc_gemvq.so")
+REF_PATH = os.path.join(HERE, "_ref", "libgemvq_ref.so")
+REF_SRC = "/root/reference/fpga/src"
+
+Q4_0, Q8_0, Q5_K, Q6_K = 2, 8, 13, 14
+F = np.float32
+
+
+def build(ref: bool = True) -> None:
+    """Compiles the oracle; also the reference's own gemvq_ref.h into _ref/ when the reference tree is present."""
+    subprocess.run(["make", "-B", "-C", HERE, "liborc_gemvq.so"], check=True, capture_output=True)
+    if ref and os.path.isdir(REF_SRC):
+        subprocess.run(["make", "-B", "-C", HERE, "ref"], check=True, capture_output=True)
+
+
+def _p(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def _fn(lib, name, res, *args):
+    f = getattr(lib, name)
+    f.restype = res
+    f.argtypes = list(args)
+    return f
+
+
+_orc = None
+_ref = None
+
+
+def orc() -> C.CDLL:
+    global _orc
+    if _orc is None:
+        lib = C.CDLL(ORC_PATH)
+        vp, i, fl = C.c_void_p, C.c_int, C.c_float
+        _fn(lib, "orc_half_to_float", fl, C.c_uint16)
+        _fn(lib, "orc_float_to_half", C.c_uint16, fl)
+        _fn(lib, "orc_nearest_int", i, fl)
+        for n in ("orc_expf", "orc_logf", "orc_silu", "orc_sigmoid", "orc_softplus"):
+            _fn(lib, n, fl, fl)
+        _fn(lib, "orc_pair_sum", fl, vp, i)
+        _fn(lib, "orc_row_bytes", C.c_size_t, i, i)
+        _fn(lib, "orc_quantize_q8_0", None, vp, i, vp, vp)
+        _fn(lib, "orc_quantize_q8_K", None, vp, i, vp, vp, vp)
+        _fn(lib, "orc_ref_gemv", None, i, vp, vp, i, i, vp, vp)
+        _fn(lib, "orc_ref_within_tolerance", i, fl, fl, C.c_double)
+        _fn(lib, "orc_fx_gemv", None, i, vp, vp, i, i, vp, vp, vp)
+        _fn(lib, "orc_fx_gemv_q", None, i, vp, vp, vp, vp, vp, i, i, vp, vp, vp)
+        _fn(lib, "orc_fixed_to_float", fl, C.c_int64)
+        _fn(lib, "orc_ref_rmsnorm", None, vp, vp, i, fl, vp)
+        _fn(lib, "orc_ref_rownorm", None, vp, vp, i, i, fl, i, vp)
+        _fn(lib, "orc_norm_scale", fl, vp, i, fl, i)
+        _fn(lib, "orc_rownorm", None, vp, vp, i, i, i, fl, i, vp)
+        _fn(lib, "orc_silu_mul", None, vp, vp, i, i, vp)
+        _fn(lib, "orc_unary", None, vp, i, i, vp)
+        _fn(lib, "orc_ref_unary", None, vp, i, i, vp)
+        _fn(lib, "orc_conv", None, vp, vp, vp, i, i, vp, vp)
+        _fn(lib, "orc_ref_conv", None, vp, vp, vp, i, i, vp, vp)
+        _fn(lib, "orc_rope", None, vp, vp, i, i, i, vp)
+        _fn(lib, "orc_ref_gdn", None, vp, vp, vp, vp, vp, vp, i, i, fl, vp, vp, vp)
+        _fn(lib, "orc_gdn", None, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i, i, fl, fl, fl, i, vp)
+        _fn(lib, "orc_attn", None, vp, vp, vp, i, i, i, i, fl, vp)
+        _fn(lib, "orc_dequant_row_q6_K", None, vp, i, vp)
+        _fn(lib, "orc_argmax", i, vp, i)
+        _fn(lib, "orc_rope_cache", None, i, i, fl, vp)
+        _fn(lib, "orc_model_create", vp, vp, vp, i, vp, i)
+        _fn(lib, "orc_model_decode", i, vp, i, i, vp)
+        _fn(lib, "orc_model_hidden", C.POINTER(fl), vp)
+        _fn(lib, "orc_model_destroy", None, vp)
+        _orc = lib
+    return _orc
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_PATH)
+
+
+def ref() -> C.CDLL:
+    """The reference's gemvq_ref.h itself, compiled from the reference tree (see Makefile target `ref`)."""
+    global _ref
+    if _ref is None:
+        lib = C.CDLL(REF_PATH)
+        vp, u, fl = C.c_void_p, C.c_uint, C.c_float
+        _fn(lib, "refshim_half_to_float", fl, C.c_uint16)
+        _fn(lib, "refshim_float_to_half", C.c_uint16, fl)
+        _fn(lib, "refshim_nearest_int", C.c_int, fl)
+        _fn(lib, "refshim_quantize_q8_k", None, vp, u, vp, vp)
+        _fn(lib, "refshim_gemv", None, vp, vp, u, u, u, vp, vp)
+        _fn(lib, "refshim_within_tolerance", C.c_int, fl, fl, C.c_double)
+        _fn(lib, "refshim_within_elementwise", C.c_int, fl, fl)
+        _fn(lib, "refshim_within_swiglu", C.c_int, fl, fl, C.c_double, fl, C.c_double)
+        _fn(lib, "refshim_rmsnorm", None, vp, vp, u, fl, vp)
+        _fn(lib, "refshim_rownorm", None, vp, vp, u, u, fl, u, vp)
+        _fn(lib, "refshim_silu_mul", None, vp, vp, u, vp)
+        _fn(lib, "refshim_unary", None, vp, u, u, vp)
+        _fn(lib, "refshim_conv", None, vp, vp, vp, u, C.c_int, vp, vp)
+        _fn(lib, "refshim_gdn", None, vp, vp, vp, vp, vp, vp, u, u, fl, vp, vp, vp)
+        _ref = lib
+    return _ref
+
+
+# ---- convenience wrappers (numpy in, numpy out) ----
+def row_bytes(t: int, cols: int) -> int:
+    return int(orc().orc_row_bytes(t, cols))
+
+
+def quantize_q8_0(x: np.ndarray):
+    x = np.ascontiguousarray(x, F)
+    q = np.empty(x.size, np.int8)
+    d = np.empty(x.size // 32, np.uint16)
+    orc().orc_quantize_q8_0(_p(x), x.size, _p(q), _p(d))
+    return q, d
+
+
+def quantize_q8_K(x: np.ndarray):
+    x = np.ascontiguousarray(x, F)
+    q = np.empty(x.size, np.int8)
+    d = np.empty(x.size // 256, F)
+    bs = np.empty(x.size // 16, np.int16)
+    orc().orc_quantize_q8_K(_p(x), x.size, _p(q), _p(d), _p(bs))
+    return q, d, bs
+
+
+def ref_gemv(t: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int):
+    x = np.ascontiguousarray(x, F)
+    y = np.empty(rows, F)
+    mag = np.empty(rows, np.float64)
+    orc().orc_ref_gemv(t, _p(w), _p(x), rows, cols, _p(y), _p(mag))
+    return y, mag
+
+
+def fx_gemv(t: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int, blocksums: bool = False):
+    x = np.ascontiguousarray(x, F)
+    y = np.empty(rows, F)
+    acc = np.empty(rows, np.int64)
+    nbs = rows * (cols // 256 * 2 if t in (Q5_K, Q6_K) else cols // 32)
+    bs = np.empty(nbs, np.int32) if blocksums else None
+    orc().orc_fx_gemv(t, _p(w), _p(x), rows, cols, _p(y), _p(bs), _p(acc))
+    return (y, bs, acc) if blocksums else y
+
+
+def norm_scale(x: np.ndarray, eps: float, l2: bool = False) -> float:
+    x = np.ascontiguousarray(x, F)
+    return float(orc().orc_norm_scale(_p(x), x.size, eps, 1 if l2 else 0))
+
+
+def rownorm(x: np.ndarray, w: np.ndarray | None, n: int, rows: int, eps: float, flags: int = 0, stride: int = 0):
+    x = np.ascontiguousarray(x, F)
+    w = np.ascontiguousarray(w, F) if w is not None else np.zeros(n, F)
+    y = np.empty(n * rows, F)
+    orc().orc_rownorm(_p(x), _p(w), n, rows, stride, eps, flags, _p(y))
+    return y
+
+
+def pair_sum(a: np.ndarray) -> float:
+    a = np.ascontiguousarray(a, F)
+    return float(orc().orc_pair_sum(_p(a), a.size))
+
+
+def silu_mul(g, u, sigmoid=False):
+    g = np.ascontiguousarray(g, F)
+    u = np.ascontiguousarray(u, F)
+    y = np.empty(g.size, F)
+    orc().orc_silu_mul(_p(g), _p(u), g.size, 1 if sigmoid else 0, _p(y))
+    return y
+
+
+def unary(x, kind):
+    x = np.ascontiguousarray(x, F)
+    y = np.empty(x.size, F)
+    orc().orc_unary(_p(x), x.size, kind, _p(y))
+    return y
+
+
+def conv(state, x, w, silu=True):
+    state, x, w = (np.ascontiguousarray(a, F) for a in (state, x, w))
+    y = np.empty(x.size, F)
+    ns = np.empty(state.size, F)
+    orc().orc_conv(_p(state), _p(x), _p(w), x.size, 1 if silu else 0, _p(y), _p(ns))
+    return y, ns
+
+
+def rope(x, cs, n_dims, ne0, rows):
+    x, cs = np.ascontiguousarray(x, F), np.ascontiguousarray(cs, F)
+    y = np.empty(x.size, F)
+    orc().orc_rope(_p(x), _p(cs), n_dims, ne0, rows, _p(y))
+    return y
+
+
+def rope_cache(pos: int, n_dims: int, base: float) -> np.ndarray:
+    cs = np.empty(n_dims, F)
+    orc().orc_rope_cache(pos, n_dims, base, _p(cs))
+    return cs
+
+
+def gdn(state, q, k, v, graw, braw, hv, hk, scale, flags=0, dt=None, a=None, z=None, w=None, l2_eps=1e-6, rms_eps=1e-6):
+    st = np.ascontiguousarray(state, F).copy()
+    args = [np.ascontiguousarray(t, F) if t is not None else None for t in (q, k, v, graw, braw, dt, a, z, w)]
+    y = np.empty(hv * 128, F)
+    orc().orc_gdn(_p(st), *[_p(t) for t in args], hv, hk, scale, l2_eps, rms_eps, flags, _p(y))
+    return y, st
+
+
+def attn(q, kc, vc, nh, nkvh, hd, n_kv, scale):
+    q = np.ascontiguousarray(q, F)
+    out = np.empty(nh * hd, F)
+    orc().orc_attn(_p(q), _p(np.ascontiguousarray(kc, np.uint16)), _p(np.ascontiguousarray(vc, np.uint16)), nh, nkvh,
+                   hd, n_kv, scale, _p(out))
+    return out
+
+
+def dequant_row_q6_K(row: np.ndarray, cols: int) -> np.ndarray:
+    y = np.empty(cols, F)
+    orc().orc_dequant_row_q6_K(_p(np.ascontiguousarray(row, np.uint8)), cols, _p(y))
+    return y
+
+
+def f2h(x: np.ndarray) -> np.ndarray:
+    o = orc()
+    return np.array([o.orc_float_to_half(float(v)) for v in np.asarray(x, F).ravel()], np.uint16)
