@@ -593,6 +593,11 @@ void gemvq_ctx_destroy(gemvq_ctx * c) {
 
 const char * gemvq_last_error(const gemvq_ctx * c) { return c ? c->err.c_str() : g_create_error.c_str(); }
 
+// Internal (not part of the public ABI): lets the model driver report its own errors through gemvq_last_error.
+__attribute__((visibility("hidden"))) void gq_set_error(gemvq_ctx * c, const char * what) {
+    if (c) c->err = what;
+}
+
 void gemvq_features(gemvq_ctx *, uint32_t out[2]) {
     out[0] = GEMVQ_FEATURES;
     out[1] = GEMVQ_FEATURES2;

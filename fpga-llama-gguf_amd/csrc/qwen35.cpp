@@ -1,0 +1,366 @@
+// Per-token command list of a Qwen3.5-shaped hybrid decoder, captured once as a hipGraph (include/gemvq_qwen35.h).
+//
+// Layer order follows llama.cpp's qwen35 graph as the reference offloads it (llama.cpp/patches/0006: all input
+// projections of a layer right after its norm) in the fused forms of the reference kernel (fpga/src/gemvqc16.h):
+//   DeltaNet layer: deferred RMSNORM -> GEMV group {qkv + CONV epilog, z, beta, alpha} -> GDN (L2 q/k, gates,
+//                   gated output norm) -> ssm_out GEMV + residual ADD epilog
+//   attention layer: deferred RMSNORM -> GEMV group {q+gate, k, v} -> ATTN (q/k norm, RoPE, KV append, softmax,
+//                   sigmoid gate) -> attn_output GEMV + ADD
+//   both: deferred RMSNORM -> {ffn_gate, ffn_up} SwiGLU pair -> ffn_down GEMV + ADD
+// then the output norm, the head GEMV with the ARGMAX epilog and NEXT_TOKEN.
+#include "gemvq_qwen35.h"
+
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+namespace {
+
+constexpr int F32 = 0;
+
+uint32_t fb(float f) {
+    uint32_t b;
+    std::memcpy(&b, &f, 4);
+    return b;
+}
+
+size_t up16(size_t n) { return (n + 15) / 16 * 16; }
+
+struct T {
+    const gemvq_tensor_desc * d = nullptr;
+    uint64_t w_off = 0;     // quantized: weight arena offset
+    uint32_t act_off = 0;   // F32: activation buffer offset
+};
+
+}  // namespace
+
+struct gemvq_qwen35 {
+    gemvq_ctx * ctx = nullptr;
+    gemvq_qw_config c{};
+    std::vector<gemvq_tensor_desc> descs;  // copy of the caller's table
+    std::map<std::string, T> t;
+    std::vector<uint32_t> cmds;
+    int graph = -1;
+    std::vector<int> kv;  // per layer (attention layers only)
+    // activation layout
+    uint32_t tok = 16, pos = 32, key = 48;
+    uint32_t h = 0, xn = 0, qkv = 0, cqkv = 0, z = 0, ba = 0, y = 0, tmp = 0, qg = 0, kk = 0, vv = 0, att = 0, ffn = 0,
+             logits = 0, rope = 0, prompt = 0, out = 0;
+    std::vector<uint32_t> conv_state;  // per layer
+    size_t act_floats = 0;
+};
+
+namespace {
+
+const gemvq_tensor_desc * find(const gemvq_tensor_desc * tab, int n, const std::string & name) {
+    for (int i = 0; i < n; ++i)
+        if (name == tab[i].name) return &tab[i];
+    return nullptr;
+}
+
+bool is_attn(const gemvq_qw_config & c, int il) { return (il + 1) % c.attn_interval == 0; }
+
+int conv_ch(const gemvq_qw_config & c) { return 2 * c.ssm_k_heads * c.ssm_head_dim + c.ssm_v_heads * c.ssm_head_dim; }
+
+// Layout of the activation buffer; returns the number of floats.
+size_t layout(gemvq_qwen35 & m, const gemvq_tensor_desc * tab, int n) {
+    const gemvq_qw_config & c = m.c;
+    size_t off = 64;
+    auto take = [&](size_t floats) {
+        const size_t o = off;
+        off += up16(floats);
+        return uint32_t(o);
+    };
+    for (int i = 0; i < n; ++i) {
+        if (tab[i].type != F32) continue;
+        T & x = m.t[tab[i].name];
+        x.d = &tab[i];
+        x.act_off = take(size_t(tab[i].ne0) * size_t(tab[i].ne1 > 0 ? tab[i].ne1 : 1));
+    }
+    const int ch = conv_ch(c), S = c.ssm_head_dim, hv = c.ssm_v_heads;
+    m.conv_state.assign(c.n_layer, 0);
+    for (int il = 0; il < c.n_layer; ++il)
+        if (!is_attn(c, il)) m.conv_state[il] = take(size_t(ch) * 3);
+    m.rope = take(size_t(c.n_ctx) * c.n_rot);
+    m.prompt = take(size_t(c.n_ctx));
+    m.out = take(size_t(c.n_ctx) + 16);
+    m.h = take(c.n_embd);
+    m.xn = take(std::max(c.n_embd, c.n_ff));
+    m.qkv = take(ch);
+    m.cqkv = take(ch);
+    m.z = take(size_t(hv) * S);
+    m.ba = take(2 * up16(hv));
+    m.y = take(size_t(hv) * S);
+    m.tmp = take(c.n_embd);
+    m.qg = take(size_t(2) * c.n_head * c.head_dim);
+    m.kk = take(size_t(c.n_head_kv) * c.head_dim);
+    m.vv = take(size_t(c.n_head_kv) * c.head_dim);
+    m.att = take(size_t(c.n_head) * c.head_dim);
+    m.ffn = take(c.n_ff);
+    m.logits = take(c.n_vocab);
+    return off;
+}
+
+struct Emit {
+    std::vector<uint32_t> & w;
+    void cmd(std::initializer_list<uint32_t> words) {
+        size_t k = 0;
+        for (uint32_t v : words) {
+            w.push_back(v);
+            ++k;
+        }
+        for (; k < GEMVQ_CMD_WORDS; ++k) w.push_back(0);
+    }
+    void gemv(const T & t, uint32_t x, uint32_t y, uint32_t flags = 0) {
+        cmd({GEMVQ_OP_GEMV, uint32_t(t.d->type) | flags, uint32_t(t.d->ne1), uint32_t(t.d->ne0), uint32_t(t.w_off),
+             uint32_t(t.w_off >> 32), x, y});
+    }
+};
+
+bool build_commands(gemvq_qwen35 & m, std::string & err) {
+    const gemvq_qw_config & c = m.c;
+    Emit e{m.cmds};
+    auto W = [&](const std::string & name) -> const T * {
+        auto it = m.t.find(name);
+        if (it == m.t.end() || !it->second.d) {
+            err = "missing tensor " + name;
+            return nullptr;
+        }
+        return &it->second;
+    };
+    const float eps = c.eps;
+    const int E = c.n_embd, S = c.ssm_head_dim, hv = c.ssm_v_heads, hk = c.ssm_k_heads, ch = conv_ch(c);
+    const T * emb = W("token_embd.weight");
+    const T * onorm = W("output_norm.weight");
+    const T * head = W("output.weight");
+    if (!emb || !onorm || !head) return false;
+    e.cmd({GEMVQ_OP_GET_ROWS, uint32_t(emb->d->type), uint32_t(emb->d->ne1), uint32_t(emb->d->ne0),
+           uint32_t(emb->w_off), uint32_t(emb->w_off >> 32), m.tok, m.h});
+    for (int il = 0; il < c.n_layer; ++il) {
+        const std::string p = "blk." + std::to_string(il) + ".";
+        const T * an = W(p + "attn_norm.weight");
+        const T * pn = W(p + "post_attention_norm.weight");
+        const T * fg = W(p + "ffn_gate.weight");
+        const T * fu = W(p + "ffn_up.weight");
+        const T * fd = W(p + "ffn_down.weight");
+        if (!an || !pn || !fg || !fu || !fd) return false;
+        e.cmd({GEMVQ_OP_RMSNORM, uint32_t(E), m.h, an->act_off, m.xn, fb(eps), 1, GEMVQ_NORM_DEFER});
+        if (is_attn(c, il)) {
+            const T * wq = W(p + "attn_q.weight");
+            const T * wk = W(p + "attn_k.weight");
+            const T * wv = W(p + "attn_v.weight");
+            const T * qn = W(p + "attn_q_norm.weight");
+            const T * kn = W(p + "attn_k_norm.weight");
+            const T * wo = W(p + "attn_output.weight");
+            if (!wq || !wk || !wv || !qn || !kn || !wo) return false;
+            e.gemv(*wq, m.xn, m.qg);
+            e.gemv(*wk, m.xn, m.kk);
+            e.gemv(*wv, m.xn, m.vv);
+            const uint32_t hd = uint32_t(c.head_dim);
+            e.cmd({GEMVQ_OP_ATTN, uint32_t(c.n_head) | (uint32_t(c.n_head_kv) << 16), m.qg, uint32_t(m.kv[il]), m.att,
+                   hd | (uint32_t(c.n_rot) << 16), m.pos, 1u});
+            e.cmd({m.kk, m.vv, fb(1.0f / std::sqrt(float(c.head_dim))), fb(eps), qn->act_off, kn->act_off, m.rope,
+                   m.qg + hd});
+            e.gemv(*wo, m.att, m.tmp, GEMVQ_GEMV_ADD);
+            e.cmd({GEMVQ_OP_ADD, uint32_t(E), m.tmp, m.h, m.h});
+        } else {
+            const T * wqkv = W(p + "attn_qkv.weight");
+            const T * wz = W(p + "attn_gate.weight");
+            const T * wb = W(p + "ssm_beta.weight");
+            const T * wa = W(p + "ssm_alpha.weight");
+            const T * cw = W(p + "ssm_conv1d.weight");
+            const T * dt = W(p + "ssm_dt.bias");
+            const T * a = W(p + "ssm_a");
+            const T * sn = W(p + "ssm_norm.weight");
+            const T * so = W(p + "ssm_out.weight");
+            if (!wqkv || !wz || !wb || !wa || !cw || !dt || !a || !sn || !so) return false;
+            const uint32_t ba2 = m.ba + uint32_t(up16(hv));
+            e.gemv(*wqkv, m.xn, m.qkv, GEMVQ_GEMV_CONV);
+            e.cmd({GEMVQ_OP_CONV, uint32_t(ch), m.qkv, cw->act_off, m.cqkv, m.conv_state[il], m.conv_state[il], 1u});
+            e.gemv(*wz, m.xn, m.z);
+            e.gemv(*wb, m.xn, m.ba);
+            e.gemv(*wa, m.xn, ba2);
+            // state rows of this layer: layer slot * hv * 128
+            int slot = 0;
+            for (int j = 0; j < il; ++j) slot += !is_attn(c, j);
+            const uint32_t row = uint32_t(slot) * uint32_t(hv) * 128u;
+            const uint32_t flags = GEMVQ_GDN_L2_QK | GEMVQ_GDN_GATED | GEMVQ_GDN_GATES;
+            e.cmd({GEMVQ_OP_GDN, uint32_t(hv) | (uint32_t(hk) << 16), m.cqkv, m.cqkv + uint32_t(hk * S),
+                   m.cqkv + uint32_t(2 * hk * S), ba2, m.ba, m.y});
+            e.cmd({row, row, fb(1.0f / std::sqrt(float(S))), flags, fb(eps), fb(eps), sn->act_off, m.z});
+            e.cmd({dt->act_off, a->act_off});
+            e.gemv(*so, m.y, m.tmp, GEMVQ_GEMV_ADD);
+            e.cmd({GEMVQ_OP_ADD, uint32_t(E), m.tmp, m.h, m.h});
+        }
+        e.cmd({GEMVQ_OP_RMSNORM, uint32_t(E), m.h, pn->act_off, m.xn, fb(eps), 1, GEMVQ_NORM_DEFER});
+        e.gemv(*fg, m.xn, m.ffn, GEMVQ_GEMV_SWIGLU);
+        e.gemv(*fu, m.xn, m.ffn);
+        e.gemv(*fd, m.ffn, m.tmp, GEMVQ_GEMV_ADD);
+        e.cmd({GEMVQ_OP_ADD, uint32_t(E), m.tmp, m.h, m.h});
+    }
+    e.cmd({GEMVQ_OP_RMSNORM, uint32_t(E), m.h, onorm->act_off, m.xn, fb(eps), 1, GEMVQ_NORM_DEFER});
+    e.gemv(*head, m.xn, m.logits, GEMVQ_GEMV_ARGMAX);
+    e.cmd({GEMVQ_OP_ARGMAX, uint32_t(head->d->ne1), m.logits, m.key});
+    e.cmd({GEMVQ_OP_NEXT_TOKEN, m.key, m.tok, m.pos, m.prompt, 0u, m.out});
+    return true;
+}
+
+}  // namespace
+
+extern "C" void gq_set_error(gemvq_ctx * ctx, const char * what);  // gq_runtime.hip
+
+namespace {
+int set_err(gemvq_ctx * ctx, const std::string & what) {
+    gq_set_error(ctx, what.c_str());
+    return GEMVQ_EINVAL;
+}
+}  // namespace
+
+extern "C" {
+
+int gemvq_qwen35_sizes(const gemvq_qw_config * cfg, const gemvq_tensor_desc * tab, int n, size_t * act_floats,
+                       size_t * weight_bytes, size_t * state_rows) {
+    if (!cfg || !tab || n <= 0) return GEMVQ_EINVAL;
+    gemvq_qwen35 m;
+    m.c = *cfg;
+    const size_t act = layout(m, tab, n);
+    size_t wb = 0;
+    for (int i = 0; i < n; ++i)
+        if (tab[i].type != F32) wb += (tab[i].nbytes + 255) / 256 * 256;
+    int gdn_layers = 0;
+    for (int il = 0; il < cfg->n_layer; ++il) gdn_layers += !is_attn(*cfg, il);
+    if (act_floats) *act_floats = act;
+    if (weight_bytes) *weight_bytes = wb + 4096;
+    if (state_rows) *state_rows = size_t(gdn_layers) * cfg->ssm_v_heads * 128;
+    return 0;
+}
+
+gemvq_qwen35 * gemvq_qwen35_create(gemvq_ctx * ctx, const gemvq_qw_config * cfg, const gemvq_tensor_desc * tab,
+                                   int n, const uint8_t * blob) {
+    if (!ctx || !cfg || !tab || !blob || n <= 0) return nullptr;
+    auto * m = new gemvq_qwen35();
+    m->ctx = ctx;
+    m->c = *cfg;
+    const gemvq_qw_config & c = m->c;
+    if (c.n_rot % 2 || c.n_rot > c.head_dim || c.ssm_head_dim != 128 || c.attn_interval <= 0 || c.n_ctx <= 0) {
+        set_err(ctx, "gemvq_qwen35_create: unsupported configuration");
+        delete m;
+        return nullptr;
+    }
+    m->descs.assign(tab, tab + n);
+    m->act_floats = layout(*m, m->descs.data(), n);
+    for (int i = 0; i < n; ++i) {
+        T & x = m->t[tab[i].name];
+        x.d = &m->descs[i];
+        if (tab[i].type == F32) {
+            if (gemvq_act_write(ctx, x.act_off, blob + tab[i].offset, size_t(tab[i].ne0) * std::max(1, tab[i].ne1))) {
+                delete m;
+                return nullptr;
+            }
+        } else if (gemvq_upload_weight(ctx, tab[i].type, tab[i].ne1, tab[i].ne0, blob + tab[i].offset, &x.w_off)) {
+            delete m;
+            return nullptr;
+        }
+    }
+    m->kv.assign(c.n_layer, -1);
+    for (int il = 0; il < c.n_layer; ++il) {
+        if (!is_attn(c, il)) continue;
+        m->kv[il] = gemvq_kv_create(ctx, c.n_ctx, c.n_head_kv, c.head_dim);
+        if (m->kv[il] < 0) {
+            delete m;
+            return nullptr;
+        }
+    }
+    // ggml's rope cache for every position (theta advanced by theta *= base^(-2 / n_rot), ggml-xrt.cpp:875-946
+    // with ext_factor 0): cos and sin of pair i at 2i, 2i + 1
+    std::vector<float> rope(size_t(c.n_ctx) * c.n_rot);
+    const float theta_scale = std::pow(c.rope_base, -2.0f / float(c.n_rot));
+    for (int p = 0; p < c.n_ctx; ++p) {
+        float theta = float(p);
+        for (int i0 = 0; i0 < c.n_rot; i0 += 2) {
+            rope[size_t(p) * c.n_rot + i0] = std::cos(theta);
+            rope[size_t(p) * c.n_rot + i0 + 1] = std::sin(theta);
+            theta *= theta_scale;
+        }
+    }
+    std::string err;
+    if (gemvq_act_write(ctx, m->rope, rope.data(), rope.size()) || !build_commands(*m, err)) {
+        if (!err.empty()) set_err(ctx, err);
+        delete m;
+        return nullptr;
+    }
+    if (gemvq_graph_create(ctx, m->cmds.data(), unsigned(m->cmds.size() / GEMVQ_CMD_WORDS), &m->graph)) {
+        delete m;
+        return nullptr;
+    }
+    return m;
+}
+
+void gemvq_qwen35_destroy(gemvq_qwen35 * m) {
+    if (!m) return;
+    if (m->graph >= 0) gemvq_graph_destroy(m->ctx, m->graph);
+    delete m;
+}
+
+int gemvq_qwen35_reset(gemvq_qwen35 * m, const int32_t * prompt, int n) {
+    if (!m || !prompt || n < 1 || n > m->c.n_ctx) return GEMVQ_EINVAL;
+    gemvq_ctx * ctx = m->ctx;
+    int st = gemvq_sync(ctx);
+    if (!st) st = gemvq_state_clear(ctx);
+    if (!st) st = gemvq_kv_clear(ctx);
+    const int ch = conv_ch(m->c);
+    std::vector<float> zeros(size_t(ch) * 3, 0.0f);
+    for (int il = 0; il < m->c.n_layer && !st; ++il)
+        if (!is_attn(m->c, il)) st = gemvq_act_write(ctx, m->conv_state[il], zeros.data(), zeros.size());
+    std::vector<int32_t> p(size_t(m->c.n_ctx), 0);
+    std::memcpy(p.data(), prompt, size_t(n) * 4);
+    if (!st) st = gemvq_act_write(ctx, m->prompt, p.data(), p.size());
+    std::vector<int32_t> o(size_t(m->c.n_ctx) + 16, -1);
+    o[0] = prompt[0];
+    if (!st) st = gemvq_act_write(ctx, m->out, o.data(), o.size());
+    const int32_t scal[48] = {};
+    if (!st) st = gemvq_act_write(ctx, 16, scal, 48);
+    if (!st) st = gemvq_act_write(ctx, m->tok, &prompt[0], 1);
+    if (st) return st;
+    // NEXT_TOKEN reads the prompt length from its command; rebuild the graph when it changes
+    const size_t last = m->cmds.size() - GEMVQ_CMD_WORDS;
+    if (m->cmds[last + 5] != uint32_t(n)) {
+        m->cmds[last + 5] = uint32_t(n);
+        if (m->graph >= 0) gemvq_graph_destroy(ctx, m->graph);
+        m->graph = -1;
+        st = gemvq_graph_create(ctx, m->cmds.data(), unsigned(m->cmds.size() / GEMVQ_CMD_WORDS), &m->graph);
+    }
+    return st;
+}
+
+int gemvq_qwen35_step(gemvq_qwen35 * m, int n) {
+    if (!m || m->graph < 0) return GEMVQ_EINVAL;
+    return gemvq_graph_replay(m->ctx, m->graph, n);
+}
+
+int gemvq_qwen35_tokens(gemvq_qwen35 * m, int32_t * out, int n) {
+    if (!m || !out || n < 0 || n > m->c.n_ctx) return GEMVQ_EINVAL;
+    return gemvq_act_read(m->ctx, m->out, out, size_t(n));
+}
+
+int gemvq_qwen35_logits(gemvq_qwen35 * m, float * out) {
+    if (!m || !out) return GEMVQ_EINVAL;
+    return gemvq_act_read(m->ctx, m->logits, out, size_t(m->c.n_vocab));
+}
+
+int gemvq_qwen35_hidden(gemvq_qwen35 * m, float * out) {
+    if (!m || !out) return GEMVQ_EINVAL;
+    return gemvq_act_read(m->ctx, m->h, out, size_t(m->c.n_embd));
+}
+
+int gemvq_qwen35_commands(gemvq_qwen35 * m, uint32_t * words, size_t n_words) {
+    if (!m) return GEMVQ_EINVAL;
+    if (words && n_words >= m->cmds.size()) std::memcpy(words, m->cmds.data(), m->cmds.size() * 4);
+    return int(m->cmds.size() / GEMVQ_CMD_WORDS);
+}
+
+int gemvq_qwen35_graph(gemvq_qwen35 * m) { return m ? m->graph : -1; }
+
+}  // extern "C"

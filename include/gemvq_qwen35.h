@@ -1,0 +1,63 @@
+/* Batch-1 greedy decode of a Qwen3.5-shaped hybrid model (Gated DeltaNet and gated-attention layers in a fixed
+ * interval) on the command-list backend of gemvq_hip.h.
+ *
+ * This is the work the reference's ggml backend does for every token (ggml-xrt.cpp:2190-2745: node fusion into
+ * command lists, operand placement in the activation buffer, GDN state traffic), done once: the model's per-token
+ * command list is built at create time, validated, and captured as one hipGraph. A token is one replay. The token
+ * id, its position and the greedy argmax stay on the device (NEXT_TOKEN), so a whole prompt + generation is a
+ * sequence of replays with no host round trip. Tensor names follow GGUF / llama.cpp's qwen35 conventions. */
+#ifndef GEMVQ_QWEN35_H
+#define GEMVQ_QWEN35_H
+#include <stddef.h>
+#include <stdint.h>
+
+#include "gemvq_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct {
+    int32_t n_layer, n_embd, n_ff, n_vocab;
+    int32_t n_head, n_head_kv, head_dim, n_rot;
+    int32_t ssm_k_heads, ssm_v_heads, ssm_head_dim, ssm_conv;
+    int32_t attn_interval, n_ctx;  /* layer il is full attention when (il + 1) % attn_interval == 0 */
+    float eps, rope_base;
+} gemvq_qw_config;
+
+/* One tensor of a model blob (GGUF-style): ggml type id, ne0 = columns, ne1 = rows, byte offset and size. */
+typedef struct {
+    char name[64];
+    int32_t type, ne0, ne1, pad;
+    uint64_t offset, nbytes;
+} gemvq_tensor_desc;
+
+typedef struct gemvq_qwen35 gemvq_qwen35;
+
+/* Context sizes a model needs (activation floats, weight bytes, GDN state rows). */
+int gemvq_qwen35_sizes(const gemvq_qw_config * cfg, const gemvq_tensor_desc * table, int n_tensors,
+                       size_t * act_floats, size_t * weight_bytes, size_t * state_rows);
+/* Uploads the weights into ctx, allocates KV buffers, lays out the activation buffer and captures the per-token
+ * graph. Returns NULL on failure (gemvq_last_error(ctx) says why). */
+gemvq_qwen35 * gemvq_qwen35_create(gemvq_ctx * ctx, const gemvq_qw_config * cfg, const gemvq_tensor_desc * table,
+                                   int n_tensors, const uint8_t * blob);
+void gemvq_qwen35_destroy(gemvq_qwen35 * m);
+/* Clears recurrent states and KV, stores the prompt (n >= 1 ids) and sets position 0 with token prompt[0]. */
+int gemvq_qwen35_reset(gemvq_qwen35 * m, const int32_t * prompt, int n);
+/* Enqueues n decode steps (graph replays); asynchronous. */
+int gemvq_qwen35_step(gemvq_qwen35 * m, int n);
+/* Token ids at positions 0 .. n - 1 (prompt tokens, then generated ones); synchronizes. */
+int gemvq_qwen35_tokens(gemvq_qwen35 * m, int32_t * out, int n);
+/* Logits of the last step (n_vocab floats); synchronizes. */
+int gemvq_qwen35_logits(gemvq_qwen35 * m, float * out);
+/* Hidden state after the last layer of the last step (n_embd floats); synchronizes. */
+int gemvq_qwen35_hidden(gemvq_qwen35 * m, float * out);
+/* The per-token command list (words) and the number of commands; n_words = 0 queries the size. */
+int gemvq_qwen35_commands(gemvq_qwen35 * m, uint32_t * words, size_t n_words);
+/* The captured graph id (for gemvq_graph_time). */
+int gemvq_qwen35_graph(gemvq_qwen35 * m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -233,3 +233,48 @@ def dequant_row_q6_K(row: np.ndarray, cols: int) -> np.ndarray:
 def f2h(x: np.ndarray) -> np.ndarray:
     o = orc()
     return np.array([o.orc_float_to_half(float(v)) for v in np.asarray(x, F).ravel()], np.uint16)
+
+
+class Model:
+    """The oracle decoder (qwen35_oracle.c) on the same tensor table and blob as the GPU model."""
+
+    def __init__(self, cfg_c, table, n: int, data: np.ndarray, threads: int = 0):
+        self.lib = orc()
+        self.data = data  # keep the blob alive
+        self.n_vocab = cfg_c.n_vocab
+        self.n_embd = cfg_c.n_embd
+        threads = threads or min(16, os.cpu_count() or 1)
+        self.h = self.lib.orc_model_create(C.byref(cfg_c), table, n, data.ctypes.data, threads)
+        if not self.h:
+            raise RuntimeError("orc_model_create failed")
+
+    def decode(self, token: int, pos: int, logits: np.ndarray | None = None) -> int:
+        r = self.lib.orc_model_decode(self.h, int(token), int(pos), _p(logits) if logits is not None else None)
+        if r < 0:
+            raise RuntimeError("orc_model_decode failed")
+        return r
+
+    def hidden(self) -> np.ndarray:
+        p = self.lib.orc_model_hidden(self.h)
+        return np.ctypeslib.as_array(p, shape=(self.n_embd,)).copy()
+
+    def generate(self, prompt: np.ndarray, n_gen: int) -> np.ndarray:
+        toks = [int(t) for t in prompt]
+        cur = toks[0]
+        for pos in range(len(prompt) - 1 + n_gen):
+            nxt = self.decode(cur, pos)
+            cur = toks[pos + 1] if pos + 1 < len(prompt) else nxt
+            if pos + 1 >= len(prompt):
+                toks.append(nxt)
+        return np.array(toks, np.int32)
+
+    def close(self):
+        if self.h:
+            self.lib.orc_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,260 @@
+"""Every opcode and fused epilog on the GPU through the C ABI, bit-exact against the oracle (the canonical
+arithmetic), plus the reference CPU path's tolerances where the reference defines them."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def assert_bits(got, want, what=""):
+    got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    bad = np.nonzero(got.view(np.uint32) != want.view(np.uint32))[0]
+    assert bad.size == 0, f"{what}: {bad.size}/{want.size} differ; first {bad[:4]}: got {got[bad[:4]]} want {want[bad[:4]]}"
+
+
+@pytest.fixture()
+def ctx(gq):
+    c = gq.Context(act_floats=1 << 20, weight_bytes=1 << 27, state_rows=64 * 128)
+    yield c
+    c.close()
+
+
+def test_features(gq, ctx):
+    assert ctx.run([]) == 0
+    f = ctx.read(0, 2, np.uint32)
+    assert f[0] >> 16 == 0x6B51 and f[1] >> 16 == 0x6B52
+    assert tuple(int(v) for v in f) == ctx.features()
+
+
+def test_rmsnorm_rows_strided_l2(gq, orc, ctx):
+    n, rows = 4096, 1
+    x = gq.normal(0, 11, 16384) * 3
+    w = gq.uniform(0, 12, 16384, 0.5, 1.5)
+    ctx.write(0, x)
+    ctx.write(16384, w)
+    for n, rows, flags, stride in [(4096, 1, 0, 0), (2560, 1, 0, 0), (12288, 1, 0, 0), (128, 16, 0, 0),
+                                   (256, 8, 0, 2 * 256), (128, 32, gq.NORM_L2 | gq.NORM_NO_WEIGHT, 0),
+                                   (16384, 1, gq.NORM_NO_WEIGHT, 0)]:
+        cmd = gq.rmsnorm(n, 0, 16384, 32768, 1e-6, rows=rows, flags=flags, stride_words=stride // 16)
+        assert ctx.run(cmd) == 0, ctx.error()
+        y = ctx.read(32768, n * rows)
+        want = orc.rownorm(x, None if flags & gq.NORM_NO_WEIGHT else w[:n], n, rows, 1e-6, flags, stride)
+        assert_bits(y, want, f"rmsnorm n={n} rows={rows} flags={flags}")
+        if flags == 0 and stride == 0:  # the reference CPU path (double sums) within its element-wise tolerance
+            ref = np.empty(n * rows, np.float32)
+            orc.orc().orc_ref_rownorm(x.ctypes.data, w.ctypes.data, n, rows, 1e-6, 0, ref.ctypes.data)
+            assert np.all(np.abs(y - ref) <= 1e-6 + 2e-5 * np.abs(ref))
+
+
+def test_elementwise(gq, orc, ctx):
+    n = 4096
+    a = gq.normal(0, 21, n) * 4
+    b = gq.normal(0, 22, n)
+    a[:8] = [0.0, -0.0, 20.0, 20.5, -87.5, 88.0, -20.0, 1e-3]
+    ctx.write(0, a)
+    ctx.write(n, b)
+    checks = [
+        (gq.add(n, 0, n, 2 * n), a + b),
+        (gq.mul(n, 0, n, 2 * n), a * b),
+        (gq.silu_mul(n, 0, n, 2 * n), orc.silu_mul(a, b)),
+        (gq.silu_mul(n, 0, n, 2 * n, sigmoid=True), orc.silu_mul(a, b, sigmoid=True)),
+        (gq.unary(n, 0, gq.UNARY_SILU, 2 * n), orc.unary(a, 1)),
+        (gq.unary(n, 0, gq.UNARY_SIGMOID, 2 * n), orc.unary(a, 2)),
+        (gq.unary(n, 0, gq.UNARY_SOFTPLUS, 2 * n), orc.unary(a, 3)),
+        (gq.unary(n, 0, gq.UNARY_COPY, 2 * n), a),
+        (gq.fill(n, 2 * n, 0.25), np.full(n, 0.25, np.float32)),
+    ]
+    for c, want in checks:
+        assert ctx.run(c) == 0, ctx.error()
+        assert_bits(ctx.read(2 * n, n), want, f"op {c[0]} flags {c[5]}")
+    # strided rows: 16 rows of 128 every 256 floats
+    assert ctx.run(gq.unary(2048, 0, gq.UNARY_SIGMOID, 2 * n, row=128, stride=256)) == 0
+    strided = a.reshape(16, 256)[:, :128].ravel()
+    assert_bits(ctx.read(2 * n, 2048), orc.unary(strided, 2), "strided unary")
+    assert ctx.run(gq.silu_mul(2048, 0, n, 2 * n, sigmoid=True, row=128, stride=256)) == 0
+    assert_bits(ctx.read(2 * n, 2048), orc.silu_mul(strided, b[:2048], sigmoid=True), "strided silu_mul")
+
+
+def test_conv_and_rope(gq, orc, ctx):
+    ch = 8192
+    st = gq.normal(0, 31, 3 * ch)
+    x = gq.normal(0, 32, ch)
+    w = gq.normal(0, 33, 4 * ch) * 0.5
+    ctx.write(0, x)
+    ctx.write(ch, w)
+    ctx.write(5 * ch, st)
+    assert ctx.run(gq.conv(ch, 0, ch, 8 * ch, 5 * ch, 5 * ch, silu=True)) == 0, ctx.error()
+    y, ns = orc.conv(st, x, w, silu=True)
+    assert_bits(ctx.read(8 * ch, ch), y, "conv y")
+    assert_bits(ctx.read(5 * ch, 3 * ch), ns, "conv state (in place)")
+    # RoPE NEOX on 20 heads of 256, first 64 dims, cache from the position table
+    ne0, rows, nd = 256, 20, 64
+    xr = gq.normal(0, 34, ne0 * rows)
+    table = np.concatenate([orc.rope_cache(p, nd, 1e7) for p in range(40)])
+    ctx.write(0, xr)
+    ctx.write(1 << 14, table)
+    ctx.write(1 << 15, np.array([37], np.int32))
+    assert ctx.run(gq.rope(nd, 0, 1 << 14, 1 << 16, ne0, rows, pos_off=1 << 15)) == 0, ctx.error()
+    assert_bits(ctx.read(1 << 16, ne0 * rows), orc.rope(xr, table[37 * nd:38 * nd], nd, ne0, rows), "rope")
+
+
+@pytest.mark.parametrize("flags,hv,hk", [(0, 4, 2), (2 | 4 | 8, 32, 16), (2 | 8, 8, 8), (4, 2, 1)])
+def test_gdn_step(gq, orc, ctx, flags, hv, hk):
+    S = 128
+    q = gq.normal(1, 41, hk * S)
+    k = gq.normal(1, 42, hk * S)
+    if not flags & 2:  # unnormalized q/k: keep the state bounded as the model would
+        q /= np.linalg.norm(q.reshape(hk, S), axis=1).repeat(S)
+        k /= np.linalg.norm(k.reshape(hk, S), axis=1).repeat(S)
+    v = gq.normal(1, 43, hv * S)
+    g = gq.normal(1, 44, hv) if flags & 8 else -np.log1p(np.exp(gq.normal(1, 44, hv))).astype(np.float32)
+    beta = gq.normal(1, 45, hv) if flags & 8 else (1 / (1 + np.exp(-gq.normal(1, 45, hv)))).astype(np.float32)
+    dt, a = gq.normal(1, 46, hv), -np.abs(gq.normal(1, 47, hv))
+    z = gq.normal(1, 48, hv * S)
+    w = gq.uniform(1, 49, S, 0.5, 1.5)
+    state = gq.normal(1, 50, hv * S * S) * 0.1
+    offs = dict(q=0, k=4096, v=8192, g=16384, beta=16384 + 64, y=20480, w=24576, z=24576 + 128, dt=32768, a=32768 + 64)
+    for name, arr in dict(q=q, k=k, v=v, g=g, beta=beta, w=w, z=z, dt=dt, a=a).items():
+        ctx.write(offs[name], arr)
+    ctx.state_write(128, state)
+    c = gq.gdn(hv, hk, offs["q"], offs["k"], offs["v"], offs["g"], offs["beta"], offs["y"], 128, 128,
+               1 / np.sqrt(S), flags, 1e-6, 1e-6, offs["w"], offs["z"], offs["dt"], offs["a"])
+    assert ctx.run(c) == 0, ctx.error()
+    y_want, st_want = orc.gdn(state, q, k, v, g, beta, hv, hk, float(1 / np.sqrt(S)), flags, dt, a, z, w)
+    assert_bits(ctx.read(offs["y"], hv * S), y_want, "gdn y")
+    assert_bits(ctx.state_read(128, hv * 128), st_want, "gdn state")
+    if flags == 0:  # the reference CPU step (gemvq_ref.h:363-397) within its rounding-aware tolerance
+        st_ref = state.copy()
+        y_ref = np.empty(hv * S, np.float32)
+        ymag = np.empty(hv * S)
+        orc.orc().orc_ref_gdn(st_ref.ctypes.data, q.ctypes.data, k.ctypes.data, v.ctypes.data, g.ctypes.data,
+                              beta.ctypes.data, hv, hk, float(1 / np.sqrt(S)), y_ref.ctypes.data, ymag.ctypes.data, None)
+        assert np.all(np.abs(y_want - y_ref) <= 1e-6 + 4e-6 * ymag)
+
+
+def test_attention(gq, orc, ctx):
+    nh, nkv, hd, nrot, n_ctx = 16, 4, 256, 64, 200
+    kv = ctx.kv_create(n_ctx, nkv, hd)
+    qn = gq.uniform(2, 51, hd, 0.5, 1.5)
+    kn = gq.uniform(2, 52, hd, 0.5, 1.5)
+    table = np.concatenate([orc.rope_cache(p, nrot, 1e7) for p in range(n_ctx)])
+    O = dict(qg=0, k=8192, v=9216, qn=10240, kn=10496, cs=16384, pos=65536, y=70000 // 16 * 16)
+    ctx.write(O["qn"], qn)
+    ctx.write(O["kn"], kn)
+    ctx.write(O["cs"], table)
+    kc = np.zeros((n_ctx, nkv, hd), np.uint16)
+    vc = np.zeros((n_ctx, nkv, hd), np.uint16)
+    for pos in range(130):  # crosses two chunk boundaries
+        qg = gq.normal(3, 1000 + pos, 2 * nh * hd)
+        k = gq.normal(3, 5000 + pos, nkv * hd)
+        v = gq.normal(3, 9000 + pos, nkv * hd)
+        ctx.write(O["qg"], qg)
+        ctx.write(O["k"], k)
+        ctx.write(O["v"], v)
+        ctx.write(O["pos"], np.array([pos], np.int32))
+        c = gq.attn(nh, nkv, O["qg"], kv, O["y"], hd, nrot, O["pos"], O["k"], O["v"], 1 / 16, 1e-6, O["qn"],
+                    O["kn"], O["cs"], gate=O["qg"] + hd)
+        assert ctx.run(c) == 0, ctx.error()
+        cs = table[pos * nrot:(pos + 1) * nrot]
+        qh = orc.rope(orc.rownorm(qg, qn, hd, nh, 1e-6, 0, 2 * hd), cs, nrot, hd, nh)
+        kh = orc.rope(orc.rownorm(k, kn, hd, nkv, 1e-6), cs, nrot, hd, nkv)
+        kc[pos] = orc.f2h(kh).reshape(nkv, hd)
+        vc[pos] = orc.f2h(v).reshape(nkv, hd)
+        if pos in (0, 1, 63, 64, 65, 127, 128, 129):
+            att = orc.attn(qh, kc, vc, nh, nkv, hd, pos + 1, 1 / 16)
+            gate = qg.reshape(nh, 2 * hd)[:, hd:].ravel()
+            want = orc.silu_mul(gate, att, sigmoid=True)
+            assert_bits(ctx.read(O["y"], nh * hd), want, f"attention at pos {pos}")
+    k_dev, v_dev = ctx.kv_read(kv, 0, 130, nkv * hd)
+    assert np.array_equal(k_dev, kc[:130].ravel()) and np.array_equal(v_dev, vc[:130].ravel())
+
+
+def test_gemv_fused_epilogs(gq, orc, ctx):
+    """SwiGLU pair, residual ADD, CONV, ARGMAX epilogs and the deferred norm fold (gemvqc16.h:31-51)."""
+    E, F = 2560, 9728
+    eps = 1e-6
+    x = gq.normal(0, 61, E)
+    r = gq.normal(0, 62, E)
+    nw = gq.uniform(0, 63, E, 0.5, 1.5)
+    wg = gq.matrix(gq.Q8_0, F, E, 0, 64)
+    wu = gq.matrix(gq.Q8_0, F, E, 0, 65)
+    wd = gq.matrix(gq.Q8_0, E, F, 0, 66)
+    og, ou, od = (ctx.upload(gq.Q8_0, a, b, w) for a, b, w in ((F, E, wg), (F, E, wu), (E, F, wd)))
+    X, R, NW, XN, ACT, T, Y = 0, 4096, 8192, 12288, 16384, 32768, 36864
+    ctx.write(X, x)
+    ctx.write(R, r)
+    ctx.write(NW, nw)
+    cmds = (gq.rmsnorm(E, X, NW, XN, eps, flags=gq.NORM_DEFER) + gq.gemv(gq.Q8_0, F, E, og, XN, ACT, gq.GEMV_SWIGLU) +
+            gq.gemv(gq.Q8_0, F, E, ou, XN, ACT) + gq.gemv(gq.Q8_0, E, F, od, ACT, T, gq.GEMV_ADD) + gq.add(E, T, R, Y))
+    assert ctx.run(cmds) == 0, ctx.error()
+    assert ctx.launch_count() == 2
+    xn = orc.rownorm(x, nw, E, 1, eps)
+    g = orc.fx_gemv(gq.Q8_0, wg, xn, F, E)
+    u = orc.fx_gemv(gq.Q8_0, wu, xn, F, E)
+    act = orc.silu_mul(g, u)
+    assert_bits(ctx.read(ACT, F), act, "swiglu")
+    want = orc.fx_gemv(gq.Q8_0, wd, act, E, F) + r
+    assert_bits(ctx.read(Y, E), want, "down + residual")
+    # conv epilog on a Q4_0 GEMV, in-place state
+    ch, K = 512, 256
+    wc = gq.matrix(gq.Q4_0, ch, K, 0, 67)
+    oc = ctx.upload(gq.Q4_0, ch, K, wc)
+    xc = gq.normal(0, 68, K)
+    st = gq.normal(0, 69, 3 * ch)
+    kw = gq.normal(0, 70, 4 * ch)
+    ctx.write(X, xc)
+    ctx.write(40960, kw)
+    ctx.write(49152, st)
+    cmds = gq.gemv(gq.Q4_0, ch, K, oc, X, T, gq.GEMV_CONV) + gq.conv(ch, T, 40960, Y, 49152, 49152)
+    assert ctx.run(cmds) == 0, ctx.error()
+    yc, ns = orc.conv(st, orc.fx_gemv(gq.Q4_0, wc, xc, ch, K), kw)
+    assert_bits(ctx.read(Y, ch), yc, "conv epilog")
+    assert_bits(ctx.read(49152, 3 * ch), ns, "conv epilog state")
+    # argmax epilog on a Q6_K head with an L2 deferred norm (no weight); ties resolve to the first index
+    V, D = 3000, 512
+    wh = gq.matrix(gq.Q6_K, V, D, 0, 71)
+    oh = ctx.upload(gq.Q6_K, V, D, wh)
+    xh = gq.normal(0, 72, D)
+    ctx.write(X, xh)
+    ctx.write(65536, np.zeros(16, np.float32))
+    cmds = (gq.rmsnorm(D, X, 0, XN, 1e-6, flags=gq.NORM_DEFER | gq.NORM_L2 | gq.NORM_NO_WEIGHT) +
+            gq.gemv(gq.Q6_K, V, D, oh, XN, ACT, gq.GEMV_ARGMAX) + gq.argmax(V, ACT, 65536))
+    assert ctx.run(cmds) == 0, ctx.error()
+    logits = orc.fx_gemv(gq.Q6_K, wh, orc.rownorm(xh, None, D, 1, 1e-6, 3), V, D)
+    assert_bits(ctx.read(ACT, V), logits, "head logits")
+    key = ctx.read(65536, 2, np.uint32)
+    assert 0xFFFFFFFF - int(key[0]) == int(np.argmax(logits))
+
+
+def test_get_rows_and_next_token(gq, orc, ctx):
+    V, D = 1000, 1024
+    w = gq.matrix(gq.Q6_K, V, D, 0, 81)
+    o = ctx.upload(gq.Q6_K, V, D, w)
+    ctx.write(0, np.array([777], np.int32))
+    assert ctx.run(gq.get_rows(gq.Q6_K, V, D, o, 0, 1024)) == 0, ctx.error()
+    rb = gq.row_bytes(gq.Q6_K, D)
+    assert_bits(ctx.read(1024, D), orc.dequant_row_q6_K(w[777 * rb:778 * rb], D), "get_rows Q6_K")
+    # NEXT_TOKEN: prompt phase then the argmax key
+    KEY, TOK, POS, PR, OUT = 4096, 4112, 4128, 4144, 4400
+    ctx.write(PR, np.array([5, 6, 7], np.int32))
+    ctx.write(POS, np.array([0], np.int32))
+    ctx.write(KEY, np.array([0, 0], np.uint32))
+    c = gq.next_token(KEY, TOK, POS, PR, 3, OUT)
+    assert ctx.run(c) == 0
+    assert ctx.read(TOK, 1, np.int32)[0] == 6 and ctx.read(POS, 1, np.int32)[0] == 1
+    ctx.write(POS, np.array([2], np.int32))
+    key_lo = 0xFFFFFFFF - 42
+    ctx.write(KEY, np.array([key_lo, 0x80000000], np.uint32))
+    assert ctx.run(c) == 0
+    assert ctx.read(TOK, 1, np.int32)[0] == 42 and ctx.read(OUT + 3, 1, np.int32)[0] == 42
+    assert tuple(ctx.read(KEY, 2, np.uint32)) == (0, 0)
+
+
+def test_invalid_commands_rejected(gq, ctx):
+    """Validation returns the 1-based index of the first bad command and runs nothing (gemvqc16.cpp:455-466)."""
+    good = gq.fill(16, 0, 1.0)
+    assert ctx.run(good + gq.cmd(99)) == 2
+    assert ctx.run(good + good + gq.gemv(gq.Q4_0, 16, 256, 123456, 0, 256)) == 3  # unknown weight
+    assert ctx.run(gq.add(16, 3, 0, 32)) == 1                                      # misaligned offset
+    assert ctx.run(gq.add(16, 0, 0, ctx.act_floats)) == 1                          # out of range
+    assert ctx.run(gq.gdn(64, 3, 0, 0, 0, 0, 0, 0, 0, 0, 1.0)) == 1                # hv not a multiple of hk
