@@ -111,12 +111,37 @@ __device__ __forceinline__ float silu_(float x) { return x / (1.0f + expf_(-x));
 __device__ __forceinline__ float sigmoid_(float x) { return 1.0f / (1.0f + expf_(-x)); }
 __device__ __forceinline__ float softplus_(float x) { return x > 20.0f ? x : logf_(1.0f + expf_(x)); }
 
-// Pairwise (adjacent-pair tree) sums. Lane l holds element l of an aligned group of `width` lanes: after the xor
-// steps 1, 2, 4, .. every lane of the group holds the tree sum (a + b == b + a bitwise, so both lanes of a pair agree).
+// Cross-lane moves through DPP (in-VALU, no LDS round trip). quad_perm [1,0,3,2] and [2,3,0,1] swap neighbours at
+// distance 1 and 2; row_half_mirror (lane i <- 7 - i within 8) and row_mirror (i <- 15 - i within 16) act as the
+// swaps at distance 4 and 8 once every aligned group below that size holds one value.
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(dpp_i32<CTRL>(__float_as_int(v)));
+}
+template <int CTRL>
+__device__ __forceinline__ long long dpp_i64(long long v) {
+    const int lo = dpp_i32<CTRL>(int(uint32_t(uint64_t(v))));
+    const int hi = dpp_i32<CTRL>(int(uint64_t(v) >> 32));
+    return (long long)((uint64_t(uint32_t(hi)) << 32) | uint32_t(lo));
+}
+
+// Pairwise (adjacent-pair tree) sums. Lane l holds element l of an aligned group of `width` lanes: after the steps
+// at distance 1, 2, 4, .. every lane of the group holds the tree sum (a + b == b + a bitwise, so both lanes of a
+// pair agree).
 template <int WIDTH>
 __device__ __forceinline__ float pair_sum_lanes(float v) {
+    if (WIDTH > 1) v = v + dpp_f32<DPP_XOR1>(v);
+    if (WIDTH > 2) v = v + dpp_f32<DPP_XOR2>(v);
+    if (WIDTH > 4) v = v + dpp_f32<DPP_HALF_MIRROR>(v);
+    if (WIDTH > 8) v = v + dpp_f32<DPP_MIRROR>(v);
 #pragma unroll
-    for (int s = 1; s < WIDTH; s <<= 1) v = v + __shfl_xor(v, s, WAVE);
+    for (int s = 16; s < WIDTH; s <<= 1) v = v + __shfl_xor(v, s, WAVE);
     return v;
 }
 
@@ -130,16 +155,32 @@ __device__ __forceinline__ float tree(float * v) {
     return v[0];
 }
 
+__device__ __forceinline__ long long readlane_i64(long long v, int lane) {
+    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(uint64_t(v))), lane));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint64_t(v) >> 32), lane));
+    return (long long)((uint64_t(hi) << 32) | lo);
+}
+
+// Exact integer sum over the wave (any order gives the same result); uniform result.
 __device__ __forceinline__ long long wave_sum_i64(long long v) {
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) v += __shfl_xor(v, s, WAVE);
-    return v;
+    v += dpp_i64<DPP_XOR1>(v);
+    v += dpp_i64<DPP_XOR2>(v);
+    v += dpp_i64<DPP_HALF_MIRROR>(v);
+    v += dpp_i64<DPP_MIRROR>(v);
+    return (readlane_i64(v, 0) + readlane_i64(v, 16)) + (readlane_i64(v, 32) + readlane_i64(v, 48));
 }
 
 __device__ __forceinline__ int sum_lanes4_i32(int v) {
-    v += __shfl_xor(v, 1, WAVE);
-    v += __shfl_xor(v, 2, WAVE);
+    v += dpp_i32<DPP_XOR1>(v);
+    v += dpp_i32<DPP_XOR2>(v);
     return v;
+}
+
+// An integer-valued double with |d| < 2^53 as int64 (exact).
+__device__ __forceinline__ long long dint_to_i64(double d) {
+    const double hi = floor(d * 2.3283064365386963e-10);  // d / 2^32
+    const double lo = d - hi * 4294967296.0;              // 0 <= lo < 2^32, exact
+    return (long long)((uint64_t(uint32_t(int(hi))) << 32) + uint64_t(uint32_t(lo)));
 }
 
 // Fixed-point term of the reference kernel (gemvqw_engine.h:352-445): floor(s * m * 2^(e + 40)) for the signed

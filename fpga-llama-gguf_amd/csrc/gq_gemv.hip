@@ -22,7 +22,7 @@ struct Lds {
     int8_t xq[MAXK];           // quantized activation
     uint32_t info[MAXK / 32];  // Q8_0: fp16 scale | (sum of the block's quants) << 16; Q8_K: FP32 d bits per super-block
     int16_t bs[MAXK / 16];     // Q8_K bsums
-    float red[NWAVES + 64];
+    float red[2 * NWAVES + 64];
     unsigned long long key[NWAVES];
 };
 
@@ -62,57 +62,116 @@ __device__ float block_norm_scale(const float * x, int n, float eps, int l2, Lds
     return l2 ? 1.0f / fmaxf(sqrtf(sum), eps) : 1.0f / sqrtf(sum / float(n) + eps);
 }
 
-// Q8_0 of the activation (gemvq_ref.h:236-245): one thread per 32-block.
-__device__ void quantize_q8_0(const GemvArgs & a, float scale, Lds & s) {
-    const int nb = a.cols / 32;
-    for (int b = threadIdx.x; b < nb; b += NT) {
-        float v[32];
-        const float4 * p = reinterpret_cast<const float4 *>(a.x + size_t(b) * 32);
+// Q8_0 of the activation (gemvq_ref.h:236-245), one thread per 32-block, rounds of 256 blocks. With a deferred
+// norm the blocks stay in registers while the sum of squares is reduced: tree over the block's 32 squares, pairwise
+// over the 64 blocks of a wave, the 4 waves of a round, and the rounds (at most 2 here: n <= 16384), which is the
+// canonical pairwise tree over all n elements; then v = (x * scale) * w is quantized.
+__device__ __forceinline__ void load_block(const float * p, float * v) {
+    const float4 * q = reinterpret_cast<const float4 *>(p);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float4 t = p[i];
-            v[4 * i] = t.x;
-            v[4 * i + 1] = t.y;
-            v[4 * i + 2] = t.z;
-            v[4 * i + 3] = t.w;
+    for (int i = 0; i < 8; ++i) {
+        const float4 t = q[i];
+        v[4 * i] = t.x;
+        v[4 * i + 1] = t.y;
+        v[4 * i + 2] = t.z;
+        v[4 * i + 3] = t.w;
+    }
+}
+
+__device__ __forceinline__ void quantize_block(const float * v, int b, Lds & s) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t packed[8];
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int q = int(roundf(v[4 * i + j] * id));
+            sum += q;
+            w |= (uint32_t(q) & 0xffu) << (8 * j);
         }
-        if (a.xsrc == XSRC_NORM) {
-            if (a.norm_w) {
-                const float4 * wp = reinterpret_cast<const float4 *>(a.norm_w + size_t(b) * 32);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float4 t = wp[i];
-                    v[4 * i] = (v[4 * i] * scale) * t.x;
-                    v[4 * i + 1] = (v[4 * i + 1] * scale) * t.y;
-                    v[4 * i + 2] = (v[4 * i + 2] * scale) * t.z;
-                    v[4 * i + 3] = (v[4 * i + 3] * scale) * t.w;
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < 32; ++j) v[j] = v[j] * scale;
-            }
+        packed[i] = w;
+    }
+    uint4 * dst = reinterpret_cast<uint4 *>(s.xq + size_t(b) * 32);
+    dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+    s.info[b] = f2h(d) | (uint32_t(sum & 0xffff) << 16);
+}
+
+template <int ROUNDS>  // rounds of 256 blocks the registers hold (cols <= 8192: 1)
+__device__ void prologue_q8_0(const GemvArgs & a, Lds & s) {
+    const int nb = a.cols / 32, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (a.xsrc != XSRC_NORM) {
+        for (int b = tid; b < nb; b += NT) {
+            float v[32];
+            load_block(a.x + size_t(b) * 32, v);
+            quantize_block(v, b, s);
         }
-        float amax = 0.0f;
+        return;
+    }
+    float v0[32], v1[ROUNDS > 1 ? 32 : 1];
+    const int b0 = tid, b1 = tid + NT;
+    float r0 = 0.0f, r1 = 0.0f;
+    {
+        float sq[32];
+        if (b0 < nb) {
+            load_block(a.x + size_t(b0) * 32, v0);
 #pragma unroll
-        for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
-        const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
-        uint32_t packed[8];
-        int sum = 0;
+            for (int j = 0; j < 32; ++j) sq[j] = v0[j] * v0[j];
+        } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            uint32_t w = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int q = int(roundf(v[4 * i + j] * id));
-                sum += q;
-                w |= (uint32_t(q) & 0xffu) << (8 * j);
-            }
-            packed[i] = w;
+            for (int j = 0; j < 32; ++j) v0[j] = sq[j] = 0.0f;
         }
-        uint4 * dst = reinterpret_cast<uint4 *>(s.xq + size_t(b) * 32);
-        dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-        dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
-        s.info[b] = f2h(d) | (uint32_t(sum & 0xffff) << 16);
+        r0 = pair_sum_lanes<64>(tree<32>(sq));
+    }
+    if constexpr (ROUNDS > 1) {
+        float sq[32];
+        if (b1 < nb) {
+            load_block(a.x + size_t(b1) * 32, v1);
+#pragma unroll
+            for (int j = 0; j < 32; ++j) sq[j] = v1[j] * v1[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 32; ++j) v1[j] = sq[j] = 0.0f;
+        }
+        r1 = pair_sum_lanes<64>(tree<32>(sq));
+    }
+    if (lane == 0) {
+        s.red[wave] = r0;
+        s.red[4 + wave] = r1;
+    }
+    __syncthreads();
+    const float sum = ((s.red[0] + s.red[1]) + (s.red[2] + s.red[3])) + ((s.red[4] + s.red[5]) + (s.red[6] + s.red[7]));
+    const float scale = a.norm_l2 ? 1.0f / fmaxf(sqrtf(sum), a.norm_eps) : 1.0f / sqrtf(sum / float(a.cols) + a.norm_eps);
+    if (b0 < nb) {
+        if (a.norm_w) {
+            float w[32];
+            load_block(a.norm_w + size_t(b0) * 32, w);
+#pragma unroll
+            for (int j = 0; j < 32; ++j) v0[j] = (v0[j] * scale) * w[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 32; ++j) v0[j] = v0[j] * scale;
+        }
+        quantize_block(v0, b0, s);
+    }
+    if constexpr (ROUNDS > 1) {
+      if (b1 < nb) {
+        if (a.norm_w) {
+            float w[32];
+            load_block(a.norm_w + size_t(b1) * 32, w);
+#pragma unroll
+            for (int j = 0; j < 32; ++j) v1[j] = (v1[j] * scale) * w[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 32; ++j) v1[j] = v1[j] * scale;
+        }
+        quantize_block(v1, b1, s);
+      }
     }
 }
 
@@ -178,7 +237,8 @@ __device__ void quantize_q8_K(const GemvArgs & a, float scale, Lds & s) {
 // ---- per-lane activation slices ----
 struct XB {  // one 32-block (Q4_0 / Q8_0)
     uint32_t q[8];
-    int m, e, neg, sum;
+    float dx40;  // the block's fp16 scale times 2^40 (exact)
+    int sum;     // sum of its quants (for the Q4_0 offset of 8)
 };
 struct XK {  // one 64-weight unit (Q5_K / Q6_K)
     uint32_t q[16];
@@ -194,13 +254,10 @@ __device__ __forceinline__ void load_xb(const Lds & s, int b, int nb, XB & x) {
     x.q[0] = lo.x; x.q[1] = lo.y; x.q[2] = lo.z; x.q[3] = lo.w;
     x.q[4] = hi.x; x.q[5] = hi.y; x.q[6] = hi.z; x.q[7] = hi.w;
     const uint32_t inf = s.info[b];
-    half_parts(inf & 0xffffu, x.m, x.e);
-    x.neg = (inf >> 15) & 1;
+    x.dx40 = h2f(inf & 0xffffu) * 1099511627776.0f;  // * 2^40
     x.sum = int(int16_t(inf >> 16));
 }
 
-// Unit u of a K-quant row: super-block u / 4, part u % 4. Q6_K part (n, p) = (u % 4 / 2, u % 2): weights
-// 128n + 32p + [0, 32) (group A) and 128n + 32p + 64 + [0, 32) (group B). Q5_K part j: weights 64j + [0, 64).
 template <int TYPE>
 __device__ __forceinline__ void load_xk(const Lds & s, int u, int nu, XK & x) {
     u = u < nu ? u : nu - 1;
@@ -240,10 +297,10 @@ struct WB {  // one 32-block: Q4_0 uses lo (16 quant bytes), Q8_0 lo and hi (32 
     uint32_t d;
 };
 struct WK {  // one 64-weight K-quant unit
-    uint4 a0, a1;       // Q6_K ql bytes / Q5_K qs bytes of the unit
-    uint4 h0, h1;       // high-bit bytes
+    uint4 a0, a1;         // Q6_K ql bytes / Q5_K qs bytes of the unit
+    uint4 h0, h1;         // high-bit bytes
     uint32_t s0, s1, s2;  // Q6_K: scale byte pairs of groups A and B; Q5_K: the 12 packed scale bytes
-    uint32_t d;         // Q6_K: d; Q5_K: d | dmin << 16
+    uint32_t d;           // Q6_K: d; Q5_K: d | dmin << 16
 };
 
 template <int TYPE>
@@ -276,13 +333,11 @@ __device__ __forceinline__ int dot_block(const WB & w, const XB & x) {
     return s;
 }
 
-// floor(sumi * dw * dx * 2^40) (gemvqw_engine.h:417-427).
-__device__ __forceinline__ long long block_term(int sumi, uint32_t dw, const XB & x) {
-    int mw, ew;
-    half_parts(dw, mw, ew);
-    const int neg = int((dw >> 15) & 1) ^ x.neg;
-    const long long p = (long long)(neg ? -sumi : sumi) * (long long)(mw * x.m);
-    return fixed_term(p, ew + x.e);
+// floor(sumi * dw * dx * 2^40) (gemvqw_engine.h:417-427) as an integer-valued double: dw * dx * 2^40 is exact in
+// FP32 (two 11-bit significands), its product with the 20-bit sumi exact in FP64, floor exact.
+__device__ __forceinline__ double block_term(int sumi, uint32_t dw, const XB & x) {
+    const float s = float(__builtin_bit_cast(_Float16, uint16_t(dw))) * x.dx40;  // exact conversion
+    return floor(double(sumi) * double(s));
 }
 
 template <int TYPE>
@@ -377,7 +432,8 @@ __device__ __forceinline__ void dot_unit(const WK & w, const XK & x, int part, i
     }
 }
 
-// floor(S * d * dx * 2^40) - floor(M * dmin * dx * 2^40) (gemvqw_engine.h:429-444).
+// floor(S * d * dx * 2^40) - floor(M * dmin * dx * 2^40) (gemvqw_engine.h:429-444), exact in int64 (the FP32 dx
+// has a 24-bit significand, so these products do not fit a double).
 template <int TYPE>
 __device__ __forceinline__ long long superblock_term(int S, int M, const WK & w, const XK & x) {
     int md, ed;
@@ -395,38 +451,77 @@ __device__ __forceinline__ long long superblock_term(int S, int M, const WK & w,
     return t;
 }
 
-// ---- one row ----
+// ---- rows: weight loads are issued one task ahead of the compute ----
 template <int TYPE, int NU>
-__device__ __forceinline__ long long row_blocks(const WeightView & w, int r, int nb, const XB * xb, int lane,
-                                                int32_t * dbg) {
-    WB wb[NU];
+struct Rows {
+    static constexpr bool KQ = TYPE == T_Q5_K || TYPE == T_Q6_K;
+    WB wb[KQ ? 1 : NU], wb2[KQ ? 1 : NU];  // g (or the matrix) and u of a SwiGLU pair
+    WK wk[KQ ? NU : 1], wk2[KQ ? NU : 1];
+    float e[8];  // epilog operands: ADD residual (e[0]); CONV state (e[0..2]) and kernel (e[4..7])
+};
+
+// Loads of one row (and its epilog operands), specialized by epilog kind so that no branch surrounds a load: a
+// load behind a branch, or issued after the next row's weights, makes the compute wait for every load before it.
+template <int TYPE, int NU, int EPI>
+__device__ __forceinline__ void load_row(const GemvMember & m, int r, int lane, int nb, int nu, Rows<TYPE, NU> & R) {
+    if constexpr (Rows<TYPE, NU>::KQ) {
+        const int nsb = nu >> 2;
 #pragma unroll
-    for (int k = 0; k < NU; ++k) {
-        const int b = lane + 64 * k;
-        load_wb<TYPE>(w, size_t(r) * nb + (b < nb ? b : nb - 1), wb[k]);
+        for (int k = 0; k < NU; ++k) {
+            const int u0 = lane + 64 * k, u = u0 < nu ? u0 : nu - 1;
+            load_wk<TYPE>(m.w, size_t(r) * nsb + (u >> 2), u & 3, R.wk[k]);
+            if constexpr (EPI == EPI_SWIGLU) load_wk<TYPE>(m.w2, size_t(r) * nsb + (u >> 2), u & 3, R.wk2[k]);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < NU; ++k) {
+            const int b = lane + 64 * k, bb = b < nb ? b : nb - 1;
+            load_wb<TYPE>(m.w, size_t(r) * nb + bb, R.wb[k]);
+            if constexpr (EPI == EPI_SWIGLU) load_wb<TYPE>(m.w2, size_t(r) * nb + bb, R.wb2[k]);
+        }
     }
-    long long acc = 0;
+    if constexpr (EPI == EPI_ADD) R.e[0] = m.res[r];
+    if constexpr (EPI == EPI_CONV) {
+        R.e[0] = m.conv_src[3 * r];
+        R.e[1] = m.conv_src[3 * r + 1];
+        R.e[2] = m.conv_src[3 * r + 2];
+        const float4 k = *reinterpret_cast<const float4 *>(m.conv_w + 4 * size_t(r));
+        R.e[4] = k.x;
+        R.e[5] = k.y;
+        R.e[6] = k.z;
+        R.e[7] = k.w;
+    }
+}
+
+template <int TYPE, int NU>
+__device__ __forceinline__ void load_row_any(const GemvMember & m, int r, int lane, int nb, int nu, Rows<TYPE, NU> & R) {
+    switch (m.epi) {
+    case EPI_SWIGLU: load_row<TYPE, NU, EPI_SWIGLU>(m, r, lane, nb, nu, R); break;
+    case EPI_ADD: load_row<TYPE, NU, EPI_ADD>(m, r, lane, nb, nu, R); break;
+    case EPI_CONV: load_row<TYPE, NU, EPI_CONV>(m, r, lane, nb, nu, R); break;
+    default: load_row<TYPE, NU, EPI_PLAIN>(m, r, lane, nb, nu, R); break;
+    }
+}
+
+template <int TYPE, int NU, bool DBG>
+__device__ __forceinline__ long long row_blocks(const WB * wb, int r, int nb, const XB * xb, int lane, int32_t * dbg) {
+    double acc = 0.0;
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
         const int b = lane + 64 * k;
         const int si = dot_block<TYPE>(wb[k], xb[k]);
-        const long long t = block_term(si, wb[k].d, xb[k]);
-        acc += b < nb ? t : 0;
-        if (dbg && b < nb) dbg[size_t(r) * nb + b] = si;
+        const double t = block_term(si, wb[k].d, xb[k]);
+        acc += b < nb ? t : 0.0;
+        if constexpr (DBG) {
+            if (dbg && b < nb) dbg[size_t(r) * nb + b] = si;
+        }
     }
-    return wave_sum_i64(acc);
+    return wave_sum_i64(dint_to_i64(acc));
 }
 
-template <int TYPE, int NU>
-__device__ __forceinline__ long long row_units(const WeightView & w, int r, int nu, const XK * xk, int lane,
-                                               int32_t * dbg) {
+template <int TYPE, int NU, bool DBG>
+__device__ __forceinline__ long long row_units(const WK * wk, int r, int nu, const XK * xk, int lane, int32_t * dbg) {
     const int nsb = nu >> 2;
-    WK wk[NU];
-#pragma unroll
-    for (int k = 0; k < NU; ++k) {
-        const int u0 = lane + 64 * k, u = u0 < nu ? u0 : nu - 1;
-        load_wk<TYPE>(w, size_t(r) * nsb + (u >> 2), u & 3, wk[k]);
-    }
     long long acc = 0;
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
@@ -436,9 +531,10 @@ __device__ __forceinline__ long long row_units(const WeightView & w, int r, int 
         if (u >= nu) S = M = 0;
         S = sum_lanes4_i32(S);
         M = sum_lanes4_i32(M);
-        if (u < nu && (u & 3) == 0) {
-            acc += superblock_term<TYPE>(S, M, wk[k], xk[k]);
-            if (dbg) {
+        const long long t = superblock_term<TYPE>(S, M, wk[k], xk[k]);
+        acc += (u < nu && (u & 3) == 0) ? t : 0;
+        if constexpr (DBG) {
+            if (dbg && u < nu && (u & 3) == 0) {
                 const size_t i = (size_t(r) * nsb + (u >> 2)) * 2;
                 dbg[i] = S;
                 dbg[i + 1] = M;
@@ -448,72 +544,119 @@ __device__ __forceinline__ long long row_units(const WeightView & w, int r, int 
     return wave_sum_i64(acc);
 }
 
-template <int TYPE, int NU>
+struct Ctx {  // per-wave state shared by the row loops
+    int lane, nb, nu;
+    unsigned long long best;
+};
+
+// One row: dots, exact row sum, epilog (lane 0 stores).
+template <int TYPE, int NU, int EPI, bool DBG>
+__device__ __forceinline__ void row_compute(const GemvArgs & a, const GemvMember & m, bool argmax, int32_t * dbg, int r,
+                                            const Rows<TYPE, NU> & R, const XB * xb, const XK * xk, Ctx & c) {
+    long long acc, acc2 = 0;
+    if constexpr (Rows<TYPE, NU>::KQ) {
+        acc = row_units<TYPE, NU, DBG>(R.wk, r, c.nu, xk, c.lane, dbg);
+        if constexpr (EPI == EPI_SWIGLU) acc2 = row_units<TYPE, NU, false>(R.wk2, r, c.nu, xk, c.lane, nullptr);
+    } else {
+        acc = row_blocks<TYPE, NU, DBG>(R.wb, r, c.nb, xb, c.lane, dbg);
+        if constexpr (EPI == EPI_SWIGLU) acc2 = row_blocks<TYPE, NU, false>(R.wb2, r, c.nb, xb, c.lane, nullptr);
+    }
+    if (c.lane == 0) {
+        const float v = fixed_to_float(acc);
+        float out = v;
+        if constexpr (EPI == EPI_SWIGLU) {
+            out = (v / (1.0f + expf_(-v))) * fixed_to_float(acc2);  // gemvqc_ops.h:88-92
+        } else if constexpr (EPI == EPI_ADD) {
+            out = v + R.e[0];  // gemvqc16.cpp:282-301
+        } else if constexpr (EPI == EPI_CONV) {  // gemvqc_ops.h:387-431 on the row result
+            float sum = 0.0f;
+            sum += R.e[0] * R.e[4];
+            sum += R.e[1] * R.e[5];
+            sum += R.e[2] * R.e[6];
+            sum += v * R.e[7];
+            out = m.conv_silu ? silu_(sum) : sum;
+            m.conv_dst[3 * r] = R.e[1];
+            m.conv_dst[3 * r + 1] = R.e[2];
+            m.conv_dst[3 * r + 2] = v;
+        }
+        m.y[r] = out;
+        if (argmax) {
+            const unsigned long long key = argmax_key(out, uint32_t(r));
+            c.best = key > c.best ? key : c.best;
+        }
+    }
+}
+
+// Rows r0..r1-1 of one member, two register buffers in turn: the loads of row r + 1 are in flight while row r is
+// reduced, and no buffer is copied (a copy of registers that are still being loaded would wait for them). Rows
+// past r1 - 1 reload the last row, which the caches serve; their results are not stored.
+template <int TYPE, int NU, int EPI, bool DBG>
+__device__ __forceinline__ void run_rows(const GemvArgs & a, const GemvMember & m, int mi, int r0, int r1,
+                                         Rows<TYPE, NU> & A, const XB * xb, const XK * xk, Ctx & c) {
+    const bool argmax = EPI == EPI_PLAIN && a.argmax_key != nullptr && mi == 0;
+    int32_t * dbg = (DBG && mi == 0) ? a.dbg : nullptr;
+    Rows<TYPE, NU> B;
+    for (int r = r0;; r += 2) {
+        load_row<TYPE, NU, EPI>(m, min(r + 1, r1 - 1), c.lane, c.nb, c.nu, B);
+        row_compute<TYPE, NU, EPI, DBG>(a, m, argmax, dbg, r, A, xb, xk, c);
+        if (r + 1 >= r1) break;
+        load_row<TYPE, NU, EPI>(m, min(r + 2, r1 - 1), c.lane, c.nb, c.nu, A);
+        row_compute<TYPE, NU, EPI, DBG>(a, m, argmax, dbg, r + 1, B, xb, xk, c);
+        if (r + 2 >= r1) break;
+    }
+}
+
+template <int TYPE, int NU, bool DBG>
 __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
     __shared__ Lds s;
     constexpr bool KQ = TYPE == T_Q5_K || TYPE == T_Q6_K;
-    const float scale = a.xsrc == XSRC_NORM ? block_norm_scale(a.x, a.cols, a.norm_eps, a.norm_l2, s) : 1.0f;
-    if (KQ) quantize_q8_K(a, scale, s);
-    else quantize_q8_0(a, scale, s);
+    Ctx c;
+    c.lane = threadIdx.x & 63;
+    c.nb = a.cols / 32;
+    c.nu = a.cols / 64;
+    c.best = 0;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: member fields load as scalars
+    // each wave owns a contiguous range of tasks (streams through consecutive rows)
+    const int nwt = gridDim.x * NWAVES, per = (a.total_tasks + nwt - 1) / nwt;
+    const int t0 = (blockIdx.x * NWAVES + wave) * per;
+    const int t1 = min(a.total_tasks, t0 + per);
+    int mi0 = 0;
+#pragma unroll
+    for (int i = 1; i < 4; ++i)
+        if (i < a.n_members && t0 >= a.m[i].task_begin) mi0 = i;
+    // the first row's weights are requested before the activation prologue
+    Rows<TYPE, NU> cur;
+    if (t0 < t1) load_row_any<TYPE, NU>(a.m[mi0], t0 - a.m[mi0].task_begin, c.lane, c.nb, c.nu, cur);
+    if constexpr (KQ) {
+        const float scale = a.xsrc == XSRC_NORM ? block_norm_scale(a.x, a.cols, a.norm_eps, a.norm_l2, s) : 1.0f;
+        quantize_q8_K(a, scale, s);
+    } else {
+        prologue_q8_0<(NU > 4 ? 2 : 1)>(a, s);
+    }
     __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nb = a.cols / 32, nu = a.cols / 64;
     XB xb[KQ ? 1 : NU];
     XK xk[KQ ? NU : 1];
-    if (KQ) {
+    if constexpr (KQ) {
 #pragma unroll
-        for (int k = 0; k < NU; ++k) load_xk<TYPE>(s, lane + 64 * k, nu, xk[k]);
+        for (int k = 0; k < NU; ++k) load_xk<TYPE>(s, c.lane + 64 * k, c.nu, xk[k]);
     } else {
 #pragma unroll
-        for (int k = 0; k < NU; ++k) load_xb(s, lane + 64 * k, nb, xb[k]);
+        for (int k = 0; k < NU; ++k) load_xb(s, c.lane + 64 * k, c.nb, xb[k]);
     }
-    unsigned long long best = 0;
-    const int nwt = gridDim.x * NWAVES;
-    for (int t = blockIdx.x * NWAVES + wave; t < a.total_tasks; t += nwt) {
-        int mi = 0;
-#pragma unroll
-        for (int i = 1; i < 4; ++i)
-            if (i < a.n_members && t >= a.m[i].task_begin) mi = i;
+    for (int mi = mi0; mi < a.n_members && t0 < t1; ++mi) {
         const GemvMember & m = a.m[mi];
-        const int r = t - m.task_begin;
-        int32_t * dbg = mi == 0 ? a.dbg : nullptr;
-        long long acc, acc2 = 0;
-        if (KQ) {
-            acc = row_units<TYPE, NU>(m.w, r, nu, xk, lane, dbg);
-            if (m.epi == EPI_SWIGLU) acc2 = row_units<TYPE, NU>(m.w2, r, nu, xk, lane, nullptr);
-        } else {
-            acc = row_blocks<TYPE, NU>(m.w, r, nb, xb, lane, dbg);
-            if (m.epi == EPI_SWIGLU) acc2 = row_blocks<TYPE, NU>(m.w2, r, nb, xb, lane, nullptr);
-        }
-        if (lane == 0) {
-            const float v = fixed_to_float(acc);
-            float out = v;
-            if (m.epi == EPI_SWIGLU) {
-                out = (v / (1.0f + expf_(-v))) * fixed_to_float(acc2);  // gemvqc_ops.h:88-92
-            } else if (m.epi == EPI_ADD) {
-                out = v + m.res[r];  // gemvqc16.cpp:282-301
-            } else if (m.epi == EPI_CONV) {  // gemvqc_ops.h:387-431 on the row result
-                const float s0 = m.conv_src[3 * r], s1 = m.conv_src[3 * r + 1], s2 = m.conv_src[3 * r + 2];
-                const float4 k = *reinterpret_cast<const float4 *>(m.conv_w + 4 * size_t(r));
-                float sum = 0.0f;
-                sum += s0 * k.x;
-                sum += s1 * k.y;
-                sum += s2 * k.z;
-                sum += v * k.w;
-                out = m.conv_silu ? silu_(sum) : sum;
-                m.conv_dst[3 * r] = s1;
-                m.conv_dst[3 * r + 1] = s2;
-                m.conv_dst[3 * r + 2] = v;
-            }
-            m.y[r] = out;
-            if (a.argmax_key && mi == 0) {
-                const unsigned long long key = argmax_key(out, uint32_t(r));
-                best = key > best ? key : best;
-            }
+        const int r0 = max(t0, m.task_begin) - m.task_begin, r1 = min(t1, m.task_begin + m.rows) - m.task_begin;
+        if (r0 >= r1) continue;
+        if (mi != mi0) load_row_any<TYPE, NU>(m, r0, c.lane, c.nb, c.nu, cur);
+        switch (m.epi) {
+        case EPI_SWIGLU: run_rows<TYPE, NU, EPI_SWIGLU, DBG>(a, m, mi, r0, r1, cur, xb, xk, c); break;
+        case EPI_ADD: run_rows<TYPE, NU, EPI_ADD, DBG>(a, m, mi, r0, r1, cur, xb, xk, c); break;
+        case EPI_CONV: run_rows<TYPE, NU, EPI_CONV, DBG>(a, m, mi, r0, r1, cur, xb, xk, c); break;
+        default: run_rows<TYPE, NU, EPI_PLAIN, DBG>(a, m, mi, r0, r1, cur, xb, xk, c); break;
         }
     }
     if (a.argmax_key) {
-        if (lane == 0) s.key[wave] = best;
+        if (c.lane == 0) s.key[wave] = c.best;
         __syncthreads();
         if (threadIdx.x == 0) {
             unsigned long long b = s.key[0];
@@ -525,9 +668,11 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
 
 template <int TYPE, int NU>
 hipError_t launch_typed(const GemvArgs & a, hipStream_t st) {
-    int grid = (a.total_tasks + NWAVES - 1) / NWAVES;
-    grid = grid < 1024 ? grid : 1024;
-    hipLaunchKernelGGL((gemv_kernel<TYPE, NU>), dim3(grid), dim3(NT), 0, st, a);
+    // about 16 tasks per workgroup (4 per wave) amortize the activation prologue; at most 1024 workgroups
+    int grid = (a.total_tasks + 15) / 16;
+    grid = grid < 1 ? 1 : grid > 1024 ? 1024 : grid;
+    if (a.dbg) GQ_LAUNCH((gemv_kernel<TYPE, NU, true>), dim3(grid), dim3(NT), 0, st, a);
+    else GQ_LAUNCH((gemv_kernel<TYPE, NU, false>), dim3(grid), dim3(NT), 0, st, a);
     return hipGetLastError();
 }
 

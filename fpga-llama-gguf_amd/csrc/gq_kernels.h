@@ -1,5 +1,6 @@
 // Launch descriptors of the gfx950 kernels (shared by the kernels and the host command processor).
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -151,6 +152,19 @@ struct NextTokenArgs {
 };
 
 constexpr int ATTN_CHUNK = 64;
+
+// Profiling: when set (by gemvq_profile on the calling thread), launchers start kernels through
+// hipExtLaunchKernelGGL with these events, which record the kernel's own start and end on the device.
+extern thread_local hipEvent_t g_prof_start, g_prof_stop;
+
+#define GQ_LAUNCH(kernel, grid, block, shmem, stream, ...)                                                         \
+    do {                                                                                                            \
+        if (::gq::g_prof_start)                                                                                     \
+            hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, ::gq::g_prof_start, ::gq::g_prof_stop, 0,     \
+                                  __VA_ARGS__);                                                                     \
+        else                                                                                                        \
+            hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                                    \
+    } while (0)
 
 hipError_t launch_gemv(const GemvArgs & a, int type, hipStream_t s);
 hipError_t launch_norm(const NormArgs & a, hipStream_t s);

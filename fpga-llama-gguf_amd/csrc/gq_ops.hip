@@ -176,16 +176,18 @@ __global__ __launch_bounds__(64) void gated_norm_kernel(GatedNormArgs a) {
 }
 
 // ---- attention core (one token, GQA, fp16 KV) ----
-// Workgroup (KV head, chunk of 64 positions), 256 threads. Each workgroup normalizes and rotates its q heads and
-// the new key, scores its positions (pairwise over head_dim, 4 dims per lane), runs the chunk's softmax part
-// (max, e^(s - max), sequential sums over positions), writes the partials; the last workgroup of a KV head
-// combines the chunks in order and applies the sigmoid output gate.
+// Workgroup (KV head, chunk of 64 positions), 256 threads. The chunk's keys and values are staged into LDS with
+// one coalesced pass; the workgroup normalizes and rotates its q heads and the new key, scores its positions
+// (pairwise over head_dim, 4 dims per lane), computes e^(s - chunk max) in parallel and the chunk's sums over
+// positions in order, and writes the partials. The last workgroup of a KV head combines the chunks in order and
+// applies the sigmoid output gate.
 constexpr int ATT_T = 256;
 constexpr int MAXHD = 256;
-constexpr int MAXG = 8;
+constexpr int MAXG = 4;   // q heads per KV head
+constexpr int MAXCH = 64; // chunks (n_ctx <= 4096)
 
 __device__ float head_norm_scale(const float * v, int hd, float eps, float * red) {
-    // pairwise over hd (<= 256): lane l of wave 0..3 holds element tid (one element per thread)
+    // pairwise over hd (<= 256): element tid in thread tid
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float e = tid < hd ? v[tid] : 0.0f;
     const float t = pair_sum_lanes<64>(e * e);
@@ -197,17 +199,31 @@ __device__ float head_norm_scale(const float * v, int hd, float eps, float * red
 }
 
 __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
+    __shared__ uint16_t ks[ATTN_CHUNK * MAXHD], vs[ATTN_CHUNK * MAXHD];
     __shared__ float qs[MAXG][MAXHD];      // fp16-rounded q of the group's heads
-    __shared__ float kcur[MAXHD], vcur[MAXHD];
     __shared__ float tmp[MAXHD];
     __shared__ float sc[MAXG][ATTN_CHUNK];
     __shared__ float red[4];
     __shared__ float mx[MAXG], lsum[MAXG];
+    __shared__ float fc[MAXG][MAXCH];
     __shared__ int last;
     const int kvh = blockIdx.x % a.n_head_kv, chunk = blockIdx.x / a.n_head_kv;
     const int pos = *a.pos, nc = (pos + ATTN_CHUNK) / ATTN_CHUNK;
-    if (chunk >= nc) return;
+    if (pos < 0 || pos >= a.n_ctx || chunk >= nc) return;  // positions past the KV capacity are not stored
     const int tid = threadIdx.x, hd = a.head_dim, G = a.n_head / a.n_head_kv, half = a.n_rot / 2;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int t0 = chunk * ATTN_CHUNK, t1 = min(t0 + ATTN_CHUNK, pos + 1), nt = t1 - t0;
+    // stage the chunk's cached keys and values (positions before pos) into LDS, 16 bytes per load
+    {
+        const int per = hd / 8;  // 16-byte pieces per row
+        for (int c = tid; c < nt * per; c += ATT_T) {
+            const int ti = c / per, pc = c % per, t = t0 + ti;
+            if (t == pos) continue;
+            const size_t off = (size_t(t) * a.n_head_kv + kvh) * hd + pc * 8;
+            *reinterpret_cast<uint4 *>(ks + ti * hd + pc * 8) = *reinterpret_cast<const uint4 *>(a.kc + off);
+            *reinterpret_cast<uint4 *>(vs + ti * hd + pc * 8) = *reinterpret_cast<const uint4 *>(a.vc + off);
+        }
+    }
     const float * cs = a.cs + size_t(pos) * a.n_rot;
     // q heads of the group: RMS norm with weight, NEOX RoPE on the first n_rot dims, fp16 rounding.
     for (int g = 0; g < G; ++g) {
@@ -224,8 +240,8 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
         }
         __syncthreads();
     }
-    // the new key and value of this KV head
-    {
+    // the new key and value of this KV head (in the chunk that holds pos)
+    if (chunk == nc - 1) {
         const float * kr = a.k + size_t(kvh) * hd;
         const float s = head_norm_scale(kr, hd, a.eps, red);
         if (tid < hd) tmp[tid] = (kr[tid] * s) * a.kn[tid];
@@ -235,30 +251,19 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
             if (tid < half) o = tmp[tid] * cs[2 * tid] - tmp[tid + half] * cs[2 * tid + 1];
             else if (tid < a.n_rot) o = tmp[tid - half] * cs[2 * (tid - half) + 1] + tmp[tid] * cs[2 * (tid - half)];
             const uint32_t kb = f2h(o), vb = f2h(a.v[size_t(kvh) * hd + tid]);
-            kcur[tid] = h2f(kb);
-            vcur[tid] = h2f(vb);
-            if (chunk == nc - 1) {
-                const size_t off = (size_t(pos) * a.n_head_kv + kvh) * hd + tid;
-                a.kc[off] = uint16_t(kb);
-                a.vc[off] = uint16_t(vb);
-            }
+            ks[(pos - t0) * hd + tid] = uint16_t(kb);
+            vs[(pos - t0) * hd + tid] = uint16_t(vb);
+            const size_t off = (size_t(pos) * a.n_head_kv + kvh) * hd + tid;
+            a.kc[off] = uint16_t(kb);
+            a.vc[off] = uint16_t(vb);
         }
-        __syncthreads();
     }
-    // scores: wave w takes positions t0 + w, t0 + w + 4, ...; lane l holds dims 4l .. 4l + 3
-    const int t0 = chunk * ATTN_CHUNK, t1 = min(t0 + ATTN_CHUNK, pos + 1), nt = t1 - t0;
-    const int lane = tid & 63, wave = tid >> 6;
+    __syncthreads();
+    // scores: wave w takes positions w, w + 4, ..; lane l holds dims 4l .. 4l + 3
     for (int ti = wave; ti < nt; ti += 4) {
-        const int t = t0 + ti;
         float kv4[4];
-        if (t == pos) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) kv4[i] = 4 * lane + i < hd ? kcur[4 * lane + i] : 0.0f;
-        } else {
-            const uint16_t * kp = a.kc + (size_t(t) * a.n_head_kv + kvh) * hd;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) kv4[i] = 4 * lane + i < hd ? h2f(kp[4 * lane + i]) : 0.0f;
-        }
+        for (int i = 0; i < 4; ++i) kv4[i] = 4 * lane + i < hd ? h2f(ks[ti * hd + 4 * lane + i]) : 0.0f;
         for (int g = 0; g < G; ++g) {
             float pr[4];
 #pragma unroll
@@ -268,36 +273,35 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
         }
     }
     __syncthreads();
-    // chunk max and e^(s - max), sum over positions in order
-    if (tid < G) {
-        float m = sc[tid][0];
-        for (int i = 1; i < nt; ++i) m = fmaxf(m, sc[tid][i]);
-        float l = 0.0f;
-        for (int i = 0; i < nt; ++i) {
-            const float p = expf_(sc[tid][i] - m);
-            sc[tid][i] = p;
-            l += p;
-        }
-        mx[tid] = m;
-        lsum[tid] = l;
+    // chunk max (wave g for head g), e^(s - max) in parallel, the sum over positions in order
+    if (wave < G) {
+        const float s = lane < nt ? sc[wave][lane] : -__builtin_inff();
+        float m = s;
+#pragma unroll
+        for (int st = 32; st >= 1; st >>= 1) m = fmaxf(m, __shfl_xor(m, st, WAVE));
+        if (lane < nt) sc[wave][lane] = expf_(s - m);
+        if (lane == 0) mx[wave] = m;
     }
     __syncthreads();
+    if (tid < G) {
+        float l = 0.0f;
+        for (int i = 0; i < nt; ++i) l += sc[tid][i];
+        lsum[tid] = l;
+    }
     // o[g][d] = sum over positions in order of p * v
     const int pstride = 2 + hd, nchmax = (a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
     for (int od = tid; od < G * hd; od += ATT_T) {
         const int g = od / hd, d = od % hd;
         float o = 0.0f;
-        for (int i = 0; i < nt; ++i) {
-            const int t = t0 + i;
-            const float vv = t == pos ? vcur[d] : h2f(a.vc[(size_t(t) * a.n_head_kv + kvh) * hd + d]);
-            o += sc[g][i] * vv;
-        }
+        for (int i = 0; i < nt; ++i) o += sc[g][i] * h2f(vs[i * hd + d]);
         float * pp = a.part + (size_t(kvh * G + g) * nchmax + chunk) * pstride;
         pp[2 + d] = o;
-        if (d == 0) {
-            pp[0] = mx[g];
-            pp[1] = lsum[g];
-        }
+    }
+    __syncthreads();
+    if (tid < G) {
+        float * pp = a.part + (size_t(kvh * G + tid) * nchmax + chunk) * pstride;
+        pp[0] = mx[tid];
+        pp[1] = lsum[tid];
     }
     __threadfence();
     __syncthreads();
@@ -305,19 +309,36 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
     __syncthreads();
     if (!last) return;
     __threadfence();
+    // combine: M = max of the chunk maxima, f_c = e^(m_c - M), L = sum_c l_c f_c, O = sum_c o_c f_c (in order)
+    if (wave < G) {
+        const float * pp = a.part + size_t(kvh * G + wave) * nchmax * pstride;
+        float m = -__builtin_inff();
+        for (int c = lane; c < nc; c += 64) m = fmaxf(m, __builtin_nontemporal_load(pp + size_t(c) * pstride));
+#pragma unroll
+        for (int st = 32; st >= 1; st >>= 1) m = fmaxf(m, __shfl_xor(m, st, WAVE));
+        for (int c = lane; c < nc; c += 64) fc[wave][c] = expf_(__builtin_nontemporal_load(pp + size_t(c) * pstride) - m);
+    }
+    __syncthreads();
+    if (tid < G) {
+        const float * pp = a.part + size_t(kvh * G + tid) * nchmax * pstride;
+        float L = 0.0f;
+        for (int c = 0; c < nc; ++c) L += __builtin_nontemporal_load(pp + size_t(c) * pstride + 1) * fc[tid][c];
+        lsum[tid] = L;
+    }
+    __syncthreads();
     for (int od = tid; od < G * hd; od += ATT_T) {
         const int g = od / hd, d = od % hd, h = kvh * G + g;
-        const float * pp = a.part + size_t(h) * nchmax * pstride;
-        float M = __builtin_nontemporal_load(pp);
-        for (int c = 1; c < nc; ++c) M = fmaxf(M, __builtin_nontemporal_load(pp + size_t(c) * pstride));
-        float L = 0.0f, O = 0.0f;
-        for (int c = 0; c < nc; ++c) {
-            const float * pc = pp + size_t(c) * pstride;
-            const float f = expf_(__builtin_nontemporal_load(pc) - M);
-            L += __builtin_nontemporal_load(pc + 1) * f;
-            O += __builtin_nontemporal_load(pc + 2 + d) * f;
+        const float * pp = a.part + size_t(h) * nchmax * pstride + 2 + d;
+        float O = 0.0f;
+        for (int c0 = 0; c0 < nc; c0 += 8) {  // 8 independent loads in flight, the sum still in chunk order
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = c0 + j < nc ? __builtin_nontemporal_load(pp + size_t(c0 + j) * pstride) : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (c0 + j < nc) O += v[j] * fc[g][c0 + j];
         }
-        float out = O / L;
+        float out = O / lsum[g];
         if (a.gate) {
             const float gt = a.gate[size_t(h) * 2 * hd + d];
             out = (1.0f / (1.0f + expf_(-gt))) * out;
@@ -394,61 +415,62 @@ __global__ void next_token_kernel(NextTokenArgs a) {
 }  // namespace
 
 hipError_t launch_norm(const NormArgs & a, hipStream_t s) {
-    hipLaunchKernelGGL(norm_kernel, dim3(a.rows), dim3(256), 0, s, a);
+    GQ_LAUNCH(norm_kernel, dim3(a.rows), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_ew(const EwArgs & a, hipStream_t s) {
     int grid = (a.n + 255) / 256;
     grid = grid < 1024 ? grid : 1024;
-    hipLaunchKernelGGL(ew_kernel, dim3(grid), dim3(256), 0, s, a);
+    GQ_LAUNCH(ew_kernel, dim3(grid), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_conv(const ConvArgs & a, hipStream_t s) {
-    hipLaunchKernelGGL(conv_kernel, dim3((a.ch + 255) / 256), dim3(256), 0, s, a);
+    GQ_LAUNCH(conv_kernel, dim3((a.ch + 255) / 256), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_rope(const RopeArgs & a, hipStream_t s) {
     if (a.ne0 > 1024) return hipErrorInvalidValue;
     const int t = ((a.ne0 + 63) / 64) * 64;
-    hipLaunchKernelGGL(rope_kernel, dim3(a.rows), dim3(t), 0, s, a);
+    GQ_LAUNCH(rope_kernel, dim3(a.rows), dim3(t), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_gdn(const GdnArgs & a, hipStream_t s) {
-    hipLaunchKernelGGL(gdn_kernel, dim3(a.hv * (128 / GDN_ROWS)), dim3(128), 0, s, a);
+    GQ_LAUNCH(gdn_kernel, dim3(a.hv * (128 / GDN_ROWS)), dim3(128), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_gated_norm(const GatedNormArgs & a, hipStream_t s) {
-    hipLaunchKernelGGL(gated_norm_kernel, dim3(a.heads), dim3(64), 0, s, a);
+    GQ_LAUNCH(gated_norm_kernel, dim3(a.heads), dim3(64), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_attn(const AttnArgs & a, hipStream_t s) {
-    if (a.head_dim > MAXHD || a.head_dim % 4 || a.n_head % a.n_head_kv || a.n_head / a.n_head_kv > MAXG)
+    if (a.head_dim > MAXHD || a.head_dim % 8 || a.n_head % a.n_head_kv || a.n_head / a.n_head_kv > MAXG ||
+        (a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK > MAXCH)
         return hipErrorInvalidValue;
     const int nch = (a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
-    hipLaunchKernelGGL(attn_kernel, dim3(a.n_head_kv * nch), dim3(ATT_T), 0, s, a);
+    GQ_LAUNCH(attn_kernel, dim3(a.n_head_kv * nch), dim3(ATT_T), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_get_rows(const GetRowsArgs & a, hipStream_t s) {
-    hipLaunchKernelGGL(get_rows_kernel, dim3((a.cols + 255) / 256), dim3(256), 0, s, a);
+    GQ_LAUNCH(get_rows_kernel, dim3((a.cols + 255) / 256), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_argmax(const float * x, int n, unsigned long long * key, hipStream_t s) {
     int grid = (n + 255) / 256;
     grid = grid < 256 ? grid : 256;
-    hipLaunchKernelGGL(argmax_kernel, dim3(grid), dim3(256), 0, s, x, n, key);
+    GQ_LAUNCH(argmax_kernel, dim3(grid), dim3(256), 0, s, x, n, key);
     return hipGetLastError();
 }
 
 hipError_t launch_next_token(const NextTokenArgs & a, hipStream_t s) {
-    hipLaunchKernelGGL(next_token_kernel, dim3(1), dim3(1), 0, s, a);
+    GQ_LAUNCH(next_token_kernel, dim3(1), dim3(1), 0, s, a);
     return hipGetLastError();
 }
 

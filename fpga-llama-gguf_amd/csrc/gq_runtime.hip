@@ -16,6 +16,10 @@
 
 using namespace gq;
 
+namespace gq {
+thread_local hipEvent_t g_prof_start = nullptr, g_prof_stop = nullptr;
+}
+
 namespace {
 
 struct Weight {
@@ -153,6 +157,7 @@ bool shape_ok(int t, int rows, int cols) {
 struct Compiler {
     gemvq_ctx * c;
     std::vector<Launch> out;
+    std::vector<std::pair<int, int>> spans;  // per launch: first command, number of commands
     int bad = 0;  // 1-based index of the first invalid command
     std::string why;
 
@@ -204,6 +209,7 @@ struct Compiler {
                     NormArgs a{A(k[2]), (flags & GEMVQ_NORM_NO_WEIGHT) ? nullptr : A(k[3]), A(k[4]), int(nn), int(rows),
                                int(st), bits_f(k[5]), int(flags & 3)};
                     out.push_back(LNorm{a});
+                    spans.push_back({int(i), 1});
                 }
                 break;
             }
@@ -213,6 +219,7 @@ struct Compiler {
                 if (nn == 0 || !range(k[2], nn) || !range(k[3], nn) || !range(k[4], nn)) return reject(i, "ADD/MUL range");
                 EwArgs a{A(k[2]), A(k[3]), A(k[4]), int(nn), 0, 0, op == GEMVQ_OP_ADD ? EW_ADD : EW_MUL, 0.0f};
                 out.push_back(LEw{a});
+                    spans.push_back({int(i), 1});
                 break;
             }
             case GEMVQ_OP_SILU_MUL: {
@@ -227,6 +234,7 @@ struct Compiler {
                 EwArgs a{A(k[2]), A(k[3]), A(k[4]), int(nn), int(row), int(stride),
                          (k[5] & GEMVQ_SILU_MUL_SIGMOID) ? EW_SIGMOID_MUL : EW_SILU_MUL, 0.0f};
                 out.push_back(LEw{a});
+                    spans.push_back({int(i), 1});
                 break;
             }
             case GEMVQ_OP_UNARY: {
@@ -241,6 +249,7 @@ struct Compiler {
                 const int ops[5] = {0, EW_SILU, EW_SIGMOID, EW_SOFTPLUS, EW_COPY};
                 EwArgs a{A(k[2]), nullptr, A(k[4]), int(nn), int(row), int(stride), ops[kind], 0.0f};
                 out.push_back(LEw{a});
+                    spans.push_back({int(i), 1});
                 break;
             }
             case GEMVQ_OP_GDN: {
@@ -277,9 +286,11 @@ struct Compiler {
                 a.l2_eps = bits_f(k2[4]);
                 a.flags = int(flags);
                 out.push_back(LGdn{a});
+                spans.push_back({int(i), gates ? 3 : 2});
                 if (flags & GEMVQ_GDN_GATED) {
                     GatedNormArgs g{A(k[7]), A(k2[7]), A(k2[6]), int(hv), bits_f(k2[5])};
                     out.push_back(LGated{g});
+                    spans.push_back({int(i), gates ? 3 : 2});
                 }
                 i += gates ? 3 : 2;
                 continue;
@@ -291,6 +302,7 @@ struct Compiler {
                     return reject(i, "CONV range");
                 ConvArgs a{A(k[2]), A(k[3]), A(k[5]), A(k[6]), A(k[4]), int(ch), int(k[7] & 1)};
                 out.push_back(LConv{a});
+                    spans.push_back({int(i), 1});
                 break;
             }
             case GEMVQ_OP_STATE_LOAD:
@@ -305,6 +317,7 @@ struct Compiler {
                 RopeArgs a{A(k[2]), A(k[3]), pos_off ? reinterpret_cast<const int32_t *>(A(pos_off)) : nullptr, A(k[4]),
                            int(nd), int(ne0), int(rows)};
                 out.push_back(LRope{a});
+                    spans.push_back({int(i), 1});
                 break;
             }
             case GEMVQ_OP_ATTN: {
@@ -314,7 +327,7 @@ struct Compiler {
                 const uint32_t kv = k[3], flags = k[7];
                 if (kv >= c->kvs.size()) return reject(i, "ATTN kv buffer");
                 const KvBuf & b = c->kvs[kv];
-                if (nkv == 0 || nh % nkv || nh / nkv > 8 || int(nkv) != b.n_head_kv || int(hd) != b.head_dim || hd > 256 ||
+                if (nkv == 0 || nh % nkv || nh / nkv > 4 || (b.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK > 64 || int(nkv) != b.n_head_kv || int(hd) != b.head_dim || hd > 256 ||
                     hd % 16 || nrot > hd || nrot % 2)
                     return reject(i, "ATTN shape");
                 const uint32_t qstride = (flags & 1) ? 2 * hd : hd;
@@ -346,6 +359,7 @@ struct Compiler {
                 a.scale = bits_f(k2[2]);
                 a.eps = bits_f(k2[3]);
                 out.push_back(LAttn{a});
+                spans.push_back({int(i), 2});
                 i += 2;
                 continue;
             }
@@ -358,11 +372,13 @@ struct Compiler {
                 GetRowsArgs a{weight_view(c->warena + woff, type, rows, cols), reinterpret_cast<const int32_t *>(A(k[6])),
                               A(k[7]), rows, cols, type};
                 out.push_back(LRows{a});
+                    spans.push_back({int(i), 1});
                 break;
             }
             case GEMVQ_OP_ARGMAX: {
                 if (k[1] == 0 || !range(k[2], k[1]) || !range(k[3], 2)) return reject(i, "ARGMAX range");
                 out.push_back(LArgmax{A(k[2]), int(k[1]), reinterpret_cast<unsigned long long *>(A(k[3]))});
+                spans.push_back({int(i), 1});
                 break;
             }
             case GEMVQ_OP_NEXT_TOKEN: {
@@ -378,12 +394,14 @@ struct Compiler {
                 a.out = reinterpret_cast<int32_t *>(A(k[6]));
                 a.max_pos = int(c->act_floats - k[6]);
                 out.push_back(LNext{a});
+                    spans.push_back({int(i), 1});
                 break;
             }
             case GEMVQ_OP_FILL: {
                 if (k[1] == 0 || !range(k[2], k[1])) return reject(i, "FILL range");
                 EwArgs a{nullptr, nullptr, A(k[2]), int(k[1]), 0, 0, EW_FILL, bits_f(k[3])};
                 out.push_back(LEw{a});
+                    spans.push_back({int(i), 1});
                 break;
             }
             default:
@@ -505,10 +523,53 @@ struct Compiler {
             c->dbg_used = true;
         }
         out.push_back(LGemv{a, type});
+        spans.push_back({int(i0), int(i - i0)});
         used = i - i0;
         return true;
     }
 };
+
+// Kernel name (template instance) and algorithmic bytes of a launch: GGUF-sized weights, fp32 vectors read and
+// written once, recurrent state and KV cache read and written. `pos` is the token position (attention reads
+// pos + 1 cached keys and values).
+std::pair<std::string, uint64_t> describe(const Launch & l, int pos) {
+    if (auto * g = std::get_if<LGemv>(&l)) {
+        const GemvArgs & a = g->a;
+        const bool kq = g->type == T_Q5_K || g->type == T_Q6_K;
+        const int nu = (a.cols / (kq ? 64 : 32) + 63) / 64;
+        uint64_t b = uint64_t(a.cols) * 4 * (a.xsrc == XSRC_NORM && a.norm_w ? 2 : 1);
+        for (int i = 0; i < a.n_members; ++i) {
+            const GemvMember & m = a.m[i];
+            const uint64_t rows = uint64_t(m.rows);
+            b += rows * gguf_row_bytes(g->type, a.cols) * (m.epi == EPI_SWIGLU ? 2 : 1) + rows * 4;
+            if (m.epi == EPI_ADD) b += rows * 4;
+            if (m.epi == EPI_CONV) b += rows * 40;
+        }
+        return {"gemv_kernel<" + std::to_string(g->type) + "," + std::to_string(nu) + ">", b};
+    }
+    if (auto * x = std::get_if<LNorm>(&l))
+        return {"norm_kernel", uint64_t(x->a.n) * x->a.rows * 8 + (x->a.w ? uint64_t(x->a.n) * 4 : 0)};
+    if (auto * x = std::get_if<LEw>(&l))
+        return {"ew_kernel", uint64_t(x->a.n) * 4 * (x->a.op == EW_FILL ? 1 : x->a.b ? 3 : 2)};
+    if (auto * x = std::get_if<LConv>(&l)) return {"conv_kernel", uint64_t(x->a.ch) * 48};
+    if (auto * x = std::get_if<LRope>(&l))
+        return {"rope_kernel", uint64_t(x->a.ne0) * x->a.rows * 8 + uint64_t(x->a.n_dims) * 4};
+    if (auto * x = std::get_if<LGdn>(&l)) {
+        const uint64_t hv = uint64_t(x->a.hv), hk = uint64_t(x->a.hk);
+        return {"gdn_kernel", 2 * hv * 128 * 128 * 4 + (2 * hk + 2 * hv) * 128 * 4 + hv * 16};
+    }
+    if (auto * x = std::get_if<LGated>(&l)) return {"gated_norm_kernel", uint64_t(x->a.heads) * 128 * 12 + 512};
+    if (auto * x = std::get_if<LAttn>(&l)) {
+        const AttnArgs & a = x->a;
+        const uint64_t kv = uint64_t(pos + 1) * a.n_head_kv * a.head_dim * 2 * 2;
+        const uint64_t vec = uint64_t(a.n_head) * a.head_dim * 4 * (a.gate ? 3 : 2) + uint64_t(a.n_head_kv) * a.head_dim * 8;
+        return {"attn_kernel", kv + vec};
+    }
+    if (auto * x = std::get_if<LRows>(&l))
+        return {"get_rows_kernel", uint64_t(x->a.cols) * 4 + gguf_row_bytes(x->a.type, x->a.cols)};
+    if (auto * x = std::get_if<LArgmax>(&l)) return {"argmax_kernel", uint64_t(x->n) * 4};
+    return {"next_token_kernel", 32};
+}
 
 hipError_t issue(const std::vector<Launch> & ls, hipStream_t s) {
     for (const Launch & l : ls) {
@@ -529,17 +590,19 @@ hipError_t issue(const std::vector<Launch> & ls, hipStream_t s) {
     return hipSuccess;
 }
 
-int compile_list(gemvq_ctx * c, const uint32_t * cmds, unsigned n, std::vector<Launch> & out) {
+int compile_list(gemvq_ctx * c, const uint32_t * cmds, unsigned n, std::vector<Launch> & out,
+                 std::vector<std::pair<int, int>> * spans = nullptr) {
     if (n > GEMVQ_MAX_CMDS) {
         c->err = "command list too long";
         return int(GEMVQ_MAX_CMDS) + 1;
     }
-    Compiler cp{c, {}, 0, {}};
+    Compiler cp{c, {}, {}, 0, {}};
     if (!cp.compile(cmds, n)) {
         c->err = cp.why;
         return cp.bad;
     }
     out = std::move(cp.out);
+    if (spans) *spans = std::move(cp.spans);
     c->last_launches = int(out.size());
     return 0;
 }
@@ -690,7 +753,7 @@ int gemvq_kv_create(gemvq_ctx * c, int n_ctx, int n_head_kv, int head_dim) {
     b.head_dim = head_dim;
     const size_t kvn = size_t(n_ctx) * n_head_kv * head_dim;
     const size_t nch = size_t(n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
-    const size_t partn = size_t(8) * n_head_kv * nch * (2 + head_dim);
+    const size_t partn = size_t(4) * n_head_kv * nch * (2 + head_dim);
     hipError_t e = hipMalloc(&b.k, kvn * 2);
     if (e == hipSuccess) e = hipMalloc(&b.v, kvn * 2);
     if (e == hipSuccess) e = hipMalloc(&b.part, partn * 4);
@@ -853,6 +916,61 @@ int gemvq_graph_time(gemvq_ctx * c, int graph, int times, double * us) {
     if (e != hipSuccess) return fail(c, e, "graph time");
     *us = double(ms) * 1000.0 / times;
     return 0;
+}
+
+int gemvq_profile(gemvq_ctx * c, const uint32_t * cmds, unsigned n, int reps, gemvq_launch_stat * out, int max_out) {
+    if (!c || !cmds || n == 0 || reps <= 0) return einval(c, "gemvq_profile: arguments");
+    hipSetDevice(c->device);
+    std::vector<Launch> ls;
+    std::vector<std::pair<int, int>> spans;
+    const int st = compile_list(c, cmds, n, ls, &spans);
+    if (st) return st;
+    // the token position (attention bytes depend on it): the first ATTN's pos operand
+    int pos = 0;
+    for (const Launch & l : ls)
+        if (auto * x = std::get_if<LAttn>(&l)) {
+            hipMemcpy(&pos, x->a.pos, 4, hipMemcpyDeviceToHost);
+            break;
+        }
+    const size_t L = ls.size();
+    std::vector<hipEvent_t> e0(L), e1(L);
+    std::vector<double> sum(L, 0.0);
+    hipError_t e = hipSuccess;
+    for (size_t i = 0; i < L && e == hipSuccess; ++i) {
+        e = hipEventCreate(&e0[i]);
+        if (e == hipSuccess) e = hipEventCreate(&e1[i]);
+    }
+    for (int r = 0; r < reps && e == hipSuccess; ++r) {
+        for (size_t i = 0; i < L && e == hipSuccess; ++i) {
+            g_prof_start = e0[i];
+            g_prof_stop = e1[i];
+            e = issue({ls[i]}, c->stream);
+        }
+        g_prof_start = g_prof_stop = nullptr;
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        for (size_t i = 0; i < L && e == hipSuccess; ++i) {
+            float ms = 0.0f;
+            e = hipEventElapsedTime(&ms, e0[i], e1[i]);
+            sum[i] += ms;
+        }
+    }
+    g_prof_start = g_prof_stop = nullptr;
+    for (size_t i = 0; i < L; ++i) {
+        if (e0[i]) hipEventDestroy(e0[i]);
+        if (e1[i]) hipEventDestroy(e1[i]);
+    }
+    if (e != hipSuccess) return fail(c, e, "profile");
+    for (size_t i = 0; i < L && int(i) < max_out; ++i) {
+        const auto d = describe(ls[i], pos);
+        gemvq_launch_stat & o = out[i];
+        std::memset(&o, 0, sizeof(o));
+        std::strncpy(o.name, d.first.c_str(), sizeof(o.name) - 1);
+        o.first_cmd = spans[i].first;
+        o.n_cmds = spans[i].second;
+        o.bytes = d.second;
+        o.us = sum[i] * 1000.0 / reps;
+    }
+    return int(L);
 }
 
 }  // extern "C"

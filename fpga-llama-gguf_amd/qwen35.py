@@ -232,6 +232,14 @@ class Model:
     def sync(self) -> None:
         self.ctx.sync()
 
+    def step_direct(self, n: int = 1) -> None:
+        """n decode steps as plain stream launches of the same command list (no graph; each step synchronizes)."""
+        cmds = self.commands()
+        for _ in range(n):
+            st = self.ctx.run(cmds)
+            if st:
+                raise gq.GemvqError(f"step_direct: command {st}: {self.ctx.error()}")
+
     def tokens(self, n: int) -> np.ndarray:
         out = np.empty(n, np.int32)
         self._ok(self.lib.gemvq_qwen35_tokens(self.h, out.ctypes.data, n), "tokens")

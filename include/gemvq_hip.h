@@ -153,6 +153,20 @@ int gemvq_debug_blocksums(gemvq_ctx * ctx, int32_t * dst, size_t n);
  * HIP events on the context stream (the replays run back to back between the events). */
 int gemvq_graph_time(gemvq_ctx * ctx, int graph, int times, double * us_per_replay);
 
+/* Profiling (the counterpart of the reference's TRACE opcode and XRT-TIMING totals, gemvqc16.h:92-98,
+ * ggml-xrt.cpp:285-314, 1302-1397): runs a command list `reps` times, each kernel launched with device start/stop
+ * events (hipExtLaunchKernelGGL), and reports per launch the kernel, the commands it executes, its algorithmic
+ * bytes (GGUF-sized weights, fp32 vectors read and written once, state and KV cache traffic) and its average
+ * duration. The list's side effects happen `reps` times. Returns the number of launches (>= 0) or a status. */
+typedef struct {
+    char name[40];
+    int32_t first_cmd, n_cmds;
+    uint64_t bytes;
+    double us;
+} gemvq_launch_stat;
+int gemvq_profile(gemvq_ctx * ctx, const uint32_t * cmds, unsigned n_cmds, int reps, gemvq_launch_stat * out,
+                  int max_out);
+
 #ifdef __cplusplus
 }
 #endif
