@@ -176,132 +176,163 @@ __global__ __launch_bounds__(64) void gated_norm_kernel(GatedNormArgs a) {
 }
 
 // ---- attention core (one token, GQA, fp16 KV) ----
-// Workgroup (KV head, chunk of 64 positions), 256 threads. The chunk's keys and values are staged into LDS with
-// one coalesced pass; the workgroup normalizes and rotates its q heads and the new key, scores its positions
-// (pairwise over head_dim, 4 dims per lane), computes e^(s - chunk max) in parallel and the chunk's sums over
-// positions in order, and writes the partials. The last workgroup of a KV head combines the chunks in order and
-// applies the sigmoid output gate.
+// Workgroup (KV head, chunk of 64 positions), 256 threads; HD = head_dim, a power of two in [16, 256]. Every
+// global read of a phase is issued in one round (a dependent chain of global loads costs about a microsecond per
+// link, far more than the arithmetic here):
+//   1. the chunk's cached keys and values (thread t holds 16-byte piece t % (HD / 8) of rows t / (HD / 8) + k *
+//      (2048 / HD)), the q rows of the group's heads, the new key and value, the norm weights and the RoPE row;
+//   2. RMS norm with weight and NEOX RoPE of the q heads and the new key (element e in thread e), fp16 rounding;
+//      the new key and value go to the cache;
+//   3. scores from registers: 8 products and their adjacent tree in the thread, the tree over the HD / 8 pieces
+//      of a row across lanes (together the pairwise sum over head_dim), times scale;
+//   4. the chunk max per head, e^(s - max), then thread d sums p and p * v[d] over the positions in order for
+//      every head of the group and writes the partials (max, sum, o[hd]);
+//   5. the last workgroup of the KV head loads all chunks' partials (16 chunks per round), forms M = max m_c,
+//      f_c = e^(m_c - M), L = sum l_c f_c and O = sum o_c f_c in chunk order, and writes O / L times the sigmoid
+//      of the gate.
 constexpr int ATT_T = 256;
 constexpr int MAXHD = 256;
-constexpr int MAXG = 4;   // q heads per KV head
-constexpr int MAXCH = 64; // chunks (n_ctx <= 4096)
+constexpr int MAXG = 4;    // q heads per KV head
+constexpr int MAXCH = 64;  // chunks (n_ctx <= 4096)
+constexpr int CMB = 16;    // chunks per load round of the combine
 
-__device__ float head_norm_scale(const float * v, int hd, float eps, float * red) {
-    // pairwise over hd (<= 256): element tid in thread tid
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float e = tid < hd ? v[tid] : 0.0f;
-    const float t = pair_sum_lanes<64>(e * e);
-    if (lane == 0) red[wave] = t;
-    __syncthreads();
-    const float sum = (red[0] + red[1]) + (red[2] + red[3]);
-    __syncthreads();
-    return 1.0f / sqrtf(sum / float(hd) + eps);
-}
-
+template <int HD>
 __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
-    __shared__ uint16_t ks[ATTN_CHUNK * MAXHD], vs[ATTN_CHUNK * MAXHD];
-    __shared__ float qs[MAXG][MAXHD];      // fp16-rounded q of the group's heads
-    __shared__ float tmp[MAXHD];
-    __shared__ float sc[MAXG][ATTN_CHUNK];
-    __shared__ float red[4];
-    __shared__ float mx[MAXG], lsum[MAXG];
-    __shared__ float fc[MAXG][MAXCH];
+    constexpr int PER = HD / 8;                    // 16-byte pieces per row
+    constexpr int RPP = ATT_T / PER;               // rows per pass
+    constexpr int NP = (ATTN_CHUNK + RPP - 1) / RPP;  // passes
+    __shared__ __align__(16) uint16_t vs[ATTN_CHUNK * HD];
+    __shared__ __align__(16) float qs[MAXG + 1][HD];  // q heads and the new key: normalized, then rotated + rounded
+    __shared__ __align__(16) float pr[ATTN_CHUNK][MAXG];  // scores, then e^(s - max)
+    __shared__ float red[MAXG + 1][4];
+    __shared__ float mx[MAXG], fcs[MAXG][MAXCH], lcs[MAXG][MAXCH];
     __shared__ int last;
     const int kvh = blockIdx.x % a.n_head_kv, chunk = blockIdx.x / a.n_head_kv;
     const int pos = *a.pos, nc = (pos + ATTN_CHUNK) / ATTN_CHUNK;
     if (pos < 0 || pos >= a.n_ctx || chunk >= nc) return;  // positions past the KV capacity are not stored
-    const int tid = threadIdx.x, hd = a.head_dim, G = a.n_head / a.n_head_kv, half = a.n_rot / 2;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int t0 = chunk * ATTN_CHUNK, t1 = min(t0 + ATTN_CHUNK, pos + 1), nt = t1 - t0;
-    // stage the chunk's cached keys and values (positions before pos) into LDS, 16 bytes per load
-    {
-        const int per = hd / 8;  // 16-byte pieces per row
-        for (int c = tid; c < nt * per; c += ATT_T) {
-            const int ti = c / per, pc = c % per, t = t0 + ti;
-            if (t == pos) continue;
-            const size_t off = (size_t(t) * a.n_head_kv + kvh) * hd + pc * 8;
-            *reinterpret_cast<uint4 *>(ks + ti * hd + pc * 8) = *reinterpret_cast<const uint4 *>(a.kc + off);
-            *reinterpret_cast<uint4 *>(vs + ti * hd + pc * 8) = *reinterpret_cast<const uint4 *>(a.vc + off);
-        }
+    const int tid = threadIdx.x, G = a.n_head / a.n_head_kv, half = a.n_rot / 2;
+    const int lane = tid & 63, wave = tid >> 6, pc = tid % PER;
+    const int t0 = chunk * ATTN_CHUNK, nt = min(ATTN_CHUNK, pos + 1 - t0);
+    const bool has_new = chunk == nc - 1;  // this chunk holds pos
+    // ---- 1. loads ----
+    uint4 kr[NP], vr[NP];  // rows past the chunk re-read its last row (stored memory); they are not used
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+        const int ti = min(tid / PER + j * RPP, nt - 1);
+        const size_t off = (size_t(t0 + ti) * a.n_head_kv + kvh) * HD + pc * 8;
+        kr[j] = *reinterpret_cast<const uint4 *>(a.kc + off);
+        vr[j] = *reinterpret_cast<const uint4 *>(a.vc + off);
     }
-    const float * cs = a.cs + size_t(pos) * a.n_rot;
-    // q heads of the group: RMS norm with weight, NEOX RoPE on the first n_rot dims, fp16 rounding.
-    for (int g = 0; g < G; ++g) {
-        const int h = kvh * G + g;
-        const float * qr = a.q + size_t(h) * a.q_stride;
-        const float s = head_norm_scale(qr, hd, a.eps, red);
-        if (tid < hd) tmp[tid] = (qr[tid] * s) * a.qn[tid];
-        __syncthreads();
-        if (tid < hd) {
-            float o = tmp[tid];
-            if (tid < half) o = tmp[tid] * cs[2 * tid] - tmp[tid + half] * cs[2 * tid + 1];
-            else if (tid < a.n_rot) o = tmp[tid - half] * cs[2 * (tid - half) + 1] + tmp[tid] * cs[2 * (tid - half)];
-            qs[g][tid] = h2f(f2h(o));
-        }
-        __syncthreads();
+    const bool el = tid < HD;
+    const int e = el ? tid : 0;  // element of each head this thread holds
+    float xv[MAXG + 1];
+#pragma unroll
+    for (int g = 0; g < MAXG; ++g) xv[g] = (g < G && el) ? a.q[size_t(kvh * G + g) * a.q_stride + e] : 0.0f;
+    xv[MAXG] = (has_new && el) ? a.k[size_t(kvh) * HD + e] : 0.0f;
+    const float wq = a.qn[e], wk = a.kn[e];
+    const float vv = has_new ? a.v[size_t(kvh) * HD + e] : 0.0f;
+    const int pi = e < half ? e : e - half;  // the RoPE pair of this element
+    const bool rot = e < a.n_rot;
+    const float cs0 = rot ? a.cs[size_t(pos) * a.n_rot + 2 * pi] : 0.0f;
+    const float cs1 = rot ? a.cs[size_t(pos) * a.n_rot + 2 * pi + 1] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {  // values to LDS (the row of pos is overwritten with the new value below)
+        const int ti = tid / PER + j * RPP;
+        if (ti < nt) *reinterpret_cast<uint4 *>(vs + ti * HD + pc * 8) = vr[j];
     }
-    // the new key and value of this KV head (in the chunk that holds pos)
-    if (chunk == nc - 1) {
-        const float * kr = a.k + size_t(kvh) * hd;
-        const float s = head_norm_scale(kr, hd, a.eps, red);
-        if (tid < hd) tmp[tid] = (kr[tid] * s) * a.kn[tid];
-        __syncthreads();
-        if (tid < hd) {
-            float o = tmp[tid];
-            if (tid < half) o = tmp[tid] * cs[2 * tid] - tmp[tid + half] * cs[2 * tid + 1];
-            else if (tid < a.n_rot) o = tmp[tid - half] * cs[2 * (tid - half) + 1] + tmp[tid] * cs[2 * (tid - half)];
-            const uint32_t kb = f2h(o), vb = f2h(a.v[size_t(kvh) * hd + tid]);
-            ks[(pos - t0) * hd + tid] = uint16_t(kb);
-            vs[(pos - t0) * hd + tid] = uint16_t(vb);
-            const size_t off = (size_t(pos) * a.n_head_kv + kvh) * hd + tid;
+    // ---- 2. norms (pairwise over head_dim), RoPE, fp16 rounding ----
+#pragma unroll
+    for (int g = 0; g <= MAXG; ++g) {
+        const float t = pair_sum_lanes<64>(xv[g] * xv[g]);
+        if (lane == 0) red[g][wave] = t;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g <= MAXG; ++g) {
+        const float sum = (red[g][0] + red[g][1]) + (red[g][2] + red[g][3]);
+        const float sc = 1.0f / sqrtf(sum / float(HD) + a.eps);
+        if (el) qs[g][e] = (xv[g] * sc) * (g < MAXG ? wq : wk);
+    }
+    __syncthreads();
+    float rv[MAXG + 1];
+#pragma unroll
+    for (int g = 0; g <= MAXG; ++g) {
+        const float x0 = qs[g][pi], x1 = qs[g][pi + half];
+        rv[g] = e < half ? x0 * cs0 - x1 * cs1 : (rot ? x0 * cs1 + x1 * cs0 : qs[g][e]);
+    }
+    __syncthreads();
+    if (el) {
+#pragma unroll
+        for (int g = 0; g <= MAXG; ++g) qs[g][e] = h2f(f2h(rv[g]));
+        if (has_new) {
+            const uint32_t kb = f2h(rv[MAXG]), vb = f2h(vv);
+            vs[(pos - t0) * HD + e] = uint16_t(vb);
+            const size_t off = (size_t(pos) * a.n_head_kv + kvh) * HD + e;
             a.kc[off] = uint16_t(kb);
             a.vc[off] = uint16_t(vb);
         }
     }
     __syncthreads();
-    // scores: wave w takes positions w, w + 4, ..; lane l holds dims 4l .. 4l + 3
-    for (int ti = wave; ti < nt; ti += 4) {
-        float kv4[4];
+    // ---- 3. scores ----
+    float qv[MAXG][8], kn[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) kv4[i] = 4 * lane + i < hd ? h2f(ks[ti * hd + 4 * lane + i]) : 0.0f;
-        for (int g = 0; g < G; ++g) {
-            float pr[4];
+    for (int g = 0; g < MAXG; ++g)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) pr[i] = 4 * lane + i < hd ? qs[g][4 * lane + i] * kv4[i] : 0.0f;
-            const float dot = pair_sum_lanes<64>(tree<4>(pr));
-            if (lane == 0) sc[g][ti] = dot * a.scale;
+        for (int i = 0; i < 8; ++i) qv[g][i] = qs[g][pc * 8 + i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kn[i] = qs[MAXG][pc * 8 + i];
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+        const int ti = tid / PER + j * RPP;
+        const bool is_new = t0 + ti == pos;
+        const uint32_t kw[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
+        float kf[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kf[i] = is_new ? kn[i] : h2f((kw[i / 2] >> (16 * (i % 2))) & 0xffffu);
+#pragma unroll
+        for (int g = 0; g < MAXG; ++g) {
+            float t[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) t[i] = qv[g][i] * kf[i];
+            const float dot = pair_sum_lanes<PER>(tree<8>(t));
+            if (pc == 0 && ti < nt) pr[ti][g] = dot * a.scale;
         }
     }
     __syncthreads();
-    // chunk max (wave g for head g), e^(s - max) in parallel, the sum over positions in order
+    // ---- 4. chunk softmax numerators, partial sums in position order ----
     if (wave < G) {
-        const float s = lane < nt ? sc[wave][lane] : -__builtin_inff();
-        float m = s;
+        const float sv = lane < nt ? pr[lane][wave] : -__builtin_inff();
+        float m = sv;
 #pragma unroll
         for (int st = 32; st >= 1; st >>= 1) m = fmaxf(m, __shfl_xor(m, st, WAVE));
-        if (lane < nt) sc[wave][lane] = expf_(s - m);
+        if (lane < nt) pr[lane][wave] = expf_(sv - m);
         if (lane == 0) mx[wave] = m;
     }
     __syncthreads();
-    if (tid < G) {
-        float l = 0.0f;
-        for (int i = 0; i < nt; ++i) l += sc[tid][i];
-        lsum[tid] = l;
-    }
-    // o[g][d] = sum over positions in order of p * v
-    const int pstride = 2 + hd, nchmax = (a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
-    for (int od = tid; od < G * hd; od += ATT_T) {
-        const int g = od / hd, d = od % hd;
-        float o = 0.0f;
-        for (int i = 0; i < nt; ++i) o += sc[g][i] * h2f(vs[i * hd + d]);
-        float * pp = a.part + (size_t(kvh * G + g) * nchmax + chunk) * pstride;
-        pp[2 + d] = o;
-    }
-    __syncthreads();
-    if (tid < G) {
-        float * pp = a.part + (size_t(kvh * G + tid) * nchmax + chunk) * pstride;
-        pp[0] = mx[tid];
-        pp[1] = lsum[tid];
+    const int pstride = 2 + HD, nchmax = (a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
+    if (el) {
+        float o[MAXG] = {}, l[MAXG] = {};
+#pragma unroll 8
+        for (int i = 0; i < nt; ++i) {
+            const float4 p4 = *reinterpret_cast<const float4 *>(pr[i]);
+            const float p[4] = {p4.x, p4.y, p4.z, p4.w};
+            const float v = h2f(vs[i * HD + e]);
+#pragma unroll
+            for (int g = 0; g < MAXG; ++g) {
+                l[g] += p[g];
+                o[g] += p[g] * v;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < MAXG; ++g) {
+            if (g >= G) break;
+            float * pp = a.part + (size_t(kvh * G + g) * nchmax + chunk) * pstride;
+            pp[2 + e] = o[g];
+            if (e == 0) {
+                pp[0] = mx[g];
+                pp[1] = l[g];
+            }
+        }
     }
     __threadfence();
     __syncthreads();
@@ -309,41 +340,63 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
     __syncthreads();
     if (!last) return;
     __threadfence();
-    // combine: M = max of the chunk maxima, f_c = e^(m_c - M), L = sum_c l_c f_c, O = sum_c o_c f_c (in order)
+    // ---- 5. combine (last workgroup of the KV head) ----
+    const float * pk = a.part + size_t(kvh * G) * nchmax * pstride;
+    float gt[MAXG], ov[MAXG][CMB];
+#pragma unroll
+    for (int g = 0; g < MAXG; ++g)
+        gt[g] = (a.gate && g < G) ? a.gate[size_t(kvh * G + g) * 2 * HD + e] : 0.0f;
+    float mc = -__builtin_inff(), lc = 0.0f;
+    if (wave < G && lane < nc) {
+        mc = __builtin_nontemporal_load(pk + (size_t(wave) * nchmax + lane) * pstride);
+        lc = __builtin_nontemporal_load(pk + (size_t(wave) * nchmax + lane) * pstride + 1);
+    }
+#pragma unroll
+    for (int g = 0; g < MAXG; ++g)
+#pragma unroll
+        for (int c = 0; c < CMB; ++c)
+            ov[g][c] = (g < G && c < nc) ? __builtin_nontemporal_load(pk + (size_t(g) * nchmax + c) * pstride + 2 + e)
+                                         : 0.0f;
     if (wave < G) {
-        const float * pp = a.part + size_t(kvh * G + wave) * nchmax * pstride;
-        float m = -__builtin_inff();
-        for (int c = lane; c < nc; c += 64) m = fmaxf(m, __builtin_nontemporal_load(pp + size_t(c) * pstride));
+        float M = mc;
 #pragma unroll
-        for (int st = 32; st >= 1; st >>= 1) m = fmaxf(m, __shfl_xor(m, st, WAVE));
-        for (int c = lane; c < nc; c += 64) fc[wave][c] = expf_(__builtin_nontemporal_load(pp + size_t(c) * pstride) - m);
+        for (int st = 32; st >= 1; st >>= 1) M = fmaxf(M, __shfl_xor(M, st, WAVE));
+        if (lane < nc) {
+            fcs[wave][lane] = expf_(mc - M);
+            lcs[wave][lane] = lc;
+        }
     }
     __syncthreads();
-    if (tid < G) {
-        const float * pp = a.part + size_t(kvh * G + tid) * nchmax * pstride;
-        float L = 0.0f;
-        for (int c = 0; c < nc; ++c) L += __builtin_nontemporal_load(pp + size_t(c) * pstride + 1) * fc[tid][c];
-        lsum[tid] = L;
+    float O[MAXG] = {}, L[MAXG] = {};
+    for (int c0 = 0;;) {
+#pragma unroll
+        for (int c = 0; c < CMB; ++c) {
+            if (c0 + c >= nc) break;
+#pragma unroll
+            for (int g = 0; g < MAXG; ++g) {
+                const float f = fcs[g][c0 + c];
+                L[g] += lcs[g][c0 + c] * f;
+                O[g] += ov[g][c] * f;
+            }
+        }
+        c0 += CMB;
+        if (c0 >= nc) break;
+#pragma unroll
+        for (int g = 0; g < MAXG; ++g)
+#pragma unroll
+            for (int c = 0; c < CMB; ++c)
+                ov[g][c] = (g < G && c0 + c < nc)
+                               ? __builtin_nontemporal_load(pk + (size_t(g) * nchmax + c0 + c) * pstride + 2 + e)
+                               : 0.0f;
     }
-    __syncthreads();
-    for (int od = tid; od < G * hd; od += ATT_T) {
-        const int g = od / hd, d = od % hd, h = kvh * G + g;
-        const float * pp = a.part + size_t(h) * nchmax * pstride + 2 + d;
-        float O = 0.0f;
-        for (int c0 = 0; c0 < nc; c0 += 8) {  // 8 independent loads in flight, the sum still in chunk order
-            float v[8];
+    if (el) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = c0 + j < nc ? __builtin_nontemporal_load(pp + size_t(c0 + j) * pstride) : 0.0f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (c0 + j < nc) O += v[j] * fc[g][c0 + j];
+        for (int g = 0; g < MAXG; ++g) {
+            if (g >= G) break;
+            float out = O[g] / L[g];
+            if (a.gate) out = (1.0f / (1.0f + expf_(-gt[g]))) * out;
+            a.y[size_t(kvh * G + g) * HD + e] = out;
         }
-        float out = O / lsum[g];
-        if (a.gate) {
-            const float gt = a.gate[size_t(h) * 2 * hd + d];
-            out = (1.0f / (1.0f + expf_(-gt))) * out;
-        }
-        a.y[size_t(h) * hd + d] = out;
     }
     if (tid == 0) a.counter[kvh] = 0u;
 }
@@ -449,11 +502,17 @@ hipError_t launch_gated_norm(const GatedNormArgs & a, hipStream_t s) {
 }
 
 hipError_t launch_attn(const AttnArgs & a, hipStream_t s) {
-    if (a.head_dim > MAXHD || a.head_dim % 8 || a.n_head % a.n_head_kv || a.n_head / a.n_head_kv > MAXG ||
-        (a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK > MAXCH)
+    if (a.n_head % a.n_head_kv || a.n_head / a.n_head_kv > MAXG || (a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK > MAXCH)
         return hipErrorInvalidValue;
-    const int nch = (a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
-    GQ_LAUNCH(attn_kernel, dim3(a.n_head_kv * nch), dim3(ATT_T), 0, s, a);
+    const dim3 grid(a.n_head_kv * ((a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK));
+    switch (a.head_dim) {
+    case 16: GQ_LAUNCH(attn_kernel<16>, grid, dim3(ATT_T), 0, s, a); break;
+    case 32: GQ_LAUNCH(attn_kernel<32>, grid, dim3(ATT_T), 0, s, a); break;
+    case 64: GQ_LAUNCH(attn_kernel<64>, grid, dim3(ATT_T), 0, s, a); break;
+    case 128: GQ_LAUNCH(attn_kernel<128>, grid, dim3(ATT_T), 0, s, a); break;
+    case 256: GQ_LAUNCH(attn_kernel<256>, grid, dim3(ATT_T), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

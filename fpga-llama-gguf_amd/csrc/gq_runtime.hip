@@ -328,7 +328,7 @@ struct Compiler {
                 if (kv >= c->kvs.size()) return reject(i, "ATTN kv buffer");
                 const KvBuf & b = c->kvs[kv];
                 if (nkv == 0 || nh % nkv || nh / nkv > 4 || (b.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK > 64 || int(nkv) != b.n_head_kv || int(hd) != b.head_dim || hd > 256 ||
-                    hd % 16 || nrot > hd || nrot % 2)
+                    hd < 16 || (hd & (hd - 1)) || nrot > hd || nrot % 2)
                     return reject(i, "ATTN shape");
                 const uint32_t qstride = (flags & 1) ? 2 * hd : hd;
                 if (!range(k[2], uint64_t(qstride) * (nh - 1) + hd) || !range(k[4], uint64_t(nh) * hd) || !range(k[6], 1) ||

@@ -132,19 +132,23 @@ def test_gdn_step(gq, orc, ctx, flags, hv, hk):
         assert np.all(np.abs(y_want - y_ref) <= 1e-6 + 4e-6 * ymag)
 
 
-def test_attention(gq, orc, ctx):
-    nh, nkv, hd, nrot, n_ctx = 16, 4, 256, 64, 200
+@pytest.mark.parametrize("nh,nkv,hd,nrot,n_ctx,npos,checks", [
+    (16, 4, 256, 64, 200, 130, (0, 1, 63, 64, 65, 127, 128, 129)),  # Qwen3.5 shape, crosses two chunk boundaries
+    (6, 2, 128, 128, 1100, 1041, (1023, 1024, 1040)),  # 17 chunks: two load rounds in the combine
+    (4, 4, 64, 16, 80, 70, (5, 69)),  # one q head per KV head
+])
+def test_attention(gq, orc, ctx, nh, nkv, hd, nrot, n_ctx, npos, checks):
     kv = ctx.kv_create(n_ctx, nkv, hd)
     qn = gq.uniform(2, 51, hd, 0.5, 1.5)
     kn = gq.uniform(2, 52, hd, 0.5, 1.5)
     table = np.concatenate([orc.rope_cache(p, nrot, 1e7) for p in range(n_ctx)])
-    O = dict(qg=0, k=8192, v=9216, qn=10240, kn=10496, cs=16384, pos=65536, y=70000 // 16 * 16)
+    O = dict(qg=0, k=8192, v=9216, qn=10240, kn=10496, pos=10752, y=10768, cs=16384)  # cs: n_ctx * nrot floats
     ctx.write(O["qn"], qn)
     ctx.write(O["kn"], kn)
     ctx.write(O["cs"], table)
     kc = np.zeros((n_ctx, nkv, hd), np.uint16)
     vc = np.zeros((n_ctx, nkv, hd), np.uint16)
-    for pos in range(130):  # crosses two chunk boundaries
+    for pos in range(npos):
         qg = gq.normal(3, 1000 + pos, 2 * nh * hd)
         k = gq.normal(3, 5000 + pos, nkv * hd)
         v = gq.normal(3, 9000 + pos, nkv * hd)
@@ -160,13 +164,13 @@ def test_attention(gq, orc, ctx):
         kh = orc.rope(orc.rownorm(k, kn, hd, nkv, 1e-6), cs, nrot, hd, nkv)
         kc[pos] = orc.f2h(kh).reshape(nkv, hd)
         vc[pos] = orc.f2h(v).reshape(nkv, hd)
-        if pos in (0, 1, 63, 64, 65, 127, 128, 129):
+        if pos in checks:
             att = orc.attn(qh, kc, vc, nh, nkv, hd, pos + 1, 1 / 16)
             gate = qg.reshape(nh, 2 * hd)[:, hd:].ravel()
             want = orc.silu_mul(gate, att, sigmoid=True)
             assert_bits(ctx.read(O["y"], nh * hd), want, f"attention at pos {pos}")
-    k_dev, v_dev = ctx.kv_read(kv, 0, 130, nkv * hd)
-    assert np.array_equal(k_dev, kc[:130].ravel()) and np.array_equal(v_dev, vc[:130].ravel())
+    k_dev, v_dev = ctx.kv_read(kv, 0, npos, nkv * hd)
+    assert np.array_equal(k_dev, kc[:npos].ravel()) and np.array_equal(v_dev, vc[:npos].ravel())
 
 
 def test_gemv_fused_epilogs(gq, orc, ctx):
