@@ -333,7 +333,7 @@ static void ref_q4_1(const uint8_t * w, const float * x, int rows, int cols, flo
             const float dw = orc_half_to_float(rd16(blk)), mw = orc_half_to_float(rd16(blk + 2));
             const float term = (dw * d8[b]) * (float)sumi + mw * s8[b];
             sum += term;
-            m += fabs((dw * d8[b]) * (float)sumi) + fabs(mw * s8[b]);
+            m += fabsf((dw * d8[b]) * (float)sumi) + fabsf(mw * s8[b]); /* a float sum, as std::fabs(float) gives */
         }
         y[r] = sum;
         if (mag) mag[r] = m;

@@ -6,6 +6,7 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, os.path.join(ROOT, "fpga-llama-gguf_amd"))
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 
 
 def pytest_configure(config):
@@ -24,4 +25,6 @@ def gq():
 def orc():
     import oracle
 
+    if not os.path.exists(oracle.ORC_PATH):  # a fresh checkout: the oracle builds in seconds
+        oracle.build(ref=False)
     return oracle

@@ -85,3 +85,15 @@ def test_gemv_edge_inputs(gq, orc):
     w8 = w8.ravel()
     y8 = run_gemv(gq, gq.Q8_0, rows, cols, w8, x)
     assert_bits(y8, orc.fx_gemv(gq.Q8_0, w8, x, rows, cols), "negative scales")
+
+
+@pytest.mark.parametrize("t", [2, 8, 13, 14])
+def test_gemv_against_reference_vectors(gq, t):
+    """The GPU GEMV on the stored inputs against the reference's own CPU results (tests/golden), within the
+    reference tolerance |got - ref| <= 1e-6 + 1e-5 |ref| + 1e-6 sum |block terms| (gemvq_ref.h:267-272)."""
+    from golden_data import golden
+
+    g = golden()
+    y = run_gemv(gq, t, 16, 512, g[f"gemv{t}_w"], g["gemv_x"])
+    ref, mag = g[f"gemv{t}_y"].astype(np.float64), g[f"gemv{t}_mag"]
+    assert np.all(np.abs(y - ref) <= 1e-6 + 1e-5 * np.abs(ref) + 1e-6 * mag)
