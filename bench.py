@@ -37,6 +37,19 @@ class LaunchStat(C.Structure):
                 ("us", C.c_double)]
 
 
+def measured_traffic(kernel: str) -> tuple[int | None, str | None]:
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, each
+    scaled by the same counter on a copy kernel of known size), if that kernel was measured."""
+    path = os.path.join(ROOT, "profiles", "c5_decode_pmc.md")
+    if not os.path.exists(path):
+        return None, None
+    for line in open(path):
+        parts = line.split()
+        if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
+            return int(float(parts[2])), os.path.relpath(path, ROOT)
+    return None, None
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -71,6 +84,20 @@ def cpu_baseline(blob, cfg, prompt, n_tokens: int, threads: int) -> dict:
                       f"{dt:.1f} s)"}
 
 
+def copy_probe(mib: int) -> int:
+    """y = -x over mib MiB of float32: an element-wise kernel that reads and writes exactly mib MiB each."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    x = torch.ones(n, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(5):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_read": n * 4, "copy_probe_bytes_written": n * 4, "launches": 5}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -83,7 +110,12 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=32, help="(testing) fewer layers; the reported line is then invalid")
     ap.add_argument("--direct", action="store_true",
                     help="plain stream launches instead of graph replays (for tracing tools); slower per step")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy kernel of MIB MiB 5 times (calibrates the HBM byte counters "
+                         "of rocprofv3 --pmc) and exit")
     args = ap.parse_args()
+    if args.copy_probe:
+        return copy_probe(args.copy_probe)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               f"(the multi-GPU sharding is a design note, not code)", file=sys.stderr)
@@ -142,6 +174,7 @@ def main() -> int:
             f"{a['bytes'] / a['us'] / 1e3:8.1f} GB/s")
     dom_name, dom = max(agg.items(), key=lambda kv: kv[1]["us"])
     achieved = dom["bytes"] / dom["us"] / 1e3  # GB/s
+    traffic, traffic_src = measured_traffic(dom_name)
     m.close()
 
     cpu = None
@@ -182,7 +215,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "launches": dom["n"],
             "bytes_per_launch": dom["bytes"] // dom["n"],
             "us_per_launch": round(dom["us"] / dom["n"], 3),

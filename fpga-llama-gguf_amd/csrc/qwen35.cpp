@@ -291,11 +291,7 @@ gemvq_qwen35 * gemvq_qwen35_create(gemvq_ctx * ctx, const gemvq_qw_config * cfg,
         delete m;
         return nullptr;
     }
-    if (gemvq_graph_create(ctx, m->cmds.data(), unsigned(m->cmds.size() / GEMVQ_CMD_WORDS), &m->graph)) {
-        delete m;
-        return nullptr;
-    }
-    return m;
+    return m;  // the per-token graph is captured by the first gemvq_qwen35_step
 }
 
 void gemvq_qwen35_destroy(gemvq_qwen35 * m) {
@@ -324,19 +320,22 @@ int gemvq_qwen35_reset(gemvq_qwen35 * m, const int32_t * prompt, int n) {
     if (!st) st = gemvq_act_write(ctx, 16, scal, 48);
     if (!st) st = gemvq_act_write(ctx, m->tok, &prompt[0], 1);
     if (st) return st;
-    // NEXT_TOKEN reads the prompt length from its command; rebuild the graph when it changes
+    // NEXT_TOKEN reads the prompt length from its command; the graph is captured again when it changes
     const size_t last = m->cmds.size() - GEMVQ_CMD_WORDS;
     if (m->cmds[last + 5] != uint32_t(n)) {
         m->cmds[last + 5] = uint32_t(n);
         if (m->graph >= 0) gemvq_graph_destroy(ctx, m->graph);
         m->graph = -1;
-        st = gemvq_graph_create(ctx, m->cmds.data(), unsigned(m->cmds.size() / GEMVQ_CMD_WORDS), &m->graph);
     }
     return st;
 }
 
 int gemvq_qwen35_step(gemvq_qwen35 * m, int n) {
-    if (!m || m->graph < 0) return GEMVQ_EINVAL;
+    if (!m) return GEMVQ_EINVAL;
+    if (m->graph < 0) {
+        const int st = gemvq_graph_create(m->ctx, m->cmds.data(), unsigned(m->cmds.size() / GEMVQ_CMD_WORDS), &m->graph);
+        if (st) return st;
+    }
     return gemvq_graph_replay(m->ctx, m->graph, n);
 }
 

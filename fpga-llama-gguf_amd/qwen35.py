@@ -191,7 +191,8 @@ def _lib():
 
 
 class Model:
-    """The model on the GPU: one context sized for it, the weights uploaded, the per-token graph captured."""
+    """The model on the GPU: one context sized for it, the weights uploaded, the per-token command list built (its
+    graph is captured by the first `step`)."""
 
     def __init__(self, blob: Blob, device: int = 0):
         self.lib = _lib()

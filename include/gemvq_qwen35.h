@@ -37,14 +37,15 @@ typedef struct gemvq_qwen35 gemvq_qwen35;
 /* Context sizes a model needs (activation floats, weight bytes, GDN state rows). */
 int gemvq_qwen35_sizes(const gemvq_qw_config * cfg, const gemvq_tensor_desc * table, int n_tensors,
                        size_t * act_floats, size_t * weight_bytes, size_t * state_rows);
-/* Uploads the weights into ctx, allocates KV buffers, lays out the activation buffer and captures the per-token
- * graph. Returns NULL on failure (gemvq_last_error(ctx) says why). */
+/* Uploads the weights into ctx, allocates KV buffers, lays out the activation buffer and builds the per-token
+ * command list. Returns NULL on failure (gemvq_last_error(ctx) says why). */
 gemvq_qwen35 * gemvq_qwen35_create(gemvq_ctx * ctx, const gemvq_qw_config * cfg, const gemvq_tensor_desc * table,
                                    int n_tensors, const uint8_t * blob);
 void gemvq_qwen35_destroy(gemvq_qwen35 * m);
 /* Clears recurrent states and KV, stores the prompt (n >= 1 ids) and sets position 0 with token prompt[0]. */
 int gemvq_qwen35_reset(gemvq_qwen35 * m, const int32_t * prompt, int n);
-/* Enqueues n decode steps (graph replays); asynchronous. */
+/* Enqueues n decode steps (replays of the per-token graph, captured by the first step after create or after a
+ * reset with a new prompt length); asynchronous. */
 int gemvq_qwen35_step(gemvq_qwen35 * m, int n);
 /* Token ids at positions 0 .. n - 1 (prompt tokens, then generated ones); synchronizes. */
 int gemvq_qwen35_tokens(gemvq_qwen35 * m, int32_t * out, int n);
@@ -54,7 +55,7 @@ int gemvq_qwen35_logits(gemvq_qwen35 * m, float * out);
 int gemvq_qwen35_hidden(gemvq_qwen35 * m, float * out);
 /* The per-token command list (words) and the number of commands; n_words = 0 queries the size. */
 int gemvq_qwen35_commands(gemvq_qwen35 * m, uint32_t * words, size_t n_words);
-/* The captured graph id (for gemvq_graph_time). */
+/* The captured graph id (for gemvq_graph_time); -1 before the first step. */
 int gemvq_qwen35_graph(gemvq_qwen35 * m);
 
 #ifdef __cplusplus
