@@ -9,46 +9,13 @@ namespace gq {
 
 constexpr int WAVE = 64;
 
-// IEEE binary16 <-> binary32, round to nearest even; overflow gives infinity (gemvq_ref.h:16-52).
-__device__ __forceinline__ float h2f(uint32_t h) {
-    const uint32_t sign = (h & 0x8000u) << 16;
-    uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu, bits;
-    if (e == 0) {
-        if (m == 0) {
-            bits = sign;
-        } else {
-            const int lz = __builtin_clz(m) - 21;  // shifts that bring the leading bit to position 10
-            m <<= lz;
-            bits = sign | (uint32_t(113 - lz) << 23) | ((m & 0x3ffu) << 13);
-        }
-    } else if (e == 31) {
-        bits = sign | 0x7f800000u | (m << 13);
-    } else {
-        bits = sign | ((e + 112u) << 23) | (m << 13);
-    }
-    return __uint_as_float(bits);
-}
+// IEEE binary16 -> binary32 (gemvq_ref.h:16-30): exact for every half, subnormals included (the hardware
+// conversion; fp16 denormals are preserved in the default mode), NaN stays NaN.
+__device__ __forceinline__ float h2f(uint32_t h) { return float(__builtin_bit_cast(_Float16, uint16_t(h))); }
 
-__device__ __forceinline__ uint32_t f2h(float f) {
-    const uint32_t bits = __float_as_uint(f);
-    const uint32_t sign = (bits >> 16) & 0x8000u;
-    const int e = int((bits >> 23) & 0xff) - 127 + 15;
-    uint32_t m = bits & 0x7fffffu;
-    if (e >= 31) return sign | 0x7c00u;
-    if (e <= 0) {
-        if (e < -10) return sign;
-        m |= 0x800000u;
-        const int sh = 14 - e;
-        uint32_t r = m >> sh;
-        const uint32_t rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1);
-        if (rem > half || (rem == half && (r & 1u))) ++r;
-        return sign | r;
-    }
-    uint32_t out = (uint32_t(e) << 10) | (m >> 13);
-    const uint32_t rem = m & 0x1fffu;
-    if (rem > 0x1000u || (rem == 0x1000u && (out & 1u))) ++out;
-    return sign | out;
-}
+// binary32 -> binary16, round to nearest even, subnormal results rounded, overflow to infinity (gemvq_ref.h:32-52):
+// the hardware conversion in the default rounding mode.
+__device__ __forceinline__ uint32_t f2h(float f) { return __builtin_bit_cast(uint16_t, _Float16(f)); }
 
 // exp: Cody-Waite reduction x = n ln2 + r (ln2 in a 15-bit and a low part), Taylor series of e^r to r^7/7! by
 // Horner with fused multiply-adds, exact scaling by 2^n; results below the normal range flush to +0.
@@ -143,6 +110,31 @@ __device__ __forceinline__ float pair_sum_lanes(float v) {
 #pragma unroll
     for (int s = 16; s < WIDTH; s <<= 1) v = v + __shfl_xor(v, s, WAVE);
     return v;
+}
+
+// The same for N independent values at once (their cross-lane steps interleave instead of waiting in turn).
+template <int WIDTH, int N>
+__device__ __forceinline__ void pair_sum_lanes_n(float * v) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if (WIDTH > 1) v[i] = v[i] + dpp_f32<DPP_XOR1>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if (WIDTH > 2) v[i] = v[i] + dpp_f32<DPP_XOR2>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if (WIDTH > 4) v[i] = v[i] + dpp_f32<DPP_HALF_MIRROR>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if (WIDTH > 8) v[i] = v[i] + dpp_f32<DPP_MIRROR>(v[i]);
+#pragma unroll
+    for (int st = 16; st < WIDTH; st <<= 1) {
+        float o[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) o[i] = __shfl_xor(v[i], st, WAVE);
+#pragma unroll
+        for (int i = 0; i < N; ++i) v[i] = v[i] + o[i];
+    }
 }
 
 // In-register adjacent tree of N (power of two) consecutive elements.

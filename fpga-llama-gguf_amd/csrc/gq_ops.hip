@@ -114,6 +114,25 @@ __global__ __launch_bounds__(128) void gdn_kernel(GdnArgs a) {
         q[0] = q0.x; q[1] = q0.y; q[2] = q0.z; q[3] = q0.w; q[4] = q1.x; q[5] = q1.y; q[6] = q1.z; q[7] = q1.w;
         k[0] = k0.x; k[1] = k0.y; k[2] = k0.z; k[3] = k0.w; k[4] = k1.x; k[5] = k1.y; k[6] = k1.z; k[7] = k1.w;
     }
+    // all state rows of this thread are requested before any is written (src and dst may be the same rows)
+    constexpr int IT = GDN_ROWS / 8;
+    float x[IT][8], vj[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int j = chunk * GDN_ROWS + it * 8 + grp;
+        const size_t row = (size_t(h) * 128 + j) * 128 + 8 * l16;
+        const float4 s0 = *reinterpret_cast<const float4 *>(a.src + row);
+        const float4 s1 = *reinterpret_cast<const float4 *>(a.src + row + 4);
+        x[it][0] = s0.x; x[it][1] = s0.y; x[it][2] = s0.z; x[it][3] = s0.w;
+        x[it][4] = s1.x; x[it][5] = s1.y; x[it][6] = s1.z; x[it][7] = s1.w;
+        vj[it] = a.v[h * 128 + j];
+    }
+    const float g_raw = a.g[h], b_raw = a.beta[h];
+    float dtv = 0.0f, av = 0.0f;
+    if (a.flags & 8) {
+        dtv = a.dt[h];
+        av = a.a[h];
+    }
     if (a.flags & 2) {  // L2 norm of q and k per key head (ggml_l2_norm)
         float sq[8], sk[8];
 #pragma unroll
@@ -129,35 +148,44 @@ __global__ __launch_bounds__(128) void gdn_kernel(GdnArgs a) {
             k[i] = k[i] * fk;
         }
     }
-    float gv = a.g[h], bt = a.beta[h];
+    float gv = g_raw, bt = b_raw;
     if (a.flags & 8) {  // gates from the raw projections: beta = sigmoid(b), g = softplus(a_raw + dt) * a
-        gv = softplus_(a.g[h] + a.dt[h]) * a.a[h];
-        bt = sigmoid_(a.beta[h]);
+        gv = softplus_(g_raw + dtv) * av;
+        bt = sigmoid_(b_raw);
     }
     const float decay = expf_(gv);
-    for (int it = 0; it < GDN_ROWS / 8; ++it) {
-        const int j = chunk * GDN_ROWS + it * 8 + grp;
-        const size_t row = (size_t(h) * 128 + j) * 128 + 8 * l16;
-        const float4 s0 = *reinterpret_cast<const float4 *>(a.src + row);
-        const float4 s1 = *reinterpret_cast<const float4 *>(a.src + row + 4);
-        float x[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    float dot[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
         float pr[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            x[i] = x[i] * decay;
-            pr[i] = x[i] * k[i];
+            x[it][i] = x[it][i] * decay;
+            pr[i] = x[it][i] * k[i];
         }
-        const float dot = pair_sum_lanes<16>(tree<8>(pr));
-        const float delta = (a.v[h * 128 + j] - dot) * bt;
+        dot[it] = tree<8>(pr);
+    }
+    pair_sum_lanes_n<16, IT>(dot);
+    float out[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const float delta = (vj[it] - dot[it]) * bt;
+        float pr[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            x[i] = x[i] + k[i] * delta;
-            pr[i] = x[i] * q[i];
+            x[it][i] = x[it][i] + k[i] * delta;
+            pr[i] = x[it][i] * q[i];
         }
-        const float out = pair_sum_lanes<16>(tree<8>(pr));
-        *reinterpret_cast<float4 *>(a.dst + row) = make_float4(x[0], x[1], x[2], x[3]);
-        *reinterpret_cast<float4 *>(a.dst + row + 4) = make_float4(x[4], x[5], x[6], x[7]);
-        if (l16 == 0) a.y[h * 128 + j] = out * a.scale;
+        out[it] = tree<8>(pr);
+    }
+    pair_sum_lanes_n<16, IT>(out);
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int j = chunk * GDN_ROWS + it * 8 + grp;
+        const size_t row = (size_t(h) * 128 + j) * 128 + 8 * l16;
+        *reinterpret_cast<float4 *>(a.dst + row) = make_float4(x[it][0], x[it][1], x[it][2], x[it][3]);
+        *reinterpret_cast<float4 *>(a.dst + row + 4) = make_float4(x[it][4], x[it][5], x[it][6], x[it][7]);
+        if (l16 == 0) a.y[h * 128 + j] = out[it] * a.scale;
     }
 }
 
@@ -241,11 +269,13 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
         if (ti < nt) *reinterpret_cast<uint4 *>(vs + ti * HD + pc * 8) = vr[j];
     }
     // ---- 2. norms (pairwise over head_dim), RoPE, fp16 rounding ----
+    float sq[MAXG + 1];
 #pragma unroll
-    for (int g = 0; g <= MAXG; ++g) {
-        const float t = pair_sum_lanes<64>(xv[g] * xv[g]);
-        if (lane == 0) red[g][wave] = t;
-    }
+    for (int g = 0; g <= MAXG; ++g) sq[g] = xv[g] * xv[g];
+    pair_sum_lanes_n<64, MAXG + 1>(sq);
+    if (lane == 0)
+#pragma unroll
+        for (int g = 0; g <= MAXG; ++g) red[g][wave] = sq[g];
     __syncthreads();
 #pragma unroll
     for (int g = 0; g <= MAXG; ++g) {
@@ -281,10 +311,10 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
         for (int i = 0; i < 8; ++i) qv[g][i] = qs[g][pc * 8 + i];
 #pragma unroll
     for (int i = 0; i < 8; ++i) kn[i] = qs[MAXG][pc * 8 + i];
+    float dots[NP][MAXG];
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
-        const int ti = tid / PER + j * RPP;
-        const bool is_new = t0 + ti == pos;
+        const bool is_new = t0 + tid / PER + j * RPP == pos;
         const uint32_t kw[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
         float kf[8];
 #pragma unroll
@@ -294,9 +324,16 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
             float t[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) t[i] = qv[g][i] * kf[i];
-            const float dot = pair_sum_lanes<PER>(tree<8>(t));
-            if (pc == 0 && ti < nt) pr[ti][g] = dot * a.scale;
+            dots[j][g] = tree<8>(t);
         }
+    }
+    pair_sum_lanes_n<PER, NP * MAXG>(&dots[0][0]);
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+        const int ti = tid / PER + j * RPP;
+        if (pc == 0 && ti < nt)
+            *reinterpret_cast<float4 *>(pr[ti]) =
+                make_float4(dots[j][0] * a.scale, dots[j][1] * a.scale, dots[j][2] * a.scale, dots[j][3] * a.scale);
     }
     __syncthreads();
     // ---- 4. chunk softmax numerators, partial sums in position order ----
@@ -334,12 +371,14 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
             }
         }
     }
-    __threadfence();
     __syncthreads();
-    if (tid == 0) last = atomicAdd(a.counter + kvh, 1u) == unsigned(nc - 1);
+    if (tid == 0) {  // the partials are released (agent scope) by the counter update; the last workgroup acquires
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        last = atomicAdd(a.counter + kvh, 1u) == unsigned(nc - 1);
+        if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
     __syncthreads();
     if (!last) return;
-    __threadfence();
     // ---- 5. combine (last workgroup of the KV head) ----
     const float * pk = a.part + size_t(kvh * G) * nchmax * pstride;
     float gt[MAXG], ov[MAXG][CMB];
