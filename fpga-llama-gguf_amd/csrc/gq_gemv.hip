@@ -102,9 +102,44 @@ __device__ __forceinline__ void quantize_block(const float * v, int b, Lds & s) 
     s.info[b] = f2h(d) | (uint32_t(sum & 0xffff) << 16);
 }
 
+// The DeltaNet gated output norm applied while quantizing (gemvqc_gdn.h:284-346): per head of 128, x =
+// silu(z) * ((y * s) * w) with s = 1 / sqrt(sum(y^2) / 128 + eps), the sum the pairwise tree over the head (the
+// tree over each 32-block, then over the head's 4 consecutive blocks, held by 4 aligned lanes). cols <= 8192 and a
+// multiple of 128. Workgroup 0 also stores the gated values, which the separate norm would have written.
+__device__ __forceinline__ void prologue_gated(const GemvArgs & a, Lds & s) {
+    const int nb = a.cols / 32, b = threadIdx.x;
+    if (b >= nb) return;  // whole groups of 4 lanes (nb is a multiple of 4)
+    float v[32], z[32], w[32];
+    load_block(a.x + size_t(b) * 32, v);
+    load_block(a.gate_z + size_t(b) * 32, z);
+    load_block(a.norm_w + size_t(b & 3) * 32, w);
+    float sq[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) sq[j] = v[j] * v[j];
+    const float sum = pair_sum_lanes<4>(tree<32>(sq));
+    const float sc = 1.0f / sqrtf(sum / 128.0f + a.norm_eps);
+    if (a.gate_silu) {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) v[j] = z[j] * ((v[j] * sc) * w[j]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) v[j] = silu_(z[j]) * ((v[j] * sc) * w[j]);
+    }
+    if (blockIdx.x == 0) {
+        float4 * o = reinterpret_cast<float4 *>(a.x_out + size_t(b) * 32);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    }
+    quantize_block(v, b, s);
+}
+
 template <int ROUNDS>  // rounds of 256 blocks the registers hold (cols <= 8192: 1)
 __device__ void prologue_q8_0(const GemvArgs & a, Lds & s) {
     const int nb = a.cols / 32, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (a.xsrc == XSRC_GATED) {
+        prologue_gated(a, s);
+        return;
+    }
     if (a.xsrc != XSRC_NORM) {
         for (int b = tid; b < nb; b += NT) {
             float v[32];
@@ -568,6 +603,8 @@ __device__ __forceinline__ void row_compute(const GemvArgs & a, const GemvMember
             out = (v / (1.0f + expf_(-v))) * fixed_to_float(acc2);  // gemvqc_ops.h:88-92
         } else if constexpr (EPI == EPI_ADD) {
             out = v + R.e[0];  // gemvqc16.cpp:282-301
+        } else if constexpr (EPI == EPI_SILU) {
+            out = silu_(v);  // gemvqc_ops.h:70-79 (UNARY SiLU) on the row result
         } else if constexpr (EPI == EPI_CONV) {  // gemvqc_ops.h:387-431 on the row result
             float sum = 0.0f;
             sum += R.e[0] * R.e[4];
@@ -652,6 +689,7 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
         case EPI_SWIGLU: run_rows<TYPE, NU, EPI_SWIGLU, DBG>(a, m, mi, r0, r1, cur, xb, xk, c); break;
         case EPI_ADD: run_rows<TYPE, NU, EPI_ADD, DBG>(a, m, mi, r0, r1, cur, xb, xk, c); break;
         case EPI_CONV: run_rows<TYPE, NU, EPI_CONV, DBG>(a, m, mi, r0, r1, cur, xb, xk, c); break;
+        case EPI_SILU: run_rows<TYPE, NU, EPI_SILU, DBG>(a, m, mi, r0, r1, cur, xb, xk, c); break;
         default: run_rows<TYPE, NU, EPI_PLAIN, DBG>(a, m, mi, r0, r1, cur, xb, xk, c); break;
         }
     }
@@ -666,11 +704,22 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
     }
 }
 
+// Workgroups of `kernel` that fit on the device at once (a grid beyond it runs a second, mostly idle round).
+template <typename K>
+int resident_blocks(K kernel) {
+    int dev = 0, cus = 0, occ = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, NT, 0) != hipSuccess || occ < 1 || cus < 1)
+        return 1024;
+    return occ * cus;
+}
+
 template <int TYPE, int NU>
 hipError_t launch_typed(const GemvArgs & a, hipStream_t st) {
-    // about 16 tasks per workgroup (4 per wave) amortize the activation prologue; at most 1024 workgroups
+    // about 16 tasks per workgroup (4 per wave) amortize the activation prologue; no more workgroups than fit
+    static const int cap = resident_blocks(gemv_kernel<TYPE, NU, false>);
     int grid = (a.total_tasks + 15) / 16;
-    grid = grid < 1 ? 1 : grid > 1024 ? 1024 : grid;
+    grid = grid < 1 ? 1 : grid > cap ? cap : grid;
     if (a.dbg) GQ_LAUNCH((gemv_kernel<TYPE, NU, true>), dim3(grid), dim3(NT), 0, st, a);
     else GQ_LAUNCH((gemv_kernel<TYPE, NU, false>), dim3(grid), dim3(NT), 0, st, a);
     return hipGetLastError();

@@ -21,8 +21,8 @@ struct WeightView {
     const uint8_t * d;
 };
 
-enum : int { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_ADD = 2, EPI_CONV = 3 };
-enum : int { XSRC_RAW = 0, XSRC_NORM = 1 };
+enum : int { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_ADD = 2, EPI_CONV = 3, EPI_SILU = 4 };
+enum : int { XSRC_RAW = 0, XSRC_NORM = 1, XSRC_GATED = 2 };  // XSRC_GATED: gate_silu says whether z is silu(z)
 
 struct GemvMember {
     WeightView w;    // matrix (g of a SwiGLU pair)
@@ -39,10 +39,13 @@ struct GemvMember {
 };
 
 struct GemvArgs {
-    const float * x;          // activation (act + x_off)
-    const float * norm_w;     // deferred norm weight (NULL: no weight)
+    const float * x;          // activation (act + x_off); XSRC_GATED: the raw DeltaNet output
+    const float * norm_w;     // deferred norm weight (NULL: no weight); XSRC_GATED: the gated norm's weight [128]
     float norm_eps;
-    int xsrc;                 // XSRC_RAW or XSRC_NORM
+    int xsrc;                 // XSRC_RAW, XSRC_NORM or XSRC_GATED
+    const float * gate_z;     // XSRC_GATED: z (the output gate) [cols]
+    float * x_out;            // XSRC_GATED: the gated activation is also written here (by workgroup 0)
+    int gate_silu;            // XSRC_GATED: gate_z holds silu(z) already
     int norm_l2;
     int cols;
     int n_members;
@@ -110,10 +113,11 @@ struct GdnArgs {
 
 struct GatedNormArgs {    // per head of 128: y = silu(z) * ((y * s) * w), s = 1 / sqrt(mean(y^2) + eps)
     float * y;
-    const float * z;
+    const float * z;          // z, or silu(z) when z_silu
     const float * w;
     int heads;
     float eps;
+    int z_silu;
 };
 
 struct AttnArgs {
@@ -152,6 +156,7 @@ struct NextTokenArgs {
 };
 
 constexpr int ATTN_CHUNK = 64;
+constexpr int GDN_MAX_HEADS = 64;  // value heads of one GDN command
 
 // Profiling: when set (by gemvq_profile on the calling thread), launchers start kernels through
 // hipExtLaunchKernelGGL with these events, which record the kernel's own start and end on the device.

@@ -197,8 +197,9 @@ __global__ __launch_bounds__(64) void gated_norm_kernel(GatedNormArgs a) {
     const float sum = pair_sum_lanes<64>(y0 * y0 + y1 * y1);
     const float s = 1.0f / sqrtf(sum / 128.0f + a.eps);
     const float z0 = a.z[h * 128 + 2 * l], z1 = a.z[h * 128 + 2 * l + 1];
-    const float o0 = silu_(z0) * ((y0 * s) * a.w[2 * l]);
-    const float o1 = silu_(z1) * ((y1 * s) * a.w[2 * l + 1]);
+    const float g0 = a.z_silu ? z0 : silu_(z0), g1 = a.z_silu ? z1 : silu_(z1);
+    const float o0 = g0 * ((y0 * s) * a.w[2 * l]);
+    const float o1 = g1 * ((y1 * s) * a.w[2 * l + 1]);
     y[2 * l] = o0;
     y[2 * l + 1] = o1;
 }

@@ -67,6 +67,7 @@ struct gemvq_ctx {
     size_t dbg_n = 0;
     int32_t * dbg_dst = nullptr;  // host destination; non-NULL while armed
     bool dbg_used = false;        // the list being compiled writes the dump
+    float * gdn_raw = nullptr;    // raw DeltaNet output when its gated norm is folded into the next GEMV
     int last_launches = 0;
     std::string err;
 };
@@ -177,6 +178,18 @@ struct Compiler {
         return (w.type == type && w.rows == rows && w.cols == cols) ? &w : nullptr;
     }
 
+    // A GDN's gated output norm pending for the GEMV group that reads its output next.
+    struct Gated { bool on = false; uint32_t y; const float * z; const float * w; float eps; int z_silu; } gated;
+
+    // The command at `next` is a Q4_0 / Q8_0 GEMV that reads exactly the GDN output y (cols = heads * 128 <= 8192).
+    bool fold_gated(const uint32_t * cmds, unsigned n, unsigned next, uint32_t y, uint32_t cols) const {
+        if (next >= n || cols > 8192) return false;
+        const uint32_t * g = cmds + size_t(next) * GEMVQ_CMD_WORDS;
+        const int t = int(g[1] & 0xffu);
+        const bool apart = g[7] + uint64_t(g[2]) <= y || uint64_t(y) + cols <= g[7];  // its output is not the GDN's
+        return g[0] == GEMVQ_OP_GEMV && g[6] == y && g[3] == cols && (t == T_Q4_0 || t == T_Q8_0) && apart;
+    }
+
     bool compile(const uint32_t * cmds, unsigned n) {
         struct Deferred { bool on = false; uint32_t n, x, w, y; float eps; uint32_t flags; } defer;
         for (unsigned i = 0; i < n;) {
@@ -259,7 +272,7 @@ struct Compiler {
                 const bool gates = flags & GEMVQ_GDN_GATES;
                 if (gates && i + 2 >= n) return reject(i, "GDN needs its gates slot");
                 const uint32_t * k3 = gates ? k2 + GEMVQ_CMD_WORDS : nullptr;
-                if (hv == 0 || hk == 0 || hv > 64 || hv % hk) return reject(i, "GDN heads");
+                if (hv == 0 || hk == 0 || hv > GDN_MAX_HEADS || hv % hk) return reject(i, "GDN heads");
                 if (!range(k[2], hk * 128) || !range(k[3], hk * 128) || !range(k[4], hv * 128) || !range(k[5], hv) ||
                     !range(k[6], hv) || !range(k[7], hv * 128))
                     return reject(i, "GDN range");
@@ -285,14 +298,22 @@ struct Compiler {
                 a.scale = bits_f(k2[2]);
                 a.l2_eps = bits_f(k2[4]);
                 a.flags = int(flags);
+                const unsigned next = i + (gates ? 3 : 2);
+                if ((flags & GEMVQ_GDN_GATED) && fold_gated(cmds, n, next, k[7], hv * 128)) {
+                    // the gated norm runs in the next GEMV's activation prologue: the step writes its raw output
+                    // to scratch, and that GEMV writes the gated values to y as the norm would have
+                    a.y = c->gdn_raw;
+                    a.flags = int(flags & ~GEMVQ_GDN_GATED);
+                    gated = {true, k[7], A(k2[7]), A(k2[6]), bits_f(k2[5]), int(bool(flags & GEMVQ_GDN_Z_SILU))};
+                }
                 out.push_back(LGdn{a});
                 spans.push_back({int(i), gates ? 3 : 2});
-                if (flags & GEMVQ_GDN_GATED) {
-                    GatedNormArgs g{A(k[7]), A(k2[7]), A(k2[6]), int(hv), bits_f(k2[5])};
+                if ((flags & GEMVQ_GDN_GATED) && !gated.on) {
+                    GatedNormArgs g{A(k[7]), A(k2[7]), A(k2[6]), int(hv), bits_f(k2[5]), int(bool(flags & GEMVQ_GDN_Z_SILU))};
                     out.push_back(LGated{g});
                     spans.push_back({int(i), gates ? 3 : 2});
                 }
-                i += gates ? 3 : 2;
+                i = next;
                 continue;
             }
             case GEMVQ_OP_CONV: {
@@ -428,7 +449,7 @@ struct Compiler {
             const int rows = int(k[2]);
             if (gemvs > 0 && (k[6] != x_off || k[3] != cols || t != type)) break;
             if (!type_ok(t) || !shape_ok(t, rows, int(k[3]))) return reject(i, "GEMV format or shape");
-            if (flags & ~(GEMVQ_GEMV_SWIGLU | GEMVQ_GEMV_CONV | GEMVQ_GEMV_ADD | GEMVQ_GEMV_ARGMAX))
+            if (flags & ~(GEMVQ_GEMV_SWIGLU | GEMVQ_GEMV_CONV | GEMVQ_GEMV_ADD | GEMVQ_GEMV_ARGMAX | GEMVQ_GEMV_SILU))
                 return reject(i, "GEMV flags");
             if (__builtin_popcount(flags) > 1) return reject(i, "GEMV: at most one epilog bit");
             const uint64_t woff = uint64_t(k[4]) | (uint64_t(k[5]) << 32);
@@ -436,6 +457,8 @@ struct Compiler {
             if (!w) return reject(i, "GEMV weight offset, format or shape does not match an uploaded weight");
             if (!range(k[6], k[3]) || !range(k[7], uint64_t(rows))) return reject(i, "GEMV range");
             if (gemvs + ((flags & GEMVQ_GEMV_SWIGLU) ? 2 : 1) > GEMVQ_GROUP) break;
+            // workgroup 0 writes the gated activation while the group runs: no member may write over it
+            if (gated.on && gemvs > 0 && !(k[7] + uint64_t(rows) <= gated.y || uint64_t(gated.y) + cols <= k[7])) break;
             if (gemvs == 0) {
                 type = t;
                 x_off = k[6];
@@ -462,6 +485,8 @@ struct Compiler {
                 m.y = A(u[7]);
                 y_off = u[7];
                 step = 2;
+            } else if (flags & GEMVQ_GEMV_SILU) {
+                m.epi = EPI_SILU;
             } else if (flags & (GEMVQ_GEMV_CONV | GEMVQ_GEMV_ADD | GEMVQ_GEMV_ARGMAX)) {
                 if (i + 1 >= n) return reject(i, "GEMV epilog without its command");
                 const uint32_t * e = k + GEMVQ_CMD_WORDS;
@@ -506,7 +531,16 @@ struct Compiler {
         a.total_tasks = tasks;
         a.x = A(x_off);
         a.xsrc = XSRC_RAW;
-        if (defer.on && defer.y == x_off && defer.n == cols) {
+        if (gated.on) {  // the group right after the GDN whose output it reads (checked when the GDN compiled)
+            a.xsrc = XSRC_GATED;
+            a.x = c->gdn_raw;
+            a.gate_z = gated.z;
+            a.norm_w = gated.w;
+            a.norm_eps = gated.eps;
+            a.x_out = A(gated.y);
+            a.gate_silu = gated.z_silu;
+            gated.on = false;
+        } else if (defer.on && defer.y == x_off && defer.n == cols) {
             a.xsrc = XSRC_NORM;
             a.x = A(defer.x);
             a.norm_w = (defer.flags & GEMVQ_NORM_NO_WEIGHT) ? nullptr : A(defer.w);
@@ -537,7 +571,7 @@ std::pair<std::string, uint64_t> describe(const Launch & l, int pos) {
         const GemvArgs & a = g->a;
         const bool kq = g->type == T_Q5_K || g->type == T_Q6_K;
         const int nu = (a.cols / (kq ? 64 : 32) + 63) / 64;
-        uint64_t b = uint64_t(a.cols) * 4 * (a.xsrc == XSRC_NORM && a.norm_w ? 2 : 1);
+        uint64_t b = uint64_t(a.cols) * 4 * (a.xsrc == XSRC_GATED ? 3 : a.xsrc == XSRC_NORM && a.norm_w ? 2 : 1);
         for (int i = 0; i < a.n_members; ++i) {
             const GemvMember & m = a.m[i];
             const uint64_t rows = uint64_t(m.rows);
@@ -620,6 +654,7 @@ gemvq_ctx * gemvq_ctx_create(int device, size_t act_floats, size_t weight_bytes,
     if (e == hipSuccess) e = hipMemset(c->act, 0, std::max<size_t>(act_floats, 16) * sizeof(float));
     if (e == hipSuccess && weight_bytes) e = hipMalloc(&c->warena, weight_bytes);
     if (e == hipSuccess && state_rows) e = hipMalloc(&c->state, state_rows * 128 * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&c->gdn_raw, size_t(GDN_MAX_HEADS) * 128 * sizeof(float));
     if (e == hipSuccess && state_rows) e = hipMemset(c->state, 0, state_rows * 128 * sizeof(float));
     if (e != hipSuccess) {
         g_create_error = std::string("gemvq_ctx_create: ") + hipGetErrorString(e);
@@ -649,6 +684,7 @@ void gemvq_ctx_destroy(gemvq_ctx * c) {
     hipFree(c->act);
     hipFree(c->warena);
     hipFree(c->state);
+    hipFree(c->gdn_raw);
     hipFree(c->dbg);
     if (c->stream) hipStreamDestroy(c->stream);
     delete c;

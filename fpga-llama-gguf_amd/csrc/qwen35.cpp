@@ -2,8 +2,9 @@
 //
 // Layer order follows llama.cpp's qwen35 graph as the reference offloads it (llama.cpp/patches/0006: all input
 // projections of a layer right after its norm) in the fused forms of the reference kernel (fpga/src/gemvqc16.h):
-//   DeltaNet layer: deferred RMSNORM -> GEMV group {qkv + CONV epilog, z, beta, alpha} -> GDN (L2 q/k, gates,
-//                   gated output norm) -> ssm_out GEMV + residual ADD epilog
+//   DeltaNet layer: deferred RMSNORM -> GEMV group {qkv + CONV epilog, z + SiLU epilog, beta, alpha} -> GDN (L2
+//                   q/k, gates, gated output norm on silu(z)) -> ssm_out GEMV + residual ADD epilog (the runtime
+//                   applies the gated norm in that GEMV's activation prologue)
 //   attention layer: deferred RMSNORM -> GEMV group {q+gate, k, v} -> ATTN (q/k norm, RoPE, KV append, softmax,
 //                   sigmoid gate) -> attn_output GEMV + ADD
 //   both: deferred RMSNORM -> {ffn_gate, ffn_up} SwiGLU pair -> ffn_down GEMV + ADD
@@ -179,14 +180,14 @@ bool build_commands(gemvq_qwen35 & m, std::string & err) {
             const uint32_t ba2 = m.ba + uint32_t(up16(hv));
             e.gemv(*wqkv, m.xn, m.qkv, GEMVQ_GEMV_CONV);
             e.cmd({GEMVQ_OP_CONV, uint32_t(ch), m.qkv, cw->act_off, m.cqkv, m.conv_state[il], m.conv_state[il], 1u});
-            e.gemv(*wz, m.xn, m.z);
+            e.gemv(*wz, m.xn, m.z, GEMVQ_GEMV_SILU);  // the gate's SiLU, once per element
             e.gemv(*wb, m.xn, m.ba);
             e.gemv(*wa, m.xn, ba2);
             // state rows of this layer: layer slot * hv * 128
             int slot = 0;
             for (int j = 0; j < il; ++j) slot += !is_attn(c, j);
             const uint32_t row = uint32_t(slot) * uint32_t(hv) * 128u;
-            const uint32_t flags = GEMVQ_GDN_L2_QK | GEMVQ_GDN_GATED | GEMVQ_GDN_GATES;
+            const uint32_t flags = GEMVQ_GDN_L2_QK | GEMVQ_GDN_GATED | GEMVQ_GDN_GATES | GEMVQ_GDN_Z_SILU;
             e.cmd({GEMVQ_OP_GDN, uint32_t(hv) | (uint32_t(hk) << 16), m.cqkv, m.cqkv + uint32_t(hk * S),
                    m.cqkv + uint32_t(2 * hk * S), ba2, m.ba, m.y});
             e.cmd({row, row, fb(1.0f / std::sqrt(float(S))), flags, fb(eps), fb(eps), sn->act_off, m.z});

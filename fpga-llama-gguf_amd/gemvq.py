@@ -22,8 +22,8 @@ Q4_0, Q8_0, Q5_K, Q6_K = 2, 8, 13, 14
 # opcodes (gemvqc16.h:100-111 plus the opcodes of this backend)
 OP_GEMV, OP_RMSNORM, OP_ADD, OP_SILU_MUL, OP_MUL, OP_UNARY, OP_GDN, OP_CONV, OP_STATE_LOAD, OP_ROPE, OP_TRACE = range(1, 12)
 OP_ATTN, OP_GET_ROWS, OP_ARGMAX, OP_NEXT_TOKEN, OP_FILL = 12, 13, 14, 15, 16
-GEMV_SWIGLU, GEMV_CONV, GEMV_ADD, GEMV_ARGMAX = 0x100, 0x200, 0x400, 0x800
-GDN_WITH_GEMV, GDN_L2_QK, GDN_GATED, GDN_GATES, GDN_WITH_OUT = 1, 2, 4, 8, 16
+GEMV_SWIGLU, GEMV_CONV, GEMV_ADD, GEMV_ARGMAX, GEMV_SILU = 0x100, 0x200, 0x400, 0x800, 0x1000
+GDN_WITH_GEMV, GDN_L2_QK, GDN_GATED, GDN_GATES, GDN_WITH_OUT, GDN_Z_SILU = 1, 2, 4, 8, 16, 32
 NORM_L2, NORM_NO_WEIGHT, NORM_DEFER = 1, 2, 4
 SILU_MUL_SIGMOID = 1
 UNARY_SILU, UNARY_SIGMOID, UNARY_SOFTPLUS, UNARY_COPY = 1, 2, 3, 4

@@ -22,8 +22,9 @@
  *   GEMV      [1, format | flags, rows, cols, w_off lo, w_off hi, x_off, y_off]
  *             format 2 Q4_0, 8 Q8_0, 13 Q5_K, 14 Q6_K; flags GEMVQ_GEMV_SWIGLU (0x100), GEMVQ_GEMV_CONV (0x200),
  *             GEMVQ_GEMV_ADD (0x400) as gemvqc16.h:31-45, and GEMVQ_GEMV_ARGMAX (0x800): the next command is an
- *             ARGMAX over this GEMV's y (consumed; y is written). Groups of up to 4 GEMVs with the same x_off, cols
- *             and format run as one pass; a group ends after a GEMV whose y overlaps x.
+ *             ARGMAX over this GEMV's y (consumed; y is written), and GEMVQ_GEMV_SILU (0x1000): y = silu(W x) =
+ *             v / (1 + e^-v) (the UNARY SiLU folded into the GEMV, no command consumed). Groups of up to 4 GEMVs with
+ *             the same x_off, cols and format run as one pass; a group ends after a GEMV whose y overlaps x.
  *   RMSNORM   [2, n, x_off, w_off, y_off, eps bits, rows, flags]  flags bit0 L2, bit1 no weight, bit2 deferred
  *             (the following GEMVs with x_off == y_off and cols == n quantize the normalized row), bits 23:8 row
  *             stride in 16-float words (0: packed).
@@ -34,6 +35,9 @@
  *             + [src_row, dst_row, scale bits, flags, l2_eps bits, rms_eps bits, w_off, z_off]
  *             (+ [dt_off, a_off, 0...] with GEMVQ_GDN_GATES) as gemvqc16.h:60-81; GEMVQ_GDN_WITH_GEMV and
  *             GEMVQ_GDN_WITH_OUT are accepted (the results are those of the commands run one by one).
+ *             GEMVQ_GDN_Z_SILU (32): z_off already holds silu(z), the gated norm multiplies by it directly. A GDN with
+ *             the gated norm followed by a Q4_0 / Q8_0 GEMV reading its y applies the norm in that GEMV's activation
+ *             prologue (one launch less; y is still written).
  *   ATTN      [12, n_head | n_head_kv << 16, q_off, kv, y_off, head_dim | n_rot << 16, pos_off, flags]
  *             + [k_off, v_off, scale bits, eps bits, qn_off, kn_off, cs_off, gate_off]
  *             One token of GQA attention (q head h reads KV head h / (n_head / n_head_kv)). q rows (head_dim floats)
@@ -80,12 +84,14 @@ extern "C" {
 #define GEMVQ_GEMV_CONV 0x200u
 #define GEMVQ_GEMV_ADD 0x400u
 #define GEMVQ_GEMV_ARGMAX 0x800u
+#define GEMVQ_GEMV_SILU 0x1000u
 #define GEMVQ_GROUP 4u
 #define GEMVQ_GDN_WITH_GEMV 1u
 #define GEMVQ_GDN_L2_QK 2u
 #define GEMVQ_GDN_GATED 4u
 #define GEMVQ_GDN_GATES 8u
 #define GEMVQ_GDN_WITH_OUT 16u
+#define GEMVQ_GDN_Z_SILU 32u
 #define GEMVQ_NORM_L2 1u
 #define GEMVQ_NORM_NO_WEIGHT 2u
 #define GEMVQ_NORM_DEFER 4u

@@ -699,7 +699,8 @@ void orc_gdn(float * state, const float * q, const float * k, const float * v, c
         if (flags & 4) {
             float * yh = y + h * S;
             const float s = orc_norm_scale(yh, S, rms_eps, 0);
-            for (int i = 0; i < S; ++i) yh[i] = orc_silu(z[h * S + i]) * ((yh[i] * s) * w[i]);
+            for (int i = 0; i < S; ++i)
+                yh[i] = ((flags & 32) ? z[h * S + i] : orc_silu(z[h * S + i])) * ((yh[i] * s) * w[i]);
         }
     }
     free(qn); free(kn);

@@ -82,7 +82,8 @@ void orc_ref_unary(const float * x, int n, int kind, float * y);
 void orc_ref_gdn(float * state, const float * q, const float * k, const float * v, const float * g, const float * beta,
                  int hv, int hk, float scale, float * y, double * y_mag, double * s_mag);
 /* Canonical fused step (GDN opcode): flags bit1 L2-normalize q/k (l2_eps), bit2 gated output norm
- * (rms_eps, w[128], z[hv*128]), bit3 gates from raw projections (beta = sigmoid(b), g = softplus(a_raw + dt) * a).
+ * (rms_eps, w[128], z[hv*128]), bit3 gates from raw projections (beta = sigmoid(b), g = softplus(a_raw + dt) * a),
+ * bit5 z already holds silu(z).
  * state updated in place, y receives the (gated) output. */
 void orc_gdn(float * state, const float * q, const float * k, const float * v, const float * graw, const float * braw,
              const float * dt, const float * a, const float * z, const float * w, int hv, int hk, float scale,

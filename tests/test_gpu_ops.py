@@ -132,6 +132,47 @@ def test_gdn_step(gq, orc, ctx, flags, hv, hk):
         assert np.all(np.abs(y_want - y_ref) <= 1e-6 + 4e-6 * ymag)
 
 
+@pytest.mark.parametrize("hv,hk,wtype,z_silu", [(32, 16, 2, True), (32, 16, 2, False), (8, 2, 8, False)])
+def test_gdn_gated_norm_folded_into_gemv(gq, orc, ctx, hv, hk, wtype, z_silu):
+    """A GDN with the gated output norm followed by a GEMV that reads its output: the norm runs in the GEMV's
+    activation prologue (no separate launch). Results equal the unfused sequence and the oracle, bit for bit, and the
+    gated output is still written to the GDN's y."""
+    S, R = 128, 96
+    cols = hv * S
+    flags = gq.GDN_L2_QK | gq.GDN_GATED | gq.GDN_GATES | (gq.GDN_Z_SILU if z_silu else 0)
+    q, k, v = gq.normal(5, 1, hk * S), gq.normal(5, 2, hk * S), gq.normal(5, 3, hv * S)
+    g, beta, dt, a = gq.normal(5, 4, hv), gq.normal(5, 5, hv), gq.normal(5, 6, hv), -np.abs(gq.normal(5, 7, hv))
+    z, w = gq.normal(5, 8, cols), gq.uniform(5, 9, S, 0.5, 1.5)
+    if z_silu:  # the gate already activated (a SiLU epilog upstream): z holds silu(z)
+        z = orc.unary(z, 1)
+    state = gq.normal(5, 10, hv * S * S) * 0.1
+    res = gq.normal(5, 11, R)
+    W = gq.matrix(wtype, R, cols, 5, 12)
+    off = ctx.upload(wtype, R, cols, W)
+    O = dict(q=0, k=4096, v=8192, g=12288, beta=12352, dt=12416, a=12480, y=16384, w=24576, z=28672, res=36864,
+             out=37376, dummy=38400)
+    for name, arr in dict(q=q, k=k, v=v, g=g, beta=beta, dt=dt, a=a, w=w, z=z).items():
+        ctx.write(O[name], arr)
+    gdn = gq.gdn(hv, hk, O["q"], O["k"], O["v"], O["g"], O["beta"], O["y"], 256, 256, 1 / np.sqrt(S), flags,
+                 1e-6, 1e-6, O["w"], O["z"], O["dt"], O["a"])
+    gemv = gq.gemv(wtype, R, cols, off, O["y"], O["out"], gq.GEMV_ADD) + gq.add(R, O["out"], O["res"], O["res"])
+    results = []
+    for fused in (True, False):
+        ctx.state_write(256, state)
+        ctx.write(O["res"], res)
+        ctx.write(O["y"], np.zeros(cols, np.float32))
+        cmds = gdn + (gemv if fused else gq.fill(16, O["dummy"], 0.0) + gemv)
+        assert ctx.run(cmds) == 0, ctx.error()
+        assert ctx.launch_count() == (2 if fused else 4)  # folded: no separate gated-norm launch
+        results.append((ctx.read(O["res"], R), ctx.read(O["y"], cols), ctx.state_read(256, hv * 128)))
+    y_want, st_want = orc.gdn(state, q, k, v, g, beta, hv, hk, float(1 / np.sqrt(S)), flags, dt, a, z, w)
+    out_want = orc.fx_gemv(wtype, W, y_want, R, cols) + res
+    for (o, y, st), what in zip(results, ("folded", "separate")):
+        assert_bits(y, y_want, f"{what}: gated y")
+        assert_bits(st, st_want, f"{what}: state")
+        assert_bits(o, out_want, f"{what}: GEMV + residual")
+
+
 @pytest.mark.parametrize("nh,nkv,hd,nrot,n_ctx,npos,checks", [
     (16, 4, 256, 64, 200, 130, (0, 1, 63, 64, 65, 127, 128, 129)),  # Qwen3.5 shape, crosses two chunk boundaries
     (6, 2, 128, 128, 1100, 1041, (1023, 1024, 1040)),  # 17 chunks: two load rounds in the combine
@@ -228,6 +269,15 @@ def test_gemv_fused_epilogs(gq, orc, ctx):
     assert_bits(ctx.read(ACT, V), logits, "head logits")
     key = ctx.read(65536, 2, np.uint32)
     assert 0xFFFFFFFF - int(key[0]) == int(np.argmax(logits))
+    # SiLU epilog (a UNARY SiLU folded into the GEMV) on a group member next to a plain one
+    zs = gq.matrix(gq.Q4_0, 384, K, 0, 73)
+    oz = ctx.upload(gq.Q4_0, 384, K, zs)
+    cmds = gq.gemv(gq.Q4_0, ch, K, oc, X, T) + gq.gemv(gq.Q4_0, 384, K, oz, X, Y, gq.GEMV_SILU)
+    ctx.write(X, xc)
+    assert ctx.run(cmds) == 0, ctx.error()
+    assert ctx.launch_count() == 1
+    assert_bits(ctx.read(T, ch), orc.fx_gemv(gq.Q4_0, wc, xc, ch, K), "plain member")
+    assert_bits(ctx.read(Y, 384), orc.unary(orc.fx_gemv(gq.Q4_0, zs, xc, 384, K), 1), "silu epilog")
 
 
 def test_get_rows_and_next_token(gq, orc, ctx):
