@@ -97,3 +97,21 @@ def test_gemv_against_reference_vectors(gq, t):
     y = run_gemv(gq, t, 16, 512, g[f"gemv{t}_w"], g["gemv_x"])
     ref, mag = g[f"gemv{t}_y"].astype(np.float64), g[f"gemv{t}_mag"]
     assert np.all(np.abs(y - ref) <= 1e-6 + 1e-5 * np.abs(ref) + 1e-6 * mag)
+
+
+@pytest.mark.parametrize("t,rows,cols", [(14, 151936, 4096), (13, 12288, 4096)])
+def test_c3_k_quant_full_shapes(gq, orc, t, rows, cols):
+    """C3 at its real shapes: the Q6_K output head [151936 x 4096] and a Q5_K projection [12288 x 4096] against
+    Q8_K activations. Every row's result and block sums are checked against the oracle on a sample of rows (rows are
+    independent), and those rows against the reference's sequential path within its tolerance."""
+    w = gq.matrix(t, rows, cols, SEED, 30 + t, std=0.02)
+    x = gq.normal(SEED, 40 + t, cols)
+    y, dbg = run_gemv(gq, t, rows, cols, w, x, blocksums=True)
+    rb = gq.row_bytes(t, cols)
+    sample = np.arange(0, rows, 37)
+    ws = w.reshape(rows, rb)[sample].ravel()
+    yo, bso, _ = orc.fx_gemv(t, ws, x, len(sample), cols, blocksums=True)
+    assert_bits(y[sample], yo, f"C3 type {t}")
+    assert np.array_equal(dbg.reshape(rows, -1)[sample].ravel(), bso)
+    yr, mag = orc.ref_gemv(t, ws, x, len(sample), cols)
+    assert np.all(np.abs(y[sample].astype(np.float64) - yr) <= 1e-6 + 1e-5 * np.abs(yr) + 1e-6 * mag)

@@ -43,3 +43,24 @@ def test_graph_replay_is_deterministic(gq, q35):
         a = m.generate(prompt, 30)
         b = m.generate(prompt, 30)
     assert np.array_equal(a, b)
+
+
+def test_full_width_model_greedy_matches_oracle(gq, orc, q35):
+    """The C5 widths (hidden 4096, FFN 12288, vocab 151936, 16/4 heads of 256, 32/16 DeltaNet heads) with 4 layers
+    (3 DeltaNet + 1 attention): greedy tokens, logits and hidden state identical to the oracle decoder."""
+    cfg = q35.Config(n_layer=4, n_ctx=64)
+    blob = q35.generate(cfg, seed=0)
+    prompt = q35.prompt_ids(cfg, 8)
+    n_gen = 16
+    om = orc.Model(q35.config_c(cfg), blob.table, blob.n, blob.data)
+    want = om.generate(prompt, n_gen)
+    with q35.Model(blob) as m:
+        got = m.generate(prompt, n_gen)
+        lg, hd = m.logits(), m.hidden()
+    assert np.array_equal(got, want), f"first mismatch at {np.nonzero(got != want)[0][:3]}"
+    lo = np.empty(cfg.n_vocab, np.float32)
+    om2 = orc.Model(q35.config_c(cfg), blob.table, blob.n, blob.data)
+    for pos in range(len(prompt) - 1 + n_gen):
+        om2.decode(int(want[pos]), pos, lo if pos == len(prompt) - 2 + n_gen else None)
+    assert np.array_equal(lg.view(np.uint32), lo.view(np.uint32))
+    assert np.array_equal(hd.view(np.uint32), om2.hidden().view(np.uint32))

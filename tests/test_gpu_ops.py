@@ -312,3 +312,50 @@ def test_invalid_commands_rejected(gq, ctx):
     assert ctx.run(gq.add(16, 3, 0, 32)) == 1                                      # misaligned offset
     assert ctx.run(gq.add(16, 0, 0, ctx.act_floats)) == 1                          # out of range
     assert ctx.run(gq.gdn(64, 3, 0, 0, 0, 0, 0, 0, 0, 0, 1.0)) == 1                # hv not a multiple of hk
+
+
+def test_c4_gated_deltanet_layer(gq, orc):
+    """C4: one Gated DeltaNet layer at hidden 4096 as the decoder issues it: deferred RMS norm, the {qkv + CONV, z +
+    SiLU, beta, alpha} Q4_0 GEMV group, the GDN step with L2 q/k, gates and the gated norm (folded into ssm_out's
+    prologue), ssm_out Q4_0 [4096 x 4096] + residual. State N(0, 0.1^2), conv cache N(0, 1), gate logits N(0, 1)."""
+    E, Hk, Hv, S = 4096, 16, 32, 128
+    ch = 2 * Hk * S + Hv * S
+    eps = 1e-6
+    x, nw = gq.normal(7, 1, E), gq.uniform(7, 2, E, 0.5, 1.5)
+    Wqkv, Wz = gq.matrix(2, ch, E, 7, 3), gq.matrix(2, Hv * S, E, 7, 4)
+    Wb, Wa, Wo = gq.matrix(2, Hv, E, 7, 5), gq.matrix(2, Hv, E, 7, 6), gq.matrix(2, E, Hv * S, 7, 7)
+    cw, cst = gq.normal(7, 8, 4 * ch, std=0.5), gq.normal(7, 9, 3 * ch)
+    dt, a, sw = gq.normal(7, 10, Hv), -np.abs(gq.normal(7, 11, Hv)), gq.uniform(7, 12, S, 0.5, 1.5)
+    state = gq.normal(7, 13, Hv * S * S) * 0.1
+    ctx = gq.Context(act_floats=1 << 17, weight_bytes=48 << 20, state_rows=Hv * 128)
+    oq, oz, ob, oa, oo = (ctx.upload(2, r, c, w) for r, c, w in
+                          ((ch, E, Wqkv), (Hv * S, E, Wz), (Hv, E, Wb), (Hv, E, Wa), (E, Hv * S, Wo)))
+    O = dict(x=0, nw=4096, xn=8192, qkv=12288, cqkv=20480, z=28672, ba=32768, y=32832, cw=40960, cst=73728,
+             dt=98304, a=98368, sw=98432, out=98560)
+    for k_, v_ in dict(x=x, nw=nw, cw=cw, cst=cst, dt=dt, a=a, sw=sw).items():
+        ctx.write(O[k_], v_)
+    ctx.state_write(0, state)
+    flags = gq.GDN_L2_QK | gq.GDN_GATED | gq.GDN_GATES | gq.GDN_Z_SILU
+    cmds = (gq.rmsnorm(E, O["x"], O["nw"], O["xn"], eps, flags=gq.NORM_DEFER) +
+            gq.gemv(2, ch, E, oq, O["xn"], O["qkv"], gq.GEMV_CONV) +
+            gq.conv(ch, O["qkv"], O["cw"], O["cqkv"], O["cst"], O["cst"]) +
+            gq.gemv(2, Hv * S, E, oz, O["xn"], O["z"], gq.GEMV_SILU) +
+            gq.gemv(2, Hv, E, ob, O["xn"], O["ba"]) + gq.gemv(2, Hv, E, oa, O["xn"], O["ba"] + 32) +
+            gq.gdn(Hv, Hk, O["cqkv"], O["cqkv"] + Hk * S, O["cqkv"] + 2 * Hk * S, O["ba"] + 32, O["ba"], O["y"], 0, 0,
+                   1 / np.sqrt(S), flags, eps, eps, O["sw"], O["z"], O["dt"], O["a"]) +
+            gq.gemv(2, E, Hv * S, oo, O["y"], O["out"], gq.GEMV_ADD) + gq.add(E, O["out"], O["x"], O["x"]))
+    assert ctx.run(cmds) == 0, ctx.error()
+    assert ctx.launch_count() == 3  # group (norm folded), GDN, ssm_out (gated norm folded)
+    xn = orc.rownorm(x, nw, E, 1, eps)
+    yc, ns = orc.conv(cst, orc.fx_gemv(2, Wqkv, xn, ch, E), cw)
+    z = orc.unary(orc.fx_gemv(2, Wz, xn, Hv * S, E), 1)
+    b, al = orc.fx_gemv(2, Wb, xn, Hv, E), orc.fx_gemv(2, Wa, xn, Hv, E)
+    y, st = orc.gdn(state, yc[:Hk * S], yc[Hk * S:2 * Hk * S], yc[2 * Hk * S:], al, b, Hv, Hk, float(1 / np.sqrt(S)),
+                    flags, dt, a, z, sw)
+    assert_bits(ctx.read(O["cst"], 3 * ch), ns, "conv state")
+    assert_bits(ctx.read(O["cqkv"], ch), yc, "conv output")
+    assert_bits(ctx.read(O["z"], Hv * S), z, "silu(z)")
+    assert_bits(ctx.state_read(0, Hv * 128), st, "DeltaNet state")
+    assert_bits(ctx.read(O["y"], Hv * S), y, "gated output")
+    assert_bits(ctx.read(O["x"], E), orc.fx_gemv(2, Wo, y, E, Hv * S) + x, "layer output")
+    ctx.close()
