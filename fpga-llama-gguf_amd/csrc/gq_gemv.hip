@@ -22,6 +22,7 @@ struct Lds {
     int8_t xq[MAXK];           // quantized activation
     uint32_t info[MAXK / 32];  // Q8_0: fp16 scale | (sum of the block's quants) << 16; Q8_K: FP32 d bits per super-block
     int16_t bs[MAXK / 16];     // Q8_K bsums
+    uint16_t s1[MAXK / 32];    // Q8_1: fp16 of (sum of the block's quants) * d, for Q4_1 weights
     float red[2 * NWAVES + 64];
     unsigned long long key[NWAVES];
 };
@@ -100,6 +101,7 @@ __device__ __forceinline__ void quantize_block(const float * v, int b, Lds & s) 
     dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
     dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
     s.info[b] = f2h(d) | (uint32_t(sum & 0xffff) << 16);
+    s.s1[b] = uint16_t(f2h(float(sum) * d));  // ggml quantize_row_q8_1: s = fp16(sum * d) with the FP32 d
 }
 
 // The DeltaNet gated output norm applied while quantizing (gemvqc_gdn.h:284-346): per head of 128, x =
@@ -270,10 +272,11 @@ __device__ void quantize_q8_K(const GemvArgs & a, float scale, Lds & s) {
 }
 
 // ---- per-lane activation slices ----
-struct XB {  // one 32-block (Q4_0 / Q8_0)
+struct XB {  // one 32-block (Q4_0 / Q4_1 / Q8_0)
     uint32_t q[8];
     float dx40;  // the block's fp16 scale times 2^40 (exact)
     int sum;     // sum of its quants (for the Q4_0 offset of 8)
+    float sx40;  // Q4_1: the block's fp16 s (Q8_1) times 2^40 (exact)
 };
 struct XK {  // one 64-weight unit (Q5_K / Q6_K)
     uint32_t q[16];
@@ -282,6 +285,7 @@ struct XK {  // one 64-weight unit (Q5_K / Q6_K)
 };
 
 // Lanes past the last unit load a valid unit (their terms are never added).
+template <int TYPE>
 __device__ __forceinline__ void load_xb(const Lds & s, int b, int nb, XB & x) {
     b = b < nb ? b : nb - 1;
     const uint4 * p = reinterpret_cast<const uint4 *>(s.xq + size_t(b) * 32);
@@ -291,6 +295,7 @@ __device__ __forceinline__ void load_xb(const Lds & s, int b, int nb, XB & x) {
     const uint32_t inf = s.info[b];
     x.dx40 = h2f(inf & 0xffffu) * 1099511627776.0f;  // * 2^40
     x.sum = int(int16_t(inf >> 16));
+    x.sx40 = TYPE == T_Q4_1 ? h2f(s.s1[b]) * 1099511627776.0f : 0.0f;
 }
 
 template <int TYPE>
@@ -327,9 +332,9 @@ __device__ __forceinline__ void load_xk(const Lds & s, int u, int nu, XK & x) {
 }
 
 // ---- weight loads and unit dots ----
-struct WB {  // one 32-block: Q4_0 uses lo (16 quant bytes), Q8_0 lo and hi (32 quant bytes)
+struct WB {  // one 32-block: Q4_0 / Q4_1 use lo (16 quant bytes), Q8_0 lo and hi (32 quant bytes)
     uint4 lo, hi;
-    uint32_t d;
+    uint32_t d;  // fp16 d (Q4_1: d | m << 16)
 };
 struct WK {  // one 64-weight K-quant unit
     uint4 a0, a1;         // Q6_K ql bytes / Q5_K qs bytes of the unit
@@ -343,17 +348,26 @@ __device__ __forceinline__ void load_wb(const WeightView & w, size_t idx, WB & o
     o.lo = *reinterpret_cast<const uint4 *>(w.a + idx * 16);
     if (TYPE == T_Q4_0) {
         o.d = *reinterpret_cast<const uint16_t *>(w.b + idx * 2);
+    } else if (TYPE == T_Q4_1) {
+        o.d = *reinterpret_cast<const uint32_t *>(w.b + idx * 4);
     } else {
         o.hi = *reinterpret_cast<const uint4 *>(w.b + idx * 16);
         o.d = *reinterpret_cast<const uint16_t *>(w.c + idx * 2);
     }
 }
 
-// Integer block sum (gemvq_ref.h:250-257): Q4_0 (nibble - 8) or Q8_0 weights times the Q8_0 activation block.
+// Integer block sum (gemvq_ref.h:250-257, 218-220): Q4_0 (nibble - 8), Q4_1 (nibble) or Q8_0 weights times the
+// Q8_0 / Q8_1 activation block.
 template <int TYPE>
 __device__ __forceinline__ int dot_block(const WB & w, const XB & x) {
     int s = 0;
-    if (TYPE == T_Q4_0) {
+    if (TYPE == T_Q4_1) {
+        const uint32_t q[4] = {w.lo.x, w.lo.y, w.lo.z, w.lo.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s = sdot4(q[i] & 0x0F0F0F0Fu, x.q[i], s);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s = sdot4((q[i] >> 4) & 0x0F0F0F0Fu, x.q[4 + i], s);
+    } else if (TYPE == T_Q4_0) {
         const uint32_t q[4] = {w.lo.x, w.lo.y, w.lo.z, w.lo.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) s = sdot4(q[i] & 0x0F0F0F0Fu, x.q[i], s);
@@ -370,9 +384,14 @@ __device__ __forceinline__ int dot_block(const WB & w, const XB & x) {
 
 // floor(sumi * dw * dx * 2^40) (gemvqw_engine.h:417-427) as an integer-valued double: dw * dx * 2^40 is exact in
 // FP32 (two 11-bit significands), its product with the 20-bit sumi exact in FP64, floor exact.
+template <int TYPE>
 __device__ __forceinline__ double block_term(int sumi, uint32_t dw, const XB & x) {
     const float s = float(__builtin_bit_cast(_Float16, uint16_t(dw))) * x.dx40;  // exact conversion
-    return floor(double(sumi) * double(s));
+    const double t = floor(double(sumi) * double(s));
+    if (TYPE != T_Q4_1) return t;
+    // Q4_1: + floor(m * s_x * 2^40), the product of two fp16 values exact in FP32
+    const float ms = float(__builtin_bit_cast(_Float16, uint16_t(dw >> 16))) * x.sx40;
+    return t + floor(double(ms));
 }
 
 template <int TYPE>
@@ -545,7 +564,7 @@ __device__ __forceinline__ long long row_blocks(const WB * wb, int r, int nb, co
     for (int k = 0; k < NU; ++k) {
         const int b = lane + 64 * k;
         const int si = dot_block<TYPE>(wb[k], xb[k]);
-        const double t = block_term(si, wb[k].d, xb[k]);
+        const double t = block_term<TYPE>(si, wb[k].d, xb[k]);
         acc += b < nb ? t : 0.0;
         if constexpr (DBG) {
             if (dbg && b < nb) dbg[size_t(r) * nb + b] = si;
@@ -678,7 +697,7 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
         for (int k = 0; k < NU; ++k) load_xk<TYPE>(s, c.lane + 64 * k, c.nu, xk[k]);
     } else {
 #pragma unroll
-        for (int k = 0; k < NU; ++k) load_xb(s, c.lane + 64 * k, c.nb, xb[k]);
+        for (int k = 0; k < NU; ++k) load_xb<TYPE>(s, c.lane + 64 * k, c.nb, xb[k]);
     }
     for (int mi = mi0; mi < a.n_members && t0 < t1; ++mi) {
         const GemvMember & m = a.m[mi];
@@ -754,6 +773,7 @@ hipError_t launch_gemv(const GemvArgs & a, int type, hipStream_t st) {
     if (a.cols <= 0 || a.cols > MAXK || a.total_tasks <= 0) return hipErrorInvalidValue;
     switch (type) {
     case T_Q4_0: return launch_nu<T_Q4_0>(a, st);
+    case T_Q4_1: return launch_nu<T_Q4_1>(a, st);
     case T_Q8_0: return launch_nu<T_Q8_0>(a, st);
     case T_Q5_K: return a.cols % 256 ? hipErrorInvalidValue : launch_nu<T_Q5_K>(a, st);
     case T_Q6_K: return a.cols % 256 ? hipErrorInvalidValue : launch_nu<T_Q6_K>(a, st);

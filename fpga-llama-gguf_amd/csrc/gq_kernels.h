@@ -6,11 +6,12 @@
 
 namespace gq {
 
-enum : int { T_Q4_0 = 2, T_Q8_0 = 8, T_Q5_K = 13, T_Q6_K = 14 };
+enum : int { T_Q4_0 = 2, T_Q4_1 = 3, T_Q8_0 = 8, T_Q5_K = 13, T_Q6_K = 14 };
 
 // Repacked weight layout (layout only, original bits): the GGUF block fields of all rows split into
 // field-major regions, each row-major, so that lane l of a wave reads unit l of a row from consecutive bytes.
 //   Q4_0: qs[rows][nb][16], d[rows][nb] (u16)
+//   Q4_1: qs[rows][nb][16], dm[rows][nb] (u32: d | m << 16)
 //   Q8_0: qs_lo[rows][nb][16] (bytes 0..15 of each block's quants), qs_hi[rows][nb][16], d[rows][nb]
 //   Q5_K: qs[rows][nsb][128], qh[rows][nsb][32], meta[rows][nsb][16] (d, dmin, 12 scale bytes)
 //   Q6_K: ql[rows][nsb][128], qh[rows][nsb][64], sc[rows][nsb][16], d[rows][nsb] (u16)
@@ -187,6 +188,7 @@ hipError_t launch_next_token(const NextTokenArgs & a, hipStream_t s);
 __host__ __device__ inline size_t gguf_row_bytes(int type, int cols) {
     switch (type) {
     case T_Q4_0: return size_t(cols / 32) * 18;
+    case T_Q4_1: return size_t(cols / 32) * 20;
     case T_Q8_0: return size_t(cols / 32) * 34;
     case T_Q5_K: return size_t(cols / 256) * 176;
     case T_Q6_K: return size_t(cols / 256) * 210;
@@ -197,7 +199,7 @@ __host__ __device__ inline size_t gguf_row_bytes(int type, int cols) {
 __host__ __device__ inline WeightView weight_view(const uint8_t * base, int type, int rows, int cols) {
     WeightView v;
     const size_t R = size_t(rows);
-    if (type == T_Q4_0) {
+    if (type == T_Q4_0 || type == T_Q4_1) {
         const size_t nb = size_t(cols / 32);
         v.a = base;
         v.b = base + R * nb * 16;

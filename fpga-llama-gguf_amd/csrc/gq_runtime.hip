@@ -95,7 +95,20 @@ float bits_f(uint32_t b) {
 // ---- layout-only repack (gq_kernels.h: the GGUF block fields split into field-major regions) ----
 void repack_rows(int type, int rows, int cols, const uint8_t * src, uint8_t * dst, bool inverse) {
     const size_t R = size_t(rows);
-    if (type == T_Q4_0 || type == T_Q8_0) {
+    if (type == T_Q4_1) {  // qs, then d | m << 16 per block
+        const size_t nb = size_t(cols / 32);
+        uint8_t * qa = dst, * dm = dst + R * nb * 16;
+        for (size_t i = 0; i < R * nb; ++i) {
+            uint8_t * blk = const_cast<uint8_t *>(src) + i * 20;
+            if (!inverse) {
+                std::memcpy(dm + 4 * i, blk, 4);
+                std::memcpy(qa + 16 * i, blk + 4, 16);
+            } else {
+                std::memcpy(blk, dm + 4 * i, 4);
+                std::memcpy(blk + 4, qa + 16 * i, 16);
+            }
+        }
+    } else if (type == T_Q4_0 || type == T_Q8_0) {
         const size_t nb = size_t(cols / 32), bb = type == T_Q4_0 ? 18 : 34;
         uint8_t * qa = dst;
         uint8_t * qb = dst + R * nb * 16;
@@ -147,7 +160,7 @@ void repack_rows(int type, int rows, int cols, const uint8_t * src, uint8_t * ds
     }
 }
 
-bool type_ok(int t) { return t == T_Q4_0 || t == T_Q8_0 || t == T_Q5_K || t == T_Q6_K; }
+bool type_ok(int t) { return t == T_Q4_0 || t == T_Q4_1 || t == T_Q8_0 || t == T_Q5_K || t == T_Q6_K; }
 
 bool shape_ok(int t, int rows, int cols) {
     if (rows <= 0 || cols <= 0 || cols > int(GEMVQ_MAX_COLS)) return false;

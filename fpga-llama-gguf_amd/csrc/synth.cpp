@@ -100,6 +100,26 @@ void q4_0_row(const float * x, int64_t cols, uint8_t * out) {
     }
 }
 
+// ggml quantize_row_q4_1_ref: d = (max - min) / 15, m = min, q = min(15, (int8)((x - min) / d + 0.5)).
+void q4_1_row(const float * x, int64_t cols, uint8_t * out) {
+    for (int64_t b = 0; b < cols / 32; ++b, x += 32, out += 20) {
+        float mn = 3.402823466e38f, mx = -3.402823466e38f;
+        for (int j = 0; j < 32; ++j) {
+            if (x[j] < mn) mn = x[j];
+            if (x[j] > mx) mx = x[j];
+        }
+        const float d = (mx - mn) / 15.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
+        put16(out, f2h(d));
+        put16(out + 2, f2h(mn));
+        for (int j = 0; j < 16; ++j) {
+            const float x0 = (x[j] - mn) * id, x1 = (x[16 + j] - mn) * id;
+            const uint8_t xi0 = uint8_t(std::min(15, int(int8_t(x0 + 0.5f))));
+            const uint8_t xi1 = uint8_t(std::min(15, int(int8_t(x1 + 0.5f))));
+            out[4 + j] = uint8_t(xi0 | (xi1 << 4));
+        }
+    }
+}
+
 // ggml quantize_row_q8_0_ref: d = amax / 127, q = roundf(x / d).
 void q8_0_row(const float * x, int64_t cols, uint8_t * out) {
     for (int64_t b = 0; b < cols / 32; ++b, x += 32, out += 34) {
@@ -390,6 +410,7 @@ void gqs_uniform(uint64_t seed, uint64_t stream, uint64_t first, size_t n, float
 size_t gqs_row_bytes(int type, int64_t cols) {
     switch (type) {
     case 2: return cols % 32 ? 0 : size_t(cols / 32) * 18;
+    case 3: return cols % 32 ? 0 : size_t(cols / 32) * 20;
     case 8: return cols % 32 ? 0 : size_t(cols / 32) * 34;
     case 13: return cols % 256 ? 0 : size_t(cols / 256) * 176;
     case 14: return cols % 256 ? 0 : size_t(cols / 256) * 210;
@@ -405,6 +426,7 @@ size_t gqs_quantize(int type, const float * x, int64_t rows, int64_t cols, uint8
         uint8_t * o = out + size_t(r) * rb;
         switch (type) {
         case 2: q4_0_row(xr, cols, o); break;
+        case 3: q4_1_row(xr, cols, o); break;
         case 8: q8_0_row(xr, cols, o); break;
         case 13: q5_K_row(xr, cols, o); break;
         case 14: q6_K_row(xr, cols, o); break;

@@ -18,7 +18,7 @@ HIP_LIB_PATH = os.path.join(PKG, "libgemvq_hip.so")
 SYNTH_LIB_PATH = os.path.join(PKG, "libgemvq_synth.so")
 
 # ggml type ids
-Q4_0, Q8_0, Q5_K, Q6_K = 2, 8, 13, 14
+Q4_0, Q4_1, Q8_0, Q5_K, Q6_K = 2, 3, 8, 13, 14
 # opcodes (gemvqc16.h:100-111 plus the opcodes of this backend)
 OP_GEMV, OP_RMSNORM, OP_ADD, OP_SILU_MUL, OP_MUL, OP_UNARY, OP_GDN, OP_CONV, OP_STATE_LOAD, OP_ROPE, OP_TRACE = range(1, 12)
 OP_ATTN, OP_GET_ROWS, OP_ARGMAX, OP_NEXT_TOKEN, OP_FILL = 12, 13, 14, 15, 16
@@ -36,7 +36,8 @@ def fbits(x: float) -> int:
 
 
 def row_bytes(t: int, cols: int) -> int:
-    return {Q4_0: cols // 32 * 18, Q8_0: cols // 32 * 34, Q5_K: cols // 256 * 176, Q6_K: cols // 256 * 210}[t]
+    return {Q4_0: cols // 32 * 18, Q4_1: cols // 32 * 20, Q8_0: cols // 32 * 34, Q5_K: cols // 256 * 176,
+            Q6_K: cols // 256 * 210}[t]
 
 
 # ---------------------------------------------------------------------------------------------------------------

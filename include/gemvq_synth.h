@@ -16,8 +16,8 @@ uint64_t gqs_u64(uint64_t seed, uint64_t stream, uint64_t i);
 void gqs_normal(uint64_t seed, uint64_t stream, uint64_t first, size_t n, float mean, float stddev, float * out);
 void gqs_uniform(uint64_t seed, uint64_t stream, uint64_t first, size_t n, float lo, float hi, float * out);
 
-/* ggml quantize_row_{q4_0,q8_0,q5_K,q6_K}_ref on `rows` rows of `cols` floats (GGUF block bytes out). type is the
- * ggml type id (2, 8, 13, 14). Returns the bytes written, 0 for an unsupported type or shape. */
+/* ggml quantize_row_{q4_0,q4_1,q8_0,q5_K,q6_K}_ref on `rows` rows of `cols` floats (GGUF block bytes out). type is
+ * the ggml type id (2, 3, 8, 13, 14). Returns the bytes written, 0 for an unsupported type or shape. */
 size_t gqs_quantize(int type, const float * x, int64_t rows, int64_t cols, uint8_t * out);
 size_t gqs_row_bytes(int type, int64_t cols);
 

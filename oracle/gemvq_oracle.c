@@ -177,6 +177,23 @@ void orc_quantize_q8_0(const float * x, int n, int8_t * q, uint16_t * d_bits) {
     }
 }
 
+/* Q8_1 (gemvq_ref.h:201-212, ggml quantize_row_q8_1_ref): d = amax / 127, q = roundf(x / d), d_bits = fp16(d),
+ * s_bits = fp16(sum(q) * d) with the FP32 d. */
+void orc_quantize_q8_1(const float * x, int n, int8_t * q, uint16_t * d_bits, uint16_t * s_bits) {
+    for (int b = 0; b < n / 32; ++b) {
+        float amax = 0.0f;
+        for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(x[b * 32 + j]));
+        const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
+        int sum = 0;
+        for (int j = 0; j < 32; ++j) {
+            q[b * 32 + j] = (int8_t)roundf(x[b * 32 + j] * id);
+            sum += q[b * 32 + j];
+        }
+        d_bits[b] = orc_float_to_half(d);
+        s_bits[b] = orc_float_to_half((float)sum * d);
+    }
+}
+
 /* Q8_K: gemvq_ref.h:62-81 (ggml quantize_row_q8_K_ref), plus ggml's bsums (sum of each 16 quants). */
 void orc_quantize_q8_K(const float * x, int n, int8_t * q, float * d, int16_t * bsums) {
     for (int b = 0; b < n / 256; ++b) {
@@ -438,7 +455,27 @@ void orc_fx_gemv_q(int fmt, const uint8_t * w, const int8_t * xq, const uint16_t
     for (int r = 0; r < rows; ++r) {
         const uint8_t * row = w + (size_t)r * rb;
         __int128 acc = 0;
-        if (fmt == ORC_Q4_0 || fmt == ORC_Q8_0) {
+        if (fmt == ORC_Q4_1) {
+            /* Q4_1 x Q8_1 (gemvq_ref.h:194-229): term = floor(sumi * d_w * d_x * 2^40) + floor(m_w * s_x * 2^40), both
+             * products of fp16 values exact; xbsums carries the fp16 bits of each block's s_x. */
+            const int nb = cols / 32;
+            const uint16_t * xs16 = (const uint16_t *)xbsums;
+            for (int b = 0; b < nb; ++b) {
+                const uint8_t * blk = row + (size_t)b * 20;
+                int sumi = 0;
+                for (int j = 0; j < 16; ++j)
+                    sumi += (blk[4 + j] & 15) * xq[b * 32 + j] + (blk[4 + j] >> 4) * xq[b * 32 + j + 16];
+                if (blocksums) blocksums[(size_t)r * nb + b] = sumi;
+                const orc_parts pw = half_parts(rd16(blk)), pm = half_parts(rd16(blk + 2));
+                const orc_parts px = half_parts(xd16[b]), ps = half_parts(xs16[b]);
+                __int128 p1 = (__int128)sumi * (pw.m * px.m);
+                if (pw.neg != px.neg) p1 = -p1;
+                acc += fixed_of(p1, pw.e + px.e);
+                __int128 p2 = (__int128)(pm.m * ps.m);
+                if (pm.neg != ps.neg) p2 = -p2;
+                acc += fixed_of(p2, pm.e + ps.e);
+            }
+        } else if (fmt == ORC_Q4_0 || fmt == ORC_Q8_0) {
             const int nb = cols / 32, bb = fmt == ORC_Q4_0 ? 18 : 34;
             for (int b = 0; b < nb; ++b) {
                 const uint8_t * blk = row + (size_t)b * bb;
@@ -519,6 +556,12 @@ void orc_fx_gemv(int fmt, const uint8_t * w, const float * x, int rows, int cols
         orc_quantize_q8_K(x, cols, q, d, bs);
         orc_fx_gemv_q(fmt, w, q, NULL, d, bs, rows, cols, y, blocksums, acc);
         free(d); free(bs);
+    } else if (fmt == ORC_Q4_1) {
+        uint16_t * dh = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)(cols / 32));
+        uint16_t * sh = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)(cols / 32));
+        orc_quantize_q8_1(x, cols, q, dh, sh);
+        orc_fx_gemv_q(fmt, w, q, dh, NULL, (const int16_t *)sh, rows, cols, y, blocksums, acc);
+        free(dh); free(sh);
     } else {
         uint16_t * dh = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)(cols / 32));
         orc_quantize_q8_0(x, cols, q, dh);

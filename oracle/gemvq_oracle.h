@@ -42,6 +42,8 @@ size_t orc_row_bytes(int fmt, int cols);
 /* ---- activation quantizers (gemvq_ref.h:62-81, 236-245) ---- */
 /* Q8_0: per 32 values d_bits = fp16(amax / 127), q = roundf(x * (1 / (amax / 127))). */
 void orc_quantize_q8_0(const float * x, int n, int8_t * q, uint16_t * d_bits);
+/* Q8_1 (for Q4_1 weights): Q8_0's quants, d_bits = fp16(amax / 127), s_bits = fp16(sum(q) * (amax / 127)). */
+void orc_quantize_q8_1(const float * x, int n, int8_t * q, uint16_t * d_bits, uint16_t * s_bits);
 /* Q8_K: per 256 values iscale = -127 / max (signed value of largest magnitude, first on ties), q = min(127,
  * nearest_int(iscale * x)), d = 1 / iscale; bsums per 16 values. */
 void orc_quantize_q8_K(const float * x, int n, int8_t * q, float * d, int16_t * bsums);
@@ -51,12 +53,14 @@ void orc_ref_gemv(int fmt, const uint8_t * w, const float * x, int rows, int col
 int orc_ref_within_tolerance(float got, float ref, double mag);
 
 /* ---- GEMV, canonical fixed-point path ----
- * y[r] = fp32(sum_b floor(term_b * 2^40)) * 2^-40. blocksums (optional): per row the integer block sums, Q4_0/Q8_0
- * one int32 per 32-block (sum_j w_j * q8_j with the Q4_0 weights minus 8), Q5_K/Q6_K two int32 per super-block
+ * y[r] = fp32(sum_b floor(term_b * 2^40)) * 2^-40. blocksums (optional): per row the integer block sums, Q4_0/Q4_1/
+ * Q8_0 one int32 per 32-block (sum_j w_j * q8_j with the Q4_0 weights minus 8; Q4_1 (this build's extension of the
+ * kernel arithmetic, which has no Q4_1): term = floor(sumi d_w d_x 2^40) + floor(m_w s_x 2^40)), Q5_K/Q6_K two int32 per super-block
  * (S = sum sc * (q . q8), M = sum m * bsum, M = 0 for Q6_K). acc (optional): the int64 fixed-point row sums. */
 void orc_fx_gemv(int fmt, const uint8_t * w, const float * x, int rows, int cols, float * y, int32_t * blocksums,
                  int64_t * acc);
-/* Same on an already quantized x (Q8_0: q + fp16 scale bits; Q8_K: q + FP32 d + bsums). */
+/* Same on an already quantized x (Q8_0: q + fp16 scale bits; Q8_1: q + fp16 d bits + the fp16 s bits passed as
+ * xbsums; Q8_K: q + FP32 d + bsums). */
 void orc_fx_gemv_q(int fmt, const uint8_t * w, const int8_t * xq, const uint16_t * xd16, const float * xd32,
                    const int16_t * xbsums, int rows, int cols, float * y, int32_t * blocksums, int64_t * acc);
 float orc_fixed_to_float(int64_t acc);

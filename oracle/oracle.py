@@ -14,7 +14,7 @@ ORC_PATH = os.path.join(HERE, "liborc_gemvq.so")
 REF_PATH = os.path.join(HERE, "_ref", "libgemvq_ref.so")
 REF_SRC = "/root/reference/fpga/src"
 
-Q4_0, Q8_0, Q5_K, Q6_K = 2, 8, 13, 14
+Q4_0, Q4_1, Q8_0, Q5_K, Q6_K = 2, 3, 8, 13, 14
 F = np.float32
 
 
@@ -57,6 +57,7 @@ def orc() -> C.CDLL:
         _fn(lib, "orc_row_bytes", C.c_size_t, i, i)
         _fn(lib, "orc_quantize_q8_0", None, vp, i, vp, vp)
         _fn(lib, "orc_quantize_q8_K", None, vp, i, vp, vp, vp)
+        _fn(lib, "orc_quantize_q8_1", None, vp, i, vp, vp, vp)
         _fn(lib, "orc_ref_gemv", None, i, vp, vp, i, i, vp, vp)
         _fn(lib, "orc_ref_within_tolerance", i, fl, fl, C.c_double)
         _fn(lib, "orc_fx_gemv", None, i, vp, vp, i, i, vp, vp, vp)
@@ -125,6 +126,15 @@ def quantize_q8_0(x: np.ndarray):
     d = np.empty(x.size // 32, np.uint16)
     orc().orc_quantize_q8_0(_p(x), x.size, _p(q), _p(d))
     return q, d
+
+
+def quantize_q8_1(x: np.ndarray):
+    x = np.ascontiguousarray(x, F)
+    q = np.empty(x.size, np.int8)
+    d = np.empty(x.size // 32, np.uint16)
+    s_ = np.empty(x.size // 32, np.uint16)
+    orc().orc_quantize_q8_1(_p(x), x.size, _p(q), _p(d), _p(s_))
+    return q, d, s_
 
 
 def quantize_q8_K(x: np.ndarray):

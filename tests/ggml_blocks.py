@@ -8,9 +8,9 @@ from __future__ import annotations
 
 import numpy as np
 
-Q4_0, Q8_0, Q5_K, Q6_K = 2, 8, 13, 14
-BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q5_K: 176, Q6_K: 210}
-BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q5_K: 256, Q6_K: 256}
+Q4_0, Q4_1, Q8_0, Q5_K, Q6_K = 2, 3, 8, 13, 14
+BLOCK_BYTES = {Q4_0: 18, Q4_1: 20, Q8_0: 34, Q5_K: 176, Q6_K: 210}
+BLOCK_ELEMS = {Q4_0: 32, Q4_1: 32, Q8_0: 32, Q5_K: 256, Q6_K: 256}
 
 
 def half(bits) -> np.ndarray:
@@ -29,6 +29,17 @@ def q4_0(w, rows, cols):
     qs = b[..., 2:18].astype(np.int32)
     q = np.concatenate([(qs & 15) - 8, (qs >> 4) - 8], axis=-1)
     return q.reshape(rows, cols), d
+
+
+def q4_1(w, rows, cols):
+    """-> (ints [rows, cols] in 0..15, d [rows, nb], m [rows, nb] float64). Block: d, m (fp16), 16 bytes of nibbles;
+    value = d * q + m."""
+    b = blocks(Q4_1, w, rows, cols)
+    d = half(b[..., 0:2].copy().view(np.uint16)[..., 0])
+    m = half(b[..., 2:4].copy().view(np.uint16)[..., 0])
+    qs = b[..., 4:20].astype(np.int32)
+    q = np.concatenate([qs & 15, qs >> 4], axis=-1)
+    return q.reshape(rows, cols), d, m
 
 
 def q8_0(w, rows, cols):
@@ -124,6 +135,17 @@ def quantize_q8_0(x: np.ndarray):
     return q.astype(np.int8).ravel(), d
 
 
+def quantize_q8_1(x: np.ndarray):
+    """Q8_0's quants and d, plus s = fp16(sum(q) * d) with the FP32 d (ggml quantize_row_q8_1_ref)."""
+    q, dbits = quantize_q8_0(x)
+    xr = np.asarray(x, np.float32).reshape(-1, 32)
+    d = (np.max(np.abs(xr), axis=1) / np.float32(127)).astype(np.float32)
+    sums = q.astype(np.int32).reshape(-1, 32).sum(axis=1).astype(np.float32)
+    with np.errstate(over="ignore"):
+        sbits = (sums * d).astype(np.float32).astype(np.float16).view(np.uint16)
+    return q, dbits, sbits
+
+
 def nearest_int(v: np.ndarray) -> np.ndarray:
     """Round half to even (the FP32 magic-number trick evaluates exactly this for |v| < 2^22)."""
     return np.rint(np.asarray(v, np.float64)).astype(np.int32)
@@ -152,6 +174,9 @@ def block_sums(t: int, w, xq: np.ndarray, rows: int, cols: int, xbs: np.ndarray 
     """Exact integer block sums in the oracle's debug layout: Q4_0/Q8_0 one per 32-block; K-quants (S, M) per
     super-block with S = sum over groups of scale * (q . q8) and M = sum over sub-blocks of min * bsum (Q6_K: 0)."""
     xq = np.asarray(xq, np.int64)
+    if t == Q4_1:
+        q = q4_1(w, rows, cols)[0]
+        return (q.astype(np.int64) * xq[None, :]).reshape(rows, -1, 32).sum(axis=2).ravel()
     if t in (Q4_0, Q8_0):
         q, _ = (q4_0 if t == Q4_0 else q8_0)(w, rows, cols)
         return (q.astype(np.int64) * xq[None, :]).reshape(rows, -1, 32).sum(axis=2).ravel()

@@ -37,6 +37,7 @@ def run_gemv(gq, t, rows, cols, w, x, blocksums=False):
 
 @pytest.mark.parametrize("t,rows,cols", [
     (2, 64, 256), (2, 100, 2560), (2, 33, 4096), (2, 64, 12288), (2, 16, 16384), (2, 17, 9728),
+    (3, 64, 256), (3, 100, 4096), (3, 17, 12288),
     (8, 64, 256), (8, 100, 2560), (8, 40, 9728), (8, 31, 4096),
     (13, 64, 256), (13, 50, 4096), (13, 20, 12288),
     (14, 64, 256), (14, 50, 4096), (14, 20, 12288), (14, 7, 16384),
@@ -87,7 +88,7 @@ def test_gemv_edge_inputs(gq, orc):
     assert_bits(y8, orc.fx_gemv(gq.Q8_0, w8, x, rows, cols), "negative scales")
 
 
-@pytest.mark.parametrize("t", [2, 8, 13, 14])
+@pytest.mark.parametrize("t", [2, 3, 8, 13, 14])
 def test_gemv_against_reference_vectors(gq, t):
     """The GPU GEMV on the stored inputs against the reference's own CPU results (tests/golden), within the
     reference tolerance |got - ref| <= 1e-6 + 1e-5 |ref| + 1e-6 sum |block terms| (gemvq_ref.h:267-272)."""

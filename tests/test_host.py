@@ -47,7 +47,7 @@ def test_every_declared_symbol_is_exported(libs):
     assert total >= 40
 
 
-@pytest.mark.parametrize("t", [B.Q4_0, B.Q8_0, B.Q5_K, B.Q6_K])
+@pytest.mark.parametrize("t", [B.Q4_0, B.Q4_1, B.Q8_0, B.Q5_K, B.Q6_K])
 def test_repack_round_trip(gq, libs, t):
     rows, cols = 37, 2048
     rng = np.random.default_rng(t)
@@ -61,7 +61,7 @@ def test_repack_round_trip(gq, libs, t):
 def test_repack_rejects_bad_shapes(gq, libs):
     lib = gq.hip_lib()
     buf = np.zeros(1 << 16, np.uint8)
-    for t, rows, cols in [(3, 4, 256), (2, 4, 48), (13, 4, 128), (2, 0, 256), (8, 4, 32768)]:
+    for t, rows, cols in [(1, 4, 256), (6, 4, 256), (2, 4, 48), (3, 4, 40), (13, 4, 128), (2, 0, 256), (8, 4, 32768)]:
         assert lib.gemvq_repack(t, rows, cols, buf.ctypes.data, buf.ctypes.data) == gq.EINVAL, (t, rows, cols)
 
 
@@ -128,10 +128,26 @@ def q4_0_ggml(x: np.ndarray) -> np.ndarray:
     return out.ravel()
 
 
+def q4_1_ggml(x: np.ndarray) -> np.ndarray:
+    """ggml quantize_row_q4_1_ref: d = (max - min) / 15, m = min, q = min(15, (int8)((x - min) / d + 0.5))."""
+    x = x.astype(np.float32).reshape(-1, 32)
+    out = np.zeros((x.shape[0], 20), np.uint8)
+    for b, row in enumerate(x):
+        mn, mx = row.min(), row.max()
+        d = np.float32((mx - mn) / np.float32(15))
+        idv = np.float32(1) / d if d != 0 else np.float32(0)
+        q = np.minimum(15, np.trunc(((row - mn) * idv).astype(np.float32) + np.float32(0.5))).astype(np.uint8)
+        out[b, 0:2] = np.array([d], np.float16).view(np.uint8)
+        out[b, 2:4] = np.array([mn], np.float16).view(np.uint8)
+        out[b, 4:] = q[:16] | (q[16:] << 4)
+    return out.ravel()
+
+
 def test_weight_quantizers_closed_form(gq, libs):
     x = gq.normal(5, 1, 64 * 256, std=0.02)
     x[:32] = 0.0
     assert np.array_equal(gq.quantize(B.Q4_0, x, 64, 256), q4_0_ggml(x))
+    assert np.array_equal(gq.quantize(B.Q4_1, x, 64, 256), q4_1_ggml(x))
     # Q8_0 weights use the activation quantizer's closed form
     q, d = B.quantize_q8_0(x)
     blk = np.concatenate([d.view(np.uint8).reshape(-1, 2), q.view(np.uint8).reshape(-1, 32)], axis=1).ravel()

@@ -18,7 +18,7 @@ import pytest
 import ggml_blocks as B
 from golden_data import golden
 
-FORMATS = [(B.Q4_0, 32), (B.Q8_0, 32), (B.Q5_K, 256), (B.Q6_K, 256)]
+FORMATS = [(B.Q4_0, 32), (B.Q4_1, 32), (B.Q8_0, 32), (B.Q5_K, 256), (B.Q6_K, 256)]
 
 
 # ---------------------------------------------------------------------------------------------------------------
@@ -63,7 +63,10 @@ def random_blocks(t: int, rows: int, cols: int, seed: int) -> np.ndarray:
     nb = rows * cols // B.BLOCK_ELEMS[t]
     blk = rng.integers(0, 256, (nb, B.BLOCK_BYTES[t]), dtype=np.uint8)
     halves = lambda lo, hi: rng.uniform(lo, hi, nb).astype(np.float16).view(np.uint8).reshape(nb, 2)  # noqa: E731
-    if t in (B.Q4_0, B.Q8_0):
+    if t == B.Q4_1:
+        blk[:, 0:2] = halves(0.0, 0.005)
+        blk[:, 2:4] = halves(-0.04, 0.0)
+    elif t in (B.Q4_0, B.Q8_0):
         blk[:, 0:2] = halves(-0.01, 0.01)
     elif t == B.Q5_K:
         blk[:, 0:2] = halves(-0.002, 0.002)
@@ -98,6 +101,24 @@ def canonical_rows(t: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int):
         return Fraction(v)
 
     TWO40 = 1 << 40
+    if t == B.Q4_1:  # floor(sumi d_w d_x 2^40) + floor(m_w s_x 2^40) per block
+        xq, xd, xs = B.quantize_q8_1(x)
+        sums = B.block_sums(t, w, xq, rows, cols).reshape(rows, -1)
+        blk = B.blocks(t, w, rows, cols)
+        dw = blk[..., 0:2].copy().view(np.float16)[..., 0]
+        mw = blk[..., 2:4].copy().view(np.float16)[..., 0]
+        dx, sx = xd.view(np.float16), xs.view(np.float16)
+        out, f64 = [], []
+        for r in range(rows):
+            acc, v = 0, 0.0
+            for b in range(sums.shape[1]):
+                t1 = sums[r, b] * frac(dw[r, b]) * frac(dx[b])
+                t2 = frac(mw[r, b]) * frac(sx[b])
+                acc += (t1 * TWO40).__floor__() + (t2 * TWO40).__floor__()
+                v += float(t1 + t2)
+            out.append(f32_round(acc) / TWO40)
+            f64.append(v)
+        return np.array(out, np.float32), np.array(f64), sums.ravel()
     if t in (B.Q4_0, B.Q8_0):
         xq, xd = B.quantize_q8_0(x)
         sums = B.block_sums(t, w, xq, rows, cols).reshape(rows, -1)
@@ -146,6 +167,18 @@ def test_fx_gemv_exact_closed_form(orc, gq, t, blk, source):
     assert np.array_equal(bs.astype(np.int64), want_bs.astype(np.int64)), "block sums"
     assert np.array_equal(y.view(np.uint32), want_y.view(np.uint32)), "fixed-point row values"
     assert np.all(np.abs(y - f64) <= 1e-6 + 1e-5 * np.abs(f64))
+    # the reference's sequential FP32 path within its own tolerance of the canonical result
+    yr, mag = orc.ref_gemv(t, w, x, rows, cols)
+    assert all(orc.orc().orc_ref_within_tolerance(float(a), float(b), float(m)) for a, b, m in zip(y, yr, mag))
+
+
+def test_q8_1_closed_form(orc, gq):
+    x = gq.normal(0, 3, 2048)
+    x[:32] = 0.0
+    q, d, s_ = orc.quantize_q8_1(x)
+    qw, dw, sw = B.quantize_q8_1(x)
+    assert np.array_equal(q, qw) and np.array_equal(d, dw) and np.array_equal(s_, sw)
+    assert d[0] == 0 and s_[0] == 0
 
 
 def q6_K_unit_block(idx: int, qv: int) -> np.ndarray:
@@ -212,11 +245,10 @@ def test_ref_gemv_reproduces_reference_vectors(orc, t):
     y, mag = orc.ref_gemv(t, w, x, 16, 512)
     assert np.array_equal(y.view(np.uint32), g[f"gemv{t}_y"].view(np.uint32))
     assert np.array_equal(mag, g[f"gemv{t}_mag"])
-    if t != 3:  # the canonical path (no Q4_1 kernel) within the reference tolerance of the reference result
-        yf = orc.fx_gemv(t, w, x, 16, 512)
-        o = orc.orc()
-        assert all(o.orc_ref_within_tolerance(float(a), float(b), float(m))
-                   for a, b, m in zip(yf, g[f"gemv{t}_y"], g[f"gemv{t}_mag"]))
+    yf = orc.fx_gemv(t, w, x, 16, 512)  # the canonical path within the reference tolerance of the reference
+    o = orc.orc()
+    assert all(o.orc_ref_within_tolerance(float(a), float(b), float(m))
+               for a, b, m in zip(yf, g[f"gemv{t}_y"], g[f"gemv{t}_mag"]))
 
 
 @pytest.mark.parametrize("t,blk", FORMATS)
