@@ -1,6 +1,7 @@
 """Builds the native libraries of the package in-tree (no CMake, no JIT cache).
 
-libgemvq_hip.so    the gfx950 kernels, the command processor and the C ABI of include/gemvq_hip.h (hipcc)
+libgemvq_hip.so    the gfx950 kernels, the command processor, the C ABI of include/gemvq_hip.h and the GGUF reader
+                   of include/gemvq_gguf.h (hipcc)
 libgemvq_synth.so  the host-only synthetic data generator of include/gemvq_synth.h (g++)
 """
 from __future__ import annotations
@@ -19,7 +20,7 @@ BUILD = os.path.join(PKG, "_build")
 HIP_LIB = os.path.join(PKG, "libgemvq_hip.so")
 SYNTH_LIB = os.path.join(PKG, "libgemvq_synth.so")
 
-HIP_SOURCES = ["gq_gemv.hip", "gq_ops.hip", "gq_runtime.hip", "qwen35.cpp"]
+HIP_SOURCES = ["gq_gemv.hip", "gq_ops.hip", "gq_runtime.hip", "qwen35.cpp", "gguf.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -ffp-contract=off: no multiply-add is fused unless written as fmaf (results are reproduced bit for bit on the CPU);
 # packed FP32 instructions are disabled (they are avoided on this hardware).

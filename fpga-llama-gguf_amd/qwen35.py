@@ -74,8 +74,9 @@ def config_c(cfg: Config) -> ConfigC:
     return ConfigC(*[getattr(cfg, f[0]) for f in ConfigC._fields_])
 
 
-def tensor_specs(cfg: Config) -> list[tuple[str, int, int, int, str]]:
-    """(name, type, ne0 = cols, ne1 = rows, init) for every tensor; init is 'w', 'ones', 'zeros', 'neg1', 'conv'."""
+def tensor_specs(cfg: Config, types: dict[str, int] | None = None) -> list[tuple[str, int, int, int, str]]:
+    """(name, type, ne0 = cols, ne1 = rows, init) for every tensor; init is 'w', 'ones', 'zeros', 'neg1', 'conv'.
+    `types` overrides the ggml type of named matrices (a real "Q4_0" Qwen3.5 file holds some Q4_1 ffn_down)."""
     E, S = cfg.n_embd, cfg.ssm_head_dim
     specs = [("token_embd.weight", cfg.etype, E, cfg.n_vocab, "w")]
     for il in range(cfg.n_layer):
@@ -105,6 +106,11 @@ def tensor_specs(cfg: Config) -> list[tuple[str, int, int, int, str]]:
                   (p + "ffn_up.weight", cfg.wtype, E, cfg.n_ff, "w"),
                   (p + "ffn_down.weight", cfg.wtype, cfg.n_ff, E, "w")]
     specs += [("output_norm.weight", F32, E, 1, "ones"), ("output.weight", cfg.etype, E, cfg.n_vocab, "w")]
+    if types:
+        unknown = set(types) - {n for n, t, *_ in specs if t != F32}
+        if unknown:
+            raise KeyError(f"type overrides for tensors that are not matrices: {sorted(unknown)}")
+        specs = [(n, types.get(n, t), a, b, i) for n, t, a, b, i in specs]
     return specs
 
 
@@ -124,6 +130,7 @@ class Blob:
     table: C.Array
     data: np.ndarray
     n: int
+    owner: object = None  # what keeps `data` alive (the GGUF mapping of a model read from a file)
 
     def tensor(self, name: str) -> np.ndarray:
         for d in self.table:
@@ -132,9 +139,9 @@ class Blob:
         raise KeyError(name)
 
 
-def generate(cfg: Config, seed: int = 0, threads: int = 0) -> Blob:
+def generate(cfg: Config, seed: int = 0, threads: int = 0, types: dict[str, int] | None = None) -> Blob:
     """All tensors of the model from `seed`: tensor i uses RNG stream 1000 + i."""
-    specs = tensor_specs(cfg)
+    specs = tensor_specs(cfg, types)
     table = (TensorDesc * len(specs))()
     off = 0
     for i, (name, t, ne0, ne1, _) in enumerate(specs):

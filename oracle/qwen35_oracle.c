@@ -147,6 +147,10 @@ static void gemv(orc_model * m, const orc_t * w, const float * x, float * y) {
         d32 = (float *)malloc(sizeof(float) * (size_t)(cols / 256));
         bs = (int16_t *)malloc(sizeof(int16_t) * (size_t)(cols / 16));
         orc_quantize_q8_K(x, cols, q, d32, bs);
+    } else if (fmt == ORC_Q4_1) { /* Q8_1: the fp16 s bits travel in bs */
+        d16 = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)(cols / 32));
+        bs = (int16_t *)malloc(sizeof(int16_t) * (size_t)(cols / 32));
+        orc_quantize_q8_1(x, cols, q, d16, (uint16_t *)bs);
     } else {
         d16 = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)(cols / 32));
         orc_quantize_q8_0(x, cols, q, d16);

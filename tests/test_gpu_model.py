@@ -64,3 +64,33 @@ def test_full_width_model_greedy_matches_oracle(gq, orc, q35):
         om2.decode(int(want[pos]), pos, lo if pos == len(prompt) - 2 + n_gen else None)
     assert np.array_equal(lg.view(np.uint32), lo.view(np.uint32))
     assert np.array_equal(hd.view(np.uint32), om2.hidden().view(np.uint32))
+
+
+def test_model_from_gguf_file_matches_oracle(gq, orc, q35, tmp_path):
+    """A model written to a GGUF file, with Q4_1 ffn_down in two layers (the type mix of real Qwen3.5 Q4_0 files),
+    read back through the GGUF reader and decoded from the file's mapping: tokens and logits identical to the oracle
+    decoder on the in-memory tensors."""
+    import gguf
+
+    cfg = q35.tiny(n_layer=8)
+    types = {f"blk.{il}.ffn_down.weight": gq.Q4_1 for il in (1, 3)}
+    blob = q35.generate(cfg, seed=4, types=types)
+    path = str(tmp_path / "model.gguf")
+    gguf.write_model(path, blob)
+    fb = gguf.open_model(path, n_ctx=cfg.n_ctx)
+    prompt = q35.prompt_ids(cfg, 6, seed=4)
+    n_gen = 16
+    om = orc.Model(q35.config_c(cfg), blob.table, blob.n, blob.data)
+    want = om.generate(prompt, n_gen)
+    try:
+        with q35.Model(fb) as m:
+            got = m.generate(prompt, n_gen)
+            lg = m.logits()
+    finally:
+        fb.owner.close()
+    assert np.array_equal(got, want), f"first mismatch at {np.nonzero(got != want)[0][:3]}"
+    lo = np.empty(cfg.n_vocab, np.float32)
+    om2 = orc.Model(q35.config_c(cfg), blob.table, blob.n, blob.data)
+    for pos in range(len(prompt) - 1 + n_gen):
+        om2.decode(int(want[pos]), pos, lo if pos == len(prompt) - 2 + n_gen else None)
+    assert np.array_equal(lg.view(np.uint32), lo.view(np.uint32))

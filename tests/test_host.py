@@ -23,7 +23,7 @@ def libs(gq):
 
         build.build()
     return {"gemvq_hip.h": C.CDLL(gq.HIP_LIB_PATH), "gemvq_qwen35.h": C.CDLL(gq.HIP_LIB_PATH),
-            "gemvq_synth.h": C.CDLL(gq.SYNTH_LIB_PATH)}
+            "gemvq_gguf.h": C.CDLL(gq.HIP_LIB_PATH), "gemvq_synth.h": C.CDLL(gq.SYNTH_LIB_PATH)}
 
 
 def declared_functions(header: str) -> list[str]:
