@@ -162,6 +162,41 @@ __device__ __forceinline__ long long wave_sum_i64(long long v) {
     return (readlane_i64(v, 0) + readlane_i64(v, 16)) + (readlane_i64(v, 32) + readlane_i64(v, 48));
 }
 
+__device__ __forceinline__ long long shfl_xor_i64(long long v, int m) {
+    const int lo = __shfl_xor(int(uint32_t(uint64_t(v))), m, WAVE);
+    const int hi = __shfl_xor(int(uint64_t(v) >> 32), m, WAVE);
+    return (long long)((uint64_t(uint32_t(hi)) << 32) | uint32_t(lo));
+}
+
+// Exact int64 totals of G rows (G = 1, 2 or 4) held as per-lane partials p[0..G-1]: afterwards every lane of lane
+// group g (64 / G consecutive lanes) holds the total of row g. The halving exchanges give each half of the wave half
+// of the rows, so the cross-lane steps are shared by the rows instead of repeated for each.
+template <int G>
+__device__ __forceinline__ long long reduce_rows(const long long * p) {
+    const int lane = threadIdx.x & 63;
+    long long v;
+    if constexpr (G == 4) {
+        const bool up = lane & 32;
+        const long long k0 = up ? p[2] : p[0], k1 = up ? p[3] : p[1];
+        const long long g0 = up ? p[0] : p[2], g1 = up ? p[1] : p[3];
+        const long long a0 = k0 + shfl_xor_i64(g0, 32), a1 = k1 + shfl_xor_i64(g1, 32);
+        const bool up16 = lane & 16;
+        v = (up16 ? a1 : a0) + shfl_xor_i64(up16 ? a0 : a1, 16);
+    } else if constexpr (G == 2) {
+        const bool up = lane & 32;
+        v = (up ? p[1] : p[0]) + shfl_xor_i64(up ? p[0] : p[1], 32);
+        v += shfl_xor_i64(v, 16);
+    } else {
+        v = p[0] + shfl_xor_i64(p[0], 32);
+        v += shfl_xor_i64(v, 16);
+    }
+    v += dpp_i64<DPP_XOR1>(v);
+    v += dpp_i64<DPP_XOR2>(v);
+    v += dpp_i64<DPP_HALF_MIRROR>(v);
+    v += dpp_i64<DPP_MIRROR>(v);
+    return v;
+}
+
 __device__ __forceinline__ int sum_lanes4_i32(int v) {
     v += dpp_i32<DPP_XOR1>(v);
     v += dpp_i32<DPP_XOR2>(v);

@@ -63,14 +63,22 @@ __device__ float block_norm_scale(const float * x, int n, float eps, int l2, Lds
     return l2 ? 1.0f / fmaxf(sqrtf(sum), eps) : 1.0f / sqrtf(sum / float(n) + eps);
 }
 
-// Q8_0 of the activation (gemvq_ref.h:236-245), one thread per 32-block, rounds of 256 blocks. With a deferred
-// norm the blocks stay in registers while the sum of squares is reduced: tree over the block's 32 squares, pairwise
-// over the 64 blocks of a wave, the 4 waves of a round, and the rounds (at most 2 here: n <= 16384), which is the
-// canonical pairwise tree over all n elements; then v = (x * scale) * w is quantized.
-__device__ __forceinline__ void load_block(const float * p, float * v) {
+// Q8_0 of the activation (gemvq_ref.h:236-245) on half-blocks: thread t holds items t + 256 g (an item is 16
+// consecutive floats; the two halves of a 32-block sit in adjacent lanes). The loads are issued by prologue_fetch
+// before the first weight rows are requested, so they are not queued behind them; prologue_finish then folds the
+// deferred norm or the gated output norm and quantizes into LDS.
+template <int R, bool GATED>  // rounds of 256 items the registers hold (cols <= 4096 R); the gated output norm
+struct XF {
+    float v[R][16];
+    float w[R <= 2 ? R : 1][16];  // NORM: the norm weight (the activation again without one); GATED: the gated norm's
+                                  // weight (one head, item % 8)
+    float z[GATED ? R : 1][16];   // GATED: the output gate
+};
+
+__device__ __forceinline__ void load16(const float * p, float * v) {
     const float4 * q = reinterpret_cast<const float4 *>(p);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4; ++i) {
         const float4 t = q[i];
         v[4 * i] = t.x;
         v[4 * i + 1] = t.y;
@@ -79,15 +87,44 @@ __device__ __forceinline__ void load_block(const float * p, float * v) {
     }
 }
 
-__device__ __forceinline__ void quantize_block(const float * v, int b, Lds & s) {
+// Item index clamped into the vector (threads past the end load a valid item and store nothing).
+__device__ __forceinline__ int item_of(int g, int n16) {
+    const int i = int(threadIdx.x) + NT * g;
+    return i < n16 ? i : n16 - 1;
+}
+
+// Every load is unconditional (an operand a source does not use is read from the activation itself), so the loads
+// cannot be moved into the branches that use them, behind the weight loads.
+template <int R, bool GATED>
+__device__ __forceinline__ void prologue_fetch(const GemvArgs & a, XF<R, GATED> & f) {
+    const int n16 = a.cols / 16;
+    const bool normw = a.xsrc == XSRC_NORM && a.norm_w != nullptr;
+#pragma unroll
+    for (int g = 0; g < R; ++g) {
+        const int i = item_of(g, n16);
+        const float * xi = a.x + size_t(i) * 16;
+        load16(xi, f.v[g]);
+        if constexpr (GATED) {
+            load16(a.gate_z + size_t(i) * 16, f.z[g]);
+            load16(a.norm_w + size_t(i & 7) * 16, f.w[g]);
+        } else if constexpr (R <= 2) {
+            load16(normw ? a.norm_w + size_t(i) * 16 : xi, f.w[g]);
+        }
+    }
+}
+
+// Q8_0 of one 32-block held as two halves by lanes l and l ^ 1: d = amax / 127 over the block, q = round(v / d)
+// (half away from zero), the block's quant sum, and for Q4_1 weights the Q8_1 s = fp16(sum * d).
+__device__ __forceinline__ void quantize_half(const float * v, int item, bool valid, Lds & s) {
     float amax = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    amax = fmaxf(amax, dpp_f32<DPP_XOR1>(amax));
     const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
-    uint32_t packed[8];
+    uint32_t packed[4];
     int sum = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4; ++i) {
         uint32_t w = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -97,118 +134,102 @@ __device__ __forceinline__ void quantize_block(const float * v, int b, Lds & s) 
         }
         packed[i] = w;
     }
-    uint4 * dst = reinterpret_cast<uint4 *>(s.xq + size_t(b) * 32);
-    dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-    dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
-    s.info[b] = f2h(d) | (uint32_t(sum & 0xffff) << 16);
-    s.s1[b] = uint16_t(f2h(float(sum) * d));  // ggml quantize_row_q8_1: s = fp16(sum * d) with the FP32 d
+    sum += __shfl_xor(sum, 1, WAVE);
+    if (valid) {
+        *reinterpret_cast<uint4 *>(s.xq + size_t(item) * 16) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+        if ((item & 1) == 0) {
+            s.info[item >> 1] = f2h(d) | (uint32_t(sum & 0xffff) << 16);
+            s.s1[item >> 1] = uint16_t(f2h(float(sum) * d));  // ggml quantize_row_q8_1: s = fp16(sum * d), FP32 d
+        }
+    }
 }
 
-// The DeltaNet gated output norm applied while quantizing (gemvqc_gdn.h:284-346): per head of 128, x =
-// silu(z) * ((y * s) * w) with s = 1 / sqrt(sum(y^2) / 128 + eps), the sum the pairwise tree over the head (the
-// tree over each 32-block, then over the head's 4 consecutive blocks, held by 4 aligned lanes). cols <= 8192 and a
-// multiple of 128. Workgroup 0 also stores the gated values, which the separate norm would have written.
-__device__ __forceinline__ void prologue_gated(const GemvArgs & a, Lds & s) {
-    const int nb = a.cols / 32, b = threadIdx.x;
-    if (b >= nb) return;  // whole groups of 4 lanes (nb is a multiple of 4)
-    float v[32], z[32], w[32];
-    load_block(a.x + size_t(b) * 32, v);
-    load_block(a.gate_z + size_t(b) * 32, z);
-    load_block(a.norm_w + size_t(b & 3) * 32, w);
-    float sq[32];
+// Norm scale over the whole vector: tree over each item's 16 squares, pairwise over the 64 items of a wave, the 4
+// waves of a round and the rounds (padded to a power of two with zeros): the canonical pairwise tree over n.
+template <int R, bool GATED>
+__device__ __forceinline__ float norm_scale_items(const GemvArgs & a, const XF<R, GATED> & f, Lds & s) {
+    const int n16 = a.cols / 16, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float r[R];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) sq[j] = v[j] * v[j];
-    const float sum = pair_sum_lanes<4>(tree<32>(sq));
-    const float sc = 1.0f / sqrtf(sum / 128.0f + a.norm_eps);
-    if (a.gate_silu) {
+    for (int g = 0; g < R; ++g) {
+        float sq[16];
 #pragma unroll
-        for (int j = 0; j < 32; ++j) v[j] = z[j] * ((v[j] * sc) * w[j]);
-    } else {
-#pragma unroll
-        for (int j = 0; j < 32; ++j) v[j] = silu_(z[j]) * ((v[j] * sc) * w[j]);
+        for (int j = 0; j < 16; ++j) sq[j] = f.v[g][j] * f.v[g][j];
+        r[g] = int(threadIdx.x) + NT * g < n16 ? tree<16>(sq) : 0.0f;
     }
-    if (blockIdx.x == 0) {
-        float4 * o = reinterpret_cast<float4 *>(a.x_out + size_t(b) * 32);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-    }
-    quantize_block(v, b, s);
-}
-
-template <int ROUNDS>  // rounds of 256 blocks the registers hold (cols <= 8192: 1)
-__device__ void prologue_q8_0(const GemvArgs & a, Lds & s) {
-    const int nb = a.cols / 32, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (a.xsrc == XSRC_GATED) {
-        prologue_gated(a, s);
-        return;
-    }
-    if (a.xsrc != XSRC_NORM) {
-        for (int b = tid; b < nb; b += NT) {
-            float v[32];
-            load_block(a.x + size_t(b) * 32, v);
-            quantize_block(v, b, s);
-        }
-        return;
-    }
-    float v0[32], v1[ROUNDS > 1 ? 32 : 1];
-    const int b0 = tid, b1 = tid + NT;
-    float r0 = 0.0f, r1 = 0.0f;
-    {
-        float sq[32];
-        if (b0 < nb) {
-            load_block(a.x + size_t(b0) * 32, v0);
-#pragma unroll
-            for (int j = 0; j < 32; ++j) sq[j] = v0[j] * v0[j];
-        } else {
-#pragma unroll
-            for (int j = 0; j < 32; ++j) v0[j] = sq[j] = 0.0f;
-        }
-        r0 = pair_sum_lanes<64>(tree<32>(sq));
-    }
-    if constexpr (ROUNDS > 1) {
-        float sq[32];
-        if (b1 < nb) {
-            load_block(a.x + size_t(b1) * 32, v1);
-#pragma unroll
-            for (int j = 0; j < 32; ++j) sq[j] = v1[j] * v1[j];
-        } else {
-#pragma unroll
-            for (int j = 0; j < 32; ++j) v1[j] = sq[j] = 0.0f;
-        }
-        r1 = pair_sum_lanes<64>(tree<32>(sq));
-    }
+    pair_sum_lanes_n<64, R>(r);
     if (lane == 0) {
-        s.red[wave] = r0;
-        s.red[4 + wave] = r1;
+#pragma unroll
+        for (int g = 0; g < R; ++g) s.red[NWAVES * g + wave] = r[g];
     }
     __syncthreads();
-    const float sum = ((s.red[0] + s.red[1]) + (s.red[2] + s.red[3])) + ((s.red[4] + s.red[5]) + (s.red[6] + s.red[7]));
-    const float scale = a.norm_l2 ? 1.0f / fmaxf(sqrtf(sum), a.norm_eps) : 1.0f / sqrtf(sum / float(a.cols) + a.norm_eps);
-    if (b0 < nb) {
-        if (a.norm_w) {
-            float w[32];
-            load_block(a.norm_w + size_t(b0) * 32, w);
+    float rs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int j = 0; j < 32; ++j) v0[j] = (v0[j] * scale) * w[j];
-        } else {
+    for (int g = 0; g < R; ++g)
+        rs[g] = (s.red[NWAVES * g] + s.red[NWAVES * g + 1]) + (s.red[NWAVES * g + 2] + s.red[NWAVES * g + 3]);
+    const float sum = R == 1 ? rs[0] : R == 2 ? rs[0] + rs[1] : (rs[0] + rs[1]) + (rs[2] + rs[3]);
+    return a.norm_l2 ? 1.0f / fmaxf(sqrtf(sum), a.norm_eps) : 1.0f / sqrtf(sum / float(a.cols) + a.norm_eps);
+}
+
+// Without the gated norm the three sources share one path: v = (x * scale) * w with scale and w exactly 1 where a
+// source has no norm or no weight (x * 1 is x), so no branch separates them; the norm's sum is formed either way.
+template <int R, bool GATED>
+__device__ __forceinline__ void prologue_finish(const GemvArgs & a, XF<R, GATED> & f, Lds & s) {
+    const int n16 = a.cols / 16;
+    if constexpr (GATED) {
+        // the DeltaNet gated output norm (gemvqc_gdn.h:284-346): per head of 128 (8 items, 8 lanes), x =
+        // silu(z) * ((y * sc) * w) with sc = 1 / sqrt(sum(y^2) / 128 + eps); workgroup 0 also stores x, which the
+        // separate norm would have written
+        float hs[R];
 #pragma unroll
-            for (int j = 0; j < 32; ++j) v0[j] = v0[j] * scale;
+        for (int g = 0; g < R; ++g) {
+            float sq[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) sq[j] = f.v[g][j] * f.v[g][j];
+            hs[g] = tree<16>(sq);
         }
-        quantize_block(v0, b0, s);
-    }
-    if constexpr (ROUNDS > 1) {
-      if (b1 < nb) {
-        if (a.norm_w) {
-            float w[32];
-            load_block(a.norm_w + size_t(b1) * 32, w);
+        pair_sum_lanes_n<8, R>(hs);
 #pragma unroll
-            for (int j = 0; j < 32; ++j) v1[j] = (v1[j] * scale) * w[j];
-        } else {
+        for (int g = 0; g < R; ++g) {
+            const float sc = 1.0f / sqrtf(hs[g] / 128.0f + a.norm_eps);
+            float * v = f.v[g];
+            if (a.gate_silu) {
 #pragma unroll
-            for (int j = 0; j < 32; ++j) v1[j] = v1[j] * scale;
+                for (int j = 0; j < 16; ++j) v[j] = f.z[g][j] * ((v[j] * sc) * f.w[g][j]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) v[j] = silu_(f.z[g][j]) * ((v[j] * sc) * f.w[g][j]);
+            }
+            const int i = int(threadIdx.x) + NT * g;
+            if (blockIdx.x == 0 && i < n16) {
+                float4 * o = reinterpret_cast<float4 *>(a.x_out + size_t(i) * 16);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) o[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+            }
+            quantize_half(v, i, i < n16, s);
         }
-        quantize_block(v1, b1, s);
-      }
+    } else {
+        const bool norm = a.xsrc == XSRC_NORM, normw = norm && a.norm_w != nullptr;
+        const float scale = norm_scale_items<R, GATED>(a, f, s);
+        const float sc = norm ? scale : 1.0f;
+#pragma unroll
+        for (int g = 0; g < R; ++g) {
+            const int i = int(threadIdx.x) + NT * g;
+            float * v = f.v[g];
+            if constexpr (R <= 2) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) v[j] = (v[j] * sc) * (normw ? f.w[g][j] : 1.0f);
+            } else if (normw) {  // wide vectors: the weight is read now (registers hold only the activation)
+                float w[16];
+                load16(a.norm_w + size_t(item_of(g, n16)) * 16, w);
+#pragma unroll
+                for (int j = 0; j < 16; ++j) v[j] = (v[j] * sc) * w[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) v[j] = v[j] * sc;
+            }
+            quantize_half(v, i, i < n16, s);
+        }
     }
 }
 
@@ -284,18 +305,21 @@ struct XK {  // one 64-weight unit (Q5_K / Q6_K)
     int m, e, neg;
 };
 
-// Lanes past the last unit load a valid unit (their terms are never added).
+// Lanes past the last block hold a zero block (zero quants and scales), whose terms are exactly zero.
 template <int TYPE>
 __device__ __forceinline__ void load_xb(const Lds & s, int b, int nb, XB & x) {
-    b = b < nb ? b : nb - 1;
+    const bool in = b < nb;
+    b = in ? b : nb - 1;
     const uint4 * p = reinterpret_cast<const uint4 *>(s.xq + size_t(b) * 32);
     const uint4 lo = p[0], hi = p[1];
     x.q[0] = lo.x; x.q[1] = lo.y; x.q[2] = lo.z; x.q[3] = lo.w;
     x.q[4] = hi.x; x.q[5] = hi.y; x.q[6] = hi.z; x.q[7] = hi.w;
-    const uint32_t inf = s.info[b];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x.q[i] = in ? x.q[i] : 0u;
+    const uint32_t inf = in ? s.info[b] : 0u;
     x.dx40 = h2f(inf & 0xffffu) * 1099511627776.0f;  // * 2^40
     x.sum = int(int16_t(inf >> 16));
-    x.sx40 = TYPE == T_Q4_1 ? h2f(s.s1[b]) * 1099511627776.0f : 0.0f;
+    x.sx40 = TYPE == T_Q4_1 && in ? h2f(s.s1[b]) * 1099511627776.0f : 0.0f;
 }
 
 template <int TYPE>
@@ -505,76 +529,70 @@ __device__ __forceinline__ long long superblock_term(int S, int M, const WK & w,
     return t;
 }
 
-// ---- rows: weight loads are issued one task ahead of the compute ----
-template <int TYPE, int NU>
-struct Rows {
+// ---- rows: a wave owns a range of rows of one member and keeps D of them in flight ----
+// Per-row register cost decides D (1 to 4): the weight slots of D rows stay near 64 VGPRs.
+template <int TYPE, int NU, bool PAIR>
+constexpr int slots() {
+    const int per = (TYPE == T_Q5_K || TYPE == T_Q6_K ? 20 : TYPE == T_Q8_0 ? 9 : 5) * NU * (PAIR ? 2 : 1);
+    const int d = 64 / per;
+    return d < 1 ? 1 : d > 4 ? 4 : d;
+}
+
+template <int TYPE, int NU, bool PAIR>
+struct Slot {  // one row in flight
     static constexpr bool KQ = TYPE == T_Q5_K || TYPE == T_Q6_K;
-    WB wb[KQ ? 1 : NU], wb2[KQ ? 1 : NU];  // g (or the matrix) and u of a SwiGLU pair
-    WK wk[KQ ? NU : 1], wk2[KQ ? NU : 1];
-    float e[8];  // epilog operands: ADD residual (e[0]); CONV state (e[0..2]) and kernel (e[4..7])
+    WB wb[KQ ? 1 : NU], wb2[(KQ || !PAIR) ? 1 : NU];  // g (or the matrix) and u of a SwiGLU pair
+    WK wk[KQ ? NU : 1], wk2[(KQ && PAIR) ? NU : 1];
+    float e;  // epilog operands: ADD residual (every lane); CONV: lanes 0-2 the state, lanes 3-6 the kernel
 };
 
-// Loads of one row (and its epilog operands), specialized by epilog kind so that no branch surrounds a load: a
-// load behind a branch, or issued after the next row's weights, makes the compute wait for every load before it.
-template <int TYPE, int NU, int EPI>
-__device__ __forceinline__ void load_row(const GemvMember & m, int r, int lane, int nb, int nu, Rows<TYPE, NU> & R) {
-    if constexpr (Rows<TYPE, NU>::KQ) {
+// Loads of row r: the same code for every epilog kind, so that no branch surrounds a load (a load behind a branch
+// makes the waits after the branch count it conservatively). The second matrix of a pair kernel is the member's own
+// matrix for members that are not SwiGLU, and the epilog operand address (ea/eb, set at launch) falls back to the
+// row's output for kinds without one.
+template <int TYPE, int NU, bool PAIR>
+__device__ __forceinline__ void load_slot(const GemvMember & m, int r, int lane, int nb, int nu, Slot<TYPE, NU, PAIR> & o) {
+    if constexpr (Slot<TYPE, NU, PAIR>::KQ) {
         const int nsb = nu >> 2;
 #pragma unroll
         for (int k = 0; k < NU; ++k) {
             const int u0 = lane + 64 * k, u = u0 < nu ? u0 : nu - 1;
-            load_wk<TYPE>(m.w, size_t(r) * nsb + (u >> 2), u & 3, R.wk[k]);
-            if constexpr (EPI == EPI_SWIGLU) load_wk<TYPE>(m.w2, size_t(r) * nsb + (u >> 2), u & 3, R.wk2[k]);
+            load_wk<TYPE>(m.w, size_t(r) * nsb + (u >> 2), u & 3, o.wk[k]);
+            if constexpr (PAIR) load_wk<TYPE>(m.w2, size_t(r) * nsb + (u >> 2), u & 3, o.wk2[k]);
         }
     } else {
 #pragma unroll
         for (int k = 0; k < NU; ++k) {
             const int b = lane + 64 * k, bb = b < nb ? b : nb - 1;
-            load_wb<TYPE>(m.w, size_t(r) * nb + bb, R.wb[k]);
-            if constexpr (EPI == EPI_SWIGLU) load_wb<TYPE>(m.w2, size_t(r) * nb + bb, R.wb2[k]);
+            load_wb<TYPE>(m.w, size_t(r) * nb + bb, o.wb[k]);
+            if constexpr (PAIR) load_wb<TYPE>(m.w2, size_t(r) * nb + bb, o.wb2[k]);
         }
     }
-    if constexpr (EPI == EPI_ADD) R.e[0] = m.res[r];
-    if constexpr (EPI == EPI_CONV) {
-        R.e[0] = m.conv_src[3 * r];
-        R.e[1] = m.conv_src[3 * r + 1];
-        R.e[2] = m.conv_src[3 * r + 2];
-        const float4 k = *reinterpret_cast<const float4 *>(m.conv_w + 4 * size_t(r));
-        R.e[4] = k.x;
-        R.e[5] = k.y;
-        R.e[6] = k.z;
-        R.e[7] = k.w;
-    }
+    const int l = (lane < 7 ? lane : 6) * m.e_lane;
+    const float * pa = m.ea + (size_t(r) * m.e_sa + l);
+    const float * pb = m.eb + (size_t(r) * m.e_sb + (l - m.e_split));
+    o.e = *(lane < m.e_split ? pa : pb);
 }
 
+// Per-lane partial of one row (its lane's units), exact: the block terms are integers below 2^53 summed in FP64.
+// dbg (block sums for the tests) is written only for a row that exists.
 template <int TYPE, int NU>
-__device__ __forceinline__ void load_row_any(const GemvMember & m, int r, int lane, int nb, int nu, Rows<TYPE, NU> & R) {
-    switch (m.epi) {
-    case EPI_SWIGLU: load_row<TYPE, NU, EPI_SWIGLU>(m, r, lane, nb, nu, R); break;
-    case EPI_ADD: load_row<TYPE, NU, EPI_ADD>(m, r, lane, nb, nu, R); break;
-    case EPI_CONV: load_row<TYPE, NU, EPI_CONV>(m, r, lane, nb, nu, R); break;
-    default: load_row<TYPE, NU, EPI_PLAIN>(m, r, lane, nb, nu, R); break;
-    }
-}
-
-template <int TYPE, int NU, bool DBG>
-__device__ __forceinline__ long long row_blocks(const WB * wb, int r, int nb, const XB * xb, int lane, int32_t * dbg) {
+__device__ __forceinline__ long long lane_blocks(const WB * wb, int r, bool valid, int nb, const XB * xb, int lane,
+                                                 int32_t * dbg) {
     double acc = 0.0;
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
         const int b = lane + 64 * k;
         const int si = dot_block<TYPE>(wb[k], xb[k]);
-        const double t = block_term<TYPE>(si, wb[k].d, xb[k]);
-        acc += b < nb ? t : 0.0;
-        if constexpr (DBG) {
-            if (dbg && b < nb) dbg[size_t(r) * nb + b] = si;
-        }
+        acc += block_term<TYPE>(si, wb[k].d, xb[k]);  // units past the row's end hold a zero activation
+        if (dbg && valid && b < nb) dbg[size_t(r) * nb + b] = si;
     }
-    return wave_sum_i64(dint_to_i64(acc));
+    return dint_to_i64(acc);
 }
 
-template <int TYPE, int NU, bool DBG>
-__device__ __forceinline__ long long row_units(const WK * wk, int r, int nu, const XK * xk, int lane, int32_t * dbg) {
+template <int TYPE, int NU>
+__device__ __forceinline__ long long lane_units(const WK * wk, int r, bool valid, int nu, const XK * xk, int lane,
+                                                int32_t * dbg) {
     const int nsb = nu >> 2;
     long long acc = 0;
 #pragma unroll
@@ -587,15 +605,13 @@ __device__ __forceinline__ long long row_units(const WK * wk, int r, int nu, con
         M = sum_lanes4_i32(M);
         const long long t = superblock_term<TYPE>(S, M, wk[k], xk[k]);
         acc += (u < nu && (u & 3) == 0) ? t : 0;
-        if constexpr (DBG) {
-            if (dbg && u < nu && (u & 3) == 0) {
-                const size_t i = (size_t(r) * nsb + (u >> 2)) * 2;
-                dbg[i] = S;
-                dbg[i + 1] = M;
-            }
+        if (dbg && valid && u < nu && (u & 3) == 0) {
+            const size_t i = (size_t(r) * nsb + (u >> 2)) * 2;
+            dbg[i] = S;
+            dbg[i + 1] = M;
         }
     }
-    return wave_sum_i64(acc);
+    return acc;
 }
 
 struct Ctx {  // per-wave state shared by the row loops
@@ -603,91 +619,152 @@ struct Ctx {  // per-wave state shared by the row loops
     unsigned long long best;
 };
 
-// One row: dots, exact row sum, epilog (lane 0 stores).
-template <int TYPE, int NU, int EPI, bool DBG>
-__device__ __forceinline__ void row_compute(const GemvArgs & a, const GemvMember & m, bool argmax, int32_t * dbg, int r,
-                                            const Rows<TYPE, NU> & R, const XB * xb, const XK * xk, Ctx & c) {
-    long long acc, acc2 = 0;
-    if constexpr (Rows<TYPE, NU>::KQ) {
-        acc = row_units<TYPE, NU, DBG>(R.wk, r, c.nu, xk, c.lane, dbg);
-        if constexpr (EPI == EPI_SWIGLU) acc2 = row_units<TYPE, NU, false>(R.wk2, r, c.nu, xk, c.lane, nullptr);
+__device__ __forceinline__ float lane_value(float v, int j) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+}
+
+template <int TYPE, int NU, bool PAIR, int EPI>
+__device__ __forceinline__ void lane_partials(const Slot<TYPE, NU, PAIR> & R, int r, bool valid, const XB * xb,
+                                              const XK * xk, Ctx & c, int32_t * dbg, long long & p, long long & p2) {
+    if constexpr (Slot<TYPE, NU, PAIR>::KQ) {
+        p = lane_units<TYPE, NU>(R.wk, r, valid, c.nu, xk, c.lane, dbg);
+        if constexpr (PAIR && EPI == EPI_SWIGLU) p2 = lane_units<TYPE, NU>(R.wk2, r, valid, c.nu, xk, c.lane, nullptr);
     } else {
-        acc = row_blocks<TYPE, NU, DBG>(R.wb, r, c.nb, xb, c.lane, dbg);
-        if constexpr (EPI == EPI_SWIGLU) acc2 = row_blocks<TYPE, NU, false>(R.wb2, r, c.nb, xb, c.lane, nullptr);
+        p = lane_blocks<TYPE, NU>(R.wb, r, valid, c.nb, xb, c.lane, dbg);
+        if constexpr (PAIR && EPI == EPI_SWIGLU) p2 = lane_blocks<TYPE, NU>(R.wb2, r, valid, c.nb, xb, c.lane, nullptr);
     }
-    if (c.lane == 0) {
-        const float v = fixed_to_float(acc);
+}
+
+// The n (<= D) rows base, base + stride, ... of a chunk: the row totals are reduced together (lane group g holds row g), the
+// epilog runs once for all of them on the groups' first lanes, which store; CONV, whose operands sit in lanes 0-6
+// of ev[j], is finished row by row on lane 0. ev holds the rows' epilog operands, taken from the slots before
+// they were refilled.
+template <int TYPE, int NU, bool PAIR, int EPI>
+__device__ __forceinline__ void finish_chunk(const GemvMember & m, bool argmax, int base, int stride, int n,
+                                             const long long * p, const long long * p2, const float * ev, Ctx & c) {
+    constexpr int DS = slots<TYPE, NU, PAIR>();
+    constexpr int G = DS == 1 ? 1 : DS == 2 ? 2 : 4;
+    constexpr int GW = 64 / G;
+    long long pp[G], qq[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        pp[j] = j < DS ? p[j < DS ? j : 0] : 0;
+        qq[j] = j < DS ? p2[j < DS ? j : 0] : 0;
+    }
+    const long long tot = reduce_rows<G>(pp);
+    if constexpr (EPI == EPI_CONV) {
+#pragma unroll
+        for (int j = 0; j < DS; ++j) {
+            if (j < n) {
+                float e[7];
+#pragma unroll
+                for (int k = 0; k < 7; ++k) e[k] = lane_value(ev[j], k);
+                const float v = fixed_to_float(readlane_i64(tot, j * GW));
+                if (c.lane == 0) {  // gemvqc_ops.h:387-431 on the row result
+                    const int r = base + j * stride;
+                    float sum = 0.0f;
+                    sum += e[0] * e[3];
+                    sum += e[1] * e[4];
+                    sum += e[2] * e[5];
+                    sum += v * e[6];
+                    m.y[r] = m.conv_silu ? silu_(sum) : sum;
+                    m.conv_dst[3 * r] = e[1];
+                    m.conv_dst[3 * r + 1] = e[2];
+                    m.conv_dst[3 * r + 2] = v;
+                }
+            }
+        }
+    } else {
+        const int g = c.lane / GW;
+        const float v = fixed_to_float(tot);
         float out = v;
-        if constexpr (EPI == EPI_SWIGLU) {
-            out = (v / (1.0f + expf_(-v))) * fixed_to_float(acc2);  // gemvqc_ops.h:88-92
+        if constexpr (PAIR && EPI == EPI_SWIGLU) {
+            const long long tot2 = reduce_rows<G>(qq);
+            out = (v / (1.0f + expf_(-v))) * fixed_to_float(tot2);  // gemvqc_ops.h:88-92
         } else if constexpr (EPI == EPI_ADD) {
-            out = v + R.e[0];  // gemvqc16.cpp:282-301
+            uint32_t eb = 0;  // the residual of row g (every lane of a slot holds its row's), gathered bitwise
+#pragma unroll
+            for (int j = 0; j < DS; ++j) eb |= (g == j ? 0xffffffffu : 0u) & __float_as_uint(ev[j]);
+            out = v + __uint_as_float(eb);  // gemvqc16.cpp:282-301
         } else if constexpr (EPI == EPI_SILU) {
             out = silu_(v);  // gemvqc_ops.h:70-79 (UNARY SiLU) on the row result
-        } else if constexpr (EPI == EPI_CONV) {  // gemvqc_ops.h:387-431 on the row result
-            float sum = 0.0f;
-            sum += R.e[0] * R.e[4];
-            sum += R.e[1] * R.e[5];
-            sum += R.e[2] * R.e[6];
-            sum += v * R.e[7];
-            out = m.conv_silu ? silu_(sum) : sum;
-            m.conv_dst[3 * r] = R.e[1];
-            m.conv_dst[3 * r + 1] = R.e[2];
-            m.conv_dst[3 * r + 2] = v;
         }
-        m.y[r] = out;
-        if (argmax) {
-            const unsigned long long key = argmax_key(out, uint32_t(r));
-            c.best = key > c.best ? key : c.best;
+        if ((c.lane & (GW - 1)) == 0 && g < n) {
+            const int r = base + g * stride;
+            m.y[r] = out;
+            if (argmax) {
+                const unsigned long long key = argmax_key(out, uint32_t(r));
+                c.best = key > c.best ? key : c.best;
+            }
         }
     }
 }
 
-// Rows r0..r1-1 of one member, two register buffers in turn: the loads of row r + 1 are in flight while row r is
-// reduced, and no buffer is copied (a copy of registers that are still being loaded would wait for them). Rows
-// past r1 - 1 reload the last row, which the caches serve; their results are not stored.
-template <int TYPE, int NU, int EPI, bool DBG>
-__device__ __forceinline__ void run_rows(const GemvArgs & a, const GemvMember & m, int mi, int r0, int r1,
-                                         Rows<TYPE, NU> & A, const XB * xb, const XK * xk, Ctx & c) {
+// The n rows w, w + S, w + 2 S, ... of one member (k-th row w + k S): slot j holds row k = kb + j; while more
+// than D rows remain, a slot is refilled with the row D further on as soon as its partial is formed
+// (unconditionally, so the waits stay exact); the last chunk only reduces.
+template <int TYPE, int NU, bool PAIR, int EPI>
+__device__ __forceinline__ void run_rows(const GemvArgs & a, const GemvMember & m, int mi, int w, int S, int n,
+                                         Slot<TYPE, NU, PAIR> * sl, const XB * xb, const XK * xk, Ctx & c) {
+    constexpr int DS = slots<TYPE, NU, PAIR>();
     const bool argmax = EPI == EPI_PLAIN && a.argmax_key != nullptr && mi == 0;
-    int32_t * dbg = (DBG && mi == 0) ? a.dbg : nullptr;
-    Rows<TYPE, NU> B;
-    for (int r = r0;; r += 2) {
-        load_row<TYPE, NU, EPI>(m, min(r + 1, r1 - 1), c.lane, c.nb, c.nu, B);
-        row_compute<TYPE, NU, EPI, DBG>(a, m, argmax, dbg, r, A, xb, xk, c);
-        if (r + 1 >= r1) break;
-        load_row<TYPE, NU, EPI>(m, min(r + 2, r1 - 1), c.lane, c.nb, c.nu, A);
-        row_compute<TYPE, NU, EPI, DBG>(a, m, argmax, dbg, r + 1, B, xb, xk, c);
-        if (r + 2 >= r1) break;
+    int32_t * dbg = mi == 0 ? a.dbg : nullptr;
+    long long p[DS], p2[DS];
+    float ev[DS];
+    int kb = 0;
+    for (; kb + DS < n; kb += DS) {
+#pragma unroll
+        for (int j = 0; j < DS; ++j) {
+            p2[j] = 0;
+            lane_partials<TYPE, NU, PAIR, EPI>(sl[j], w + (kb + j) * S, true, xb, xk, c, dbg, p[j], p2[j]);
+            ev[j] = sl[j].e;
+            load_slot<TYPE, NU, PAIR>(m, w + min(kb + DS + j, n - 1) * S, c.lane, c.nb, c.nu, sl[j]);
+        }
+        finish_chunk<TYPE, NU, PAIR, EPI>(m, argmax, w + kb * S, S, DS, p, p2, ev, c);
     }
+#pragma unroll
+    for (int j = 0; j < DS; ++j) {
+        p2[j] = 0;
+        lane_partials<TYPE, NU, PAIR, EPI>(sl[j], w + (kb + j) * S, kb + j < n, xb, xk, c, dbg, p[j], p2[j]);
+        ev[j] = sl[j].e;
+    }
+    finish_chunk<TYPE, NU, PAIR, EPI>(m, argmax, w + kb * S, S, min(DS, n - kb), p, p2, ev, c);
 }
 
-template <int TYPE, int NU, bool DBG>
+// Waves are assigned to members in order: member i owns the global waves wave_begin .. wave_begin + waves - 1;
+// waves past the last member only take part in the prologue.
+template <int TYPE, int NU, bool PAIR, bool GATED>
 __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
     __shared__ Lds s;
     constexpr bool KQ = TYPE == T_Q5_K || TYPE == T_Q6_K;
+    constexpr int DS = slots<TYPE, NU, PAIR>();
+    constexpr int RX = KQ ? 1 : (NU + 1) / 2;  // rounds of 4096 activation floats (cols <= 2048 NU)
     Ctx c;
     c.lane = threadIdx.x & 63;
     c.nb = a.cols / 32;
     c.nu = a.cols / 64;
     c.best = 0;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: member fields load as scalars
-    // each wave owns a contiguous range of tasks (streams through consecutive rows)
-    const int nwt = gridDim.x * NWAVES, per = (a.total_tasks + nwt - 1) / nwt;
-    const int t0 = (blockIdx.x * NWAVES + wave) * per;
-    const int t1 = min(a.total_tasks, t0 + per);
-    int mi0 = 0;
+    const int gw = blockIdx.x * NWAVES + wave;
+    int mi = 0;
 #pragma unroll
     for (int i = 1; i < 4; ++i)
-        if (i < a.n_members && t0 >= a.m[i].task_begin) mi0 = i;
-    // the first row's weights are requested before the activation prologue
-    Rows<TYPE, NU> cur;
-    if (t0 < t1) load_row_any<TYPE, NU>(a.m[mi0], t0 - a.m[mi0].task_begin, c.lane, c.nb, c.nu, cur);
+        if (i < a.n_members && gw >= a.m[i].wave_begin) mi = i;
+    const GemvMember & m = a.m[mi];
+    const int w = gw - m.wave_begin, S = m.waves;                   // rows w, w + S, ... of the member
+    const int n = w < S && w < m.rows ? (m.rows - 1 - w) / S + 1 : 0;  // waves past the last member have none
+    XF<RX, GATED> xf;
+    if constexpr (!KQ) prologue_fetch<RX, GATED>(a, xf);  // the activation is requested first
+    __builtin_amdgcn_sched_barrier(0);                    // and stays ahead of the weight loads
+    Slot<TYPE, NU, PAIR> sl[DS];  // the first D rows (a wave without rows reloads the member's last row)
+#pragma unroll
+    for (int j = 0; j < DS; ++j)
+        load_slot<TYPE, NU, PAIR>(m, n > 0 ? w + min(j, n - 1) * S : m.rows - 1, c.lane, c.nb, c.nu, sl[j]);
     if constexpr (KQ) {
         const float scale = a.xsrc == XSRC_NORM ? block_norm_scale(a.x, a.cols, a.norm_eps, a.norm_l2, s) : 1.0f;
         quantize_q8_K(a, scale, s);
     } else {
-        prologue_q8_0<(NU > 4 ? 2 : 1)>(a, s);
+        prologue_finish<RX, GATED>(a, xf, s);
     }
     __syncthreads();
     XB xb[KQ ? 1 : NU];
@@ -699,21 +776,25 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int k = 0; k < NU; ++k) load_xb<TYPE>(s, c.lane + 64 * k, c.nb, xb[k]);
     }
-    for (int mi = mi0; mi < a.n_members && t0 < t1; ++mi) {
-        const GemvMember & m = a.m[mi];
-        const int r0 = max(t0, m.task_begin) - m.task_begin, r1 = min(t1, m.task_begin + m.rows) - m.task_begin;
-        if (r0 >= r1) continue;
-        if (mi != mi0) load_row_any<TYPE, NU>(m, r0, c.lane, c.nb, c.nu, cur);
+    if (n > 0) {
         switch (m.epi) {
-        case EPI_SWIGLU: run_rows<TYPE, NU, EPI_SWIGLU, DBG>(a, m, mi, r0, r1, cur, xb, xk, c); break;
-        case EPI_ADD: run_rows<TYPE, NU, EPI_ADD, DBG>(a, m, mi, r0, r1, cur, xb, xk, c); break;
-        case EPI_CONV: run_rows<TYPE, NU, EPI_CONV, DBG>(a, m, mi, r0, r1, cur, xb, xk, c); break;
-        case EPI_SILU: run_rows<TYPE, NU, EPI_SILU, DBG>(a, m, mi, r0, r1, cur, xb, xk, c); break;
-        default: run_rows<TYPE, NU, EPI_PLAIN, DBG>(a, m, mi, r0, r1, cur, xb, xk, c); break;
+        case EPI_SWIGLU:
+            if constexpr (PAIR) run_rows<TYPE, NU, PAIR, EPI_SWIGLU>(a, m, mi, w, S, n, sl, xb, xk, c);
+            break;
+        case EPI_ADD: run_rows<TYPE, NU, PAIR, EPI_ADD>(a, m, mi, w, S, n, sl, xb, xk, c); break;
+        case EPI_CONV: run_rows<TYPE, NU, PAIR, EPI_CONV>(a, m, mi, w, S, n, sl, xb, xk, c); break;
+        case EPI_SILU: run_rows<TYPE, NU, PAIR, EPI_SILU>(a, m, mi, w, S, n, sl, xb, xk, c); break;
+        default: run_rows<TYPE, NU, PAIR, EPI_PLAIN>(a, m, mi, w, S, n, sl, xb, xk, c); break;
         }
     }
     if (a.argmax_key) {
-        if (c.lane == 0) s.key[wave] = c.best;
+        unsigned long long best = c.best;  // held by the lane-group leaders
+#pragma unroll
+        for (int st = 1; st < 64; st <<= 1) {
+            const unsigned long long o = (unsigned long long)shfl_xor_i64((long long)best, st);
+            best = o > best ? o : best;
+        }
+        if (c.lane == 0) s.key[wave] = best;
         __syncthreads();
         if (threadIdx.x == 0) {
             unsigned long long b = s.key[0];
@@ -733,15 +814,70 @@ int resident_blocks(K kernel) {
     return occ * cus;
 }
 
-template <int TYPE, int NU>
-hipError_t launch_typed(const GemvArgs & a, hipStream_t st) {
-    // about 16 tasks per workgroup (4 per wave) amortize the activation prologue; no more workgroups than fit
-    static const int cap = resident_blocks(gemv_kernel<TYPE, NU, false>);
-    int grid = (a.total_tasks + 15) / 16;
-    grid = grid < 1 ? 1 : grid > cap ? cap : grid;
-    if (a.dbg) GQ_LAUNCH((gemv_kernel<TYPE, NU, true>), dim3(grid), dim3(NT), 0, st, a);
-    else GQ_LAUNCH((gemv_kernel<TYPE, NU, false>), dim3(grid), dim3(NT), 0, st, a);
+// The members' waves: enough for ds rows each when they fit on the device at once (every row is requested before
+// the activation prologue ends); otherwise the resident waves, shared in proportion to the rows, stream them. A
+// member's rows are dealt to its waves in turn, so the rows in flight at any moment form one region of the matrix.
+int plan_waves(GemvArgs & a, int cap_blocks, int ds) {
+    int need = 0;
+    for (int i = 0; i < a.n_members; ++i) need += (a.m[i].rows + ds - 1) / ds;
+    const bool fits = (need + NWAVES - 1) / NWAVES <= cap_blocks;
+    const long long waves = (long long)cap_blocks * NWAVES;
+    long long total = 0;
+    for (int i = 0; i < a.n_members; ++i) total += a.m[i].rows;
+    int w = 0;
+    for (int i = 0; i < a.n_members; ++i) {
+        long long wi = fits ? (a.m[i].rows + ds - 1) / ds : waves * a.m[i].rows / total;
+        wi = wi < 1 ? 1 : wi > a.m[i].rows ? a.m[i].rows : wi;
+        a.m[i].wave_begin = w;
+        a.m[i].waves = int(wi);
+        w += int(wi);
+    }
+    const int grid = (w + NWAVES - 1) / NWAVES;
+    return grid < 1 ? 1 : grid;
+}
+
+// Epilog operand addresses of a member: with l = min(lane, 6) * e_lane, lanes below e_split read ea[r * e_sa + l],
+// the others eb[r * e_sb + l - e_split] (CONV: lanes 0-2 the state, lanes 3-6 the kernel; ADD: the residual).
+void epilog_operands(GemvMember & m) {
+    m.e_lane = 0;
+    m.e_split = 64;
+    m.e_sa = m.e_sb = 1;
+    m.ea = m.eb = m.y;
+    if (m.epi == EPI_ADD) {
+        m.ea = m.eb = m.res;
+    } else if (m.epi == EPI_CONV) {
+        m.e_lane = 1;
+        m.e_split = 3;
+        m.ea = m.conv_src;
+        m.e_sa = 3;
+        m.eb = m.conv_w;
+        m.e_sb = 4;
+    }
+    if (m.epi != EPI_SWIGLU) m.w2 = m.w;
+}
+
+template <int TYPE, int NU, bool PAIR, bool GATED>
+hipError_t launch_typed(const GemvArgs & a0, hipStream_t st) {
+    static const int cap = resident_blocks(gemv_kernel<TYPE, NU, PAIR, GATED>);
+    GemvArgs a = a0;
+    for (int i = 0; i < a.n_members; ++i) epilog_operands(a.m[i]);
+    const int grid = plan_waves(a, cap, slots<TYPE, NU, PAIR>());
+    GQ_LAUNCH((gemv_kernel<TYPE, NU, PAIR, GATED>), dim3(grid), dim3(NT), 0, st, a);
     return hipGetLastError();
+}
+
+// The gated activation prologue exists for Q4_0 / Q8_0 rows of at most 8192 columns without a SwiGLU pair.
+template <int TYPE, int NU>
+hipError_t launch_pair(const GemvArgs & a, hipStream_t st) {
+    bool pair = false;
+    for (int i = 0; i < a.n_members; ++i) pair = pair || a.m[i].epi == EPI_SWIGLU;
+    if (a.xsrc == XSRC_GATED) {
+        if constexpr ((TYPE == T_Q4_0 || TYPE == T_Q8_0) && NU <= 4) {
+            if (!pair) return launch_typed<TYPE, NU, false, true>(a, st);
+        }
+        return hipErrorInvalidValue;
+    }
+    return pair ? launch_typed<TYPE, NU, true, false>(a, st) : launch_typed<TYPE, NU, false, false>(a, st);
 }
 
 template <int TYPE>
@@ -749,18 +885,18 @@ hipError_t launch_nu(const GemvArgs & a, hipStream_t st) {
     constexpr bool KQ = TYPE == T_Q5_K || TYPE == T_Q6_K;
     const int nu = (a.cols / (KQ ? 64 : 32) + 63) / 64;  // cols <= 16384: K-quants nu <= 4, Q4_0 / Q8_0 nu <= 8
     switch (nu) {
-    case 1: return launch_typed<TYPE, 1>(a, st);
-    case 2: return launch_typed<TYPE, 2>(a, st);
-    case 3: return launch_typed<TYPE, 3>(a, st);
-    case 4: return launch_typed<TYPE, 4>(a, st);
+    case 1: return launch_pair<TYPE, 1>(a, st);
+    case 2: return launch_pair<TYPE, 2>(a, st);
+    case 3: return launch_pair<TYPE, 3>(a, st);
+    case 4: return launch_pair<TYPE, 4>(a, st);
     default: break;
     }
     if constexpr (!KQ) {
         switch (nu) {
-        case 5: return launch_typed<TYPE, 5>(a, st);
-        case 6: return launch_typed<TYPE, 6>(a, st);
-        case 7: return launch_typed<TYPE, 7>(a, st);
-        case 8: return launch_typed<TYPE, 8>(a, st);
+        case 5: return launch_pair<TYPE, 5>(a, st);
+        case 6: return launch_pair<TYPE, 6>(a, st);
+        case 7: return launch_pair<TYPE, 7>(a, st);
+        case 8: return launch_pair<TYPE, 8>(a, st);
         default: break;
         }
     }

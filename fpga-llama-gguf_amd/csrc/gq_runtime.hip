@@ -200,7 +200,8 @@ struct Compiler {
         const uint32_t * g = cmds + size_t(next) * GEMVQ_CMD_WORDS;
         const int t = int(g[1] & 0xffu);
         const bool apart = g[7] + uint64_t(g[2]) <= y || uint64_t(y) + cols <= g[7];  // its output is not the GDN's
-        return g[0] == GEMVQ_OP_GEMV && g[6] == y && g[3] == cols && (t == T_Q4_0 || t == T_Q8_0) && apart;
+        return g[0] == GEMVQ_OP_GEMV && g[6] == y && g[3] == cols && (t == T_Q4_0 || t == T_Q8_0) && apart &&
+               !(g[1] & GEMVQ_GEMV_SWIGLU);  // the gated prologue has no SwiGLU-pair variant
     }
 
     bool compile(const uint32_t * cmds, unsigned n) {
@@ -472,6 +473,7 @@ struct Compiler {
             if (gemvs + ((flags & GEMVQ_GEMV_SWIGLU) ? 2 : 1) > GEMVQ_GROUP) break;
             // workgroup 0 writes the gated activation while the group runs: no member may write over it
             if (gated.on && gemvs > 0 && !(k[7] + uint64_t(rows) <= gated.y || uint64_t(gated.y) + cols <= k[7])) break;
+            if (gated.on && (flags & GEMVQ_GEMV_SWIGLU)) break;
             if (gemvs == 0) {
                 type = t;
                 x_off = k[6];

@@ -214,6 +214,47 @@ def test_attention(gq, orc, ctx, nh, nkv, hd, nrot, n_ctx, npos, checks):
     assert np.array_equal(k_dev, kc[:npos].ravel()) and np.array_equal(v_dev, vc[:npos].ravel())
 
 
+@pytest.mark.parametrize("t", [2, 14])
+def test_gemv_epilogs_on_streamed_rows(gq, orc, t):
+    """Members long enough that each wave streams several chunks of rows (50000 rows: more than the resident waves
+    hold at once; a wave's range is not a whole number of chunks): plain + ARGMAX, residual ADD, SiLU, CONV (in-place
+    state) and the SwiGLU pair, each against the oracle bit for bit."""
+    R, K = 50000, 256
+    c = gq.Context(act_floats=1 << 20, weight_bytes=1 << 26, state_rows=0)
+    try:
+        x = gq.normal(0, 81, K)
+        w1 = gq.matrix(t, R, K, 0, 82)
+        w2 = gq.matrix(t, R, K, 0, 83)
+        o1, o2 = c.upload(t, R, K, w1), c.upload(t, R, K, w2)
+        X, RES, Y, Y2, KEY, CW, ST = 0, 1024, 65536, 131072, 196608, 262144, 524288
+        c.write(X, x)
+        res = gq.normal(0, 84, R)
+        c.write(RES, res)
+        y1 = orc.fx_gemv(t, w1, x, R, K)
+        y2 = orc.fx_gemv(t, w2, x, R, K)
+        c.write(KEY, np.zeros(4, np.float32))
+        assert c.run(gq.gemv(t, R, K, o1, X, Y, gq.GEMV_ARGMAX) + gq.argmax(R, Y, KEY)) == 0, c.error()
+        assert_bits(c.read(Y, R), y1, "plain")
+        assert 0xFFFFFFFF - int(c.read(KEY, 2, np.uint32)[0]) == int(np.argmax(y1))
+        assert c.run(gq.gemv(t, R, K, o1, X, Y2, gq.GEMV_ADD) + gq.add(R, Y2, RES, Y2)) == 0, c.error()
+        assert_bits(c.read(Y2, R), y1 + res, "add")
+        assert c.run(gq.gemv(t, R, K, o2, X, Y, gq.GEMV_SILU)) == 0, c.error()
+        assert_bits(c.read(Y, R), orc.unary(y2, 1), "silu")
+        assert c.run(gq.gemv(t, R, K, o1, X, Y, gq.GEMV_SWIGLU) + gq.gemv(t, R, K, o2, X, Y)) == 0, c.error()
+        assert_bits(c.read(Y, R), orc.silu_mul(y1, y2), "swiglu")
+        if t == 2:
+            st = gq.normal(0, 85, 3 * R)
+            kw = gq.normal(0, 86, 4 * R)
+            c.write(CW, kw)
+            c.write(ST, st)
+            assert c.run(gq.gemv(t, R, K, o2, X, Y2, gq.GEMV_CONV) + gq.conv(R, Y2, CW, Y, ST, ST)) == 0, c.error()
+            yc, ns = orc.conv(st, y2, kw)
+            assert_bits(c.read(Y, R), yc, "conv")
+            assert_bits(c.read(ST, 3 * R), ns, "conv state")
+    finally:
+        c.close()
+
+
 def test_gemv_fused_epilogs(gq, orc, ctx):
     """SwiGLU pair, residual ADD, CONV, ARGMAX epilogs and the deferred norm fold (gemvqc16.h:31-51)."""
     E, F = 2560, 9728
