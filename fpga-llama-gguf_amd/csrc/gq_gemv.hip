@@ -367,16 +367,30 @@ struct WK {  // one 64-weight K-quant unit
     uint32_t d;           // Q6_K: d; Q5_K: d | dmin << 16
 };
 
+// Weight loads are non-temporal: each byte is read once per token, so the stream should not displace what L2 holds
+// for reuse (activations, states, the KV cache).
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld16(const uint8_t * p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t ld2(const uint8_t * p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p));
+}
+__device__ __forceinline__ uint32_t ld4(const uint8_t * p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
+}
+
 template <int TYPE>
 __device__ __forceinline__ void load_wb(const WeightView & w, size_t idx, WB & o) {
-    o.lo = *reinterpret_cast<const uint4 *>(w.a + idx * 16);
+    o.lo = ld16(w.a + idx * 16);
     if (TYPE == T_Q4_0) {
-        o.d = *reinterpret_cast<const uint16_t *>(w.b + idx * 2);
+        o.d = ld2(w.b + idx * 2);
     } else if (TYPE == T_Q4_1) {
-        o.d = *reinterpret_cast<const uint32_t *>(w.b + idx * 4);
+        o.d = ld4(w.b + idx * 4);
     } else {
-        o.hi = *reinterpret_cast<const uint4 *>(w.b + idx * 16);
-        o.d = *reinterpret_cast<const uint16_t *>(w.c + idx * 2);
+        o.hi = ld16(w.b + idx * 16);
+        o.d = ld2(w.c + idx * 2);
     }
 }
 
@@ -422,25 +436,25 @@ template <int TYPE>
 __device__ __forceinline__ void load_wk(const WeightView & w, size_t sbi, int part, WK & o) {
     if (TYPE == T_Q6_K) {
         const int n = part >> 1, p = part & 1;
-        const uint4 * ql = reinterpret_cast<const uint4 *>(w.a + sbi * 128 + 64 * n + 32 * p);
-        const uint4 * qh = reinterpret_cast<const uint4 *>(w.b + sbi * 64 + 32 * n);
-        o.a0 = ql[0];
-        o.a1 = ql[1];
-        o.h0 = qh[0];
-        o.h1 = qh[1];
+        const uint8_t * ql = w.a + sbi * 128 + 64 * n + 32 * p;
+        const uint8_t * qh = w.b + sbi * 64 + 32 * n;
+        o.a0 = ld16(ql);
+        o.a1 = ld16(ql + 16);
+        o.h0 = ld16(qh);
+        o.h1 = ld16(qh + 16);
         const uint8_t * sc = w.c + sbi * 16;
-        o.s0 = *reinterpret_cast<const uint16_t *>(sc + 8 * n + 2 * p);
-        o.s1 = *reinterpret_cast<const uint16_t *>(sc + 8 * n + 4 + 2 * p);
+        o.s0 = ld2(sc + 8 * n + 2 * p);
+        o.s1 = ld2(sc + 8 * n + 4 + 2 * p);
         o.s2 = 0;
-        o.d = *reinterpret_cast<const uint16_t *>(w.d + sbi * 2);
+        o.d = ld2(w.d + sbi * 2);
     } else {
-        const uint4 * qs = reinterpret_cast<const uint4 *>(w.a + sbi * 128 + 32 * part);
-        const uint4 * qh = reinterpret_cast<const uint4 *>(w.b + sbi * 32);
-        o.a0 = qs[0];
-        o.a1 = qs[1];
-        o.h0 = qh[0];
-        o.h1 = qh[1];
-        const uint4 meta = *reinterpret_cast<const uint4 *>(w.c + sbi * 16);
+        const uint8_t * qs = w.a + sbi * 128 + 32 * part;
+        const uint8_t * qh = w.b + sbi * 32;
+        o.a0 = ld16(qs);
+        o.a1 = ld16(qs + 16);
+        o.h0 = ld16(qh);
+        o.h1 = ld16(qh + 16);
+        const uint4 meta = ld16(w.c + sbi * 16);
         o.d = meta.x;
         o.s0 = meta.y;
         o.s1 = meta.z;
@@ -745,14 +759,18 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
     c.nu = a.cols / 64;
     c.best = 0;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: member fields load as scalars
-    const int gw = blockIdx.x * NWAVES + wave;
+    // Workgroup b serves slice b % 8 of every member's rows (workgroups are dealt to the XCDs in turn, so a slice's
+    // rows stream through one XCD's L2; placement only affects speed, never which rows run).
+    const int xs = blockIdx.x & 7, lw = (blockIdx.x >> 3) * NWAVES + wave;  // slice, wave index within it
     int mi = 0;
 #pragma unroll
     for (int i = 1; i < 4; ++i)
-        if (i < a.n_members && gw >= a.m[i].wave_begin) mi = i;
+        if (i < a.n_members && lw >= a.m[i].wave_begin) mi = i;
     const GemvMember & m = a.m[mi];
-    const int w = gw - m.wave_begin, S = m.waves;                   // rows w, w + S, ... of the member
-    const int n = w < S && w < m.rows ? (m.rows - 1 - w) / S + 1 : 0;  // waves past the last member have none
+    const int s_lo = int((long long)xs * m.rows / 8), len = int((long long)(xs + 1) * m.rows / 8) - s_lo;
+    const int wv = lw - m.wave_begin, S = m.waves;                  // rows s_lo + wv, s_lo + wv + S, ... of the slice
+    const int n = wv < S && wv < len ? (len - 1 - wv) / S + 1 : 0;  // waves past the last member have none
+    const int w = s_lo + wv;
     XF<RX, GATED> xf;
     if constexpr (!KQ) prologue_fetch<RX, GATED>(a, xf);  // the activation is requested first
     __builtin_amdgcn_sched_barrier(0);                    // and stays ahead of the weight loads
@@ -814,26 +832,29 @@ int resident_blocks(K kernel) {
     return occ * cus;
 }
 
-// The members' waves: enough for ds rows each when they fit on the device at once (every row is requested before
-// the activation prologue ends); otherwise the resident waves, shared in proportion to the rows, stream them. A
-// member's rows are dealt to its waves in turn, so the rows in flight at any moment form one region of the matrix.
+// Every member's rows are split into 8 contiguous slices, one per XCD; the same member layout repeats on each XCD
+// (workgroups b with b % 8 == x serve slice x). A member's waves per slice: enough for ds rows each when all fit
+// on the device at once (every row is requested before the activation prologue ends); otherwise the resident waves,
+// shared in proportion to the rows, stream them. A slice's rows are dealt to its waves in turn, so the rows in flight
+// form one region of the slice.
 int plan_waves(GemvArgs & a, int cap_blocks, int ds) {
+    const int cap_x = cap_blocks / 8 < 1 ? 1 : cap_blocks / 8;  // workgroups per XCD
     int need = 0;
-    for (int i = 0; i < a.n_members; ++i) need += (a.m[i].rows + ds - 1) / ds;
-    const bool fits = (need + NWAVES - 1) / NWAVES <= cap_blocks;
-    const long long waves = (long long)cap_blocks * NWAVES;
+    for (int i = 0; i < a.n_members; ++i) need += ((a.m[i].rows + 7) / 8 + ds - 1) / ds;
+    const bool fits = (need + NWAVES - 1) / NWAVES <= cap_x;
+    const long long waves = (long long)cap_x * NWAVES;
     long long total = 0;
     for (int i = 0; i < a.n_members; ++i) total += a.m[i].rows;
     int w = 0;
     for (int i = 0; i < a.n_members; ++i) {
-        long long wi = fits ? (a.m[i].rows + ds - 1) / ds : waves * a.m[i].rows / total;
-        wi = wi < 1 ? 1 : wi > a.m[i].rows ? a.m[i].rows : wi;
+        const int per = (a.m[i].rows + 7) / 8;
+        long long wi = fits ? (per + ds - 1) / ds : waves * a.m[i].rows / total;
+        wi = wi < 1 ? 1 : wi > per ? per : wi;
         a.m[i].wave_begin = w;
         a.m[i].waves = int(wi);
         w += int(wi);
     }
-    const int grid = (w + NWAVES - 1) / NWAVES;
-    return grid < 1 ? 1 : grid;
+    return 8 * ((w + NWAVES - 1) / NWAVES);
 }
 
 // Epilog operand addresses of a member: with l = min(lane, 6) * e_lane, lanes below e_split read ea[r * e_sa + l],
@@ -918,3 +939,4 @@ hipError_t launch_gemv(const GemvArgs & a, int type, hipStream_t st) {
 }
 
 }  // namespace gq
+

@@ -35,8 +35,8 @@ struct GemvMember {
     const float * conv_w;     // CONV kernel [rows][4]
     int rows;
     int task_begin;  // first row of the member in the group's row order
-    int wave_begin;  // set at launch: the member's first wave in the grid
-    int waves;       // set at launch: the member's waves; wave w takes rows w, w + waves, w + 2 waves, ...
+    int wave_begin;  // set at launch: the member's first wave within each XCD slice
+    int waves;       // set at launch: the member's waves per slice; wave w takes the slice's rows w, w + waves, ...
     const float * ea;  // set at launch: epilog operand addresses (see epilog_operands)
     const float * eb;
     int e_sa, e_sb, e_split, e_lane;
