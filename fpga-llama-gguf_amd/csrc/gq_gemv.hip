@@ -128,7 +128,10 @@ __device__ __forceinline__ void quantize_half(const float * v, int item, bool va
         uint32_t w = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int q = int(roundf(v[4 * i + j] * id));
+            // roundf (half away from zero) as y + copysign(0.5 - 2^-25, y) truncated: equal for every |y| <= 128,
+            // and |y| <= 127 (1 + 2^-22) here
+            const float y = v[4 * i + j] * id;
+            const int q = int(y + copysignf(0.49999997f, y));
             sum += q;
             w |= (uint32_t(q) & 0xffu) << (8 * j);
         }
@@ -172,7 +175,7 @@ __device__ __forceinline__ float norm_scale_items(const GemvArgs & a, const XF<R
 }
 
 // Without the gated norm the three sources share one path: v = (x * scale) * w with scale and w exactly 1 where a
-// source has no norm or no weight (x * 1 is x), so no branch separates them; the norm's sum is formed either way.
+// source has no norm or no weight (x * 1 is x), so no branch separates the loads.
 template <int R, bool GATED>
 __device__ __forceinline__ void prologue_finish(const GemvArgs & a, XF<R, GATED> & f, Lds & s) {
     const int n16 = a.cols / 16;
@@ -210,8 +213,7 @@ __device__ __forceinline__ void prologue_finish(const GemvArgs & a, XF<R, GATED>
         }
     } else {
         const bool norm = a.xsrc == XSRC_NORM, normw = norm && a.norm_w != nullptr;
-        const float scale = norm_scale_items<R, GATED>(a, f, s);
-        const float sc = norm ? scale : 1.0f;
+        const float sc = norm ? norm_scale_items<R, GATED>(a, f, s) : 1.0f;  // the same on every thread
 #pragma unroll
         for (int g = 0; g < R; ++g) {
             const int i = int(threadIdx.x) + NT * g;

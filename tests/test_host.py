@@ -177,3 +177,18 @@ def test_model_sizes(gq):
             by_layer[il] = by_layer.get(il, 0) + Q.tensor_bytes(t, ne0, ne1)
     assert by_layer[0] == 122_830_848 and by_layer[3] == 117_964_800  # a DeltaNet layer, an attention layer
     assert sum(by_layer.values()) + 151936 * gq.row_bytes(B.Q6_K, 4096) == 4_402_163_712
+
+
+def test_activation_rounding_matches_roundf(tmp_path):
+    """The GEMV activation quantizer rounds with an add and a truncation; exhaustively equal to roundf for every
+    float of magnitude <= 128 (the quantizer's range)."""
+    import shutil
+    import subprocess
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc is not available")
+    exe = tmp_path / "round_check"
+    subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-fno-fast-math", os.path.join(os.path.dirname(__file__),
+                    "round_check.c"), "-o", str(exe), "-lm"], check=True)
+    n, bad = map(int, subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split())
+    assert n == 2248146946 and bad == 0
