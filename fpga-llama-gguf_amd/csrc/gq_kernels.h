@@ -139,7 +139,7 @@ struct AttnArgs {
     uint16_t * kc;        // [n_ctx][n_head_kv][head_dim]
     uint16_t * vc;
     float * part;         // partials: [n_head][max_chunks][2 + head_dim]
-    unsigned int * counter;  // [n_head_kv]
+    unsigned int * counter;  // [n_head_kv * ATTN_MAXG]: finished chunks per q head
     int n_head, n_head_kv, head_dim, n_rot, q_stride, n_ctx;
     float scale, eps;
 };
@@ -162,6 +162,7 @@ struct NextTokenArgs {
 };
 
 constexpr int ATTN_CHUNK = 64;
+constexpr int ATTN_MAXG = 4;  // q heads per KV head
 constexpr int GDN_MAX_HEADS = 64;  // value heads of one GDN command
 
 // Profiling: when set (by gemvq_profile on the calling thread), launchers start kernels through

@@ -205,23 +205,22 @@ __global__ __launch_bounds__(64) void gated_norm_kernel(GatedNormArgs a) {
 }
 
 // ---- attention core (one token, GQA, fp16 KV) ----
-// Workgroup (KV head, chunk of 64 positions), 256 threads; HD = head_dim, a power of two in [16, 256]. Every
-// global read of a phase is issued in one round (a dependent chain of global loads costs about a microsecond per
-// link, far more than the arithmetic here):
+// Workgroup (q head, chunk of 64 positions), 256 threads; HD = head_dim, a power of two in [16, 256]. The G q heads
+// of a KV head and chunk run on workgroups that are dealt to the same XCD, whose L2 then serves the chunk's keys and
+// values to all of them. Every global read of a phase is issued in one round (a dependent chain of global loads
+// costs about a microsecond per link, far more than the arithmetic here):
 //   1. the chunk's cached keys and values (thread t holds 16-byte piece t % (HD / 8) of rows t / (HD / 8) + k *
-//      (2048 / HD)), the q rows of the group's heads, the new key and value, the norm weights and the RoPE row;
-//   2. RMS norm with weight and NEOX RoPE of the q heads and the new key (element e in thread e), fp16 rounding;
-//      the new key and value go to the cache;
+//      (2048 / HD)), the head's q row, the new key and value, the norm weights and the RoPE row;
+//   2. RMS norm with weight and NEOX RoPE of q and the new key (element e in thread e), fp16 rounding; the first
+//      q head of the KV head stores the new key and value in the cache;
 //   3. scores from registers: 8 products and their adjacent tree in the thread, the tree over the HD / 8 pieces
 //      of a row across lanes (together the pairwise sum over head_dim), times scale;
-//   4. the chunk max per head, e^(s - max), then thread d sums p and p * v[d] over the positions in order for
-//      every head of the group and writes the partials (max, sum, o[hd]);
-//   5. the last workgroup of the KV head loads all chunks' partials (16 chunks per round), forms M = max m_c,
+//   4. the chunk max, e^(s - max), then thread d sums p and p * v[d] over the positions in order and writes the
+//      partials (max, sum, o[hd]);
+//   5. the last workgroup of the q head loads all chunks' partials (16 chunks per round), forms M = max m_c,
 //      f_c = e^(m_c - M), L = sum l_c f_c and O = sum o_c f_c in chunk order, and writes O / L times the sigmoid
 //      of the gate.
 constexpr int ATT_T = 256;
-constexpr int MAXHD = 256;
-constexpr int MAXG = 4;    // q heads per KV head
 constexpr int MAXCH = 64;  // chunks (n_ctx <= 4096)
 constexpr int CMB = 16;    // chunks per load round of the combine
 
@@ -231,15 +230,18 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
     constexpr int RPP = ATT_T / PER;               // rows per pass
     constexpr int NP = (ATTN_CHUNK + RPP - 1) / RPP;  // passes
     __shared__ __align__(16) uint16_t vs[ATTN_CHUNK * HD];
-    __shared__ __align__(16) float qs[MAXG + 1][HD];  // q heads and the new key: normalized, then rotated + rounded
-    __shared__ __align__(16) float pr[ATTN_CHUNK][MAXG];  // scores, then e^(s - max)
-    __shared__ float red[MAXG + 1][4];
-    __shared__ float mx[MAXG], fcs[MAXG][MAXCH], lcs[MAXG][MAXCH];
+    __shared__ __align__(16) float qs[2][HD];  // q and the new key: normalized, then rotated + rounded
+    __shared__ float pr[ATTN_CHUNK];           // scores, then e^(s - max)
+    __shared__ float red[2][4];
+    __shared__ float mx, fcs[MAXCH], lcs[MAXCH];
     __shared__ int last;
-    const int kvh = blockIdx.x % a.n_head_kv, chunk = blockIdx.x / a.n_head_kv;
+    // workgroup b: unit u = (KV head, chunk) with u % 8 == b % 8 (one XCD), q head g of the unit's KV head
+    const int G = a.n_head / a.n_head_kv, b = blockIdx.x;
+    const int u = (b / (8 * G)) * 8 + (b & 7), g = (b >> 3) % G;
+    const int kvh = u % a.n_head_kv, chunk = u / a.n_head_kv, hq = kvh * G + g;
     const int pos = *a.pos, nc = (pos + ATTN_CHUNK) / ATTN_CHUNK;
     if (pos < 0 || pos >= a.n_ctx || chunk >= nc) return;  // positions past the KV capacity are not stored
-    const int tid = threadIdx.x, G = a.n_head / a.n_head_kv, half = a.n_rot / 2;
+    const int tid = threadIdx.x, half = a.n_rot / 2;
     const int lane = tid & 63, wave = tid >> 6, pc = tid % PER;
     const int t0 = chunk * ATTN_CHUNK, nt = min(ATTN_CHUNK, pos + 1 - t0);
     const bool has_new = chunk == nc - 1;  // this chunk holds pos
@@ -253,13 +255,13 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
         vr[j] = *reinterpret_cast<const uint4 *>(a.vc + off);
     }
     const bool el = tid < HD;
-    const int e = el ? tid : 0;  // element of each head this thread holds
-    float xv[MAXG + 1];
-#pragma unroll
-    for (int g = 0; g < MAXG; ++g) xv[g] = (g < G && el) ? a.q[size_t(kvh * G + g) * a.q_stride + e] : 0.0f;
-    xv[MAXG] = (has_new && el) ? a.k[size_t(kvh) * HD + e] : 0.0f;
+    const int e = el ? tid : 0;  // element of the head this thread holds
+    float xv[2];
+    xv[0] = el ? a.q[size_t(hq) * a.q_stride + e] : 0.0f;
+    xv[1] = (has_new && el) ? a.k[size_t(kvh) * HD + e] : 0.0f;
     const float wq = a.qn[e], wk = a.kn[e];
     const float vv = has_new ? a.v[size_t(kvh) * HD + e] : 0.0f;
+    const float gt = a.gate ? a.gate[size_t(hq) * 2 * HD + e] : 0.0f;
     const int pi = e < half ? e : e - half;  // the RoPE pair of this element
     const bool rot = e < a.n_rot;
     const float cs0 = rot ? a.cs[size_t(pos) * a.n_rot + 2 * pi] : 0.0f;
@@ -270,175 +272,140 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
         if (ti < nt) *reinterpret_cast<uint4 *>(vs + ti * HD + pc * 8) = vr[j];
     }
     // ---- 2. norms (pairwise over head_dim), RoPE, fp16 rounding ----
-    float sq[MAXG + 1];
-#pragma unroll
-    for (int g = 0; g <= MAXG; ++g) sq[g] = xv[g] * xv[g];
-    pair_sum_lanes_n<64, MAXG + 1>(sq);
-    if (lane == 0)
-#pragma unroll
-        for (int g = 0; g <= MAXG; ++g) red[g][wave] = sq[g];
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g <= MAXG; ++g) {
-        const float sum = (red[g][0] + red[g][1]) + (red[g][2] + red[g][3]);
-        const float sc = 1.0f / sqrtf(sum / float(HD) + a.eps);
-        if (el) qs[g][e] = (xv[g] * sc) * (g < MAXG ? wq : wk);
+    float sq[2] = {xv[0] * xv[0], xv[1] * xv[1]};
+    pair_sum_lanes_n<64, 2>(sq);
+    if (lane == 0) {
+        red[0][wave] = sq[0];
+        red[1][wave] = sq[1];
     }
     __syncthreads();
-    float rv[MAXG + 1];
 #pragma unroll
-    for (int g = 0; g <= MAXG; ++g) {
-        const float x0 = qs[g][pi], x1 = qs[g][pi + half];
-        rv[g] = e < half ? x0 * cs0 - x1 * cs1 : (rot ? x0 * cs1 + x1 * cs0 : qs[g][e]);
+    for (int h = 0; h < 2; ++h) {
+        const float sum = (red[h][0] + red[h][1]) + (red[h][2] + red[h][3]);
+        const float sc = 1.0f / sqrtf(sum / float(HD) + a.eps);
+        if (el) qs[h][e] = (xv[h] * sc) * (h == 0 ? wq : wk);
+    }
+    __syncthreads();
+    float rv[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const float x0 = qs[h][pi], x1 = qs[h][pi + half];
+        rv[h] = e < half ? x0 * cs0 - x1 * cs1 : (rot ? x0 * cs1 + x1 * cs0 : qs[h][e]);
     }
     __syncthreads();
     if (el) {
-#pragma unroll
-        for (int g = 0; g <= MAXG; ++g) qs[g][e] = h2f(f2h(rv[g]));
+        qs[0][e] = h2f(f2h(rv[0]));
+        qs[1][e] = h2f(f2h(rv[1]));
         if (has_new) {
-            const uint32_t kb = f2h(rv[MAXG]), vb = f2h(vv);
+            const uint32_t kb = f2h(rv[1]), vb = f2h(vv);
             vs[(pos - t0) * HD + e] = uint16_t(vb);
-            const size_t off = (size_t(pos) * a.n_head_kv + kvh) * HD + e;
-            a.kc[off] = uint16_t(kb);
-            a.vc[off] = uint16_t(vb);
+            if (g == 0) {  // one q head per KV head stores the new key and value
+                const size_t off = (size_t(pos) * a.n_head_kv + kvh) * HD + e;
+                a.kc[off] = uint16_t(kb);
+                a.vc[off] = uint16_t(vb);
+            }
         }
     }
     __syncthreads();
     // ---- 3. scores ----
-    float qv[MAXG][8], kn[8];
+    float qv[8], kn[8];
 #pragma unroll
-    for (int g = 0; g < MAXG; ++g)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) qv[g][i] = qs[g][pc * 8 + i];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) kn[i] = qs[MAXG][pc * 8 + i];
-    float dots[NP][MAXG];
+    for (int i = 0; i < 8; ++i) {
+        qv[i] = qs[0][pc * 8 + i];
+        kn[i] = qs[1][pc * 8 + i];
+    }
+    float dots[NP];
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
         const bool is_new = t0 + tid / PER + j * RPP == pos;
         const uint32_t kw[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
-        float kf[8];
+        float t[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) kf[i] = is_new ? kn[i] : h2f((kw[i / 2] >> (16 * (i % 2))) & 0xffffu);
-#pragma unroll
-        for (int g = 0; g < MAXG; ++g) {
-            float t[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) t[i] = qv[g][i] * kf[i];
-            dots[j][g] = tree<8>(t);
-        }
+        for (int i = 0; i < 8; ++i) t[i] = qv[i] * (is_new ? kn[i] : h2f((kw[i / 2] >> (16 * (i % 2))) & 0xffffu));
+        dots[j] = tree<8>(t);
     }
-    pair_sum_lanes_n<PER, NP * MAXG>(&dots[0][0]);
+    pair_sum_lanes_n<PER, NP>(dots);
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
         const int ti = tid / PER + j * RPP;
-        if (pc == 0 && ti < nt)
-            *reinterpret_cast<float4 *>(pr[ti]) =
-                make_float4(dots[j][0] * a.scale, dots[j][1] * a.scale, dots[j][2] * a.scale, dots[j][3] * a.scale);
+        if (pc == 0 && ti < nt) pr[ti] = dots[j] * a.scale;
     }
     __syncthreads();
     // ---- 4. chunk softmax numerators, partial sums in position order ----
-    if (wave < G) {
-        const float sv = lane < nt ? pr[lane][wave] : -__builtin_inff();
+    if (wave == 0) {
+        const float sv = lane < nt ? pr[lane] : -__builtin_inff();
         float m = sv;
 #pragma unroll
         for (int st = 32; st >= 1; st >>= 1) m = fmaxf(m, __shfl_xor(m, st, WAVE));
-        if (lane < nt) pr[lane][wave] = expf_(sv - m);
-        if (lane == 0) mx[wave] = m;
+        if (lane < nt) pr[lane] = expf_(sv - m);
+        if (lane == 0) mx = m;
     }
     __syncthreads();
     const int pstride = 2 + HD, nchmax = (a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
     if (el) {
-        float o[MAXG] = {}, l[MAXG] = {};
+        float o = 0.0f, l = 0.0f;
 #pragma unroll 8
         for (int i = 0; i < nt; ++i) {
-            const float4 p4 = *reinterpret_cast<const float4 *>(pr[i]);
-            const float p[4] = {p4.x, p4.y, p4.z, p4.w};
-            const float v = h2f(vs[i * HD + e]);
-#pragma unroll
-            for (int g = 0; g < MAXG; ++g) {
-                l[g] += p[g];
-                o[g] += p[g] * v;
-            }
+            const float p = pr[i];
+            l += p;
+            o += p * h2f(vs[i * HD + e]);
         }
-#pragma unroll
-        for (int g = 0; g < MAXG; ++g) {
-            if (g >= G) break;
-            float * pp = a.part + (size_t(kvh * G + g) * nchmax + chunk) * pstride;
-            pp[2 + e] = o[g];
-            if (e == 0) {
-                pp[0] = mx[g];
-                pp[1] = l[g];
-            }
+        float * pp = a.part + (size_t(hq) * nchmax + chunk) * pstride;
+        pp[2 + e] = o;
+        if (e == 0) {
+            pp[0] = mx;
+            pp[1] = l;
         }
     }
     __syncthreads();
     if (tid == 0) {  // the partials are released (agent scope) by the counter update; the last workgroup acquires
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        last = atomicAdd(a.counter + kvh, 1u) == unsigned(nc - 1);
+        last = atomicAdd(a.counter + hq, 1u) == unsigned(nc - 1);
         if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
     if (!last) return;
-    // ---- 5. combine (last workgroup of the KV head) ----
-    const float * pk = a.part + size_t(kvh * G) * nchmax * pstride;
-    float gt[MAXG], ov[MAXG][CMB];
-#pragma unroll
-    for (int g = 0; g < MAXG; ++g)
-        gt[g] = (a.gate && g < G) ? a.gate[size_t(kvh * G + g) * 2 * HD + e] : 0.0f;
+    // ---- 5. combine (last workgroup of the q head) ----
+    const float * pk = a.part + size_t(hq) * nchmax * pstride;
+    float ov[CMB];
     float mc = -__builtin_inff(), lc = 0.0f;
-    if (wave < G && lane < nc) {
-        mc = __builtin_nontemporal_load(pk + (size_t(wave) * nchmax + lane) * pstride);
-        lc = __builtin_nontemporal_load(pk + (size_t(wave) * nchmax + lane) * pstride + 1);
+    if (wave == 0 && lane < nc) {
+        mc = __builtin_nontemporal_load(pk + size_t(lane) * pstride);
+        lc = __builtin_nontemporal_load(pk + size_t(lane) * pstride + 1);
     }
 #pragma unroll
-    for (int g = 0; g < MAXG; ++g)
-#pragma unroll
-        for (int c = 0; c < CMB; ++c)
-            ov[g][c] = (g < G && c < nc) ? __builtin_nontemporal_load(pk + (size_t(g) * nchmax + c) * pstride + 2 + e)
-                                         : 0.0f;
-    if (wave < G) {
+    for (int c = 0; c < CMB; ++c) ov[c] = c < nc ? __builtin_nontemporal_load(pk + size_t(c) * pstride + 2 + e) : 0.0f;
+    if (wave == 0) {
         float M = mc;
 #pragma unroll
         for (int st = 32; st >= 1; st >>= 1) M = fmaxf(M, __shfl_xor(M, st, WAVE));
         if (lane < nc) {
-            fcs[wave][lane] = expf_(mc - M);
-            lcs[wave][lane] = lc;
+            fcs[lane] = expf_(mc - M);
+            lcs[lane] = lc;
         }
     }
     __syncthreads();
-    float O[MAXG] = {}, L[MAXG] = {};
+    float O = 0.0f, L = 0.0f;
     for (int c0 = 0;;) {
 #pragma unroll
         for (int c = 0; c < CMB; ++c) {
             if (c0 + c >= nc) break;
-#pragma unroll
-            for (int g = 0; g < MAXG; ++g) {
-                const float f = fcs[g][c0 + c];
-                L[g] += lcs[g][c0 + c] * f;
-                O[g] += ov[g][c] * f;
-            }
+            const float f = fcs[c0 + c];
+            L += lcs[c0 + c] * f;
+            O += ov[c] * f;
         }
         c0 += CMB;
         if (c0 >= nc) break;
 #pragma unroll
-        for (int g = 0; g < MAXG; ++g)
-#pragma unroll
-            for (int c = 0; c < CMB; ++c)
-                ov[g][c] = (g < G && c0 + c < nc)
-                               ? __builtin_nontemporal_load(pk + (size_t(g) * nchmax + c0 + c) * pstride + 2 + e)
-                               : 0.0f;
+        for (int c = 0; c < CMB; ++c)
+            ov[c] = c0 + c < nc ? __builtin_nontemporal_load(pk + size_t(c0 + c) * pstride + 2 + e) : 0.0f;
     }
     if (el) {
-#pragma unroll
-        for (int g = 0; g < MAXG; ++g) {
-            if (g >= G) break;
-            float out = O[g] / L[g];
-            if (a.gate) out = (1.0f / (1.0f + expf_(-gt[g]))) * out;
-            a.y[size_t(kvh * G + g) * HD + e] = out;
-        }
+        float out = O / L;
+        if (a.gate) out = (1.0f / (1.0f + expf_(-gt))) * out;
+        a.y[size_t(hq) * HD + e] = out;
     }
-    if (tid == 0) a.counter[kvh] = 0u;
+    if (tid == 0) a.counter[hq] = 0u;
 }
 
 // ---- embedding rows (ggml dequantize_row_*) ----
@@ -542,9 +509,12 @@ hipError_t launch_gated_norm(const GatedNormArgs & a, hipStream_t s) {
 }
 
 hipError_t launch_attn(const AttnArgs & a, hipStream_t s) {
-    if (a.n_head % a.n_head_kv || a.n_head / a.n_head_kv > MAXG || (a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK > MAXCH)
+    if (a.n_head % a.n_head_kv || a.n_head / a.n_head_kv > ATTN_MAXG || (a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK > MAXCH)
         return hipErrorInvalidValue;
-    const dim3 grid(a.n_head_kv * ((a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK));
+    // units (KV head, chunk) in groups of 8, each group followed by its q heads: workgroup b serves unit
+    // (b / (8 G)) 8 + b % 8 (units past the last are idle) and q head (b / 8) % G of its KV head
+    const int units = a.n_head_kv * ((a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK);
+    const dim3 grid(((units + 7) / 8) * 8 * (a.n_head / a.n_head_kv));
     switch (a.head_dim) {
     case 16: GQ_LAUNCH(attn_kernel<16>, grid, dim3(ATT_T), 0, s, a); break;
     case 32: GQ_LAUNCH(attn_kernel<32>, grid, dim3(ATT_T), 0, s, a); break;

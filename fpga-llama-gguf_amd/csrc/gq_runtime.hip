@@ -808,10 +808,10 @@ int gemvq_kv_create(gemvq_ctx * c, int n_ctx, int n_head_kv, int head_dim) {
     hipError_t e = hipMalloc(&b.k, kvn * 2);
     if (e == hipSuccess) e = hipMalloc(&b.v, kvn * 2);
     if (e == hipSuccess) e = hipMalloc(&b.part, partn * 4);
-    if (e == hipSuccess) e = hipMalloc(&b.counter, size_t(n_head_kv) * 4);
+    if (e == hipSuccess) e = hipMalloc(&b.counter, size_t(n_head_kv) * ATTN_MAXG * 4);
     if (e == hipSuccess) e = hipMemset(b.k, 0, kvn * 2);
     if (e == hipSuccess) e = hipMemset(b.v, 0, kvn * 2);
-    if (e == hipSuccess) e = hipMemset(b.counter, 0, size_t(n_head_kv) * 4);
+    if (e == hipSuccess) e = hipMemset(b.counter, 0, size_t(n_head_kv) * ATTN_MAXG * 4);
     if (e != hipSuccess) {
         hipFree(b.k);
         hipFree(b.v);
@@ -844,7 +844,7 @@ int gemvq_kv_clear(gemvq_ctx * c) {
         const size_t kvn = size_t(b.n_ctx) * b.n_head_kv * b.head_dim;
         if (e == hipSuccess) e = hipMemsetAsync(b.k, 0, kvn * 2, c->stream);
         if (e == hipSuccess) e = hipMemsetAsync(b.v, 0, kvn * 2, c->stream);
-        if (e == hipSuccess) e = hipMemsetAsync(b.counter, 0, size_t(b.n_head_kv) * 4, c->stream);
+        if (e == hipSuccess) e = hipMemsetAsync(b.counter, 0, size_t(b.n_head_kv) * ATTN_MAXG * 4, c->stream);
     }
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     return e == hipSuccess ? 0 : fail(c, e, "kv clear");
