@@ -1,944 +1,24 @@
-// Fused GEMV pass for gfx950 (the GEMV command and its groups and epilogs, fpga/src/gemvqc16.h:26-45).
-//
-// One workgroup of 4 waves. The prologue quantizes the activation once into LDS exactly as ggml does for the
-// weight type (Q8_0 for Q4_0 / Q8_0, Q8_K for Q5_K / Q6_K), optionally folding a deferred RMS norm into the values
-// it quantizes. Each wave then streams whole rows: lane l owns the units u = l + 64k of every row (a unit is one
-// 32-weight block for Q4_0 / Q8_0, 64 weights for the K-quants) and keeps their activations in registers. Block
-// dots are int8 v_dot4 sums; each block (super-block) term is exact and truncated to the fixed-point LSB 2^-40
-// (the reference kernel's arithmetic, gemvqw_engine.h:352-445), so the int64 row sum does not depend on the lane
-// or reduction order, and is rounded to FP32 once. Epilogs (SwiGLU pair, residual add, conv, argmax) run on the
-// row result before it is stored.
-#include "gq_device.h"
+// GEMV dispatch by weight type (the instances live in gq_gemv_q4_0 / _q4_1 / _q8_0 / _kq.hip, compiled apart).
 #include "gq_kernels.h"
 
 namespace gq {
-namespace {
 
-constexpr int NT = 256;        // threads per workgroup
-constexpr int NWAVES = NT / WAVE;
-constexpr int MAXK = 16384;
-
-struct Lds {
-    int8_t xq[MAXK];           // quantized activation
-    uint32_t info[MAXK / 32];  // Q8_0: fp16 scale | (sum of the block's quants) << 16; Q8_K: FP32 d bits per super-block
-    int16_t bs[MAXK / 16];     // Q8_K bsums
-    uint16_t s1[MAXK / 32];    // Q8_1: fp16 of (sum of the block's quants) * d, for Q4_1 weights
-    float red[2 * NWAVES + 64];
-    unsigned long long key[NWAVES];
-};
-
-// Canonical norm scale over n floats (pairwise tree of the squares; words of 16 floats per thread, 256 words per
-// round, rounds combined pairwise with zero padding).
-__device__ float block_norm_scale(const float * x, int n, float eps, int l2, Lds & s) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nw = n / 16, rounds = (nw + NT - 1) / NT;  // n <= 16384: at most 4 rounds
-    float rs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        if (g < rounds) {  // uniform over the workgroup
-        const int w = g * NT + tid;
-        float ws = 0.0f;
-        if (w < nw) {
-            const float4 * p = reinterpret_cast<const float4 *>(x + size_t(w) * 16);
-            float sq[16];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4 v = p[i];
-                sq[4 * i] = v.x * v.x;
-                sq[4 * i + 1] = v.y * v.y;
-                sq[4 * i + 2] = v.z * v.z;
-                sq[4 * i + 3] = v.w * v.w;
-            }
-            ws = tree<16>(sq);
-        }
-        ws = pair_sum_lanes<64>(ws);
-        if (lane == 0) s.red[wave] = ws;
-        __syncthreads();
-        rs[g] = (s.red[0] + s.red[1]) + (s.red[2] + s.red[3]);
-        __syncthreads();
-        }
-    }
-    // pairwise over the rounds; absent rounds are +0 and leave the tree's values unchanged
-    const float sum = (rs[0] + rs[1]) + (rs[2] + rs[3]);
-    return l2 ? 1.0f / fmaxf(sqrtf(sum), eps) : 1.0f / sqrtf(sum / float(n) + eps);
-}
-
-// Q8_0 of the activation (gemvq_ref.h:236-245) on half-blocks: thread t holds items t + 256 g (an item is 16
-// consecutive floats; the two halves of a 32-block sit in adjacent lanes). The loads are issued by prologue_fetch
-// before the first weight rows are requested, so they are not queued behind them; prologue_finish then folds the
-// deferred norm or the gated output norm and quantizes into LDS.
-template <int R, bool GATED>  // rounds of 256 items the registers hold (cols <= 4096 R); the gated output norm
-struct XF {
-    float v[R][16];
-    float w[R <= 2 ? R : 1][16];  // NORM: the norm weight (the activation again without one); GATED: the gated norm's
-                                  // weight (one head, item % 8)
-    float z[GATED ? R : 1][16];   // GATED: the output gate
-};
-
-__device__ __forceinline__ void load16(const float * p, float * v) {
-    const float4 * q = reinterpret_cast<const float4 *>(p);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float4 t = q[i];
-        v[4 * i] = t.x;
-        v[4 * i + 1] = t.y;
-        v[4 * i + 2] = t.z;
-        v[4 * i + 3] = t.w;
-    }
-}
-
-// Item index clamped into the vector (threads past the end load a valid item and store nothing).
-__device__ __forceinline__ int item_of(int g, int n16) {
-    const int i = int(threadIdx.x) + NT * g;
-    return i < n16 ? i : n16 - 1;
-}
-
-// Every load is unconditional (an operand a source does not use is read from the activation itself), so the loads
-// cannot be moved into the branches that use them, behind the weight loads.
-template <int R, bool GATED>
-__device__ __forceinline__ void prologue_fetch(const GemvArgs & a, XF<R, GATED> & f) {
-    const int n16 = a.cols / 16;
-    const bool normw = a.xsrc == XSRC_NORM && a.norm_w != nullptr;
-#pragma unroll
-    for (int g = 0; g < R; ++g) {
-        const int i = item_of(g, n16);
-        const float * xi = a.x + size_t(i) * 16;
-        load16(xi, f.v[g]);
-        if constexpr (GATED) {
-            load16(a.gate_z + size_t(i) * 16, f.z[g]);
-            load16(a.norm_w + size_t(i & 7) * 16, f.w[g]);
-        } else if constexpr (R <= 2) {
-            load16(normw ? a.norm_w + size_t(i) * 16 : xi, f.w[g]);
-        }
-    }
-}
-
-// Q8_0 of one 32-block held as two halves by lanes l and l ^ 1: d = amax / 127 over the block, q = round(v / d)
-// (half away from zero), the block's quant sum, and for Q4_1 weights the Q8_1 s = fp16(sum * d).
-__device__ __forceinline__ void quantize_half(const float * v, int item, bool valid, Lds & s) {
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(v[j]));
-    amax = fmaxf(amax, dpp_f32<DPP_XOR1>(amax));
-    const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
-    uint32_t packed[4];
-    int sum = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        uint32_t w = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            // roundf (half away from zero) as y + copysign(0.5 - 2^-25, y) truncated: equal for every |y| <= 128,
-            // and |y| <= 127 (1 + 2^-22) here
-            const float y = v[4 * i + j] * id;
-            const int q = int(y + copysignf(0.49999997f, y));
-            sum += q;
-            w |= (uint32_t(q) & 0xffu) << (8 * j);
-        }
-        packed[i] = w;
-    }
-    sum += __shfl_xor(sum, 1, WAVE);
-    if (valid) {
-        *reinterpret_cast<uint4 *>(s.xq + size_t(item) * 16) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-        if ((item & 1) == 0) {
-            s.info[item >> 1] = f2h(d) | (uint32_t(sum & 0xffff) << 16);
-            s.s1[item >> 1] = uint16_t(f2h(float(sum) * d));  // ggml quantize_row_q8_1: s = fp16(sum * d), FP32 d
-        }
-    }
-}
-
-// Norm scale over the whole vector: tree over each item's 16 squares, pairwise over the 64 items of a wave, the 4
-// waves of a round and the rounds (padded to a power of two with zeros): the canonical pairwise tree over n.
-template <int R, bool GATED>
-__device__ __forceinline__ float norm_scale_items(const GemvArgs & a, const XF<R, GATED> & f, Lds & s) {
-    const int n16 = a.cols / 16, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    float r[R];
-#pragma unroll
-    for (int g = 0; g < R; ++g) {
-        float sq[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) sq[j] = f.v[g][j] * f.v[g][j];
-        r[g] = int(threadIdx.x) + NT * g < n16 ? tree<16>(sq) : 0.0f;
-    }
-    pair_sum_lanes_n<64, R>(r);
-    if (lane == 0) {
-#pragma unroll
-        for (int g = 0; g < R; ++g) s.red[NWAVES * g + wave] = r[g];
-    }
-    __syncthreads();
-    float rs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int g = 0; g < R; ++g)
-        rs[g] = (s.red[NWAVES * g] + s.red[NWAVES * g + 1]) + (s.red[NWAVES * g + 2] + s.red[NWAVES * g + 3]);
-    const float sum = R == 1 ? rs[0] : R == 2 ? rs[0] + rs[1] : (rs[0] + rs[1]) + (rs[2] + rs[3]);
-    return a.norm_l2 ? 1.0f / fmaxf(sqrtf(sum), a.norm_eps) : 1.0f / sqrtf(sum / float(a.cols) + a.norm_eps);
-}
-
-// Without the gated norm the three sources share one path: v = (x * scale) * w with scale and w exactly 1 where a
-// source has no norm or no weight (x * 1 is x), so no branch separates the loads.
-template <int R, bool GATED>
-__device__ __forceinline__ void prologue_finish(const GemvArgs & a, XF<R, GATED> & f, Lds & s) {
-    const int n16 = a.cols / 16;
-    if constexpr (GATED) {
-        // the DeltaNet gated output norm (gemvqc_gdn.h:284-346): per head of 128 (8 items, 8 lanes), x =
-        // silu(z) * ((y * sc) * w) with sc = 1 / sqrt(sum(y^2) / 128 + eps); workgroup 0 also stores x, which the
-        // separate norm would have written
-        float hs[R];
-#pragma unroll
-        for (int g = 0; g < R; ++g) {
-            float sq[16];
-#pragma unroll
-            for (int j = 0; j < 16; ++j) sq[j] = f.v[g][j] * f.v[g][j];
-            hs[g] = tree<16>(sq);
-        }
-        pair_sum_lanes_n<8, R>(hs);
-#pragma unroll
-        for (int g = 0; g < R; ++g) {
-            const float sc = 1.0f / sqrtf(hs[g] / 128.0f + a.norm_eps);
-            float * v = f.v[g];
-            if (a.gate_silu) {
-#pragma unroll
-                for (int j = 0; j < 16; ++j) v[j] = f.z[g][j] * ((v[j] * sc) * f.w[g][j]);
-            } else {
-#pragma unroll
-                for (int j = 0; j < 16; ++j) v[j] = silu_(f.z[g][j]) * ((v[j] * sc) * f.w[g][j]);
-            }
-            const int i = int(threadIdx.x) + NT * g;
-            if (blockIdx.x == 0 && i < n16) {
-                float4 * o = reinterpret_cast<float4 *>(a.x_out + size_t(i) * 16);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) o[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
-            }
-            quantize_half(v, i, i < n16, s);
-        }
-    } else {
-        const bool norm = a.xsrc == XSRC_NORM, normw = norm && a.norm_w != nullptr;
-        const float sc = norm ? norm_scale_items<R, GATED>(a, f, s) : 1.0f;  // the same on every thread
-#pragma unroll
-        for (int g = 0; g < R; ++g) {
-            const int i = int(threadIdx.x) + NT * g;
-            float * v = f.v[g];
-            if constexpr (R <= 2) {
-#pragma unroll
-                for (int j = 0; j < 16; ++j) v[j] = (v[j] * sc) * (normw ? f.w[g][j] : 1.0f);
-            } else if (normw) {  // wide vectors: the weight is read now (registers hold only the activation)
-                float w[16];
-                load16(a.norm_w + size_t(item_of(g, n16)) * 16, w);
-#pragma unroll
-                for (int j = 0; j < 16; ++j) v[j] = (v[j] * sc) * w[j];
-            } else {
-#pragma unroll
-                for (int j = 0; j < 16; ++j) v[j] = v[j] * sc;
-            }
-            quantize_half(v, i, i < n16, s);
-        }
-    }
-}
-
-// Q8_K of the activation (gemvq_ref.h:62-81): one wave per 256-block, 4 values per lane; the signed value of the
-// largest magnitude at the first index; bsums per 16.
-__device__ void quantize_q8_K(const GemvArgs & a, float scale, Lds & s) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nsb = a.cols / 256;
-    for (int sb = wave; sb < nsb; sb += NWAVES) {
-        const int base = sb * 256 + lane * 4;
-        const float4 t = *reinterpret_cast<const float4 *>(a.x + base);
-        float v[4] = {t.x, t.y, t.z, t.w};
-        if (a.xsrc == XSRC_NORM) {
-            if (a.norm_w) {
-                const float4 w = *reinterpret_cast<const float4 *>(a.norm_w + base);
-                v[0] = (v[0] * scale) * w.x;
-                v[1] = (v[1] * scale) * w.y;
-                v[2] = (v[2] * scale) * w.z;
-                v[3] = (v[3] * scale) * w.w;
-            } else {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) v[j] = v[j] * scale;
-            }
-        }
-        float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-#pragma unroll
-        for (int st = 32; st >= 1; st >>= 1) amax = fmaxf(amax, __shfl_xor(amax, st, WAVE));
-        int cand = 1 << 20;
-#pragma unroll
-        for (int j = 3; j >= 0; --j)
-            if (fabsf(v[j]) == amax) cand = lane * 4 + j;
-#pragma unroll
-        for (int st = 32; st >= 1; st >>= 1) cand = min(cand, __shfl_xor(cand, st, WAVE));
-        float vmax = 0.0f;
-        {
-            const int src = (cand >> 2) & 63, j = cand & 3;
-            const float c0 = __shfl(v[0], src, WAVE), c1 = __shfl(v[1], src, WAVE), c2 = __shfl(v[2], src, WAVE),
-                        c3 = __shfl(v[3], src, WAVE);
-            vmax = j == 0 ? c0 : j == 1 ? c1 : j == 2 ? c2 : c3;
-        }
-        uint32_t packed = 0;
-        int part = 0;
-        float d = 0.0f;
-        if (amax != 0.0f) {
-            const float iscale = -127.0f / vmax;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float biased = iscale * v[j] + 12582912.0f;
-                int q = int(__float_as_uint(biased) & 0x007fffffu) - 0x00400000;
-                q = q < 127 ? q : 127;
-                part += q;
-                packed |= (uint32_t(q) & 0xffu) << (8 * j);
-            }
-            d = 1.0f / iscale;
-        }
-        *reinterpret_cast<uint32_t *>(s.xq + base) = packed;
-        part += __shfl_xor(part, 1, WAVE);
-        part += __shfl_xor(part, 2, WAVE);
-        if ((lane & 3) == 0) s.bs[sb * 16 + (lane >> 2)] = int16_t(part);
-        if (lane == 0) s.info[sb] = __float_as_uint(d);
-    }
-}
-
-// ---- per-lane activation slices ----
-struct XB {  // one 32-block (Q4_0 / Q4_1 / Q8_0)
-    uint32_t q[8];
-    float dx40;  // the block's fp16 scale times 2^40 (exact)
-    int sum;     // sum of its quants (for the Q4_0 offset of 8)
-    float sx40;  // Q4_1: the block's fp16 s (Q8_1) times 2^40 (exact)
-};
-struct XK {  // one 64-weight unit (Q5_K / Q6_K)
-    uint32_t q[16];
-    int bs[4];
-    int m, e, neg;
-};
-
-// Lanes past the last block hold a zero block (zero quants and scales), whose terms are exactly zero.
-template <int TYPE>
-__device__ __forceinline__ void load_xb(const Lds & s, int b, int nb, XB & x) {
-    const bool in = b < nb;
-    b = in ? b : nb - 1;
-    const uint4 * p = reinterpret_cast<const uint4 *>(s.xq + size_t(b) * 32);
-    const uint4 lo = p[0], hi = p[1];
-    x.q[0] = lo.x; x.q[1] = lo.y; x.q[2] = lo.z; x.q[3] = lo.w;
-    x.q[4] = hi.x; x.q[5] = hi.y; x.q[6] = hi.z; x.q[7] = hi.w;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) x.q[i] = in ? x.q[i] : 0u;
-    const uint32_t inf = in ? s.info[b] : 0u;
-    x.dx40 = h2f(inf & 0xffffu) * 1099511627776.0f;  // * 2^40
-    x.sum = int(int16_t(inf >> 16));
-    x.sx40 = TYPE == T_Q4_1 && in ? h2f(s.s1[b]) * 1099511627776.0f : 0.0f;
-}
-
-template <int TYPE>
-__device__ __forceinline__ void load_xk(const Lds & s, int u, int nu, XK & x) {
-    u = u < nu ? u : nu - 1;
-    const int sb = u >> 2, part = u & 3;
-    int off0, off1, g0, g1;
-    if (TYPE == T_Q6_K) {
-        const int n = part >> 1, p = part & 1;
-        off0 = sb * 256 + 128 * n + 32 * p;
-        off1 = off0 + 64;
-        g0 = (128 * n + 32 * p) / 16;
-        g1 = g0 + 4;
-    } else {
-        off0 = sb * 256 + 64 * part;
-        off1 = off0 + 32;
-        g0 = (64 * part) / 16;
-        g1 = g0 + 2;
-    }
-    const uint4 * p0 = reinterpret_cast<const uint4 *>(s.xq + off0);
-    const uint4 * p1 = reinterpret_cast<const uint4 *>(s.xq + off1);
-    const uint4 a0 = p0[0], a1 = p0[1], b0 = p1[0], b1 = p1[1];
-    x.q[0] = a0.x; x.q[1] = a0.y; x.q[2] = a0.z; x.q[3] = a0.w;
-    x.q[4] = a1.x; x.q[5] = a1.y; x.q[6] = a1.z; x.q[7] = a1.w;
-    x.q[8] = b0.x; x.q[9] = b0.y; x.q[10] = b0.z; x.q[11] = b0.w;
-    x.q[12] = b1.x; x.q[13] = b1.y; x.q[14] = b1.z; x.q[15] = b1.w;
-    x.bs[0] = s.bs[sb * 16 + g0];
-    x.bs[1] = s.bs[sb * 16 + g0 + 1];
-    x.bs[2] = s.bs[sb * 16 + g1];
-    x.bs[3] = s.bs[sb * 16 + g1 + 1];
-    const float d = __uint_as_float(s.info[sb]);
-    float_parts(d, x.m, x.e);
-    x.neg = d < 0.0f;
-}
-
-// ---- weight loads and unit dots ----
-struct WB {  // one 32-block: Q4_0 / Q4_1 use lo (16 quant bytes), Q8_0 lo and hi (32 quant bytes)
-    uint4 lo, hi;
-    uint32_t d;  // fp16 d (Q4_1: d | m << 16)
-};
-struct WK {  // one 64-weight K-quant unit
-    uint4 a0, a1;         // Q6_K ql bytes / Q5_K qs bytes of the unit
-    uint4 h0, h1;         // high-bit bytes
-    uint32_t s0, s1, s2;  // Q6_K: scale byte pairs of groups A and B; Q5_K: the 12 packed scale bytes
-    uint32_t d;           // Q6_K: d; Q5_K: d | dmin << 16
-};
-
-// Weight loads are non-temporal: each byte is read once per token, so the stream should not displace what L2 holds
-// for reuse (activations, states, the KV cache).
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 ld16(const uint8_t * p) {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ uint32_t ld2(const uint8_t * p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p));
-}
-__device__ __forceinline__ uint32_t ld4(const uint8_t * p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
-}
-
-template <int TYPE>
-__device__ __forceinline__ void load_wb(const WeightView & w, size_t idx, WB & o) {
-    o.lo = ld16(w.a + idx * 16);
-    if (TYPE == T_Q4_0) {
-        o.d = ld2(w.b + idx * 2);
-    } else if (TYPE == T_Q4_1) {
-        o.d = ld4(w.b + idx * 4);
-    } else {
-        o.hi = ld16(w.b + idx * 16);
-        o.d = ld2(w.c + idx * 2);
-    }
-}
-
-// Integer block sum (gemvq_ref.h:250-257, 218-220): Q4_0 (nibble - 8), Q4_1 (nibble) or Q8_0 weights times the
-// Q8_0 / Q8_1 activation block.
-template <int TYPE>
-__device__ __forceinline__ int dot_block(const WB & w, const XB & x) {
-    int s = 0;
-    if (TYPE == T_Q4_1) {
-        const uint32_t q[4] = {w.lo.x, w.lo.y, w.lo.z, w.lo.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s = sdot4(q[i] & 0x0F0F0F0Fu, x.q[i], s);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s = sdot4((q[i] >> 4) & 0x0F0F0F0Fu, x.q[4 + i], s);
-    } else if (TYPE == T_Q4_0) {
-        const uint32_t q[4] = {w.lo.x, w.lo.y, w.lo.z, w.lo.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s = sdot4(q[i] & 0x0F0F0F0Fu, x.q[i], s);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s = sdot4((q[i] >> 4) & 0x0F0F0F0Fu, x.q[4 + i], s);
-        s -= 8 * x.sum;
-    } else {
-        const uint32_t q[8] = {w.lo.x, w.lo.y, w.lo.z, w.lo.w, w.hi.x, w.hi.y, w.hi.z, w.hi.w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) s = sdot4(q[i], x.q[i], s);
-    }
-    return s;
-}
-
-// floor(sumi * dw * dx * 2^40) (gemvqw_engine.h:417-427) as an integer-valued double: dw * dx * 2^40 is exact in
-// FP32 (two 11-bit significands), its product with the 20-bit sumi exact in FP64, floor exact.
-template <int TYPE>
-__device__ __forceinline__ double block_term(int sumi, uint32_t dw, const XB & x) {
-    const float s = float(__builtin_bit_cast(_Float16, uint16_t(dw))) * x.dx40;  // exact conversion
-    const double t = floor(double(sumi) * double(s));
-    if (TYPE != T_Q4_1) return t;
-    // Q4_1: + floor(m * s_x * 2^40), the product of two fp16 values exact in FP32
-    const float ms = float(__builtin_bit_cast(_Float16, uint16_t(dw >> 16))) * x.sx40;
-    return t + floor(double(ms));
-}
-
-template <int TYPE>
-__device__ __forceinline__ void load_wk(const WeightView & w, size_t sbi, int part, WK & o) {
-    if (TYPE == T_Q6_K) {
-        const int n = part >> 1, p = part & 1;
-        const uint8_t * ql = w.a + sbi * 128 + 64 * n + 32 * p;
-        const uint8_t * qh = w.b + sbi * 64 + 32 * n;
-        o.a0 = ld16(ql);
-        o.a1 = ld16(ql + 16);
-        o.h0 = ld16(qh);
-        o.h1 = ld16(qh + 16);
-        const uint8_t * sc = w.c + sbi * 16;
-        o.s0 = ld2(sc + 8 * n + 2 * p);
-        o.s1 = ld2(sc + 8 * n + 4 + 2 * p);
-        o.s2 = 0;
-        o.d = ld2(w.d + sbi * 2);
-    } else {
-        const uint8_t * qs = w.a + sbi * 128 + 32 * part;
-        const uint8_t * qh = w.b + sbi * 32;
-        o.a0 = ld16(qs);
-        o.a1 = ld16(qs + 16);
-        o.h0 = ld16(qh);
-        o.h1 = ld16(qh + 16);
-        const uint4 meta = ld16(w.c + sbi * 16);
-        o.d = meta.x;
-        o.s0 = meta.y;
-        o.s1 = meta.z;
-        o.s2 = meta.w;
-    }
-}
-
-__device__ __forceinline__ uint32_t pick(const uint4 & v, int i) {
-    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
-}
-
-// Scale bytes of a Q5_K super-block (6-bit scale and min of sub-block j, gemvq_ref.h:84-92).
-__device__ __forceinline__ int sbyte(const WK & w, int i) {
-    const uint32_t v = i < 4 ? w.s0 : i < 8 ? w.s1 : w.s2;
-    return int((v >> (8 * (i & 3))) & 0xffu);
-}
-__device__ __forceinline__ void scale_min_k4(const WK & w, int j, int & sc, int & m) {
-    if (j < 4) {
-        sc = sbyte(w, j) & 63;
-        m = sbyte(w, j + 4) & 63;
-    } else {
-        sc = (sbyte(w, j + 4) & 0xF) | ((sbyte(w, j - 4) >> 6) << 4);
-        m = (sbyte(w, j + 4) >> 4) | ((sbyte(w, j) >> 6) << 4);
-    }
-}
-
-// Integer sums of one unit: S = sum sc * (q . q8), M = sum m * bsum (gemvq_ref.h:95-192).
-template <int TYPE>
-__device__ __forceinline__ void dot_unit(const WK & w, const XK & x, int part, int & S, int & M) {
-    if (TYPE == T_Q6_K) {
-        const int p = part & 1;
-        int dA0 = 0, dA1 = 0, dB0 = 0, dB1 = 0;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t ql = pick(i < 4 ? w.a0 : w.a1, i & 3), qh = pick(i < 4 ? w.h0 : w.h1, i & 3);
-            const uint32_t qa = (ql & 0x0F0F0F0Fu) | (((qh >> (2 * p)) & 0x03030303u) << 4);
-            const uint32_t qb = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * p + 4)) & 0x03030303u) << 4);
-            if (i < 4) {
-                dA0 = sdot4(qa, x.q[i], dA0);
-                dB0 = sdot4(qb, x.q[8 + i], dB0);
-            } else {
-                dA1 = sdot4(qa, x.q[i], dA1);
-                dB1 = sdot4(qb, x.q[8 + i], dB1);
-            }
-        }
-        const int scA0 = int(int8_t(w.s0 & 0xff)), scA1 = int(int8_t((w.s0 >> 8) & 0xff));
-        const int scB0 = int(int8_t(w.s1 & 0xff)), scB1 = int(int8_t((w.s1 >> 8) & 0xff));
-        S = scA0 * (dA0 - 32 * x.bs[0]) + scA1 * (dA1 - 32 * x.bs[1]) + scB0 * (dB0 - 32 * x.bs[2]) +
-            scB1 * (dB1 - 32 * x.bs[3]);
-        M = 0;
-    } else {
-        const int j = part;
-        int d0 = 0, d1 = 0;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t qs = pick(i < 4 ? w.a0 : w.a1, i & 3), qh = pick(i < 4 ? w.h0 : w.h1, i & 3);
-            const uint32_t q0 = (qs & 0x0F0F0F0Fu) | (((qh >> (2 * j)) & 0x01010101u) << 4);
-            const uint32_t q1 = ((qs >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * j + 1)) & 0x01010101u) << 4);
-            d0 = sdot4(q0, x.q[i], d0);
-            d1 = sdot4(q1, x.q[8 + i], d1);
-        }
-        int sc0, m0, sc1, m1;
-        scale_min_k4(w, 2 * j, sc0, m0);
-        scale_min_k4(w, 2 * j + 1, sc1, m1);
-        S = sc0 * d0 + sc1 * d1;
-        M = m0 * (x.bs[0] + x.bs[1]) + m1 * (x.bs[2] + x.bs[3]);
-    }
-}
-
-// floor(S * d * dx * 2^40) - floor(M * dmin * dx * 2^40) (gemvqw_engine.h:429-444), exact in int64 (the FP32 dx
-// has a 24-bit significand, so these products do not fit a double).
-template <int TYPE>
-__device__ __forceinline__ long long superblock_term(int S, int M, const WK & w, const XK & x) {
-    int md, ed;
-    half_parts(w.d & 0xffffu, md, ed);
-    const int negs = int((w.d >> 15) & 1) ^ x.neg;
-    const long long ps = (long long)(negs ? -S : S) * ((long long)md * (long long)x.m);
-    long long t = fixed_term(ps, ed + x.e);
-    if (TYPE == T_Q5_K) {
-        int mm, em;
-        half_parts(w.d >> 16, mm, em);
-        const int negm = int((w.d >> 31) & 1) ^ x.neg;
-        const long long pm = (long long)(negm ? -M : M) * ((long long)mm * (long long)x.m);
-        t -= fixed_term(pm, em + x.e);
-    }
-    return t;
-}
-
-// ---- rows: a wave owns a range of rows of one member and keeps D of them in flight ----
-// Per-row register cost decides D (1 to 4): the weight slots of D rows stay near 64 VGPRs.
-template <int TYPE, int NU, bool PAIR>
-constexpr int slots() {
-    const int per = (TYPE == T_Q5_K || TYPE == T_Q6_K ? 20 : TYPE == T_Q8_0 ? 9 : 5) * NU * (PAIR ? 2 : 1);
-    const int d = 64 / per;
-    return d < 1 ? 1 : d > 4 ? 4 : d;
-}
-
-template <int TYPE, int NU, bool PAIR>
-struct Slot {  // one row in flight
-    static constexpr bool KQ = TYPE == T_Q5_K || TYPE == T_Q6_K;
-    WB wb[KQ ? 1 : NU], wb2[(KQ || !PAIR) ? 1 : NU];  // g (or the matrix) and u of a SwiGLU pair
-    WK wk[KQ ? NU : 1], wk2[(KQ && PAIR) ? NU : 1];
-    float e;  // epilog operands: ADD residual (every lane); CONV: lanes 0-2 the state, lanes 3-6 the kernel
-};
-
-// Loads of row r: the same code for every epilog kind, so that no branch surrounds a load (a load behind a branch
-// makes the waits after the branch count it conservatively). The second matrix of a pair kernel is the member's own
-// matrix for members that are not SwiGLU, and the epilog operand address (ea/eb, set at launch) falls back to the
-// row's output for kinds without one.
-template <int TYPE, int NU, bool PAIR>
-__device__ __forceinline__ void load_slot(const GemvMember & m, int r, int lane, int nb, int nu, Slot<TYPE, NU, PAIR> & o) {
-    if constexpr (Slot<TYPE, NU, PAIR>::KQ) {
-        const int nsb = nu >> 2;
-#pragma unroll
-        for (int k = 0; k < NU; ++k) {
-            const int u0 = lane + 64 * k, u = u0 < nu ? u0 : nu - 1;
-            load_wk<TYPE>(m.w, size_t(r) * nsb + (u >> 2), u & 3, o.wk[k]);
-            if constexpr (PAIR) load_wk<TYPE>(m.w2, size_t(r) * nsb + (u >> 2), u & 3, o.wk2[k]);
-        }
-    } else {
-#pragma unroll
-        for (int k = 0; k < NU; ++k) {
-            const int b = lane + 64 * k, bb = b < nb ? b : nb - 1;
-            load_wb<TYPE>(m.w, size_t(r) * nb + bb, o.wb[k]);
-            if constexpr (PAIR) load_wb<TYPE>(m.w2, size_t(r) * nb + bb, o.wb2[k]);
-        }
-    }
-    const int l = (lane < 7 ? lane : 6) * m.e_lane;
-    const float * pa = m.ea + (size_t(r) * m.e_sa + l);
-    const float * pb = m.eb + (size_t(r) * m.e_sb + (l - m.e_split));
-    o.e = *(lane < m.e_split ? pa : pb);
-}
-
-// Per-lane partial of one row (its lane's units), exact: the block terms are integers below 2^53 summed in FP64.
-// dbg (block sums for the tests) is written only for a row that exists.
-template <int TYPE, int NU>
-__device__ __forceinline__ long long lane_blocks(const WB * wb, int r, bool valid, int nb, const XB * xb, int lane,
-                                                 int32_t * dbg) {
-    double acc = 0.0;
-#pragma unroll
-    for (int k = 0; k < NU; ++k) {
-        const int b = lane + 64 * k;
-        const int si = dot_block<TYPE>(wb[k], xb[k]);
-        acc += block_term<TYPE>(si, wb[k].d, xb[k]);  // units past the row's end hold a zero activation
-        if (dbg && valid && b < nb) dbg[size_t(r) * nb + b] = si;
-    }
-    return dint_to_i64(acc);
-}
-
-template <int TYPE, int NU>
-__device__ __forceinline__ long long lane_units(const WK * wk, int r, bool valid, int nu, const XK * xk, int lane,
-                                                int32_t * dbg) {
-    const int nsb = nu >> 2;
-    long long acc = 0;
-#pragma unroll
-    for (int k = 0; k < NU; ++k) {
-        const int u = lane + 64 * k;
-        int S = 0, M = 0;
-        dot_unit<TYPE>(wk[k], xk[k], u & 3, S, M);
-        if (u >= nu) S = M = 0;
-        S = sum_lanes4_i32(S);
-        M = sum_lanes4_i32(M);
-        const long long t = superblock_term<TYPE>(S, M, wk[k], xk[k]);
-        acc += (u < nu && (u & 3) == 0) ? t : 0;
-        if (dbg && valid && u < nu && (u & 3) == 0) {
-            const size_t i = (size_t(r) * nsb + (u >> 2)) * 2;
-            dbg[i] = S;
-            dbg[i + 1] = M;
-        }
-    }
-    return acc;
-}
-
-struct Ctx {  // per-wave state shared by the row loops
-    int lane, nb, nu;
-    unsigned long long best;
-};
-
-__device__ __forceinline__ float lane_value(float v, int j) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
-}
-
-template <int TYPE, int NU, bool PAIR, int EPI>
-__device__ __forceinline__ void lane_partials(const Slot<TYPE, NU, PAIR> & R, int r, bool valid, const XB * xb,
-                                              const XK * xk, Ctx & c, int32_t * dbg, long long & p, long long & p2) {
-    if constexpr (Slot<TYPE, NU, PAIR>::KQ) {
-        p = lane_units<TYPE, NU>(R.wk, r, valid, c.nu, xk, c.lane, dbg);
-        if constexpr (PAIR && EPI == EPI_SWIGLU) p2 = lane_units<TYPE, NU>(R.wk2, r, valid, c.nu, xk, c.lane, nullptr);
-    } else {
-        p = lane_blocks<TYPE, NU>(R.wb, r, valid, c.nb, xb, c.lane, dbg);
-        if constexpr (PAIR && EPI == EPI_SWIGLU) p2 = lane_blocks<TYPE, NU>(R.wb2, r, valid, c.nb, xb, c.lane, nullptr);
-    }
-}
-
-// The n (<= D) rows base, base + stride, ... of a chunk: the row totals are reduced together (lane group g holds row g), the
-// epilog runs once for all of them on the groups' first lanes, which store; CONV, whose operands sit in lanes 0-6
-// of ev[j], is finished row by row on lane 0. ev holds the rows' epilog operands, taken from the slots before
-// they were refilled.
-template <int TYPE, int NU, bool PAIR, int EPI>
-__device__ __forceinline__ void finish_chunk(const GemvMember & m, bool argmax, int base, int stride, int n,
-                                             const long long * p, const long long * p2, const float * ev, Ctx & c) {
-    constexpr int DS = slots<TYPE, NU, PAIR>();
-    constexpr int G = DS == 1 ? 1 : DS == 2 ? 2 : 4;
-    constexpr int GW = 64 / G;
-    long long pp[G], qq[G];
-#pragma unroll
-    for (int j = 0; j < G; ++j) {
-        pp[j] = j < DS ? p[j < DS ? j : 0] : 0;
-        qq[j] = j < DS ? p2[j < DS ? j : 0] : 0;
-    }
-    const long long tot = reduce_rows<G>(pp);
-    if constexpr (EPI == EPI_CONV) {
-#pragma unroll
-        for (int j = 0; j < DS; ++j) {
-            if (j < n) {
-                float e[7];
-#pragma unroll
-                for (int k = 0; k < 7; ++k) e[k] = lane_value(ev[j], k);
-                const float v = fixed_to_float(readlane_i64(tot, j * GW));
-                if (c.lane == 0) {  // gemvqc_ops.h:387-431 on the row result
-                    const int r = base + j * stride;
-                    float sum = 0.0f;
-                    sum += e[0] * e[3];
-                    sum += e[1] * e[4];
-                    sum += e[2] * e[5];
-                    sum += v * e[6];
-                    m.y[r] = m.conv_silu ? silu_(sum) : sum;
-                    m.conv_dst[3 * r] = e[1];
-                    m.conv_dst[3 * r + 1] = e[2];
-                    m.conv_dst[3 * r + 2] = v;
-                }
-            }
-        }
-    } else {
-        const int g = c.lane / GW;
-        const float v = fixed_to_float(tot);
-        float out = v;
-        if constexpr (PAIR && EPI == EPI_SWIGLU) {
-            const long long tot2 = reduce_rows<G>(qq);
-            out = (v / (1.0f + expf_(-v))) * fixed_to_float(tot2);  // gemvqc_ops.h:88-92
-        } else if constexpr (EPI == EPI_ADD) {
-            uint32_t eb = 0;  // the residual of row g (every lane of a slot holds its row's), gathered bitwise
-#pragma unroll
-            for (int j = 0; j < DS; ++j) eb |= (g == j ? 0xffffffffu : 0u) & __float_as_uint(ev[j]);
-            out = v + __uint_as_float(eb);  // gemvqc16.cpp:282-301
-        } else if constexpr (EPI == EPI_SILU) {
-            out = silu_(v);  // gemvqc_ops.h:70-79 (UNARY SiLU) on the row result
-        }
-        if ((c.lane & (GW - 1)) == 0 && g < n) {
-            const int r = base + g * stride;
-            m.y[r] = out;
-            if (argmax) {
-                const unsigned long long key = argmax_key(out, uint32_t(r));
-                c.best = key > c.best ? key : c.best;
-            }
-        }
-    }
-}
-
-// The n rows w, w + S, w + 2 S, ... of one member (k-th row w + k S): slot j holds row k = kb + j; while more
-// than D rows remain, a slot is refilled with the row D further on as soon as its partial is formed
-// (unconditionally, so the waits stay exact); the last chunk only reduces.
-template <int TYPE, int NU, bool PAIR, int EPI>
-__device__ __forceinline__ void run_rows(const GemvArgs & a, const GemvMember & m, int mi, int w, int S, int n,
-                                         Slot<TYPE, NU, PAIR> * sl, const XB * xb, const XK * xk, Ctx & c) {
-    constexpr int DS = slots<TYPE, NU, PAIR>();
-    const bool argmax = EPI == EPI_PLAIN && a.argmax_key != nullptr && mi == 0;
-    int32_t * dbg = mi == 0 ? a.dbg : nullptr;
-    long long p[DS], p2[DS];
-    float ev[DS];
-    int kb = 0;
-    for (; kb + DS < n; kb += DS) {
-#pragma unroll
-        for (int j = 0; j < DS; ++j) {
-            p2[j] = 0;
-            lane_partials<TYPE, NU, PAIR, EPI>(sl[j], w + (kb + j) * S, true, xb, xk, c, dbg, p[j], p2[j]);
-            ev[j] = sl[j].e;
-            load_slot<TYPE, NU, PAIR>(m, w + min(kb + DS + j, n - 1) * S, c.lane, c.nb, c.nu, sl[j]);
-        }
-        finish_chunk<TYPE, NU, PAIR, EPI>(m, argmax, w + kb * S, S, DS, p, p2, ev, c);
-    }
-#pragma unroll
-    for (int j = 0; j < DS; ++j) {
-        p2[j] = 0;
-        lane_partials<TYPE, NU, PAIR, EPI>(sl[j], w + (kb + j) * S, kb + j < n, xb, xk, c, dbg, p[j], p2[j]);
-        ev[j] = sl[j].e;
-    }
-    finish_chunk<TYPE, NU, PAIR, EPI>(m, argmax, w + kb * S, S, min(DS, n - kb), p, p2, ev, c);
-}
-
-// Waves are assigned to members in order: member i owns the global waves wave_begin .. wave_begin + waves - 1;
-// waves past the last member only take part in the prologue.
-template <int TYPE, int NU, bool PAIR, bool GATED>
-__global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
-    __shared__ Lds s;
-    constexpr bool KQ = TYPE == T_Q5_K || TYPE == T_Q6_K;
-    constexpr int DS = slots<TYPE, NU, PAIR>();
-    constexpr int RX = KQ ? 1 : (NU + 1) / 2;  // rounds of 4096 activation floats (cols <= 2048 NU)
-    Ctx c;
-    c.lane = threadIdx.x & 63;
-    c.nb = a.cols / 32;
-    c.nu = a.cols / 64;
-    c.best = 0;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: member fields load as scalars
-    // Workgroup b serves slice b % 8 of every member's rows (workgroups are dealt to the XCDs in turn, so a slice's
-    // rows stream through one XCD's L2; placement only affects speed, never which rows run).
-    const int xs = blockIdx.x & 7, lw = (blockIdx.x >> 3) * NWAVES + wave;  // slice, wave index within it
-    int mi = 0;
-#pragma unroll
-    for (int i = 1; i < 4; ++i)
-        if (i < a.n_members && lw >= a.m[i].wave_begin) mi = i;
-    const GemvMember & m = a.m[mi];
-    const int s_lo = int((long long)xs * m.rows / 8), len = int((long long)(xs + 1) * m.rows / 8) - s_lo;
-    const int wv = lw - m.wave_begin, S = m.waves;                  // rows s_lo + wv, s_lo + wv + S, ... of the slice
-    const int n = wv < S && wv < len ? (len - 1 - wv) / S + 1 : 0;  // waves past the last member have none
-    const int w = s_lo + wv;
-    XF<RX, GATED> xf;
-    if constexpr (!KQ) prologue_fetch<RX, GATED>(a, xf);  // the activation is requested first
-    __builtin_amdgcn_sched_barrier(0);                    // and stays ahead of the weight loads
-    Slot<TYPE, NU, PAIR> sl[DS];  // the first D rows (a wave without rows reloads the member's last row)
-#pragma unroll
-    for (int j = 0; j < DS; ++j)
-        load_slot<TYPE, NU, PAIR>(m, n > 0 ? w + min(j, n - 1) * S : m.rows - 1, c.lane, c.nb, c.nu, sl[j]);
-    if constexpr (KQ) {
-        const float scale = a.xsrc == XSRC_NORM ? block_norm_scale(a.x, a.cols, a.norm_eps, a.norm_l2, s) : 1.0f;
-        quantize_q8_K(a, scale, s);
-    } else {
-        prologue_finish<RX, GATED>(a, xf, s);
-    }
-    __syncthreads();
-    XB xb[KQ ? 1 : NU];
-    XK xk[KQ ? NU : 1];
-    if constexpr (KQ) {
-#pragma unroll
-        for (int k = 0; k < NU; ++k) load_xk<TYPE>(s, c.lane + 64 * k, c.nu, xk[k]);
-    } else {
-#pragma unroll
-        for (int k = 0; k < NU; ++k) load_xb<TYPE>(s, c.lane + 64 * k, c.nb, xb[k]);
-    }
-    if (n > 0) {
-        switch (m.epi) {
-        case EPI_SWIGLU:
-            if constexpr (PAIR) run_rows<TYPE, NU, PAIR, EPI_SWIGLU>(a, m, mi, w, S, n, sl, xb, xk, c);
-            break;
-        case EPI_ADD: run_rows<TYPE, NU, PAIR, EPI_ADD>(a, m, mi, w, S, n, sl, xb, xk, c); break;
-        case EPI_CONV: run_rows<TYPE, NU, PAIR, EPI_CONV>(a, m, mi, w, S, n, sl, xb, xk, c); break;
-        case EPI_SILU: run_rows<TYPE, NU, PAIR, EPI_SILU>(a, m, mi, w, S, n, sl, xb, xk, c); break;
-        default: run_rows<TYPE, NU, PAIR, EPI_PLAIN>(a, m, mi, w, S, n, sl, xb, xk, c); break;
-        }
-    }
-    if (a.argmax_key) {
-        unsigned long long best = c.best;  // held by the lane-group leaders
-#pragma unroll
-        for (int st = 1; st < 64; st <<= 1) {
-            const unsigned long long o = (unsigned long long)shfl_xor_i64((long long)best, st);
-            best = o > best ? o : best;
-        }
-        if (c.lane == 0) s.key[wave] = best;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            unsigned long long b = s.key[0];
-            for (int i = 1; i < NWAVES; ++i) b = s.key[i] > b ? s.key[i] : b;
-            if (b) atomicMax(a.argmax_key, b);
-        }
-    }
-}
-
-// Workgroups of `kernel` that fit on the device at once (a grid beyond it runs a second, mostly idle round).
-template <typename K>
-int resident_blocks(K kernel) {
-    int dev = 0, cus = 0, occ = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, NT, 0) != hipSuccess || occ < 1 || cus < 1)
-        return 1024;
-    return occ * cus;
-}
-
-// Every member's rows are split into 8 contiguous slices, one per XCD; the same member layout repeats on each XCD
-// (workgroups b with b % 8 == x serve slice x). A member's waves per slice: enough for ds rows each when all fit
-// on the device at once (every row is requested before the activation prologue ends); otherwise the resident waves,
-// shared in proportion to the rows, stream them. A slice's rows are dealt to its waves in turn, so the rows in flight
-// form one region of the slice.
-int plan_waves(GemvArgs & a, int cap_blocks, int ds) {
-    const int cap_x = cap_blocks / 8 < 1 ? 1 : cap_blocks / 8;  // workgroups per XCD
-    int need = 0;
-    for (int i = 0; i < a.n_members; ++i) need += ((a.m[i].rows + 7) / 8 + ds - 1) / ds;
-    const bool fits = (need + NWAVES - 1) / NWAVES <= cap_x;
-    const long long waves = (long long)cap_x * NWAVES;
-    long long total = 0;
-    for (int i = 0; i < a.n_members; ++i) total += a.m[i].rows;
-    int w = 0;
-    for (int i = 0; i < a.n_members; ++i) {
-        const int per = (a.m[i].rows + 7) / 8;
-        long long wi = fits ? (per + ds - 1) / ds : waves * a.m[i].rows / total;
-        wi = wi < 1 ? 1 : wi > per ? per : wi;
-        a.m[i].wave_begin = w;
-        a.m[i].waves = int(wi);
-        w += int(wi);
-    }
-    return 8 * ((w + NWAVES - 1) / NWAVES);
-}
-
-// Epilog operand addresses of a member: with l = min(lane, 6) * e_lane, lanes below e_split read ea[r * e_sa + l],
-// the others eb[r * e_sb + l - e_split] (CONV: lanes 0-2 the state, lanes 3-6 the kernel; ADD: the residual).
-void epilog_operands(GemvMember & m) {
-    m.e_lane = 0;
-    m.e_split = 64;
-    m.e_sa = m.e_sb = 1;
-    m.ea = m.eb = m.y;
-    if (m.epi == EPI_ADD) {
-        m.ea = m.eb = m.res;
-    } else if (m.epi == EPI_CONV) {
-        m.e_lane = 1;
-        m.e_split = 3;
-        m.ea = m.conv_src;
-        m.e_sa = 3;
-        m.eb = m.conv_w;
-        m.e_sb = 4;
-    }
-    if (m.epi != EPI_SWIGLU) m.w2 = m.w;
-}
-
-template <int TYPE, int NU, bool PAIR, bool GATED>
-hipError_t launch_typed(const GemvArgs & a0, hipStream_t st) {
-    static const int cap = resident_blocks(gemv_kernel<TYPE, NU, PAIR, GATED>);
-    GemvArgs a = a0;
-    for (int i = 0; i < a.n_members; ++i) epilog_operands(a.m[i]);
-    const int grid = plan_waves(a, cap, slots<TYPE, NU, PAIR>());
-    GQ_LAUNCH((gemv_kernel<TYPE, NU, PAIR, GATED>), dim3(grid), dim3(NT), 0, st, a);
-    return hipGetLastError();
-}
-
-// The gated activation prologue exists for Q4_0 / Q8_0 rows of at most 8192 columns without a SwiGLU pair.
-template <int TYPE, int NU>
-hipError_t launch_pair(const GemvArgs & a, hipStream_t st) {
-    bool pair = false;
-    for (int i = 0; i < a.n_members; ++i) pair = pair || a.m[i].epi == EPI_SWIGLU;
-    if (a.xsrc == XSRC_GATED) {
-        if constexpr ((TYPE == T_Q4_0 || TYPE == T_Q8_0) && NU <= 4) {
-            if (!pair) return launch_typed<TYPE, NU, false, true>(a, st);
-        }
-        return hipErrorInvalidValue;
-    }
-    return pair ? launch_typed<TYPE, NU, true, false>(a, st) : launch_typed<TYPE, NU, false, false>(a, st);
-}
-
-template <int TYPE>
-hipError_t launch_nu(const GemvArgs & a, hipStream_t st) {
-    constexpr bool KQ = TYPE == T_Q5_K || TYPE == T_Q6_K;
-    const int nu = (a.cols / (KQ ? 64 : 32) + 63) / 64;  // cols <= 16384: K-quants nu <= 4, Q4_0 / Q8_0 nu <= 8
-    switch (nu) {
-    case 1: return launch_pair<TYPE, 1>(a, st);
-    case 2: return launch_pair<TYPE, 2>(a, st);
-    case 3: return launch_pair<TYPE, 3>(a, st);
-    case 4: return launch_pair<TYPE, 4>(a, st);
-    default: break;
-    }
-    if constexpr (!KQ) {
-        switch (nu) {
-        case 5: return launch_pair<TYPE, 5>(a, st);
-        case 6: return launch_pair<TYPE, 6>(a, st);
-        case 7: return launch_pair<TYPE, 7>(a, st);
-        case 8: return launch_pair<TYPE, 8>(a, st);
-        default: break;
-        }
-    }
-    return hipErrorInvalidValue;
-}
-
-}  // namespace
+hipError_t launch_gemv_q4_0(const GemvArgs & a, hipStream_t st);
+hipError_t launch_gemv_q4_1(const GemvArgs & a, hipStream_t st);
+hipError_t launch_gemv_q8_0(const GemvArgs & a, hipStream_t st);
+hipError_t launch_gemv_q5_k(const GemvArgs & a, hipStream_t st);
+hipError_t launch_gemv_q6_k(const GemvArgs & a, hipStream_t st);
 
 hipError_t launch_gemv(const GemvArgs & a, int type, hipStream_t st) {
-    if (a.cols <= 0 || a.cols > MAXK || a.total_tasks <= 0) return hipErrorInvalidValue;
+    if (a.cols <= 0 || a.cols > GEMV_MAXK || a.total_tasks <= 0) return hipErrorInvalidValue;
     switch (type) {
-    case T_Q4_0: return launch_nu<T_Q4_0>(a, st);
-    case T_Q4_1: return launch_nu<T_Q4_1>(a, st);
-    case T_Q8_0: return launch_nu<T_Q8_0>(a, st);
-    case T_Q5_K: return a.cols % 256 ? hipErrorInvalidValue : launch_nu<T_Q5_K>(a, st);
-    case T_Q6_K: return a.cols % 256 ? hipErrorInvalidValue : launch_nu<T_Q6_K>(a, st);
+    case T_Q4_0: return launch_gemv_q4_0(a, st);
+    case T_Q4_1: return launch_gemv_q4_1(a, st);
+    case T_Q8_0: return launch_gemv_q8_0(a, st);
+    case T_Q5_K: return a.cols % 256 ? hipErrorInvalidValue : launch_gemv_q5_k(a, st);
+    case T_Q6_K: return a.cols % 256 ? hipErrorInvalidValue : launch_gemv_q6_k(a, st);
     default: return hipErrorInvalidValue;
     }
 }
 
 }  // namespace gq
-

@@ -1,0 +1,8 @@
+// GEMV instances for Q8_0 weights (the kernel is in gq_gemv_impl.h).
+#include "gq_gemv_impl.h"
+
+namespace gq {
+
+hipError_t launch_gemv_q8_0(const GemvArgs & a, hipStream_t st) { return launch_nu<T_Q8_0>(a, st); }
+
+}  // namespace gq

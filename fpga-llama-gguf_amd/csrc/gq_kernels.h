@@ -161,6 +161,7 @@ struct NextTokenArgs {
     int max_pos;
 };
 
+constexpr int GEMV_MAXK = 16384;  // GEMV columns at most
 constexpr int ATTN_CHUNK = 64;
 constexpr int ATTN_MAXG = 4;  // q heads per KV head
 constexpr int GDN_MAX_HEADS = 64;  // value heads of one GDN command
