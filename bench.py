@@ -98,6 +98,156 @@ def copy_probe(mib: int) -> int:
     return 0
 
 
+# ---------------------------------------------------------------------------------------------------------------
+# C1-C4: the single-op configurations, each timed over rotated weight copies (>= 512 MB, twice the 256 MB
+# memory-side cache) inside one graph, and as single launches; the oracle on the host on the same bytes.
+def _cfg_units(seed: int = 0):
+    """[(name, description, algorithmic bytes per unit, rotated copies, setup(ctx) -> builder(copy) -> commands,
+    cpu(oracle) -> (function, args[, scale]))]."""
+    units = []
+
+    # C1: Q4_0 GEMV [9728 x 2560], x ~ N(0, 1) quantized to Q8_0 on the GPU
+    R1, K1 = 9728, 2560
+    w1 = gq.matrix(gq.Q4_0, R1, K1, seed, 1)
+    x1 = gq.normal(seed, 2, K1)
+
+    C1_COPIES = 40
+
+    def c1(ctx):
+        offs = [ctx.upload(gq.Q4_0, R1, K1, w1) for _ in range(C1_COPIES)]
+        ctx.write(0, x1)
+        return lambda i: gq.gemv(gq.Q4_0, R1, K1, offs[i], 0, 4096)
+    units.append(("C1", "Q4_0 GEMV 9728x2560", w1.size + 4 * K1 + 4 * R1, C1_COPIES, c1,
+                  lambda orc: (orc.fx_gemv, (gq.Q4_0, w1, x1, R1, K1))))
+
+    # C2: norm + SwiGLU gate/up (Q8_0 [9728 x 2560] x 2) + down (Q8_0 [2560 x 9728]) + residual
+    E, F = 2560, 9728
+    wg, wu = gq.matrix(gq.Q8_0, F, E, seed, 3), gq.matrix(gq.Q8_0, F, E, seed, 4)
+    wd = gq.matrix(gq.Q8_0, E, F, seed, 5)
+    x2, r2, nw2 = gq.normal(seed, 6, E), gq.normal(seed, 7, E), gq.uniform(seed, 8, E, 0.5, 1.5)
+    C2_COPIES = 8
+
+    def c2(ctx):
+        offs = [(ctx.upload(gq.Q8_0, F, E, wg), ctx.upload(gq.Q8_0, F, E, wu), ctx.upload(gq.Q8_0, E, F, wd))
+                for _ in range(C2_COPIES)]
+        ctx.write(0, x2)
+        ctx.write(4096, r2)
+        ctx.write(8192, nw2)
+        X, XN, ACT, T, Y = 0, 12288, 16384, 32768, 36864
+        return lambda i: (gq.rmsnorm(E, X, 8192, XN, 1e-6, flags=gq.NORM_DEFER) +
+                          gq.gemv(gq.Q8_0, F, E, offs[i][0], XN, ACT, gq.GEMV_SWIGLU) +
+                          gq.gemv(gq.Q8_0, F, E, offs[i][1], XN, ACT) +
+                          gq.gemv(gq.Q8_0, E, F, offs[i][2], ACT, T, gq.GEMV_ADD) + gq.add(E, T, 4096, Y))
+
+    def c2_cpu(orc):
+        def run():
+            xn = orc.rownorm(x2, nw2, E, 1, 1e-6)
+            act = orc.silu_mul(orc.fx_gemv(gq.Q8_0, wg, xn, F, E), orc.fx_gemv(gq.Q8_0, wu, xn, F, E))
+            return orc.fx_gemv(gq.Q8_0, wd, act, E, F) + r2
+        return run, ()
+
+    units.append(("C2", "RMSNorm + Q8_0 SwiGLU gate/up 2x9728x2560 + down 2560x9728 + residual",
+                  wg.size + wu.size + wd.size + 4 * 4 * E, C2_COPIES, c2, c2_cpu))
+
+    # C3: Q6_K head [151936 x 4096] and Q5_K [12288 x 4096], x quantized to Q8_K
+    V, D3 = 151936, 4096
+    wh = gq.matrix(gq.Q6_K, V, D3, seed, 9)
+    w5 = gq.matrix(gq.Q5_K, 12288, D3, seed, 10)
+    x3 = gq.normal(seed, 11, D3)
+
+    def c3h(ctx):
+        offs = [ctx.upload(gq.Q6_K, V, D3, wh) for _ in range(2)]
+        ctx.write(0, x3)
+        return lambda i: gq.gemv(gq.Q6_K, V, D3, offs[i], 0, 8192)
+
+    def c35(ctx):
+        offs = [ctx.upload(gq.Q5_K, 12288, D3, w5) for _ in range(16)]
+        ctx.write(0, x3)
+        return lambda i: gq.gemv(gq.Q5_K, 12288, D3, offs[i], 0, 8192)
+
+    sl = 16384  # the CPU times a row slice of the head and scales it
+    units.append(("C3 head", "Q6_K GEMV 151936x4096", wh.size + 4 * D3 + 4 * V, 2, c3h,
+                  lambda orc: (orc.fx_gemv, (gq.Q6_K, wh[:sl * gq.row_bytes(gq.Q6_K, D3)], x3, sl, D3), V / sl)))
+    units.append(("C3 Q5_K", "Q5_K GEMV 12288x4096", w5.size + 4 * D3 + 4 * 12288, 16, c35,
+                  lambda orc: (orc.fx_gemv, (gq.Q5_K, w5, x3, 12288, D3))))
+
+    # C4: conv over 8192 channels (3x8192 cache, 4x8192 kernel), the GDN step (32 value / 16 key heads, L2 q/k,
+    # gates, gated norm) and ssm_out Q4_0 [4096 x 4096] + residual
+    Hk, Hv, S = 16, 32, 128
+    ch = 2 * Hk * S + Hv * S
+    wo = gq.matrix(gq.Q4_0, 4096, Hv * S, seed, 12)
+    qkv, cw, cst = gq.normal(seed, 13, ch), gq.normal(seed, 14, 4 * ch, std=0.5), gq.normal(seed, 15, 3 * ch)
+    z, ba = gq.normal(seed, 16, Hv * S), gq.normal(seed, 17, 2 * Hv)
+    dt, av, sw = gq.normal(seed, 18, Hv), -np.abs(gq.normal(seed, 19, Hv)), gq.uniform(seed, 20, S, 0.5, 1.5)
+    state = gq.normal(seed, 21, Hv * S * S) * 0.1
+    C4_COPIES = 48
+    O = dict(qkv=0, cqkv=8192, z=16384, ba=20480, y=20544, dt=24640, a=24704, sw=24768, x=24896, out=28992,
+             res=33088, cw=37184, cst=69952)
+
+    def c4(ctx):
+        offs = [ctx.upload(gq.Q4_0, 4096, Hv * S, wo) for _ in range(C4_COPIES)]
+        for k_, v_ in dict(qkv=qkv, cw=cw, z=z, ba=ba, dt=dt, a=av, sw=sw, x=gq.normal(seed, 22, 4096)).items():
+            ctx.write(O[k_], v_)
+        for i in range(C4_COPIES):
+            ctx.write(O["cst"] + 3 * ch * i, cst)
+            ctx.state_write(i * Hv * S, state)
+        flags = gq.GDN_L2_QK | gq.GDN_GATED | gq.GDN_GATES
+
+        def cmds(i):
+            st = O["cst"] + 3 * ch * i
+            return (gq.conv(ch, O["qkv"], O["cw"], O["cqkv"], st, st) +
+                    gq.gdn(Hv, Hk, O["cqkv"], O["cqkv"] + Hk * S, O["cqkv"] + 2 * Hk * S, O["ba"] + Hv, O["ba"],
+                           O["y"], i * Hv * S, i * Hv * S, 1 / np.sqrt(S), flags, 1e-6, 1e-6, O["sw"], O["z"], O["dt"],
+                           O["a"]) +
+                    gq.gemv(gq.Q4_0, 4096, Hv * S, offs[i], O["y"], O["out"], gq.GEMV_ADD) +
+                    gq.add(4096, O["out"], O["x"], O["res"]))
+        return cmds
+
+    def c4_cpu(orc):
+        def run():
+            yc, _ = orc.conv(cst, qkv, cw)
+            y, _ = orc.gdn(state, yc[:Hk * S], yc[Hk * S:2 * Hk * S], yc[2 * Hk * S:], ba[Hv:], ba[:Hv], Hv, Hk,
+                           float(1 / np.sqrt(S)), gq.GDN_L2_QK | gq.GDN_GATED | gq.GDN_GATES, dt, av, z, sw)
+            return orc.fx_gemv(gq.Q4_0, wo, y, 4096, Hv * S)
+        return run, ()
+
+    units.append(("C4", "conv 8192 ch + GDN step (32 heads) + gated norm + ssm_out Q4_0 4096x4096 + residual",
+                  wo.size + 2 * Hv * S * S * 4 + 2 * 3 * ch * 4 + 4 * ch * 4 + 4 * 4096 * 3, C4_COPIES, c4, c4_cpu))
+    return units
+
+
+def configs(args) -> int:
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle  # noqa: E402  (the CPU baseline only)
+
+    for name, desc, nbytes, copies, setup, cpu in _cfg_units():
+        ctx = gq.Context(act_floats=1 << 21, weight_bytes=1_100_000_000, state_rows=48 * 32 * 128)
+        build = setup(ctx)
+        cmds = sum((build(i) for i in range(copies)), [])
+        g = ctx.graph(cmds)
+        ctx.replay(g, 2)
+        ctx.sync()
+        t_graph = ctx.graph_time_us(g, 5) / copies
+        stats = profile(ctx, np.array(build(0), np.uint32), args.profile_reps)
+        t_single = sum(s["us"] for s in stats)
+        ctx.close()
+        spec = cpu(oracle)
+        fn, fargs = spec[0], spec[1]
+        scale = spec[2] if len(spec) > 2 else 1.0
+        fn(*fargs)
+        t0 = time.perf_counter()
+        fn(*fargs)
+        t_cpu = (time.perf_counter() - t0) * scale
+        line = {"config": name, "what": desc, "algorithmic_bytes": nbytes, "copies_rotated": copies,
+                "graph_us_per_unit": round(t_graph, 3), "graph_GBps": round(nbytes / t_graph / 1e3, 1),
+                "graph_frac_of_8TBps": round(nbytes / t_graph / 1e3 / HBM_PEAK_GBPS, 4),
+                "single_launch_device_us": round(t_single, 3), "launches_per_unit": len(stats),
+                "cpu_oracle_s": round(t_cpu, 4), "cpu_GBps": round(nbytes / t_cpu / 1e9, 2),
+                "cpu_kind": "port (oracle, one thread)"}
+        print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -113,9 +263,13 @@ def main() -> int:
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy kernel of MIB MiB 5 times (calibrates the HBM byte counters "
                          "of rocprofv3 --pmc) and exit")
+    ap.add_argument("--configs", action="store_true",
+                    help="only time the single-op configurations C1-C4 (one JSON line each) and exit")
     args = ap.parse_args()
     if args.copy_probe:
         return copy_probe(args.copy_probe)
+    if args.configs:
+        return configs(args)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               f"(the multi-GPU sharding is a design note, not code)", file=sys.stderr)

@@ -94,3 +94,29 @@ def test_model_from_gguf_file_matches_oracle(gq, orc, q35, tmp_path):
     for pos in range(len(prompt) - 1 + n_gen):
         om2.decode(int(want[pos]), pos, lo if pos == len(prompt) - 2 + n_gen else None)
     assert np.array_equal(lg.view(np.uint32), lo.view(np.uint32))
+
+
+@pytest.mark.timeout(600)
+def test_c5_greedy_128_steps_matches_oracle(gq, orc, q35):
+    """The full C5 model (32 layers: 24 DeltaNet + 8 attention, hidden 4096, FFN 12288, vocab 151936, Q4_0 layers,
+    Q6_K embedding and head, seed 0): 128 greedy tokens after an 8-token prompt, identical to the oracle decoder's,
+    and the last step's logits bit for bit."""
+    cfg = q35.Config(n_ctx=160)
+    blob = q35.generate(cfg, seed=0)
+    prompt = q35.prompt_ids(cfg, 8)
+    n_gen = 128
+    om = orc.Model(q35.config_c(cfg), blob.table, blob.n, blob.data)
+    lo = np.empty(cfg.n_vocab, np.float32)
+    toks = [int(t) for t in prompt]
+    for pos in range(len(prompt) - 1 + n_gen):  # the oracle's greedy decode, keeping the last logits
+        last = pos == len(prompt) - 2 + n_gen
+        nxt = om.decode(toks[pos], pos, lo if last else None)
+        if pos + 1 >= len(prompt):
+            toks.append(nxt)
+    om.close()
+    want = np.array(toks, np.int32)
+    with q35.Model(blob) as m:
+        got = m.generate(prompt, n_gen)
+        lg = m.logits()
+    assert np.array_equal(got, want), f"first mismatch at {np.nonzero(got != want)[0][:3]}"
+    assert np.array_equal(lg.view(np.uint32), lo.view(np.uint32))
