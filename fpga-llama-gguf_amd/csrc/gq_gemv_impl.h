@@ -825,15 +825,21 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
     }
 }
 
-// Workgroups of `kernel` that fit on the device at once (a grid beyond it runs a second, mostly idle round).
+// Workgroups of `kernel` that fit on the device at once (a grid beyond it runs a second, mostly idle round), at
+// most `per_cu` per CU.
 template <typename K>
-int resident_blocks(K kernel) {
+int resident_blocks(K kernel, int per_cu = 1 << 20) {
     int dev = 0, cus = 0, occ = 0;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, NT, 0) != hipSuccess || occ < 1 || cus < 1)
         return 1024;
-    return occ * cus;
+    return (occ < per_cu ? occ : per_cu) * cus;
 }
+
+// Workgroups per CU a launch may use: every workgroup reads and quantizes the whole activation, so beyond three per
+// CU the extra activation reads cost more than the extra rows in flight gain (measured on the decode layers' gate/up
+// pairs and projection groups, about 1 us per launch).
+constexpr int GEMV_WG_PER_CU = 3;
 
 // Every member's rows are split into 8 contiguous slices, one per XCD; the same member layout repeats on each XCD
 // (workgroups b with b % 8 == x serve slice x). A member's waves per slice: enough for ds rows each when all fit
@@ -882,7 +888,7 @@ void epilog_operands(GemvMember & m) {
 
 template <int TYPE, int NU, bool PAIR, bool GATED, int DS>
 hipError_t launch_typed(const GemvArgs & a0, hipStream_t st) {
-    static const int cap = resident_blocks(gemv_kernel<TYPE, NU, PAIR, GATED, DS>);
+    static const int cap = resident_blocks(gemv_kernel<TYPE, NU, PAIR, GATED, DS>, GEMV_WG_PER_CU);
     GemvArgs a = a0;
     for (int i = 0; i < a.n_members; ++i) epilog_operands(a.m[i]);
     const int grid = plan_waves(a, cap, DS);
