@@ -28,7 +28,15 @@ struct Lds {
     unsigned long long key[NWAVES];
 };
 
-// Canonical norm scale over n floats (pairwise tree of the squares; words of 16 floats per thread, 256 words per
+// Pairwise tree over the workgroup's per-wave values (NWAVES, a power of two, consecutive).
+__device__ __forceinline__ float wave_tree(const float * r) {
+    float t[NWAVES];
+#pragma unroll
+    for (int i = 0; i < NWAVES; ++i) t[i] = r[i];
+    return tree<NWAVES>(t);
+}
+
+// Canonical norm scale over n floats (pairwise tree of the squares; words of 16 floats per thread, NT words per
 // round, rounds combined pairwise with zero padding).
 __device__ float block_norm_scale(const float * x, int n, float eps, int l2, Lds & s) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -55,7 +63,7 @@ __device__ float block_norm_scale(const float * x, int n, float eps, int l2, Lds
         ws = pair_sum_lanes<64>(ws);
         if (lane == 0) s.red[wave] = ws;
         __syncthreads();
-        rs[g] = (s.red[0] + s.red[1]) + (s.red[2] + s.red[3]);
+        rs[g] = wave_tree(s.red);
         __syncthreads();
         }
     }
@@ -68,7 +76,7 @@ __device__ float block_norm_scale(const float * x, int n, float eps, int l2, Lds
 // consecutive floats; the two halves of a 32-block sit in adjacent lanes). The loads are issued by prologue_fetch
 // before the first weight rows are requested, so they are not queued behind them; prologue_finish then folds the
 // deferred norm or the gated output norm and quantizes into LDS.
-template <int R, bool GATED>  // rounds of 256 items the registers hold (cols <= 4096 R); the gated output norm
+template <int R, bool GATED>  // rounds of NT items the registers hold (cols <= 16 NT R); the gated output norm
 struct XF {
     float v[R][16];
     float w[R <= 2 ? R : 1][16];  // NORM: the norm weight (the activation again without one); GATED: the gated norm's
@@ -170,7 +178,7 @@ __device__ __forceinline__ float norm_scale_items(const GemvArgs & a, const XF<R
     float rs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int g = 0; g < R; ++g)
-        rs[g] = (s.red[NWAVES * g] + s.red[NWAVES * g + 1]) + (s.red[NWAVES * g + 2] + s.red[NWAVES * g + 3]);
+        rs[g] = wave_tree(s.red + NWAVES * g);
     const float sum = R == 1 ? rs[0] : R == 2 ? rs[0] + rs[1] : (rs[0] + rs[1]) + (rs[2] + rs[3]);
     return a.norm_l2 ? 1.0f / fmaxf(sqrtf(sum), a.norm_eps) : 1.0f / sqrtf(sum / float(a.cols) + a.norm_eps);
 }
@@ -755,7 +763,7 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
     __shared__ Lds s;
     constexpr bool KQ = TYPE == T_Q5_K || TYPE == T_Q6_K;
 
-    constexpr int RX = KQ ? 1 : (NU + 1) / 2;  // rounds of 4096 activation floats (cols <= 2048 NU)
+    constexpr int RX = KQ ? 1 : (128 * NU + NT - 1) / NT;  // rounds of 16 NT activation floats (cols <= 2048 NU)
     Ctx c;
     c.lane = threadIdx.x & 63;
     c.nb = a.cols / 32;
@@ -836,10 +844,11 @@ int resident_blocks(K kernel, int per_cu = 1 << 20) {
     return (occ < per_cu ? occ : per_cu) * cus;
 }
 
-// Workgroups per CU a launch may use: every workgroup reads and quantizes the whole activation, so beyond three per
-// CU the extra activation reads cost more than the extra rows in flight gain (measured on the decode layers' gate/up
-// pairs and projection groups, about 1 us per launch).
-constexpr int GEMV_WG_PER_CU = 3;
+// Waves per CU a launch may use: every workgroup reads and quantizes the whole activation, so beyond twelve waves
+// per CU the extra activation reads cost more than the extra rows in flight gain (measured on the decode layers'
+// gate/up pairs and projection groups, about 1 us per launch).
+constexpr int GEMV_WAVES_PER_CU = 12;
+constexpr int GEMV_WG_PER_CU = GEMV_WAVES_PER_CU / NWAVES > 0 ? GEMV_WAVES_PER_CU / NWAVES : 1;
 
 // Every member's rows are split into 8 contiguous slices, one per XCD; the same member layout repeats on each XCD
 // (workgroups b with b % 8 == x serve slice x). A member's waves per slice: enough for ds rows each when all fit
