@@ -124,14 +124,15 @@ __device__ __forceinline__ void prologue_fetch(const GemvArgs & a, XF<R, GATED> 
 
 // Q8_0 of one 32-block held as two halves by lanes l and l ^ 1: d = amax / 127 over the block, q = round(v / d)
 // (half away from zero), the block's quant sum, and for Q4_1 weights the Q8_1 s = fp16(sum * d).
-__device__ __forceinline__ void quantize_half(const float * v, int item, bool valid, Lds & s) {
+// The arithmetic of one half-block (both lanes of the pair must run it): its 16 quants packed little-endian, the
+// block's quant sum, and the block's FP32 d.
+__device__ __forceinline__ float quantize_half_core(const float * v, uint32_t * packed, int & sum) {
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(v[j]));
     amax = fmaxf(amax, dpp_f32<DPP_XOR1>(amax));
     const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
-    uint32_t packed[4];
-    int sum = 0;
+    sum = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         uint32_t w = 0;
@@ -147,6 +148,13 @@ __device__ __forceinline__ void quantize_half(const float * v, int item, bool va
         packed[i] = w;
     }
     sum += __shfl_xor(sum, 1, WAVE);
+    return d;
+}
+
+__device__ __forceinline__ void quantize_half(const float * v, int item, bool valid, Lds & s) {
+    uint32_t packed[4];
+    int sum;
+    const float d = quantize_half_core(v, packed, sum);
     if (valid) {
         *reinterpret_cast<uint4 *>(s.xq + size_t(item) * 16) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
         if ((item & 1) == 0) {

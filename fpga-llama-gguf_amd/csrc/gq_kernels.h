@@ -161,7 +161,32 @@ struct NextTokenArgs {
     int max_pos;
 };
 
+// Batched GEMV (n_tok tokens per weight read): the activation rows are quantized once into Q8_0 blocks whose 32
+// quants are stored in the MFMA operand order (8-byte group g holds quants 4g..4g+3 and 16+4g..16+4g+3), with
+// d * 2^40 per block as FP32; token rows n_tok..n_pad-1 are zero.
+struct GemmQuantArgs {
+    const float * x;       // token t's row at x + t * x_stride
+    const float * norm_w;  // per-token RMS norm folded into the quantization: its weight (NULL: none)
+    int8_t * q;            // [n_pad][cols]
+    float * d40;           // [n_pad][cols / 32]
+    int n_tok, n_pad, cols, x_stride;
+    int norm, norm_l2;
+    float eps;
+};
+
+struct GemmArgs {
+    WeightView w;       // matrix (g of a SwiGLU pair)
+    WeightView w2;      // u of a SwiGLU pair
+    const int8_t * q;   // the quantized activation (GemmQuantArgs)
+    const float * d40;
+    float * y;          // token t, row r at y[t * y_stride + r]
+    const float * res;  // ADD: res[t * res_stride + r]
+    int rows, cols, n_tok, y_stride, res_stride;
+    int epi;            // EPI_PLAIN, EPI_SWIGLU, EPI_ADD or EPI_SILU
+};
+
 constexpr int GEMV_MAXK = 16384;  // GEMV columns at most
+constexpr int GEMM_MAX_TOK = 32;  // tokens of one batched GEMV (two tiles of 16)
 constexpr int ATTN_CHUNK = 64;
 constexpr int ATTN_MAXG = 4;  // q heads per KV head
 constexpr int GDN_MAX_HEADS = 64;  // value heads of one GDN command
@@ -190,6 +215,8 @@ hipError_t launch_attn(const AttnArgs & a, hipStream_t s);
 hipError_t launch_get_rows(const GetRowsArgs & a, hipStream_t s);
 hipError_t launch_argmax(const float * x, int n, unsigned long long * key, hipStream_t s);
 hipError_t launch_next_token(const NextTokenArgs & a, hipStream_t s);
+hipError_t launch_gemm_quant(const GemmQuantArgs & a, hipStream_t s);
+hipError_t launch_gemm(const GemmArgs & a, int type, hipStream_t s);
 
 // Layout helpers (host and device).
 __host__ __device__ inline size_t gguf_row_bytes(int type, int cols) {

@@ -46,7 +46,9 @@ struct LAttn { AttnArgs a; };
 struct LRows { GetRowsArgs a; };
 struct LArgmax { const float * x; int n; unsigned long long * key; };
 struct LNext { NextTokenArgs a; };
-using Launch = std::variant<LGemv, LNorm, LEw, LConv, LRope, LGdn, LGated, LAttn, LRows, LArgmax, LNext>;
+struct LGemmQ { GemmQuantArgs a; };
+struct LGemm { GemmArgs a; int type; };
+using Launch = std::variant<LGemv, LNorm, LEw, LConv, LRope, LGdn, LGated, LAttn, LRows, LArgmax, LNext, LGemmQ, LGemm>;
 
 }  // namespace
 
@@ -68,6 +70,8 @@ struct gemvq_ctx {
     int32_t * dbg_dst = nullptr;  // host destination; non-NULL while armed
     bool dbg_used = false;        // the list being compiled writes the dump
     float * gdn_raw = nullptr;    // raw DeltaNet output when its gated norm is folded into the next GEMV
+    int8_t * gemm_q = nullptr;    // a batched GEMV's quantized activation rows (GEMM_MAX_TOK x GEMV_MAXK)
+    float * gemm_d = nullptr;     // and their block scales
     int last_launches = 0;
     std::string err;
 };
@@ -398,6 +402,12 @@ struct Compiler {
                 i += 2;
                 continue;
             }
+            case GEMVQ_OP_GEMM: {
+                unsigned used = 0;
+                if (!gemm(cmds, n, i, used)) return false;
+                i += used;
+                continue;
+            }
             case GEMVQ_OP_GET_ROWS: {
                 const int type = int(k[1] & 0xffu), rows = int(k[2]), cols = int(k[3]);
                 const uint64_t woff = uint64_t(k[4]) | (uint64_t(k[5]) << 32);
@@ -444,6 +454,80 @@ struct Compiler {
             }
             ++i;
         }
+        return true;
+    }
+
+    // A batched GEMV at command i (two slots; a SwiGLU g takes its u command too): the activation rows are
+    // quantized once into the context's scratch rows, then every weight row is read once for all the tokens.
+    bool gemm(const uint32_t * cmds, unsigned n, unsigned i, unsigned & used) {
+        if (i + 1 >= n) return reject(i, "GEMM needs its second slot");
+        const uint32_t * k = cmds + size_t(i) * GEMVQ_CMD_WORDS, * k2 = k + GEMVQ_CMD_WORDS;
+        const int t = int(k[1] & 0xffu), rows = int(k[2]);
+        const uint32_t flags = k[1] & ~0xffu, cols = k[3], ntok = k2[0], xs = k2[1], ys = k2[2], nflags = k2[7];
+        if (t != T_Q4_0 && t != T_Q8_0) return reject(i, "GEMM format (Q4_0 or Q8_0)");
+        if (rows <= 0 || cols == 0 || cols % 512 || cols > GEMVQ_MAX_COLS) return reject(i, "GEMM shape (cols a multiple of 512)");
+        if (flags & ~(GEMVQ_GEMV_SWIGLU | GEMVQ_GEMV_ADD | GEMVQ_GEMV_SILU) || __builtin_popcount(flags) > 1)
+            return reject(i, "GEMM flags");
+        if (ntok < 1 || ntok > GEMVQ_GEMM_MAX_TOK) return reject(i, "GEMM token count");
+        if (xs % 16 || xs < cols || ys % 16 || ys < uint32_t(rows)) return reject(i, "GEMM strides");
+        const uint64_t woff = uint64_t(k[4]) | (uint64_t(k[5]) << 32);
+        if (!weight(woff, t, rows, int(cols))) return reject(i, "GEMM weight offset, format or shape does not match an uploaded weight");
+        if (!range(k[6], uint64_t(xs) * (ntok - 1) + cols) || !range(k[7], uint64_t(ys) * (ntok - 1) + rows))
+            return reject(i, "GEMM range");
+        const bool norm = nflags & GEMVQ_NORM_DEFER, normw = norm && !(nflags & GEMVQ_NORM_NO_WEIGHT);
+        if (nflags & ~(GEMVQ_NORM_DEFER | GEMVQ_NORM_NO_WEIGHT | GEMVQ_NORM_L2) || (normw && !range(k2[5], cols)))
+            return reject(i, "GEMM norm");
+        GemmArgs g{};
+        g.w = weight_view(c->warena + woff, t, rows, int(cols));
+        g.rows = rows;
+        g.cols = int(cols);
+        g.n_tok = int(ntok);
+        g.y = A(k[7]);
+        g.y_stride = int(ys);
+        g.epi = EPI_PLAIN;
+        used = 2;
+        if (flags & GEMVQ_GEMV_SWIGLU) {
+            if (i + 3 >= n) return reject(i, "SwiGLU GEMM without its u GEMM");
+            const uint32_t * u = k + 2 * GEMVQ_CMD_WORDS, * u2 = u + GEMVQ_CMD_WORDS;
+            const uint64_t uoff = uint64_t(u[4]) | (uint64_t(u[5]) << 32);
+            if (u[0] != GEMVQ_OP_GEMM || u[1] != uint32_t(t) || int(u[2]) != rows || u[3] != cols || u[6] != k[6] ||
+                u2[0] != ntok || u2[1] != xs || u2[5] != k2[5] || u2[6] != k2[6] || u2[7] != nflags)
+                return reject(i + 2, "SwiGLU u GEMM must match its g GEMM");
+            if (u2[2] % 16 || u2[2] < uint32_t(rows) || !weight(uoff, t, rows, int(cols)) ||
+                !range(u[7], uint64_t(u2[2]) * (ntok - 1) + rows))
+                return reject(i + 2, "SwiGLU u GEMM weight, stride or range");
+            g.epi = EPI_SWIGLU;
+            g.w2 = weight_view(c->warena + uoff, t, rows, int(cols));
+            g.y = A(u[7]);
+            g.y_stride = int(u2[2]);
+            used = 4;
+        } else if (flags & GEMVQ_GEMV_ADD) {
+            const uint32_t rs = k2[4];
+            if (rs % 16 || rs < uint32_t(rows) || !range(k2[3], uint64_t(rs) * (ntok - 1) + rows)) return reject(i, "GEMM residual");
+            g.epi = EPI_ADD;
+            g.res = A(k2[3]);
+            g.res_stride = int(rs);
+        } else if (flags & GEMVQ_GEMV_SILU) {
+            g.epi = EPI_SILU;
+        }
+        GemmQuantArgs q{};
+        q.x = A(k[6]);
+        q.norm_w = normw ? A(k2[5]) : nullptr;
+        q.q = c->gemm_q;
+        q.d40 = c->gemm_d;
+        q.n_tok = int(ntok);
+        q.n_pad = int((ntok + 15) / 16 * 16);
+        q.cols = int(cols);
+        q.x_stride = int(xs);
+        q.norm = norm ? 1 : 0;
+        q.norm_l2 = (nflags & GEMVQ_NORM_L2) ? 1 : 0;
+        q.eps = bits_f(k2[6]);
+        g.q = c->gemm_q;
+        g.d40 = c->gemm_d;
+        out.push_back(LGemmQ{q});
+        spans.push_back({int(i), int(used)});
+        out.push_back(LGemm{g, t});
+        spans.push_back({int(i), int(used)});
         return true;
     }
 
@@ -617,6 +701,18 @@ std::pair<std::string, uint64_t> describe(const Launch & l, int pos) {
     if (auto * x = std::get_if<LRows>(&l))
         return {"get_rows_kernel", uint64_t(x->a.cols) * 4 + gguf_row_bytes(x->a.type, x->a.cols)};
     if (auto * x = std::get_if<LArgmax>(&l)) return {"argmax_kernel", uint64_t(x->n) * 4};
+    if (auto * x = std::get_if<LGemmQ>(&l)) {
+        const GemmQuantArgs & a = x->a;
+        return {"gemm_quant_kernel", uint64_t(a.n_tok) * a.cols * (4 + 1) + uint64_t(a.n_tok) * (a.cols / 32) * 4 +
+                                         (a.norm_w ? uint64_t(a.cols) * 4 : 0)};
+    }
+    if (auto * x = std::get_if<LGemm>(&l)) {
+        const GemmArgs & a = x->a;
+        const uint64_t w = uint64_t(a.rows) * gguf_row_bytes(x->type, a.cols) * (a.epi == EPI_SWIGLU ? 2 : 1);
+        const uint64_t act = uint64_t(a.n_tok) * (a.cols + (a.cols / 32) * 4);
+        const uint64_t out = uint64_t(a.n_tok) * a.rows * 4 * (a.epi == EPI_ADD ? 2 : 1);
+        return {"gemm_kernel<" + std::to_string(x->type) + ">", w + act + out};
+    }
     return {"next_token_kernel", 32};
 }
 
@@ -634,6 +730,8 @@ hipError_t issue(const std::vector<Launch> & ls, hipStream_t s) {
         else if (auto * x = std::get_if<LRows>(&l)) e = launch_get_rows(x->a, s);
         else if (auto * x = std::get_if<LArgmax>(&l)) e = launch_argmax(x->x, x->n, x->key, s);
         else if (auto * x = std::get_if<LNext>(&l)) e = launch_next_token(x->a, s);
+        else if (auto * x = std::get_if<LGemmQ>(&l)) e = launch_gemm_quant(x->a, s);
+        else if (auto * x = std::get_if<LGemm>(&l)) e = launch_gemm(x->a, x->type, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -670,6 +768,8 @@ gemvq_ctx * gemvq_ctx_create(int device, size_t act_floats, size_t weight_bytes,
     if (e == hipSuccess && weight_bytes) e = hipMalloc(&c->warena, weight_bytes);
     if (e == hipSuccess && state_rows) e = hipMalloc(&c->state, state_rows * 128 * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&c->gdn_raw, size_t(GDN_MAX_HEADS) * 128 * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&c->gemm_q, size_t(GEMM_MAX_TOK) * GEMV_MAXK);
+    if (e == hipSuccess) e = hipMalloc(&c->gemm_d, size_t(GEMM_MAX_TOK) * (GEMV_MAXK / 32) * sizeof(float));
     if (e == hipSuccess && state_rows) e = hipMemset(c->state, 0, state_rows * 128 * sizeof(float));
     if (e != hipSuccess) {
         g_create_error = std::string("gemvq_ctx_create: ") + hipGetErrorString(e);
@@ -700,6 +800,8 @@ void gemvq_ctx_destroy(gemvq_ctx * c) {
     hipFree(c->warena);
     hipFree(c->state);
     hipFree(c->gdn_raw);
+    hipFree(c->gemm_q);
+    hipFree(c->gemm_d);
     hipFree(c->dbg);
     if (c->stream) hipStreamDestroy(c->stream);
     delete c;

@@ -21,7 +21,8 @@ SYNTH_LIB_PATH = os.path.join(PKG, "libgemvq_synth.so")
 Q4_0, Q4_1, Q8_0, Q5_K, Q6_K = 2, 3, 8, 13, 14
 # opcodes (gemvqc16.h:100-111 plus the opcodes of this backend)
 OP_GEMV, OP_RMSNORM, OP_ADD, OP_SILU_MUL, OP_MUL, OP_UNARY, OP_GDN, OP_CONV, OP_STATE_LOAD, OP_ROPE, OP_TRACE = range(1, 12)
-OP_ATTN, OP_GET_ROWS, OP_ARGMAX, OP_NEXT_TOKEN, OP_FILL = 12, 13, 14, 15, 16
+OP_ATTN, OP_GET_ROWS, OP_ARGMAX, OP_NEXT_TOKEN, OP_FILL, OP_GEMM = 12, 13, 14, 15, 16, 17
+GEMM_MAX_TOK = 32
 GEMV_SWIGLU, GEMV_CONV, GEMV_ADD, GEMV_ARGMAX, GEMV_SILU = 0x100, 0x200, 0x400, 0x800, 0x1000
 GDN_WITH_GEMV, GDN_L2_QK, GDN_GATED, GDN_GATES, GDN_WITH_OUT, GDN_Z_SILU = 1, 2, 4, 8, 16, 32
 NORM_L2, NORM_NO_WEIGHT, NORM_DEFER = 1, 2, 4
@@ -113,6 +114,16 @@ def next_token(key: int, tok: int, pos: int, prompt: int, n_prompt: int, out: in
 
 def fill(n: int, y: int, value: float) -> list[int]:
     return cmd(OP_FILL, n, y, fbits(value))
+
+
+def gemm(fmt: int, rows: int, cols: int, w_off: int, x_off: int, y_off: int, n_tok: int, x_stride: int,
+         y_stride: int, flags: int = 0, res_off: int = 0, res_stride: int = 0, norm_w: int = 0, eps: float = 0.0,
+         norm_flags: int = 0) -> list[int]:
+    """Batched GEMV over n_tok token rows (x_stride / y_stride floats apart); norm_flags NORM_DEFER folds a per-token
+    RMS norm (weight at norm_w unless NORM_NO_WEIGHT) into the activation quantization."""
+    out = cmd(OP_GEMM, fmt | flags, rows, cols, w_off & 0xFFFFFFFF, w_off >> 32, x_off, y_off)
+    out += cmd(n_tok, x_stride, y_stride, res_off, res_stride, norm_w, fbits(eps), norm_flags)
+    return out
 
 
 # ---------------------------------------------------------------------------------------------------------------

@@ -53,6 +53,18 @@
  *             the prompt token act_i32[prompt_off + pos + 1] while pos + 1 < n_prompt; act_i32[out_off + pos + 1]
  *             = token; act_i32[tok_off] = token; act_i32[pos_off] = pos + 1; the key is cleared.
  *   FILL      [16, n, y_off, value bits, 0, 0, 0, 0]  y = value.
+ *   GEMM      [17, format | flags, rows, cols, w_off lo, w_off hi, x_off, y_off]
+ *             + [n_tok, x_stride, y_stride, res_off, res_stride, norm_w_off, eps bits, norm_flags]
+ *             The batched GEMV (the reference's planned batched path, ROADMAP.md:78-96; no counterpart in its
+ *             kernel): n_tok (1..GEMVQ_GEMM_MAX_TOK) token rows read each weight row once. Token t's input row is at
+ *             x_off + t * x_stride and its output row at y_off + t * y_stride; each output row equals, bit for bit,
+ *             what a GEMV command on that token row writes. Format 2 Q4_0 or 8 Q8_0, cols a multiple of 512.
+ *             flags: GEMVQ_GEMV_SWIGLU (the next command is the u GEMM with the same format, rows, cols, x_off,
+ *             n_tok, x_stride and norm words and no flags; y = silu(g) * u goes to the u command's y_off /
+ *             y_stride), GEMVQ_GEMV_ADD (y = W x + res, token t's residual at res_off + t * res_stride) or
+ *             GEMVQ_GEMV_SILU. norm_flags GEMVQ_NORM_DEFER: every token row is RMS-normalized first (weight at
+ *             norm_w_off unless GEMVQ_NORM_NO_WEIGHT, GEMVQ_NORM_L2 for the L2 norm, eps), as a deferred RMSNORM
+ *             before a GEMV. The rows are read before any output is written, so y may overlap x.
  */
 #ifndef GEMVQ_HIP_H
 #define GEMVQ_HIP_H
@@ -80,6 +92,8 @@ extern "C" {
 #define GEMVQ_OP_ARGMAX 14u
 #define GEMVQ_OP_NEXT_TOKEN 15u
 #define GEMVQ_OP_FILL 16u
+#define GEMVQ_OP_GEMM 17u
+#define GEMVQ_GEMM_MAX_TOK 32u
 #define GEMVQ_GEMV_SWIGLU 0x100u
 #define GEMVQ_GEMV_CONV 0x200u
 #define GEMVQ_GEMV_ADD 0x400u
@@ -100,7 +114,8 @@ extern "C" {
 #define GEMVQ_MAX_CMDS 4096u
 /* Feature words (gemvqc16.h:126-134 layout, marker 0x6B51 / 0x6B52). */
 #define GEMVQ_FEATURES 0x6B51FFFBu
-#define GEMVQ_FEATURES2 0x6B520003u /* bit0 SILU_MUL sigmoid + strided g, bit1 ATTN/GET_ROWS/ARGMAX/NEXT_TOKEN */
+#define GEMVQ_FEATURES2 0x6B520007u /* bit0 SILU_MUL sigmoid + strided g, bit1 ATTN/GET_ROWS/ARGMAX/NEXT_TOKEN,
+                                       bit2 GEMM */
 
 typedef struct gemvq_ctx gemvq_ctx;
 

@@ -1,0 +1,129 @@
+"""The batched GEMV (GEMM command) on the GPU through the C ABI. Every token's output row must equal, bit for bit, the
+oracle's single-token GEMV of that token's row and the GPU's own GEMV command on it: the same activation quantizer,
+the same exact block terms, the same epilogs, only the block sums come from int8 MFMAs. Covered: Q4_0 and Q8_0;
+1, 5, 16, 17 and 32 tokens (one and two token tiles, padding tokens); row counts that are not a multiple of the
+16-row tile; 2560, 4096 and 12288 columns; strided rows; the SwiGLU pair, residual ADD and SiLU epilogs; the folded
+per-token RMS norm (with and without weight, L2); output rows over the input rows; invalid commands."""
+import numpy as np
+import pytest
+
+from test_gpu_ops import assert_bits
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture()
+def ctx(gq):
+    c = gq.Context(act_floats=1 << 21, weight_bytes=1 << 28)
+    yield c
+    c.close()
+
+
+def up16(n: int) -> int:
+    return (n + 15) // 16 * 16
+
+
+@pytest.mark.parametrize("fmt", [2, 8])
+@pytest.mark.parametrize("rows,cols,ntok", [(1000, 2560, 1), (1000, 2560, 5), (4096, 4096, 16), (333, 4096, 17),
+                                            (512, 12288, 32)])
+def test_gemm_rows_equal_single_token_gemv(gq, orc, ctx, fmt, rows, cols, ntok):
+    xs, ys = cols + 16, up16(rows) + 32  # strided token rows
+    w = gq.matrix(fmt, rows, cols, 3, 10 + fmt, std=0.02)
+    off = ctx.upload(fmt, rows, cols, w)
+    x = gq.normal(3, 11, ntok * xs) * 2.0
+    X, Y, Y1 = 0, up16(ntok * xs), up16(ntok * xs) + up16(ntok * ys)
+    ctx.write(X, x)
+    print(f"[gemm] fmt {fmt} rows {rows} cols {cols} tokens {ntok}", flush=True)
+    assert ctx.run(gq.gemm(fmt, rows, cols, off, X, Y, ntok, xs, ys)) == 0, ctx.error()
+    assert ctx.launch_count() == 2  # the activation quantization, then the weight pass
+    y = ctx.read(Y, ntok * ys).reshape(ntok, ys)[:, :rows]
+    for t in range(ntok):
+        want = orc.fx_gemv(fmt, w, x[t * xs:t * xs + cols], rows, cols)
+        assert_bits(y[t], want, f"token {t}")
+    for t in sorted({0, ntok // 2, ntok - 1}):  # the single-token GEMV command on the same row
+        assert ctx.run(gq.gemv(fmt, rows, cols, off, X + t * xs, Y1)) == 0, ctx.error()
+        assert_bits(ctx.read(Y1, rows), y[t], f"GEMV command, token {t}")
+
+
+@pytest.mark.parametrize("fmt", [2, 8])
+def test_gemm_epilogs_and_norm(gq, orc, ctx, fmt):
+    rows, cols, ntok, eps = 2000, 4096, 9, 1e-6
+    wg, wu = gq.matrix(fmt, rows, cols, 4, 20, std=0.02), gq.matrix(fmt, rows, cols, 4, 21, std=0.02)
+    og, ou = ctx.upload(fmt, rows, cols, wg), ctx.upload(fmt, rows, cols, wu)
+    x = gq.normal(4, 22, ntok * cols) * 3.0
+    nw = gq.uniform(4, 23, cols, 0.5, 1.5)
+    res = gq.normal(4, 24, ntok * rows)
+    X, NW, RES, Y, YG = 0, 1 << 16, 1 << 17, 1 << 18, 1 << 19
+    ctx.write(X, x)
+    ctx.write(NW, nw)
+    ctx.write(RES, res)
+    rows_of = lambda a: [a[t * cols:(t + 1) * cols] for t in range(ntok)]
+    xn = [orc.rownorm(r, nw, cols, 1, eps) for r in rows_of(x)]
+    xl2 = [orc.rownorm(r, None, cols, 1, eps, gq.NORM_L2 | gq.NORM_NO_WEIGHT) for r in rows_of(x)]
+    g = [orc.fx_gemv(fmt, wg, r, rows, cols) for r in xn]
+    u = [orc.fx_gemv(fmt, wu, r, rows, cols) for r in xn]
+    norm = dict(norm_w=NW, eps=eps, norm_flags=gq.NORM_DEFER)
+    # SwiGLU pair on the normalized rows
+    cmd = (gq.gemm(fmt, rows, cols, og, X, YG, ntok, cols, rows, gq.GEMV_SWIGLU, **norm) +
+           gq.gemm(fmt, rows, cols, ou, X, Y, ntok, cols, rows, **norm))
+    assert ctx.run(cmd) == 0, ctx.error()
+    assert ctx.launch_count() == 2
+    y = ctx.read(Y, ntok * rows).reshape(ntok, rows)
+    for t in range(ntok):
+        assert_bits(y[t], orc.silu_mul(g[t], u[t]), f"swiglu token {t}")
+    # residual ADD and SiLU on the same normalized rows
+    assert ctx.run(gq.gemm(fmt, rows, cols, og, X, Y, ntok, cols, rows, gq.GEMV_ADD, RES, rows, **norm)) == 0, ctx.error()
+    y = ctx.read(Y, ntok * rows).reshape(ntok, rows)
+    for t in range(ntok):
+        assert_bits(y[t], g[t] + res[t * rows:(t + 1) * rows], f"add token {t}")
+    assert ctx.run(gq.gemm(fmt, rows, cols, ou, X, Y, ntok, cols, rows, gq.GEMV_SILU, **norm)) == 0, ctx.error()
+    y = ctx.read(Y, ntok * rows).reshape(ntok, rows)
+    for t in range(ntok):
+        assert_bits(y[t], orc.unary(u[t], 1), f"silu token {t}")
+    # the L2 norm without weight
+    assert ctx.run(gq.gemm(fmt, rows, cols, og, X, Y, ntok, cols, rows, eps=eps,
+                           norm_flags=gq.NORM_DEFER | gq.NORM_L2 | gq.NORM_NO_WEIGHT)) == 0, ctx.error()
+    y = ctx.read(Y, ntok * rows).reshape(ntok, rows)
+    for t in range(ntok):
+        assert_bits(y[t], orc.fx_gemv(fmt, wg, xl2[t], rows, cols), f"l2 token {t}")
+    # the same as a deferred RMSNORM + GEMV command per token
+    for t in (0, ntok - 1):
+        c = gq.rmsnorm(cols, X + t * cols, NW, YG, eps, flags=gq.NORM_DEFER) + gq.gemv(fmt, rows, cols, og, YG, YG + 8192)
+        assert ctx.run(c) == 0, ctx.error()
+        assert_bits(ctx.read(YG + 8192, rows), g[t], f"deferred norm GEMV token {t}")
+
+
+def test_gemm_output_over_input(gq, orc, ctx):
+    """Output rows written over the input rows (the quantization reads every row first)."""
+    rows, cols, ntok = 512, 512, 7
+    w = gq.matrix(2, rows, cols, 5, 30)
+    off = ctx.upload(2, rows, cols, w)
+    x = gq.normal(5, 31, ntok * cols)
+    ctx.write(0, x)
+    assert ctx.run(gq.gemm(2, rows, cols, off, 0, 0, ntok, cols, rows)) == 0, ctx.error()
+    y = ctx.read(0, ntok * rows).reshape(ntok, rows)
+    for t in range(ntok):
+        assert_bits(y[t], orc.fx_gemv(2, w, x[t * cols:(t + 1) * cols], rows, cols), f"token {t}")
+
+
+def test_gemm_invalid_commands_rejected(gq, ctx):
+    w = gq.matrix(2, 64, 1024, 6, 40)
+    off = ctx.upload(2, 64, 1024, w)
+    wk = gq.matrix(14, 64, 1024, 6, 41)
+    ok = ctx.upload(14, 64, 1024, wk)
+    good = gq.gemm(2, 64, 1024, off, 0, 65536, 4, 1024, 64)
+    assert ctx.run(good) == 0, ctx.error()
+    bad = [
+        gq.gemm(14, 64, 1024, ok, 0, 65536, 4, 1024, 64),                         # K-quant weights
+        gq.gemm(2, 64, 1024, off, 0, 65536, 0, 1024, 64),                         # no tokens
+        gq.gemm(2, 64, 1024, off, 0, 65536, gq.GEMM_MAX_TOK + 1, 1024, 64),       # too many tokens
+        gq.gemm(2, 64, 1024, off, 0, 65536, 4, 1000, 64),                         # stride below cols
+        gq.gemm(2, 64, 1024, off, 0, 65536, 4, 1024, 48),                         # output stride below rows
+        gq.gemm(2, 64, 1024, off, 0, ctx.act_floats - 64, 4, 1024, 64),          # output out of range
+        gq.gemm(2, 64, 1024, off, 0, 65536, 4, 1024, 64, gq.GEMV_CONV),           # unsupported epilog
+        gq.gemm(2, 64, 1024, off, 0, 65536, 4, 1024, 64, gq.GEMV_SWIGLU),         # SwiGLU without its u
+        gq.gemm(2, 64, 1024, off + 1, 0, 65536, 4, 1024, 64),                     # unknown weight
+        gq.gemm(2, 64, 1024, off, 0, 65536, 4, 1024, 64, gq.GEMV_ADD, 3, 64),     # misaligned residual
+    ]
+    for i, c in enumerate(bad):
+        assert ctx.run(good + c) == 3, (i, ctx.error())  # nothing runs; the first bad command is slot 3

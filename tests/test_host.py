@@ -76,6 +76,8 @@ def test_command_words(gq):
     a = gq.attn(16, 4, 0, 1, 2, 256, 64, 3, 4, 5, 0.0625, 1e-6, 6, 7, 8, gate=256)
     assert len(a) == 16 and a[1] == 16 | (4 << 16) and a[5] == 256 | (64 << 16) and a[7] == 1 and a[15] == 256
     assert all(len(c) == 8 for c in (gq.add(16, 0, 16, 32), gq.fill(16, 0, 1.0), gq.next_token(0, 16, 32, 48, 5, 64)))
+    m = gq.gemm(2, 64, 1024, (7 << 32) | 5, 16, 32, 4, 1024, 64, gq.GEMV_ADD, 48, 64, 80, 1e-6, gq.NORM_DEFER)
+    assert m == [17, 2 | 0x400, 64, 1024, 5, 7, 16, 32, 4, 1024, 64, 48, 64, 80, eps, 4]
 
 
 # ---- synthetic data ---------------------------------------------------------------------------------------------
