@@ -248,6 +248,58 @@ def configs(args) -> int:
     return 0
 
 
+# ---------------------------------------------------------------------------------------------------------------
+# The batched GEMV (GEMM command) on the C5 layer shapes: M tokens per weight read, over rotated weight copies
+# (>= 512 MB) in one graph, against M single-token GEMVs of the same rows.
+def batched(args) -> int:
+    shapes = [("FFN gate/up pair 2x12288x4096 (+ norm)", 12288, 4096, True),
+              ("FFN down 4096x12288 (+ residual)", 4096, 12288, False),
+              ("DeltaNet q/k/v 8192x4096", 8192, 4096, False)]
+    for name, R, K, pair in shapes:
+        w = gq.matrix(gq.Q4_0, R, K, 0, 90 + R % 7, std=0.02)
+        mats = 2 if pair else 1
+        per = w.size * mats
+        copies = max(2, int(np.ceil(520e6 / per)))
+        ctx = gq.Context(act_floats=1 << 22, weight_bytes=per * copies + (1 << 20))
+        offs = [[ctx.upload(gq.Q4_0, R, K, w) for _ in range(mats)] for _ in range(copies)]
+        X, NW, Y, YG, RES = 0, 1 << 19, 1 << 20, 3 << 19, 1 << 21  # 32 rows of up to 12288 floats each
+        ctx.write(X, gq.normal(0, 91, 32 * K))
+        ctx.write(NW, gq.uniform(0, 92, K, 0.5, 1.5))
+        ctx.write(RES, gq.normal(0, 93, 32 * R))
+        norm = dict(norm_w=NW, eps=1e-6, norm_flags=gq.NORM_DEFER) if pair else {}
+
+        def unit(o, m):
+            if pair:
+                return (gq.gemm(gq.Q4_0, R, K, o[0], X, YG, m, K, R, gq.GEMV_SWIGLU, **norm) +
+                        gq.gemm(gq.Q4_0, R, K, o[1], X, Y, m, K, R, **norm))
+            if K == 12288:
+                return gq.gemm(gq.Q4_0, R, K, o[0], X, Y, m, K, R, gq.GEMV_ADD, RES, R)
+            return gq.gemm(gq.Q4_0, R, K, o[0], X, Y, m, K, R)
+
+        def single(o):
+            if pair:
+                return (gq.rmsnorm(K, X, NW, YG, 1e-6, flags=gq.NORM_DEFER) + gq.gemv(gq.Q4_0, R, K, o[0], YG, Y, gq.GEMV_SWIGLU) +
+                        gq.gemv(gq.Q4_0, R, K, o[1], YG, Y))
+            if K == 12288:
+                return gq.gemv(gq.Q4_0, R, K, o[0], X, Y, gq.GEMV_ADD) + gq.add(R, Y, RES, Y)
+            return gq.gemv(gq.Q4_0, R, K, o[0], X, Y)
+
+        g1 = ctx.graph(sum((single(o) for o in offs), []))
+        ctx.replay(g1, 2)
+        t1 = ctx.graph_time_us(g1, 5) / copies
+        for m in (1, 2, 4, 8, 16, 32):
+            g = ctx.graph(sum((unit(o, m) for o in offs), []))
+            ctx.replay(g, 2)
+            t = ctx.graph_time_us(g, 5) / copies
+            ops = 2.0 * R * K * m * mats
+            print(json.dumps({"batched": name, "tokens": m, "us_per_launch_pair": round(t, 3),
+                              "weight_GBps": round(per / t / 1e3, 1), "token_rows_per_us": round(m / t, 3),
+                              "int8_TOPs": round(ops / t / 1e6, 2), "vs_single_token": round(m * t1 / t, 2),
+                              "single_token_us": round(t1, 3), "copies_rotated": copies}), flush=True)
+        ctx.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -265,7 +317,11 @@ def main() -> int:
                          "of rocprofv3 --pmc) and exit")
     ap.add_argument("--configs", action="store_true",
                     help="only time the single-op configurations C1-C4 (one JSON line each) and exit")
+    ap.add_argument("--batched", action="store_true",
+                    help="only time the batched GEMV on the C5 layer shapes at 1..32 tokens and exit")
     args = ap.parse_args()
+    if args.batched:
+        return batched(args)
     if args.copy_probe:
         return copy_probe(args.copy_probe)
     if args.configs:

@@ -12,11 +12,21 @@
 namespace gq {
 namespace {
 
-constexpr int GT = 16;  // rows and tokens per MFMA tile
-constexpr int GU = 4;   // blocks per load round of a wave
+constexpr int GT = 16;                 // rows and tokens per MFMA tile
+constexpr int GU = 16;                 // blocks per round of a workgroup (each wave sums GU / NWAVES of them)
+constexpr int GW = GU / NWAVES;        // blocks per wave per round
+constexpr int ROW_LDS = GU * 16 + 16;  // LDS bytes per staged row: 16 quant bytes per block, padded so that the 16
+                                       // rows of an operand read fall in distinct banks
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));  // native vectors (promoted to registers, unlike uint4)
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Activation scratch: token t's block b, 8-byte group g (quants 4g..4g+3 and 16+4g..16+4g+3) at byte
+// ((t * 4 + g) * nb + b) * 8, so a lane's groups of consecutive blocks are contiguous.
+__device__ __forceinline__ size_t act_group(int tok, int g, int nb, int b) {
+    return ((size_t(tok) * 4 + g) * nb + b) * 8;
+}
 
 // ---- activation: token rows -> Q8_0 blocks in operand order ----
 // Workgroup t quantizes token t exactly as the single-token prologue: thread i holds the 16-float items i, i + NT,
@@ -25,10 +35,11 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 __global__ __launch_bounds__(NT) void gemm_quant_kernel(GemmQuantArgs a) {
     __shared__ Lds s;
     const int tok = blockIdx.x, nb = a.cols / 32, n16 = a.cols / 16;
-    int8_t * q = a.q + size_t(tok) * a.cols;
+    int8_t * q = a.q;
     float * d40 = a.d40 + size_t(tok) * nb;
     if (tok >= a.n_tok) {  // padding tokens: zero quants and scales, whose terms are exactly zero
-        for (int i = threadIdx.x; i < n16; i += NT) reinterpret_cast<uint4 *>(q)[i] = make_uint4(0u, 0u, 0u, 0u);
+        uint4 * z = reinterpret_cast<uint4 *>(q + act_group(tok, 0, nb, 0));
+        for (int i = threadIdx.x; i < n16; i += NT) z[i] = make_uint4(0u, 0u, 0u, 0u);  // 4 groups x nb x 8 bytes
         for (int i = threadIdx.x; i < nb; i += NT) d40[i] = 0.0f;
         return;
     }
@@ -49,19 +60,12 @@ __global__ __launch_bounds__(NT) void gemm_quant_kernel(GemmQuantArgs a) {
         uint32_t packed[4];
         int sum;
         const float d = quantize_half_core(v, packed, sum);
-        // half h of block b: its word g (quants 16h + 4g .. 16h + 4g + 3) goes to byte 8g + 4h of the block
+        // half h of block b: its word g (quants 16h + 4g .. 16h + 4g + 3) is word h of group g
         const int b = i >> 1, h = i & 1;
-        uint32_t * qb = reinterpret_cast<uint32_t *>(q + size_t(b) * 32);
 #pragma unroll
-        for (int g = 0; g < 4; ++g) qb[2 * g + h] = packed[g];
+        for (int g = 0; g < 4; ++g) *reinterpret_cast<uint32_t *>(q + act_group(tok, g, nb, b) + 4 * h) = packed[g];
         if (h == 0) d40[b] = h2f(f2h(d)) * 1099511627776.0f;  // * 2^40, exact
     }
-}
-
-// ---- weights and activation operands of one round (GU blocks) of a wave ----
-__device__ __forceinline__ uint2 ld8(const uint8_t * p) {
-    const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p));
-    return make_uint2(v.x, v.y);
 }
 
 template <int TYPE>
@@ -69,44 +73,42 @@ __device__ __forceinline__ const uint8_t * scale_region(const WeightView & w) {
     return TYPE == T_Q4_0 ? w.b : w.c;
 }
 
-// Lane (r, g) (r = lane % 16, g = lane / 16) holds the A operand of weight row r of the tile and the B operand of
-// token r of each token tile; its results are rows 4g..4g+3 of the tile for token r, so it also loads those rows'
-// scales (4 blocks in 8 bytes) and its token's d * 2^40 (4 blocks in 16 bytes).
-template <int TYPE, bool PAIR, int T>
-struct Round {
-    static constexpr bool Q8 = TYPE == T_Q8_0;
-    uint32_t wa[GU], wb[Q8 ? GU : 1];
-    uint32_t ua[PAIR ? GU : 1], ub[(PAIR && Q8) ? GU : 1];
-    uint2 dw[4], du[PAIR ? 4 : 1];
-    uint2 xq[T][GU];
-    float4 dx[T];
+// One round's weights as loaded by the workgroup: thread t takes block t % 16 of the round in row t / 16 of the tile
+// (its 16 quant bytes, or 32 for Q8_0, and its fp16 scale), so 16 consecutive threads read 256 contiguous bytes of
+// one row.
+// (Named members rather than arrays: the register allocator keeps them in VGPRs.)
+template <int TYPE, bool PAIR>
+struct WRound {
+    v4u g0, g1, u0, u1;  // quant bytes (g1 / u1: the high halves of Q8_0 blocks) of the matrix and of u
+    uint32_t gd, ud;       // fp16 scales
 };
 
-template <int TYPE, bool PAIR, int T>
-__device__ __forceinline__ void load_round(const GemmArgs & a, int nb, int ra, const int * ro, int b, int r, int g,
-                                           Round<TYPE, PAIR, T> & o) {
-#pragma unroll
-    for (int j = 0; j < GU; ++j) {
-        const size_t blk = size_t(ra) * nb + b + j;
-        o.wa[j] = ld4(a.w.a + blk * 16 + 4 * g);
-        if constexpr (TYPE == T_Q8_0) o.wb[j] = ld4(a.w.b + blk * 16 + 4 * g);
-        if constexpr (PAIR) {
-            o.ua[j] = ld4(a.w2.a + blk * 16 + 4 * g);
-            if constexpr (TYPE == T_Q8_0) o.ub[j] = ld4(a.w2.b + blk * 16 + 4 * g);
-        }
+template <int TYPE, bool PAIR>
+__device__ __forceinline__ void load_wround(const GemmArgs & a, int nb, int row, int rd, WRound<TYPE, PAIR> & o) {
+    const size_t blk = size_t(row) * nb + rd * GU + (threadIdx.x & 15);
+    o.g0 = *reinterpret_cast<const v4u *>(a.w.a + blk * 16);
+    if constexpr (TYPE == T_Q8_0) o.g1 = *reinterpret_cast<const v4u *>(a.w.b + blk * 16);
+    o.gd = *reinterpret_cast<const uint16_t *>(scale_region<TYPE>(a.w) + blk * 2);
+    if constexpr (PAIR) {
+        o.u0 = *reinterpret_cast<const v4u *>(a.w2.a + blk * 16);
+        if constexpr (TYPE == T_Q8_0) o.u1 = *reinterpret_cast<const v4u *>(a.w2.b + blk * 16);
+        o.ud = *reinterpret_cast<const uint16_t *>(scale_region<TYPE>(a.w2) + blk * 2);
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const size_t off = (size_t(ro[i]) * nb + b) * 2;
-        o.dw[i] = ld8(scale_region<TYPE>(a.w) + off);
-        if constexpr (PAIR) o.du[i] = ld8(scale_region<TYPE>(a.w2) + off);
-    }
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-        const size_t tok = size_t(t * GT + r);
-#pragma unroll
-        for (int j = 0; j < GU; ++j) o.xq[t][j] = *reinterpret_cast<const uint2 *>(a.q + (tok * nb + b + j) * 32 + 8 * g);
-        o.dx[t] = *reinterpret_cast<const float4 *>(a.d40 + tok * nb + b);
+}
+
+// Thread t's part of a round into an LDS buffer: its 16 quant bytes of every matrix-half at row t / 16, block t % 16
+// (rows padded to ROW_LDS bytes), and its scale.
+template <int TYPE, bool PAIR>
+__device__ __forceinline__ void stage(const WRound<TYPE, PAIR> & w, uint8_t * lq, uint16_t * ld) {
+    constexpr int QH = TYPE == T_Q8_0 ? 2 : 1, QBUF = GT * ROW_LDS;
+    const int t = threadIdx.x, o = (t >> 4) * ROW_LDS + (t & 15) * 16, od = (t >> 4) * GU + (t & 15);
+    *reinterpret_cast<v4u *>(lq + o) = w.g0;
+    if constexpr (QH == 2) *reinterpret_cast<v4u *>(lq + QBUF + o) = w.g1;
+    ld[od] = uint16_t(w.gd);
+    if constexpr (PAIR) {
+        *reinterpret_cast<v4u *>(lq + QH * QBUF + o) = w.u0;
+        if constexpr (QH == 2) *reinterpret_cast<v4u *>(lq + 3 * QBUF + o) = w.u1;
+        ld[GT * GU + od] = uint16_t(w.ud);
     }
 }
 
@@ -124,49 +126,76 @@ __device__ __forceinline__ long a_operand(uint32_t lo, uint32_t hi) {
     return long((uint64_t(w1) << 32) | w0);
 }
 
+// A lane's activation operands of one round: its token's groups g of the wave's GW blocks (GW * 8 contiguous bytes)
+// and their d * 2^40.
+template <int T>
+struct XRound {
+    v4u q[T][GW / 2];
+    v4f d[T];
+};
+
+template <int T>
+__device__ __forceinline__ void load_xround(const GemmArgs & a, int nb, int r, int g, int b, XRound<T> & o) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const int tok = t * GT + r;
+        const v4u * p = reinterpret_cast<const v4u *>(a.q + act_group(tok, g, nb, b));
+#pragma unroll
+        for (int k = 0; k < GW / 2; ++k) o.q[t][k] = p[k];
+        o.d[t] = *reinterpret_cast<const v4f *>(a.d40 + size_t(tok) * nb + b);
+    }
+}
+
+__device__ __forceinline__ float lane_of(const v4f & v, int j) { return v[j]; }
 __device__ __forceinline__ uint32_t half_of(const uint2 & v, int j) {
     const uint32_t w = (j >> 1) ? v.y : v.x;
     return (j & 1) ? w >> 16 : w & 0xffffu;
 }
-__device__ __forceinline__ float lane_of(const float4 & v, int j) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; }
 
-// The round's block terms: per block and token tile one MFMA gives the lane's 4 sums (rows 4g + i, token r); each
-// term is floor(sumi * s) with s = fp16(d_w) * d_x * 2^40 exact in FP32 and the product exact in FP64; the GU terms
-// are summed in FP64 (integers below 2^53) and moved to the int64 totals.
+// The wave's GW blocks of a staged round: per block and token tile one MFMA gives the lane's 4 sums (rows 4g + i,
+// token r); each term is floor(sumi * s) with s = fp16(d_w) * d_x * 2^40 exact in FP32 and the product exact in FP64;
+// the GW terms are summed in FP64 (integers below 2^53) and moved to the int64 totals.
 template <int TYPE, bool PAIR, int T>
-__device__ __forceinline__ void round_terms(const Round<TYPE, PAIR, T> & o, long long (*tot)[4], long long (*totu)[4]) {
-    double acc[T][4], accu[T][4];
+__device__ __forceinline__ void round_terms(const uint8_t * lq, const uint16_t * ld, int wave, int r, int g,
+                                            const XRound<T> & x, long long (*tot)[4], long long (*totu)[4]) {
+    constexpr int NM = PAIR ? 2 : 1, QH = TYPE == T_Q8_0 ? 2 : 1;
+    constexpr int QBUF = GT * ROW_LDS, DBUF = GT * GU;  // bytes of one matrix-half's quants, scales of one matrix
+    double acc[NM][T][4];
 #pragma unroll
-    for (int t = 0; t < T; ++t)
+    for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[t][i] = accu[t][i] = 0.0;
+        for (int t = 0; t < T; ++t)
 #pragma unroll
-    for (int j = 0; j < GU; ++j) {
-        uint32_t hw = 0u, hu = 0u;
-        if constexpr (TYPE == T_Q8_0) hw = o.wb[j];
-        const long aw = a_operand<TYPE>(o.wa[j], hw);
-        long au = 0;
-        if constexpr (PAIR) {
-            if constexpr (TYPE == T_Q8_0) hu = o.ub[j];
-            au = a_operand<TYPE>(o.ua[j], hu);
+            for (int i = 0; i < 4; ++i) acc[m][t][i] = 0.0;
+    uint2 dw[NM][4];  // scales of rows 4g + i for the wave's GW = 4 blocks
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dw[m][i] = *reinterpret_cast<const uint2 *>(ld + m * DBUF + (4 * g + i) * GU + wave * GW);
+#pragma unroll
+    for (int j = 0; j < GW; ++j) {
+        const int blk = wave * GW + j;
+        long aop[NM];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            const uint8_t * p = lq + (m * QH) * QBUF + r * ROW_LDS + blk * 16 + 4 * g;
+            const uint32_t lo = *reinterpret_cast<const uint32_t *>(p);
+            const uint32_t hi = QH == 2 ? *reinterpret_cast<const uint32_t *>(p + QBUF) : 0u;
+            aop[m] = a_operand<TYPE>(lo, hi);
         }
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const long bx = long((uint64_t(o.xq[t][j].y) << 32) | o.xq[t][j].x);
-            const float dx = lane_of(o.dx[t], j);
+            const v4u qv = x.q[t][j >> 1];
+            const long bx = (j & 1) ? long((uint64_t(qv[3]) << 32) | qv[2]) : long((uint64_t(qv[1]) << 32) | qv[0]);
+            const float dx = lane_of(x.d[t], j);
             const v4i zero = {0, 0, 0, 0};
-            const v4i sw = __builtin_amdgcn_mfma_i32_16x16x32_i8(aw, bx, zero, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float s = h2f(half_of(o.dw[i], j)) * dx;
-                acc[t][i] += floor(double(sw[i]) * double(s));
-            }
-            if constexpr (PAIR) {
-                const v4i su = __builtin_amdgcn_mfma_i32_16x16x32_i8(au, bx, zero, 0, 0, 0);
+            for (int m = 0; m < NM; ++m) {
+                const v4i sm = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop[m], bx, zero, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float s = h2f(half_of(o.du[i], j)) * dx;
-                    accu[t][i] += floor(double(su[i]) * double(s));
+                    const float sc = h2f(half_of(dw[m][i], j)) * dx;
+                    acc[m][t][i] += floor(double(sm[i]) * double(sc));
                 }
             }
         }
@@ -175,25 +204,29 @@ __device__ __forceinline__ void round_terms(const Round<TYPE, PAIR, T> & o, long
     for (int t = 0; t < T; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            tot[t][i] += dint_to_i64(acc[t][i]);
-            if constexpr (PAIR) totu[t][i] += dint_to_i64(accu[t][i]);
+            tot[t][i] += dint_to_i64(acc[0][t][i]);
+            if constexpr (PAIR) totu[t][i] += dint_to_i64(acc[PAIR ? 1 : 0][t][i]);
         }
 }
 
-// Workgroup b: rows 16b .. 16b + 15 (clamped loads past the last row, nothing stored for them); wave w sums the
-// blocks w * nb / 4 .. (w + 1) * nb / 4 - 1, and wave 0 adds the other waves' int64 totals (exact in any order),
-// applies the epilog and stores token t's row at y + t * y_stride.
+// Workgroup b: rows 16b .. 16b + 15 (clamped loads past the last row, nothing stored for them), the whole K range in
+// rounds of GU blocks. Round rd + 2's weights are requested while round rd is summed (two rounds in flight) and
+// round rd + 1's are staged in LDS for the next; wave w sums blocks w * GW .. of each round, and wave 0 adds the
+// other waves' int64 totals (exact in any order), applies the epilog and stores token t's row at y + t * y_stride.
+// Loads past the last round repeat the last round (cache hits), so every load is unconditional and the waits stay
+// exact.
 template <int TYPE, bool PAIR, int T>
 __global__ __launch_bounds__(NT) void gemm_kernel(GemmArgs a) {
-    __shared__ long long red[NWAVES - 1][PAIR ? 2 : 1][T][4][WAVE];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int NM = PAIR ? 2 : 1, QH = TYPE == T_Q8_0 ? 2 : 1;
+    constexpr int QBUF = GT * ROW_LDS, DBUF = GT * GU;
+    __shared__ __align__(16) uint8_t lq[2][NM * QH * QBUF];
+    __shared__ __align__(16) uint16_t ld[2][NM * DBUF];
+    __shared__ long long red[NWAVES - 1][NM][T][4][WAVE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int r0 = int(blockIdx.x) * GT;
-    const int ra = min(r0 + r, a.rows - 1);
-    int ro[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ro[i] = min(r0 + 4 * g + i, a.rows - 1);
-    const int nb = a.cols / 32, nbw = nb / NWAVES, b0 = wave * nbw, b1 = b0 + nbw;  // nbw % GU == 0
+    const int nb = a.cols / 32, nr = nb / GU;
+    const int lrow = min(r0 + (tid >> 4), a.rows - 1);
     long long tot[T][4], totu[PAIR ? T : 1][4];
 #pragma unroll
     for (int t = 0; t < T; ++t)
@@ -202,14 +235,30 @@ __global__ __launch_bounds__(NT) void gemm_kernel(GemmArgs a) {
             tot[t][i] = 0;
             totu[PAIR ? t : 0][i] = 0;
         }
-    Round<TYPE, PAIR, T> cur, nxt;
-    load_round<TYPE, PAIR, T>(a, nb, ra, ro, b0, r, g, cur);
-    for (int b = b0; b + GU < b1; b += GU) {  // the next round is requested before this one's terms
-        load_round<TYPE, PAIR, T>(a, nb, ra, ro, b + GU, r, g, nxt);
-        round_terms<TYPE, PAIR, T>(cur, tot, totu);
-        cur = nxt;
+    // rounds alternate between two LDS buffers and two register slots, so every load lands in a free slot
+    WRound<TYPE, PAIR> w0, wa, wb;
+    XRound<T> xa, xb;
+    load_wround<TYPE, PAIR>(a, nb, lrow, 0, w0);
+    load_wround<TYPE, PAIR>(a, nb, lrow, min(1, nr - 1), wb);
+    load_xround<T>(a, nb, r, g, wave * GW, xa);
+    stage<TYPE, PAIR>(w0, lq[0], ld[0]);
+    __syncthreads();
+    int rd = 0;
+    for (; rd + 1 < nr; rd += 2) {
+        // round rd from buffer 0 and xa; round rd + 1's weights (wb) go to buffer 1
+        load_xround<T>(a, nb, r, g, (rd + 1) * GU + wave * GW, xb);
+        load_wround<TYPE, PAIR>(a, nb, lrow, min(rd + 2, nr - 1), wa);
+        round_terms<TYPE, PAIR, T>(lq[0], ld[0], wave, r, g, xa, tot, totu);
+        stage<TYPE, PAIR>(wb, lq[1], ld[1]);
+        __syncthreads();
+        // round rd + 1 from buffer 1 and xb; round rd + 2's weights (wa) go to buffer 0
+        load_xround<T>(a, nb, r, g, min(rd + 2, nr - 1) * GU + wave * GW, xa);
+        load_wround<TYPE, PAIR>(a, nb, lrow, min(rd + 3, nr - 1), wb);
+        round_terms<TYPE, PAIR, T>(lq[1], ld[1], wave, r, g, xb, tot, totu);
+        stage<TYPE, PAIR>(wa, lq[0], ld[0]);
+        __syncthreads();
     }
-    round_terms<TYPE, PAIR, T>(cur, tot, totu);
+    if (rd < nr) round_terms<TYPE, PAIR, T>(lq[0], ld[0], wave, r, g, xa, tot, totu);  // an odd last round
     if (wave > 0) {
 #pragma unroll
         for (int t = 0; t < T; ++t)
@@ -226,9 +275,9 @@ __global__ __launch_bounds__(NT) void gemm_kernel(GemmArgs a) {
         const int tok = t * GT + r;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            long long s = tot[t][i], su = 0;
+            long long sw = tot[t][i], su = 0;
 #pragma unroll
-            for (int k = 0; k < NWAVES - 1; ++k) s += red[k][0][t][i][lane];
+            for (int k = 0; k < NWAVES - 1; ++k) sw += red[k][0][t][i][lane];
             if constexpr (PAIR) {
                 su = totu[t][i];
 #pragma unroll
@@ -236,7 +285,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(GemmArgs a) {
             }
             const int row = r0 + 4 * g + i;
             if (row >= a.rows || tok >= a.n_tok) continue;
-            const float v = fixed_to_float(s);
+            const float v = fixed_to_float(sw);
             float out = v;
             if (PAIR && a.epi == EPI_SWIGLU) {
                 out = (v / (1.0f + expf_(-v))) * fixed_to_float(su);  // gemvqc_ops.h:88-92
