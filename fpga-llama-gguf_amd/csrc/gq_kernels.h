@@ -91,6 +91,7 @@ struct ConvArgs {
     float * y;
     int ch;
     int silu;
+    int n_tok;  // token rows of x and y (ch floats apart), run in order: each token's window ends at its row
 };
 
 struct RopeArgs {
@@ -115,6 +116,8 @@ struct GdnArgs {
     int hv, hk;
     float scale, l2_eps;
     int flags;
+    int n_tok;             // tokens run in order on the same state
+    int s_qkv, s_gb, s_y;  // row strides (floats) between tokens of q / k / v, of g / beta, of y
 };
 
 struct GatedNormArgs {    // per head of 128: y = silu(z) * ((y * s) * w), s = 1 / sqrt(mean(y^2) + eps)

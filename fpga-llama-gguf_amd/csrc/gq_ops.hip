@@ -61,20 +61,28 @@ __global__ void ew_kernel(EwArgs a) {
     }
 }
 
-// ---- CONV opcode (gemvqc_ops.h:387-431): window [state (3), x], summed from t = 0 ----
+// ---- CONV opcode (gemvqc_ops.h:387-431): window [state (3), x], summed from t = 0; n_tok tokens in order, the
+// state moving one place per token ----
 __global__ void conv_kernel(ConvArgs a) {
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
     if (c >= a.ch) return;
-    const float s0 = a.s_src[3 * c], s1 = a.s_src[3 * c + 1], s2 = a.s_src[3 * c + 2], x = a.x[c];
-    float sum = 0.0f;
-    sum += s0 * a.w[4 * c];
-    sum += s1 * a.w[4 * c + 1];
-    sum += s2 * a.w[4 * c + 2];
-    sum += x * a.w[4 * c + 3];
-    a.y[c] = a.silu ? silu_(sum) : sum;
-    a.s_dst[3 * c] = s1;
-    a.s_dst[3 * c + 1] = s2;
-    a.s_dst[3 * c + 2] = x;
+    float s0 = a.s_src[3 * c], s1 = a.s_src[3 * c + 1], s2 = a.s_src[3 * c + 2];
+    const float w0 = a.w[4 * c], w1 = a.w[4 * c + 1], w2 = a.w[4 * c + 2], w3 = a.w[4 * c + 3];
+    for (int t = 0; t < a.n_tok; ++t) {
+        const float x = a.x[size_t(t) * a.ch + c];
+        float sum = 0.0f;
+        sum += s0 * w0;
+        sum += s1 * w1;
+        sum += s2 * w2;
+        sum += x * w3;
+        a.y[size_t(t) * a.ch + c] = a.silu ? silu_(sum) : sum;
+        s0 = s1;
+        s1 = s2;
+        s2 = x;
+    }
+    a.s_dst[3 * c] = s0;
+    a.s_dst[3 * c + 1] = s1;
+    a.s_dst[3 * c + 2] = s2;
 }
 
 // ---- ROPE opcode (gemvqc_ops.h:275-312): NEOX pairs (i, i + n_dims / 2) ----
@@ -101,22 +109,16 @@ __global__ void rope_kernel(RopeArgs a) {
 
 // ---- GDN step (gemvqc_gdn.h:73-187 with the input load of :223-281) ----
 // Workgroup (value head h, chunk of 32 state rows), 128 threads: 16 lanes per row, 8 consecutive floats per lane.
+// The rows of a head are independent given q, k, v, beta and the decay, so a chunk needs nothing from the others.
+// n_tok tokens run in order with the chunk's state in registers (loaded once, stored once).
 constexpr int GDN_ROWS = 32;
 __global__ __launch_bounds__(128) void gdn_kernel(GdnArgs a) {
     const int chunks = 128 / GDN_ROWS;
     const int h = blockIdx.x / chunks, chunk = blockIdx.x % chunks, kh = h % a.hk;
     const int l16 = threadIdx.x & 15, grp = threadIdx.x >> 4;  // 8 row groups
-    float q[8], k[8];
-    {
-        const float4 * qp = reinterpret_cast<const float4 *>(a.q + kh * 128 + 8 * l16);
-        const float4 * kp = reinterpret_cast<const float4 *>(a.k + kh * 128 + 8 * l16);
-        const float4 q0 = qp[0], q1 = qp[1], k0 = kp[0], k1 = kp[1];
-        q[0] = q0.x; q[1] = q0.y; q[2] = q0.z; q[3] = q0.w; q[4] = q1.x; q[5] = q1.y; q[6] = q1.z; q[7] = q1.w;
-        k[0] = k0.x; k[1] = k0.y; k[2] = k0.z; k[3] = k0.w; k[4] = k1.x; k[5] = k1.y; k[6] = k1.z; k[7] = k1.w;
-    }
-    // all state rows of this thread are requested before any is written (src and dst may be the same rows)
     constexpr int IT = GDN_ROWS / 8;
-    float x[IT][8], vj[IT];
+    // all state rows of this thread are requested before any is written (src and dst may be the same rows)
+    float x[IT][8];
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
         const int j = chunk * GDN_ROWS + it * 8 + grp;
@@ -125,67 +127,82 @@ __global__ __launch_bounds__(128) void gdn_kernel(GdnArgs a) {
         const float4 s1 = *reinterpret_cast<const float4 *>(a.src + row + 4);
         x[it][0] = s0.x; x[it][1] = s0.y; x[it][2] = s0.z; x[it][3] = s0.w;
         x[it][4] = s1.x; x[it][5] = s1.y; x[it][6] = s1.z; x[it][7] = s1.w;
-        vj[it] = a.v[h * 128 + j];
     }
-    const float g_raw = a.g[h], b_raw = a.beta[h];
     float dtv = 0.0f, av = 0.0f;
     if (a.flags & 8) {
         dtv = a.dt[h];
         av = a.a[h];
     }
-    if (a.flags & 2) {  // L2 norm of q and k per key head (ggml_l2_norm)
-        float sq[8], sk[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            sq[i] = q[i] * q[i];
-            sk[i] = k[i] * k[i];
+    for (int tk = 0; tk < a.n_tok; ++tk) {
+        const float * qt = a.q + size_t(tk) * a.s_qkv, * kt = a.k + size_t(tk) * a.s_qkv, * vt = a.v + size_t(tk) * a.s_qkv;
+        float q[8], k[8], vj[IT];
+        {
+            const float4 * qp = reinterpret_cast<const float4 *>(qt + kh * 128 + 8 * l16);
+            const float4 * kp = reinterpret_cast<const float4 *>(kt + kh * 128 + 8 * l16);
+            const float4 q0 = qp[0], q1 = qp[1], k0 = kp[0], k1 = kp[1];
+            q[0] = q0.x; q[1] = q0.y; q[2] = q0.z; q[3] = q0.w; q[4] = q1.x; q[5] = q1.y; q[6] = q1.z; q[7] = q1.w;
+            k[0] = k0.x; k[1] = k0.y; k[2] = k0.z; k[3] = k0.w; k[4] = k1.x; k[5] = k1.y; k[6] = k1.z; k[7] = k1.w;
         }
-        const float tq = pair_sum_lanes<16>(tree<8>(sq)), tk = pair_sum_lanes<16>(tree<8>(sk));
-        const float fq = 1.0f / fmaxf(sqrtf(tq), a.l2_eps), fk = 1.0f / fmaxf(sqrtf(tk), a.l2_eps);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            q[i] = q[i] * fq;
-            k[i] = k[i] * fk;
+        for (int it = 0; it < IT; ++it) vj[it] = vt[h * 128 + chunk * GDN_ROWS + it * 8 + grp];
+        const float g_raw = a.g[size_t(tk) * a.s_gb + h], b_raw = a.beta[size_t(tk) * a.s_gb + h];
+        if (a.flags & 2) {  // L2 norm of q and k per key head (ggml_l2_norm)
+            float sq[8], sk[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                sq[i] = q[i] * q[i];
+                sk[i] = k[i] * k[i];
+            }
+            const float tq = pair_sum_lanes<16>(tree<8>(sq)), tkk = pair_sum_lanes<16>(tree<8>(sk));
+            const float fq = 1.0f / fmaxf(sqrtf(tq), a.l2_eps), fk = 1.0f / fmaxf(sqrtf(tkk), a.l2_eps);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                q[i] = q[i] * fq;
+                k[i] = k[i] * fk;
+            }
+        }
+        float gv = g_raw, bt = b_raw;
+        if (a.flags & 8) {  // gates from the raw projections: beta = sigmoid(b), g = softplus(a_raw + dt) * a
+            gv = softplus_(g_raw + dtv) * av;
+            bt = sigmoid_(b_raw);
+        }
+        const float decay = expf_(gv);
+        float dot[IT];
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            float pr[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                x[it][i] = x[it][i] * decay;
+                pr[i] = x[it][i] * k[i];
+            }
+            dot[it] = tree<8>(pr);
+        }
+        pair_sum_lanes_n<16, IT>(dot);
+        float out[IT];
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const float delta = (vj[it] - dot[it]) * bt;
+            float pr[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                x[it][i] = x[it][i] + k[i] * delta;
+                pr[i] = x[it][i] * q[i];
+            }
+            out[it] = tree<8>(pr);
+        }
+        pair_sum_lanes_n<16, IT>(out);
+        if (l16 == 0) {
+#pragma unroll
+            for (int it = 0; it < IT; ++it) a.y[size_t(tk) * a.s_y + h * 128 + chunk * GDN_ROWS + it * 8 + grp] = out[it] * a.scale;
         }
     }
-    float gv = g_raw, bt = b_raw;
-    if (a.flags & 8) {  // gates from the raw projections: beta = sigmoid(b), g = softplus(a_raw + dt) * a
-        gv = softplus_(g_raw + dtv) * av;
-        bt = sigmoid_(b_raw);
-    }
-    const float decay = expf_(gv);
-    float dot[IT];
-#pragma unroll
-    for (int it = 0; it < IT; ++it) {
-        float pr[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            x[it][i] = x[it][i] * decay;
-            pr[i] = x[it][i] * k[i];
-        }
-        dot[it] = tree<8>(pr);
-    }
-    pair_sum_lanes_n<16, IT>(dot);
-    float out[IT];
-#pragma unroll
-    for (int it = 0; it < IT; ++it) {
-        const float delta = (vj[it] - dot[it]) * bt;
-        float pr[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            x[it][i] = x[it][i] + k[i] * delta;
-            pr[i] = x[it][i] * q[i];
-        }
-        out[it] = tree<8>(pr);
-    }
-    pair_sum_lanes_n<16, IT>(out);
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
         const int j = chunk * GDN_ROWS + it * 8 + grp;
         const size_t row = (size_t(h) * 128 + j) * 128 + 8 * l16;
         *reinterpret_cast<float4 *>(a.dst + row) = make_float4(x[it][0], x[it][1], x[it][2], x[it][3]);
         *reinterpret_cast<float4 *>(a.dst + row + 4) = make_float4(x[it][4], x[it][5], x[it][6], x[it][7]);
-        if (l16 == 0) a.y[h * 128 + j] = out[it] * a.scale;
     }
 }
 

@@ -291,15 +291,21 @@ struct Compiler {
                 if (gates && i + 2 >= n) return reject(i, "GDN needs its gates slot");
                 const uint32_t * k3 = gates ? k2 + GEMVQ_CMD_WORDS : nullptr;
                 if (hv == 0 || hk == 0 || hv > GDN_MAX_HEADS || hv % hk) return reject(i, "GDN heads");
-                if (!range(k[2], hk * 128) || !range(k[3], hk * 128) || !range(k[4], hv * 128) || !range(k[5], hv) ||
-                    !range(k[6], hv) || !range(k[7], hv * 128))
+                // tokens (gates slot words 2..4): n_tok, the q / k / v row stride, the g / beta row stride; y and
+                // z rows are packed (hv * 128 floats apart)
+                const uint32_t ntok = gates && k3[2] ? k3[2] : 1, sq = ntok > 1 ? k3[3] : 0, sg = ntok > 1 ? k3[4] : 0;
+                const uint64_t yz = uint64_t(hv) * 128 * (ntok - 1);
+                if (ntok > GEMVQ_GEMM_MAX_TOK || (ntok > 1 && (sq % 16 || sg % 16))) return reject(i, "GDN tokens");
+                if (!range(k[2], uint64_t(sq) * (ntok - 1) + hk * 128) || !range(k[3], uint64_t(sq) * (ntok - 1) + hk * 128) ||
+                    !range(k[4], uint64_t(sq) * (ntok - 1) + hv * 128) || !range(k[5], uint64_t(sg) * (ntok - 1) + hv) ||
+                    !range(k[6], uint64_t(sg) * (ntok - 1) + hv) || !range(k[7], yz + hv * 128))
                     return reject(i, "GDN range");
                 const uint64_t src = k2[0], dst = k2[1];
                 if (src + uint64_t(hv) * 128 > c->state_rows || dst + uint64_t(hv) * 128 > c->state_rows)
                     return reject(i, "GDN state rows");
                 if (src != dst && (src < dst + hv * 128ull && dst < src + hv * 128ull)) return reject(i, "GDN state overlap");
                 if (gates && (!range(k3[0], hv) || !range(k3[1], hv))) return reject(i, "GDN gates range");
-                if ((flags & GEMVQ_GDN_GATED) && (!range(k2[6], 128) || !range(k2[7], hv * 128))) return reject(i, "GDN gated range");
+                if ((flags & GEMVQ_GDN_GATED) && (!range(k2[6], 128) || !range(k2[7], yz + hv * 128))) return reject(i, "GDN gated range");
                 GdnArgs a{};
                 a.q = A(k[2]);
                 a.k = A(k[3]);
@@ -316,8 +322,12 @@ struct Compiler {
                 a.scale = bits_f(k2[2]);
                 a.l2_eps = bits_f(k2[4]);
                 a.flags = int(flags);
+                a.n_tok = int(ntok);
+                a.s_qkv = int(sq);
+                a.s_gb = int(sg);
+                a.s_y = int(hv * 128);
                 const unsigned next = i + (gates ? 3 : 2);
-                if ((flags & GEMVQ_GDN_GATED) && fold_gated(cmds, n, next, k[7], hv * 128)) {
+                if ((flags & GEMVQ_GDN_GATED) && ntok == 1 && fold_gated(cmds, n, next, k[7], hv * 128)) {
                     // the gated norm runs in the next GEMV's activation prologue: the step writes its raw output
                     // to scratch, and that GEMV writes the gated values to y as the norm would have
                     a.y = c->gdn_raw;
@@ -327,7 +337,7 @@ struct Compiler {
                 out.push_back(LGdn{a});
                 spans.push_back({int(i), gates ? 3 : 2});
                 if ((flags & GEMVQ_GDN_GATED) && !gated.on) {
-                    GatedNormArgs g{A(k[7]), A(k2[7]), A(k2[6]), int(hv), bits_f(k2[5]), int(bool(flags & GEMVQ_GDN_Z_SILU))};
+                    GatedNormArgs g{A(k[7]), A(k2[7]), A(k2[6]), int(hv * ntok), bits_f(k2[5]), int(bool(flags & GEMVQ_GDN_Z_SILU))};
                     out.push_back(LGated{g});
                     spans.push_back({int(i), gates ? 3 : 2});
                 }
@@ -335,11 +345,12 @@ struct Compiler {
                 continue;
             }
             case GEMVQ_OP_CONV: {
-                const uint32_t ch = k[1];
-                if (ch == 0 || ch % 16 || !range(k[2], ch) || !range(k[3], 4ull * ch) || !range(k[4], ch) ||
-                    !range(k[5], 3ull * ch) || !range(k[6], 3ull * ch))
+                const uint32_t ch = k[1], ntok = (k[7] >> 16) ? (k[7] >> 16) : 1;  // packed token rows
+                if (ch == 0 || ch % 16 || ntok > GEMVQ_GEMM_MAX_TOK || !range(k[2], uint64_t(ch) * ntok) ||
+                    !range(k[3], 4ull * ch) || !range(k[4], uint64_t(ch) * ntok) || !range(k[5], 3ull * ch) ||
+                    !range(k[6], 3ull * ch))
                     return reject(i, "CONV range");
-                ConvArgs a{A(k[2]), A(k[3]), A(k[5]), A(k[6]), A(k[4]), int(ch), int(k[7] & 1)};
+                ConvArgs a{A(k[2]), A(k[3]), A(k[5]), A(k[6]), A(k[4]), int(ch), int(k[7] & 1), int(ntok)};
                 out.push_back(LConv{a});
                     spans.push_back({int(i), 1});
                 break;
@@ -590,7 +601,8 @@ struct Compiler {
                 if (i + 1 >= n) return reject(i, "GEMV epilog without its command");
                 const uint32_t * e = k + GEMVQ_CMD_WORDS;
                 if (flags & GEMVQ_GEMV_CONV) {
-                    if (e[0] != GEMVQ_OP_CONV || e[1] != uint32_t(rows) || e[2] != k[7] || rows % 16) return reject(i + 1, "CONV epilog");
+                    if (e[0] != GEMVQ_OP_CONV || e[1] != uint32_t(rows) || e[2] != k[7] || rows % 16 || (e[7] >> 16) > 1)
+                        return reject(i + 1, "CONV epilog");
                     if (!range(e[3], 4ull * rows) || !range(e[4], uint64_t(rows)) || !range(e[5], 3ull * rows) ||
                         !range(e[6], 3ull * rows))
                         return reject(i + 1, "CONV epilog range");
@@ -684,12 +696,12 @@ std::pair<std::string, uint64_t> describe(const Launch & l, int pos) {
         return {"norm_kernel", uint64_t(x->a.n) * x->a.rows * 8 + (x->a.w ? uint64_t(x->a.n) * 4 : 0)};
     if (auto * x = std::get_if<LEw>(&l))
         return {"ew_kernel", uint64_t(x->a.n) * 4 * (x->a.op == EW_FILL ? 1 : x->a.b ? 3 : 2)};
-    if (auto * x = std::get_if<LConv>(&l)) return {"conv_kernel", uint64_t(x->a.ch) * 48};
+    if (auto * x = std::get_if<LConv>(&l)) return {"conv_kernel", uint64_t(x->a.ch) * (40 + 8 * x->a.n_tok)};
     if (auto * x = std::get_if<LRope>(&l))
         return {"rope_kernel", uint64_t(x->a.ne0) * x->a.rows * 8 + uint64_t(x->a.n_dims) * 4};
     if (auto * x = std::get_if<LGdn>(&l)) {
         const uint64_t hv = uint64_t(x->a.hv), hk = uint64_t(x->a.hk);
-        return {"gdn_kernel", 2 * hv * 128 * 128 * 4 + (2 * hk + 2 * hv) * 128 * 4 + hv * 16};
+        return {"gdn_kernel", 2 * hv * 128 * 128 * 4 + ((2 * hk + 2 * hv) * 128 * 4 + hv * 16) * uint64_t(x->a.n_tok)};
     }
     if (auto * x = std::get_if<LGated>(&l)) return {"gated_norm_kernel", uint64_t(x->a.heads) * 128 * 12 + 512};
     if (auto * x = std::get_if<LAttn>(&l)) {

@@ -11,6 +11,7 @@
 // then the output norm, the head GEMV with the ARGMAX epilog and NEXT_TOKEN.
 #include "gemvq_qwen35.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -19,7 +20,7 @@
 
 namespace {
 
-constexpr int F32 = 0;
+constexpr int F32 = 0, T_Q4_0 = 2, T_Q8_0 = 8;  // ggml type ids
 
 uint32_t fb(float f) {
     uint32_t b;
@@ -51,6 +52,12 @@ struct gemvq_qwen35 {
              logits = 0, rope = 0, prompt = 0, out = 0;
     std::vector<uint32_t> conv_state;  // per layer
     size_t act_floats = 0;
+    // batched prefill: rows of up to GEMVQ_GEMM_MAX_TOK prompt tokens (token ids and positions one per 16 floats)
+    bool can_batch = false;
+    std::string batch_why;
+    uint32_t bh = 0, bqkv = 0, bcqkv = 0, bz = 0, bbeta = 0, balpha = 0, by = 0, bqg = 0, bk = 0, bv = 0, batt = 0,
+             bffn = 0, bid = 0, bpos = 0;
+    std::vector<int32_t> prompt_ids;
 };
 
 namespace {
@@ -101,6 +108,21 @@ size_t layout(gemvq_qwen35 & m, const gemvq_tensor_desc * tab, int n) {
     m.att = take(size_t(c.n_head) * c.head_dim);
     m.ffn = take(c.n_ff);
     m.logits = take(c.n_vocab);
+    const size_t B = GEMVQ_GEMM_MAX_TOK;
+    m.bh = take(B * c.n_embd);
+    m.bqkv = take(B * ch);
+    m.bcqkv = take(B * ch);
+    m.bz = take(B * hv * S);
+    m.bbeta = take(B * up16(hv));
+    m.balpha = take(B * up16(hv));
+    m.by = take(B * hv * S);
+    m.bqg = take(B * 2 * c.n_head * c.head_dim);
+    m.bk = take(B * c.n_head_kv * c.head_dim);
+    m.bv = take(B * c.n_head_kv * c.head_dim);
+    m.batt = take(B * c.n_head * c.head_dim);
+    m.bffn = take(B * c.n_ff);
+    m.bid = take(B * 16);
+    m.bpos = take(B * 16);
     return off;
 }
 
@@ -118,7 +140,91 @@ struct Emit {
         cmd({GEMVQ_OP_GEMV, uint32_t(t.d->type) | flags, uint32_t(t.d->ne1), uint32_t(t.d->ne0), uint32_t(t.w_off),
              uint32_t(t.w_off >> 32), x, y});
     }
+    // batched GEMV over ntok rows; norm: the per-token RMS norm folded into its quantization
+    void gemm(const T & t, uint32_t x, uint32_t xs, uint32_t y, uint32_t ys, uint32_t ntok, uint32_t flags = 0,
+              uint32_t res = 0, uint32_t rs = 0, const T * norm = nullptr, float eps = 0.0f) {
+        cmd({GEMVQ_OP_GEMM, uint32_t(t.d->type) | flags, uint32_t(t.d->ne1), uint32_t(t.d->ne0), uint32_t(t.w_off),
+             uint32_t(t.w_off >> 32), x, y});
+        cmd({ntok, xs, ys, res, rs, norm ? norm->act_off : 0u, fb(eps), norm ? GEMVQ_NORM_DEFER : 0u});
+    }
 };
+
+// The projections a batched prefill runs as GEMM commands: Q4_0 / Q8_0 with columns a multiple of 512.
+bool batchable(const gemvq_qwen35 & m, std::string & why) {
+    const gemvq_qw_config & c = m.c;
+    if (c.n_embd % 512 || c.n_ff % 512 || (c.ssm_v_heads * c.ssm_head_dim) % 512 || (c.n_head * c.head_dim) % 512) {
+        why = "widths are not multiples of 512";
+        return false;
+    }
+    for (const auto & kv : m.t) {
+        const std::string & n = kv.first;
+        if (n.rfind("blk.", 0) != 0 || !kv.second.d || kv.second.d->type == F32) continue;
+        if (n.find("ssm_conv1d") != std::string::npos) continue;
+        const int t = kv.second.d->type;
+        if ((t != T_Q4_0 && t != T_Q8_0) || kv.second.d->ne0 % 512) {
+            why = "tensor " + n + " has no batched GEMV (Q4_0 / Q8_0, columns a multiple of 512)";
+            return false;
+        }
+    }
+    return true;
+}
+
+// Prompt positions p0 .. p0 + ntok - 1 through every layer (no head): the projections as GEMM commands over the
+// token rows, the conv and the DeltaNet step over the tokens in order, attention token by token (each token's
+// keys and values are in the cache before the next token reads them). The results equal ntok decode steps bit for
+// bit, except that no logits are computed.
+bool build_chunk(const gemvq_qwen35 & m, uint32_t ntok, std::vector<uint32_t> & w) {
+    const gemvq_qw_config & c = m.c;
+    Emit e{w};
+    auto W = [&](const std::string & name) { return &m.t.at(name); };
+    const float eps = c.eps;
+    const uint32_t E = uint32_t(c.n_embd), S = uint32_t(c.ssm_head_dim), hv = uint32_t(c.ssm_v_heads),
+                   hk = uint32_t(c.ssm_k_heads), ch = uint32_t(conv_ch(c)), F = uint32_t(c.n_ff);
+    const uint32_t hd = uint32_t(c.head_dim), qrow = 2 * uint32_t(c.n_head) * hd, kvrow = uint32_t(c.n_head_kv) * hd,
+                   arow = uint32_t(c.n_head) * hd, hvs = hv * S, gb = uint32_t(up16(hv));
+    const T * emb = W("token_embd.weight");
+    for (uint32_t i = 0; i < ntok; ++i)
+        e.cmd({GEMVQ_OP_GET_ROWS, uint32_t(emb->d->type), uint32_t(emb->d->ne1), uint32_t(emb->d->ne0),
+               uint32_t(emb->w_off), uint32_t(emb->w_off >> 32), m.bid + 16 * i, m.bh + i * E});
+    int slot = 0;
+    for (int il = 0; il < c.n_layer; ++il) {
+        const std::string p = "blk." + std::to_string(il) + ".";
+        const T * an = W(p + "attn_norm.weight");
+        const T * pn = W(p + "post_attention_norm.weight");
+        if (is_attn(c, il)) {
+            e.gemm(*W(p + "attn_q.weight"), m.bh, E, m.bqg, qrow, ntok, 0, 0, 0, an, eps);
+            e.gemm(*W(p + "attn_k.weight"), m.bh, E, m.bk, kvrow, ntok, 0, 0, 0, an, eps);
+            e.gemm(*W(p + "attn_v.weight"), m.bh, E, m.bv, kvrow, ntok, 0, 0, 0, an, eps);
+            for (uint32_t i = 0; i < ntok; ++i) {
+                e.cmd({GEMVQ_OP_ATTN, uint32_t(c.n_head) | (uint32_t(c.n_head_kv) << 16), m.bqg + i * qrow,
+                       uint32_t(m.kv[il]), m.batt + i * arow, hd | (uint32_t(c.n_rot) << 16), m.bpos + 16 * i, 1u});
+                e.cmd({m.bk + i * kvrow, m.bv + i * kvrow, fb(1.0f / std::sqrt(float(c.head_dim))), fb(eps),
+                       W(p + "attn_q_norm.weight")->act_off, W(p + "attn_k_norm.weight")->act_off, m.rope,
+                       m.bqg + i * qrow + hd});
+            }
+            e.gemm(*W(p + "attn_output.weight"), m.batt, arow, m.bh, E, ntok, GEMVQ_GEMV_ADD, m.bh, E);
+        } else {
+            e.gemm(*W(p + "attn_qkv.weight"), m.bh, E, m.bqkv, ch, ntok, 0, 0, 0, an, eps);
+            e.cmd({GEMVQ_OP_CONV, ch, m.bqkv, W(p + "ssm_conv1d.weight")->act_off, m.bcqkv, m.conv_state[il],
+                   m.conv_state[il], 1u | (ntok << 16)});
+            e.gemm(*W(p + "attn_gate.weight"), m.bh, E, m.bz, hvs, ntok, GEMVQ_GEMV_SILU, 0, 0, an, eps);
+            e.gemm(*W(p + "ssm_beta.weight"), m.bh, E, m.bbeta, gb, ntok, 0, 0, 0, an, eps);
+            e.gemm(*W(p + "ssm_alpha.weight"), m.bh, E, m.balpha, gb, ntok, 0, 0, 0, an, eps);
+            const uint32_t row = uint32_t(slot) * hv * 128u;
+            const uint32_t flags = GEMVQ_GDN_L2_QK | GEMVQ_GDN_GATED | GEMVQ_GDN_GATES | GEMVQ_GDN_Z_SILU;
+            e.cmd({GEMVQ_OP_GDN, hv | (hk << 16), m.bcqkv, m.bcqkv + hk * S, m.bcqkv + 2 * hk * S, m.balpha, m.bbeta, m.by});
+            e.cmd({row, row, fb(1.0f / std::sqrt(float(S))), flags, fb(eps), fb(eps), W(p + "ssm_norm.weight")->act_off,
+                   m.bz});
+            e.cmd({W(p + "ssm_dt.bias")->act_off, W(p + "ssm_a")->act_off, ntok, ch, gb});
+            e.gemm(*W(p + "ssm_out.weight"), m.by, hvs, m.bh, E, ntok, GEMVQ_GEMV_ADD, m.bh, E);
+            ++slot;
+        }
+        e.gemm(*W(p + "ffn_gate.weight"), m.bh, E, m.bffn, F, ntok, GEMVQ_GEMV_SWIGLU, 0, 0, pn, eps);
+        e.gemm(*W(p + "ffn_up.weight"), m.bh, E, m.bffn, F, ntok, 0, 0, 0, pn, eps);
+        e.gemm(*W(p + "ffn_down.weight"), m.bffn, F, m.bh, E, ntok, GEMVQ_GEMV_ADD, m.bh, E);
+    }
+    return true;
+}
 
 bool build_commands(gemvq_qwen35 & m, std::string & err) {
     const gemvq_qw_config & c = m.c;
@@ -292,6 +398,7 @@ gemvq_qwen35 * gemvq_qwen35_create(gemvq_ctx * ctx, const gemvq_qw_config * cfg,
         delete m;
         return nullptr;
     }
+    m->can_batch = batchable(*m, m->batch_why);
     return m;  // the per-token graph is captured by the first gemvq_qwen35_step
 }
 
@@ -321,6 +428,7 @@ int gemvq_qwen35_reset(gemvq_qwen35 * m, const int32_t * prompt, int n) {
     if (!st) st = gemvq_act_write(ctx, 16, scal, 48);
     if (!st) st = gemvq_act_write(ctx, m->tok, &prompt[0], 1);
     if (st) return st;
+    m->prompt_ids.assign(prompt, prompt + n);
     // NEXT_TOKEN reads the prompt length from its command; the graph is captured again when it changes
     const size_t last = m->cmds.size() - GEMVQ_CMD_WORDS;
     if (m->cmds[last + 5] != uint32_t(n)) {
@@ -328,6 +436,41 @@ int gemvq_qwen35_reset(gemvq_qwen35 * m, const int32_t * prompt, int n) {
         if (m->graph >= 0) gemvq_graph_destroy(ctx, m->graph);
         m->graph = -1;
     }
+    return st;
+}
+
+int gemvq_qwen35_prefill(gemvq_qwen35 * m, int n) {
+    if (!m || n < 0) return GEMVQ_EINVAL;
+    gemvq_ctx * ctx = m->ctx;
+    if (n == 0) return 0;
+    if (!m->can_batch) return set_err(ctx, "gemvq_qwen35_prefill: " + m->batch_why);
+    int32_t pos = 0;
+    int st = gemvq_sync(ctx);
+    if (!st) st = gemvq_act_read(ctx, m->pos, &pos, 1);
+    if (st) return st;
+    const int np = int(m->prompt_ids.size());
+    if (pos < 0 || pos + n > np - 1) return set_err(ctx, "gemvq_qwen35_prefill: positions past the last prompt token but one");
+    std::vector<uint32_t> w;
+    for (int p0 = pos; p0 < pos + n && !st;) {
+        const int nt = std::min<int>(GEMVQ_GEMM_MAX_TOK, pos + n - p0);
+        std::vector<int32_t> slots(size_t(32) * GEMVQ_GEMM_MAX_TOK, 0);  // ids, then positions, one per 16 floats
+        for (int i = 0; i < nt; ++i) {
+            slots[size_t(16) * i] = m->prompt_ids[size_t(p0 + i)];
+            slots[size_t(16) * (GEMVQ_GEMM_MAX_TOK + i)] = p0 + i;
+        }
+        st = gemvq_act_write(ctx, m->bid, slots.data(), size_t(16) * GEMVQ_GEMM_MAX_TOK);
+        if (!st) st = gemvq_act_write(ctx, m->bpos, slots.data() + size_t(16) * GEMVQ_GEMM_MAX_TOK, size_t(16) * GEMVQ_GEMM_MAX_TOK);
+        w.clear();
+        build_chunk(*m, uint32_t(nt), w);
+        if (!st) st = gemvq_run(ctx, w.data(), unsigned(w.size() / GEMVQ_CMD_WORDS));
+        p0 += nt;
+    }
+    if (st) return st;
+    // what the steps' NEXT_TOKEN would have left: the next prompt token at the next position, the ids so far
+    const int32_t end = pos + n, tok = m->prompt_ids[size_t(end)];
+    st = gemvq_act_write(ctx, m->pos, &end, 1);
+    if (!st) st = gemvq_act_write(ctx, m->tok, &tok, 1);
+    if (!st) st = gemvq_act_write(ctx, m->out + size_t(pos) + 1, m->prompt_ids.data() + pos + 1, size_t(n));
     return st;
 }
 

@@ -188,6 +188,7 @@ def _lib():
         gq._c_fn(lib, "gemvq_qwen35_destroy", None, vp)
         gq._c_fn(lib, "gemvq_qwen35_reset", C.c_int, vp, vp, C.c_int)
         gq._c_fn(lib, "gemvq_qwen35_step", C.c_int, vp, C.c_int)
+        gq._c_fn(lib, "gemvq_qwen35_prefill", C.c_int, vp, C.c_int)
         gq._c_fn(lib, "gemvq_qwen35_tokens", C.c_int, vp, vp, C.c_int)
         gq._c_fn(lib, "gemvq_qwen35_logits", C.c_int, vp, vp)
         gq._c_fn(lib, "gemvq_qwen35_hidden", C.c_int, vp, vp)
@@ -236,6 +237,15 @@ class Model:
 
     def step(self, n: int = 1) -> None:
         self._ok(self.lib.gemvq_qwen35_step(self.h, n), "step")
+
+    def prefill(self, n: int) -> bool:
+        """Runs the next n prompt positions batched (GEMM commands); False (nothing run) when the model's
+        projections have no batched form, in which case `step(n)` does the same work."""
+        st = self.lib.gemvq_qwen35_prefill(self.h, n)
+        if st == gq.EINVAL and any(w in self.ctx.error() for w in ("no batched GEMV", "multiples of 512")):
+            return False
+        self._ok(st, "prefill")
+        return True
 
     def sync(self) -> None:
         self.ctx.sync()

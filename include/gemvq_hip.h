@@ -30,10 +30,14 @@
  *             stride in 16-float words (0: packed).
  *   ADD 3, SILU_MUL 4, MUL 5, UNARY 6, CONV 8, ROPE 10 as gemvqc16.h:52-59, 85-91; ROPE word 7 (pos_off): if
  *             nonzero, cs_off is a table of n_dims floats per position and the row is selected by the int32
- *             position stored at act[pos_off].
+ *             position stored at act[pos_off]. CONV word 7 bits 31:16 (0 or 1: one token): n_tok packed token
+ *             rows of x and y run in order, each window ending at its token (up to GEMVQ_GEMM_MAX_TOK).
  *   GDN       [7, H_v | H_k << 16, q_off, k_off, v_off, g_off, beta_off, y_off]
  *             + [src_row, dst_row, scale bits, flags, l2_eps bits, rms_eps bits, w_off, z_off]
- *             (+ [dt_off, a_off, 0...] with GEMVQ_GDN_GATES) as gemvqc16.h:60-81; GEMVQ_GDN_WITH_GEMV and
+ *             (+ [dt_off, a_off, n_tok, qkv_stride, gb_stride, 0, 0, 0] with GEMVQ_GDN_GATES) as gemvqc16.h:60-81;
+ *             n_tok (0 or 1: one token; up to GEMVQ_GEMM_MAX_TOK) tokens run in order on the same state, token t's
+ *             q / k / v at t * qkv_stride, its g / beta at t * gb_stride, its y and z rows packed (hv * 128 apart);
+ *             the gated norm then covers every token's heads. GEMVQ_GDN_WITH_GEMV and
  *             GEMVQ_GDN_WITH_OUT are accepted (the results are those of the commands run one by one).
  *             GEMVQ_GDN_Z_SILU (32): z_off already holds silu(z), the gated norm multiplies by it directly. A GDN with
  *             the gated norm followed by a Q4_0 / Q8_0 GEMV reading its y applies the norm in that GEMV's activation

@@ -120,3 +120,66 @@ def test_c5_greedy_128_steps_matches_oracle(gq, orc, q35):
         lg = m.logits()
     assert np.array_equal(got, want), f"first mismatch at {np.nonzero(got != want)[0][:3]}"
     assert np.array_equal(lg.view(np.uint32), lo.view(np.uint32))
+
+
+def _decode_state(m, cfg, npos):
+    """DeltaNet states, the attention layers' K/V up to npos, and the device's token ids up to npos + 1."""
+    gdn_layers = sum(1 for il in range(cfg.n_layer) if (il + 1) % cfg.attn_interval != 0)
+    st = m.ctx.state_read(0, gdn_layers * cfg.ssm_v_heads * 128)
+    kvs = [m.ctx.kv_read(i, 0, npos, cfg.n_head_kv * cfg.head_dim)
+           for i in range(cfg.n_layer - gdn_layers)]
+    return st, kvs, m.tokens(npos + 1)
+
+
+def test_batched_prefill_equals_decode_steps(gq, q35):
+    """The batched prefill (GEMM commands over chunks of up to 32 prompt tokens, the conv and DeltaNet step over the
+    tokens in order, attention token by token) leaves the model where the decode steps do, bit for bit: DeltaNet
+    states, KV cache, token ids; and the generation that follows has identical tokens, logits and hidden state. C5
+    widths, 4 layers (3 DeltaNet + 1 attention); 44 prompt positions = chunks of 32 and 12; and a prefill split
+    around decode steps."""
+    cfg = q35.Config(n_layer=4, n_ctx=96)
+    blob = q35.generate(cfg, seed=1)
+    prompt = q35.prompt_ids(cfg, 45, seed=1)
+    n_gen = 12
+    with q35.Model(blob) as m:
+        m.reset(prompt)
+        m.step(len(prompt) - 1)
+        s_steps = _decode_state(m, cfg, len(prompt) - 1)
+        m.step(n_gen)
+        t_steps, l_steps, h_steps = m.tokens(len(prompt) + n_gen), m.logits(), m.hidden()
+
+        m.reset(prompt)
+        print("[prefill] 44 positions", flush=True)
+        assert m.prefill(len(prompt) - 1)
+        s_pre = _decode_state(m, cfg, len(prompt) - 1)
+        assert np.array_equal(s_pre[0].view(np.uint32), s_steps[0].view(np.uint32)), "DeltaNet states"
+        for a, b in zip(s_pre[1], s_steps[1]):
+            assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1]), "KV cache"
+        assert np.array_equal(s_pre[2], s_steps[2]), "token ids"
+        m.step(n_gen)
+        assert np.array_equal(m.tokens(len(prompt) + n_gen), t_steps)
+        assert np.array_equal(m.logits().view(np.uint32), l_steps.view(np.uint32))
+        assert np.array_equal(m.hidden().view(np.uint32), h_steps.view(np.uint32))
+
+        m.reset(prompt)  # prefill, steps, prefill again: positions read back from the device
+        print("[prefill] split 7 + 3 steps + 34", flush=True)
+        assert m.prefill(7)
+        m.step(3)
+        assert m.prefill(len(prompt) - 1 - 10)
+        m.step(n_gen)
+        assert np.array_equal(m.tokens(len(prompt) + n_gen), t_steps)
+        assert np.array_equal(m.logits().view(np.uint32), l_steps.view(np.uint32))
+        m.reset(prompt)
+        with pytest.raises(gq.GemvqError):
+            m.prefill(len(prompt))  # the last prompt token is a decode step (its logits pick the first new token)
+
+
+def test_batched_prefill_declines_unbatchable_models(gq, q35):
+    """Projections without a batched form (columns not a multiple of 512): prefill runs nothing and says so."""
+    cfg = q35.tiny(n_layer=4)
+    blob = q35.generate(cfg, seed=2)
+    with q35.Model(blob) as m:
+        m.reset(q35.prompt_ids(cfg, 10, seed=2))
+        assert not m.prefill(5)
+        m.step(9)
+        assert m.tokens(10)[9] >= 0
