@@ -208,11 +208,16 @@ struct Compiler {
                !(g[1] & GEMVQ_GEMV_SWIGLU);  // the gated prologue has no SwiGLU-pair variant
     }
 
+    // The activation rows a batched GEMV quantized last, while nothing since could have changed them: the next GEMM
+    // on the same rows (same norm) reuses the scratch instead of quantizing again.
+    struct LastQuant { bool on = false; GemmQuantArgs q; uint32_t x_off, x_len; } lastq;
+
     bool compile(const uint32_t * cmds, unsigned n) {
         struct Deferred { bool on = false; uint32_t n, x, w, y; float eps; uint32_t flags; } defer;
         for (unsigned i = 0; i < n;) {
             const uint32_t * k = cmds + size_t(i) * GEMVQ_CMD_WORDS;
             const uint32_t op = k[0];
+            if (op != GEMVQ_OP_GEMM) lastq.on = false;
             switch (op) {
             case GEMVQ_OP_GEMV: {
                 unsigned used = 0;
@@ -535,10 +540,23 @@ struct Compiler {
         q.eps = bits_f(k2[6]);
         g.q = c->gemm_q;
         g.d40 = c->gemm_d;
-        out.push_back(LGemmQ{q});
-        spans.push_back({int(i), int(used)});
+        const uint32_t x_len = xs * (ntok - 1) + cols;
+        const bool same = lastq.on && lastq.x_off == k[6] && lastq.x_len == x_len && lastq.q.n_tok == q.n_tok &&
+                          lastq.q.cols == q.cols && lastq.q.x_stride == q.x_stride && lastq.q.norm == q.norm &&
+                          lastq.q.norm_l2 == q.norm_l2 && lastq.q.norm_w == q.norm_w && lastq.q.eps == q.eps;
+        if (!same) {
+            out.push_back(LGemmQ{q});
+            spans.push_back({int(i), int(used)});
+            lastq = {true, q, k[6], x_len};
+        }
         out.push_back(LGemm{g, t});
         spans.push_back({int(i), int(used)});
+        // outputs written over the quantized rows (or the norm weight) end the reuse
+        const uint32_t y_off = uint32_t(g.y - c->act), y_len = uint32_t(g.y_stride) * (ntok - 1) + uint32_t(rows);
+        const bool hits_x = y_off < lastq.x_off + lastq.x_len && lastq.x_off < y_off + y_len;
+        const uint32_t w_off = q.norm_w ? uint32_t(q.norm_w - c->act) : 0;
+        const bool hits_w = q.norm_w && y_off < w_off + cols && w_off < y_off + y_len;
+        if (hits_x || hits_w) lastq.on = false;
         return true;
     }
 

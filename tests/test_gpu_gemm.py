@@ -127,3 +127,32 @@ def test_gemm_invalid_commands_rejected(gq, ctx):
     ]
     for i, c in enumerate(bad):
         assert ctx.run(good + c) == 3, (i, ctx.error())  # nothing runs; the first bad command is slot 3
+
+
+def test_gemm_reuses_quantized_rows_until_overwritten(gq, orc, ctx):
+    """Consecutive GEMMs on the same rows and norm quantize them once; a GEMM whose output overwrites those rows
+    makes the next one quantize again (its result is that of the new rows)."""
+    rows, cols, ntok = 512, 512, 6
+    w1, w2 = gq.matrix(2, rows, cols, 7, 50), gq.matrix(8, rows, cols, 7, 51)
+    o1, o2 = ctx.upload(2, rows, cols, w1), ctx.upload(8, rows, cols, w2)
+    x = gq.normal(7, 52, ntok * cols)
+    X, Y1, Y2 = 0, 8192, 16384
+    ctx.write(X, x)
+    assert ctx.run(gq.gemm(2, rows, cols, o1, X, Y1, ntok, cols, rows) +
+                   gq.gemm(8, rows, cols, o2, X, Y2, ntok, cols, rows)) == 0, ctx.error()
+    assert ctx.launch_count() == 3  # one quantization, two weight passes
+    xr = [x[t * cols:(t + 1) * cols] for t in range(ntok)]
+    y1 = ctx.read(Y1, ntok * rows).reshape(ntok, rows)
+    y2 = ctx.read(Y2, ntok * rows).reshape(ntok, rows)
+    for t in range(ntok):
+        assert_bits(y1[t], orc.fx_gemv(2, w1, xr[t], rows, cols), f"first GEMM token {t}")
+        assert_bits(y2[t], orc.fx_gemv(8, w2, xr[t], rows, cols), f"second GEMM token {t}")
+    # the first GEMM now writes over x (rows == cols): the second must see the new rows
+    ctx.write(X, x)
+    assert ctx.run(gq.gemm(2, rows, cols, o1, X, X, ntok, cols, rows) +
+                   gq.gemm(8, rows, cols, o2, X, Y2, ntok, cols, rows)) == 0, ctx.error()
+    assert ctx.launch_count() == 4
+    y2 = ctx.read(Y2, ntok * rows).reshape(ntok, rows)
+    for t in range(ntok):
+        xn = orc.fx_gemv(2, w1, xr[t], rows, cols)
+        assert_bits(y2[t], orc.fx_gemv(8, w2, xn, rows, cols), f"after overwrite token {t}")
