@@ -14,8 +14,13 @@ constexpr int WAVE = 64;
 __device__ __forceinline__ float h2f(uint32_t h) { return float(__builtin_bit_cast(_Float16, uint16_t(h))); }
 
 // binary32 -> binary16, round to nearest even, subnormal results rounded, overflow to infinity (gemvq_ref.h:32-52):
-// the hardware conversion in the default rounding mode.
-__device__ __forceinline__ uint32_t f2h(float f) { return __builtin_bit_cast(uint16_t, _Float16(f)); }
+// the hardware conversion in the default rounding mode, of the binary32 value. The empty asm makes that value exist:
+// without it the compiler may fold a product into the conversion (v_fma_mixlo_f16, one rounding of the exact
+// product), which differs from rounding the FP32 product first whenever that product lands on an fp16 tie.
+__device__ __forceinline__ uint32_t f2h(float f) {
+    __asm__("" : "+v"(f));
+    return __builtin_bit_cast(uint16_t, _Float16(f));
+}
 
 // exp: Cody-Waite reduction x = n ln2 + r (ln2 in a 15-bit and a low part), Taylor series of e^r to r^7/7! by
 // Horner with fused multiply-adds, exact scaling by 2^n; results below the normal range flush to +0.

@@ -5,8 +5,9 @@
 // rounded to FP32 once (gemvqw_engine.h:352-445), the same epilogs. Only the block sums change hands: one int8
 // v_mfma_i32_16x16x32_i8 per 32-weight block gives them for 16 rows x 16 tokens. A block's 32 quants may be
 // permuted as long as the weight and the activation operands agree, so lane group g (lanes 16g..16g+15) takes quants
-// 4g..4g+3 and 16+4g..16+4g+3: Q4_0 packs exactly those as the low and high nibbles of quant bytes 4g..4g+3, Q8_0
-// holds them as bytes 4g..4g+3 of its two 16-byte halves, and the activation quantizer stores them in that order.
+// 4g..4g+3 and 16+4g..16+4g+3: Q4_0 and Q4_1 pack exactly those as the low and high nibbles of quant bytes 4g..4g+3,
+// Q8_0 holds them as bytes 4g..4g+3 of its two 16-byte halves, and the activation quantizer stores them in that
+// order. Q4_1 adds the term floor(m_w * s_x * 2^40) with the Q8_1 s_x of each activation block (gemvq_ref.h:194-229).
 #include "gq_gemv_impl.h"
 
 namespace gq {
@@ -36,11 +37,11 @@ __global__ __launch_bounds__(NT) void gemm_quant_kernel(GemmQuantArgs a) {
     __shared__ Lds s;
     const int tok = blockIdx.x, nb = a.cols / 32, n16 = a.cols / 16;
     int8_t * q = a.q;
-    float * d40 = a.d40 + size_t(tok) * nb;
+    float * d40 = a.d40 + size_t(tok) * nb, * s40 = a.s40 + size_t(tok) * nb;
     if (tok >= a.n_tok) {  // padding tokens: zero quants and scales, whose terms are exactly zero
         uint4 * z = reinterpret_cast<uint4 *>(q + act_group(tok, 0, nb, 0));
         for (int i = threadIdx.x; i < n16; i += NT) z[i] = make_uint4(0u, 0u, 0u, 0u);  // 4 groups x nb x 8 bytes
-        for (int i = threadIdx.x; i < nb; i += NT) d40[i] = 0.0f;
+        for (int i = threadIdx.x; i < nb; i += NT) d40[i] = s40[i] = 0.0f;
         return;
     }
     const float * x = a.x + size_t(tok) * a.x_stride;
@@ -64,13 +65,18 @@ __global__ __launch_bounds__(NT) void gemm_quant_kernel(GemmQuantArgs a) {
         const int b = i >> 1, h = i & 1;
 #pragma unroll
         for (int g = 0; g < 4; ++g) *reinterpret_cast<uint32_t *>(q + act_group(tok, g, nb, b) + 4 * h) = packed[g];
-        if (h == 0) d40[b] = h2f(f2h(d)) * 1099511627776.0f;  // * 2^40, exact
+        if (h == 0) {
+            d40[b] = h2f(f2h(d)) * 1099511627776.0f;                   // * 2^40, exact
+            s40[b] = h2f(f2h(float(sum) * d)) * 1099511627776.0f;      // ggml quantize_row_q8_1: fp16(sum * d)
+        }
     }
 }
 
+// Per-block scale words: fp16 d (Q4_0 in region b, Q8_0 in region c), or d | m << 16 (Q4_1, region b).
 template <int TYPE>
-__device__ __forceinline__ const uint8_t * scale_region(const WeightView & w) {
-    return TYPE == T_Q4_0 ? w.b : w.c;
+__device__ __forceinline__ uint32_t load_scale(const WeightView & w, size_t blk) {
+    if constexpr (TYPE == T_Q4_1) return *reinterpret_cast<const uint32_t *>(w.b + blk * 4);
+    return *reinterpret_cast<const uint16_t *>((TYPE == T_Q4_0 ? w.b : w.c) + blk * 2);
 }
 
 // One round's weights as loaded by the workgroup: thread t takes block t % 16 of the round in row t / 16 of the tile
@@ -88,35 +94,39 @@ __device__ __forceinline__ void load_wround(const GemmArgs & a, int nb, int row,
     const size_t blk = size_t(row) * nb + rd * GU + (threadIdx.x & 15);
     o.g0 = *reinterpret_cast<const v4u *>(a.w.a + blk * 16);
     if constexpr (TYPE == T_Q8_0) o.g1 = *reinterpret_cast<const v4u *>(a.w.b + blk * 16);
-    o.gd = *reinterpret_cast<const uint16_t *>(scale_region<TYPE>(a.w) + blk * 2);
+    o.gd = load_scale<TYPE>(a.w, blk);
     if constexpr (PAIR) {
         o.u0 = *reinterpret_cast<const v4u *>(a.w2.a + blk * 16);
         if constexpr (TYPE == T_Q8_0) o.u1 = *reinterpret_cast<const v4u *>(a.w2.b + blk * 16);
-        o.ud = *reinterpret_cast<const uint16_t *>(scale_region<TYPE>(a.w2) + blk * 2);
+        o.ud = load_scale<TYPE>(a.w2, blk);
     }
 }
 
 // Thread t's part of a round into an LDS buffer: its 16 quant bytes of every matrix-half at row t / 16, block t % 16
 // (rows padded to ROW_LDS bytes), and its scale.
 template <int TYPE, bool PAIR>
-__device__ __forceinline__ void stage(const WRound<TYPE, PAIR> & w, uint8_t * lq, uint16_t * ld) {
+__device__ __forceinline__ void stage(const WRound<TYPE, PAIR> & w, uint8_t * lq, uint32_t * ld) {
     constexpr int QH = TYPE == T_Q8_0 ? 2 : 1, QBUF = GT * ROW_LDS;
     const int t = threadIdx.x, o = (t >> 4) * ROW_LDS + (t & 15) * 16, od = (t >> 4) * GU + (t & 15);
     *reinterpret_cast<v4u *>(lq + o) = w.g0;
     if constexpr (QH == 2) *reinterpret_cast<v4u *>(lq + QBUF + o) = w.g1;
-    ld[od] = uint16_t(w.gd);
+    ld[od] = w.gd;
     if constexpr (PAIR) {
         *reinterpret_cast<v4u *>(lq + QH * QBUF + o) = w.u0;
         if constexpr (QH == 2) *reinterpret_cast<v4u *>(lq + 3 * QBUF + o) = w.u1;
-        ld[GT * GU + od] = uint16_t(w.ud);
+        ld[GT * GU + od] = w.ud;
     }
 }
 
-// The A operand of one block: Q4_0 nibbles (low: quants 4g..4g+3, high: 16+4g..) minus 8 in every byte; Q8_0 its
-// two words as they are.
+// The A operand of one block: Q4_0 nibbles (low: quants 4g..4g+3, high: 16+4g..) minus 8 in every byte; Q4_1 the
+// nibbles as they are; Q8_0 its two words as they are.
 template <int TYPE>
 __device__ __forceinline__ long a_operand(uint32_t lo, uint32_t hi) {
     uint32_t w0 = lo, w1 = hi;
+    if constexpr (TYPE == T_Q4_1) {
+        w0 = lo & 0x0F0F0F0Fu;
+        w1 = (lo >> 4) & 0x0F0F0F0Fu;
+    }
     if constexpr (TYPE == T_Q4_0) {
         const uint32_t n0 = lo & 0x0F0F0F0Fu, n1 = (lo >> 4) & 0x0F0F0F0Fu;
         // per byte: ((v | 0x80) - 8) ^ 0x80 = v - 8 as int8 for 0 <= v <= 15, no borrow between bytes
@@ -132,9 +142,10 @@ template <int T>
 struct XRound {
     v4u q[T][GW / 2];
     v4f d[T];
+    v4f s[T];  // Q4_1 only
 };
 
-template <int T>
+template <int TYPE, int T>
 __device__ __forceinline__ void load_xround(const GemmArgs & a, int nb, int r, int g, int b, XRound<T> & o) {
 #pragma unroll
     for (int t = 0; t < T; ++t) {
@@ -143,20 +154,18 @@ __device__ __forceinline__ void load_xround(const GemmArgs & a, int nb, int r, i
 #pragma unroll
         for (int k = 0; k < GW / 2; ++k) o.q[t][k] = p[k];
         o.d[t] = *reinterpret_cast<const v4f *>(a.d40 + size_t(tok) * nb + b);
+        if constexpr (TYPE == T_Q4_1) o.s[t] = *reinterpret_cast<const v4f *>(a.s40 + size_t(tok) * nb + b);
     }
 }
 
 __device__ __forceinline__ float lane_of(const v4f & v, int j) { return v[j]; }
-__device__ __forceinline__ uint32_t half_of(const uint2 & v, int j) {
-    const uint32_t w = (j >> 1) ? v.y : v.x;
-    return (j & 1) ? w >> 16 : w & 0xffffu;
-}
+
 
 // The wave's GW blocks of a staged round: per block and token tile one MFMA gives the lane's 4 sums (rows 4g + i,
 // token r); each term is floor(sumi * s) with s = fp16(d_w) * d_x * 2^40 exact in FP32 and the product exact in FP64;
 // the GW terms are summed in FP64 (integers below 2^53) and moved to the int64 totals.
 template <int TYPE, bool PAIR, int T>
-__device__ __forceinline__ void round_terms(const uint8_t * lq, const uint16_t * ld, int wave, int r, int g,
+__device__ __forceinline__ void round_terms(const uint8_t * lq, const uint32_t * ld, int wave, int r, int g,
                                             const XRound<T> & x, long long (*tot)[4], long long (*totu)[4]) {
     constexpr int NM = PAIR ? 2 : 1, QH = TYPE == T_Q8_0 ? 2 : 1;
     constexpr int QBUF = GT * ROW_LDS, DBUF = GT * GU;  // bytes of one matrix-half's quants, scales of one matrix
@@ -167,11 +176,11 @@ __device__ __forceinline__ void round_terms(const uint8_t * lq, const uint16_t *
         for (int t = 0; t < T; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[m][t][i] = 0.0;
-    uint2 dw[NM][4];  // scales of rows 4g + i for the wave's GW = 4 blocks
+    v4u dw[NM][4];  // scale words of rows 4g + i for the wave's GW = 4 blocks
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dw[m][i] = *reinterpret_cast<const uint2 *>(ld + m * DBUF + (4 * g + i) * GU + wave * GW);
+        for (int i = 0; i < 4; ++i) dw[m][i] = *reinterpret_cast<const v4u *>(ld + m * DBUF + (4 * g + i) * GU + wave * GW);
 #pragma unroll
     for (int j = 0; j < GW; ++j) {
         const int blk = wave * GW + j;
@@ -194,8 +203,12 @@ __device__ __forceinline__ void round_terms(const uint8_t * lq, const uint16_t *
                 const v4i sm = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop[m], bx, zero, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float sc = h2f(half_of(dw[m][i], j)) * dx;
-                    acc[m][t][i] += floor(double(sm[i]) * double(sc));
+                    const uint32_t sw = dw[m][i][j];
+                    const float sc = h2f(sw & 0xffffu) * dx;
+                    double term = floor(double(sm[i]) * double(sc));
+                    if constexpr (TYPE == T_Q4_1)  // + floor(m * s_x * 2^40), the product of two fp16 values exact
+                        term += floor(double(h2f(sw >> 16) * lane_of(x.s[t], j)));
+                    acc[m][t][i] += term;
                 }
             }
         }
@@ -220,7 +233,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(GemmArgs a) {
     constexpr int NM = PAIR ? 2 : 1, QH = TYPE == T_Q8_0 ? 2 : 1;
     constexpr int QBUF = GT * ROW_LDS, DBUF = GT * GU;
     __shared__ __align__(16) uint8_t lq[2][NM * QH * QBUF];
-    __shared__ __align__(16) uint16_t ld[2][NM * DBUF];
+    __shared__ __align__(16) uint32_t ld[2][NM * DBUF];
     __shared__ long long red[NWAVES - 1][NM][T][4][WAVE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
@@ -240,19 +253,19 @@ __global__ __launch_bounds__(NT) void gemm_kernel(GemmArgs a) {
     XRound<T> xa, xb;
     load_wround<TYPE, PAIR>(a, nb, lrow, 0, w0);
     load_wround<TYPE, PAIR>(a, nb, lrow, min(1, nr - 1), wb);
-    load_xround<T>(a, nb, r, g, wave * GW, xa);
+    load_xround<TYPE, T>(a, nb, r, g, wave * GW, xa);
     stage<TYPE, PAIR>(w0, lq[0], ld[0]);
     __syncthreads();
     int rd = 0;
     for (; rd + 1 < nr; rd += 2) {
         // round rd from buffer 0 and xa; round rd + 1's weights (wb) go to buffer 1
-        load_xround<T>(a, nb, r, g, (rd + 1) * GU + wave * GW, xb);
+        load_xround<TYPE, T>(a, nb, r, g, (rd + 1) * GU + wave * GW, xb);
         load_wround<TYPE, PAIR>(a, nb, lrow, min(rd + 2, nr - 1), wa);
         round_terms<TYPE, PAIR, T>(lq[0], ld[0], wave, r, g, xa, tot, totu);
         stage<TYPE, PAIR>(wb, lq[1], ld[1]);
         __syncthreads();
         // round rd + 1 from buffer 1 and xb; round rd + 2's weights (wa) go to buffer 0
-        load_xround<T>(a, nb, r, g, min(rd + 2, nr - 1) * GU + wave * GW, xa);
+        load_xround<TYPE, T>(a, nb, r, g, min(rd + 2, nr - 1) * GU + wave * GW, xa);
         load_wround<TYPE, PAIR>(a, nb, lrow, min(rd + 3, nr - 1), wb);
         round_terms<TYPE, PAIR, T>(lq[1], ld[1], wave, r, g, xb, tot, totu);
         stage<TYPE, PAIR>(wa, lq[0], ld[0]);
@@ -329,6 +342,7 @@ hipError_t launch_gemm(const GemmArgs & a, int type, hipStream_t s) {
         return hipErrorInvalidValue;
     switch (type) {
     case T_Q4_0: return launch_type<T_Q4_0>(a, s);
+    case T_Q4_1: return launch_type<T_Q4_1>(a, s);
     case T_Q8_0: return launch_type<T_Q8_0>(a, s);
     default: return hipErrorInvalidValue;
     }

@@ -172,6 +172,7 @@ struct GemmQuantArgs {
     const float * norm_w;  // per-token RMS norm folded into the quantization: its weight (NULL: none)
     int8_t * q;            // [n_pad][cols]
     float * d40;           // [n_pad][cols / 32]
+    float * s40;           // [n_pad][cols / 32]: the Q8_1 s = fp16(sum of the block's quants * d), times 2^40
     int n_tok, n_pad, cols, x_stride;
     int norm, norm_l2;
     float eps;
@@ -182,6 +183,7 @@ struct GemmArgs {
     WeightView w2;      // u of a SwiGLU pair
     const int8_t * q;   // the quantized activation (GemmQuantArgs)
     const float * d40;
+    const float * s40;  // Q4_1 weights: the activation blocks' Q8_1 s * 2^40
     float * y;          // token t, row r at y[t * y_stride + r]
     const float * res;  // ADD: res[t * res_stride + r]
     int rows, cols, n_tok, y_stride, res_stride;

@@ -72,6 +72,7 @@ struct gemvq_ctx {
     float * gdn_raw = nullptr;    // raw DeltaNet output when its gated norm is folded into the next GEMV
     int8_t * gemm_q = nullptr;    // a batched GEMV's quantized activation rows (GEMM_MAX_TOK x GEMV_MAXK)
     float * gemm_d = nullptr;     // and their block scales
+    float * gemm_s = nullptr;     // and their Q8_1 block sums (for Q4_1 weights)
     int last_launches = 0;
     std::string err;
 };
@@ -480,7 +481,7 @@ struct Compiler {
         const uint32_t * k = cmds + size_t(i) * GEMVQ_CMD_WORDS, * k2 = k + GEMVQ_CMD_WORDS;
         const int t = int(k[1] & 0xffu), rows = int(k[2]);
         const uint32_t flags = k[1] & ~0xffu, cols = k[3], ntok = k2[0], xs = k2[1], ys = k2[2], nflags = k2[7];
-        if (t != T_Q4_0 && t != T_Q8_0) return reject(i, "GEMM format (Q4_0 or Q8_0)");
+        if (t != T_Q4_0 && t != T_Q4_1 && t != T_Q8_0) return reject(i, "GEMM format (Q4_0, Q4_1 or Q8_0)");
         if (rows <= 0 || cols == 0 || cols % 512 || cols > GEMVQ_MAX_COLS) return reject(i, "GEMM shape (cols a multiple of 512)");
         if (flags & ~(GEMVQ_GEMV_SWIGLU | GEMVQ_GEMV_ADD | GEMVQ_GEMV_SILU) || __builtin_popcount(flags) > 1)
             return reject(i, "GEMM flags");
@@ -531,6 +532,7 @@ struct Compiler {
         q.norm_w = normw ? A(k2[5]) : nullptr;
         q.q = c->gemm_q;
         q.d40 = c->gemm_d;
+        q.s40 = c->gemm_s;
         q.n_tok = int(ntok);
         q.n_pad = int((ntok + 15) / 16 * 16);
         q.cols = int(cols);
@@ -540,6 +542,7 @@ struct Compiler {
         q.eps = bits_f(k2[6]);
         g.q = c->gemm_q;
         g.d40 = c->gemm_d;
+        g.s40 = c->gemm_s;
         const uint32_t x_len = xs * (ntok - 1) + cols;
         const bool same = lastq.on && lastq.x_off == k[6] && lastq.x_len == x_len && lastq.q.n_tok == q.n_tok &&
                           lastq.q.cols == q.cols && lastq.q.x_stride == q.x_stride && lastq.q.norm == q.norm &&
@@ -800,6 +803,7 @@ gemvq_ctx * gemvq_ctx_create(int device, size_t act_floats, size_t weight_bytes,
     if (e == hipSuccess) e = hipMalloc(&c->gdn_raw, size_t(GDN_MAX_HEADS) * 128 * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&c->gemm_q, size_t(GEMM_MAX_TOK) * GEMV_MAXK);
     if (e == hipSuccess) e = hipMalloc(&c->gemm_d, size_t(GEMM_MAX_TOK) * (GEMV_MAXK / 32) * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&c->gemm_s, size_t(GEMM_MAX_TOK) * (GEMV_MAXK / 32) * sizeof(float));
     if (e == hipSuccess && state_rows) e = hipMemset(c->state, 0, state_rows * 128 * sizeof(float));
     if (e != hipSuccess) {
         g_create_error = std::string("gemvq_ctx_create: ") + hipGetErrorString(e);
@@ -832,6 +836,7 @@ void gemvq_ctx_destroy(gemvq_ctx * c) {
     hipFree(c->gdn_raw);
     hipFree(c->gemm_q);
     hipFree(c->gemm_d);
+    hipFree(c->gemm_s);
     hipFree(c->dbg);
     if (c->stream) hipStreamDestroy(c->stream);
     delete c;

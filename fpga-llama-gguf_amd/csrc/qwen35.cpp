@@ -20,7 +20,7 @@
 
 namespace {
 
-constexpr int F32 = 0, T_Q4_0 = 2, T_Q8_0 = 8;  // ggml type ids
+constexpr int F32 = 0, T_Q4_0 = 2, T_Q4_1 = 3, T_Q8_0 = 8;  // ggml type ids
 
 uint32_t fb(float f) {
     uint32_t b;
@@ -149,7 +149,7 @@ struct Emit {
     }
 };
 
-// The projections a batched prefill runs as GEMM commands: Q4_0 / Q8_0 with columns a multiple of 512.
+// The projections a batched prefill runs as GEMM commands: Q4_0 / Q4_1 / Q8_0 with columns a multiple of 512.
 bool batchable(const gemvq_qwen35 & m, std::string & why) {
     const gemvq_qw_config & c = m.c;
     if (c.n_embd % 512 || c.n_ff % 512 || (c.ssm_v_heads * c.ssm_head_dim) % 512 || (c.n_head * c.head_dim) % 512) {
@@ -161,8 +161,8 @@ bool batchable(const gemvq_qwen35 & m, std::string & why) {
         if (n.rfind("blk.", 0) != 0 || !kv.second.d || kv.second.d->type == F32) continue;
         if (n.find("ssm_conv1d") != std::string::npos) continue;
         const int t = kv.second.d->type;
-        if ((t != T_Q4_0 && t != T_Q8_0) || kv.second.d->ne0 % 512) {
-            why = "tensor " + n + " has no batched GEMV (Q4_0 / Q8_0, columns a multiple of 512)";
+        if ((t != T_Q4_0 && t != T_Q4_1 && t != T_Q8_0) || kv.second.d->ne0 % 512) {
+            why = "tensor " + n + " has no batched GEMV (Q4_0 / Q4_1 / Q8_0, columns a multiple of 512)";
             return false;
         }
     }

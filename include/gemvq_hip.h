@@ -62,7 +62,8 @@
  *             The batched GEMV (the reference's planned batched path, ROADMAP.md:78-96; no counterpart in its
  *             kernel): n_tok (1..GEMVQ_GEMM_MAX_TOK) token rows read each weight row once. Token t's input row is at
  *             x_off + t * x_stride and its output row at y_off + t * y_stride; each output row equals, bit for bit,
- *             what a GEMV command on that token row writes. Format 2 Q4_0 or 8 Q8_0, cols a multiple of 512.
+ *             what a GEMV command on that token row writes. Format 2 Q4_0, 3 Q4_1 or 8 Q8_0, cols a multiple of
+ *             512.
  *             flags: GEMVQ_GEMV_SWIGLU (the next command is the u GEMM with the same format, rows, cols, x_off,
  *             n_tok, x_stride and norm words and no flags; y = silu(g) * u goes to the u command's y_off /
  *             y_stride), GEMVQ_GEMV_ADD (y = W x + res, token t's residual at res_off + t * res_stride) or

@@ -50,8 +50,8 @@ int gemvq_qwen35_step(gemvq_qwen35 * m, int n);
 /* Runs the next n prompt positions (all before the last prompt token) in chunks of up to GEMVQ_GEMM_MAX_TOK tokens
  * per weight read (GEMM commands; the reference plans this batched path, ROADMAP.md:78-96, and has no counterpart):
  * afterwards the model is where n decode steps would have left it (states, KV cache, position, token ids), bit for
- * bit, without the logits. GEMVQ_EINVAL when a projection has no batched form (Q4_0 / Q8_0 with columns a multiple
- * of 512; decode steps then do the same work) or the positions pass the last prompt token but one; synchronizes. */
+ * bit, without the logits. GEMVQ_EINVAL when a projection has no batched form (Q4_0 / Q4_1 / Q8_0 with columns a
+ * multiple of 512; decode steps then do the same work) or the positions pass the last prompt token but one; synchronizes. */
 int gemvq_qwen35_prefill(gemvq_qwen35 * m, int n);
 /* Token ids at positions 0 .. n - 1 (prompt tokens, then generated ones); synchronizes. */
 int gemvq_qwen35_tokens(gemvq_qwen35 * m, int32_t * out, int n);

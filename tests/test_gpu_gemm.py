@@ -1,6 +1,6 @@
 """The batched GEMV (GEMM command) on the GPU through the C ABI. Every token's output row must equal, bit for bit, the
 oracle's single-token GEMV of that token's row and the GPU's own GEMV command on it: the same activation quantizer,
-the same exact block terms, the same epilogs, only the block sums come from int8 MFMAs. Covered: Q4_0 and Q8_0;
+the same exact block terms, the same epilogs, only the block sums come from int8 MFMAs. Covered: Q4_0, Q4_1 and Q8_0;
 1, 5, 16, 17 and 32 tokens (one and two token tiles, padding tokens); row counts that are not a multiple of the
 16-row tile; 2560, 4096 and 12288 columns; strided rows; the SwiGLU pair, residual ADD and SiLU epilogs; the folded
 per-token RMS norm (with and without weight, L2); output rows over the input rows; invalid commands."""
@@ -23,7 +23,7 @@ def up16(n: int) -> int:
     return (n + 15) // 16 * 16
 
 
-@pytest.mark.parametrize("fmt", [2, 8])
+@pytest.mark.parametrize("fmt", [2, 3, 8])
 @pytest.mark.parametrize("rows,cols,ntok", [(1000, 2560, 1), (1000, 2560, 5), (4096, 4096, 16), (333, 4096, 17),
                                             (512, 12288, 32)])
 def test_gemm_rows_equal_single_token_gemv(gq, orc, ctx, fmt, rows, cols, ntok):
@@ -45,7 +45,7 @@ def test_gemm_rows_equal_single_token_gemv(gq, orc, ctx, fmt, rows, cols, ntok):
         assert_bits(ctx.read(Y1, rows), y[t], f"GEMV command, token {t}")
 
 
-@pytest.mark.parametrize("fmt", [2, 8])
+@pytest.mark.parametrize("fmt", [2, 3, 8])
 def test_gemm_epilogs_and_norm(gq, orc, ctx, fmt):
     rows, cols, ntok, eps = 2000, 4096, 9, 1e-6
     wg, wu = gq.matrix(fmt, rows, cols, 4, 20, std=0.02), gq.matrix(fmt, rows, cols, 4, 21, std=0.02)
@@ -156,3 +156,31 @@ def test_gemm_reuses_quantized_rows_until_overwritten(gq, orc, ctx):
     for t in range(ntok):
         xn = orc.fx_gemv(2, w1, xr[t], rows, cols)
         assert_bits(y2[t], orc.fx_gemv(8, w2, xn, rows, cols), f"after overwrite token {t}")
+
+
+# An activation block whose Q8_1 sum s = fp16(sum(q) * d) falls on an fp16 tie: the FP32 product sum * d is exactly
+# halfway between two fp16 values (6.986328125, sum 160), so it must round to even (0x46fc); rounding the exact
+# product once instead (a multiply fused into the conversion) gives 0x46fd.
+TIE_BLOCK = [3205777222,1076638343,1070347095,1067654670,3217158963,3226446569,1061787943,1076228752,1066425760,3220559183,1019700895,1043250633,3213579224,1083621115,3201029249,1060894146,3219640152,3206132165,1052879561,1085371367,3231080033,3228257810,3216771732,3210901803,3208034114,1058367542,1068577287,3187710123,1073944164,3212800904,1075424494,1076089562]
+
+
+def test_q4_1_sum_on_fp16_tie(gq, orc, ctx):
+    rows, cols, ntok = 64, 512, 3
+    blk = np.array(TIE_BLOCK, np.uint32).view(np.float32)
+    x = np.zeros(ntok * cols, np.float32)
+    for t in range(ntok):
+        x[t * cols + 32 * (5 + t):t * cols + 32 * (6 + t)] = blk
+    q = np.zeros(32, np.int8)
+    d16, s16 = np.zeros(1, np.uint16), np.zeros(1, np.uint16)
+    orc.orc().orc_quantize_q8_1(blk.ctypes.data, 32, q.ctypes.data, d16.ctypes.data, s16.ctypes.data)
+    assert int(q.astype(np.int32).sum()) == 160 and s16[0] == 0x46fc  # the oracle rounds the tie to even
+    w = gq.matrix(3, rows, cols, 8, 60, std=0.02)
+    off = ctx.upload(3, rows, cols, w)
+    ctx.write(0, x)
+    assert ctx.run(gq.gemm(3, rows, cols, off, 0, 8192, ntok, cols, rows)) == 0, ctx.error()
+    y = ctx.read(8192, ntok * rows).reshape(ntok, rows)
+    for t in range(ntok):
+        want = orc.fx_gemv(3, w, x[t * cols:(t + 1) * cols], rows, cols)
+        assert_bits(y[t], want, f"GEMM token {t}")
+        assert ctx.run(gq.gemv(3, rows, cols, off, t * cols, 16384)) == 0, ctx.error()
+        assert_bits(ctx.read(16384, rows), want, f"GEMV token {t}")

@@ -131,14 +131,16 @@ def _decode_state(m, cfg, npos):
     return st, kvs, m.tokens(npos + 1)
 
 
-def test_batched_prefill_equals_decode_steps(gq, q35):
+@pytest.mark.parametrize("q4_1", [False, True])
+def test_batched_prefill_equals_decode_steps(gq, q35, q4_1):
     """The batched prefill (GEMM commands over chunks of up to 32 prompt tokens, the conv and DeltaNet step over the
     tokens in order, attention token by token) leaves the model where the decode steps do, bit for bit: DeltaNet
     states, KV cache, token ids; and the generation that follows has identical tokens, logits and hidden state. C5
     widths, 4 layers (3 DeltaNet + 1 attention); 44 prompt positions = chunks of 32 and 12; and a prefill split
-    around decode steps."""
+    around decode steps. With q4_1, two layers' ffn_down are Q4_1 (the type mix of real Qwen3.5 Q4_0 files)."""
     cfg = q35.Config(n_layer=4, n_ctx=96)
-    blob = q35.generate(cfg, seed=1)
+    types = {f"blk.{il}.ffn_down.weight": gq.Q4_1 for il in (1, 3)} if q4_1 else None
+    blob = q35.generate(cfg, seed=1, types=types)
     prompt = q35.prompt_ids(cfg, 45, seed=1)
     n_gen = 12
     with q35.Model(blob) as m:
