@@ -2,9 +2,9 @@
 """Decode benchmark: batch-1 greedy decode of the synthetic Qwen3.5-9B-shaped Q4_0 model on one MI355X.
 
 Workload: 32 layers (24 Gated DeltaNet + 8 gated attention, 3:1), hidden 4096, FFN 12288, vocab 151936, layer
-matrices Q4_0 N(0, 0.02^2), embedding and head Q6_K, norms fp32 ones; prompt of 512 random ids run token by token
-(untimed), then `--warmup` untimed and `--steps` timed greedy decode steps (one hipGraph replay each, tokens fed
-back on the device). value = timed tokens / wall time between two stream synchronizations.
+matrices Q4_0 N(0, 0.02^2), embedding and head Q6_K, norms fp32 ones; prompt of 512 random ids (run as decode steps,
+then again, after a reset, as a batched prefill; both rates are reported, neither is `value`), then `--warmup`
+untimed and `--steps` timed greedy decode steps (one hipGraph replay each, tokens fed back on the device). value = timed tokens / wall time between two stream synchronizations.
 
 roofline: the dominant kernel (largest share of a token's device time), its algorithmic bytes (GGUF weights +
 fp32 vectors read and written once + state/KV traffic) over its measured duration, from device start/stop events
@@ -305,7 +305,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=128, help="timed decode steps (tokens)")
     ap.add_argument("--warmup", type=int, default=0, help="untimed decode steps after the prompt")
-    ap.add_argument("--prompt", type=int, default=512, help="prompt length (run token by token, untimed)")
+    ap.add_argument("--prompt", type=int, default=512, help="prompt length (outside the timed steps)")
     ap.add_argument("--cpu-tokens", type=int, default=6, help="decode steps timed for the CPU baseline (0: skip)")
     ap.add_argument("--threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--profile-reps", type=int, default=3)
@@ -359,7 +359,8 @@ def main() -> int:
             prefill = {"positions": args.prompt - 1, "batched_tokens_per_s": round((args.prompt - 1) / t_pre, 1),
                        "decode_step_tokens_per_s": round((args.prompt - 1) / t_steps, 1),
                        "method": "chunks of 32 tokens: GEMM projections, conv and DeltaNet over the tokens in order, "
-                                 "attention per token; wall time of the whole prefill call"}
+                                 "attention over the chunk's tokens in one launch pair; wall time of the whole "
+                                 "prefill call"}
             log(f"prompt: {args.prompt - 1} positions batched in {t_pre:.3f} s ({prefill['batched_tokens_per_s']} tok/s) "
                 f"vs {t_steps:.3f} s as decode steps")
         else:

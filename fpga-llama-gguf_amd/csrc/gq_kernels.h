@@ -145,6 +145,11 @@ struct AttnArgs {
     unsigned int * counter;  // [n_head_kv * ATTN_MAXG]: finished chunks per q head
     int n_head, n_head_kv, head_dim, n_rot, q_stride, n_ctx;
     float scale, eps;
+    // n_tok > 1: tokens at positions *pos + t, t < n_tok, in one launch pair. Token t's q (and gate) rows start
+    // t * n_head * q_stride floats on, its new key and value t * n_head_kv * head_dim, its output t * n_head *
+    // head_dim; its partials and counters follow those of token t - 1 (part and counter hold n_tok sets).
+    int n_tok;
+    float * qr;           // n_tok > 1: normalized, rotated, fp16-rounded q rows [n_tok][n_head][head_dim]
 };
 
 struct GetRowsArgs {

@@ -241,7 +241,53 @@ constexpr int ATT_T = 256;
 constexpr int MAXCH = 64;  // chunks (n_ctx <= 4096)
 constexpr int CMB = 16;    // chunks per load round of the combine
 
+// ---- new keys, values and queries of n_tok tokens (step 2 below, one vector per workgroup) ----
+// Workgroup (slot s, token t): s < n_head normalizes and rotates q head s and writes it, fp16-rounded, to qr; the
+// others do the same for the new key of KV head s - n_head and store it and the value in the cache at *pos + t.
+// Same operations in the same order as the single-token kernel, so the cache and the rounded queries are the bits
+// that n_tok single-token launches would produce.
 template <int HD>
+__global__ __launch_bounds__(ATT_T) void attn_append_kernel(AttnArgs a) {
+    __shared__ float xs[HD];
+    __shared__ float red[4];
+    const int s = blockIdx.x, t = blockIdx.y, pos = *a.pos + t;
+    if (pos < 0 || pos >= a.n_ctx) return;  // positions past the KV capacity are not stored
+    const bool isq = s < a.n_head;
+    const int h = isq ? s : s - a.n_head;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = a.n_rot / 2;
+    const bool el = tid < HD;
+    const int e = el ? tid : 0;
+    const size_t kvo = (size_t(t) * a.n_head_kv + h) * HD + e;
+    const float x = !el ? 0.0f : isq ? a.q[size_t(t) * a.n_head * a.q_stride + size_t(h) * a.q_stride + e] : a.k[kvo];
+    const float w = isq ? a.qn[e] : a.kn[e];
+    const float vv = isq ? 0.0f : a.v[kvo];
+    const int pi = e < half ? e : e - half;
+    const bool rot = e < a.n_rot;
+    const float cs0 = rot ? a.cs[size_t(pos) * a.n_rot + 2 * pi] : 0.0f;
+    const float cs1 = rot ? a.cs[size_t(pos) * a.n_rot + 2 * pi + 1] : 0.0f;
+    float sq[1] = {x * x};
+    pair_sum_lanes_n<64, 1>(sq);
+    if (lane == 0) red[wave] = sq[0];
+    __syncthreads();
+    const float sum = (red[0] + red[1]) + (red[2] + red[3]);
+    const float sc = 1.0f / sqrtf(sum / float(HD) + a.eps);
+    if (el) xs[e] = (x * sc) * w;
+    __syncthreads();
+    const float x0 = xs[pi], x1 = xs[pi + half];
+    const float rv = e < half ? x0 * cs0 - x1 * cs1 : (rot ? x0 * cs1 + x1 * cs0 : xs[e]);
+    if (!el) return;
+    if (isq) {
+        a.qr[(size_t(t) * a.n_head + h) * HD + e] = h2f(f2h(rv));
+    } else {
+        const size_t off = (size_t(pos) * a.n_head_kv + h) * HD + e;
+        a.kc[off] = uint16_t(f2h(rv));
+        a.vc[off] = uint16_t(f2h(vv));
+    }
+}
+
+// BATCH: token t = blockIdx.y of a multi-token launch, after attn_append_kernel: the rounded query comes from qr and
+// every key and value (its own position's too) from the cache, which hold the bits the single-token kernel uses.
+template <int HD, bool BATCH>
 __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
     constexpr int PER = HD / 8;                    // 16-byte pieces per row
     constexpr int RPP = ATT_T / PER;               // rows per pass
@@ -256,12 +302,14 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
     const int G = a.n_head / a.n_head_kv, b = blockIdx.x;
     const int u = (b / (8 * G)) * 8 + (b & 7), g = (b >> 3) % G;
     const int kvh = u % a.n_head_kv, chunk = u / a.n_head_kv, hq = kvh * G + g;
-    const int pos = *a.pos, nc = (pos + ATTN_CHUNK) / ATTN_CHUNK;
+    const int t = BATCH ? int(blockIdx.y) : 0, th = t * a.n_head + hq;  // th: the (token, q head) partials set
+    const int pos = *a.pos + t, nc = (pos + ATTN_CHUNK) / ATTN_CHUNK;
     if (pos < 0 || pos >= a.n_ctx || chunk >= nc) return;  // positions past the KV capacity are not stored
     const int tid = threadIdx.x, half = a.n_rot / 2;
     const int lane = tid & 63, wave = tid >> 6, pc = tid % PER;
     const int t0 = chunk * ATTN_CHUNK, nt = min(ATTN_CHUNK, pos + 1 - t0);
-    const bool has_new = chunk == nc - 1;  // this chunk holds pos
+    const bool has_new = !BATCH && chunk == nc - 1;  // this chunk holds pos (a batch reads it from the cache)
+    const float * qrow = a.q + size_t(t) * a.n_head * a.q_stride + size_t(hq) * a.q_stride;
     // ---- 1. loads ----
     uint4 kr[NP], vr[NP];  // rows past the chunk re-read its last row (stored memory); they are not used
 #pragma unroll
@@ -274,13 +322,13 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
     const bool el = tid < HD;
     const int e = el ? tid : 0;  // element of the head this thread holds
     float xv[2];
-    xv[0] = el ? a.q[size_t(hq) * a.q_stride + e] : 0.0f;
+    xv[0] = (!BATCH && el) ? qrow[e] : 0.0f;
     xv[1] = (has_new && el) ? a.k[size_t(kvh) * HD + e] : 0.0f;
-    const float wq = a.qn[e], wk = a.kn[e];
+    const float wq = BATCH ? 0.0f : a.qn[e], wk = BATCH ? 0.0f : a.kn[e];
     const float vv = has_new ? a.v[size_t(kvh) * HD + e] : 0.0f;
-    const float gt = a.gate ? a.gate[size_t(hq) * 2 * HD + e] : 0.0f;
+    const float gt = a.gate ? a.gate[size_t(t) * a.n_head * a.q_stride + size_t(hq) * 2 * HD + e] : 0.0f;
     const int pi = e < half ? e : e - half;  // the RoPE pair of this element
-    const bool rot = e < a.n_rot;
+    const bool rot = !BATCH && e < a.n_rot;
     const float cs0 = rot ? a.cs[size_t(pos) * a.n_rot + 2 * pi] : 0.0f;
     const float cs1 = rot ? a.cs[size_t(pos) * a.n_rot + 2 * pi + 1] : 0.0f;
 #pragma unroll
@@ -289,37 +337,41 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
         if (ti < nt) *reinterpret_cast<uint4 *>(vs + ti * HD + pc * 8) = vr[j];
     }
     // ---- 2. norms (pairwise over head_dim), RoPE, fp16 rounding ----
-    float sq[2] = {xv[0] * xv[0], xv[1] * xv[1]};
-    pair_sum_lanes_n<64, 2>(sq);
-    if (lane == 0) {
-        red[0][wave] = sq[0];
-        red[1][wave] = sq[1];
-    }
-    __syncthreads();
+    if constexpr (BATCH) {
+        if (el) qs[0][e] = a.qr[size_t(th) * HD + e];
+    } else {
+        float sq[2] = {xv[0] * xv[0], xv[1] * xv[1]};
+        pair_sum_lanes_n<64, 2>(sq);
+        if (lane == 0) {
+            red[0][wave] = sq[0];
+            red[1][wave] = sq[1];
+        }
+        __syncthreads();
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const float sum = (red[h][0] + red[h][1]) + (red[h][2] + red[h][3]);
-        const float sc = 1.0f / sqrtf(sum / float(HD) + a.eps);
-        if (el) qs[h][e] = (xv[h] * sc) * (h == 0 ? wq : wk);
-    }
-    __syncthreads();
-    float rv[2];
+        for (int h = 0; h < 2; ++h) {
+            const float sum = (red[h][0] + red[h][1]) + (red[h][2] + red[h][3]);
+            const float sc = 1.0f / sqrtf(sum / float(HD) + a.eps);
+            if (el) qs[h][e] = (xv[h] * sc) * (h == 0 ? wq : wk);
+        }
+        __syncthreads();
+        float rv[2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const float x0 = qs[h][pi], x1 = qs[h][pi + half];
-        rv[h] = e < half ? x0 * cs0 - x1 * cs1 : (rot ? x0 * cs1 + x1 * cs0 : qs[h][e]);
-    }
-    __syncthreads();
-    if (el) {
-        qs[0][e] = h2f(f2h(rv[0]));
-        qs[1][e] = h2f(f2h(rv[1]));
-        if (has_new) {
-            const uint32_t kb = f2h(rv[1]), vb = f2h(vv);
-            vs[(pos - t0) * HD + e] = uint16_t(vb);
-            if (g == 0) {  // one q head per KV head stores the new key and value
-                const size_t off = (size_t(pos) * a.n_head_kv + kvh) * HD + e;
-                a.kc[off] = uint16_t(kb);
-                a.vc[off] = uint16_t(vb);
+        for (int h = 0; h < 2; ++h) {
+            const float x0 = qs[h][pi], x1 = qs[h][pi + half];
+            rv[h] = e < half ? x0 * cs0 - x1 * cs1 : (rot ? x0 * cs1 + x1 * cs0 : qs[h][e]);
+        }
+        __syncthreads();
+        if (el) {
+            qs[0][e] = h2f(f2h(rv[0]));
+            qs[1][e] = h2f(f2h(rv[1]));
+            if (has_new) {
+                const uint32_t kb = f2h(rv[1]), vb = f2h(vv);
+                vs[(pos - t0) * HD + e] = uint16_t(vb);
+                if (g == 0) {  // one q head per KV head stores the new key and value
+                    const size_t off = (size_t(pos) * a.n_head_kv + kvh) * HD + e;
+                    a.kc[off] = uint16_t(kb);
+                    a.vc[off] = uint16_t(vb);
+                }
             }
         }
     }
@@ -334,7 +386,7 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
     float dots[NP];
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
-        const bool is_new = t0 + tid / PER + j * RPP == pos;
+        const bool is_new = !BATCH && t0 + tid / PER + j * RPP == pos;
         const uint32_t kw[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
         float t[8];
 #pragma unroll
@@ -367,7 +419,7 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
             l += p;
             o += p * h2f(vs[i * HD + e]);
         }
-        float * pp = a.part + (size_t(hq) * nchmax + chunk) * pstride;
+        float * pp = a.part + (size_t(th) * nchmax + chunk) * pstride;
         pp[2 + e] = o;
         if (e == 0) {
             pp[0] = mx;
@@ -377,13 +429,13 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
     __syncthreads();
     if (tid == 0) {  // the partials are released (agent scope) by the counter update; the last workgroup acquires
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        last = atomicAdd(a.counter + hq, 1u) == unsigned(nc - 1);
+        last = atomicAdd(a.counter + th, 1u) == unsigned(nc - 1);
         if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
     if (!last) return;
     // ---- 5. combine (last workgroup of the q head) ----
-    const float * pk = a.part + size_t(hq) * nchmax * pstride;
+    const float * pk = a.part + size_t(th) * nchmax * pstride;
     float ov[CMB];
     float mc = -__builtin_inff(), lc = 0.0f;
     if (wave == 0 && lane < nc) {
@@ -420,9 +472,9 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
     if (el) {
         float out = O / L;
         if (a.gate) out = (1.0f / (1.0f + expf_(-gt))) * out;
-        a.y[size_t(hq) * HD + e] = out;
+        a.y[size_t(th) * HD + e] = out;
     }
-    if (tid == 0) a.counter[hq] = 0u;
+    if (tid == 0) a.counter[th] = 0u;
 }
 
 // ---- embedding rows (ggml dequantize_row_*) ----
@@ -525,22 +577,36 @@ hipError_t launch_gated_norm(const GatedNormArgs & a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// One token: the attention kernel alone. Several: their new keys, values and queries first (one launch), then the
+// attention of every (token, q head, chunk).
+template <int HD>
+hipError_t launch_attn_hd(const AttnArgs & a, dim3 grid, hipStream_t s) {
+    if (grid.y == 1) {
+        GQ_LAUNCH((attn_kernel<HD, false>), grid, dim3(ATT_T), 0, s, a);
+        return hipGetLastError();
+    }
+    GQ_LAUNCH(attn_append_kernel<HD>, dim3(a.n_head + a.n_head_kv, grid.y), dim3(ATT_T), 0, s, a);
+    GQ_LAUNCH((attn_kernel<HD, true>), grid, dim3(ATT_T), 0, s, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_attn(const AttnArgs & a, hipStream_t s) {
     if (a.n_head % a.n_head_kv || a.n_head / a.n_head_kv > ATTN_MAXG || (a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK > MAXCH)
         return hipErrorInvalidValue;
     // units (KV head, chunk) in groups of 8, each group followed by its q heads: workgroup b serves unit
     // (b / (8 G)) 8 + b % 8 (units past the last are idle) and q head (b / 8) % G of its KV head
     const int units = a.n_head_kv * ((a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK);
-    const dim3 grid(((units + 7) / 8) * 8 * (a.n_head / a.n_head_kv));
+    const int n_tok = a.n_tok > 1 ? a.n_tok : 1;
+    if (n_tok > GEMM_MAX_TOK || (n_tok > 1 && !a.qr)) return hipErrorInvalidValue;
+    const dim3 grid(((units + 7) / 8) * 8 * (a.n_head / a.n_head_kv), n_tok);
     switch (a.head_dim) {
-    case 16: GQ_LAUNCH(attn_kernel<16>, grid, dim3(ATT_T), 0, s, a); break;
-    case 32: GQ_LAUNCH(attn_kernel<32>, grid, dim3(ATT_T), 0, s, a); break;
-    case 64: GQ_LAUNCH(attn_kernel<64>, grid, dim3(ATT_T), 0, s, a); break;
-    case 128: GQ_LAUNCH(attn_kernel<128>, grid, dim3(ATT_T), 0, s, a); break;
-    case 256: GQ_LAUNCH(attn_kernel<256>, grid, dim3(ATT_T), 0, s, a); break;
+    case 16: return launch_attn_hd<16>(a, grid, s);
+    case 32: return launch_attn_hd<32>(a, grid, s);
+    case 64: return launch_attn_hd<64>(a, grid, s);
+    case 128: return launch_attn_hd<128>(a, grid, s);
+    case 256: return launch_attn_hd<256>(a, grid, s);
     default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 hipError_t launch_get_rows(const GetRowsArgs & a, hipStream_t s) {

@@ -30,8 +30,9 @@ struct Weight {
 struct KvBuf {
     uint16_t * k = nullptr;
     uint16_t * v = nullptr;
-    float * part = nullptr;
+    float * part = nullptr;       // attention partials and counters: one set per token of a GEMM_MAX_TOK batch
     unsigned * counter = nullptr;
+    float * qr = nullptr;         // a batch's rotated queries [GEMM_MAX_TOK][ATTN_MAXG * n_head_kv][head_dim]
     int n_ctx = 0, n_head_kv = 0, head_dim = 0;
 };
 
@@ -386,12 +387,14 @@ struct Compiler {
                 if (nkv == 0 || nh % nkv || nh / nkv > 4 || (b.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK > 64 || int(nkv) != b.n_head_kv || int(hd) != b.head_dim || hd > 256 ||
                     hd < 16 || (hd & (hd - 1)) || nrot > hd || nrot % 2)
                     return reject(i, "ATTN shape");
-                const uint32_t qstride = (flags & 1) ? 2 * hd : hd;
-                if (!range(k[2], uint64_t(qstride) * (nh - 1) + hd) || !range(k[4], uint64_t(nh) * hd) || !range(k[6], 1) ||
-                    !range(k2[0], uint64_t(nkv) * hd) || !range(k2[1], uint64_t(nkv) * hd) || !range(k2[4], hd) ||
+                const uint32_t qstride = (flags & 1) ? 2 * hd : hd, ntok = (flags >> 16) & 0xffu ? (flags >> 16) & 0xffu : 1;
+                if (ntok > GEMVQ_GEMM_MAX_TOK) return reject(i, "ATTN tokens");
+                const uint64_t qt = uint64_t(nh) * qstride * (ntok - 1), kvt = uint64_t(nkv) * hd * ntok;  // packed tokens
+                if (!range(k[2], qt + uint64_t(qstride) * (nh - 1) + hd) || !range(k[4], uint64_t(nh) * hd * ntok) ||
+                    !range(k[6], 1) || !range(k2[0], kvt) || !range(k2[1], kvt) || !range(k2[4], hd) ||
                     !range(k2[5], hd) || k2[6] + uint64_t(b.n_ctx) * nrot > c->act_floats)
                     return reject(i, "ATTN range");
-                if ((flags & 1) && !range(k2[7], uint64_t(2 * hd) * (nh - 1) + hd)) return reject(i, "ATTN gate range");
+                if ((flags & 1) && !range(k2[7], qt + uint64_t(2 * hd) * (nh - 1) + hd)) return reject(i, "ATTN gate range");
                 AttnArgs a{};
                 a.q = A(k[2]);
                 a.k = A(k2[0]);
@@ -414,6 +417,8 @@ struct Compiler {
                 a.n_ctx = b.n_ctx;
                 a.scale = bits_f(k2[2]);
                 a.eps = bits_f(k2[3]);
+                a.n_tok = int(ntok);
+                a.qr = b.qr;
                 out.push_back(LAttn{a});
                 spans.push_back({int(i), 2});
                 i += 2;
@@ -727,8 +732,9 @@ std::pair<std::string, uint64_t> describe(const Launch & l, int pos) {
     if (auto * x = std::get_if<LGated>(&l)) return {"gated_norm_kernel", uint64_t(x->a.heads) * 128 * 12 + 512};
     if (auto * x = std::get_if<LAttn>(&l)) {
         const AttnArgs & a = x->a;
-        const uint64_t kv = uint64_t(pos + 1) * a.n_head_kv * a.head_dim * 2 * 2;
-        const uint64_t vec = uint64_t(a.n_head) * a.head_dim * 4 * (a.gate ? 3 : 2) + uint64_t(a.n_head_kv) * a.head_dim * 8;
+        const uint64_t nt = uint64_t(a.n_tok > 1 ? a.n_tok : 1);  // token t reads positions 0 .. pos + t
+        const uint64_t kv = (uint64_t(pos + 1) * nt + nt * (nt - 1) / 2) * a.n_head_kv * a.head_dim * 2 * 2;
+        const uint64_t vec = (uint64_t(a.n_head) * a.head_dim * 4 * (a.gate ? 3 : 2) + uint64_t(a.n_head_kv) * a.head_dim * 8) * nt;
         return {"attn_kernel", kv + vec};
     }
     if (auto * x = std::get_if<LRows>(&l))
@@ -829,6 +835,7 @@ void gemvq_ctx_destroy(gemvq_ctx * c) {
         hipFree(b.v);
         hipFree(b.part);
         hipFree(b.counter);
+        hipFree(b.qr);
     }
     hipFree(c->act);
     hipFree(c->warena);
@@ -941,19 +948,22 @@ int gemvq_kv_create(gemvq_ctx * c, int n_ctx, int n_head_kv, int head_dim) {
     b.head_dim = head_dim;
     const size_t kvn = size_t(n_ctx) * n_head_kv * head_dim;
     const size_t nch = size_t(n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
-    const size_t partn = size_t(4) * n_head_kv * nch * (2 + head_dim);
+    const size_t heads = size_t(ATTN_MAXG) * n_head_kv * GEMM_MAX_TOK;  // (token, q head) sets of a batch
+    const size_t partn = heads * nch * (2 + head_dim);
     hipError_t e = hipMalloc(&b.k, kvn * 2);
     if (e == hipSuccess) e = hipMalloc(&b.v, kvn * 2);
     if (e == hipSuccess) e = hipMalloc(&b.part, partn * 4);
-    if (e == hipSuccess) e = hipMalloc(&b.counter, size_t(n_head_kv) * ATTN_MAXG * 4);
+    if (e == hipSuccess) e = hipMalloc(&b.counter, heads * 4);
+    if (e == hipSuccess) e = hipMalloc(&b.qr, heads * head_dim * 4);
     if (e == hipSuccess) e = hipMemset(b.k, 0, kvn * 2);
     if (e == hipSuccess) e = hipMemset(b.v, 0, kvn * 2);
-    if (e == hipSuccess) e = hipMemset(b.counter, 0, size_t(n_head_kv) * ATTN_MAXG * 4);
+    if (e == hipSuccess) e = hipMemset(b.counter, 0, heads * 4);
     if (e != hipSuccess) {
         hipFree(b.k);
         hipFree(b.v);
         hipFree(b.part);
         hipFree(b.counter);
+        hipFree(b.qr);
         return fail(c, e, "kv create");
     }
     c->kvs.push_back(b);

@@ -122,7 +122,7 @@ size_t layout(gemvq_qwen35 & m, const gemvq_tensor_desc * tab, int n) {
     m.batt = take(B * c.n_head * c.head_dim);
     m.bffn = take(B * c.n_ff);
     m.bid = take(B * 16);
-    m.bpos = take(B * 16);
+    m.bpos = take(16);
     return off;
 }
 
@@ -195,13 +195,11 @@ bool build_chunk(const gemvq_qwen35 & m, uint32_t ntok, std::vector<uint32_t> & 
             e.gemm(*W(p + "attn_q.weight"), m.bh, E, m.bqg, qrow, ntok, 0, 0, 0, an, eps);
             e.gemm(*W(p + "attn_k.weight"), m.bh, E, m.bk, kvrow, ntok, 0, 0, 0, an, eps);
             e.gemm(*W(p + "attn_v.weight"), m.bh, E, m.bv, kvrow, ntok, 0, 0, 0, an, eps);
-            for (uint32_t i = 0; i < ntok; ++i) {
-                e.cmd({GEMVQ_OP_ATTN, uint32_t(c.n_head) | (uint32_t(c.n_head_kv) << 16), m.bqg + i * qrow,
-                       uint32_t(m.kv[il]), m.batt + i * arow, hd | (uint32_t(c.n_rot) << 16), m.bpos + 16 * i, 1u});
-                e.cmd({m.bk + i * kvrow, m.bv + i * kvrow, fb(1.0f / std::sqrt(float(c.head_dim))), fb(eps),
-                       W(p + "attn_q_norm.weight")->act_off, W(p + "attn_k_norm.weight")->act_off, m.rope,
-                       m.bqg + i * qrow + hd});
-            }
+            // the chunk's tokens at positions act[bpos] + i, packed rows (q + gate, k, v, output)
+            e.cmd({GEMVQ_OP_ATTN, uint32_t(c.n_head) | (uint32_t(c.n_head_kv) << 16), m.bqg, uint32_t(m.kv[il]), m.batt,
+                   hd | (uint32_t(c.n_rot) << 16), m.bpos, 1u | (ntok << 16)});
+            e.cmd({m.bk, m.bv, fb(1.0f / std::sqrt(float(c.head_dim))), fb(eps), W(p + "attn_q_norm.weight")->act_off,
+                   W(p + "attn_k_norm.weight")->act_off, m.rope, m.bqg + hd});
             e.gemm(*W(p + "attn_output.weight"), m.batt, arow, m.bh, E, ntok, GEMVQ_GEMV_ADD, m.bh, E);
         } else {
             e.gemm(*W(p + "attn_qkv.weight"), m.bh, E, m.bqkv, ch, ntok, 0, 0, 0, an, eps);
@@ -453,13 +451,10 @@ int gemvq_qwen35_prefill(gemvq_qwen35 * m, int n) {
     std::vector<uint32_t> w;
     for (int p0 = pos; p0 < pos + n && !st;) {
         const int nt = std::min<int>(GEMVQ_GEMM_MAX_TOK, pos + n - p0);
-        std::vector<int32_t> slots(size_t(32) * GEMVQ_GEMM_MAX_TOK, 0);  // ids, then positions, one per 16 floats
-        for (int i = 0; i < nt; ++i) {
-            slots[size_t(16) * i] = m->prompt_ids[size_t(p0 + i)];
-            slots[size_t(16) * (GEMVQ_GEMM_MAX_TOK + i)] = p0 + i;
-        }
-        st = gemvq_act_write(ctx, m->bid, slots.data(), size_t(16) * GEMVQ_GEMM_MAX_TOK);
-        if (!st) st = gemvq_act_write(ctx, m->bpos, slots.data() + size_t(16) * GEMVQ_GEMM_MAX_TOK, size_t(16) * GEMVQ_GEMM_MAX_TOK);
+        std::vector<int32_t> slots(size_t(16) * GEMVQ_GEMM_MAX_TOK, 0);  // ids, one per 16 floats
+        for (int i = 0; i < nt; ++i) slots[size_t(16) * i] = m->prompt_ids[size_t(p0 + i)];
+        st = gemvq_act_write(ctx, m->bid, slots.data(), slots.size());
+        if (!st) st = gemvq_act_write(ctx, m->bpos, &p0, 1);  // the chunk's first position
         w.clear();
         build_chunk(*m, uint32_t(nt), w);
         if (!st) st = gemvq_run(ctx, w.data(), unsigned(w.size() / GEMVQ_CMD_WORDS));

@@ -93,8 +93,11 @@ def gdn(hv: int, hk: int, q: int, k: int, v: int, g: int, beta: int, y: int, src
 
 
 def attn(n_head: int, n_head_kv: int, q: int, kv: int, y: int, head_dim: int, n_rot: int, pos_off: int,
-         k: int, v: int, scale: float, eps: float, qn: int, kn: int, cs: int, gate: int | None = None) -> list[int]:
-    flags = 1 if gate is not None else 0
+         k: int, v: int, scale: float, eps: float, qn: int, kn: int, cs: int, gate: int | None = None,
+         n_tok: int = 1) -> list[int]:
+    """n_tok > 1: tokens at positions act[pos_off] + t with packed rows (q / gate, k, v and y of token t follow
+    those of token t - 1)."""
+    flags = (1 if gate is not None else 0) | ((n_tok << 16) if n_tok > 1 else 0)
     out = cmd(OP_ATTN, n_head | (n_head_kv << 16), q, kv, y, head_dim | (n_rot << 16), pos_off, flags)
     out += cmd(k, v, fbits(scale), fbits(eps), qn, kn, cs, gate or 0)
     return out

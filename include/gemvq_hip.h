@@ -50,6 +50,10 @@
  *             n_rot floats with the cos/sin table at cs_off (n_rot floats per position), K and V stored as fp16 in
  *             KV buffer kv at the position act[pos_off], softmax(q k^T * scale) V over positions 0..pos, then
  *             flags bit0: y = sigmoid(gate) * y with the gate rows at gate_off (stride 2 * head_dim).
+ *             flags bits 16..23 = n_tok (0 or 1: one token; at most GEMVQ_GEMM_MAX_TOK): tokens t < n_tok at positions
+ *             act[pos_off] + t, as n_tok one-token commands run in order (token t sees the keys of tokens < t), with
+ *             packed rows: token t's q and gate rows start t * n_head * (q row stride) floats on, its k and v rows
+ *             t * n_head_kv * head_dim, its output t * n_head * head_dim. Results are bit-identical to those commands.
  *   GET_ROWS  [13, format, rows, cols, w_off lo, w_off hi, id_off, y_off]  y = dequantized row act_i32[id_off].
  *   ARGMAX    [14, n, x_off, key_off, 0, 0, 0, 0]  max(packed key at act[key_off..+1]) with the first index of the
  *             maximum of x; the key must be cleared (NEXT_TOKEN does it).
@@ -119,8 +123,8 @@ extern "C" {
 #define GEMVQ_MAX_CMDS 4096u
 /* Feature words (gemvqc16.h:126-134 layout, marker 0x6B51 / 0x6B52). */
 #define GEMVQ_FEATURES 0x6B51FFFBu
-#define GEMVQ_FEATURES2 0x6B520007u /* bit0 SILU_MUL sigmoid + strided g, bit1 ATTN/GET_ROWS/ARGMAX/NEXT_TOKEN,
-                                       bit2 GEMM */
+#define GEMVQ_FEATURES2 0x6B52000Fu /* bit0 SILU_MUL sigmoid + strided g, bit1 ATTN/GET_ROWS/ARGMAX/NEXT_TOKEN,
+                                       bit2 GEMM, bit3 ATTN n_tok */
 
 typedef struct gemvq_ctx gemvq_ctx;
 

@@ -214,6 +214,71 @@ def test_attention(gq, orc, ctx, nh, nkv, hd, nrot, n_ctx, npos, checks):
     assert np.array_equal(k_dev, kc[:npos].ravel()) and np.array_equal(v_dev, vc[:npos].ravel())
 
 
+@pytest.mark.parametrize("nh,nkv,hd,nrot,n_ctx,p0,ntok", [
+    (16, 4, 256, 64, 200, 50, 32),  # Qwen3.5 shape, the batch crosses a chunk boundary
+    (16, 4, 256, 64, 200, 0, 5),    # from an empty cache
+    (16, 4, 256, 64, 200, 190, 16),  # the last six positions are past the capacity (not stored, no output)
+    (6, 2, 128, 128, 1100, 1020, 7),  # 17 chunks: two load rounds in the combine
+])
+def test_attention_tokens(gq, orc, ctx, nh, nkv, hd, nrot, n_ctx, p0, ntok):
+    """One ATTN command over n_tok tokens (positions act[pos] + t, packed rows) against n_tok one-token commands on
+    a second KV buffer with the same history: outputs and caches bit for bit, and the oracle for the last stored
+    token."""
+    kv_one, kv_batch = ctx.kv_create(n_ctx, nkv, hd), ctx.kv_create(n_ctx, nkv, hd)
+    qrow, kvrow, arow = 2 * nh * hd, nkv * hd, nh * hd
+    O = dict(q=0, k=262144, v=294912, qn=327680, kn=327936, pos=328192, y=328704, y2=460800, cs=600064)
+    qn = gq.uniform(2, 61, hd, 0.5, 1.5)
+    kn = gq.uniform(2, 62, hd, 0.5, 1.5)
+    table = np.concatenate([orc.rope_cache(p, nrot, 1e7) for p in range(n_ctx)])
+    ctx.write(O["qn"], qn)
+    ctx.write(O["kn"], kn)
+    ctx.write(O["cs"], table)
+
+    def one(kv, t, y):  # the one-token command of packed token t (its position in pos slot t)
+        return gq.attn(nh, nkv, O["q"] + t * qrow, kv, y, hd, nrot, O["pos"] + 16 * t, O["k"] + t * kvrow,
+                       O["v"] + t * kvrow, 1 / 16, 1e-6, O["qn"], O["kn"], O["cs"], gate=O["q"] + t * qrow + hd)
+
+    def tokens(first, n, seed):  # packed q + gate, k, v rows and the position slots of n tokens
+        qg, k, v = gq.normal(4, seed, n * qrow), gq.normal(4, seed + 1, n * kvrow), gq.normal(4, seed + 2, n * kvrow)
+        ctx.write(O["q"], qg)
+        ctx.write(O["k"], k)
+        ctx.write(O["v"], v)
+        slots = np.zeros(16 * 32, np.int32)
+        slots[0:16 * n:16] = np.arange(first, first + n)
+        ctx.write(O["pos"], slots)
+        return qg
+
+    for b0 in range(0, p0, 32):  # the same history in both buffers
+        n = min(32, p0 - b0)
+        tokens(b0, n, 100 + b0)
+        assert ctx.run(sum((one(kv, t, O["y"]) for t in range(n) for kv in (kv_one, kv_batch)), [])) == 0, ctx.error()
+    qg = tokens(p0, ntok, 7)
+    sentinel = np.full(ntok * arow, -7.25, np.float32)
+    ctx.write(O["y"], sentinel)
+    ctx.write(O["y2"], sentinel)
+    assert ctx.run(sum((one(kv_one, t, O["y"] + t * arow) for t in range(ntok)), [])) == 0, ctx.error()
+    batch = gq.attn(nh, nkv, O["q"], kv_batch, O["y2"], hd, nrot, O["pos"], O["k"], O["v"], 1 / 16, 1e-6, O["qn"],
+                    O["kn"], O["cs"], gate=O["q"] + hd, n_tok=ntok)
+    assert ctx.run(batch) == 0, ctx.error()
+    y_one, y_batch = ctx.read(O["y"], ntok * arow), ctx.read(O["y2"], ntok * arow)
+    assert_bits(y_batch, y_one, "batched vs one-token outputs")
+    npos = min(n_ctx, p0 + ntok)
+    k1, v1 = ctx.kv_read(kv_one, 0, npos, kvrow)
+    k2, v2 = ctx.kv_read(kv_batch, 0, npos, kvrow)
+    assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
+    stored = npos - p0
+    assert np.all(y_batch[stored * arow:] == -7.25) and not np.any(y_batch[:stored * arow] == -7.25)
+    t, pos = stored - 1, npos - 1  # the oracle for the last stored token
+    q_t = qg[t * qrow:(t + 1) * qrow]
+    qh = orc.rope(orc.rownorm(q_t, qn, hd, nh, 1e-6, 0, 2 * hd), table[pos * nrot:(pos + 1) * nrot], nrot, hd, nh)
+    att = orc.attn(qh, k2.reshape(npos, nkv, hd), v2.reshape(npos, nkv, hd), nh, nkv, hd, pos + 1, 1 / 16)
+    want = orc.silu_mul(q_t.reshape(nh, 2 * hd)[:, hd:].ravel(), att, sigmoid=True)
+    assert_bits(y_batch[t * arow:(t + 1) * arow], want, "oracle, last stored token")
+    too_many = gq.attn(nh, nkv, O["q"], kv_batch, O["y2"], hd, nrot, O["pos"], O["k"], O["v"], 1 / 16, 1e-6,
+                       O["qn"], O["kn"], O["cs"], gate=O["q"] + hd, n_tok=33)
+    assert ctx.run(too_many) == 1
+
+
 @pytest.mark.parametrize("t", [2, 14])
 def test_gemv_epilogs_on_streamed_rows(gq, orc, t):
     """Members long enough that each wave streams several chunks of rows (50000 rows: more than the resident waves
