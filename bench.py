@@ -116,7 +116,8 @@ def _cfg_units(seed: int = 0):
     def c1(ctx):
         offs = [ctx.upload(gq.Q4_0, R1, K1, w1) for _ in range(C1_COPIES)]
         ctx.write(0, x1)
-        return lambda i: gq.gemv(gq.Q4_0, R1, K1, offs[i], 0, 4096)
+        ctx.write(16384, x1)  # consecutive copies read different (equal) x: each is its own launch, not a group
+        return lambda i: gq.gemv(gq.Q4_0, R1, K1, offs[i], 16384 * (i & 1), 4096)
     units.append(("C1", "Q4_0 GEMV 9728x2560", w1.size + 4 * K1 + 4 * R1, C1_COPIES, c1,
                   lambda orc: (orc.fx_gemv, (gq.Q4_0, w1, x1, R1, K1))))
 
@@ -158,12 +159,14 @@ def _cfg_units(seed: int = 0):
     def c3h(ctx):
         offs = [ctx.upload(gq.Q6_K, V, D3, wh) for _ in range(2)]
         ctx.write(0, x3)
-        return lambda i: gq.gemv(gq.Q6_K, V, D3, offs[i], 0, 8192)
+        ctx.write(4096, x3)
+        return lambda i: gq.gemv(gq.Q6_K, V, D3, offs[i], 4096 * (i & 1), 8192)
 
     def c35(ctx):
         offs = [ctx.upload(gq.Q5_K, 12288, D3, w5) for _ in range(16)]
         ctx.write(0, x3)
-        return lambda i: gq.gemv(gq.Q5_K, 12288, D3, offs[i], 0, 8192)
+        ctx.write(4096, x3)
+        return lambda i: gq.gemv(gq.Q5_K, 12288, D3, offs[i], 4096 * (i & 1), 8192)
 
     sl = 16384  # the CPU times a row slice of the head and scales it
     units.append(("C3 head", "Q6_K GEMV 151936x4096", wh.size + 4 * D3 + 4 * V, 2, c3h,
@@ -225,10 +228,12 @@ def configs(args) -> int:
         build = setup(ctx)
         cmds = sum((build(i) for i in range(copies)), [])
         g = ctx.graph(cmds)
+        launches = ctx.launch_count()  # of the graph's list
         ctx.replay(g, 2)
         ctx.sync()
         t_graph = ctx.graph_time_us(g, 5) / copies
         stats = profile(ctx, np.array(build(0), np.uint32), args.profile_reps)
+        assert launches == copies * len(stats), (name, launches, copies, len(stats))  # no launch spans two copies
         t_single = sum(s["us"] for s in stats)
         ctx.close()
         spec = cpu(oracle)
@@ -239,7 +244,8 @@ def configs(args) -> int:
         fn(*fargs)
         t_cpu = (time.perf_counter() - t0) * scale
         line = {"config": name, "what": desc, "algorithmic_bytes": nbytes, "copies_rotated": copies,
-                "graph_us_per_unit": round(t_graph, 3), "graph_GBps": round(nbytes / t_graph / 1e3, 1),
+                "graph_us_per_unit": round(t_graph, 3), "graph_launches_per_unit": launches / copies,
+                "graph_GBps": round(nbytes / t_graph / 1e3, 1),
                 "graph_frac_of_8TBps": round(nbytes / t_graph / 1e3 / HBM_PEAK_GBPS, 4),
                 "single_launch_device_us": round(t_single, 3), "launches_per_unit": len(stats),
                 "cpu_oracle_s": round(t_cpu, 4), "cpu_GBps": round(nbytes / t_cpu / 1e9, 2),
@@ -262,40 +268,47 @@ def batched(args) -> int:
         copies = max(2, int(np.ceil(520e6 / per)))
         ctx = gq.Context(act_floats=1 << 22, weight_bytes=per * copies + (1 << 20))
         offs = [[ctx.upload(gq.Q4_0, R, K, w) for _ in range(mats)] for _ in range(copies)]
-        X, NW, Y, YG, RES = 0, 1 << 19, 1 << 20, 3 << 19, 1 << 21  # 32 rows of up to 12288 floats each
-        ctx.write(X, gq.normal(0, 91, 32 * K))
+        # 32 rows of up to 12288 floats each; consecutive copies read X and X2 (equal rows) in turn, so no GEMV
+        # group or reused quantization spans two copies
+        X, X2, NW, Y, YG, RES = 0, 1 << 19, 15 << 16, 1 << 20, 3 << 19, 1 << 21
+        xs = gq.normal(0, 91, 32 * K)
+        ctx.write(X, xs)
+        ctx.write(X2, xs)
         ctx.write(NW, gq.uniform(0, 92, K, 0.5, 1.5))
         ctx.write(RES, gq.normal(0, 93, 32 * R))
         norm = dict(norm_w=NW, eps=1e-6, norm_flags=gq.NORM_DEFER) if pair else {}
 
-        def unit(o, m):
+        def unit(o, m, x):
             if pair:
-                return (gq.gemm(gq.Q4_0, R, K, o[0], X, YG, m, K, R, gq.GEMV_SWIGLU, **norm) +
-                        gq.gemm(gq.Q4_0, R, K, o[1], X, Y, m, K, R, **norm))
+                return (gq.gemm(gq.Q4_0, R, K, o[0], x, YG, m, K, R, gq.GEMV_SWIGLU, **norm) +
+                        gq.gemm(gq.Q4_0, R, K, o[1], x, Y, m, K, R, **norm))
             if K == 12288:
-                return gq.gemm(gq.Q4_0, R, K, o[0], X, Y, m, K, R, gq.GEMV_ADD, RES, R)
-            return gq.gemm(gq.Q4_0, R, K, o[0], X, Y, m, K, R)
+                return gq.gemm(gq.Q4_0, R, K, o[0], x, Y, m, K, R, gq.GEMV_ADD, RES, R)
+            return gq.gemm(gq.Q4_0, R, K, o[0], x, Y, m, K, R)
 
-        def single(o):
+        def single(o, x):
             if pair:
-                return (gq.rmsnorm(K, X, NW, YG, 1e-6, flags=gq.NORM_DEFER) + gq.gemv(gq.Q4_0, R, K, o[0], YG, Y, gq.GEMV_SWIGLU) +
+                return (gq.rmsnorm(K, x, NW, YG, 1e-6, flags=gq.NORM_DEFER) + gq.gemv(gq.Q4_0, R, K, o[0], YG, Y, gq.GEMV_SWIGLU) +
                         gq.gemv(gq.Q4_0, R, K, o[1], YG, Y))
             if K == 12288:
-                return gq.gemv(gq.Q4_0, R, K, o[0], X, Y, gq.GEMV_ADD) + gq.add(R, Y, RES, Y)
-            return gq.gemv(gq.Q4_0, R, K, o[0], X, Y)
+                return gq.gemv(gq.Q4_0, R, K, o[0], x, Y, gq.GEMV_ADD) + gq.add(R, Y, RES, Y)
+            return gq.gemv(gq.Q4_0, R, K, o[0], x, Y)
 
-        g1 = ctx.graph(sum((single(o) for o in offs), []))
+        g1 = ctx.graph(sum((single(o, (X, X2)[i & 1]) for i, o in enumerate(offs)), []))
+        l1 = ctx.launch_count() / copies
         ctx.replay(g1, 2)
         t1 = ctx.graph_time_us(g1, 5) / copies
         for m in (1, 2, 4, 8, 16, 32):
-            g = ctx.graph(sum((unit(o, m) for o in offs), []))
+            g = ctx.graph(sum((unit(o, m, (X, X2)[i & 1]) for i, o in enumerate(offs)), []))
+            lm = ctx.launch_count() / copies
             ctx.replay(g, 2)
             t = ctx.graph_time_us(g, 5) / copies
             ops = 2.0 * R * K * m * mats
-            print(json.dumps({"batched": name, "tokens": m, "us_per_launch_pair": round(t, 3),
+            print(json.dumps({"batched": name, "tokens": m, "us_per_copy": round(t, 3), "launches_per_copy": lm,
                               "weight_GBps": round(per / t / 1e3, 1), "token_rows_per_us": round(m / t, 3),
                               "int8_TOPs": round(ops / t / 1e6, 2), "vs_single_token": round(m * t1 / t, 2),
-                              "single_token_us": round(t1, 3), "copies_rotated": copies}), flush=True)
+                              "single_token_us": round(t1, 3), "single_token_launches": l1,
+                              "copies_rotated": copies}), flush=True)
         ctx.close()
     return 0
 
