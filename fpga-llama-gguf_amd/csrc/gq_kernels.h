@@ -154,9 +154,10 @@ struct AttnArgs {
 
 struct GetRowsArgs {
     WeightView w;
-    const int32_t * id;
-    float * y;
+    const int32_t * id;   // token t's id at id[16 t]
+    float * y;            // token t's row at y + t * cols
     int rows, cols, type;
+    int n_tok;
 };
 
 struct NextTokenArgs {

@@ -68,8 +68,15 @@ __global__ void conv_kernel(ConvArgs a) {
     if (c >= a.ch) return;
     float s0 = a.s_src[3 * c], s1 = a.s_src[3 * c + 1], s2 = a.s_src[3 * c + 2];
     const float w0 = a.w[4 * c], w1 = a.w[4 * c + 1], w2 = a.w[4 * c + 2], w3 = a.w[4 * c + 3];
-    for (int t = 0; t < a.n_tok; ++t) {
-        const float x = a.x[size_t(t) * a.ch + c];
+    // every token's input is requested before the first output is stored (y may be x: a token's output replaces
+    // only its own input)
+    float xs[GEMM_MAX_TOK];
+#pragma unroll
+    for (int t = 0; t < GEMM_MAX_TOK; ++t) xs[t] = t < a.n_tok ? a.x[size_t(t) * a.ch + c] : 0.0f;
+#pragma unroll
+    for (int t = 0; t < GEMM_MAX_TOK; ++t) {
+        if (t >= a.n_tok) break;
+        const float x = xs[t];
         float sum = 0.0f;
         sum += s0 * w0;
         sum += s1 * w1;
@@ -110,13 +117,96 @@ __global__ void rope_kernel(RopeArgs a) {
 // ---- GDN step (gemvqc_gdn.h:73-187 with the input load of :223-281) ----
 // Workgroup (value head h, chunk of 32 state rows), 128 threads: 16 lanes per row, 8 consecutive floats per lane.
 // The rows of a head are independent given q, k, v, beta and the decay, so a chunk needs nothing from the others.
-// n_tok tokens run in order with the chunk's state in registers (loaded once, stored once).
+// n_tok tokens run in order with the chunk's state in registers (loaded once, stored once); each token's inputs
+// are requested two tokens ahead, so their latency overlaps the updates of the tokens before.
 constexpr int GDN_ROWS = 32;
+constexpr int GDN_IT = GDN_ROWS / 8;
+
+struct GdnIn {  // one token's inputs of this thread
+    float q[8], k[8], v[GDN_IT];
+    float g, b;
+};
+
+__device__ __forceinline__ void gdn_load(const GdnArgs & a, int tk, int h, int kh, int chunk, int l16, int grp, GdnIn & o) {
+    const float * qt = a.q + size_t(tk) * a.s_qkv, * kt = a.k + size_t(tk) * a.s_qkv, * vt = a.v + size_t(tk) * a.s_qkv;
+    const float4 * qp = reinterpret_cast<const float4 *>(qt + kh * 128 + 8 * l16);
+    const float4 * kp = reinterpret_cast<const float4 *>(kt + kh * 128 + 8 * l16);
+    const float4 q0 = qp[0], q1 = qp[1], k0 = kp[0], k1 = kp[1];
+    o.q[0] = q0.x; o.q[1] = q0.y; o.q[2] = q0.z; o.q[3] = q0.w; o.q[4] = q1.x; o.q[5] = q1.y; o.q[6] = q1.z; o.q[7] = q1.w;
+    o.k[0] = k0.x; o.k[1] = k0.y; o.k[2] = k0.z; o.k[3] = k0.w; o.k[4] = k1.x; o.k[5] = k1.y; o.k[6] = k1.z; o.k[7] = k1.w;
+#pragma unroll
+    for (int it = 0; it < GDN_IT; ++it) o.v[it] = vt[h * 128 + chunk * GDN_ROWS + it * 8 + grp];
+    o.g = a.g[size_t(tk) * a.s_gb + h];
+    o.b = a.beta[size_t(tk) * a.s_gb + h];
+}
+
+// One token on the state rows x (gemvq_ref.h:360-397): decay, delta rule, output row dot.
+__device__ __forceinline__ void gdn_token(const GdnArgs & a, const GdnIn & in, int tk, int h, int chunk, int l16, int grp,
+                                          float dtv, float av, float (&x)[GDN_IT][8]) {
+    constexpr int IT = GDN_IT;
+    float q[8], k[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        q[i] = in.q[i];
+        k[i] = in.k[i];
+    }
+    if (a.flags & 2) {  // L2 norm of q and k per key head (ggml_l2_norm)
+        float sq[8], sk[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            sq[i] = q[i] * q[i];
+            sk[i] = k[i] * k[i];
+        }
+        const float tq = pair_sum_lanes<16>(tree<8>(sq)), tkk = pair_sum_lanes<16>(tree<8>(sk));
+        const float fq = 1.0f / fmaxf(sqrtf(tq), a.l2_eps), fk = 1.0f / fmaxf(sqrtf(tkk), a.l2_eps);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            q[i] = q[i] * fq;
+            k[i] = k[i] * fk;
+        }
+    }
+    float gv = in.g, bt = in.b;
+    if (a.flags & 8) {  // gates from the raw projections: beta = sigmoid(b), g = softplus(a_raw + dt) * a
+        gv = softplus_(in.g + dtv) * av;
+        bt = sigmoid_(in.b);
+    }
+    const float decay = expf_(gv);
+    float dot[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        float pr[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            x[it][i] = x[it][i] * decay;
+            pr[i] = x[it][i] * k[i];
+        }
+        dot[it] = tree<8>(pr);
+    }
+    pair_sum_lanes_n<16, IT>(dot);
+    float out[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const float delta = (in.v[it] - dot[it]) * bt;
+        float pr[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            x[it][i] = x[it][i] + k[i] * delta;
+            pr[i] = x[it][i] * q[i];
+        }
+        out[it] = tree<8>(pr);
+    }
+    pair_sum_lanes_n<16, IT>(out);
+    if (l16 == 0) {
+#pragma unroll
+        for (int it = 0; it < IT; ++it) a.y[size_t(tk) * a.s_y + h * 128 + chunk * GDN_ROWS + it * 8 + grp] = out[it] * a.scale;
+    }
+}
+
 __global__ __launch_bounds__(128) void gdn_kernel(GdnArgs a) {
+    constexpr int IT = GDN_IT;
     const int chunks = 128 / GDN_ROWS;
     const int h = blockIdx.x / chunks, chunk = blockIdx.x % chunks, kh = h % a.hk;
     const int l16 = threadIdx.x & 15, grp = threadIdx.x >> 4;  // 8 row groups
-    constexpr int IT = GDN_ROWS / 8;
     // all state rows of this thread are requested before any is written (src and dst may be the same rows)
     float x[IT][8];
 #pragma unroll
@@ -133,69 +223,21 @@ __global__ __launch_bounds__(128) void gdn_kernel(GdnArgs a) {
         dtv = a.dt[h];
         av = a.a[h];
     }
-    for (int tk = 0; tk < a.n_tok; ++tk) {
-        const float * qt = a.q + size_t(tk) * a.s_qkv, * kt = a.k + size_t(tk) * a.s_qkv, * vt = a.v + size_t(tk) * a.s_qkv;
-        float q[8], k[8], vj[IT];
-        {
-            const float4 * qp = reinterpret_cast<const float4 *>(qt + kh * 128 + 8 * l16);
-            const float4 * kp = reinterpret_cast<const float4 *>(kt + kh * 128 + 8 * l16);
-            const float4 q0 = qp[0], q1 = qp[1], k0 = kp[0], k1 = kp[1];
-            q[0] = q0.x; q[1] = q0.y; q[2] = q0.z; q[3] = q0.w; q[4] = q1.x; q[5] = q1.y; q[6] = q1.z; q[7] = q1.w;
-            k[0] = k0.x; k[1] = k0.y; k[2] = k0.z; k[3] = k0.w; k[4] = k1.x; k[5] = k1.y; k[6] = k1.z; k[7] = k1.w;
-        }
-#pragma unroll
-        for (int it = 0; it < IT; ++it) vj[it] = vt[h * 128 + chunk * GDN_ROWS + it * 8 + grp];
-        const float g_raw = a.g[size_t(tk) * a.s_gb + h], b_raw = a.beta[size_t(tk) * a.s_gb + h];
-        if (a.flags & 2) {  // L2 norm of q and k per key head (ggml_l2_norm)
-            float sq[8], sk[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                sq[i] = q[i] * q[i];
-                sk[i] = k[i] * k[i];
-            }
-            const float tq = pair_sum_lanes<16>(tree<8>(sq)), tkk = pair_sum_lanes<16>(tree<8>(sk));
-            const float fq = 1.0f / fmaxf(sqrtf(tq), a.l2_eps), fk = 1.0f / fmaxf(sqrtf(tkk), a.l2_eps);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                q[i] = q[i] * fq;
-                k[i] = k[i] * fk;
-            }
-        }
-        float gv = g_raw, bt = b_raw;
-        if (a.flags & 8) {  // gates from the raw projections: beta = sigmoid(b), g = softplus(a_raw + dt) * a
-            gv = softplus_(g_raw + dtv) * av;
-            bt = sigmoid_(b_raw);
-        }
-        const float decay = expf_(gv);
-        float dot[IT];
-#pragma unroll
-        for (int it = 0; it < IT; ++it) {
-            float pr[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                x[it][i] = x[it][i] * decay;
-                pr[i] = x[it][i] * k[i];
-            }
-            dot[it] = tree<8>(pr);
-        }
-        pair_sum_lanes_n<16, IT>(dot);
-        float out[IT];
-#pragma unroll
-        for (int it = 0; it < IT; ++it) {
-            const float delta = (vj[it] - dot[it]) * bt;
-            float pr[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                x[it][i] = x[it][i] + k[i] * delta;
-                pr[i] = x[it][i] * q[i];
-            }
-            out[it] = tree<8>(pr);
-        }
-        pair_sum_lanes_n<16, IT>(out);
-        if (l16 == 0) {
-#pragma unroll
-            for (int it = 0; it < IT; ++it) a.y[size_t(tk) * a.s_y + h * 128 + chunk * GDN_ROWS + it * 8 + grp] = out[it] * a.scale;
-        }
+    // a ring of three token inputs: token tk + 2 is requested before token tk runs (uniform branches: only tokens
+    // that exist are loaded)
+    const int n = a.n_tok;
+    GdnIn r0, r1, r2;
+    gdn_load(a, 0, h, kh, chunk, l16, grp, r0);
+    if (n > 1) gdn_load(a, 1, h, kh, chunk, l16, grp, r1);
+    for (int tk = 0; tk < n; tk += 3) {
+        if (tk + 2 < n) gdn_load(a, tk + 2, h, kh, chunk, l16, grp, r2);
+        gdn_token(a, r0, tk, h, chunk, l16, grp, dtv, av, x);
+        if (tk + 1 >= n) break;
+        if (tk + 3 < n) gdn_load(a, tk + 3, h, kh, chunk, l16, grp, r0);
+        gdn_token(a, r1, tk + 1, h, chunk, l16, grp, dtv, av, x);
+        if (tk + 2 >= n) break;
+        if (tk + 4 < n) gdn_load(a, tk + 4, h, kh, chunk, l16, grp, r1);
+        gdn_token(a, r2, tk + 2, h, chunk, l16, grp, dtv, av, x);
     }
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
@@ -479,8 +521,9 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
 
 // ---- embedding rows (ggml dequantize_row_*) ----
 __global__ void get_rows_kernel(GetRowsArgs a) {
-    const int id = *a.id;
+    const int id = a.id[16 * blockIdx.y];
     if (id < 0 || id >= a.rows) return;
+    float * const yt = a.y + size_t(blockIdx.y) * a.cols;  // this token's row
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < a.cols; i += gridDim.x * blockDim.x) {
         float y;
         if (a.type == T_Q6_K) {
@@ -506,7 +549,7 @@ __global__ void get_rows_kernel(GetRowsArgs a) {
             const int8_t q = int8_t(j < 16 ? a.w.a[bi * 16 + j] : a.w.b[bi * 16 + j - 16]);
             y = float(q) * h2f(*reinterpret_cast<const uint16_t *>(a.w.c + bi * 2));
         }
-        a.y[i] = y;
+        yt[i] = y;
     }
 }
 
@@ -610,7 +653,7 @@ hipError_t launch_attn(const AttnArgs & a, hipStream_t s) {
 }
 
 hipError_t launch_get_rows(const GetRowsArgs & a, hipStream_t s) {
-    GQ_LAUNCH(get_rows_kernel, dim3((a.cols + 255) / 256), dim3(256), 0, s, a);
+    GQ_LAUNCH(get_rows_kernel, dim3((a.cols + 255) / 256, a.n_tok > 1 ? a.n_tok : 1), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -432,12 +432,14 @@ struct Compiler {
             }
             case GEMVQ_OP_GET_ROWS: {
                 const int type = int(k[1] & 0xffu), rows = int(k[2]), cols = int(k[3]);
+                const uint32_t ntok = (k[1] >> 16) & 0xffu ? (k[1] >> 16) & 0xffu : 1;  // ids 16 floats apart
                 const uint64_t woff = uint64_t(k[4]) | (uint64_t(k[5]) << 32);
                 if (type != T_Q6_K && type != T_Q4_0 && type != T_Q8_0) return reject(i, "GET_ROWS type");
+                if (ntok > GEMVQ_GEMM_MAX_TOK) return reject(i, "GET_ROWS tokens");
                 if (!weight(woff, type, rows, cols)) return reject(i, "GET_ROWS weight");
-                if (!range(k[6], 1) || !range(k[7], uint64_t(cols))) return reject(i, "GET_ROWS range");
+                if (!range(k[6], 16ull * (ntok - 1) + 1) || !range(k[7], uint64_t(cols) * ntok)) return reject(i, "GET_ROWS range");
                 GetRowsArgs a{weight_view(c->warena + woff, type, rows, cols), reinterpret_cast<const int32_t *>(A(k[6])),
-                              A(k[7]), rows, cols, type};
+                              A(k[7]), rows, cols, type, int(ntok)};
                 out.push_back(LRows{a});
                     spans.push_back({int(i), 1});
                 break;

@@ -45,6 +45,7 @@ struct gemvq_qwen35 {
     std::map<std::string, T> t;
     std::vector<uint32_t> cmds;
     int graph = -1;
+    int chunk_graph = -1;  // the prefill's full-chunk command list (positions and ids come from the act slots)
     std::vector<int> kv;  // per layer (attention layers only)
     // activation layout
     uint32_t tok = 16, pos = 32, key = 48;
@@ -183,9 +184,8 @@ bool build_chunk(const gemvq_qwen35 & m, uint32_t ntok, std::vector<uint32_t> & 
     const uint32_t hd = uint32_t(c.head_dim), qrow = 2 * uint32_t(c.n_head) * hd, kvrow = uint32_t(c.n_head_kv) * hd,
                    arow = uint32_t(c.n_head) * hd, hvs = hv * S, gb = uint32_t(up16(hv));
     const T * emb = W("token_embd.weight");
-    for (uint32_t i = 0; i < ntok; ++i)
-        e.cmd({GEMVQ_OP_GET_ROWS, uint32_t(emb->d->type), uint32_t(emb->d->ne1), uint32_t(emb->d->ne0),
-               uint32_t(emb->w_off), uint32_t(emb->w_off >> 32), m.bid + 16 * i, m.bh + i * E});
+    e.cmd({GEMVQ_OP_GET_ROWS, uint32_t(emb->d->type) | (ntok << 16), uint32_t(emb->d->ne1), uint32_t(emb->d->ne0),
+           uint32_t(emb->w_off), uint32_t(emb->w_off >> 32), m.bid, m.bh});  // the chunk's ids, 16 floats apart
     int slot = 0;
     for (int il = 0; il < c.n_layer; ++il) {
         const std::string p = "blk." + std::to_string(il) + ".";
@@ -202,12 +202,13 @@ bool build_chunk(const gemvq_qwen35 & m, uint32_t ntok, std::vector<uint32_t> & 
                    W(p + "attn_k_norm.weight")->act_off, m.rope, m.bqg + hd});
             e.gemm(*W(p + "attn_output.weight"), m.batt, arow, m.bh, E, ntok, GEMVQ_GEMV_ADD, m.bh, E);
         } else {
+            // the four projections of the normed rows back to back (one quantization), then the conv
             e.gemm(*W(p + "attn_qkv.weight"), m.bh, E, m.bqkv, ch, ntok, 0, 0, 0, an, eps);
-            e.cmd({GEMVQ_OP_CONV, ch, m.bqkv, W(p + "ssm_conv1d.weight")->act_off, m.bcqkv, m.conv_state[il],
-                   m.conv_state[il], 1u | (ntok << 16)});
             e.gemm(*W(p + "attn_gate.weight"), m.bh, E, m.bz, hvs, ntok, GEMVQ_GEMV_SILU, 0, 0, an, eps);
             e.gemm(*W(p + "ssm_beta.weight"), m.bh, E, m.bbeta, gb, ntok, 0, 0, 0, an, eps);
             e.gemm(*W(p + "ssm_alpha.weight"), m.bh, E, m.balpha, gb, ntok, 0, 0, 0, an, eps);
+            e.cmd({GEMVQ_OP_CONV, ch, m.bqkv, W(p + "ssm_conv1d.weight")->act_off, m.bcqkv, m.conv_state[il],
+                   m.conv_state[il], 1u | (ntok << 16)});
             const uint32_t row = uint32_t(slot) * hv * 128u;
             const uint32_t flags = GEMVQ_GDN_L2_QK | GEMVQ_GDN_GATED | GEMVQ_GDN_GATES | GEMVQ_GDN_Z_SILU;
             e.cmd({GEMVQ_OP_GDN, hv | (hk << 16), m.bcqkv, m.bcqkv + hk * S, m.bcqkv + 2 * hk * S, m.balpha, m.bbeta, m.by});
@@ -403,6 +404,7 @@ gemvq_qwen35 * gemvq_qwen35_create(gemvq_ctx * ctx, const gemvq_qw_config * cfg,
 void gemvq_qwen35_destroy(gemvq_qwen35 * m) {
     if (!m) return;
     if (m->graph >= 0) gemvq_graph_destroy(m->ctx, m->graph);
+    if (m->chunk_graph >= 0) gemvq_graph_destroy(m->ctx, m->chunk_graph);
     delete m;
 }
 
@@ -455,11 +457,23 @@ int gemvq_qwen35_prefill(gemvq_qwen35 * m, int n) {
         for (int i = 0; i < nt; ++i) slots[size_t(16) * i] = m->prompt_ids[size_t(p0 + i)];
         st = gemvq_act_write(ctx, m->bid, slots.data(), slots.size());
         if (!st) st = gemvq_act_write(ctx, m->bpos, &p0, 1);  // the chunk's first position
-        w.clear();
-        build_chunk(*m, uint32_t(nt), w);
-        if (!st) st = gemvq_run(ctx, w.data(), unsigned(w.size() / GEMVQ_CMD_WORDS));
+        if (!st && nt == int(GEMVQ_GEMM_MAX_TOK)) {
+            // full chunks replay one captured list: it reads the chunk's ids and first position from the slots
+            // just written (the write waits for the previous replay; the replay follows it on the same stream)
+            if (m->chunk_graph < 0) {
+                w.clear();
+                build_chunk(*m, GEMVQ_GEMM_MAX_TOK, w);
+                st = gemvq_graph_create(ctx, w.data(), unsigned(w.size() / GEMVQ_CMD_WORDS), &m->chunk_graph);
+            }
+            if (!st) st = gemvq_graph_replay(ctx, m->chunk_graph, 1);
+        } else if (!st) {
+            w.clear();
+            build_chunk(*m, uint32_t(nt), w);
+            st = gemvq_run(ctx, w.data(), unsigned(w.size() / GEMVQ_CMD_WORDS));
+        }
         p0 += nt;
     }
+    if (!st) st = gemvq_sync(ctx);
     if (st) return st;
     // what the steps' NEXT_TOKEN would have left: the next prompt token at the next position, the ids so far
     const int32_t end = pos + n, tok = m->prompt_ids[size_t(end)];

@@ -103,8 +103,10 @@ def attn(n_head: int, n_head_kv: int, q: int, kv: int, y: int, head_dim: int, n_
     return out
 
 
-def get_rows(fmt: int, rows: int, cols: int, w_off: int, id_off: int, y_off: int) -> list[int]:
-    return cmd(OP_GET_ROWS, fmt, rows, cols, w_off & 0xFFFFFFFF, w_off >> 32, id_off, y_off)
+def get_rows(fmt: int, rows: int, cols: int, w_off: int, id_off: int, y_off: int, n_tok: int = 1) -> list[int]:
+    """n_tok > 1: token t's id at act[id_off + 16 t], its row at y_off + t * cols."""
+    return cmd(OP_GET_ROWS, fmt | ((n_tok << 16) if n_tok > 1 else 0), rows, cols, w_off & 0xFFFFFFFF, w_off >> 32,
+               id_off, y_off)
 
 
 def argmax(n: int, x: int, key: int) -> list[int]:

@@ -54,7 +54,9 @@
  *             act[pos_off] + t, as n_tok one-token commands run in order (token t sees the keys of tokens < t), with
  *             packed rows: token t's q and gate rows start t * n_head * (q row stride) floats on, its k and v rows
  *             t * n_head_kv * head_dim, its output t * n_head * head_dim. Results are bit-identical to those commands.
- *   GET_ROWS  [13, format, rows, cols, w_off lo, w_off hi, id_off, y_off]  y = dequantized row act_i32[id_off].
+ *   GET_ROWS  [13, format | n_tok << 16, rows, cols, w_off lo, w_off hi, id_off, y_off]  y = dequantized row
+ *             act_i32[id_off]; with n_tok (2..GEMVQ_GEMM_MAX_TOK) token t's id is act_i32[id_off + 16 t] and its row
+ *             goes to y_off + t * cols.
  *   ARGMAX    [14, n, x_off, key_off, 0, 0, 0, 0]  max(packed key at act[key_off..+1]) with the first index of the
  *             maximum of x; the key must be cleared (NEXT_TOKEN does it).
  *   NEXT_TOKEN [15, key_off, tok_off, pos_off, prompt_off, n_prompt, out_off, 0]  token = argmax of the key, or
@@ -124,7 +126,7 @@ extern "C" {
 /* Feature words (gemvqc16.h:126-134 layout, marker 0x6B51 / 0x6B52). */
 #define GEMVQ_FEATURES 0x6B51FFFBu
 #define GEMVQ_FEATURES2 0x6B52000Fu /* bit0 SILU_MUL sigmoid + strided g, bit1 ATTN/GET_ROWS/ARGMAX/NEXT_TOKEN,
-                                       bit2 GEMM, bit3 ATTN n_tok */
+                                       bit2 GEMM, bit3 ATTN and GET_ROWS n_tok */
 
 typedef struct gemvq_ctx gemvq_ctx;
 

@@ -394,6 +394,18 @@ def test_get_rows_and_next_token(gq, orc, ctx):
     assert ctx.run(gq.get_rows(gq.Q6_K, V, D, o, 0, 1024)) == 0, ctx.error()
     rb = gq.row_bytes(gq.Q6_K, D)
     assert_bits(ctx.read(1024, D), orc.dequant_row_q6_K(w[777 * rb:778 * rb], D), "get_rows Q6_K")
+    # a block of tokens: ids 16 floats apart, rows packed; an id out of range leaves its row untouched
+    ids = [3, 999, 0, 512, -1, 777, 41]
+    slots = np.zeros(16 * len(ids), np.int32)
+    slots[::16] = ids
+    ctx.write(8192, slots)
+    ctx.write(16384, np.full(len(ids) * D, -3.5, np.float32))
+    assert ctx.run(gq.get_rows(gq.Q6_K, V, D, o, 8192, 16384, n_tok=len(ids))) == 0, ctx.error()
+    got = ctx.read(16384, len(ids) * D).reshape(len(ids), D)
+    for t, i in enumerate(ids):
+        want = orc.dequant_row_q6_K(w[i * rb:(i + 1) * rb], D) if i >= 0 else np.full(D, -3.5, np.float32)
+        assert_bits(got[t], want, f"get_rows token {t} (id {i})")
+    assert ctx.run(gq.get_rows(gq.Q6_K, V, D, o, 8192, 16384, n_tok=33)) == 1
     # NEXT_TOKEN: prompt phase then the argmax key
     KEY, TOK, POS, PR, OUT = 4096, 4112, 4128, 4144, 4400
     ctx.write(PR, np.array([5, 6, 7], np.int32))
