@@ -208,7 +208,7 @@ __device__ __forceinline__ int sum_lanes4_i32(int v) {
     return v;
 }
 
-// An integer-valued double with |d| < 2^53 as int64 (exact).
+// An integer-valued double with |d| < 2^63 as int64 (exact: the split at 2^32 and the difference are exact).
 __device__ __forceinline__ long long dint_to_i64(double d) {
     const double hi = floor(d * 2.3283064365386963e-10);  // d / 2^32
     const double lo = d - hi * 4294967296.0;              // 0 <= lo < 2^32, exact

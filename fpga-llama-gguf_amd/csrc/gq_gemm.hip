@@ -163,7 +163,8 @@ __device__ __forceinline__ float lane_of(const v4f & v, int j) { return v[j]; }
 
 // The wave's GW blocks of a staged round: per block and token tile one MFMA gives the lane's 4 sums (rows 4g + i,
 // token r); each term is floor(sumi * s) with s = fp16(d_w) * d_x * 2^40 exact in FP32 and the product exact in FP64;
-// the GW terms are summed in FP64 (integers below 2^53) and moved to the int64 totals.
+// the GW terms are summed in FP64 (exact while the sum stays below 2^53 LSB, as in the single-token kernel) and moved
+// to the int64 totals.
 template <int TYPE, bool PAIR, int T>
 __device__ __forceinline__ void round_terms(const uint8_t * lq, const uint32_t * ld, int wave, int r, int g,
                                             const XRound<T> & x, long long (*tot)[4], long long (*totu)[4]) {

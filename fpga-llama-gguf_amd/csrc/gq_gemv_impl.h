@@ -607,7 +607,8 @@ __device__ __forceinline__ void load_slot(const GemvMember & m, int r, int lane,
     o.e = *(lane < m.e_split ? pa : pb);
 }
 
-// Per-lane partial of one row (its lane's units), exact: the block terms are integers below 2^53 summed in FP64.
+// Per-lane partial of one row (its lane's units): the block terms are exact integers, summed in FP64, which is exact
+// while the partial stays below 2^53 LSB (|partial| < 8192 in output units; past that a few LSB of 2^-40 can drop).
 // dbg (block sums for the tests) is written only for a row that exists.
 template <int TYPE, int NU>
 __device__ __forceinline__ long long lane_blocks(const WB * wb, int r, bool valid, int nb, const XB * xb, int lane,

@@ -75,17 +75,18 @@ __global__ void conv_kernel(ConvArgs a) {
     for (int t = 0; t < GEMM_MAX_TOK; ++t) xs[t] = t < a.n_tok ? a.x[size_t(t) * a.ch + c] : 0.0f;
 #pragma unroll
     for (int t = 0; t < GEMM_MAX_TOK; ++t) {
-        if (t >= a.n_tok) break;
-        const float x = xs[t];
-        float sum = 0.0f;
-        sum += s0 * w0;
-        sum += s1 * w1;
-        sum += s2 * w2;
-        sum += x * w3;
-        a.y[size_t(t) * a.ch + c] = a.silu ? silu_(sum) : sum;
-        s0 = s1;
-        s1 = s2;
-        s2 = x;
+        if (t < a.n_tok) {
+            const float x = xs[t];
+            float sum = 0.0f;
+            sum += s0 * w0;
+            sum += s1 * w1;
+            sum += s2 * w2;
+            sum += x * w3;
+            a.y[size_t(t) * a.ch + c] = a.silu ? silu_(sum) : sum;
+            s0 = s1;
+            s1 = s2;
+            s2 = x;
+        }
     }
     a.s_dst[3 * c] = s0;
     a.s_dst[3 * c + 1] = s1;

@@ -45,6 +45,31 @@ def test_gemm_rows_equal_single_token_gemv(gq, orc, ctx, fmt, rows, cols, ntok):
         assert_bits(ctx.read(Y1, rows), y[t], f"GEMV command, token {t}")
 
 
+@pytest.mark.parametrize("fmt,outlier", [(2, 3e5), (8, 3e5), (3, 2e4)])
+def test_huge_activations_exact(gq, orc, ctx, fmt, outlier):
+    """Activations with outliers (block scales up to 2362): block terms reach 2^54 LSB, beyond the 2^53 LSB inside
+    which the kernels' FP64 partial sums are exact. The GEMV command and the GEMM's every token row still equal the
+    oracle's exact int64 sums bit for bit at FP32 (a partial sum can lose a few LSB of 2^-40, which moves the FP32
+    result only at a rounding boundary). (Q4_1 keeps its Q8_1 sums, fp16(sum * d), finite: outliers of 2e4.)"""
+    rows, cols, ntok = 300, 4096, 20
+    w = gq.matrix(fmt, rows, cols, 6, 40 + fmt, std=0.02)
+    off = ctx.upload(fmt, rows, cols, w)
+    x = gq.normal(6, 41, ntok * cols)
+    for t in range(0, ntok, 3):  # some tokens carry outliers, of both signs, in several blocks
+        x[t * cols + np.array([5, 1000, 2047, 4095])] = np.array([1, -1, 1, -1], np.float32) * outlier
+    X, Y, Y1 = 0, ntok * cols, ntok * cols + ntok * 512
+    ctx.write(X, x)
+    assert ctx.run(gq.gemm(fmt, rows, cols, off, X, Y, ntok, cols, 512)) == 0, ctx.error()
+    y = ctx.read(Y, ntok * 512).reshape(ntok, 512)[:, :rows]
+    for t in range(ntok):
+        want = orc.fx_gemv(fmt, w, x[t * cols:(t + 1) * cols], rows, cols)
+        assert_bits(y[t], want, f"GEMM token {t}")
+        if t % 3 == 0:
+            assert ctx.run(gq.gemv(fmt, rows, cols, off, X + t * cols, Y1)) == 0, ctx.error()
+            assert_bits(ctx.read(Y1, rows), want, f"GEMV, token {t}")
+            assert np.abs(want).max() > outlier / 300.0  # the outlier blocks dominate these rows
+
+
 @pytest.mark.parametrize("fmt", [2, 3, 8])
 def test_gemm_epilogs_and_norm(gq, orc, ctx, fmt):
     rows, cols, ntok, eps = 2000, 4096, 9, 1e-6
