@@ -229,8 +229,10 @@ __device__ __forceinline__ void round_terms(const uint8_t * lq, const uint32_t *
 // other waves' int64 totals (exact in any order), applies the epilog and stores token t's row at y + t * y_stride.
 // Loads past the last round repeat the last round (cache hits), so every load is unconditional and the waits stay
 // exact.
+// A group's workgroups are dealt to its members by tile: the member of tile b is the last whose first tile is <= b,
+// and its fields replace the first member's (the activation, columns and tokens are shared).
 template <int TYPE, bool PAIR, int T>
-__global__ __launch_bounds__(NT) void gemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(NT) void gemm_kernel(GemmArgs a0) {
     constexpr int NM = PAIR ? 2 : 1, QH = TYPE == T_Q8_0 ? 2 : 1;
     constexpr int QBUF = GT * ROW_LDS, DBUF = GT * GU;
     __shared__ __align__(16) uint8_t lq[2][NM * QH * QBUF];
@@ -238,7 +240,25 @@ __global__ __launch_bounds__(NT) void gemm_kernel(GemmArgs a) {
     __shared__ long long red[NWAVES - 1][NM][T][4][WAVE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const int r0 = int(blockIdx.x) * GT;
+    GemmArgs a = a0;
+    int tile0 = 0;
+    if (!PAIR) {
+        int mi = -1;
+        for (int i = 0; i < a0.n_more; ++i)
+            if (int(blockIdx.x) >= a0.more[i].tile0) mi = i;
+        if (mi >= 0) {
+            const GemmMore & o = a0.more[mi];
+            a.w = o.w;
+            a.y = o.y;
+            a.res = o.res;
+            a.rows = o.rows;
+            a.y_stride = o.y_stride;
+            a.res_stride = o.res_stride;
+            a.epi = o.epi;
+            tile0 = o.tile0;
+        }
+    }
+    const int r0 = (int(blockIdx.x) - tile0) * GT;
     const int nb = a.cols / 32, nr = nb / GU;
     const int lrow = min(r0 + (tid >> 4), a.rows - 1);
     long long tot[T][4], totu[PAIR ? T : 1][4];
@@ -315,7 +335,12 @@ __global__ __launch_bounds__(NT) void gemm_kernel(GemmArgs a) {
 
 template <int TYPE, bool PAIR>
 hipError_t launch_tiles(const GemmArgs & a, hipStream_t st) {
-    const dim3 grid((a.rows + GT - 1) / GT);
+    int tiles = (a.rows + GT - 1) / GT;
+    for (int i = 0; i < a.n_more; ++i) {  // members follow each other, every one at least a tile
+        if (a.more[i].tile0 != tiles || a.more[i].rows < 1) return hipErrorInvalidValue;
+        tiles += (a.more[i].rows + GT - 1) / GT;
+    }
+    const dim3 grid(tiles);
     if (a.n_tok <= GT) GQ_LAUNCH((gemm_kernel<TYPE, PAIR, 1>), grid, dim3(NT), 0, st, a);
     else GQ_LAUNCH((gemm_kernel<TYPE, PAIR, 2>), grid, dim3(NT), 0, st, a);
     return hipGetLastError();
@@ -339,8 +364,13 @@ hipError_t launch_gemm_quant(const GemmQuantArgs & a, hipStream_t s) {
 hipError_t launch_gemm(const GemmArgs & a, int type, hipStream_t s) {
     // shapes the kernels assume: whole rounds of GU blocks per wave, at most two token tiles
     if (a.rows < 1 || a.n_tok < 1 || a.n_tok > GEMM_MAX_TOK || a.cols % 512 || a.cols > GEMV_MAXK ||
-        a.y_stride < a.rows || (a.epi == EPI_ADD && a.res_stride < a.rows))
+        a.y_stride < a.rows || (a.epi == EPI_ADD && a.res_stride < a.rows) || a.n_more < 0 || a.n_more > GEMM_MAX_MORE ||
+        (a.n_more && a.epi == EPI_SWIGLU))
         return hipErrorInvalidValue;
+    for (int i = 0; i < a.n_more; ++i) {
+        const GemmMore & o = a.more[i];
+        if (o.epi == EPI_SWIGLU || o.y_stride < o.rows || (o.epi == EPI_ADD && o.res_stride < o.rows)) return hipErrorInvalidValue;
+    }
     switch (type) {
     case T_Q4_0: return launch_type<T_Q4_0>(a, s);
     case T_Q4_1: return launch_type<T_Q4_1>(a, s);

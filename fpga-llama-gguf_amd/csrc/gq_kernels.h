@@ -184,6 +184,16 @@ struct GemmQuantArgs {
     float eps;
 };
 
+constexpr int GEMM_MAX_MORE = 3;  // a GEMM group has at most four members
+
+struct GemmMore {  // a further member of a GEMM group: its own matrix, output rows and epilog, the same activation
+    WeightView w;
+    float * y;
+    const float * res;
+    int rows, y_stride, res_stride, epi;
+    int tile0;  // its first 16-row tile in the group's grid
+};
+
 struct GemmArgs {
     WeightView w;       // matrix (g of a SwiGLU pair)
     WeightView w2;      // u of a SwiGLU pair
@@ -194,6 +204,8 @@ struct GemmArgs {
     const float * res;  // ADD: res[t * res_stride + r]
     int rows, cols, n_tok, y_stride, res_stride;
     int epi;            // EPI_PLAIN, EPI_SWIGLU, EPI_ADD or EPI_SILU
+    int n_more;         // members after the first (not with a SwiGLU pair); tiles of member i + 1 follow member i's
+    GemmMore more[GEMM_MAX_MORE];
 };
 
 constexpr int GEMV_MAXK = 16384;  // GEMV columns at most

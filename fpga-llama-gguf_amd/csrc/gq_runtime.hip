@@ -559,14 +559,49 @@ struct Compiler {
             spans.push_back({int(i), int(used)});
             lastq = {true, q, k[6], x_len};
         }
-        out.push_back(LGemm{g, t});
-        spans.push_back({int(i), int(used)});
+        if (!(same && merge_gemm(g, t, int(i), int(used)))) {
+            out.push_back(LGemm{g, t});
+            spans.push_back({int(i), int(used)});
+        }
         // outputs written over the quantized rows (or the norm weight) end the reuse
         const uint32_t y_off = uint32_t(g.y - c->act), y_len = uint32_t(g.y_stride) * (ntok - 1) + uint32_t(rows);
         const bool hits_x = y_off < lastq.x_off + lastq.x_len && lastq.x_off < y_off + y_len;
         const uint32_t w_off = q.norm_w ? uint32_t(q.norm_w - c->act) : 0;
         const bool hits_w = q.norm_w && y_off < w_off + cols && w_off < y_off + y_len;
         if (hits_x || hits_w) lastq.on = false;
+        return true;
+    }
+
+    // A GEMM on the rows the previous GEMM launch quantized joins that launch as a further member (up to four, none a
+    // SwiGLU pair) when no member's output overlaps another's output or residual (so the order between them does not
+    // matter); its command span extends the launch's.
+    bool merge_gemm(const GemmArgs & g, int t, int i, int used) {
+        auto * p = out.empty() ? nullptr : std::get_if<LGemm>(&out.back());
+        if (!p || p->type != t || p->a.epi == EPI_SWIGLU || g.epi == EPI_SWIGLU || p->a.n_more >= GEMM_MAX_MORE ||
+            p->a.n_tok != g.n_tok || p->a.cols != g.cols || p->a.q != g.q)
+            return false;
+        struct R { uint64_t lo, hi; };
+        auto span = [&](const float * base, int stride, int rows) {
+            const uint64_t lo = uint64_t(base - c->act);
+            return R{lo, lo + uint64_t(stride) * uint64_t(g.n_tok - 1) + uint64_t(rows)};
+        };
+        auto meet = [](R x, R y) { return x.lo < y.hi && y.lo < x.hi; };
+        const R ny = span(g.y, g.y_stride, g.rows);
+        const bool nres = g.epi == EPI_ADD;
+        const R nr = nres ? span(g.res, g.res_stride, g.rows) : R{0, 0};
+        int tiles = 0;
+        for (int m = 0; m <= p->a.n_more; ++m) {
+            const bool first = m == 0;
+            const GemmMore * o = first ? nullptr : &p->a.more[m - 1];
+            const R y = first ? span(p->a.y, p->a.y_stride, p->a.rows) : span(o->y, o->y_stride, o->rows);
+            const int epi = first ? p->a.epi : o->epi;
+            const R res = epi == EPI_ADD ? (first ? span(p->a.res, p->a.res_stride, p->a.rows) : span(o->res, o->res_stride, o->rows))
+                                         : R{0, 0};
+            if (meet(ny, y) || (epi == EPI_ADD && meet(ny, res)) || (nres && meet(nr, y))) return false;
+            tiles += ((first ? p->a.rows : o->rows) + 15) / 16;
+        }
+        p->a.more[p->a.n_more++] = GemmMore{g.w, g.y, g.res, g.rows, g.y_stride, g.res_stride, g.epi, tiles};
+        spans.back().second = i + used - spans.back().first;
         return true;
     }
 
@@ -749,9 +784,13 @@ std::pair<std::string, uint64_t> describe(const Launch & l, int pos) {
     }
     if (auto * x = std::get_if<LGemm>(&l)) {
         const GemmArgs & a = x->a;
-        const uint64_t w = uint64_t(a.rows) * gguf_row_bytes(x->type, a.cols) * (a.epi == EPI_SWIGLU ? 2 : 1);
+        uint64_t w = uint64_t(a.rows) * gguf_row_bytes(x->type, a.cols) * (a.epi == EPI_SWIGLU ? 2 : 1);
+        uint64_t out = uint64_t(a.n_tok) * a.rows * 4 * (a.epi == EPI_ADD ? 2 : 1);
+        for (int m = 0; m < a.n_more; ++m) {
+            w += uint64_t(a.more[m].rows) * gguf_row_bytes(x->type, a.cols);
+            out += uint64_t(a.n_tok) * a.more[m].rows * 4 * (a.more[m].epi == EPI_ADD ? 2 : 1);
+        }
         const uint64_t act = uint64_t(a.n_tok) * (a.cols + (a.cols / 32) * 4);
-        const uint64_t out = uint64_t(a.n_tok) * a.rows * 4 * (a.epi == EPI_ADD ? 2 : 1);
         return {"gemm_kernel<" + std::to_string(x->type) + ">", w + act + out};
     }
     return {"next_token_kernel", 32};

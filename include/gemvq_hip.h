@@ -76,6 +76,9 @@
  *             GEMVQ_GEMV_SILU. norm_flags GEMVQ_NORM_DEFER: every token row is RMS-normalized first (weight at
  *             norm_w_off unless GEMVQ_NORM_NO_WEIGHT, GEMVQ_NORM_L2 for the L2 norm, eps), as a deferred RMSNORM
  *             before a GEMV. The rows are read before any output is written, so y may overlap x.
+ *             Consecutive GEMMs of one format on the same rows and norm words quantize the rows once and run as one
+ *             launch of up to four members, unless one is a SwiGLU pair or a member's output overlaps an earlier
+ *             member's output or residual; the results are those of the commands one by one.
  */
 #ifndef GEMVQ_HIP_H
 #define GEMVQ_HIP_H

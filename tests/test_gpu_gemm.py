@@ -183,6 +183,71 @@ def test_gemm_reuses_quantized_rows_until_overwritten(gq, orc, ctx):
         assert_bits(y2[t], orc.fx_gemv(8, w2, xn, rows, cols), f"after overwrite token {t}")
 
 
+@pytest.mark.parametrize("ntok", [3, 20])
+def test_gemm_group_of_members(gq, orc, ctx, ntok):
+    """Consecutive GEMMs of one format on the same quantized rows run as one launch (up to four members, each with its
+    own rows, output and epilog; rows that are not whole 16-row tiles); an output that overlaps an earlier member's
+    output or feeds its residual starts a new launch, so the commands' order still decides the result."""
+    cols, eps = 1024, 1e-6
+    shapes = [(100, gq.GEMV_SILU), (33, 0), (512, gq.GEMV_ADD), (16, 0), (48, 0)]
+    ws = [gq.matrix(2, r, cols, 8, 60 + j, std=0.02) for j, (r, _) in enumerate(shapes)]
+    offs = [ctx.upload(2, r, cols, w) for (r, _), w in zip(shapes, ws)]
+    x = gq.normal(8, 70, ntok * cols) * 2.0
+    nw = gq.uniform(8, 71, cols, 0.5, 1.5)
+    res = gq.normal(8, 72, ntok * 512)
+    X, NW, RES = 0, 1 << 16, 1 << 17
+    Y = [(1 << 18) + j * (1 << 15) for j in range(len(shapes))]
+    ctx.write(X, x)
+    ctx.write(NW, nw)
+    ctx.write(RES, res)
+    norm = dict(norm_w=NW, eps=eps, norm_flags=gq.NORM_DEFER)
+
+    def cmd(j, y, ys=None):
+        r, e = shapes[j]
+        ys = up16(r) if ys is None else ys
+        if e == gq.GEMV_ADD:
+            return gq.gemm(2, r, cols, offs[j], X, y, ntok, cols, ys, e, RES, 512, **norm)
+        return gq.gemm(2, r, cols, offs[j], X, y, ntok, cols, ys, e, **norm)
+
+    xn = [orc.rownorm(x[t * cols:(t + 1) * cols], nw, cols, 1, eps) for t in range(ntok)]
+
+    def want(j, t):
+        r, e = shapes[j]
+        v = orc.fx_gemv(2, ws[j], xn[t], r, cols)
+        if e == gq.GEMV_SILU:
+            return orc.unary(v, 1)
+        if e == gq.GEMV_ADD:
+            return v + res[t * 512:t * 512 + r]
+        return v
+
+    assert ctx.run(sum((cmd(j, Y[j]) for j in range(5)), [])) == 0, ctx.error()
+    assert ctx.launch_count() == 3  # one quantization, a group of four, then the fifth member's own launch
+    for j, (r, _) in enumerate(shapes):
+        got = ctx.read(Y[j], ntok * up16(r)).reshape(ntok, up16(r))[:, :r]
+        for t in range(ntok):
+            assert_bits(got[t], want(j, t), f"member {j} token {t}")
+    # the second output overlaps the first's (rows 48..80 of every token): two launches, the later command's values
+    # win where they overlap
+    assert ctx.run(cmd(0, Y[0]) + cmd(1, Y[0] + 48, ys=112)) == 0, ctx.error()
+    assert ctx.launch_count() == 3
+    got = ctx.read(Y[0], ntok * 112).reshape(ntok, 112)[:, :100]
+    for t in range(ntok):
+        first = want(0, t)
+        assert_bits(got[t, :48], first[:48], f"overlap: rows before, token {t}")
+        assert_bits(got[t, 48:81], want(1, t), f"overlap: the later command's rows, token {t}")
+        assert_bits(got[t, 81:], first[81:], f"overlap: rows after, token {t}")
+    # a member whose residual is an earlier member's output (rows 0..15 of every token): a new launch that adds the
+    # new values
+    assert ctx.run(cmd(3, RES, ys=512) + cmd(2, Y[2])) == 0, ctx.error()
+    assert ctx.launch_count() == 3
+    got = ctx.read(Y[2], ntok * 512).reshape(ntok, 512)
+    for t in range(ntok):
+        r16 = want(3, t)
+        res_t = res[t * 512:t * 512 + 512].copy()
+        res_t[:16] = r16
+        assert_bits(got[t], orc.fx_gemv(2, ws[2], xn[t], 512, cols) + res_t, f"residual after member, token {t}")
+
+
 # An activation block whose Q8_1 sum s = fp16(sum(q) * d) falls on an fp16 tie: the FP32 product sum * d is exactly
 # halfway between two fp16 values (6.986328125, sum 160), so it must round to even (0x46fc); rounding the exact
 # product once instead (a multiply fused into the conversion) gives 0x46fd.
