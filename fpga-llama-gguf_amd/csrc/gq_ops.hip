@@ -116,11 +116,13 @@ __global__ void rope_kernel(RopeArgs a) {
 }
 
 // ---- GDN step (gemvqc_gdn.h:73-187 with the input load of :223-281) ----
-// Workgroup (value head h, chunk of 32 state rows), 128 threads: 16 lanes per row, 8 consecutive floats per lane.
+// Workgroup (value head h, chunk of 8 state rows), 128 threads: 16 lanes per row, 8 consecutive floats per lane, one
+// row per thread (512 workgroups for 32 heads: the per-token chain of dependent reductions is latency-bound, so more
+// waves per SIMD hide it).
 // The rows of a head are independent given q, k, v, beta and the decay, so a chunk needs nothing from the others.
 // n_tok tokens run in order with the chunk's state in registers (loaded once, stored once); each token's inputs
 // are requested two tokens ahead, so their latency overlaps the updates of the tokens before.
-constexpr int GDN_ROWS = 32;
+constexpr int GDN_ROWS = 8;
 constexpr int GDN_IT = GDN_ROWS / 8;
 
 struct GdnIn {  // one token's inputs of this thread
