@@ -1,7 +1,7 @@
 """The batched GEMV (GEMM command) on the GPU through the C ABI. Every token's output row must equal, bit for bit, the
 oracle's single-token GEMV of that token's row and the GPU's own GEMV command on it: the same activation quantizer,
 the same exact block terms, the same epilogs, only the block sums come from int8 MFMAs. Covered: Q4_0, Q4_1 and Q8_0;
-1, 5, 16, 17 and 32 tokens (one and two token tiles, padding tokens); row counts that are not a multiple of the
+1, 5, 16, 17, 20 and 32 tokens (one and two token tiles, padding tokens); row counts that are not a multiple of the
 16-row tile; 2560, 4096 and 12288 columns; strided rows; the SwiGLU pair, residual ADD and SiLU epilogs; the folded
 per-token RMS norm (with and without weight, L2); output rows over the input rows; invalid commands."""
 import numpy as np
@@ -25,7 +25,7 @@ def up16(n: int) -> int:
 
 @pytest.mark.parametrize("fmt", [2, 3, 8])
 @pytest.mark.parametrize("rows,cols,ntok", [(1000, 2560, 1), (1000, 2560, 5), (4096, 4096, 16), (333, 4096, 17),
-                                            (512, 12288, 32)])
+                                            (512, 12288, 32), (8200, 4096, 20)])
 def test_gemm_rows_equal_single_token_gemv(gq, orc, ctx, fmt, rows, cols, ntok):
     xs, ys = cols + 16, up16(rows) + 32  # strided token rows
     w = gq.matrix(fmt, rows, cols, 3, 10 + fmt, std=0.02)
