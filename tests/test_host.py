@@ -78,6 +78,11 @@ def test_command_words(gq):
     assert all(len(c) == 8 for c in (gq.add(16, 0, 16, 32), gq.fill(16, 0, 1.0), gq.next_token(0, 16, 32, 48, 5, 64)))
     m = gq.gemm(2, 64, 1024, (7 << 32) | 5, 16, 32, 4, 1024, 64, gq.GEMV_ADD, 48, 64, 80, 1e-6, gq.NORM_DEFER)
     assert m == [17, 2 | 0x400, 64, 1024, 5, 7, 16, 32, 4, 1024, 64, 48, 64, 80, eps, 4]
+    # token counts: ATTN flags bits 23:16 (with the gate bit 0), GET_ROWS format word bits 23:16; one token is 0
+    at = gq.attn(16, 4, 0, 1, 2, 256, 64, 3, 4, 5, 0.0625, 1e-6, 6, 7, 8, gate=256, n_tok=32)
+    assert at[7] == 1 | (32 << 16) and at[:7] == a[:7] and at[8:] == a[8:]
+    assert gq.get_rows(14, 151936, 4096, (1 << 32) | 2, 16, 32, n_tok=7) == [13, 14 | (7 << 16), 151936, 4096, 2, 1, 16, 32]
+    assert gq.get_rows(14, 151936, 4096, 2, 16, 32)[1] == 14
 
 
 # ---- synthetic data ---------------------------------------------------------------------------------------------
