@@ -453,18 +453,15 @@ __device__ __forceinline__ double block_term(int sumi, uint32_t dw, const XB & x
 
 template <int TYPE>
 __device__ __forceinline__ void load_wk(const WeightView & w, size_t sbi, int part, WK & o) {
-    if (TYPE == T_Q6_K) {
+    if (TYPE == T_Q6_K) {  // the unit's ql bytes, its own 16 high-bit bytes and 4 scale bytes (the repacked layout)
         const int n = part >> 1, p = part & 1;
         const uint8_t * ql = w.a + sbi * 128 + 64 * n + 32 * p;
-        const uint8_t * qh = w.b + sbi * 64 + 32 * n;
         o.a0 = ld16(ql);
         o.a1 = ld16(ql + 16);
-        o.h0 = ld16(qh);
-        o.h1 = ld16(qh + 16);
-        const uint8_t * sc = w.c + sbi * 16;
-        o.s0 = ld2(sc + 8 * n + 2 * p);
-        o.s1 = ld2(sc + 8 * n + 4 + 2 * p);
-        o.s2 = 0;
+        o.h0 = ld16(w.b + sbi * 64 + 16 * part);
+        o.h1 = o.h0;
+        o.s0 = ld4(w.c + sbi * 16 + 4 * part);
+        o.s1 = o.s2 = 0;
         o.d = ld2(w.d + sbi * 2);
     } else {
         const uint8_t * qs = w.a + sbi * 128 + 32 * part;
@@ -504,13 +501,15 @@ __device__ __forceinline__ void scale_min_k4(const WK & w, int j, int & sc, int 
 template <int TYPE>
 __device__ __forceinline__ void dot_unit(const WK & w, const XK & x, int part, int & S, int & M) {
     if (TYPE == T_Q6_K) {
-        const int p = part & 1;
         int dA0 = 0, dA1 = 0, dB0 = 0, dB1 = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint32_t ql = pick(i < 4 ? w.a0 : w.a1, i & 3), qh = pick(i < 4 ? w.h0 : w.h1, i & 3);
-            const uint32_t qa = (ql & 0x0F0F0F0Fu) | (((qh >> (2 * p)) & 0x03030303u) << 4);
-            const uint32_t qb = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * p + 4)) & 0x03030303u) << 4);
+            // quants 4i .. 4i + 3 of the unit's groups: low nibbles from ql word i, high bits from word i & 3 of its
+            // high-bit bytes (group A at bit 2 (i >> 2) of each byte, group B 4 bits above)
+            const uint32_t ql = pick(i < 4 ? w.a0 : w.a1, i & 3), qh = pick(w.h0, i & 3);
+            const int sh = 2 * (i >> 2);
+            const uint32_t qa = (ql & 0x0F0F0F0Fu) | (((qh >> sh) & 0x03030303u) << 4);
+            const uint32_t qb = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (sh + 4)) & 0x03030303u) << 4);
             if (i < 4) {
                 dA0 = sdot4(qa, x.q[i], dA0);
                 dB0 = sdot4(qb, x.q[8 + i], dB0);
@@ -520,7 +519,7 @@ __device__ __forceinline__ void dot_unit(const WK & w, const XK & x, int part, i
             }
         }
         const int scA0 = int(int8_t(w.s0 & 0xff)), scA1 = int(int8_t((w.s0 >> 8) & 0xff));
-        const int scB0 = int(int8_t(w.s1 & 0xff)), scB1 = int(int8_t((w.s1 >> 8) & 0xff));
+        const int scB0 = int(int8_t((w.s0 >> 16) & 0xff)), scB1 = int(int8_t(w.s0 >> 24));
         S = scA0 * (dA0 - 32 * x.bs[0]) + scA1 * (dA1 - 32 * x.bs[1]) + scB0 * (dB0 - 32 * x.bs[2]) +
             scB1 * (dB1 - 32 * x.bs[3]);
         M = 0;

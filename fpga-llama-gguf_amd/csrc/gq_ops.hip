@@ -533,11 +533,14 @@ __global__ void get_rows_kernel(GetRowsArgs a) {
             const int nsb = a.cols / 256, sb = i / 256, e = i % 256;
             const size_t sbi = size_t(id) * nsb + sb;
             const int n = e / 128, r = e % 128, quarter = r / 32, l = r % 32;
+            // unit j = 2n + (quarter & 1) holds quarter & 1 (group A) and quarter | 2 (group B); its high bits and
+            // scale bytes are contiguous in the repacked layout
+            const int j = 2 * n + (quarter & 1), grp = quarter >> 1;
             const uint8_t ql = a.w.a[sbi * 128 + 64 * n + l + 32 * (quarter & 1)];
-            const uint8_t qh = a.w.b[sbi * 64 + 32 * n + l];
+            const uint8_t qh = a.w.b[sbi * 64 + 16 * j + 4 * ((l >> 2) & 3) + (l & 3)];
             const int lo = quarter < 2 ? (ql & 0xF) : (ql >> 4);
-            const int q = (lo | (((qh >> (2 * quarter)) & 3) << 4)) - 32;
-            const int8_t scv = int8_t(a.w.c[sbi * 16 + e / 16]);
+            const int q = (lo | (((qh >> (2 * (l >> 4) + 4 * grp)) & 3) << 4)) - 32;
+            const int8_t scv = int8_t(a.w.c[sbi * 16 + 4 * j + 2 * grp + l / 16]);
             const float d = h2f(*reinterpret_cast<const uint16_t *>(a.w.d + sbi * 2));
             y = (d * float(scv)) * float(q);
         } else if (a.type == T_Q4_0) {

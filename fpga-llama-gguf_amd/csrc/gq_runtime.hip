@@ -147,20 +147,43 @@ void repack_rows(int type, int rows, int cols, const uint8_t * src, uint8_t * ds
             }
         }
     } else if (type == T_Q6_K) {
+        // ql and d as they are. The high bits and scales are regrouped per 64-weight unit j = 2n + p (the quants
+        // 32p + l of half n, group A, and 64 + 32p + l, group B, l < 32), so a unit reads one contiguous piece of
+        // each: its 16 high-bit bytes, where byte b of word k holds, from bit 0, the 2-bit fields of A at l = 4k + b
+        // and 4k + 16 + b, then of B at the same l (GGUF bits 2p and 2p + 4 of qh[32n + l]); and its 4 scale bytes
+        // sc[8n + 2p], sc[8n + 2p + 1], sc[8n + 4 + 2p], sc[8n + 5 + 2p]. Every bit keeps its value.
         const size_t ns = size_t(cols / 256);
         uint8_t * ql = dst, * qh = dst + R * ns * 128, * sc = dst + R * ns * 192, * dd = dst + R * ns * 208;
         for (size_t i = 0; i < R * ns; ++i) {
             uint8_t * blk = const_cast<uint8_t *>(src) + i * 210;
+            uint8_t * h = qh + 64 * i, * s = sc + 16 * i;
             if (!inverse) {
                 std::memcpy(ql + 128 * i, blk, 128);
-                std::memcpy(qh + 64 * i, blk + 128, 64);
-                std::memcpy(sc + 16 * i, blk + 192, 16);
                 std::memcpy(dd + 2 * i, blk + 208, 2);
+                std::memset(h, 0, 64);
+                for (int j = 0; j < 4; ++j) {
+                    const int n = j >> 1, p = j & 1;
+                    for (int l = 0; l < 32; ++l) {
+                        const uint8_t v = blk[128 + 32 * n + l];
+                        const int a2 = (v >> (2 * p)) & 3, b2 = (v >> (2 * p + 4)) & 3, k = (l >> 2) & 3, up = 2 * (l >> 4);
+                        h[16 * j + 4 * k + (l & 3)] |= uint8_t((a2 << up) | (b2 << (4 + up)));
+                    }
+                    for (int q = 0; q < 4; ++q) s[4 * j + q] = blk[192 + 8 * n + 2 * p + (q & 1) + 4 * (q >> 1)];
+                }
             } else {
                 std::memcpy(blk, ql + 128 * i, 128);
-                std::memcpy(blk + 128, qh + 64 * i, 64);
-                std::memcpy(blk + 192, sc + 16 * i, 16);
                 std::memcpy(blk + 208, dd + 2 * i, 2);
+                std::memset(blk + 128, 0, 64);
+                for (int j = 0; j < 4; ++j) {
+                    const int n = j >> 1, p = j & 1;
+                    for (int l = 0; l < 32; ++l) {
+                        const int k = (l >> 2) & 3, up = 2 * (l >> 4);
+                        const uint8_t v = h[16 * j + 4 * k + (l & 3)];
+                        const int a2 = (v >> up) & 3, b2 = (v >> (4 + up)) & 3;
+                        blk[128 + 32 * n + l] |= uint8_t((a2 << (2 * p)) | (b2 << (2 * p + 4)));
+                    }
+                    for (int q = 0; q < 4; ++q) blk[192 + 8 * n + 2 * p + (q & 1) + 4 * (q >> 1)] = s[4 * j + q];
+                }
             }
         }
     }

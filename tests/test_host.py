@@ -54,7 +54,12 @@ def test_repack_round_trip(gq, libs, t):
     gguf = rng.integers(0, 256, rows * gq.row_bytes(t, cols), dtype=np.uint8)
     packed = gq.repack(t, rows, cols, gguf)
     assert packed.size == gguf.size and not np.array_equal(packed, gguf)
-    assert np.array_equal(np.sort(packed), np.sort(gguf))  # the same bytes, reordered
+    if t == B.Q6_K:  # high bits regrouped per 64-weight unit: the same bits, moved within and between bytes
+        assert np.unpackbits(packed).sum() == np.unpackbits(gguf).sum()
+        ns = cols // 256
+        assert np.array_equal(packed[:rows * ns * 128], gguf.reshape(-1, 210)[:, :128].ravel())  # ql as it is
+    else:
+        assert np.array_equal(np.sort(packed), np.sort(gguf))  # the same bytes, reordered
     assert np.array_equal(gq.unpack(t, rows, cols, packed), gguf)
 
 
