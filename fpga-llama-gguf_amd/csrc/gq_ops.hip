@@ -330,97 +330,17 @@ __global__ __launch_bounds__(ATT_T) void attn_append_kernel(AttnArgs a) {
     }
 }
 
-// BATCH: token t = blockIdx.y of a multi-token launch, after attn_append_kernel: the rounded query comes from qr and
-// every key and value (its own position's too) from the cache, which hold the bits the single-token kernel uses.
-template <int HD, bool BATCH>
-__global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
-    constexpr int PER = HD / 8;                    // 16-byte pieces per row
-    constexpr int RPP = ATT_T / PER;               // rows per pass
-    constexpr int NP = (ATTN_CHUNK + RPP - 1) / RPP;  // passes
-    __shared__ __align__(16) uint16_t vs[ATTN_CHUNK * HD];
-    __shared__ __align__(16) float qs[2][HD];  // q and the new key: normalized, then rotated + rounded
-    __shared__ float pr[ATTN_CHUNK];           // scores, then e^(s - max)
-    __shared__ float red[2][4];
-    __shared__ float mx, fcs[MAXCH], lcs[MAXCH];
-    __shared__ int last;
-    // workgroup b: unit u = (KV head, chunk) with u % 8 == b % 8 (one XCD), q head g of the unit's KV head
-    const int G = a.n_head / a.n_head_kv, b = blockIdx.x;
-    const int u = (b / (8 * G)) * 8 + (b & 7), g = (b >> 3) % G;
-    const int kvh = u % a.n_head_kv, chunk = u / a.n_head_kv, hq = kvh * G + g;
-    const int t = BATCH ? int(blockIdx.y) : 0, th = t * a.n_head + hq;  // th: the (token, q head) partials set
-    const int pos = *a.pos + t, nc = (pos + ATTN_CHUNK) / ATTN_CHUNK;
-    if (pos < 0 || pos >= a.n_ctx || chunk >= nc) return;  // positions past the KV capacity are not stored
-    const int tid = threadIdx.x, half = a.n_rot / 2;
-    const int lane = tid & 63, wave = tid >> 6, pc = tid % PER;
-    const int t0 = chunk * ATTN_CHUNK, nt = min(ATTN_CHUNK, pos + 1 - t0);
-    const bool has_new = !BATCH && chunk == nc - 1;  // this chunk holds pos (a batch reads it from the cache)
-    const float * qrow = a.q + size_t(t) * a.n_head * a.q_stride + size_t(hq) * a.q_stride;
-    // ---- 1. loads ----
-    uint4 kr[NP], vr[NP];  // rows past the chunk re-read its last row (stored memory); they are not used
-#pragma unroll
-    for (int j = 0; j < NP; ++j) {
-        const int ti = min(tid / PER + j * RPP, nt - 1);
-        const size_t off = (size_t(t0 + ti) * a.n_head_kv + kvh) * HD + pc * 8;
-        kr[j] = *reinterpret_cast<const uint4 *>(a.kc + off);
-        vr[j] = *reinterpret_cast<const uint4 *>(a.vc + off);
-    }
+// Steps 3-5 of one token on a loaded chunk (rows t0 .. t0 + nt - 1): kr holds the chunk's key pieces, vs its values,
+// qs[0] the rounded q and, with NEW, qs[1] the new key of row pos; the partials go to set th, and the workgroup that
+// completes the set's nc chunks combines them into the output row (and clears the set's counter).
+template <int HD, bool NEW>
+__device__ __forceinline__ void attn_token(const AttnArgs & a, const uint4 (&kr)[(ATTN_CHUNK + ATT_T / (HD / 8) - 1) / (ATT_T / (HD / 8))],
+                                           const uint16_t * vs, const float (*qs)[HD], float * pr, float & mx, float * fcs,
+                                           float * lcs, int & last, int pos, int t0, int chunk, int th, int nt, int nc, float gt) {
+    constexpr int PER = HD / 8, RPP = ATT_T / PER, NP = (ATTN_CHUNK + RPP - 1) / RPP;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, pc = tid % PER;
     const bool el = tid < HD;
-    const int e = el ? tid : 0;  // element of the head this thread holds
-    float xv[2];
-    xv[0] = (!BATCH && el) ? qrow[e] : 0.0f;
-    xv[1] = (has_new && el) ? a.k[size_t(kvh) * HD + e] : 0.0f;
-    const float wq = BATCH ? 0.0f : a.qn[e], wk = BATCH ? 0.0f : a.kn[e];
-    const float vv = has_new ? a.v[size_t(kvh) * HD + e] : 0.0f;
-    const float gt = a.gate ? a.gate[size_t(t) * a.n_head * a.q_stride + size_t(hq) * 2 * HD + e] : 0.0f;
-    const int pi = e < half ? e : e - half;  // the RoPE pair of this element
-    const bool rot = !BATCH && e < a.n_rot;
-    const float cs0 = rot ? a.cs[size_t(pos) * a.n_rot + 2 * pi] : 0.0f;
-    const float cs1 = rot ? a.cs[size_t(pos) * a.n_rot + 2 * pi + 1] : 0.0f;
-#pragma unroll
-    for (int j = 0; j < NP; ++j) {  // values to LDS (the row of pos is overwritten with the new value below)
-        const int ti = tid / PER + j * RPP;
-        if (ti < nt) *reinterpret_cast<uint4 *>(vs + ti * HD + pc * 8) = vr[j];
-    }
-    // ---- 2. norms (pairwise over head_dim), RoPE, fp16 rounding ----
-    if constexpr (BATCH) {
-        if (el) qs[0][e] = a.qr[size_t(th) * HD + e];
-    } else {
-        float sq[2] = {xv[0] * xv[0], xv[1] * xv[1]};
-        pair_sum_lanes_n<64, 2>(sq);
-        if (lane == 0) {
-            red[0][wave] = sq[0];
-            red[1][wave] = sq[1];
-        }
-        __syncthreads();
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const float sum = (red[h][0] + red[h][1]) + (red[h][2] + red[h][3]);
-            const float sc = 1.0f / sqrtf(sum / float(HD) + a.eps);
-            if (el) qs[h][e] = (xv[h] * sc) * (h == 0 ? wq : wk);
-        }
-        __syncthreads();
-        float rv[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const float x0 = qs[h][pi], x1 = qs[h][pi + half];
-            rv[h] = e < half ? x0 * cs0 - x1 * cs1 : (rot ? x0 * cs1 + x1 * cs0 : qs[h][e]);
-        }
-        __syncthreads();
-        if (el) {
-            qs[0][e] = h2f(f2h(rv[0]));
-            qs[1][e] = h2f(f2h(rv[1]));
-            if (has_new) {
-                const uint32_t kb = f2h(rv[1]), vb = f2h(vv);
-                vs[(pos - t0) * HD + e] = uint16_t(vb);
-                if (g == 0) {  // one q head per KV head stores the new key and value
-                    const size_t off = (size_t(pos) * a.n_head_kv + kvh) * HD + e;
-                    a.kc[off] = uint16_t(kb);
-                    a.vc[off] = uint16_t(vb);
-                }
-            }
-        }
-    }
-    __syncthreads();
+    const int e = el ? tid : 0;
     // ---- 3. scores ----
     float qv[8], kn[8];
 #pragma unroll
@@ -431,7 +351,7 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
     float dots[NP];
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
-        const bool is_new = !BATCH && t0 + tid / PER + j * RPP == pos;
+        const bool is_new = NEW && t0 + tid / PER + j * RPP == pos;
         const uint32_t kw[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
         float t[8];
 #pragma unroll
@@ -520,6 +440,96 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
         a.y[size_t(th) * HD + e] = out;
     }
     if (tid == 0) a.counter[th] = 0u;
+}
+
+template <int HD>
+__global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
+    constexpr int PER = HD / 8;                    // 16-byte pieces per row
+    constexpr int RPP = ATT_T / PER;               // rows per pass
+    constexpr int NP = (ATTN_CHUNK + RPP - 1) / RPP;  // passes
+    __shared__ __align__(16) uint16_t vs[ATTN_CHUNK * HD];
+    __shared__ __align__(16) float qs[2][HD];  // q and the new key: normalized, then rotated + rounded
+    __shared__ float pr[ATTN_CHUNK];           // scores, then e^(s - max)
+    __shared__ float red[2][4];
+    __shared__ float mx, fcs[MAXCH], lcs[MAXCH];
+    __shared__ int last;
+    // workgroup b: unit u = (KV head, chunk) with u % 8 == b % 8 (one XCD), q head g of the unit's KV head
+    const int G = a.n_head / a.n_head_kv, b = blockIdx.x;
+    const int u = (b / (8 * G)) * 8 + (b & 7), g = (b >> 3) % G;
+    const int kvh = u % a.n_head_kv, chunk = u / a.n_head_kv, hq = kvh * G + g;
+    const int th = hq;  // the q head's partials set
+    const int pos = *a.pos, nc = (pos + ATTN_CHUNK) / ATTN_CHUNK;
+    if (pos < 0 || pos >= a.n_ctx || chunk >= nc) return;  // positions past the KV capacity are not stored
+    const int tid = threadIdx.x, half = a.n_rot / 2;
+    const int lane = tid & 63, wave = tid >> 6, pc = tid % PER;
+    const int t0 = chunk * ATTN_CHUNK, nt = min(ATTN_CHUNK, pos + 1 - t0);
+    const bool has_new = chunk == nc - 1;  // this chunk holds pos
+    const float * qrow = a.q + size_t(hq) * a.q_stride;
+    // ---- 1. loads ----
+    uint4 kr[NP], vr[NP];  // rows past the chunk re-read its last row (stored memory); they are not used
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+        const int ti = min(tid / PER + j * RPP, nt - 1);
+        const size_t off = (size_t(t0 + ti) * a.n_head_kv + kvh) * HD + pc * 8;
+        kr[j] = *reinterpret_cast<const uint4 *>(a.kc + off);
+        vr[j] = *reinterpret_cast<const uint4 *>(a.vc + off);
+    }
+    const bool el = tid < HD;
+    const int e = el ? tid : 0;  // element of the head this thread holds
+    float xv[2];
+    xv[0] = el ? qrow[e] : 0.0f;
+    xv[1] = (has_new && el) ? a.k[size_t(kvh) * HD + e] : 0.0f;
+    const float wq = a.qn[e], wk = a.kn[e];
+    const float vv = has_new ? a.v[size_t(kvh) * HD + e] : 0.0f;
+    const float gt = a.gate ? a.gate[size_t(hq) * 2 * HD + e] : 0.0f;
+    const int pi = e < half ? e : e - half;  // the RoPE pair of this element
+    const bool rot = e < a.n_rot;
+    const float cs0 = rot ? a.cs[size_t(pos) * a.n_rot + 2 * pi] : 0.0f;
+    const float cs1 = rot ? a.cs[size_t(pos) * a.n_rot + 2 * pi + 1] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {  // values to LDS (the row of pos is overwritten with the new value below)
+        const int ti = tid / PER + j * RPP;
+        if (ti < nt) *reinterpret_cast<uint4 *>(vs + ti * HD + pc * 8) = vr[j];
+    }
+    // ---- 2. norms (pairwise over head_dim), RoPE, fp16 rounding ----
+    {
+        float sq[2] = {xv[0] * xv[0], xv[1] * xv[1]};
+        pair_sum_lanes_n<64, 2>(sq);
+        if (lane == 0) {
+            red[0][wave] = sq[0];
+            red[1][wave] = sq[1];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float sum = (red[h][0] + red[h][1]) + (red[h][2] + red[h][3]);
+            const float sc = 1.0f / sqrtf(sum / float(HD) + a.eps);
+            if (el) qs[h][e] = (xv[h] * sc) * (h == 0 ? wq : wk);
+        }
+        __syncthreads();
+        float rv[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float x0 = qs[h][pi], x1 = qs[h][pi + half];
+            rv[h] = e < half ? x0 * cs0 - x1 * cs1 : (rot ? x0 * cs1 + x1 * cs0 : qs[h][e]);
+        }
+        __syncthreads();
+        if (el) {
+            qs[0][e] = h2f(f2h(rv[0]));
+            qs[1][e] = h2f(f2h(rv[1]));
+            if (has_new) {
+                const uint32_t kb = f2h(rv[1]), vb = f2h(vv);
+                vs[(pos - t0) * HD + e] = uint16_t(vb);
+                if (g == 0) {  // one q head per KV head stores the new key and value
+                    const size_t off = (size_t(pos) * a.n_head_kv + kvh) * HD + e;
+                    a.kc[off] = uint16_t(kb);
+                    a.vc[off] = uint16_t(vb);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    attn_token<HD, true>(a, kr, vs, qs, pr, mx, fcs, lcs, last, pos, t0, chunk, th, nt, nc, gt);
 }
 
 // ---- embedding rows (ggml dequantize_row_*) ----
@@ -626,16 +636,66 @@ hipError_t launch_gated_norm(const GatedNormArgs & a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ---- attention of a block of tokens (after attn_append_kernel) ----
+// Workgroup (unit, q head, group of ATTN_TG tokens): the chunk's keys (registers) and values (LDS) are loaded once,
+// for the group's last stored position, and serve the group's tokens in turn; each token runs attn_token on the rows
+// up to its own position, with its rounded query from qr, so its partials, combine and output are those of a one-token
+// launch. Tokens whose position is outside the KV capacity are skipped.
+constexpr int ATTN_TG = 2;
+
+template <int HD>
+__global__ __launch_bounds__(ATT_T) void attn_group_kernel(AttnArgs a) {
+    constexpr int PER = HD / 8, RPP = ATT_T / PER, NP = (ATTN_CHUNK + RPP - 1) / RPP;
+    __shared__ __align__(16) uint16_t vs[ATTN_CHUNK * HD];
+    __shared__ __align__(16) float qs[2][HD];  // the token's rounded q (qs[1] unused)
+    __shared__ float pr[ATTN_CHUNK];
+    __shared__ float mx, fcs[MAXCH], lcs[MAXCH];
+    __shared__ int last;
+    const int G = a.n_head / a.n_head_kv, b = blockIdx.x;
+    const int u = (b / (8 * G)) * 8 + (b & 7), g = (b >> 3) % G;
+    const int kvh = u % a.n_head_kv, chunk = u / a.n_head_kv, hq = kvh * G + g;
+    const int pos0 = *a.pos, tk0 = int(blockIdx.y) * ATTN_TG, tk1 = min(tk0 + ATTN_TG, a.n_tok);
+    const int first = max(pos0 + tk0, 0), plast = min(pos0 + tk1 - 1, a.n_ctx - 1);  // the group's stored positions
+    if (first > plast || chunk >= (plast + ATTN_CHUNK) / ATTN_CHUNK) return;
+    const int tid = threadIdx.x, pc = tid % PER;
+    const int t0 = chunk * ATTN_CHUNK, ntmax = min(ATTN_CHUNK, plast + 1 - t0);
+    uint4 kr[NP], vr[NP];  // rows past ntmax re-read row ntmax - 1; they are not used
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+        const int ti = min(tid / PER + j * RPP, ntmax - 1);
+        const size_t off = (size_t(t0 + ti) * a.n_head_kv + kvh) * HD + pc * 8;
+        kr[j] = *reinterpret_cast<const uint4 *>(a.kc + off);
+        vr[j] = *reinterpret_cast<const uint4 *>(a.vc + off);
+    }
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+        const int ti = tid / PER + j * RPP;
+        if (ti < ntmax) *reinterpret_cast<uint4 *>(vs + ti * HD + pc * 8) = vr[j];
+    }
+    const bool el = tid < HD;
+    const int e = el ? tid : 0;
+    for (int t = tk0; t < tk1; ++t) {  // uniform over the workgroup
+        const int pos = pos0 + t, nc = (pos + ATTN_CHUNK) / ATTN_CHUNK;
+        if (pos < 0 || pos >= a.n_ctx || chunk >= nc) continue;
+        const int th = t * a.n_head + hq, nt = min(ATTN_CHUNK, pos + 1 - t0);
+        if (el) qs[0][e] = a.qr[size_t(th) * HD + e];
+        const float gt = a.gate ? a.gate[size_t(t) * a.n_head * a.q_stride + size_t(hq) * 2 * HD + e] : 0.0f;
+        __syncthreads();  // qs (and, the first time, vs) written
+        attn_token<HD, false>(a, kr, vs, qs, pr, mx, fcs, lcs, last, pos, t0, chunk, th, nt, nc, gt);
+        __syncthreads();  // the next token overwrites qs, pr and the combine's shared values
+    }
+}
+
 // One token: the attention kernel alone. Several: their new keys, values and queries first (one launch), then the
 // attention of every (token, q head, chunk).
 template <int HD>
 hipError_t launch_attn_hd(const AttnArgs & a, dim3 grid, hipStream_t s) {
     if (grid.y == 1) {
-        GQ_LAUNCH((attn_kernel<HD, false>), grid, dim3(ATT_T), 0, s, a);
+        GQ_LAUNCH(attn_kernel<HD>, grid, dim3(ATT_T), 0, s, a);
         return hipGetLastError();
     }
     GQ_LAUNCH(attn_append_kernel<HD>, dim3(a.n_head + a.n_head_kv, grid.y), dim3(ATT_T), 0, s, a);
-    GQ_LAUNCH((attn_kernel<HD, true>), grid, dim3(ATT_T), 0, s, a);
+    GQ_LAUNCH(attn_group_kernel<HD>, dim3(grid.x, (grid.y + ATTN_TG - 1) / ATTN_TG), dim3(ATT_T), 0, s, a);
     return hipGetLastError();
 }
 
