@@ -102,19 +102,25 @@ __device__ __forceinline__ void load_wround(const GemmArgs & a, int nb, int row,
     }
 }
 
+template <int TYPE>
+__device__ __forceinline__ uint32_t scale_word(uint32_t sw) {
+    return TYPE == T_Q4_1 ? sw : __float_as_uint(h2f(sw & 0xffffu));
+}
+
 // Thread t's part of a round into an LDS buffer: its 16 quant bytes of every matrix-half at row t / 16, block t % 16
-// (rows padded to ROW_LDS bytes), and its scale.
+// (rows padded to ROW_LDS bytes), and its scale word: Q4_0 / Q8_0 the fp16 scale as FP32 bits (converted once here,
+// not once per token lane), Q4_1 the fp16 pair (d, m) as loaded.
 template <int TYPE, bool PAIR>
 __device__ __forceinline__ void stage(const WRound<TYPE, PAIR> & w, uint8_t * lq, uint32_t * ld) {
     constexpr int QH = TYPE == T_Q8_0 ? 2 : 1, QBUF = GT * ROW_LDS;
     const int t = threadIdx.x, o = (t >> 4) * ROW_LDS + (t & 15) * 16, od = (t >> 4) * GU + (t & 15);
     *reinterpret_cast<v4u *>(lq + o) = w.g0;
     if constexpr (QH == 2) *reinterpret_cast<v4u *>(lq + QBUF + o) = w.g1;
-    ld[od] = w.gd;
+    ld[od] = scale_word<TYPE>(w.gd);
     if constexpr (PAIR) {
         *reinterpret_cast<v4u *>(lq + QH * QBUF + o) = w.u0;
         if constexpr (QH == 2) *reinterpret_cast<v4u *>(lq + 3 * QBUF + o) = w.u1;
-        ld[GT * GU + od] = w.ud;
+        ld[GT * GU + od] = scale_word<TYPE>(w.ud);
     }
 }
 
@@ -205,7 +211,7 @@ __device__ __forceinline__ void round_terms(const uint8_t * lq, const uint32_t *
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const uint32_t sw = dw[m][i][j];
-                    const float sc = h2f(sw & 0xffffu) * dx;
+                    const float sc = (TYPE == T_Q4_1 ? h2f(sw & 0xffffu) : __uint_as_float(sw)) * dx;
                     double term = floor(double(sm[i]) * double(sc));
                     if constexpr (TYPE == T_Q4_1)  // + floor(m * s_x * 2^40), the product of two fp16 values exact
                         term += floor(double(h2f(sw >> 16) * lane_of(x.s[t], j)));
