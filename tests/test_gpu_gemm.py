@@ -45,6 +45,32 @@ def test_gemm_rows_equal_single_token_gemv(gq, orc, ctx, fmt, rows, cols, ntok):
         assert_bits(ctx.read(Y1, rows), y[t], f"GEMV command, token {t}")
 
 
+@pytest.mark.parametrize("fmt", [2, 3, 8])
+@pytest.mark.parametrize("xscale", [3e-3, 1e-5])
+def test_tiny_scales_floor_every_term(gq, orc, ctx, fmt, xscale):
+    """Small activations: d_w * d_x * 2^40 falls below 2^21, so the scaled block products have fractional parts and
+    the floor of every term decides low bits of the sum (at 1e-5 the fp16 activation scales are subnormal). Every
+    token row of the GEMM and the GEMV command equal the oracle bit for bit."""
+    rows, cols, ntok = 300, 4096, 17
+    w = gq.matrix(fmt, rows, cols, 7, 50 + fmt, std=0.02)
+    off = ctx.upload(fmt, rows, cols, w)
+    x = gq.normal(7, 51, ntok * cols) * np.float32(xscale)
+    amax = np.abs(x.reshape(-1, 32)).max(axis=1)
+    assert np.median(amax / 127.0) * 0.01 < 2.0 ** -19  # typical d_x * d_w below 2^-19
+    X, Y, Y1 = 0, ntok * cols, ntok * cols + ntok * 512
+    ctx.write(X, x)
+    print(f"[gemm] tiny scales fmt {fmt} x scale {xscale}", flush=True)
+    assert ctx.run(gq.gemm(fmt, rows, cols, off, X, Y, ntok, cols, 512)) == 0, ctx.error()
+    y = ctx.read(Y, ntok * 512).reshape(ntok, 512)[:, :rows]
+    for t in range(ntok):
+        want = orc.fx_gemv(fmt, w, x[t * cols:(t + 1) * cols], rows, cols)
+        assert np.count_nonzero(want) > rows // 2
+        assert_bits(y[t], want, f"GEMM token {t}")
+        if t in (0, ntok - 1):
+            assert ctx.run(gq.gemv(fmt, rows, cols, off, X + t * cols, Y1)) == 0, ctx.error()
+            assert_bits(ctx.read(Y1, rows), want, f"GEMV, token {t}")
+
+
 @pytest.mark.parametrize("fmt,outlier", [(2, 3e5), (8, 3e5), (3, 2e4)])
 def test_huge_activations_exact(gq, orc, ctx, fmt, outlier):
     """Activations with outliers (block scales up to 2362): block terms reach 2^54 LSB, beyond the 2^53 LSB inside
