@@ -279,12 +279,12 @@ __global__ __launch_bounds__(64) void gated_norm_kernel(GatedNormArgs a) {
 //      of a row across lanes (together the pairwise sum over head_dim), times scale;
 //   4. the chunk max, e^(s - max), then thread d sums p and p * v[d] over the positions in order and writes the
 //      partials (max, sum, o[hd]);
-//   5. the last workgroup of the q head loads all chunks' partials (16 chunks per round), forms M = max m_c,
+//   5. the last workgroup of the q head loads all chunks' partials (32 chunks per round), forms M = max m_c,
 //      f_c = e^(m_c - M), L = sum l_c f_c and O = sum o_c f_c in chunk order, and writes O / L times the sigmoid
 //      of the gate.
 constexpr int ATT_T = 256;
 constexpr int MAXCH = 64;  // chunks (n_ctx <= 4096)
-constexpr int CMB = 16;    // chunks per load round of the combine
+constexpr int CMB = 32;    // chunks per load round of the combine (each round is a dependent load)
 
 // ---- new keys, values and queries of n_tok tokens (step 2 below, one vector per workgroup) ----
 // Workgroup (slot s, token t): s < n_head normalizes and rotates q head s and writes it, fp16-rounded, to qr; the

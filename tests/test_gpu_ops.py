@@ -175,7 +175,8 @@ def test_gdn_gated_norm_folded_into_gemv(gq, orc, ctx, hv, hk, wtype, z_silu):
 
 @pytest.mark.parametrize("nh,nkv,hd,nrot,n_ctx,npos,checks", [
     (16, 4, 256, 64, 200, 130, (0, 1, 63, 64, 65, 127, 128, 129)),  # Qwen3.5 shape, crosses two chunk boundaries
-    (6, 2, 128, 128, 1100, 1041, (1023, 1024, 1040)),  # 17 chunks: two load rounds in the combine
+    (6, 2, 128, 128, 1100, 1041, (1023, 1024, 1040)),  # 17 chunks
+    (6, 2, 128, 128, 2200, 2113, (2047, 2048, 2112)),  # 34 chunks: two load rounds in the combine
     (4, 4, 64, 16, 80, 70, (5, 69)),  # one q head per KV head
 ])
 def test_attention(gq, orc, ctx, nh, nkv, hd, nrot, n_ctx, npos, checks):
@@ -218,7 +219,8 @@ def test_attention(gq, orc, ctx, nh, nkv, hd, nrot, n_ctx, npos, checks):
     (16, 4, 256, 64, 200, 50, 32),  # Qwen3.5 shape, the batch crosses a chunk boundary
     (16, 4, 256, 64, 200, 0, 5),    # from an empty cache
     (16, 4, 256, 64, 200, 190, 16),  # the last six positions are past the capacity (not stored, no output)
-    (6, 2, 128, 128, 1100, 1020, 7),  # 17 chunks: two load rounds in the combine
+    (6, 2, 128, 128, 1100, 1020, 7),  # 17 chunks
+    (6, 2, 128, 128, 2200, 2100, 7),  # 34 chunks: two load rounds in the combine
 ])
 def test_attention_tokens(gq, orc, ctx, nh, nkv, hd, nrot, n_ctx, p0, ntok):
     """One ATTN command over n_tok tokens (positions act[pos] + t, packed rows) against n_tok one-token commands on
