@@ -144,12 +144,14 @@ float orc_pair_sum(const float * a, int n) {
     if (n <= 0) return 0.0f;
     int p = 1;
     while (p < n) p <<= 1;
-    float * t = (float *)calloc((size_t)p, sizeof(float));
+    float stack[1024];
+    float * t = p <= 1024 ? stack : (float *)malloc(sizeof(float) * (size_t)p);
     memcpy(t, a, (size_t)n * sizeof(float));
+    for (int i = n; i < p; ++i) t[i] = 0.0f;
     for (int s = 1; s < p; s *= 2)
         for (int i = 0; i < p; i += 2 * s) t[i] = t[i] + t[i + s];
     const float r = t[0];
-    free(t);
+    if (t != stack) free(t);
     return r;
 }
 
@@ -670,7 +672,15 @@ void orc_rope(const float * x, const float * cs, int n_dims, int ne0, int rows, 
 /* GDN reference: gemvq_ref.h:363-397 (libm exp, sequential dots). */
 void orc_ref_gdn(float * state, const float * q, const float * k, const float * v, const float * g, const float * beta,
                  int hv, int hk, float scale, float * y, double * y_mag, double * s_mag) {
+    orc_ref_gdn_mt(state, q, k, v, g, beta, hv, hk, scale, y, y_mag, s_mag, 1);
+}
+
+/* The value heads are independent, so they split over threads without changing any result. */
+void orc_ref_gdn_mt(float * state, const float * q, const float * k, const float * v, const float * g,
+                    const float * beta, int hv, int hk, float scale, float * y, double * y_mag, double * s_mag,
+                    int n_threads) {
     const int S = 128;
+#pragma omp parallel for schedule(static) num_threads(n_threads > 0 ? n_threads : 1)
     for (int h = 0; h < hv; ++h) {
         const float * qh = q + (h % hk) * S, * kh = k + (h % hk) * S;
         const float decay = expf(g[h]);
@@ -705,6 +715,13 @@ void orc_ref_gdn(float * state, const float * q, const float * k, const float * 
 void orc_gdn(float * state, const float * q, const float * k, const float * v, const float * graw, const float * braw,
              const float * dt, const float * a, const float * z, const float * w, int hv, int hk, float scale,
              float l2_eps, float rms_eps, int flags, float * y) {
+    orc_gdn_mt(state, q, k, v, graw, braw, dt, a, z, w, hv, hk, scale, l2_eps, rms_eps, flags, y, 1);
+}
+
+/* The value heads are independent, so they split over threads without changing any result. */
+void orc_gdn_mt(float * state, const float * q, const float * k, const float * v, const float * graw, const float * braw,
+                const float * dt, const float * a, const float * z, const float * w, int hv, int hk, float scale,
+                float l2_eps, float rms_eps, int flags, float * y, int n_threads) {
     const int S = 128;
     float * qn = (float *)malloc(sizeof(float) * (size_t)hk * S);
     float * kn = (float *)malloc(sizeof(float) * (size_t)hk * S);
@@ -716,8 +733,9 @@ void orc_gdn(float * state, const float * q, const float * k, const float * v, c
             kn[h * S + i] = (flags & 2) ? k[h * S + i] * sk : k[h * S + i];
         }
     }
-    float prod[128], xrow[128];
+#pragma omp parallel for schedule(static) num_threads(n_threads > 0 ? n_threads : 1)
     for (int h = 0; h < hv; ++h) {
+        float prod[128], xrow[128];
         const float * qh = qn + (h % hk) * S, * kh = kn + (h % hk) * S;
         float gv = graw[h], bt = braw[h];
         if (flags & 8) {
@@ -753,13 +771,20 @@ void orc_gdn(float * state, const float * q, const float * k, const float * v, c
 /* Attention core for one token (not on the reference card; ggml semantics with an F16 KV cache). */
 void orc_attn(const float * q, const uint16_t * kc, const uint16_t * vc, int nh, int nkvh, int hd, int n_kv,
               float scale, float * out) {
+    orc_attn_mt(q, kc, vc, nh, nkvh, hd, n_kv, scale, out, 1);
+}
+
+/* The q heads are independent, so they split over threads without changing any result. */
+void orc_attn_mt(const float * q, const uint16_t * kc, const uint16_t * vc, int nh, int nkvh, int hd, int n_kv,
+                 float scale, float * out, int n_threads) {
     const int group = nh / nkvh, CH = 64, nch = (n_kv + CH - 1) / CH;
-    float * q16 = (float *)malloc(sizeof(float) * (size_t)hd);
-    float * prod = (float *)malloc(sizeof(float) * (size_t)hd);
-    float * s = (float *)malloc(sizeof(float) * (size_t)n_kv);
-    float * mc = (float *)malloc(sizeof(float) * (size_t)nch), * lc = (float *)malloc(sizeof(float) * (size_t)nch);
-    float * oc = (float *)malloc(sizeof(float) * (size_t)nch * hd);
+#pragma omp parallel for schedule(static) num_threads(n_threads > 0 ? n_threads : 1)
     for (int h = 0; h < nh; ++h) {
+        float * q16 = (float *)malloc(sizeof(float) * (size_t)hd);
+        float * prod = (float *)malloc(sizeof(float) * (size_t)hd);
+        float * s = (float *)malloc(sizeof(float) * (size_t)n_kv);
+        float * mc = (float *)malloc(sizeof(float) * (size_t)nch), * lc = (float *)malloc(sizeof(float) * (size_t)nch);
+        float * oc = (float *)malloc(sizeof(float) * (size_t)nch * hd);
         const int kh = h / group;
         for (int d = 0; d < hd; ++d) q16[d] = orc_half_to_float(orc_float_to_half(q[h * hd + d]));
         for (int t = 0; t < n_kv; ++t) {
@@ -794,8 +819,54 @@ void orc_attn(const float * q, const uint16_t * kc, const uint16_t * vc, int nh,
             for (int d = 0; d < hd; ++d) oh[d] += oc[(size_t)c * hd + d] * f;
         }
         for (int d = 0; d < hd; ++d) oh[d] = oh[d] / L;
+        free(q16); free(prod); free(s); free(mc); free(lc); free(oc);
     }
-    free(q16); free(prod); free(s); free(mc); free(lc); free(oc);
+}
+
+/* Attention in the shape of ggml's CPU path without flash attention (the reference leaves attention to ggml's CPU
+ * backend, README.md:77): q converted to fp16 (the F16 cache's vec_dot type), each score an F16 dot with the float
+ * products summed in double (ggml_vec_dot_f16's generic form), times scale; softmax with the max subtracted, libm
+ * expf and the sum in double (ggml_vec_soft_max_f32), scaled by 1 / sum; the probabilities converted to fp16 for the
+ * product with V (again an F16 dot summed in double). Upstream ggml is not available here, so this form is
+ * restated from ggml's published generic code and is not pinned against it. */
+void orc_ref_attn(const float * q, const uint16_t * kc, const uint16_t * vc, int nh, int nkvh, int hd, int n_kv,
+                  float scale, float * out) {
+    orc_ref_attn_mt(q, kc, vc, nh, nkvh, hd, n_kv, scale, out, 1);
+}
+
+void orc_ref_attn_mt(const float * q, const uint16_t * kc, const uint16_t * vc, int nh, int nkvh, int hd, int n_kv,
+                     float scale, float * out, int n_threads) {
+    const int group = nh / nkvh;
+#pragma omp parallel for schedule(static) num_threads(n_threads > 0 ? n_threads : 1)
+    for (int h = 0; h < nh; ++h) {
+        const int kh = h / group;
+        float * q16 = (float *)malloc(sizeof(float) * (size_t)hd);
+        float * s = (float *)malloc(sizeof(float) * (size_t)n_kv);
+        float * p16 = (float *)malloc(sizeof(float) * (size_t)n_kv);
+        for (int d = 0; d < hd; ++d) q16[d] = orc_half_to_float(orc_float_to_half(q[h * hd + d]));
+        float mx = -INFINITY;
+        for (int t = 0; t < n_kv; ++t) {
+            const uint16_t * kt = kc + ((size_t)t * nkvh + kh) * hd;
+            double acc = 0.0;
+            for (int d = 0; d < hd; ++d) acc += (double)(q16[d] * orc_half_to_float(kt[d]));
+            s[t] = (float)acc * scale;
+            mx = fmaxf(mx, s[t]);
+        }
+        double sum = 0.0;
+        for (int t = 0; t < n_kv; ++t) {
+            const float e = expf(s[t] - mx);
+            sum += (double)e;
+            s[t] = e;
+        }
+        const float inv = (float)(1.0 / sum);
+        for (int t = 0; t < n_kv; ++t) p16[t] = orc_half_to_float(orc_float_to_half(s[t] * inv));
+        for (int d = 0; d < hd; ++d) {
+            double acc = 0.0;
+            for (int t = 0; t < n_kv; ++t) acc += (double)(orc_half_to_float(vc[((size_t)t * nkvh + kh) * hd + d]) * p16[t]);
+            out[h * hd + d] = (float)acc;
+        }
+        free(q16); free(s); free(p16);
+    }
 }
 
 /* ggml dequantize_row_q6_K: y = d * sc * q evaluated as (d * sc) * q. */

@@ -85,6 +85,9 @@ void orc_ref_unary(const float * x, int n, int kind, float * y);
  * the log decay, beta already the gate); y [hv][128]; y_mag / s_mag may be NULL. */
 void orc_ref_gdn(float * state, const float * q, const float * k, const float * v, const float * g, const float * beta,
                  int hv, int hk, float scale, float * y, double * y_mag, double * s_mag);
+void orc_ref_gdn_mt(float * state, const float * q, const float * k, const float * v, const float * g,
+                    const float * beta, int hv, int hk, float scale, float * y, double * y_mag, double * s_mag,
+                    int n_threads);
 /* Canonical fused step (GDN opcode): flags bit1 L2-normalize q/k (l2_eps), bit2 gated output norm
  * (rms_eps, w[128], z[hv*128]), bit3 gates from raw projections (beta = sigmoid(b), g = softplus(a_raw + dt) * a),
  * bit5 z already holds silu(z).
@@ -92,12 +95,23 @@ void orc_ref_gdn(float * state, const float * q, const float * k, const float * 
 void orc_gdn(float * state, const float * q, const float * k, const float * v, const float * graw, const float * braw,
              const float * dt, const float * a, const float * z, const float * w, int hv, int hk, float scale,
              float l2_eps, float rms_eps, int flags, float * y);
+void orc_gdn_mt(float * state, const float * q, const float * k, const float * v, const float * graw, const float * braw,
+                const float * dt, const float * a, const float * z, const float * w, int hv, int hk, float scale,
+                float l2_eps, float rms_eps, int flags, float * y, int n_threads);
 
 /* ---- attention core (one token, GQA, F16 KV cache) ----
  * q [nh][hd] fp32 (rounded to fp16 like ggml's F16 vec_dot type), kc/vc [n_kv][nkvh][hd] fp16 bits (positions
  * 0..n_kv-1), softmax in chunks of 64 positions (online max per chunk, combined over chunks in order), out [nh][hd]. */
 void orc_attn(const float * q, const uint16_t * kc, const uint16_t * vc, int nh, int nkvh, int hd, int n_kv,
               float scale, float * out);
+void orc_attn_mt(const float * q, const uint16_t * kc, const uint16_t * vc, int nh, int nkvh, int hd, int n_kv,
+                 float scale, float * out, int n_threads);
+/* The reference-arithmetic decoder's attention: ggml's CPU path without flash attention (fp16 q, F16 dots summed in
+ * double, softmax with libm expf and a double sum, fp16 probabilities times V). */
+void orc_ref_attn(const float * q, const uint16_t * kc, const uint16_t * vc, int nh, int nkvh, int hd, int n_kv,
+                  float scale, float * out);
+void orc_ref_attn_mt(const float * q, const uint16_t * kc, const uint16_t * vc, int nh, int nkvh, int hd, int n_kv,
+                     float scale, float * out, int n_threads);
 
 /* ---- Q6_K row dequantize (ggml dequantize_row_q6_K) and argmax ---- */
 void orc_dequant_row_q6_K(const uint8_t * row, int cols, float * y);

@@ -83,6 +83,16 @@ def orc() -> C.CDLL:
         _fn(lib, "orc_model_decode", i, vp, i, i, vp)
         _fn(lib, "orc_model_hidden", C.POINTER(fl), vp)
         _fn(lib, "orc_model_destroy", None, vp)
+        _fn(lib, "orc_model_set_mode", i, vp, i)
+        _fn(lib, "orc_model_set_fault", i, vp, i)
+        _fn(lib, "orc_model_set_trace", i, vp, vp)
+        _fn(lib, "orc_model_reset", i, vp)
+        _fn(lib, "orc_model_prefill", i, vp, vp, i, i)
+        _fn(lib, "orc_model_generate", i, vp, vp, i, i, vp, vp)
+        _fn(lib, "orc_fast_gemv", None, i, i, vp, vp, i, i, vp)
+        _fn(lib, "orc_gdn_mt", None, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i, i, fl, fl, fl, i, vp, i)
+        _fn(lib, "orc_attn_mt", None, vp, vp, vp, i, i, i, i, fl, vp, i)
+        _fn(lib, "orc_ref_attn", None, vp, vp, vp, i, i, i, i, fl, vp)
         _orc = lib
     return _orc
 
@@ -164,6 +174,14 @@ def fx_gemv(t: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int, blocksum
     return (y, bs, acc) if blocksums else y
 
 
+def fast_gemv(mode: int, t: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """The decoder's SIMD rows: mode 0 canonical (= fx_gemv), 1 reference (= ref_gemv)."""
+    x = np.ascontiguousarray(x, F)
+    y = np.empty(rows, F)
+    orc().orc_fast_gemv(mode, t, _p(np.ascontiguousarray(w, np.uint8)), _p(x), rows, cols, _p(y))
+    return y
+
+
 def norm_scale(x: np.ndarray, eps: float, l2: bool = False) -> float:
     x = np.ascontiguousarray(x, F)
     return float(orc().orc_norm_scale(_p(x), x.size, eps, 1 if l2 else 0))
@@ -226,11 +244,14 @@ def gdn(state, q, k, v, graw, braw, hv, hk, scale, flags=0, dt=None, a=None, z=N
     return y, st
 
 
-def attn(q, kc, vc, nh, nkvh, hd, n_kv, scale):
+def attn(q, kc, vc, nh, nkvh, hd, n_kv, scale, threads: int = 1, reference: bool = False):
     q = np.ascontiguousarray(q, F)
     out = np.empty(nh * hd, F)
-    orc().orc_attn(_p(q), _p(np.ascontiguousarray(kc, np.uint16)), _p(np.ascontiguousarray(vc, np.uint16)), nh, nkvh,
-                   hd, n_kv, scale, _p(out))
+    kc, vc = np.ascontiguousarray(kc, np.uint16), np.ascontiguousarray(vc, np.uint16)
+    if reference:
+        orc().orc_ref_attn(_p(q), _p(kc), _p(vc), nh, nkvh, hd, n_kv, scale, _p(out))
+    else:
+        orc().orc_attn_mt(_p(q), _p(kc), _p(vc), nh, nkvh, hd, n_kv, scale, _p(out), threads)
     return out
 
 
@@ -245,10 +266,14 @@ def f2h(x: np.ndarray) -> np.ndarray:
     return np.array([o.orc_float_to_half(float(v)) for v in np.asarray(x, F).ravel()], np.uint16)
 
 
+MODE_CANONICAL, MODE_REFERENCE = 0, 1
+FAULT_ATTN_RESIDUAL, FAULT_QGATE_SWAP, FAULT_GATES_SWAP, FAULT_FFN_SWAP, FAULT_ROPE_K, FAULT_SSM_RESIDUAL = range(1, 7)
+
+
 class Model:
     """The oracle decoder (qwen35_oracle.c) on the same tensor table and blob as the GPU model."""
 
-    def __init__(self, cfg_c, table, n: int, data: np.ndarray, threads: int = 0):
+    def __init__(self, cfg_c, table, n: int, data: np.ndarray, threads: int = 0, mode: int = MODE_CANONICAL):
         self.lib = orc()
         self.data = data  # keep the blob alive
         self.n_vocab = cfg_c.n_vocab
@@ -257,6 +282,40 @@ class Model:
         self.h = self.lib.orc_model_create(C.byref(cfg_c), table, n, data.ctypes.data, threads)
         if not self.h:
             raise RuntimeError("orc_model_create failed")
+        self.set_mode(mode)
+
+    def set_mode(self, mode: int) -> None:
+        if self.lib.orc_model_set_mode(self.h, mode):
+            raise ValueError(f"mode {mode}")
+
+    def set_fault(self, fault: int) -> None:
+        """Plants a wiring mistake (ORC_FAULT_*) in this decoder: only for tests of the independent checks."""
+        if self.lib.orc_model_set_fault(self.h, fault):
+            raise ValueError(f"fault {fault}")
+
+    def reset(self) -> None:
+        self.lib.orc_model_reset(self.h)
+
+    def trace(self, n_layer: int) -> np.ndarray:
+        """Turns on the residual-stream trace; the returned array [(n_layer + 1), n_embd] is filled by every later
+        decode (the stream before layer 0 and after each layer)."""
+        self._trace = np.zeros((n_layer + 1, self.n_embd), F)
+        self.lib.orc_model_set_trace(self.h, _p(self._trace))
+        return self._trace
+
+    def prefill(self, tokens: np.ndarray, pos0: int) -> None:
+        t = np.ascontiguousarray(tokens, np.int32)
+        if self.lib.orc_model_prefill(self.h, _p(t), t.size, int(pos0)):
+            raise RuntimeError("orc_model_prefill failed")
+
+    def generate_fast(self, prompt: np.ndarray, n_gen: int, logits: np.ndarray | None = None) -> np.ndarray:
+        """Greedy decode from a reset state: the prompt prefilled in chunks (all but its last token), then n_gen
+        decode steps; returns all ids, and the last step's logits in `logits`."""
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(p.size + n_gen, np.int32)
+        if self.lib.orc_model_generate(self.h, _p(p), p.size, int(n_gen), _p(out), _p(logits) if logits is not None else None):
+            raise RuntimeError("orc_model_generate failed")
+        return out
 
     def decode(self, token: int, pos: int, logits: np.ndarray | None = None) -> int:
         r = self.lib.orc_model_decode(self.h, int(token), int(pos), _p(logits) if logits is not None else None)
@@ -280,6 +339,7 @@ class Model:
 
     def close(self):
         if self.h:
+            self.lib.orc_model_set_trace(self.h, None)
             self.lib.orc_model_destroy(self.h)
             self.h = None
 

@@ -108,6 +108,9 @@ def dequantize(t: int, w, rows: int, cols: int) -> np.ndarray:
     if t in (Q4_0, Q8_0):
         q, d = (q4_0 if t == Q4_0 else q8_0)(w, rows, cols)
         return q.reshape(rows, -1, 32) * d[..., None]
+    if t == Q4_1:
+        q, d, m = q4_1(w, rows, cols)
+        return (q.reshape(rows, -1, 32) * d[..., None] + m[..., None]).reshape(rows, cols)
     if t == Q5_K:
         q, sc, mn, d, dmin = q5_K(w, rows, cols)
         q = q.reshape(rows, -1, 8, 32)

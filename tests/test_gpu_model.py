@@ -96,30 +96,71 @@ def test_model_from_gguf_file_matches_oracle(gq, orc, q35, tmp_path):
     assert np.array_equal(lg.view(np.uint32), lo.view(np.uint32))
 
 
-@pytest.mark.timeout(600)
-def test_c5_greedy_128_steps_matches_oracle(gq, orc, q35):
-    """The full C5 model (32 layers: 24 DeltaNet + 8 attention, hidden 4096, FFN 12288, vocab 151936, Q4_0 layers,
-    Q6_K embedding and head, seed 0): 128 greedy tokens after an 8-token prompt, identical to the oracle decoder's,
-    and the last step's logits bit for bit."""
-    cfg = q35.Config(n_ctx=160)
+@pytest.fixture(scope="module")
+def c5(q35):
+    """The C5 model (32 layers: 24 DeltaNet + 8 attention, hidden 4096, FFN 12288, vocab 151936, Q4_0 layers, Q6_K
+    embedding and head, seed 0), its 512-id prompt, and its GPU run: the prompt through the batched prefill (all but
+    the last prompt token), then 128 greedy decode steps, so the context reaches 640."""
+    cfg = q35.Config(n_ctx=640)
     blob = q35.generate(cfg, seed=0)
-    prompt = q35.prompt_ids(cfg, 8)
-    n_gen = 128
+    prompt = q35.prompt_ids(cfg, 512)
+    print("[c5] model generated; GPU prefill + 128 steps", flush=True)
+    with q35.Model(blob) as m:
+        m.reset(prompt)
+        assert m.prefill(len(prompt) - 1)
+        m.step(128)
+        toks, logits = m.tokens(640), m.logits()
+        m.reset(prompt)  # the logits of the first 3 generated tokens' steps, for the reference-arithmetic check
+        assert m.prefill(len(prompt) - 1)
+        m.step(C5_REF_DIVERGENCE + 1)
+        toks3, logits3 = m.tokens(len(prompt) + C5_REF_DIVERGENCE + 1), m.logits()
+    return cfg, blob, prompt, toks, logits, toks3, logits3
+
+
+@pytest.mark.timeout(900)
+def test_c5_full_size_matches_oracle(orc, q35, c5):
+    """C5 at its stated size: 128 greedy tokens identical to the oracle decoder's, and the last step's logits bit
+    for bit (the oracle runs the prompt as chunked prefill too; its prefill equals its decode steps bit for bit)."""
+    cfg, blob, prompt, toks, logits, _, _ = c5
     om = orc.Model(q35.config_c(cfg), blob.table, blob.n, blob.data)
     lo = np.empty(cfg.n_vocab, np.float32)
-    toks = [int(t) for t in prompt]
-    for pos in range(len(prompt) - 1 + n_gen):  # the oracle's greedy decode, keeping the last logits
-        last = pos == len(prompt) - 2 + n_gen
-        nxt = om.decode(toks[pos], pos, lo if last else None)
-        if pos + 1 >= len(prompt):
-            toks.append(nxt)
+    print("[c5] oracle prefill + 128 steps", flush=True)
+    want = om.generate_fast(prompt, 128, lo)
     om.close()
-    want = np.array(toks, np.int32)
-    with q35.Model(blob) as m:
-        got = m.generate(prompt, n_gen)
-        lg = m.logits()
-    assert np.array_equal(got, want), f"first mismatch at {np.nonzero(got != want)[0][:3]}"
-    assert np.array_equal(lg.view(np.uint32), lo.view(np.uint32))
+    assert np.array_equal(toks, want), f"first mismatch at {np.nonzero(toks != want)[0][:3]}"
+    assert np.array_equal(logits.view(np.uint32), lo.view(np.uint32))
+
+
+# The reference's own CPU arithmetic (gemvq_ref.h: sequential FP32 rows, double sums of squares, libm exp/log; the
+# oracle's reference mode) and the canonical arithmetic differ by FP32 rounding per operation; on this random-init
+# model Q8_0 activation quantization decisions flipped by those roundings grow the difference to percent level
+# (tests/test_oracle_model.py). Measured at C5: the first two generated tokens agree and the third differs; at that
+# step the reference decoder's own top-2 logit margin is 0.124 and the two arithmetics' logits differ by up to 0.56.
+C5_REF_DIVERGENCE = 2  # index of the first generated token where the GPU and the reference arithmetic differ
+
+
+@pytest.mark.timeout(900)
+def test_c5_against_reference_arithmetic(orc, q35, c5):
+    """The GPU's greedy tokens at C5 against the reference-arithmetic decoder: identical up to the recorded first
+    divergence; there, the GPU's token is the one the reference ranks within the two arithmetics' logit
+    difference of its own choice (a near-tie), not an unrelated token."""
+    cfg, blob, prompt, _, _, toks3, lg = c5
+    n = len(prompt)
+    om = orc.Model(q35.config_c(cfg), blob.table, blob.n, blob.data, mode=orc.MODE_REFERENCE)
+    lr = np.empty(cfg.n_vocab, np.float32)
+    print("[c5] reference-arithmetic prefill + 3 steps", flush=True)
+    ref = om.generate_fast(prompt, C5_REF_DIVERGENCE + 1, lr)
+    om.close()
+    k = n + C5_REF_DIVERGENCE
+    assert np.array_equal(toks3[:k], ref[:k]), f"earlier divergence at {np.nonzero(toks3[:k] != ref[:k])[0][:3]}"
+    g, r = int(toks3[k]), int(ref[k])
+    noise = float(np.max(np.abs(lg.astype(np.float64) - lr)))
+    margin = float(lr[r]) - float(lr[g])
+    print(f"[c5] step {C5_REF_DIVERGENCE}: GPU {g} reference {r}, reference margin {margin:.4f}, "
+          f"max logit difference {noise:.4f}", flush=True)
+    assert g != r, "the recorded divergence is gone: update C5_REF_DIVERGENCE and the design notes"
+    assert 0.0 < margin < noise
+    assert int(np.argmax(lg)) == g and int(np.argmax(lr)) == r
 
 
 def _decode_state(m, cfg, npos):

@@ -1,0 +1,165 @@
+"""The oracle's decoder pinned by independent checks (CPU only).
+
+- Its fast SIMD rows equal the scalar oracle bit for bit (both arithmetics, every format, edge-case scales).
+- Its chunked prefill equals decode steps bit for bit (both arithmetics).
+- Layer by layer it computes the same function as an independent float64 numpy decoder (tests/qwen35_f64.py):
+  every layer is recomputed in float64 from the oracle's own input to it, so the comparison does not inherit the
+  amplification of rounding differences across layers.
+- Each planted wiring mistake (a dropped residual, swapped operands, a missing rotation) fails that check.
+- A one-ulp change of one norm weight moves the logits by far more than one ulp, which is why two arithmetics that
+  differ only in FP32 rounding (canonical vs the reference's sequential FP32) do not give identical greedy tokens
+  over long decodes of this random-init model.
+"""
+import numpy as np
+import pytest
+
+import ggml_blocks as gb
+from qwen35_f64 import F64Decoder
+
+# Each (step, layer) either agrees with float64 to FP32 rounding (about 1e-7, L2 relative to the layer's contribution)
+# or a Q8_0 activation quantizer decision was flipped by an FP32 rounding difference, which moves the layer's
+# contribution by up to about 1e-2. Flips are more frequent in the reference arithmetic (its sequential FP32 row
+# sums round more than the exact fixed-point ones): measured on these configurations, about 7 % of the layer-steps
+# of the canonical decoder and 30 % of the reference one. The check: the median layer-step within FP32 rounding,
+# and none beyond what one flipped decision explains.
+LAYER_TOL = 5e-2
+ROUNDING_TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def q35():
+    import qwen35
+
+    return qwen35
+
+
+def test_fast_rows_match_scalar_oracle(orc, gq):
+    rng = np.random.default_rng(7)
+    for t in (gq.Q4_0, gq.Q4_1, gq.Q8_0, gq.Q5_K, gq.Q6_K):
+        rows, cols = 48, 2048
+        w = gq.matrix(t, rows, cols, seed=3, stream=t, std=0.02)
+        xs = [rng.standard_normal(cols).astype(np.float32) * np.float32(s) for s in (1e-6, 1e-2, 1.0, 300.0, 3e4)]
+        x0 = np.zeros(cols, np.float32)
+        x0[:300] = rng.standard_normal(300)  # zero blocks
+        xs.append(x0)
+        for x in xs:
+            want = orc.fx_gemv(t, w, x, rows, cols)
+            got = orc.fast_gemv(0, t, w, x, rows, cols)
+            assert np.array_equal(want.view(np.uint32), got.view(np.uint32)), (t, "canonical")
+            want, _ = orc.ref_gemv(t, w, x, rows, cols)
+            got = orc.fast_gemv(1, t, w, x, rows, cols)
+            assert np.array_equal(want.view(np.uint32), got.view(np.uint32)), (t, "reference")
+        # random block bytes: every scale exponent, subnormal and negative scales, all nibble values
+        wr = np.frombuffer(rng.bytes(rows * gb.BLOCK_BYTES[t] * (cols // gb.BLOCK_ELEMS[t])), np.uint8).copy()
+        blk = wr.reshape(-1, gb.BLOCK_BYTES[t])
+        for hi in {gq.Q4_0: (1,), gq.Q4_1: (1, 3), gq.Q8_0: (1,), gq.Q5_K: (1, 3), gq.Q6_K: (209,)}[t]:
+            blk[:, hi] &= 0xBF  # fp16 exponent field at most 15: scales below 2, signs and subnormals kept
+        x = rng.standard_normal(cols).astype(np.float32)
+        want = orc.fx_gemv(t, wr, x, rows, cols)
+        got = orc.fast_gemv(0, t, wr, x, rows, cols)
+        assert np.array_equal(want.view(np.uint32), got.view(np.uint32)), (t, "canonical, random blocks")
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_prefill_equals_decode_steps(orc, q35, mode):
+    cfg = q35.tiny(n_layer=4)
+    blob = q35.generate(cfg, seed=5)
+    cc = q35.config_c(cfg)
+    prompt = q35.prompt_ids(cfg, 45, seed=5)  # chunks of 32 and 12
+    a = orc.Model(cc, blob.table, blob.n, blob.data, threads=4, mode=mode)
+    b = orc.Model(cc, blob.table, blob.n, blob.data, threads=4, mode=mode)
+    la, lb = np.empty(cfg.n_vocab, np.float32), np.empty(cfg.n_vocab, np.float32)
+    ta = a.generate_fast(prompt, 6, la)
+    toks = [int(t) for t in prompt]
+    for pos in range(len(prompt) - 1 + 6):
+        nxt = b.decode(toks[pos], pos, lb if pos == len(prompt) + 4 else None)
+        if pos + 1 >= len(prompt):
+            toks.append(nxt)
+    assert np.array_equal(ta, np.array(toks, np.int32))
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    assert np.array_equal(a.hidden().view(np.uint32), b.hidden().view(np.uint32))
+
+
+def lockstep(orc, q35, blob, n_steps: int, mode: int = 0, fault: int = 0, n_prompt: int = 6):
+    """Greedy decode on the oracle; at every step each layer is recomputed by the float64 decoder from the oracle's
+    input to that layer, and the head from the oracle's last residual stream. Returns the L2-relative differences
+    per (step, layer) of the layer's contribution (the head's logits in the last column)."""
+    cfg = blob.cfg
+    om = orc.Model(q35.config_c(cfg), blob.table, blob.n, blob.data, threads=4, mode=mode)
+    om.set_fault(fault)
+    tr = om.trace(cfg.n_layer)
+    f64 = F64Decoder(blob)
+    lo = np.empty(cfg.n_vocab, np.float32)
+    toks = [int(t) for t in q35.prompt_ids(cfg, n_prompt, seed=3)]
+    err = np.zeros((n_steps, cfg.n_layer + 1))
+    for pos in range(n_steps):
+        nxt = om.decode(toks[pos], pos, lo)
+        if pos + 1 >= len(toks):
+            toks.append(nxt)
+        assert np.array_equal(tr[0], f64.embed(toks[pos]).astype(np.float32))  # the embedding row, exactly
+        for il in range(cfg.n_layer):
+            hin = tr[il].astype(np.float64)
+            ho = f64.layer(il, hin, pos)
+            err[pos, il] = np.linalg.norm(tr[il + 1] - ho) / np.linalg.norm(ho - hin)
+        lf = f64.head(tr[-1])
+        err[pos, -1] = np.linalg.norm(lo - lf) / np.linalg.norm(lf)
+    om.close()
+    return err
+
+
+def same_function(err: np.ndarray) -> bool:
+    return bool(err.max() <= LAYER_TOL and np.median(err) <= ROUNDING_TOL)
+
+
+@pytest.mark.parametrize("wtype,mode", [(2, 0), (8, 0), (2, 1), (8, 1)])
+def test_decoder_matches_float64_layer_by_layer(orc, q35, wtype, mode):
+    """8 layers (6 DeltaNet + 2 attention), 16 decode steps, Q4_0 or Q8_0 layers, both arithmetics."""
+    cfg = q35.tiny(n_layer=8, wtype=wtype)
+    blob = q35.generate(cfg, seed=0)
+    err = lockstep(orc, q35, blob, 16, mode=mode)
+    assert err.max() <= LAYER_TOL, f"worst layer difference {err.max():.3e} at {np.unravel_index(err.argmax(), err.shape)}"
+    assert np.median(err) <= ROUNDING_TOL, f"median layer difference {np.median(err):.3e}"
+    if mode == 0:  # the exact fixed-point sums: flips are rare
+        assert np.mean(err <= ROUNDING_TOL) >= 0.85
+
+
+def test_decoder_with_q4_1_layers_matches_float64(orc, q35):
+    """The type mix of real Qwen3.5 Q4_0 files: Q4_1 ffn_down in some layers."""
+    import gemvq as gq
+
+    cfg = q35.tiny(n_layer=4)
+    types = {f"blk.{il}.ffn_down.weight": gq.Q4_1 for il in (1, 3)}
+    blob = q35.generate(cfg, seed=4, types=types)
+    assert same_function(lockstep(orc, q35, blob, 10))
+
+
+@pytest.mark.parametrize("fault", [1, 2, 3, 4, 5, 6])
+def test_planted_wiring_mistakes_are_caught(orc, q35, fault):
+    """Each ORC_FAULT_* (dropped attention or DeltaNet residual, q/gate halves swapped, beta/alpha swapped, ffn
+    gate/up swapped, keys cached unrotated) planted in the oracle makes the float64 check fail."""
+    cfg = q35.tiny(n_layer=8)
+    blob = q35.generate(cfg, seed=0)
+    err = lockstep(orc, q35, blob, 10, fault=fault)
+    assert not same_function(err)
+    assert err.max() > 4 * LAYER_TOL
+
+
+def test_rounding_level_perturbation_is_amplified(orc, q35):
+    """One norm weight moved by one ulp (6e-8 relative) changes the logits of a 16-step greedy decode by orders of
+    magnitude more: an FP32 rounding difference flips Q8_0 activation quantization decisions, and each flip moves
+    the following matrix products' outputs by about 1 % of their quantization step."""
+    cfg = q35.tiny(n_layer=8)
+    blob = q35.generate(cfg, seed=0)
+    prompt = q35.prompt_ids(cfg, 6, seed=3)
+    la = np.empty(cfg.n_vocab, np.float32)
+    a = orc.Model(q35.config_c(cfg), blob.table, blob.n, blob.data, threads=4)
+    ta = a.generate_fast(prompt, 10, la)
+    pert = q35.Blob(cfg, blob.table, blob.data.copy(), blob.n)
+    w = pert.tensor("blk.0.attn_norm.weight").view(np.float32)
+    w[7] = np.nextafter(w[7], np.float32(2))
+    lb = np.empty_like(la)
+    b = orc.Model(q35.config_c(cfg), pert.table, pert.n, pert.data, threads=4)
+    b.generate_fast(prompt, 10, lb)
+    rel = np.linalg.norm(la - lb) / np.linalg.norm(la)
+    assert rel > 1e-4, rel
+    assert len(ta) == len(prompt) + 10
