@@ -71,6 +71,8 @@ struct gemvq_ctx {
     int32_t * dbg_dst = nullptr;  // host destination; non-NULL while armed
     bool dbg_used = false;        // the list being compiled writes the dump
     float * gdn_raw = nullptr;    // raw DeltaNet output when its gated norm is folded into the next GEMV
+    float * dsnap = nullptr;      // a deferred norm's row, computed before a command overwrote its source
+    float * xsnap = nullptr;      // a GEMV group's activation, copied before a member overwrites it
     int8_t * gemm_q = nullptr;    // a batched GEMV's quantized activation rows (GEMM_MAX_TOK x GEMV_MAXK)
     float * gemm_d = nullptr;     // and their block scales
     float * gemm_s = nullptr;     // and their Q8_1 block sums (for Q4_1 weights)
@@ -220,17 +222,144 @@ struct Compiler {
         return (w.type == type && w.rows == rows && w.cols == cols) ? &w : nullptr;
     }
 
-    // A GDN's gated output norm pending for the GEMV group that reads its output next.
-    struct Gated { bool on = false; uint32_t y; const float * z; const float * w; float eps; int z_silu; } gated;
+    // Act ranges (in floats) and their overlap.
+    struct Rng { uint64_t lo, hi; };
+    static bool meet(Rng a, Rng b) { return a.lo < b.hi && b.lo < a.hi; }
+    static bool meet_any(const std::vector<Rng> & a, const std::vector<Rng> & b) {
+        for (const Rng & x : a)
+            for (const Rng & y : b)
+                if (meet(x, y)) return true;
+        return false;
+    }
 
-    // The command at `next` is a Q4_0 / Q8_0 GEMV that reads exactly the GDN output y (cols = heads * 128 <= 8192).
-    bool fold_gated(const uint32_t * cmds, unsigned n, unsigned next, uint32_t y, uint32_t cols) const {
+    // What the GEMV at command i writes while its pass runs (its output; a CONV epilog's new state; an ARGMAX key)
+    // and what its epilog reads meanwhile (the residual; the conv state and kernel). Validation happens elsewhere.
+    void gemv_io(const uint32_t * cmds, unsigned n, unsigned i, std::vector<Rng> & wr, std::vector<Rng> & rd) const {
+        const uint32_t * k = cmds + size_t(i) * GEMVQ_CMD_WORDS;
+        const uint64_t rows = k[2];
+        const uint32_t flags = k[1] & ~0xffu;
+        const uint32_t * e = i + 1 < n ? k + GEMVQ_CMD_WORDS : nullptr;
+        if ((flags & GEMVQ_GEMV_SWIGLU) && e) {
+            wr.push_back({e[7], e[7] + rows});
+        } else if ((flags & GEMVQ_GEMV_ADD) && e) {
+            const uint64_t r = e[2] == k[7] ? e[3] : e[2];
+            wr.push_back({e[4], e[4] + rows});
+            rd.push_back({r, r + rows});
+        } else if ((flags & GEMVQ_GEMV_CONV) && e) {
+            wr.push_back({e[4], e[4] + rows});
+            wr.push_back({e[6], e[6] + 3 * rows});
+            rd.push_back({e[5], e[5] + 3 * rows});
+            rd.push_back({e[3], e[3] + 4 * rows});
+        } else if ((flags & GEMVQ_GEMV_ARGMAX) && e) {
+            wr.push_back({k[7], k[7] + rows});
+            wr.push_back({e[3], e[3] + 2});
+        } else {
+            wr.push_back({k[7], k[7] + rows});
+        }
+    }
+
+    // Act ranges the commands i .. i + used - 1 write (a superset is fine: it only costs a snapshot).
+    void cmd_writes(const uint32_t * cmds, unsigned n, unsigned i, unsigned used, std::vector<Rng> & wr) const {
+        for (unsigned j = i; j < i + used && j < n;) {
+            const uint32_t * k = cmds + size_t(j) * GEMVQ_CMD_WORDS;
+            const uint32_t * k2 = j + 1 < n ? k + GEMVQ_CMD_WORDS : nullptr;
+            unsigned step = 1;
+            switch (k[0]) {
+            case GEMVQ_OP_GEMV: wr.push_back({k[7], k[7] + uint64_t(k[2])}); break;
+            case GEMVQ_OP_RMSNORM:
+                if (!(k[7] & GEMVQ_NORM_DEFER)) wr.push_back({k[4], k[4] + uint64_t(k[1]) * (k[6] ? k[6] : 1)});
+                break;
+            case GEMVQ_OP_ADD: case GEMVQ_OP_MUL: case GEMVQ_OP_SILU_MUL: case GEMVQ_OP_UNARY:
+                wr.push_back({k[4], k[4] + uint64_t(k[1])});
+                break;
+            case GEMVQ_OP_FILL: wr.push_back({k[2], k[2] + uint64_t(k[1])}); break;
+            case GEMVQ_OP_CONV: {
+                const uint64_t nt = (k[7] >> 16) ? (k[7] >> 16) : 1;
+                wr.push_back({k[4], k[4] + uint64_t(k[1]) * nt});
+                wr.push_back({k[6], k[6] + 3ull * k[1]});
+                break;
+            }
+            case GEMVQ_OP_ROPE: wr.push_back({k[4], k[4] + uint64_t(k[5]) * k[6]}); break;
+            case GEMVQ_OP_GDN: {
+                const bool gates = k2 && (k2[3] & GEMVQ_GDN_GATES);
+                const uint32_t * k3 = gates && j + 2 < n ? k2 + GEMVQ_CMD_WORDS : nullptr;
+                const uint64_t nt = k3 && k3[2] ? k3[2] : 1;
+                wr.push_back({k[7], k[7] + uint64_t(k[1] & 0xffffu) * 128 * nt});
+                step = gates ? 3 : 2;
+                break;
+            }
+            case GEMVQ_OP_ATTN: {
+                const uint64_t nt = (k[7] >> 16) & 0xffu ? (k[7] >> 16) & 0xffu : 1;
+                wr.push_back({k[4], k[4] + uint64_t(k[1] & 0xffffu) * (k[5] & 0xffffu) * nt});
+                step = 2;
+                break;
+            }
+            case GEMVQ_OP_GET_ROWS: {
+                const uint64_t nt = (k[1] >> 16) & 0xffu ? (k[1] >> 16) & 0xffu : 1;
+                wr.push_back({k[7], k[7] + uint64_t(k[3]) * nt});
+                break;
+            }
+            case GEMVQ_OP_ARGMAX: wr.push_back({k[3], k[3] + 2}); break;
+            case GEMVQ_OP_NEXT_TOKEN:
+                wr.push_back({k[1], k[1] + 2});
+                wr.push_back({k[2], k[2] + 1});
+                wr.push_back({k[3], k[3] + 1});
+                wr.push_back({k[6], c->act_floats});
+                break;
+            case GEMVQ_OP_GEMM:
+                if (k2) wr.push_back({k[7], k[7] + uint64_t(k2[2]) * (k2[0] ? k2[0] - 1 : 0) + k[2]});
+                step = 2;
+                break;
+            default: break;
+            }
+            j += step;
+        }
+    }
+
+    // A GDN's gated output norm pending for the GEMV group that reads its output next: the gated vector goes to y
+    // (written by workgroup 0 of that group), computed from the raw step output (a private buffer), z and w.
+    struct Gated { bool on = false; uint32_t y, cols; const float * z; const float * w; float eps; int z_silu; } gated;
+
+    std::vector<Rng> gated_ranges() const {
+        const uint64_t z = uint64_t(gated.z - c->act), w = uint64_t(gated.w - c->act);
+        return {{gated.y, gated.y + uint64_t(gated.cols)}, {z, z + gated.cols}, {w, w + 128}};
+    }
+
+    // The command at `next` is a Q4_0 / Q8_0 GEMV that reads exactly the GDN output y (cols = heads * 128 <= 8192)
+    // and whose pass neither writes nor reads what the gated prologue reads and writes (y, z, the norm weight).
+    bool fold_gated(const uint32_t * cmds, unsigned n, unsigned next, uint32_t y, uint32_t cols, uint32_t z_off,
+                    uint32_t w_off) const {
         if (next >= n || cols > 8192) return false;
         const uint32_t * g = cmds + size_t(next) * GEMVQ_CMD_WORDS;
         const int t = int(g[1] & 0xffu);
-        const bool apart = g[7] + uint64_t(g[2]) <= y || uint64_t(y) + cols <= g[7];  // its output is not the GDN's
-        return g[0] == GEMVQ_OP_GEMV && g[6] == y && g[3] == cols && (t == T_Q4_0 || t == T_Q8_0) && apart &&
-               !(g[1] & GEMVQ_GEMV_SWIGLU);  // the gated prologue has no SwiGLU-pair variant
+        if (!(g[0] == GEMVQ_OP_GEMV && g[6] == y && g[3] == cols && (t == T_Q4_0 || t == T_Q8_0) &&
+              !(g[1] & GEMVQ_GEMV_SWIGLU)))  // the gated prologue has no SwiGLU-pair variant
+            return false;
+        std::vector<Rng> wr, rd;
+        gemv_io(cmds, n, next, wr, rd);
+        const std::vector<Rng> gr = {{y, uint64_t(y) + cols}, {z_off, uint64_t(z_off) + cols}, {w_off, uint64_t(w_off) + 128}};
+        return !meet_any(wr, gr) && !meet_any(rd, gr);
+    }
+
+    // The deferred RMSNORM pending for the GEMVs on its output (gemvqc16.h:46-51: its normalized row is fixed when
+    // the command runs; y is never written). `dirty`: the first launch of a later command that overwrote its row or
+    // weight (-1: none). A GEMV on the norm after that reads the row from the context's snapshot buffer (`snap`),
+    // into which the row is computed right before that launch.
+    struct Deferred { bool on = false, snap = false; long dirty = -1; uint32_t n, x, w, y; float eps; uint32_t flags; } defer;
+
+    std::vector<Rng> defer_ranges() const {
+        std::vector<Rng> r = {{defer.x, uint64_t(defer.x) + defer.n}};
+        if (!(defer.flags & GEMVQ_NORM_NO_WEIGHT)) r.push_back({defer.w, uint64_t(defer.w) + defer.n});
+        return r;
+    }
+
+    // The deferred row computed into the snapshot buffer, as launch `at` (before the launches that overwrite it).
+    void snapshot_defer(size_t at, int cmd) {
+        NormArgs a{A(defer.x), (defer.flags & GEMVQ_NORM_NO_WEIGHT) ? nullptr : A(defer.w), c->dsnap, int(defer.n), 1,
+                   int(defer.n), defer.eps, int(defer.flags & 3)};
+        out.insert(out.begin() + long(at), LNorm{a});
+        spans.insert(spans.begin() + long(at), {cmd, 1});
+        defer.snap = true;
     }
 
     // The activation rows a batched GEMV quantized last, while nothing since could have changed them: the next GEMM
@@ -238,17 +367,33 @@ struct Compiler {
     struct LastQuant { bool on = false; GemmQuantArgs q; uint32_t x_off, x_len; } lastq;
 
     bool compile(const uint32_t * cmds, unsigned n) {
-        struct Deferred { bool on = false; uint32_t n, x, w, y; float eps; uint32_t flags; } defer;
         for (unsigned i = 0; i < n;) {
+            const size_t before = out.size();
+            const unsigned at = i;
+            if (!compile_one(cmds, n, i)) return false;
+            // a command that overwrote the row or the weight of a pending deferred norm: a later GEMV on the norm
+            // reads a snapshot computed before that command
+            if (defer.on && !defer.snap && defer.dirty < 0) {
+                std::vector<Rng> wr;
+                cmd_writes(cmds, n, at, i - at, wr);
+                if (meet_any(wr, defer_ranges())) defer.dirty = long(before);
+            }
+        }
+        return true;
+    }
+
+    // Compiles the command at i (with the commands it consumes); advances i past them.
+    bool compile_one(const uint32_t * cmds, unsigned n, unsigned & i) {
+        {
             const uint32_t * k = cmds + size_t(i) * GEMVQ_CMD_WORDS;
             const uint32_t op = k[0];
             if (op != GEMVQ_OP_GEMM) lastq.on = false;
             switch (op) {
             case GEMVQ_OP_GEMV: {
                 unsigned used = 0;
-                if (!gemv_group(cmds, n, i, defer.on ? &defer.n : nullptr, defer, used)) return false;
+                if (!gemv_group(cmds, n, i, used)) return false;
                 i += used;
-                continue;
+                return true;
             }
             case GEMVQ_OP_RMSNORM: {
                 const uint32_t nn = k[1], rows = k[6] ? k[6] : 1, flags = k[7], stride = ((flags >> 8) & 0xffffu) * 16;
@@ -260,6 +405,8 @@ struct Compiler {
                 if (flags & GEMVQ_NORM_DEFER) {
                     if (rows != 1 || stride) return reject(i, "deferred RMSNORM needs one packed row");
                     defer.on = true;
+                    defer.snap = false;
+                    defer.dirty = -1;
                     defer.n = nn;
                     defer.x = k[2];
                     defer.w = k[3];
@@ -357,12 +504,12 @@ struct Compiler {
                 a.s_gb = int(sg);
                 a.s_y = int(hv * 128);
                 const unsigned next = i + (gates ? 3 : 2);
-                if ((flags & GEMVQ_GDN_GATED) && ntok == 1 && fold_gated(cmds, n, next, k[7], hv * 128)) {
+                if ((flags & GEMVQ_GDN_GATED) && ntok == 1 && fold_gated(cmds, n, next, k[7], hv * 128, k2[7], k2[6])) {
                     // the gated norm runs in the next GEMV's activation prologue: the step writes its raw output
                     // to scratch, and that GEMV writes the gated values to y as the norm would have
                     a.y = c->gdn_raw;
                     a.flags = int(flags & ~GEMVQ_GDN_GATED);
-                    gated = {true, k[7], A(k2[7]), A(k2[6]), bits_f(k2[5]), int(bool(flags & GEMVQ_GDN_Z_SILU))};
+                    gated = {true, k[7], hv * 128, A(k2[7]), A(k2[6]), bits_f(k2[5]), int(bool(flags & GEMVQ_GDN_Z_SILU))};
                 }
                 out.push_back(LGdn{a});
                 spans.push_back({int(i), gates ? 3 : 2});
@@ -372,7 +519,7 @@ struct Compiler {
                     spans.push_back({int(i), gates ? 3 : 2});
                 }
                 i = next;
-                continue;
+                return true;
             }
             case GEMVQ_OP_CONV: {
                 const uint32_t ch = k[1], ntok = (k[7] >> 16) ? (k[7] >> 16) : 1;  // packed token rows
@@ -445,13 +592,13 @@ struct Compiler {
                 out.push_back(LAttn{a});
                 spans.push_back({int(i), 2});
                 i += 2;
-                continue;
+                return true;
             }
             case GEMVQ_OP_GEMM: {
                 unsigned used = 0;
                 if (!gemm(cmds, n, i, used)) return false;
                 i += used;
-                continue;
+                return true;
             }
             case GEMVQ_OP_GET_ROWS: {
                 const int type = int(k[1] & 0xffu), rows = int(k[2]), cols = int(k[3]);
@@ -628,14 +775,17 @@ struct Compiler {
         return true;
     }
 
-    // A GEMV group starting at command i (gemvqc16.h:26-45, gemvqc16.cpp:646-733).
-    template <typename D>
-    bool gemv_group(const uint32_t * cmds, unsigned n, unsigned i0, const uint32_t *, const D & defer, unsigned & used) {
+    // A GEMV group starting at command i (gemvqc16.h:26-45, gemvqc16.cpp:646-733). Its members run in one launch,
+    // so a member joins only if the order against the earlier members cannot matter: it writes nothing an earlier
+    // member writes or reads, and reads nothing an earlier member writes (a residual loaded while another member's
+    // rows are stored; gemvqc16.cpp:470-474, 686). A group ends after a member that writes over x.
+    bool gemv_group(const uint32_t * cmds, unsigned n, unsigned i0, unsigned & used) {
         GemvArgs a{};
         int type = -1;
         uint32_t x_off = 0, cols = 0;
         unsigned i = i0, gemvs = 0;
         int tasks = 0;
+        std::vector<Rng> W, R;  // what the members so far write and read during the pass
         while (i < n && a.n_members < 4) {
             const uint32_t * k = cmds + size_t(i) * GEMVQ_CMD_WORDS;
             if (k[0] != GEMVQ_OP_GEMV) break;
@@ -652,8 +802,12 @@ struct Compiler {
             if (!w) return reject(i, "GEMV weight offset, format or shape does not match an uploaded weight");
             if (!range(k[6], k[3]) || !range(k[7], uint64_t(rows))) return reject(i, "GEMV range");
             if (gemvs + ((flags & GEMVQ_GEMV_SWIGLU) ? 2 : 1) > GEMVQ_GROUP) break;
-            // workgroup 0 writes the gated activation while the group runs: no member may write over it
-            if (gated.on && gemvs > 0 && !(k[7] + uint64_t(rows) <= gated.y || uint64_t(gated.y) + cols <= k[7])) break;
+            std::vector<Rng> mw, mr;
+            gemv_io(cmds, n, i, mw, mr);
+            if (gemvs > 0 && (meet_any(mw, W) || meet_any(mw, R) || meet_any(mr, W))) break;
+            // workgroup 0 writes the gated activation while the group runs, from z and the norm weight: no member
+            // may write or read those
+            if (gated.on && gemvs > 0 && (meet_any(mw, gated_ranges()) || meet_any(mr, gated_ranges()))) break;
             if (gated.on && (flags & GEMVQ_GEMV_SWIGLU)) break;
             if (gemvs == 0) {
                 type = t;
@@ -666,7 +820,6 @@ struct Compiler {
             m.task_begin = tasks;
             m.epi = EPI_PLAIN;
             m.y = A(k[7]);
-            uint32_t y_off = k[7], y_len = uint32_t(rows);
             unsigned step = 1;
             if (flags & GEMVQ_GEMV_SWIGLU) {
                 if (i + 1 >= n) return reject(i, "SwiGLU GEMV without its u GEMV");
@@ -679,7 +832,6 @@ struct Compiler {
                 m.epi = EPI_SWIGLU;
                 m.w2 = weight_view(c->warena + uoff, t, rows, int(cols));
                 m.y = A(u[7]);
-                y_off = u[7];
                 step = 2;
             } else if (flags & GEMVQ_GEMV_SILU) {
                 m.epi = EPI_SILU;
@@ -698,7 +850,6 @@ struct Compiler {
                     m.conv_dst = A(e[6]);
                     m.conv_silu = int(e[7] & 1);
                     m.y = A(e[4]);
-                    y_off = e[4];
                 } else if (flags & GEMVQ_GEMV_ADD) {
                     if (e[0] != GEMVQ_OP_ADD || e[1] != uint32_t(rows) || (e[2] != k[7] && e[3] != k[7]))
                         return reject(i + 1, "ADD epilog");
@@ -707,7 +858,6 @@ struct Compiler {
                     m.epi = EPI_ADD;
                     m.res = A(r_off);
                     m.y = A(e[4]);
-                    y_off = e[4];
                 } else {
                     if (e[0] != GEMVQ_OP_ARGMAX || e[1] != uint32_t(rows) || e[2] != k[7] || !range(e[3], 2))
                         return reject(i + 1, "ARGMAX epilog");
@@ -720,8 +870,10 @@ struct Compiler {
             tasks += rows;
             gemvs += (flags & GEMVQ_GEMV_SWIGLU) ? 2 : 1;
             i += step;
-            // a group ends after a GEMV whose y overlaps x (gemvqc16.cpp:468-474)
-            if (y_off < x_off + cols && x_off < y_off + y_len) break;
+            W.insert(W.end(), mw.begin(), mw.end());
+            R.insert(R.end(), mr.begin(), mr.end());
+            // a group ends after a GEMV whose output (or new conv state) overlaps x (gemvqc16.cpp:468-474)
+            if (meet_any(mw, {{x_off, uint64_t(x_off) + cols}})) break;
         }
         if (a.n_members == 0) return reject(i0, "GEMV");
         a.cols = int(cols);
@@ -738,11 +890,25 @@ struct Compiler {
             a.gate_silu = gated.z_silu;
             gated.on = false;
         } else if (defer.on && defer.y == x_off && defer.n == cols) {
-            a.xsrc = XSRC_NORM;
-            a.x = A(defer.x);
-            a.norm_w = (defer.flags & GEMVQ_NORM_NO_WEIGHT) ? nullptr : A(defer.w);
-            a.norm_eps = defer.eps;
-            a.norm_l2 = int(defer.flags & GEMVQ_NORM_L2);
+            // every workgroup reads the norm's row and weight in its prologue while others store rows: with a member
+            // writing over them, or after an earlier command did, the launch reads the snapshot instead
+            if (!defer.snap && defer.dirty >= 0) snapshot_defer(size_t(defer.dirty), int(i0));
+            else if (!defer.snap && meet_any(W, defer_ranges())) snapshot_defer(out.size(), int(i0));
+            if (defer.snap) {
+                a.x = c->dsnap;
+            } else {
+                a.xsrc = XSRC_NORM;
+                a.x = A(defer.x);
+                a.norm_w = (defer.flags & GEMVQ_NORM_NO_WEIGHT) ? nullptr : A(defer.w);
+                a.norm_eps = defer.eps;
+                a.norm_l2 = int(defer.flags & GEMVQ_NORM_L2);
+            }
+        } else if (meet_any(W, {{x_off, uint64_t(x_off) + cols}})) {
+            // a member writes over x while other workgroups still read it: the launch reads a copy taken before
+            EwArgs cp{A(x_off), nullptr, c->xsnap, int(cols), 0, 0, EW_COPY, 0.0f};
+            out.push_back(LEw{cp});
+            spans.push_back({int(i0), 1});
+            a.x = c->xsnap;
         }
         if (c->dbg_dst && !c->dbg_used) {
             const Weight * w0 = &c->weights[uint64_t(cmds[size_t(i0) * GEMVQ_CMD_WORDS + 4]) |
@@ -871,6 +1037,8 @@ gemvq_ctx * gemvq_ctx_create(int device, size_t act_floats, size_t weight_bytes,
     if (e == hipSuccess && weight_bytes) e = hipMalloc(&c->warena, weight_bytes);
     if (e == hipSuccess && state_rows) e = hipMalloc(&c->state, state_rows * 128 * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&c->gdn_raw, size_t(GDN_MAX_HEADS) * 128 * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&c->dsnap, size_t(GEMV_MAXK) * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&c->xsnap, size_t(GEMV_MAXK) * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&c->gemm_q, size_t(GEMM_MAX_TOK) * GEMV_MAXK);
     if (e == hipSuccess) e = hipMalloc(&c->gemm_d, size_t(GEMM_MAX_TOK) * (GEMV_MAXK / 32) * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&c->gemm_s, size_t(GEMM_MAX_TOK) * (GEMV_MAXK / 32) * sizeof(float));
@@ -905,6 +1073,8 @@ void gemvq_ctx_destroy(gemvq_ctx * c) {
     hipFree(c->warena);
     hipFree(c->state);
     hipFree(c->gdn_raw);
+    hipFree(c->dsnap);
+    hipFree(c->xsnap);
     hipFree(c->gemm_q);
     hipFree(c->gemm_d);
     hipFree(c->gemm_s);
@@ -1055,7 +1225,8 @@ int gemvq_kv_clear(gemvq_ctx * c) {
         const size_t kvn = size_t(b.n_ctx) * b.n_head_kv * b.head_dim;
         if (e == hipSuccess) e = hipMemsetAsync(b.k, 0, kvn * 2, c->stream);
         if (e == hipSuccess) e = hipMemsetAsync(b.v, 0, kvn * 2, c->stream);
-        if (e == hipSuccess) e = hipMemsetAsync(b.counter, 0, size_t(b.n_head_kv) * ATTN_MAXG * 4, c->stream);
+        const size_t heads = size_t(ATTN_MAXG) * b.n_head_kv * GEMM_MAX_TOK;  // every (token, q head) set, as created
+        if (e == hipSuccess) e = hipMemsetAsync(b.counter, 0, heads * 4, c->stream);
     }
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     return e == hipSuccess ? 0 : fail(c, e, "kv clear");
