@@ -202,6 +202,20 @@ typedef struct {
 int gemvq_profile(gemvq_ctx * ctx, const uint32_t * cmds, unsigned n_cmds, int reps, gemvq_launch_stat * out,
                   int max_out);
 
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under hipGraph capture,
+ * serving loops, harnesses that forbid hipMalloc). The batched GEMV of the GEMM command (plain epilog) on
+ * caller-owned device memory, allocating nothing: y[t * y_stride + r] = row r of the matrix times token row t of x
+ * (at x + t * x_stride), bit for bit what a GEMM command computes. w: the matrix in the device layout of
+ * gemvq_repack (type 2 Q4_0, 3 Q4_1 or 8 Q8_0; rows x cols, cols a multiple of 512 up to GEMVQ_MAX_COLS),
+ * 256-byte aligned; x and y 64-byte aligned, strides multiples of 16 floats; 1 <= n_tok <= GEMVQ_GEMM_MAX_TOK.
+ * Runs on the current device, asynchronously on `stream` (a hipStream_t; NULL for the null stream). The quantized
+ * activation rows are staged in a fixed device array of GEMVQ_STATIC_SCRATCH_BYTES per device, held until the
+ * process ends, so calls that overlap on one device race. Returns 0, GEMVQ_EINVAL (nothing launched: a size beyond
+ * the limits, a misaligned or NULL pointer) or a negated HIP error. */
+#define GEMVQ_STATIC_SCRATCH_BYTES 655360u
+int gemvq_gemm_static(int type, int rows, int cols, const void * w, const float * x, int n_tok, int x_stride,
+                      float * y, int y_stride, void * stream);
+
 #ifdef __cplusplus
 }
 #endif
