@@ -76,13 +76,16 @@ __device__ float block_norm_scale(const float * x, int n, float eps, int l2, Lds
 // consecutive floats; the two halves of a 32-block sit in adjacent lanes). The loads are issued by prologue_fetch
 // before the first weight rows are requested, so they are not queued behind them; prologue_finish then folds the
 // deferred norm or the gated output norm and quantizes into LDS.
-template <int R, bool GATED>  // rounds of NT items the registers hold (cols <= 16 NT R); the gated output norm
+template <int R, int XS>  // rounds of NT items the registers hold (cols <= 16 NT R); the prologue kind
 struct XF {
     float v[R][16];
-    float w[R <= 2 ? R : 1][16];  // NORM: the norm weight (the activation again without one); GATED: the gated norm's
-                                  // weight (one head, item % 8)
-    float z[GATED ? R : 1][16];   // GATED: the output gate
+    float w[R <= 2 ? R : 1][16];  // NORM, ACC: the norm weight (the activation again without one); GATED: the gated
+                                  // norm's weight (one head, item % 8)
+    float z[XS == XS_GATED ? R : 1][16];  // GATED: the output gate
+    unsigned long long acc[XS == XS_ACC ? R : 1][16];  // ACC: the fused ssm_out's row sums (v holds its residual)
 };
+
+typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ void load16(const float * p, float * v) {
     const float4 * q = reinterpret_cast<const float4 *>(p);
@@ -104,16 +107,25 @@ __device__ __forceinline__ int item_of(int g, int n16) {
 
 // Every load is unconditional (an operand a source does not use is read from the activation itself), so the loads
 // cannot be moved into the branches that use them, behind the weight loads.
-template <int R, bool GATED>
-__device__ __forceinline__ void prologue_fetch(const GemvArgs & a, XF<R, GATED> & f) {
+template <int R, int XS>
+__device__ __forceinline__ void prologue_fetch(const GemvArgs & a, XF<R, XS> & f) {
     const int n16 = a.cols / 16;
-    const bool normw = a.xsrc == XSRC_NORM && a.norm_w != nullptr;
+    const bool normw = (a.xsrc == XSRC_NORM || a.xsrc == XSRC_ACC) && a.norm_w != nullptr;
 #pragma unroll
     for (int g = 0; g < R; ++g) {
         const int i = item_of(g, n16);
-        const float * xi = a.x + size_t(i) * 16;
+        const float * xi = (XS == XS_ACC ? a.acc_res : a.x) + size_t(i) * 16;
         load16(xi, f.v[g]);
-        if constexpr (GATED) {
+        if constexpr (XS == XS_ACC) {
+            const u64x2 * ap = reinterpret_cast<const u64x2 *>(a.acc + size_t(i) * 16);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const u64x2 t = ap[j];
+                f.acc[g][2 * j] = t.x;
+                f.acc[g][2 * j + 1] = t.y;
+            }
+        }
+        if constexpr (XS == XS_GATED) {
             load16(a.gate_z + size_t(i) * 16, f.z[g]);
             load16(a.norm_w + size_t(i & 7) * 16, f.w[g]);
         } else if constexpr (R <= 2) {
@@ -166,8 +178,8 @@ __device__ __forceinline__ void quantize_half(const float * v, int item, bool va
 
 // Norm scale over the whole vector: tree over each item's 16 squares, pairwise over the 64 items of a wave, the 4
 // waves of a round and the rounds (padded to a power of two with zeros): the canonical pairwise tree over n.
-template <int R, bool GATED>
-__device__ __forceinline__ float norm_scale_items(const GemvArgs & a, const XF<R, GATED> & f, Lds & s) {
+template <int R, int XS>
+__device__ __forceinline__ float norm_scale_items(const GemvArgs & a, const XF<R, XS> & f, Lds & s) {
     const int n16 = a.cols / 16, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float r[R];
 #pragma unroll
@@ -193,10 +205,26 @@ __device__ __forceinline__ float norm_scale_items(const GemvArgs & a, const XF<R
 
 // Without the gated norm the three sources share one path: v = (x * scale) * w with scale and w exactly 1 where a
 // source has no norm or no weight (x * 1 is x), so no branch separates the loads.
-template <int R, bool GATED>
-__device__ __forceinline__ void prologue_finish(const GemvArgs & a, XF<R, GATED> & f, Lds & s) {
+template <int R, int XS>
+__device__ __forceinline__ void prologue_finish(const GemvArgs & a, XF<R, XS> & f, Lds & s) {
     const int n16 = a.cols / 16;
-    if constexpr (GATED) {
+    if constexpr (XS == XS_ACC) {
+        // the fused ssm_out's output, exactly as its ADD epilog forms it (the row rounded to FP32 once, then the
+        // residual added), stored by workgroup 0 (the ssm_out command's y); then the deferred norm as below
+#pragma unroll
+        for (int g = 0; g < R; ++g) {
+            float * v = f.v[g];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = fixed_to_float((long long)f.acc[g][j]) + v[j];
+            const int i = int(threadIdx.x) + NT * g;
+            if (blockIdx.x == 0 && i < n16) {
+                float4 * o = reinterpret_cast<float4 *>(a.x_out + size_t(i) * 16);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) o[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+            }
+        }
+    }
+    if constexpr (XS == XS_GATED) {
         // the DeltaNet gated output norm (gemvqc_gdn.h:284-346): per head of 128 (8 items, 8 lanes), x =
         // silu(z) * ((y * sc) * w) with sc = 1 / sqrt(sum(y^2) / 128 + eps); workgroup 0 also stores x, which the
         // separate norm would have written
@@ -229,8 +257,8 @@ __device__ __forceinline__ void prologue_finish(const GemvArgs & a, XF<R, GATED>
             quantize_half(v, i, i < n16, s);
         }
     } else {
-        const bool norm = a.xsrc == XSRC_NORM, normw = norm && a.norm_w != nullptr;
-        const float sc = norm ? norm_scale_items<R, GATED>(a, f, s) : 1.0f;  // the same on every thread
+        const bool norm = a.xsrc == XSRC_NORM || a.xsrc == XSRC_ACC, normw = norm && a.norm_w != nullptr;
+        const float sc = norm ? norm_scale_items<R, XS>(a, f, s) : 1.0f;  // the same on every thread
 #pragma unroll
         for (int g = 0; g < R; ++g) {
             const int i = int(threadIdx.x) + NT * g;
@@ -766,7 +794,7 @@ __device__ __forceinline__ void run_rows(const GemvArgs & a, const GemvMember & 
 
 // Waves are assigned to members in order: member i owns the global waves wave_begin .. wave_begin + waves - 1;
 // waves past the last member only take part in the prologue.
-template <int TYPE, int NU, bool PAIR, bool GATED, int DS>
+template <int TYPE, int NU, bool PAIR, int XS, int DS>
 __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
     __shared__ Lds s;
     constexpr bool KQ = TYPE == T_Q5_K || TYPE == T_Q6_K;
@@ -790,8 +818,15 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
     const int wv = lw - m.wave_begin, S = m.waves;                  // rows s_lo + wv, s_lo + wv + S, ... of the slice
     const int n = wv < S && wv < len ? (len - 1 - wv) / S + 1 : 0;  // waves past the last member have none
     const int w = s_lo + wv;
-    XF<RX, GATED> xf;
-    if constexpr (!KQ) prologue_fetch<RX, GATED>(a, xf);  // the activation is requested first
+    XF<RX, XS> xf;
+    // ACC: the fused step's new state rows, copied from the shadow rows into the state (one float4 per thread of
+    // the grid in turn); the first is requested with the activation and stored once the prologue is done
+    const int cp_i = int(blockIdx.x) * NT + int(threadIdx.x), cp_s = int(gridDim.x) * NT;
+    float4 cp_v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if constexpr (XS == XS_ACC) {
+        if (cp_i < a.cp_n) cp_v = a.cp_src[cp_i];
+    }
+    if constexpr (!KQ) prologue_fetch<RX, XS>(a, xf);  // the activation is requested first
     __builtin_amdgcn_sched_barrier(0);                    // and stays ahead of the weight loads
     Slot<TYPE, NU, PAIR> sl[DS];  // the first D rows (a wave without rows reloads the member's last row)
 #pragma unroll
@@ -801,7 +836,11 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
         const float scale = a.xsrc == XSRC_NORM ? block_norm_scale(a.x, a.cols, a.norm_eps, a.norm_l2, s) : 1.0f;
         quantize_q8_K(a, scale, s);
     } else {
-        prologue_finish<RX, GATED>(a, xf, s);
+        prologue_finish<RX, XS>(a, xf, s);
+    }
+    if constexpr (XS == XS_ACC) {
+        if (cp_i < a.cp_n) a.cp_dst[cp_i] = cp_v;
+        for (int i = cp_i + cp_s; i < a.cp_n; i += cp_s) a.cp_dst[i] = a.cp_src[i];
     }
     __syncthreads();
     XB xb[KQ ? 1 : NU];
@@ -903,20 +942,20 @@ void epilog_operands(GemvMember & m) {
     if (m.epi != EPI_SWIGLU) m.w2 = m.w;
 }
 
-template <int TYPE, int NU, bool PAIR, bool GATED, int DS>
+template <int TYPE, int NU, bool PAIR, int XS, int DS>
 hipError_t launch_typed(const GemvArgs & a0, hipStream_t st) {
-    static const int cap = resident_blocks(gemv_kernel<TYPE, NU, PAIR, GATED, DS>, GEMV_WG_PER_CU);
+    static const int cap = resident_blocks(gemv_kernel<TYPE, NU, PAIR, XS, DS>, GEMV_WG_PER_CU);
     GemvArgs a = a0;
     for (int i = 0; i < a.n_members; ++i) epilog_operands(a.m[i]);
     const int grid = plan_waves(a, cap, DS);
-    GQ_LAUNCH((gemv_kernel<TYPE, NU, PAIR, GATED, DS>), dim3(grid), dim3(NT), 0, st, a);
+    GQ_LAUNCH((gemv_kernel<TYPE, NU, PAIR, XS, DS>), dim3(grid), dim3(NT), 0, st, a);
     return hipGetLastError();
 }
 
 // Rows in flight per wave. A group that all fits in flight at once takes the most slots (its time is latency); a
 // larger one takes as few as keep about 16 MB in flight over the resident waves (more in flight than that only
 // queues, and streams slower).
-template <int TYPE, int NU, bool PAIR, bool GATED>
+template <int TYPE, int NU, bool PAIR, int XS>
 hipError_t launch_slots(const GemvArgs & a, hipStream_t st) {
     constexpr int DMAX = slots<TYPE, NU, PAIR>();
     uint64_t rows = 0, bytes = 0;
@@ -924,32 +963,38 @@ hipError_t launch_slots(const GemvArgs & a, hipStream_t st) {
         rows += uint64_t(a.m[i].rows);
         bytes += uint64_t(a.m[i].rows) * gguf_row_bytes(TYPE, a.cols) * (a.m[i].epi == EPI_SWIGLU ? 2 : 1);
     }
-    static const int cap_waves = resident_blocks(gemv_kernel<TYPE, NU, PAIR, GATED, DMAX>) * NWAVES;
+    static const int cap_waves = resident_blocks(gemv_kernel<TYPE, NU, PAIR, XS, DMAX>) * NWAVES;
     const uint64_t per_slot = uint64_t(cap_waves) * (bytes / (rows ? rows : 1));  // bytes in flight per slot
     constexpr uint64_t target = uint64_t(16) << 20;
     int d = DMAX;
     if (bytes > target && per_slot * DMAX > target) d = per_slot * 2 <= target ? 2 : 1;
     if constexpr (DMAX > 2) {
-        if (d == DMAX) return launch_typed<TYPE, NU, PAIR, GATED, DMAX>(a, st);
+        if (d == DMAX) return launch_typed<TYPE, NU, PAIR, XS, DMAX>(a, st);
     }
     if constexpr (DMAX >= 2) {
-        if (d >= 2) return launch_typed<TYPE, NU, PAIR, GATED, 2>(a, st);
+        if (d >= 2) return launch_typed<TYPE, NU, PAIR, XS, 2>(a, st);
     }
-    return launch_typed<TYPE, NU, PAIR, GATED, 1>(a, st);
+    return launch_typed<TYPE, NU, PAIR, XS, 1>(a, st);
 }
 
-// The gated activation prologue exists for Q4_0 / Q8_0 rows of at most 8192 columns without a SwiGLU pair.
+// The gated activation prologue exists for Q4_0 / Q8_0 rows of at most 8192 columns without a SwiGLU pair; the
+// accumulator prologue for Q4_0 / Q8_0 rows of at most 4096 columns.
 template <int TYPE, int NU>
 hipError_t launch_pair(const GemvArgs & a, hipStream_t st) {
     bool pair = false;
     for (int i = 0; i < a.n_members; ++i) pair = pair || a.m[i].epi == EPI_SWIGLU;
     if (a.xsrc == XSRC_GATED) {
         if constexpr ((TYPE == T_Q4_0 || TYPE == T_Q8_0) && NU <= 4) {
-            if (!pair) return launch_slots<TYPE, NU, false, true>(a, st);
+            if (!pair) return launch_slots<TYPE, NU, false, XS_GATED>(a, st);
         }
         return hipErrorInvalidValue;
     }
-    return pair ? launch_slots<TYPE, NU, true, false>(a, st) : launch_slots<TYPE, NU, false, false>(a, st);
+    if (a.xsrc == XSRC_ACC) {
+        if constexpr ((TYPE == T_Q4_0 || TYPE == T_Q8_0) && NU <= 2)
+            return pair ? launch_slots<TYPE, NU, true, XS_ACC>(a, st) : launch_slots<TYPE, NU, false, XS_ACC>(a, st);
+        return hipErrorInvalidValue;
+    }
+    return pair ? launch_slots<TYPE, NU, true, XS_PLAIN>(a, st) : launch_slots<TYPE, NU, false, XS_PLAIN>(a, st);
 }
 
 template <int TYPE>

@@ -23,7 +23,12 @@ struct WeightView {
 };
 
 enum : int { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_ADD = 2, EPI_CONV = 3, EPI_SILU = 4 };
-enum : int { XSRC_RAW = 0, XSRC_NORM = 1, XSRC_GATED = 2 };  // XSRC_GATED: gate_silu says whether z is silu(z)
+// XSRC_GATED: gate_silu says whether z is silu(z). XSRC_ACC: the activation is the deferred norm of
+// fixed_to_float(acc) + acc_res (a fused DeltaNet step + ssm_out left its exact row sums in acc); workgroup 0 also
+// stores that sum to x_out (the ssm_out command's residual-added output).
+enum : int { XSRC_RAW = 0, XSRC_NORM = 1, XSRC_GATED = 2, XSRC_ACC = 3 };
+// Prologue kinds of the GEMV kernel instances.
+enum : int { XS_PLAIN = 0, XS_GATED = 1, XS_ACC = 2 };
 
 struct GemvMember {
     WeightView w;    // matrix (g of a SwiGLU pair)
@@ -52,6 +57,11 @@ struct GemvArgs {
     const float * gate_z;     // XSRC_GATED: z (the output gate) [cols]
     float * x_out;            // XSRC_GATED: the gated activation is also written here (by workgroup 0)
     int gate_silu;            // XSRC_GATED: gate_z holds silu(z) already
+    const unsigned long long * acc;  // XSRC_ACC: fixed-point row sums (LSB 2^-40) of the fused ssm_out
+    const float * acc_res;           // XSRC_ACC: its residual
+    const float4 * cp_src;           // XSRC_ACC: the state rows the fused step left in the shadow rows, copied back
+    float4 * cp_dst;                 // into the state rows by the launch's threads (cp_n float4s; 0: none)
+    int cp_n;
     int norm_l2;
     int cols;
     int n_members;
@@ -118,6 +128,28 @@ struct GdnArgs {
     int flags;
     int n_tok;             // tokens run in order on the same state
     int s_qkv, s_gb, s_y;  // row strides (floats) between tokens of q / k / v, of g / beta, of y
+};
+
+// The DeltaNet step, its gated output norm and the ssm_out product in one launch (the reference's GDN_WITH_OUT,
+// gemvqc16.h:75-81, gemvqc16.cpp:872-903): `parts` workgroups per value head each run the head's step, normalize and
+// gate its 128 outputs, quantize them to Q8_0 and multiply them with their share of the rows of the head's 128
+// columns of ssm_out; each row's exact fixed-point terms are added into acc with integer atomics (order-free, so the
+// sums are those of one GEMV). Every workgroup of a head reads all of the head's state rows, so a workgroup stores
+// its 128 / parts rows of the new state to `shadow` (the dst layout); when shadow is the state itself (src != dst)
+// nothing more is needed, else the launch that consumes acc copies the shadow rows into dst.
+struct GdnOutArgs {
+    GdnArgs g;                  // one token; g.y is not used
+    const float * z;            // the output gate (silu(z) when z_silu)
+    const float * nw;           // the gated norm's weight [128]
+    float rms_eps;
+    int z_silu;
+    float * y;                  // the gated output [hv * 128] (the GDN command's y)
+    WeightView w;               // ssm_out, rows x (hv * 128), Q4_0 or Q8_0
+    int rows;
+    unsigned long long * acc;   // [rows], zero on entry
+    unsigned long long * zero;  // the other accumulator [rows], cleared for the next fused pair
+    float * shadow;             // where the new state rows go (dst, or a buffer of hv * 128 rows when src == dst)
+    int parts;                  // workgroups per head: a divisor of 128, rows / parts <= 1024
 };
 
 struct GatedNormArgs {    // per head of 128: y = silu(z) * ((y * s) * w), s = 1 / sqrt(mean(y^2) + eps)
@@ -234,6 +266,8 @@ hipError_t launch_conv(const ConvArgs & a, hipStream_t s);
 hipError_t launch_rope(const RopeArgs & a, hipStream_t s);
 hipError_t launch_gdn(const GdnArgs & a, hipStream_t s);
 hipError_t launch_gated_norm(const GatedNormArgs & a, hipStream_t s);
+hipError_t launch_gdn_out(const GdnOutArgs & a, int type, hipStream_t s);
+int gdn_out_parts(int rows);  // workgroups per head for an ssm_out of `rows` rows
 hipError_t launch_attn(const AttnArgs & a, hipStream_t s);
 hipError_t launch_get_rows(const GetRowsArgs & a, hipStream_t s);
 hipError_t launch_argmax(const float * x, int n, unsigned long long * key, hipStream_t s);

@@ -2,6 +2,7 @@
 // DeltaNet step, its gated output norm, the attention core, embedding rows, argmax and the greedy token step.
 // Reductions follow the pairwise tree over element indices; see gq_device.h for the scalar arithmetic.
 #include "gq_device.h"
+#include "gq_gdn.h"
 #include "gq_kernels.h"
 
 namespace gq {
@@ -146,62 +147,20 @@ __device__ __forceinline__ void gdn_load(const GdnArgs & a, int tk, int h, int k
 // One token on the state rows x (gemvq_ref.h:360-397): decay, delta rule, output row dot.
 __device__ __forceinline__ void gdn_token(const GdnArgs & a, const GdnIn & in, int tk, int h, int chunk, int l16, int grp,
                                           float dtv, float av, float (&x)[GDN_IT][8]) {
-    constexpr int IT = GDN_IT;
     float q[8], k[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         q[i] = in.q[i];
         k[i] = in.k[i];
     }
-    if (a.flags & 2) {  // L2 norm of q and k per key head (ggml_l2_norm)
-        float sq[8], sk[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            sq[i] = q[i] * q[i];
-            sk[i] = k[i] * k[i];
-        }
-        const float tq = pair_sum_lanes<16>(tree<8>(sq)), tkk = pair_sum_lanes<16>(tree<8>(sk));
-        const float fq = 1.0f / fmaxf(sqrtf(tq), a.l2_eps), fk = 1.0f / fmaxf(sqrtf(tkk), a.l2_eps);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            q[i] = q[i] * fq;
-            k[i] = k[i] * fk;
-        }
-    }
-    float gv = in.g, bt = in.b;
-    if (a.flags & 8) {  // gates from the raw projections: beta = sigmoid(b), g = softplus(a_raw + dt) * a
-        gv = softplus_(in.g + dtv) * av;
-        bt = sigmoid_(in.b);
-    }
-    const float decay = expf_(gv);
-    float dot[IT];
-#pragma unroll
-    for (int it = 0; it < IT; ++it) {
-        float pr[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            x[it][i] = x[it][i] * decay;
-            pr[i] = x[it][i] * k[i];
-        }
-        dot[it] = tree<8>(pr);
-    }
-    pair_sum_lanes_n<16, IT>(dot);
-    float out[IT];
-#pragma unroll
-    for (int it = 0; it < IT; ++it) {
-        const float delta = (in.v[it] - dot[it]) * bt;
-        float pr[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            x[it][i] = x[it][i] + k[i] * delta;
-            pr[i] = x[it][i] * q[i];
-        }
-        out[it] = tree<8>(pr);
-    }
-    pair_sum_lanes_n<16, IT>(out);
+    if (a.flags & 2) gdn_l2_qk(q, k, a.l2_eps);  // L2 norm of q and k per key head (ggml_l2_norm)
+    float bt;
+    const float decay = gdn_gates(a.flags & 8, in.g, in.b, dtv, av, bt);
+    float out[GDN_IT];
+    gdn_step_rows<GDN_IT>(q, k, in.v, decay, bt, x, out);
     if (l16 == 0) {
 #pragma unroll
-        for (int it = 0; it < IT; ++it) a.y[size_t(tk) * a.s_y + h * 128 + chunk * GDN_ROWS + it * 8 + grp] = out[it] * a.scale;
+        for (int it = 0; it < GDN_IT; ++it) a.y[size_t(tk) * a.s_y + h * 128 + chunk * GDN_ROWS + it * 8 + grp] = out[it] * a.scale;
     }
 }
 

@@ -42,6 +42,7 @@ struct LEw { EwArgs a; };
 struct LConv { ConvArgs a; };
 struct LRope { RopeArgs a; };
 struct LGdn { GdnArgs a; };
+struct LGdnOut { GdnOutArgs a; int type; };
 struct LGated { GatedNormArgs a; };
 struct LAttn { AttnArgs a; };
 struct LRows { GetRowsArgs a; };
@@ -49,7 +50,8 @@ struct LArgmax { const float * x; int n; unsigned long long * key; };
 struct LNext { NextTokenArgs a; };
 struct LGemmQ { GemmQuantArgs a; };
 struct LGemm { GemmArgs a; int type; };
-using Launch = std::variant<LGemv, LNorm, LEw, LConv, LRope, LGdn, LGated, LAttn, LRows, LArgmax, LNext, LGemmQ, LGemm>;
+using Launch = std::variant<LGemv, LNorm, LEw, LConv, LRope, LGdn, LGated, LAttn, LRows, LArgmax, LNext, LGemmQ, LGemm,
+                            LGdnOut>;
 
 }  // namespace
 
@@ -73,6 +75,8 @@ struct gemvq_ctx {
     float * gdn_raw = nullptr;    // raw DeltaNet output when its gated norm is folded into the next GEMV
     float * dsnap = nullptr;      // a deferred norm's row, computed before a command overwrote its source
     float * xsnap = nullptr;      // a GEMV group's activation, copied before a member overwrites it
+    unsigned long long * acc[2] = {nullptr, nullptr};  // fused DeltaNet step + ssm_out row sums, used in turn
+    float * gdn_shadow = nullptr;  // the fused step's new state rows of an in-place step (GDN_MAX_HEADS * 128 rows)
     int8_t * gemm_q = nullptr;    // a batched GEMV's quantized activation rows (GEMM_MAX_TOK x GEMV_MAXK)
     float * gemm_d = nullptr;     // and their block scales
     float * gemm_s = nullptr;     // and their Q8_1 block sums (for Q4_1 weights)
@@ -320,9 +324,62 @@ struct Compiler {
     // (written by workgroup 0 of that group), computed from the raw step output (a private buffer), z and w.
     struct Gated { bool on = false; uint32_t y, cols; const float * z; const float * w; float eps; int z_silu; } gated;
 
+    std::vector<Rng> acc_ranges() const {  // what the accumulator prologue reads and writes in the act buffer
+        std::vector<Rng> r = {{accp.y, uint64_t(accp.y) + accp.rows}, {accp.res, uint64_t(accp.res) + accp.rows}};
+        if (defer.on && !(defer.flags & GEMVQ_NORM_NO_WEIGHT)) r.push_back({defer.w, uint64_t(defer.w) + defer.n});
+        return r;
+    }
+
     std::vector<Rng> gated_ranges() const {
         const uint64_t z = uint64_t(gated.z - c->act), w = uint64_t(gated.w - c->act);
         return {{gated.y, gated.y + uint64_t(gated.cols)}, {z, z + gated.cols}, {w, w + 128}};
+    }
+
+    // The fused DeltaNet step + ssm_out pending for the GEMV group whose prologue forms the ssm_out output: y =
+    // fixed_to_float(acc) + res, the deferred norm of y being that group's activation.
+    struct AccOut {
+        bool on = false;
+        uint32_t y, res, rows;
+        unsigned long long * acc;
+        const float * cp_src;  // the shadow rows of an in-place step, copied into cp_dst by the consuming launch
+        float * cp_dst;
+        int cp_n;              // float4s (0: the step wrote its state rows itself)
+    } accp;
+    int accn = 0;        // fused pairs so far: pair j accumulates into acc[j % 2] and clears the other
+    uint32_t acc_rows = 0;
+
+    // The DeltaNet layer shape the fused step + ssm_out serves (the reference's GDN_WITH_OUT, gemvqc16.cpp:872-903):
+    // the one-token GDN with the gated norm whose next command `next` is a Q4_0 / Q8_0 GEMV on its whole output
+    // with the ADD epilog into y apart from the residual (rows at most 4096 that the fused kernel splits into whole
+    // rounds: a multiple of 1024), followed by a deferred RMSNORM of y and a GEMV on that norm whose pass neither
+    // writes nor reads y, the residual or the norm weight.
+    // Then nothing between the GDN and that GEMV reads y, which that GEMV's prologue forms.
+    bool fuse_out(const uint32_t * cmds, unsigned n, unsigned next, uint32_t gy, uint32_t cols, uint32_t & y,
+                  uint32_t & res) const {
+        if (next + 3 >= n) return false;
+        const uint32_t * g = cmds + size_t(next) * GEMVQ_CMD_WORDS, * e = g + GEMVQ_CMD_WORDS;
+        const uint32_t * r = e + GEMVQ_CMD_WORDS, * u = r + GEMVQ_CMD_WORDS;
+        const int t = int(g[1] & 0xffu);
+        const uint32_t rows = g[2];
+        const uint64_t woff = uint64_t(g[4]) | (uint64_t(g[5]) << 32);
+        if (g[0] != GEMVQ_OP_GEMV || (g[1] & ~0xffu) != GEMVQ_GEMV_ADD || (t != T_Q4_0 && t != T_Q8_0) || g[6] != gy ||
+            g[3] != cols || rows > 4096 || gdn_out_parts(int(rows)) == 0 || !weight(woff, t, int(rows), int(cols)))
+            return false;
+        if (e[0] != GEMVQ_OP_ADD || e[1] != rows || (e[2] != g[7] && e[3] != g[7])) return false;
+        res = e[2] == g[7] ? e[3] : e[2];
+        y = e[4];
+        if (!range(res, rows) || !range(y, rows) || meet({y, uint64_t(y) + rows}, {res, uint64_t(res) + rows})) return false;
+        const uint32_t nf = r[7];
+        if (r[0] != GEMVQ_OP_RMSNORM || !(nf & GEMVQ_NORM_DEFER) || (nf & GEMVQ_NORM_L2) || r[6] > 1 || ((nf >> 8) & 0xffffu) ||
+            r[1] != rows || r[2] != y || (!(nf & GEMVQ_NORM_NO_WEIGHT) && !range(r[3], rows)))
+            return false;
+        const int tu = int(u[1] & 0xffu);
+        if (u[0] != GEMVQ_OP_GEMV || u[6] != r[4] || u[3] != rows || (tu != T_Q4_0 && tu != T_Q8_0)) return false;
+        std::vector<Rng> wr, rd;
+        gemv_io(cmds, n, next + 3, wr, rd);
+        std::vector<Rng> pro = {{y, uint64_t(y) + rows}, {res, uint64_t(res) + rows}};
+        if (!(nf & GEMVQ_NORM_NO_WEIGHT)) pro.push_back({r[3], uint64_t(r[3]) + rows});
+        return !meet_any(wr, pro) && !meet_any(rd, pro);
     }
 
     // The command at `next` is a Q4_0 / Q8_0 GEMV that reads exactly the GDN output y (cols = heads * 128 <= 8192)
@@ -378,6 +435,12 @@ struct Compiler {
                 cmd_writes(cmds, n, at, i - at, wr);
                 if (meet_any(wr, defer_ranges())) defer.dirty = long(before);
             }
+        }
+        if (accp.on) return reject(n - 1, "internal: a fused DeltaNet output was not consumed");
+        if (accn % 2) {  // the last fused pair used acc[0]: clear it for the next run of the list (acc[1] is clear)
+            EwArgs z{nullptr, nullptr, reinterpret_cast<float *>(c->acc[0]), int(2 * acc_rows), 0, 0, EW_FILL, 0.0f};
+            out.push_back(LEw{z});
+            spans.push_back({int(n) - 1, 1});
         }
         return true;
     }
@@ -504,6 +567,37 @@ struct Compiler {
                 a.s_gb = int(sg);
                 a.s_y = int(hv * 128);
                 const unsigned next = i + (gates ? 3 : 2);
+                uint32_t fy = 0, fres = 0;
+                if ((flags & GEMVQ_GDN_GATED) && (flags & GEMVQ_GDN_WITH_OUT) && ntok == 1 && !accp.on &&
+                    fuse_out(cmds, n, next, k[7], hv * 128, fy, fres)) {
+                    // asked for with GEMVQ_GDN_WITH_OUT: the step, the gated norm and ssm_out in one launch; the GEMV
+                    // group on the norm that follows forms the ssm_out output from the accumulated row sums
+                    const uint32_t * g = cmds + size_t(next) * GEMVQ_CMD_WORDS;
+                    const int t = int(g[1] & 0xffu);
+                    GdnOutArgs o{};
+                    o.g = a;
+                    o.z = A(k2[7]);
+                    o.nw = A(k2[6]);
+                    o.rms_eps = bits_f(k2[5]);
+                    o.z_silu = int(bool(flags & GEMVQ_GDN_Z_SILU));
+                    o.y = A(k[7]);
+                    o.rows = int(g[2]);
+                    o.w = weight_view(c->warena + (uint64_t(g[4]) | (uint64_t(g[5]) << 32)), t, o.rows, int(hv * 128));
+                    o.acc = c->acc[accn % 2];
+                    o.zero = c->acc[(accn + 1) % 2];
+                    // every workgroup of a head reads all its state rows: an in-place step writes the new rows
+                    // to the shadow rows, which the consuming launch copies into the state
+                    const bool in_place = src == dst;
+                    o.shadow = in_place ? c->gdn_shadow : a.dst;
+                    o.parts = gdn_out_parts(o.rows);
+                    out.push_back(LGdnOut{o, t});
+                    spans.push_back({int(i), int(next + 2 - i)});
+                    accp = {true, fy, fres, g[2], o.acc, c->gdn_shadow, a.dst, in_place ? int(hv * 128 * 32) : 0};
+                    ++accn;
+                    acc_rows = std::max(acc_rows, g[2]);
+                    i = next + 2;
+                    return true;
+                }
                 if ((flags & GEMVQ_GDN_GATED) && ntok == 1 && fold_gated(cmds, n, next, k[7], hv * 128, k2[7], k2[6])) {
                     // the gated norm runs in the next GEMV's activation prologue: the step writes its raw output
                     // to scratch, and that GEMV writes the gated values to y as the norm would have
@@ -808,6 +902,7 @@ struct Compiler {
             // workgroup 0 writes the gated activation while the group runs, from z and the norm weight: no member
             // may write or read those
             if (gated.on && gemvs > 0 && (meet_any(mw, gated_ranges()) || meet_any(mr, gated_ranges()))) break;
+            if (accp.on && gemvs > 0 && (meet_any(mw, acc_ranges()) || meet_any(mr, acc_ranges()))) break;
             if (gated.on && (flags & GEMVQ_GEMV_SWIGLU)) break;
             if (gemvs == 0) {
                 type = t;
@@ -889,6 +984,21 @@ struct Compiler {
             a.x_out = A(gated.y);
             a.gate_silu = gated.z_silu;
             gated.on = false;
+        } else if (accp.on && defer.on && !defer.snap && defer.x == accp.y && defer.y == x_off && defer.n == cols) {
+            // the fused DeltaNet step + ssm_out left its row sums in acc: this prologue forms y = acc + res (stored
+            // by workgroup 0) and quantizes its deferred norm
+            a.xsrc = XSRC_ACC;
+            a.x = A(accp.res);
+            a.acc = accp.acc;
+            a.acc_res = A(accp.res);
+            a.x_out = A(accp.y);
+            a.cp_src = reinterpret_cast<const float4 *>(accp.cp_src);
+            a.cp_dst = reinterpret_cast<float4 *>(accp.cp_dst);
+            a.cp_n = accp.cp_n;
+            a.norm_w = (defer.flags & GEMVQ_NORM_NO_WEIGHT) ? nullptr : A(defer.w);
+            a.norm_eps = defer.eps;
+            a.norm_l2 = 0;
+            accp.on = false;
         } else if (defer.on && defer.y == x_off && defer.n == cols) {
             // every workgroup reads the norm's row and weight in its prologue while others store rows: with a member
             // writing over them, or after an earlier command did, the launch reads the snapshot instead
@@ -935,6 +1045,8 @@ std::pair<std::string, uint64_t> describe(const Launch & l, int pos) {
         const bool kq = g->type == T_Q5_K || g->type == T_Q6_K;
         const int nu = (a.cols / (kq ? 64 : 32) + 63) / 64;
         uint64_t b = uint64_t(a.cols) * 4 * (a.xsrc == XSRC_GATED ? 3 : a.xsrc == XSRC_NORM && a.norm_w ? 2 : 1);
+        if (a.xsrc == XSRC_ACC)  // acc, residual, y, weight; the shadow state rows read and written
+            b = uint64_t(a.cols) * (8 + 4 + 4 + (a.norm_w ? 4 : 0)) + uint64_t(a.cp_n) * 32;
         for (int i = 0; i < a.n_members; ++i) {
             const GemvMember & m = a.m[i];
             const uint64_t rows = uint64_t(m.rows);
@@ -956,6 +1068,13 @@ std::pair<std::string, uint64_t> describe(const Launch & l, int pos) {
         return {"gdn_kernel", 2 * hv * 128 * 128 * 4 + ((2 * hk + 2 * hv) * 128 * 4 + hv * 16) * uint64_t(x->a.n_tok)};
     }
     if (auto * x = std::get_if<LGated>(&l)) return {"gated_norm_kernel", uint64_t(x->a.heads) * 128 * 12 + 512};
+    if (auto * x = std::get_if<LGdnOut>(&l)) {
+        const GdnOutArgs & o = x->a;
+        const uint64_t hv = uint64_t(o.g.hv), hk = uint64_t(o.g.hk), rows = uint64_t(o.rows);
+        const uint64_t state = 2 * hv * 128 * 128 * 4, vec = (2 * hk + 3 * hv) * 128 * 4 + 512 + hv * 16;
+        return {"gdn_out_kernel<" + std::to_string(x->type) + ">",
+                state + vec + rows * gguf_row_bytes(x->type, int(hv * 128)) + rows * 8};
+    }
     if (auto * x = std::get_if<LAttn>(&l)) {
         const AttnArgs & a = x->a;
         const uint64_t nt = uint64_t(a.n_tok > 1 ? a.n_tok : 1);  // token t reads positions 0 .. pos + t
@@ -1001,6 +1120,7 @@ hipError_t issue(const std::vector<Launch> & ls, hipStream_t s) {
         else if (auto * x = std::get_if<LNext>(&l)) e = launch_next_token(x->a, s);
         else if (auto * x = std::get_if<LGemmQ>(&l)) e = launch_gemm_quant(x->a, s);
         else if (auto * x = std::get_if<LGemm>(&l)) e = launch_gemm(x->a, x->type, s);
+        else if (auto * x = std::get_if<LGdnOut>(&l)) e = launch_gdn_out(x->a, x->type, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -1039,6 +1159,11 @@ gemvq_ctx * gemvq_ctx_create(int device, size_t act_floats, size_t weight_bytes,
     if (e == hipSuccess) e = hipMalloc(&c->gdn_raw, size_t(GDN_MAX_HEADS) * 128 * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&c->dsnap, size_t(GEMV_MAXK) * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&c->xsnap, size_t(GEMV_MAXK) * sizeof(float));
+    for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+        e = hipMalloc(&c->acc[i], size_t(GEMV_MAXK) * 8);
+        if (e == hipSuccess) e = hipMemset(c->acc[i], 0, size_t(GEMV_MAXK) * 8);
+    }
+    if (e == hipSuccess) e = hipMalloc(&c->gdn_shadow, size_t(GDN_MAX_HEADS) * 128 * 128 * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&c->gemm_q, size_t(GEMM_MAX_TOK) * GEMV_MAXK);
     if (e == hipSuccess) e = hipMalloc(&c->gemm_d, size_t(GEMM_MAX_TOK) * (GEMV_MAXK / 32) * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&c->gemm_s, size_t(GEMM_MAX_TOK) * (GEMV_MAXK / 32) * sizeof(float));
@@ -1075,6 +1200,9 @@ void gemvq_ctx_destroy(gemvq_ctx * c) {
     hipFree(c->gdn_raw);
     hipFree(c->dsnap);
     hipFree(c->xsnap);
+    hipFree(c->acc[0]);
+    hipFree(c->acc[1]);
+    hipFree(c->gdn_shadow);
     hipFree(c->gemm_q);
     hipFree(c->gemm_d);
     hipFree(c->gemm_s);
