@@ -110,11 +110,11 @@ __device__ __forceinline__ int item_of(int g, int n16) {
 template <int R, int XS>
 __device__ __forceinline__ void prologue_fetch(const GemvArgs & a, XF<R, XS> & f) {
     const int n16 = a.cols / 16;
-    const bool normw = (a.xsrc == XSRC_NORM || a.xsrc == XSRC_ACC) && a.norm_w != nullptr;
+    const bool normw = (XS == XS_ACC || a.xsrc == XSRC_NORM) && a.norm_w != nullptr;  // ACC instances: always a norm
 #pragma unroll
     for (int g = 0; g < R; ++g) {
         const int i = item_of(g, n16);
-        const float * xi = (XS == XS_ACC ? a.acc_res : a.x) + size_t(i) * 16;
+        const float * xi = a.x + size_t(i) * 16;
         load16(xi, f.v[g]);
         if constexpr (XS == XS_ACC) {
             const u64x2 * ap = reinterpret_cast<const u64x2 *>(a.acc + size_t(i) * 16);
@@ -257,7 +257,7 @@ __device__ __forceinline__ void prologue_finish(const GemvArgs & a, XF<R, XS> & 
             quantize_half(v, i, i < n16, s);
         }
     } else {
-        const bool norm = a.xsrc == XSRC_NORM || a.xsrc == XSRC_ACC, normw = norm && a.norm_w != nullptr;
+        const bool norm = XS == XS_ACC || a.xsrc == XSRC_NORM, normw = norm && a.norm_w != nullptr;
         const float sc = norm ? norm_scale_items<R, XS>(a, f, s) : 1.0f;  // the same on every thread
 #pragma unroll
         for (int g = 0; g < R; ++g) {

@@ -24,7 +24,7 @@ struct WeightView {
 
 enum : int { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_ADD = 2, EPI_CONV = 3, EPI_SILU = 4 };
 // XSRC_GATED: gate_silu says whether z is silu(z). XSRC_ACC: the activation is the deferred norm of
-// fixed_to_float(acc) + acc_res (a fused DeltaNet step + ssm_out left its exact row sums in acc); workgroup 0 also
+// fixed_to_float(acc) + x (a fused DeltaNet step + ssm_out left its exact row sums in acc); workgroup 0 also
 // stores that sum to x_out (the ssm_out command's residual-added output).
 enum : int { XSRC_RAW = 0, XSRC_NORM = 1, XSRC_GATED = 2, XSRC_ACC = 3 };
 // Prologue kinds of the GEMV kernel instances.
@@ -57,11 +57,6 @@ struct GemvArgs {
     const float * gate_z;     // XSRC_GATED: z (the output gate) [cols]
     float * x_out;            // XSRC_GATED: the gated activation is also written here (by workgroup 0)
     int gate_silu;            // XSRC_GATED: gate_z holds silu(z) already
-    const unsigned long long * acc;  // XSRC_ACC: fixed-point row sums (LSB 2^-40) of the fused ssm_out
-    const float * acc_res;           // XSRC_ACC: its residual
-    const float4 * cp_src;           // XSRC_ACC: the state rows the fused step left in the shadow rows, copied back
-    float4 * cp_dst;                 // into the state rows by the launch's threads (cp_n float4s; 0: none)
-    int cp_n;
     int norm_l2;
     int cols;
     int n_members;
@@ -69,6 +64,13 @@ struct GemvArgs {
     GemvMember m[4];
     unsigned long long * argmax_key;  // non-NULL: argmax over member 0's y
     int32_t * dbg;                    // non-NULL: integer block sums of member 0
+    // XSRC_ACC (last, so the fields every launch reads keep their places): the fused ssm_out's fixed-point row sums
+    // (LSB 2^-40; x is its residual), and the state rows the fused step left in the shadow rows, copied back into
+    // the state rows by the launch's threads (cp_n float4s; 0: none)
+    const unsigned long long * acc;
+    const float4 * cp_src;
+    float4 * cp_dst;
+    int cp_n;
 };
 
 struct NormArgs {

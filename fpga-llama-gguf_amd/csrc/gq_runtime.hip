@@ -990,7 +990,6 @@ struct Compiler {
             a.xsrc = XSRC_ACC;
             a.x = A(accp.res);
             a.acc = accp.acc;
-            a.acc_res = A(accp.res);
             a.x_out = A(accp.y);
             a.cp_src = reinterpret_cast<const float4 *>(accp.cp_src);
             a.cp_dst = reinterpret_cast<float4 *>(accp.cp_dst);
