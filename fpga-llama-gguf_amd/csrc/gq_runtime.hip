@@ -1217,6 +1217,15 @@ __attribute__((visibility("hidden"))) void gq_set_error(gemvq_ctx * c, const cha
     if (c) c->err = what;
 }
 
+int gemvq_device_memory(int device, size_t * free_bytes, size_t * total_bytes) {
+    size_t f = 0, t = 0;
+    hipError_t e = hipSetDevice(device);
+    if (e == hipSuccess) e = hipMemGetInfo(&f, &t);
+    if (free_bytes) *free_bytes = f;
+    if (total_bytes) *total_bytes = t;
+    return e == hipSuccess ? 0 : -int(e);
+}
+
 void gemvq_features(gemvq_ctx *, uint32_t out[2]) {
     out[0] = GEMVQ_FEATURES;
     out[1] = GEMVQ_FEATURES2;

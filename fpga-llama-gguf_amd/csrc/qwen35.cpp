@@ -516,3 +516,28 @@ int gemvq_qwen35_commands(gemvq_qwen35 * m, uint32_t * words, size_t n_words) {
 int gemvq_qwen35_graph(gemvq_qwen35 * m) { return m ? m->graph : -1; }
 
 }  // extern "C"
+
+extern "C" int gemvq_qwen35_dry_commands(const gemvq_qw_config * cfg, const gemvq_tensor_desc * tab, int n,
+                                         uint32_t * words, size_t n_words) {
+    if (!cfg || !tab || n <= 0) return GEMVQ_EINVAL;
+    gemvq_qwen35 m;
+    m.c = *cfg;
+    m.descs.assign(tab, tab + n);
+    layout(m, m.descs.data(), n);
+    uint64_t used = 0;  // gemvq_upload_weight's placement: each matrix at the next 256-byte boundary, in table order
+    for (int i = 0; i < n; ++i) {
+        T & x = m.t[tab[i].name];
+        x.d = &m.descs[i];
+        if (tab[i].type == F32) continue;
+        x.w_off = (used + 255) & ~uint64_t(255);
+        used = x.w_off + tab[i].nbytes;
+    }
+    m.kv.assign(cfg->n_layer, -1);
+    int kv = 0;
+    for (int il = 0; il < cfg->n_layer; ++il)
+        if (is_attn(*cfg, il)) m.kv[il] = kv++;
+    std::string err;
+    if (!build_commands(m, err)) return GEMVQ_EINVAL;
+    if (words && n_words >= m.cmds.size()) std::memcpy(words, m.cmds.data(), m.cmds.size() * 4);
+    return int(m.cmds.size() / GEMVQ_CMD_WORDS);
+}

@@ -182,6 +182,8 @@ int gemvq_graph_create(gemvq_ctx * ctx, const uint32_t * cmds, unsigned n_cmds, 
 int gemvq_graph_replay(gemvq_ctx * ctx, int graph, int times);
 int gemvq_graph_destroy(gemvq_ctx * ctx, int graph);
 int gemvq_sync(gemvq_ctx * ctx);
+/* Free and total HBM of a device (hipMemGetInfo); 0 or a negative HIP error. */
+int gemvq_device_memory(int device, size_t * free_bytes, size_t * total_bytes);
 
 /* Number of kernel launches the last validated list compiled to (after fusion). */
 int gemvq_last_launch_count(const gemvq_ctx * ctx);

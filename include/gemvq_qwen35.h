@@ -63,6 +63,11 @@ int gemvq_qwen35_hidden(gemvq_qwen35 * m, float * out);
 int gemvq_qwen35_commands(gemvq_qwen35 * m, uint32_t * words, size_t n_words);
 /* The captured graph id (for gemvq_graph_time); -1 before the first step. */
 int gemvq_qwen35_graph(gemvq_qwen35 * m);
+/* The per-token command list gemvq_qwen35_create would build, without a device: weights placed as
+ * gemvq_upload_weight places them in table order, KV buffers numbered in layer order. Returns the number of commands
+ * (words copied when n_words is large enough), or GEMVQ_EINVAL. */
+int gemvq_qwen35_dry_commands(const gemvq_qw_config * cfg, const gemvq_tensor_desc * table, int n_tensors,
+                              uint32_t * words, size_t n_words);
 
 #ifdef __cplusplus
 }

@@ -23,7 +23,8 @@ def libs(gq):
 
         build.build()
     return {"gemvq_hip.h": C.CDLL(gq.HIP_LIB_PATH), "gemvq_qwen35.h": C.CDLL(gq.HIP_LIB_PATH),
-            "gemvq_gguf.h": C.CDLL(gq.HIP_LIB_PATH), "gemvq_synth.h": C.CDLL(gq.SYNTH_LIB_PATH)}
+            "gemvq_gguf.h": C.CDLL(gq.HIP_LIB_PATH), "gemvq_ggml.h": C.CDLL(gq.HIP_LIB_PATH),
+            "gemvq_synth.h": C.CDLL(gq.SYNTH_LIB_PATH)}
 
 
 def declared_functions(header: str) -> list[str]:
@@ -31,7 +32,7 @@ def declared_functions(header: str) -> list[str]:
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     text = re.sub(r"//[^\n]*", "", text)
     text = re.sub(r"#[^\n]*", "", text)
-    return re.findall(r"\b((?:gemvq|gqs)_\w+)\s*\([^;{]*\)\s*;", text)
+    return re.findall(r"\b((?:gemvq|gqs|gqg)_\w+)\s*\([^;{]*\)\s*;", text)
 
 
 def test_every_declared_symbol_is_exported(libs):
