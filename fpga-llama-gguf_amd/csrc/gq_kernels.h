@@ -245,7 +245,7 @@ struct GemmArgs {
 constexpr int GEMV_MAXK = 16384;  // GEMV columns at most
 constexpr int GEMM_MAX_TOK = 32;  // tokens of one batched GEMV (two tiles of 16)
 constexpr int ATTN_CHUNK = 64;
-constexpr int ATTN_MAXG = 4;  // q heads per KV head
+constexpr int ATTN_MAXG = 8;  // q heads per KV head
 constexpr int GDN_MAX_HEADS = 64;  // value heads of one GDN command
 
 // Profiling: when set (by gemvq_profile on the calling thread), launchers start kernels through

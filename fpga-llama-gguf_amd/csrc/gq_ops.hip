@@ -242,7 +242,7 @@ __global__ __launch_bounds__(64) void gated_norm_kernel(GatedNormArgs a) {
 //      f_c = e^(m_c - M), L = sum l_c f_c and O = sum o_c f_c in chunk order, and writes O / L times the sigmoid
 //      of the gate.
 constexpr int ATT_T = 256;
-constexpr int MAXCH = 64;  // chunks (n_ctx <= 4096)
+constexpr int MAXCH = 64;  // chunks a combine round handles (wave 0's lanes)
 constexpr int CMB = 32;    // chunks per load round of the combine (each round is a dependent load)
 
 // ---- new keys, values and queries of n_tok tokens (step 2 below, one vector per workgroup) ----
@@ -358,11 +358,13 @@ __device__ __forceinline__ void attn_token(const AttnArgs & a, const uint4 (&kr)
     }
     __syncthreads();
     if (!last) return;
-    // ---- 5. combine (last workgroup of the q head) ----
+    // ---- 5. combine (last workgroup of the q head): M over every chunk, then L and O in chunk order, MAXCH
+    //      chunks a round (wave 0 forms a round's f_c and l_c in LDS) ----
     const float * pk = a.part + size_t(th) * nchmax * pstride;
+    const int nr0 = min(nc, MAXCH);  // chunks of the first round
     float ov[CMB];
     float mc = -__builtin_inff(), lc = 0.0f;
-    if (wave == 0 && lane < nc) {
+    if (wave == 0 && lane < nr0) {
         mc = __builtin_nontemporal_load(pk + size_t(lane) * pstride);
         lc = __builtin_nontemporal_load(pk + size_t(lane) * pstride + 1);
     }
@@ -370,28 +372,47 @@ __device__ __forceinline__ void attn_token(const AttnArgs & a, const uint4 (&kr)
     for (int c = 0; c < CMB; ++c) ov[c] = c < nc ? __builtin_nontemporal_load(pk + size_t(c) * pstride + 2 + e) : 0.0f;
     if (wave == 0) {
         float M = mc;
+        for (int r0 = MAXCH; r0 < nc; r0 += MAXCH)  // contexts past MAXCH chunks: the later rounds' maxima
+            M = fmaxf(M, r0 + lane < nc ? __builtin_nontemporal_load(pk + size_t(r0 + lane) * pstride) : -__builtin_inff());
 #pragma unroll
         for (int st = 32; st >= 1; st >>= 1) M = fmaxf(M, __shfl_xor(M, st, WAVE));
-        if (lane < nc) {
+        if (lane < nr0) {
             fcs[lane] = expf_(mc - M);
             lcs[lane] = lc;
         }
+        if (lane == 0) mx = M;
     }
     __syncthreads();
     float O = 0.0f, L = 0.0f;
-    for (int c0 = 0;;) {
+    for (int r0 = 0;;) {
+        const int rn = min(MAXCH, nc - r0);
+        for (int c0 = 0;;) {  // the round's chunks, CMB value rows a dependent load
 #pragma unroll
-        for (int c = 0; c < CMB; ++c) {
-            if (c0 + c >= nc) break;
-            const float f = fcs[c0 + c];
-            L += lcs[c0 + c] * f;
-            O += ov[c] * f;
+            for (int c = 0; c < CMB; ++c) {
+                if (c0 + c >= rn) break;
+                const float f = fcs[c0 + c];
+                L += lcs[c0 + c] * f;
+                O += ov[c] * f;
+            }
+            c0 += CMB;
+            if (c0 >= rn) break;
+#pragma unroll
+            for (int c = 0; c < CMB; ++c)
+                ov[c] = c0 + c < rn ? __builtin_nontemporal_load(pk + size_t(r0 + c0 + c) * pstride + 2 + e) : 0.0f;
         }
-        c0 += CMB;
-        if (c0 >= nc) break;
+        r0 += MAXCH;
+        if (r0 >= nc) break;
+        const int rn2 = min(MAXCH, nc - r0);
+        __syncthreads();  // every thread has read this round's f_c and l_c
+        if (wave == 0 && lane < rn2) {
+            const float m2 = __builtin_nontemporal_load(pk + size_t(r0 + lane) * pstride);
+            fcs[lane] = expf_(m2 - mx);
+            lcs[lane] = __builtin_nontemporal_load(pk + size_t(r0 + lane) * pstride + 1);
+        }
 #pragma unroll
         for (int c = 0; c < CMB; ++c)
-            ov[c] = c0 + c < nc ? __builtin_nontemporal_load(pk + size_t(c0 + c) * pstride + 2 + e) : 0.0f;
+            ov[c] = c < rn2 ? __builtin_nontemporal_load(pk + size_t(r0 + c) * pstride + 2 + e) : 0.0f;
+        __syncthreads();
     }
     if (el) {
         float out = O / L;
@@ -659,7 +680,7 @@ hipError_t launch_attn_hd(const AttnArgs & a, dim3 grid, hipStream_t s) {
 }
 
 hipError_t launch_attn(const AttnArgs & a, hipStream_t s) {
-    if (a.n_head % a.n_head_kv || a.n_head / a.n_head_kv > ATTN_MAXG || (a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK > MAXCH)
+    if (a.n_head % a.n_head_kv || a.n_head / a.n_head_kv > ATTN_MAXG)
         return hipErrorInvalidValue;
     // units (KV head, chunk) in groups of 8, each group followed by its q heads: workgroup b serves unit
     // (b / (8 G)) 8 + b % 8 (units past the last are idle) and q head (b / 8) % G of its KV head

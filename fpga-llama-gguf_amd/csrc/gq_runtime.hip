@@ -648,7 +648,7 @@ struct Compiler {
                 const uint32_t kv = k[3], flags = k[7];
                 if (kv >= c->kvs.size()) return reject(i, "ATTN kv buffer");
                 const KvBuf & b = c->kvs[kv];
-                if (nkv == 0 || nh % nkv || nh / nkv > 4 || (b.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK > 64 || int(nkv) != b.n_head_kv || int(hd) != b.head_dim || hd > 256 ||
+                if (nkv == 0 || nh % nkv || nh / nkv > ATTN_MAXG || int(nkv) != b.n_head_kv || int(hd) != b.head_dim || hd > 256 ||
                     hd < 16 || (hd & (hd - 1)) || nrot > hd || nrot % 2)
                     return reject(i, "ATTN shape");
                 const uint32_t qstride = (flags & 1) ? 2 * hd : hd, ntok = (flags >> 16) & 0xffu ? (flags >> 16) & 0xffu : 1;

@@ -178,6 +178,8 @@ def test_gdn_gated_norm_folded_into_gemv(gq, orc, ctx, hv, hk, wtype, z_silu):
     (6, 2, 128, 128, 1100, 1041, (1023, 1024, 1040)),  # 17 chunks
     (6, 2, 128, 128, 2200, 2113, (2047, 2048, 2112)),  # 34 chunks: two load rounds in the combine
     (4, 4, 64, 16, 80, 70, (5, 69)),  # one q head per KV head
+    (24, 4, 128, 64, 200, 130, (64, 129)),  # 6 q heads per KV head
+    (16, 4, 256, 64, 4096, 4096, (2048, 4095)),  # the whole of a 4096-position cache, one token at a time
 ])
 def test_attention(gq, orc, ctx, nh, nkv, hd, nrot, n_ctx, npos, checks):
     kv = ctx.kv_create(n_ctx, nkv, hd)
@@ -221,6 +223,8 @@ def test_attention(gq, orc, ctx, nh, nkv, hd, nrot, n_ctx, npos, checks):
     (16, 4, 256, 64, 200, 190, 16),  # the last six positions are past the capacity (not stored, no output)
     (6, 2, 128, 128, 1100, 1020, 7),  # 17 chunks
     (6, 2, 128, 128, 2200, 2100, 7),  # 34 chunks: two load rounds in the combine
+    (16, 4, 256, 64, 4096, 4064, 32),  # a batch ending at the last position of a 4096-position cache
+    (32, 4, 64, 32, 300, 250, 9),  # 8 q heads per KV head
 ])
 def test_attention_tokens(gq, orc, ctx, nh, nkv, hd, nrot, n_ctx, p0, ntok):
     """One ATTN command over n_tok tokens (positions act[pos] + t, packed rows) against n_tok one-token commands on
