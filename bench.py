@@ -8,8 +8,10 @@ untimed and `--steps` timed greedy decode steps (one hipGraph replay each, token
 
 roofline: the dominant kernel (largest share of a token's device time), its algorithmic bytes (GGUF weights +
 fp32 vectors read and written once + state/KV traffic) over its measured duration, from device start/stop events
-of every kernel of one token (gemvq_profile). cpu_baseline: the oracle decoder (a C restatement of the reference's
-CPU arithmetic, multithreaded over rows) on the host cores for a bounded sample of decode steps at the same shape.
+of every kernel of one token (gemvq_profile). cpu_baseline: the oracle decoder in the reference's CPU arithmetic
+(gemvq_ref.h: int8 block dots, here in AVX2, each row summed sequentially in FP32, double sums of squares) on the
+host, one thread per physical core, for up to 15 s (160 steps) of decode steps at the positions of the first timed GPU steps;
+the JSON names the CPU model, sockets, cores and SIMD extensions.
 """
 from __future__ import annotations
 
@@ -67,21 +69,86 @@ def profile(ctx: gq.Context, cmds: np.ndarray, reps: int) -> list[dict]:
             for i in range(n)]
 
 
-def cpu_baseline(blob, cfg, prompt, n_tokens: int, threads: int) -> dict:
+def cpu_info() -> dict:
+    """The host CPU as lscpu reports it: model, sockets, physical cores, logical CPUs and the SIMD extensions."""
+    info, procs = {}, []
+    try:
+        with open("/proc/cpuinfo") as f:
+            cur = {}
+            for line in f:
+                if not line.strip():
+                    if cur:
+                        procs.append(cur)
+                    cur = {}
+                    continue
+                k, _, v = line.partition(":")
+                cur[k.strip()] = v.strip()
+            if cur:
+                procs.append(cur)
+    except OSError:
+        pass
+    if procs:
+        flags = set(procs[0].get("flags", "").split())
+        info["model"] = procs[0].get("model name", "")
+        info["sockets"] = len({p.get("physical id", "0") for p in procs})
+        info["physical_cores"] = len({(p.get("physical id", "0"), p.get("core id", str(i))) for i, p in enumerate(procs)})
+        info["logical_cpus"] = len(procs)
+        info["simd"] = [x for x in ("sse4_2", "avx2", "fma", "avx512f", "avx512bw", "avx512_vnni", "avx_vnni", "amx_int8")
+                        if x in flags]
+    info["allowed_cpus"] = len(os.sched_getaffinity(0))
+    return info
+
+
+def one_cpu_per_core(n: int) -> list[int]:
+    """Up to n of this process's allowed logical CPUs, the first of each physical core (sibling threads skipped)."""
+    seen, out = set(), []
+    for c in sorted(os.sched_getaffinity(0)):
+        try:
+            base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+            core = (open(base + "physical_package_id").read().strip(), open(base + "core_id").read().strip())
+        except OSError:
+            core = ("?", str(c))
+        if core in seen:
+            continue
+        seen.add(core)
+        out.append(c)
+        if len(out) == n:
+            break
+    return out
+
+
+def cpu_baseline(blob, cfg, tokens, pos0: int, max_tokens: int, seconds: float, threads: int) -> dict:
+    """The oracle decoder in the reference's CPU arithmetic on the host: decode steps at the positions (and with the
+    token ids) of the first timed GPU steps, until `seconds` have passed or max_tokens steps ran."""
+    cpus = one_cpu_per_core(threads)
+    # one OpenMP thread per physical core, bound in order (the oracle's runtime reads these when it loads)
+    os.environ["OMP_PLACES"] = ",".join(f"{{{c}}}" for c in cpus)
+    os.environ["OMP_PROC_BIND"] = "close"
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle  # noqa: E402  (the CPU baseline leg only)
 
-    om = oracle.Model(Q.config_c(cfg), blob.table, blob.n, blob.data, threads=threads)
-    om.decode(int(prompt[0]), 0)  # first touch of the weights, untimed
-    t0 = time.perf_counter()
-    for pos in range(1, 1 + n_tokens):
-        om.decode(int(prompt[pos]), pos)
-    dt = time.perf_counter() - t0
-    om.close()
-    return {"value": round(n_tokens / dt, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{n_tokens} decode steps (positions 1..{n_tokens}) of the same 9B-shape model with the oracle "
-                      f"decoder (C restatement of the reference CPU arithmetic, rows split over {threads} threads, "
-                      f"{dt:.1f} s)"}
+    old = os.sched_getaffinity(0)
+    os.sched_setaffinity(0, cpus)
+    try:
+        om = oracle.Model(Q.config_c(cfg), blob.table, blob.n, blob.data, threads=len(cpus), mode=oracle.MODE_REFERENCE)
+        om.decode(int(tokens[0]), pos0)  # first touch of the weights and the thread pool, untimed
+        max_tokens = min(max_tokens, len(tokens) - 1)
+        n, t0 = 0, time.perf_counter()
+        while n < max_tokens and (n < 2 or time.perf_counter() - t0 < seconds):
+            om.decode(int(tokens[n + 1]), pos0 + 1 + n)
+            n += 1
+        dt = time.perf_counter() - t0
+        om.close()
+    finally:
+        os.sched_setaffinity(0, old)
+    return {"value": round(n / dt, 4), "unit": "tokens/s", "cores": len(cpus), "kind": "port",
+            "arithmetic": "the reference's CPU arithmetic (gemvq_ref.h: int8 block dot products, each row summed "
+                          "sequentially in FP32, sums of squares in double, libm exp); the int8 dots in AVX2",
+            "cpu": cpu_info(),
+            "sample": f"{n} decode steps of the same 9B-shape model at positions {pos0 + 1}..{pos0 + n} with the ids "
+                      f"the GPU generated there, from an empty state (a step's work depends on its position, not on "
+                      f"the state); rows split over {len(cpus)} threads, one per physical core (CPUs {cpus[0]}.."
+                      f"{cpus[-1]}); {dt:.1f} s"}
 
 
 def copy_probe(mib: int) -> int:
@@ -319,7 +386,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=128, help="timed decode steps (tokens)")
     ap.add_argument("--warmup", type=int, default=0, help="untimed decode steps after the prompt")
     ap.add_argument("--prompt", type=int, default=512, help="prompt length (outside the timed steps)")
-    ap.add_argument("--cpu-tokens", type=int, default=6, help="decode steps timed for the CPU baseline (0: skip)")
+    ap.add_argument("--cpu-tokens", type=int, default=160, help="most decode steps timed for the CPU baseline (0: skip)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="time the CPU baseline samples for")
     ap.add_argument("--threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--profile-reps", type=int, default=3)
     ap.add_argument("--layers", type=int, default=32, help="(testing) fewer layers; the reported line is then invalid")
@@ -426,7 +494,8 @@ def main() -> int:
     cpu = None
     if args.cpu_tokens > 0:
         t = time.perf_counter()
-        cpu = cpu_baseline(blob, cfg, prompt, args.cpu_tokens, args.threads)
+        cpu = cpu_baseline(blob, cfg, toks[args.prompt + args.warmup - 1:], args.prompt + args.warmup - 1,
+                           args.cpu_tokens, args.cpu_seconds, args.threads)
         log(f"cpu baseline {cpu['value']} tok/s in {time.perf_counter() - t:.1f} s")
 
     line = {
