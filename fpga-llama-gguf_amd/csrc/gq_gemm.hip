@@ -169,12 +169,24 @@ __device__ __forceinline__ float lane_of(const v4f & v, int j) { return v[j]; }
 
 // The wave's GW blocks of a staged round: per block and token tile one MFMA gives the lane's 4 sums (rows 4g + i,
 // token r); each term is floor(sumi * s) with s = fp16(d_w) * d_x * 2^40 exact in FP32 and the product exact in FP64;
-// the GW terms are summed in FP64 (exact while the sum stays below 2^53 LSB, as in the single-token kernel) and moved
-// to the int64 totals.
+// the GW terms are summed in FP64 and moved to the int64 totals. The FP64 sum is exact while it stays below 2^53 LSB:
+// |term| <= wbound * |d_x * 2^40| (wbound: the member's largest |d_w| times its type's largest |sum of products|),
+// so a round where a lane's wbound * sum |d_x * 2^40| over a token's GW blocks reaches 2^52 (a factor 2 of margin)
+// adds every term of the wave to the int64 totals directly.
 template <int TYPE, bool PAIR, int T>
 __device__ __forceinline__ void round_terms(const uint8_t * lq, const uint32_t * ld, int wave, int r, int g,
-                                            const XRound<T> & x, long long (*tot)[4], long long (*totu)[4]) {
+                                            const XRound<T> & x, float wbound, long long (*tot)[4],
+                                            long long (*totu)[4]) {
     constexpr int NM = PAIR ? 2 : 1, QH = TYPE == T_Q8_0 ? 2 : 1;
+    float dm = 0.0f;  // the lane's largest sum of |d_x * 2^40| over the GW blocks of one token
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        float ds = 0.0f;
+#pragma unroll
+        for (int c = 0; c < GW; ++c) ds += fabsf(lane_of(x.d[t], c));
+        dm = fmaxf(dm, ds);
+    }
+    const bool exact = __builtin_amdgcn_ballot_w64(!(wbound * dm < 4503599627370496.0f)) != 0;
     constexpr int QBUF = GT * ROW_LDS, DBUF = GT * GU;  // bytes of one matrix-half's quants, scales of one matrix
     double acc[NM][T][4];
 #pragma unroll
@@ -215,7 +227,12 @@ __device__ __forceinline__ void round_terms(const uint8_t * lq, const uint32_t *
                     double term = floor(double(sm[i]) * double(sc));
                     if constexpr (TYPE == T_Q4_1)  // + floor(m * s_x * 2^40), the product of two fp16 values exact
                         term += floor(double(h2f(sw >> 16) * lane_of(x.s[t], j)));
-                    acc[m][t][i] += term;
+                    if (exact) {
+                        if (m == 0) tot[t][i] += dint_to_i64(term);
+                        else totu[PAIR ? t : 0][i] += dint_to_i64(term);
+                    } else {
+                        acc[m][t][i] += term;
+                    }
                 }
             }
         }
@@ -248,11 +265,13 @@ __global__ __launch_bounds__(NT) void gemm_kernel(GemmArgs a0) {
     const int r = lane & 15, g = lane >> 4;
     GemmArgs a = a0;
     int tile0 = 0;
+    float wbd = a0.wbound[0];  // the member's term bound
     if (!PAIR) {
         int mi = -1;
         for (int i = 0; i < a0.n_more; ++i)
             if (int(blockIdx.x) >= a0.more[i].tile0) mi = i;
         if (mi >= 0) {
+            wbd = a0.wbound[mi + 1];
             const GemmMore & o = a0.more[mi];
             a.w = o.w;
             a.y = o.y;
@@ -288,17 +307,17 @@ __global__ __launch_bounds__(NT) void gemm_kernel(GemmArgs a0) {
         // round rd from buffer 0 and xa; round rd + 1's weights (wb) go to buffer 1
         load_xround<TYPE, T>(a, nb, r, g, (rd + 1) * GU + wave * GW, xb);
         load_wround<TYPE, PAIR>(a, nb, lrow, min(rd + 2, nr - 1), wa);
-        round_terms<TYPE, PAIR, T>(lq[0], ld[0], wave, r, g, xa, tot, totu);
+        round_terms<TYPE, PAIR, T>(lq[0], ld[0], wave, r, g, xa, wbd, tot, totu);
         stage<TYPE, PAIR>(wb, lq[1], ld[1]);
         __syncthreads();
         // round rd + 1 from buffer 1 and xb; round rd + 2's weights (wa) go to buffer 0
         load_xround<TYPE, T>(a, nb, r, g, min(rd + 2, nr - 1) * GU + wave * GW, xa);
         load_wround<TYPE, PAIR>(a, nb, lrow, min(rd + 3, nr - 1), wb);
-        round_terms<TYPE, PAIR, T>(lq[1], ld[1], wave, r, g, xb, tot, totu);
+        round_terms<TYPE, PAIR, T>(lq[1], ld[1], wave, r, g, xb, wbd, tot, totu);
         stage<TYPE, PAIR>(wa, lq[0], ld[0]);
         __syncthreads();
     }
-    if (rd < nr) round_terms<TYPE, PAIR, T>(lq[0], ld[0], wave, r, g, xa, tot, totu);  // an odd last round
+    if (rd < nr) round_terms<TYPE, PAIR, T>(lq[0], ld[0], wave, r, g, xa, wbd, tot, totu);  // an odd last round
     if (wave > 0) {
 #pragma unroll
         for (int t = 0; t < T; ++t)

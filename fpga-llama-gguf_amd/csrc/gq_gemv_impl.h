@@ -634,20 +634,30 @@ __device__ __forceinline__ void load_slot(const GemvMember & m, int r, int lane,
     o.e = *(lane < m.e_split ? pa : pb);
 }
 
-// Per-lane partial of one row (its lane's units): the block terms are exact integers, summed in FP64, which is exact
-// while the partial stays below 2^53 LSB (|partial| < 8192 in output units; past that a few LSB of 2^-40 can drop).
-// dbg (block sums for the tests) is written only for a row that exists.
-template <int TYPE, int NU>
+// Per-lane partial of one row (its lane's units). The block terms are exact integers in FP64, summed in FP64 (exact
+// while every partial stays below 2^53 LSB, |partial| < 8192 in output units), or with EXACT (a wave whose partials
+// could pass that) each term t is split as t = 2^32 h + l (h = floor(t / 2^32), 0 <= l < 2^32, both exact) and the
+// h and the l are summed in two FP64 accumulators, exact for NU <= 8 terms below 2^63 LSB. dbg (block sums for the
+// tests) is written only for a row that exists.
+template <int TYPE, int NU, bool EXACT>
 __device__ __forceinline__ long long lane_blocks(const WB * wb, int r, bool valid, int nb, const XB * xb, int lane,
                                                  int32_t * dbg) {
-    double acc = 0.0;
+    double acc = 0.0, hi = 0.0;
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
         const int b = lane + 64 * k;
         const int si = dot_block<TYPE>(wb[k], xb[k]);
-        acc += block_term<TYPE>(si, wb[k].d, xb[k]);  // units past the row's end hold a zero activation
+        const double t = block_term<TYPE>(si, wb[k].d, xb[k]);  // units past the row's end hold a zero activation
+        if constexpr (EXACT) {
+            const double h = floor(t * 2.3283064365386963e-10);  // t / 2^32
+            hi += h;
+            acc += t - h * 4294967296.0;
+        } else {
+            acc += t;
+        }
         if (dbg && valid && b < nb) dbg[size_t(r) * nb + b] = si;
     }
+    if constexpr (EXACT) return (dint_to_i64(hi) << 32) + dint_to_i64(acc);
     return dint_to_i64(acc);
 }
 
@@ -678,21 +688,22 @@ __device__ __forceinline__ long long lane_units(const WK * wk, int r, bool valid
 struct Ctx {  // per-wave state shared by the row loops
     int lane, nb, nu;
     unsigned long long best;
+    bool exact;  // wave-uniform: block terms are summed in int64 (a lane's FP64 partial could pass 2^53 LSB)
 };
 
 __device__ __forceinline__ float lane_value(float v, int j) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
 }
 
-template <int TYPE, int NU, bool PAIR, int EPI>
+template <int TYPE, int NU, bool PAIR, int EPI, bool EXACT = false>
 __device__ __forceinline__ void lane_partials(const Slot<TYPE, NU, PAIR> & R, int r, bool valid, const XB * xb,
                                               const XK * xk, Ctx & c, int32_t * dbg, long long & p, long long & p2) {
     if constexpr (Slot<TYPE, NU, PAIR>::KQ) {
         p = lane_units<TYPE, NU>(R.wk, r, valid, c.nu, xk, c.lane, dbg);
         if constexpr (PAIR && EPI == EPI_SWIGLU) p2 = lane_units<TYPE, NU>(R.wk2, r, valid, c.nu, xk, c.lane, nullptr);
     } else {
-        p = lane_blocks<TYPE, NU>(R.wb, r, valid, c.nb, xb, c.lane, dbg);
-        if constexpr (PAIR && EPI == EPI_SWIGLU) p2 = lane_blocks<TYPE, NU>(R.wb2, r, valid, c.nb, xb, c.lane, nullptr);
+        p = lane_blocks<TYPE, NU, EXACT>(R.wb, r, valid, c.nb, xb, c.lane, dbg);
+        if constexpr (PAIR && EPI == EPI_SWIGLU) p2 = lane_blocks<TYPE, NU, EXACT>(R.wb2, r, valid, c.nb, xb, c.lane, nullptr);
     }
 }
 
@@ -792,6 +803,23 @@ __device__ __forceinline__ void run_rows(const GemvArgs & a, const GemvMember & 
     finish_chunk<TYPE, NU, PAIR, EPI, DS>(m, argmax, w + kb * S, S, min(DS, n - kb), p, p2, ev, c);
 }
 
+// The rows of a wave whose block terms could pass 2^53 LSB (see the kernel): one row at a time, each loaded, summed
+// exactly and finished. Kept apart from the pipelined loop above, which it would otherwise slow.
+template <int TYPE, int NU, bool PAIR, int EPI>
+__device__ __forceinline__ void exact_rows(const GemvArgs & a, const GemvMember & m, int mi, int w, int S, int n,
+                                        const XB * xb, Ctx & c) {
+    const bool argmax = EPI == EPI_PLAIN && a.argmax_key != nullptr && mi == 0;
+    int32_t * dbg = mi == 0 ? a.dbg : nullptr;
+    for (int k = 0; k < n; ++k) {
+        Slot<TYPE, NU, PAIR> sl;
+        load_slot<TYPE, NU, PAIR>(m, w + k * S, c.lane, c.nb, c.nu, sl);
+        long long p = 0, p2 = 0;
+        lane_partials<TYPE, NU, PAIR, EPI, true>(sl, w + k * S, true, xb, nullptr, c, dbg, p, p2);
+        const float ev = sl.e;
+        finish_chunk<TYPE, NU, PAIR, EPI, 1>(m, argmax, w + k * S, S, 1, &p, &p2, &ev, c);
+    }
+}
+
 // Waves are assigned to members in order: member i owns the global waves wave_begin .. wave_begin + waves - 1;
 // waves past the last member only take part in the prologue.
 template <int TYPE, int NU, bool PAIR, int XS, int DS>
@@ -805,6 +833,7 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
     c.nb = a.cols / 32;
     c.nu = a.cols / 64;
     c.best = 0;
+    c.exact = false;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: member fields load as scalars
     // Workgroup b serves slice b % 8 of every member's rows (workgroups are dealt to the XCDs in turn, so a slice's
     // rows stream through one XCD's L2; placement only affects speed, never which rows run).
@@ -851,8 +880,16 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
     } else {
 #pragma unroll
         for (int k = 0; k < NU; ++k) load_xb<TYPE>(s, c.lane + 64 * k, c.nb, xb[k]);
+        // A lane adds its NU block terms in FP64, exact while every partial stays below 2^53 LSB. |term| <= wbound *
+        // |d_x| * 2^40 (wbound: the matrix's largest |d_w| times the largest |sum of products| of its type, from the
+        // upload), so while wbound * sum |d_x| * 2^40 < 2^52 over a lane's blocks (a factor 2 of margin for the FP32
+        // bound) its FP64 sum is exact; a wave with a lane past that sums its terms in int64.
+        float dsum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NU; ++k) dsum += fabsf(xb[k].dx40);
+        c.exact = __builtin_amdgcn_ballot_w64(!(a.wbound[mi] * dsum < 4503599627370496.0f)) != 0;
     }
-    if (n > 0) {
+    if (n > 0 && (KQ || !c.exact)) {
         switch (m.epi) {
         case EPI_SWIGLU:
             if constexpr (PAIR) run_rows<TYPE, NU, PAIR, EPI_SWIGLU, DS>(a, m, mi, w, S, n, sl, xb, xk, c);
@@ -861,6 +898,18 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
         case EPI_CONV: run_rows<TYPE, NU, PAIR, EPI_CONV, DS>(a, m, mi, w, S, n, sl, xb, xk, c); break;
         case EPI_SILU: run_rows<TYPE, NU, PAIR, EPI_SILU, DS>(a, m, mi, w, S, n, sl, xb, xk, c); break;
         default: run_rows<TYPE, NU, PAIR, EPI_PLAIN, DS>(a, m, mi, w, S, n, sl, xb, xk, c); break;
+        }
+    } else if (n > 0) {
+        if constexpr (!KQ) {
+            switch (m.epi) {
+            case EPI_SWIGLU:
+                if constexpr (PAIR) exact_rows<TYPE, NU, PAIR, EPI_SWIGLU>(a, m, mi, w, S, n, xb, c);
+                break;
+            case EPI_ADD: exact_rows<TYPE, NU, PAIR, EPI_ADD>(a, m, mi, w, S, n, xb, c); break;
+            case EPI_CONV: exact_rows<TYPE, NU, PAIR, EPI_CONV>(a, m, mi, w, S, n, xb, c); break;
+            case EPI_SILU: exact_rows<TYPE, NU, PAIR, EPI_SILU>(a, m, mi, w, S, n, xb, c); break;
+            default: exact_rows<TYPE, NU, PAIR, EPI_PLAIN>(a, m, mi, w, S, n, xb, c); break;
+            }
         }
     }
     if (a.argmax_key) {
@@ -896,6 +945,9 @@ int resident_blocks(K kernel, int per_cu = 1 << 20) {
 // gate/up pairs and projection groups, about 1 us per launch).
 constexpr int GEMV_WAVES_PER_CU = 12;
 constexpr int GEMV_WG_PER_CU = GEMV_WAVES_PER_CU / NWAVES > 0 ? GEMV_WAVES_PER_CU / NWAVES : 1;
+// Activations of more than 8192 columns (NU >= 5: the 12288-column FFN down projection): two workgroups per CU
+// (measured: three cost 1.2 us more per launch, each workgroup reading and quantizing 48 KB).
+constexpr int gemv_wg_per_cu(int nu) { return nu >= 5 && GEMV_WG_PER_CU > 2 ? 2 : GEMV_WG_PER_CU; }
 
 // Every member's rows are split into 8 contiguous slices, one per XCD; the same member layout repeats on each XCD
 // (workgroups b with b % 8 == x serve slice x). A member's waves per slice: enough for ds rows each when all fit
@@ -944,7 +996,7 @@ void epilog_operands(GemvMember & m) {
 
 template <int TYPE, int NU, bool PAIR, int XS, int DS>
 hipError_t launch_typed(const GemvArgs & a0, hipStream_t st) {
-    static const int cap = resident_blocks(gemv_kernel<TYPE, NU, PAIR, XS, DS>, GEMV_WG_PER_CU);
+    static const int cap = resident_blocks(gemv_kernel<TYPE, NU, PAIR, XS, DS>, gemv_wg_per_cu(NU));
     GemvArgs a = a0;
     for (int i = 0; i < a.n_members; ++i) epilog_operands(a.m[i]);
     const int grid = plan_waves(a, cap, DS);

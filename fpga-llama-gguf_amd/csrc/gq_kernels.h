@@ -71,6 +71,7 @@ struct GemvArgs {
     const float4 * cp_src;
     float4 * cp_dst;
     int cp_n;
+    float wbound[4];  // per member (Q4_0 / Q4_1 / Q8_0): the largest block term magnitude over |d_x| * 2^40
 };
 
 struct NormArgs {
@@ -240,6 +241,8 @@ struct GemmArgs {
     int epi;            // EPI_PLAIN, EPI_SWIGLU, EPI_ADD or EPI_SILU
     int n_more;         // members after the first (not with a SwiGLU pair); tiles of member i + 1 follow member i's
     GemmMore more[GEMM_MAX_MORE];
+    float wbound[GEMM_MAX_MORE + 1];  // per member: the largest block term magnitude over |d_x| * 2^40 (INFINITY:
+                                      // unknown, every round's terms are summed in int64)
 };
 
 constexpr int GEMV_MAXK = 16384;  // GEMV columns at most

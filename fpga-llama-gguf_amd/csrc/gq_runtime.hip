@@ -25,7 +25,37 @@ namespace {
 struct Weight {
     int type, rows, cols;
     size_t bytes;
+    float wbound;  // Q4_0 / Q4_1 / Q8_0: the largest block term magnitude over |d_x| * 2^40 (see weight_bound)
 };
+
+// IEEE binary16 to float (subnormals, infinities and NaN included).
+float half_to_float_host(uint16_t h) {
+    const int e = (h >> 10) & 31, m = h & 1023;
+    const float v = e == 0 ? std::ldexp(float(m), -24) : e == 31 ? (m ? NAN : INFINITY) : std::ldexp(float(1024 + m), e - 25);
+    return (h & 0x8000) ? -v : v;
+}
+
+// The largest |block term| / (|d_x| 2^40) of a Q4_0 / Q4_1 / Q8_0 matrix: over its blocks, |d_w| times the largest
+// |sum of products| with Q8_0 quants (|q_x| <= 127: 32 * 8 * 127 for Q4_0, 32 * 15 * 127 for Q4_1, 32 * 128 * 127
+// for Q8_0), plus for Q4_1 |m_w| times the largest |s_x| / d_x (32 * 127); rounded up to FP32. 0 for other types.
+float weight_bound(int type, int rows, int cols, const uint8_t * gguf) {
+    if (type != T_Q4_0 && type != T_Q4_1 && type != T_Q8_0) return 0.0f;
+    const size_t nb = size_t(rows) * size_t(cols / 32), bb = type == T_Q4_0 ? 18 : type == T_Q4_1 ? 20 : 34;
+    const double smax = type == T_Q4_0 ? 32.0 * 8 * 127 : type == T_Q4_1 ? 32.0 * 15 * 127 : 32.0 * 128 * 127;
+    const auto h = [](const uint8_t * p) {
+        uint16_t u;
+        std::memcpy(&u, p, 2);
+        return std::fabs(double(half_to_float_host(u)));
+    };
+    double best = 0.0;
+    for (size_t i = 0; i < nb; ++i) {
+        const uint8_t * blk = gguf + i * bb;
+        double t = h(blk) * smax;
+        if (type == T_Q4_1) t += h(blk + 2) * (32.0 * 127);
+        if (!(t <= best)) best = t;  // a NaN scale makes the bound NaN: every launch on it sums in int64
+    }
+    return std::nextafter(float(best), INFINITY);
+}
 
 struct KvBuf {
     uint16_t * k = nullptr;
@@ -759,7 +789,8 @@ struct Compiler {
         if (ntok < 1 || ntok > GEMVQ_GEMM_MAX_TOK) return reject(i, "GEMM token count");
         if (xs % 16 || xs < cols || ys % 16 || ys < uint32_t(rows)) return reject(i, "GEMM strides");
         const uint64_t woff = uint64_t(k[4]) | (uint64_t(k[5]) << 32);
-        if (!weight(woff, t, rows, int(cols))) return reject(i, "GEMM weight offset, format or shape does not match an uploaded weight");
+        const Weight * gw = weight(woff, t, rows, int(cols));
+        if (!gw) return reject(i, "GEMM weight offset, format or shape does not match an uploaded weight");
         if (!range(k[6], uint64_t(xs) * (ntok - 1) + cols) || !range(k[7], uint64_t(ys) * (ntok - 1) + rows))
             return reject(i, "GEMM range");
         const bool norm = nflags & GEMVQ_NORM_DEFER, normw = norm && !(nflags & GEMVQ_NORM_NO_WEIGHT);
@@ -767,6 +798,7 @@ struct Compiler {
             return reject(i, "GEMM norm");
         GemmArgs g{};
         g.w = weight_view(c->warena + woff, t, rows, int(cols));
+        g.wbound[0] = gw->wbound;
         g.rows = rows;
         g.cols = int(cols);
         g.n_tok = int(ntok);
@@ -781,9 +813,10 @@ struct Compiler {
             if (u[0] != GEMVQ_OP_GEMM || u[1] != uint32_t(t) || int(u[2]) != rows || u[3] != cols || u[6] != k[6] ||
                 u2[0] != ntok || u2[1] != xs || u2[5] != k2[5] || u2[6] != k2[6] || u2[7] != nflags)
                 return reject(i + 2, "SwiGLU u GEMM must match its g GEMM");
-            if (u2[2] % 16 || u2[2] < uint32_t(rows) || !weight(uoff, t, rows, int(cols)) ||
-                !range(u[7], uint64_t(u2[2]) * (ntok - 1) + rows))
+            const Weight * uw = weight(uoff, t, rows, int(cols));
+            if (u2[2] % 16 || u2[2] < uint32_t(rows) || !uw || !range(u[7], uint64_t(u2[2]) * (ntok - 1) + rows))
                 return reject(i + 2, "SwiGLU u GEMM weight, stride or range");
+            if (!(uw->wbound <= g.wbound[0])) g.wbound[0] = uw->wbound;
             g.epi = EPI_SWIGLU;
             g.w2 = weight_view(c->warena + uoff, t, rows, int(cols));
             g.y = A(u[7]);
@@ -864,6 +897,7 @@ struct Compiler {
             if (meet(ny, y) || (epi == EPI_ADD && meet(ny, res)) || (nres && meet(nr, y))) return false;
             tiles += ((first ? p->a.rows : o->rows) + 15) / 16;
         }
+        p->a.wbound[p->a.n_more + 1] = g.wbound[0];
         p->a.more[p->a.n_more++] = GemmMore{g.w, g.y, g.res, g.rows, g.y_stride, g.res_stride, g.epi, tiles};
         spans.back().second = i + used - spans.back().first;
         return true;
@@ -910,6 +944,7 @@ struct Compiler {
                 cols = k[3];
             }
             GemvMember m{};
+            float wb = w->wbound;  // the member's term bound (a SwiGLU pair: the larger of its two matrices)
             m.w = weight_view(c->warena + woff, t, rows, int(cols));
             m.rows = rows;
             m.task_begin = tasks;
@@ -923,7 +958,9 @@ struct Compiler {
                 if (u[0] != GEMVQ_OP_GEMV || int(u[1] & 0xffu) != t || (u[1] & ~0xffu) || int(u[2]) != rows || u[3] != cols ||
                     u[6] != x_off)
                     return reject(i + 1, "SwiGLU u GEMV must match its g GEMV");
-                if (!weight(uoff, t, rows, int(cols)) || !range(u[7], uint64_t(rows))) return reject(i + 1, "SwiGLU u weight or range");
+                const Weight * uw = weight(uoff, t, rows, int(cols));
+                if (!uw || !range(u[7], uint64_t(rows))) return reject(i + 1, "SwiGLU u weight or range");
+                if (!(uw->wbound <= wb)) wb = uw->wbound;
                 m.epi = EPI_SWIGLU;
                 m.w2 = weight_view(c->warena + uoff, t, rows, int(cols));
                 m.y = A(u[7]);
@@ -961,6 +998,7 @@ struct Compiler {
                 }
                 step = 2;
             }
+            a.wbound[a.n_members] = wb;
             a.m[a.n_members++] = m;
             tasks += rows;
             gemvs += (flags & GEMVQ_GEMV_SWIGLU) ? 2 : 1;
@@ -1259,7 +1297,7 @@ int gemvq_upload_weight(gemvq_ctx * c, int type, int rows, int cols, const void 
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     hipHostFree(host);
     if (e != hipSuccess) return fail(c, e, "weight upload");
-    c->weights[off] = Weight{type, rows, cols, bytes};
+    c->weights[off] = Weight{type, rows, cols, bytes, weight_bound(type, rows, cols, static_cast<const uint8_t *>(gguf_rows))};
     c->wused = off + bytes;
     *w_off = off;
     return 0;

@@ -77,6 +77,7 @@ extern "C" int gemvq_gemm_static(int type, int rows, int cols, const void * w, c
     g.n_tok = n_tok;
     g.y_stride = y_stride;
     g.epi = EPI_PLAIN;
+    g.wbound[0] = INFINITY;  // the caller's matrix was never scanned: every round's terms are summed in int64
     const hipStream_t s = static_cast<hipStream_t>(stream);
     e = launch_gemm_quant(q, s);
     if (e == hipSuccess) e = launch_gemm(g, type, s);

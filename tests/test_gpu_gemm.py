@@ -96,6 +96,54 @@ def test_huge_activations_exact(gq, orc, ctx, fmt, outlier):
             assert np.abs(want).max() > outlier / 300.0  # the outlier blocks dominate these rows
 
 
+def _q4_0_block(d_bits: int, nibbles) -> bytes:
+    """One Q4_0 block: fp16 d, then byte j holding element j (low nibble) and element j + 16 (high nibble)."""
+    q = np.asarray(nibbles, np.uint8)
+    return int(d_bits).to_bytes(2, "little") + bytes((q[:16] | (q[16:] << 4)).tolist())
+
+
+def test_fp64_partial_past_2_53_is_exact(gq, orc, ctx):
+    """Rows whose FP64 partial sums would drop low bits: a block term of -260096 * 2^40 LSB and a term of 3 LSB in one
+    partial (row 0: one GEMV lane, blocks 0 and 64; row 1: one GEMM wave's round, blocks 0 and 2), cancelled by
+    +260096 * 2^40 in another partial. In FP64 the 3 is lost (the ulp at 2^58 is 64) and the row would be 0; the
+    kernels see the matrix's term bound and the activation's scales reach 2^53 LSB and sum those terms in int64, so
+    the row is 3 * 2^-40, the oracle's exact sum. Other rows are random."""
+    rows, cols = 64, 4096
+    nb = cols // 32
+    big_neg, big_pos, tiny, zero = 0x3400, 0xB400, 0x0001, 0x0000  # fp16: 0.25, -0.25, 2^-24, 0
+    all8, plus1 = [0] * 32, [8] * 32  # all8: every weight -8; plus1: +1 at element 1, 0 elsewhere
+    plus1[1] = 9
+    w = bytearray(gq.matrix(gq.Q4_0, rows, cols, 7, 60, std=0.02).tobytes())
+    row_bytes = nb * 18
+
+    def set_row(r, blocks):
+        for b in range(nb):
+            d, q = blocks.get(b, (zero, [8] * 32))
+            w[r * row_bytes + b * 18:r * row_bytes + (b + 1) * 18] = _q4_0_block(d, q)
+
+    set_row(0, {0: (big_neg, all8), 1: (big_pos, all8), 64: (tiny, plus1)})
+    set_row(1, {0: (big_neg, all8), 2: (tiny, plus1), 4: (big_pos, all8)})
+    w = np.frombuffer(bytes(w), np.uint8)
+    x = np.zeros(cols, np.float32)
+    for b in (0, 1, 4):  # d_x = 4064 / 127 = 32, every quant 127
+        x[32 * b:32 * b + 32] = 4064.0
+    for b in (2, 64):  # d_x = 2^-16, quants 127 and 3
+        x[32 * b] = 127 * 2.0 ** -16
+        x[32 * b + 1] = 3 * 2.0 ** -16
+    want = orc.fx_gemv(gq.Q4_0, w, x, rows, cols)
+    assert want[0] == want[1] == np.float32(3 * 2.0 ** -40)
+    off = ctx.upload(gq.Q4_0, rows, cols, w)
+    X, Y = 0, 8192
+    xt = np.concatenate([x, gq.normal(7, 61, cols)])  # a second token for the GEMM
+    ctx.write(X, xt)
+    assert ctx.run(gq.gemv(gq.Q4_0, rows, cols, off, X, Y)) == 0, ctx.error()
+    assert_bits(ctx.read(Y, rows), want, "GEMV")
+    assert ctx.run(gq.gemm(gq.Q4_0, rows, cols, off, X, Y, 2, cols, 64)) == 0, ctx.error()
+    y = ctx.read(Y, 2 * 64).reshape(2, 64)
+    assert_bits(y[0], want, "GEMM token 0")
+    assert_bits(y[1], orc.fx_gemv(gq.Q4_0, w, xt[cols:], rows, cols), "GEMM token 1")
+
+
 @pytest.mark.parametrize("fmt", [2, 3, 8])
 def test_gemm_epilogs_and_norm(gq, orc, ctx, fmt):
     rows, cols, ntok, eps = 2000, 4096, 9, 1e-6
