@@ -167,18 +167,11 @@ __device__ __forceinline__ void load_xround(const GemmArgs & a, int nb, int r, i
 __device__ __forceinline__ float lane_of(const v4f & v, int j) { return v[j]; }
 
 
-// The wave's GW blocks of a staged round: per block and token tile one MFMA gives the lane's 4 sums (rows 4g + i,
-// token r); each term is floor(sumi * s) with s = fp16(d_w) * d_x * 2^40 exact in FP32 and the product exact in FP64;
-// the GW terms are summed in FP64 and moved to the int64 totals. The FP64 sum is exact while it stays below 2^53 LSB:
-// |term| <= wbound * |d_x * 2^40| (wbound: the member's largest |d_w| times its type's largest |sum of products|),
-// so a round where a lane's wbound * sum |d_x * 2^40| over a token's GW blocks reaches 2^52 (a factor 2 of margin)
-// adds every term of the wave to the int64 totals directly.
-template <int TYPE, bool PAIR, int T>
-__device__ __forceinline__ void round_terms(const uint8_t * lq, const uint32_t * ld, int wave, int r, int g,
-                                            const XRound<T> & x, float wbound, long long (*tot)[4],
-                                            long long (*totu)[4]) {
-    constexpr int NM = PAIR ? 2 : 1, QH = TYPE == T_Q8_0 ? 2 : 1;
-    float dm = 0.0f;  // the lane's largest sum of |d_x * 2^40| over the GW blocks of one token
+// Whether a round needs the int64 path: some lane's wbound * (largest sum of |d_x * 2^40| over a token's GW blocks)
+// reaches 2^52 (one ballot, so the branch on it is uniform over the wave).
+template <int T>
+__device__ __forceinline__ bool round_needs_exact(const XRound<T> & x, float wbound) {
+    float dm = 0.0f;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         float ds = 0.0f;
@@ -186,7 +179,19 @@ __device__ __forceinline__ void round_terms(const uint8_t * lq, const uint32_t *
         for (int c = 0; c < GW; ++c) ds += fabsf(lane_of(x.d[t], c));
         dm = fmaxf(dm, ds);
     }
-    const bool exact = __builtin_amdgcn_ballot_w64(!(wbound * dm < 4503599627370496.0f)) != 0;
+    return __builtin_amdgcn_ballot_w64(!(wbound * dm < 4503599627370496.0f)) != 0;
+}
+
+// The wave's GW blocks of a staged round: per block and token tile one MFMA gives the lane's 4 sums (rows 4g + i,
+// token r); each term is floor(sumi * s) with s = fp16(d_w) * d_x * 2^40 exact in FP32 and the product exact in FP64;
+// the GW terms are summed in FP64 and moved to the int64 totals. The FP64 sum is exact while it stays below 2^53 LSB:
+// |term| <= wbound * |d_x * 2^40| (wbound: the member's largest |d_w| times its type's largest |sum of products|),
+// so a round where a lane's wbound * sum |d_x * 2^40| over a token's GW blocks reaches 2^52 (a factor 2 of margin)
+// adds every term of the wave to the int64 totals directly (EXACT).
+template <int TYPE, bool PAIR, int T, bool EXACT>
+__device__ __forceinline__ void round_terms_k(const uint8_t * lq, const uint32_t * ld, int wave, int r, int g,
+                                              const XRound<T> & x, long long (*tot)[4], long long (*totu)[4]) {
+    constexpr int NM = PAIR ? 2 : 1, QH = TYPE == T_Q8_0 ? 2 : 1;
     constexpr int QBUF = GT * ROW_LDS, DBUF = GT * GU;  // bytes of one matrix-half's quants, scales of one matrix
     double acc[NM][T][4];
 #pragma unroll
@@ -227,7 +232,7 @@ __device__ __forceinline__ void round_terms(const uint8_t * lq, const uint32_t *
                     double term = floor(double(sm[i]) * double(sc));
                     if constexpr (TYPE == T_Q4_1)  // + floor(m * s_x * 2^40), the product of two fp16 values exact
                         term += floor(double(h2f(sw >> 16) * lane_of(x.s[t], j)));
-                    if (exact) {
+                    if constexpr (EXACT) {
                         if (m == 0) tot[t][i] += dint_to_i64(term);
                         else totu[PAIR ? t : 0][i] += dint_to_i64(term);
                     } else {
@@ -237,13 +242,26 @@ __device__ __forceinline__ void round_terms(const uint8_t * lq, const uint32_t *
             }
         }
     }
+    if constexpr (!EXACT) {
 #pragma unroll
-    for (int t = 0; t < T; ++t)
+        for (int t = 0; t < T; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            tot[t][i] += dint_to_i64(acc[0][t][i]);
-            if constexpr (PAIR) totu[t][i] += dint_to_i64(acc[PAIR ? 1 : 0][t][i]);
-        }
+            for (int i = 0; i < 4; ++i) {
+                tot[t][i] += dint_to_i64(acc[0][t][i]);
+                if constexpr (PAIR) totu[t][i] += dint_to_i64(acc[PAIR ? 1 : 0][t][i]);
+            }
+    }
+}
+
+// The GW blocks of a round through one of two loops, chosen once per round (not per term, which kept the compiler
+// from scheduling the round as one block): the FP64-sum loop, or, where the bound says an FP64 partial could pass
+// 2^53 LSB, the one adding every term to the int64 totals.
+template <int TYPE, bool PAIR, int T>
+__device__ __forceinline__ void round_terms(const uint8_t * lq, const uint32_t * ld, int wave, int r, int g,
+                                            const XRound<T> & x, float wbound, long long (*tot)[4],
+                                            long long (*totu)[4]) {
+    if (round_needs_exact<T>(x, wbound)) round_terms_k<TYPE, PAIR, T, true>(lq, ld, wave, r, g, x, tot, totu);
+    else round_terms_k<TYPE, PAIR, T, false>(lq, ld, wave, r, g, x, tot, totu);
 }
 
 // Workgroup b: rows 16b .. 16b + 15 (clamped loads past the last row, nothing stored for them), the whole K range in
