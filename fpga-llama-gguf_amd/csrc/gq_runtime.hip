@@ -7,10 +7,13 @@
 
 #include <hip/hip_runtime.h>
 
+#include <chrono>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
+#include <thread>
 #include <variant>
 #include <vector>
 
@@ -112,6 +115,11 @@ struct gemvq_ctx {
     float * gemm_s = nullptr;     // and their Q8_1 block sums (for Q4_1 weights)
     int last_launches = 0;
     std::string err;
+    // Failure handling (ggml-xrt.cpp:69-78, 1258-1264, 2761-2770): every wait for the device is bounded by wait_ms;
+    // a launch or copy that failed or did not finish in time leaves the device in an unknown state, so the context
+    // refuses further device work (usable = false) until it is destroyed.
+    unsigned wait_ms = 180000;
+    bool usable = true;
 };
 
 static std::string g_create_error;
@@ -119,8 +127,34 @@ static std::string g_create_error;
 namespace {
 
 int fail(gemvq_ctx * c, hipError_t e, const char * what) {
-    if (c) c->err = std::string(what) + ": " + hipGetErrorString(e);
+    if (c) {
+        c->err = std::string(what) + ": " + hipGetErrorString(e);
+        c->usable = false;
+    }
     return -int(e);
+}
+
+// The status of an entry point on a context that an earlier device failure made unusable.
+int unusable(gemvq_ctx * c) {
+    c->err = "context unusable after a failed or timed-out device operation (" + c->err + ")";
+    return GEMVQ_EUNUSABLE;
+}
+
+// Waits for the context's stream for at most c->wait_ms (polling; a yield between polls). 0, a negated HIP error
+// (the stream reported a failure) or GEMVQ_ETIMEDOUT; either failure makes the context unusable.
+int wait_stream(gemvq_ctx * c, const char * what) {
+    const auto deadline = std::chrono::steady_clock::now() + std::chrono::milliseconds(c->wait_ms);
+    for (;;) {
+        const hipError_t e = hipStreamQuery(c->stream);
+        if (e == hipSuccess) return 0;
+        if (e != hipErrorNotReady) return fail(c, e, what);
+        if (std::chrono::steady_clock::now() > deadline) {
+            c->err = std::string(what) + ": the device did not finish within " + std::to_string(c->wait_ms) + " ms";
+            c->usable = false;
+            return GEMVQ_ETIMEDOUT;
+        }
+        std::this_thread::yield();
+    }
 }
 
 int einval(gemvq_ctx * c, const std::string & what) {
@@ -1185,8 +1219,19 @@ int compile_list(gemvq_ctx * c, const uint32_t * cmds, unsigned n, std::vector<L
 extern "C" {
 
 gemvq_ctx * gemvq_ctx_create(int device, size_t act_floats, size_t weight_bytes, size_t state_rows) {
+    unsigned wait_ms = 180000;  // GEMVQ_WAIT_TIMEOUT_MS (ggml-xrt.cpp:69-78's GGML_XRT_WAIT_TIMEOUT_MS)
+    if (const char * v = std::getenv("GEMVQ_WAIT_TIMEOUT_MS")) {
+        char * end = nullptr;
+        const unsigned long ms = std::strtoul(v, &end, 10);
+        if (end == v || *end != '\0' || ms == 0 || ms > 0xffffffffUL) {
+            g_create_error = "gemvq_ctx_create: GEMVQ_WAIT_TIMEOUT_MS must be a positive integer";
+            return nullptr;
+        }
+        wait_ms = unsigned(ms);
+    }
     auto * c = new gemvq_ctx();
     c->device = device;
+    c->wait_ms = wait_ms;
     hipError_t e = hipSetDevice(device);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipMalloc(&c->act, std::max<size_t>(act_floats, 16) * sizeof(float));
@@ -1284,6 +1329,7 @@ int gemvq_unpack(int type, int rows, int cols, const void * packed, void * gguf_
 
 int gemvq_upload_weight(gemvq_ctx * c, int type, int rows, int cols, const void * gguf_rows, uint64_t * w_off) {
     if (!c || !w_off || !gguf_rows) return einval(c, "gemvq_upload_weight: null argument");
+    if (!c->usable) return unusable(c);
     if (!type_ok(type) || !shape_ok(type, rows, cols)) return einval(c, "gemvq_upload_weight: unsupported type or shape");
     const size_t bytes = gguf_row_bytes(type, cols) * size_t(rows);
     const size_t off = (c->wused + 255) & ~size_t(255);
@@ -1294,9 +1340,9 @@ int gemvq_upload_weight(gemvq_ctx * c, int type, int rows, int cols, const void 
     if (e != hipSuccess) return fail(c, e, "hipHostMalloc");
     repack_rows(type, rows, cols, static_cast<const uint8_t *>(gguf_rows), static_cast<uint8_t *>(host), false);
     e = hipMemcpyAsync(c->warena + off, host, bytes, hipMemcpyHostToDevice, c->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    hipHostFree(host);
-    if (e != hipSuccess) return fail(c, e, "weight upload");
+    const int ws = e == hipSuccess ? wait_stream(c, "weight upload") : fail(c, e, "weight upload");
+    if (ws == 0 || ws == GEMVQ_ETIMEDOUT) hipHostFree(host);  // a failed stream may still read it: kept
+    if (ws) return ws;
     c->weights[off] = Weight{type, rows, cols, bytes, weight_bound(type, rows, cols, static_cast<const uint8_t *>(gguf_rows))};
     c->wused = off + bytes;
     *w_off = off;
@@ -1307,48 +1353,49 @@ uint64_t gemvq_weight_bytes_used(const gemvq_ctx * c) { return c ? c->wused : 0;
 
 int gemvq_act_write(gemvq_ctx * c, size_t off, const void * src, size_t n) {
     if (!c || !src || off + n > c->act_floats) return einval(c, "gemvq_act_write: range");
+    if (!c->usable) return unusable(c);
     hipSetDevice(c->device);
     hipError_t e = hipMemcpyAsync(c->act + off, src, n * 4, hipMemcpyHostToDevice, c->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    return e == hipSuccess ? 0 : fail(c, e, "act write");
+    return e == hipSuccess ? wait_stream(c, "act write") : fail(c, e, "act write");
 }
 
 int gemvq_act_read(gemvq_ctx * c, size_t off, void * dst, size_t n) {
     if (!c || !dst || off + n > c->act_floats) return einval(c, "gemvq_act_read: range");
+    if (!c->usable) return unusable(c);
     hipSetDevice(c->device);
     hipError_t e = hipMemcpyAsync(dst, c->act + off, n * 4, hipMemcpyDeviceToHost, c->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    return e == hipSuccess ? 0 : fail(c, e, "act read");
+    return e == hipSuccess ? wait_stream(c, "act read") : fail(c, e, "act read");
 }
 
 int gemvq_state_write(gemvq_ctx * c, size_t row, const float * src, size_t rows) {
     if (!c || !src || row + rows > c->state_rows) return einval(c, "gemvq_state_write: range");
+    if (!c->usable) return unusable(c);
     hipSetDevice(c->device);
     hipError_t e = hipMemcpyAsync(c->state + row * 128, src, rows * 512, hipMemcpyHostToDevice, c->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    return e == hipSuccess ? 0 : fail(c, e, "state write");
+    return e == hipSuccess ? wait_stream(c, "state write") : fail(c, e, "state write");
 }
 
 int gemvq_state_read(gemvq_ctx * c, size_t row, float * dst, size_t rows) {
     if (!c || !dst || row + rows > c->state_rows) return einval(c, "gemvq_state_read: range");
+    if (!c->usable) return unusable(c);
     hipSetDevice(c->device);
     hipError_t e = hipMemcpyAsync(dst, c->state + row * 128, rows * 512, hipMemcpyDeviceToHost, c->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    return e == hipSuccess ? 0 : fail(c, e, "state read");
+    return e == hipSuccess ? wait_stream(c, "state read") : fail(c, e, "state read");
 }
 
 int gemvq_state_clear(gemvq_ctx * c) {
     if (!c) return GEMVQ_EINVAL;
+    if (!c->usable) return unusable(c);
     if (!c->state_rows) return 0;
     hipSetDevice(c->device);
     hipError_t e = hipMemsetAsync(c->state, 0, c->state_rows * 512, c->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    return e == hipSuccess ? 0 : fail(c, e, "state clear");
+    return e == hipSuccess ? wait_stream(c, "state clear") : fail(c, e, "state clear");
 }
 
 int gemvq_kv_create(gemvq_ctx * c, int n_ctx, int n_head_kv, int head_dim) {
     if (!c || n_ctx <= 0 || n_head_kv <= 0 || head_dim <= 0 || head_dim > 256 || head_dim % 16)
         return einval(c, "gemvq_kv_create: shape");
+    if (!c->usable) return unusable(c);
     hipSetDevice(c->device);
     KvBuf b;
     b.n_ctx = n_ctx;
@@ -1380,6 +1427,7 @@ int gemvq_kv_create(gemvq_ctx * c, int n_ctx, int n_head_kv, int head_dim) {
 
 int gemvq_kv_read(gemvq_ctx * c, int kv, int pos0, int npos, uint16_t * k, uint16_t * v) {
     if (!c || kv < 0 || size_t(kv) >= c->kvs.size()) return einval(c, "gemvq_kv_read: buffer");
+    if (!c->usable) return unusable(c);
     const KvBuf & b = c->kvs[kv];
     if (pos0 < 0 || npos < 0 || pos0 + npos > b.n_ctx) return einval(c, "gemvq_kv_read: range");
     hipSetDevice(c->device);
@@ -1387,12 +1435,12 @@ int gemvq_kv_read(gemvq_ctx * c, int kv, int pos0, int npos, uint16_t * k, uint1
     hipError_t e = hipSuccess;
     if (k) e = hipMemcpyAsync(k, b.k + off, n * 2, hipMemcpyDeviceToHost, c->stream);
     if (e == hipSuccess && v) e = hipMemcpyAsync(v, b.v + off, n * 2, hipMemcpyDeviceToHost, c->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    return e == hipSuccess ? 0 : fail(c, e, "kv read");
+    return e == hipSuccess ? wait_stream(c, "kv read") : fail(c, e, "kv read");
 }
 
 int gemvq_kv_clear(gemvq_ctx * c) {
     if (!c) return GEMVQ_EINVAL;
+    if (!c->usable) return unusable(c);
     hipSetDevice(c->device);
     hipError_t e = hipSuccess;
     for (auto & b : c->kvs) {
@@ -1402,12 +1450,12 @@ int gemvq_kv_clear(gemvq_ctx * c) {
         const size_t heads = size_t(ATTN_MAXG) * b.n_head_kv * GEMM_MAX_TOK;  // every (token, q head) set, as created
         if (e == hipSuccess) e = hipMemsetAsync(b.counter, 0, heads * 4, c->stream);
     }
-    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    return e == hipSuccess ? 0 : fail(c, e, "kv clear");
+    return e == hipSuccess ? wait_stream(c, "kv clear") : fail(c, e, "kv clear");
 }
 
 int gemvq_run(gemvq_ctx * c, const uint32_t * cmds, unsigned n) {
     if (!c || (n && !cmds)) return einval(c, "gemvq_run: null argument");
+    if (!c->usable) return unusable(c);
     hipSetDevice(c->device);
     if (n == 0) {  // feature probe (gemvqc16.cpp:1076-1082)
         const uint32_t f[2] = {GEMVQ_FEATURES, GEMVQ_FEATURES2};
@@ -1421,8 +1469,10 @@ int gemvq_run(gemvq_ctx * c, const uint32_t * cmds, unsigned n) {
         return st;
     }
     hipError_t e = issue(ls, c->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    if (e == hipSuccess && c->dbg_used) {
+    if (e != hipSuccess) return fail(c, e, "run");
+    const int ws = wait_stream(c, "run");
+    if (ws) return ws;
+    if (c->dbg_used) {
         e = hipMemcpy(c->dbg_dst, c->dbg, c->dbg_n * 4, hipMemcpyDeviceToHost);
         c->dbg_dst = nullptr;
         c->dbg_used = false;
@@ -1432,6 +1482,7 @@ int gemvq_run(gemvq_ctx * c, const uint32_t * cmds, unsigned n) {
 
 int gemvq_graph_create(gemvq_ctx * c, const uint32_t * cmds, unsigned n, int * graph) {
     if (!c || !cmds || !graph || n == 0) return einval(c, "gemvq_graph_create: arguments");
+    if (!c->usable) return unusable(c);
     hipSetDevice(c->device);
     std::vector<Launch> ls;
     int32_t * const armed = c->dbg_dst;
@@ -1465,6 +1516,7 @@ int gemvq_graph_create(gemvq_ctx * c, const uint32_t * cmds, unsigned n, int * g
 int gemvq_graph_replay(gemvq_ctx * c, int graph, int times) {
     if (!c || graph < 0 || size_t(graph) >= c->graphs.size() || !c->graphs[graph] || times < 0)
         return einval(c, "gemvq_graph_replay: graph");
+    if (!c->usable) return unusable(c);
     hipSetDevice(c->device);
     for (int t = 0; t < times; ++t) {
         const hipError_t e = hipGraphLaunch(c->graphs[graph], c->stream);
@@ -1486,10 +1538,18 @@ int gemvq_graph_destroy(gemvq_ctx * c, int graph) {
 
 int gemvq_sync(gemvq_ctx * c) {
     if (!c) return GEMVQ_EINVAL;
+    if (!c->usable) return unusable(c);
     hipSetDevice(c->device);
-    const hipError_t e = hipStreamSynchronize(c->stream);
-    return e == hipSuccess ? 0 : fail(c, e, "sync");
+    return wait_stream(c, "sync");
 }
+
+int gemvq_set_wait_timeout(gemvq_ctx * c, unsigned ms) {
+    if (!c || ms == 0) return einval(c, "gemvq_set_wait_timeout: a positive number of milliseconds");
+    c->wait_ms = ms;
+    return 0;
+}
+
+int gemvq_usable(const gemvq_ctx * c) { return c && c->usable ? 1 : 0; }
 
 int gemvq_last_launch_count(const gemvq_ctx * c) { return c ? c->last_launches : -1; }
 
@@ -1508,6 +1568,7 @@ int gemvq_debug_blocksums(gemvq_ctx * c, int32_t * dst, size_t n) {
 int gemvq_graph_time(gemvq_ctx * c, int graph, int times, double * us) {
     if (!c || !us || times <= 0 || graph < 0 || size_t(graph) >= c->graphs.size() || !c->graphs[graph])
         return einval(c, "gemvq_graph_time: arguments");
+    if (!c->usable) return unusable(c);
     hipSetDevice(c->device);
     hipEvent_t a, b;
     hipEventCreate(&a);
@@ -1515,11 +1576,12 @@ int gemvq_graph_time(gemvq_ctx * c, int graph, int times, double * us) {
     hipError_t e = hipEventRecord(a, c->stream);
     for (int t = 0; t < times && e == hipSuccess; ++t) e = hipGraphLaunch(c->graphs[graph], c->stream);
     if (e == hipSuccess) e = hipEventRecord(b, c->stream);
-    if (e == hipSuccess) e = hipEventSynchronize(b);
+    const int ws = e == hipSuccess ? wait_stream(c, "graph time") : fail(c, e, "graph time");
     float ms = 0.0f;
-    if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+    if (ws == 0) e = hipEventElapsedTime(&ms, a, b);
     hipEventDestroy(a);
     hipEventDestroy(b);
+    if (ws) return ws;
     if (e != hipSuccess) return fail(c, e, "graph time");
     *us = double(ms) * 1000.0 / times;
     return 0;
@@ -1527,6 +1589,7 @@ int gemvq_graph_time(gemvq_ctx * c, int graph, int times, double * us) {
 
 int gemvq_profile(gemvq_ctx * c, const uint32_t * cmds, unsigned n, int reps, gemvq_launch_stat * out, int max_out) {
     if (!c || !cmds || n == 0 || reps <= 0) return einval(c, "gemvq_profile: arguments");
+    if (!c->usable) return unusable(c);
     hipSetDevice(c->device);
     std::vector<Launch> ls;
     std::vector<std::pair<int, int>> spans;
@@ -1543,18 +1606,20 @@ int gemvq_profile(gemvq_ctx * c, const uint32_t * cmds, unsigned n, int reps, ge
     std::vector<hipEvent_t> e0(L), e1(L);
     std::vector<double> sum(L, 0.0);
     hipError_t e = hipSuccess;
+    int ws = 0;
     for (size_t i = 0; i < L && e == hipSuccess; ++i) {
         e = hipEventCreate(&e0[i]);
         if (e == hipSuccess) e = hipEventCreate(&e1[i]);
     }
-    for (int r = 0; r < reps && e == hipSuccess; ++r) {
+    for (int r = 0; r < reps && e == hipSuccess && ws == 0; ++r) {
         for (size_t i = 0; i < L && e == hipSuccess; ++i) {
             g_prof_start = e0[i];
             g_prof_stop = e1[i];
             e = issue({ls[i]}, c->stream);
         }
         g_prof_start = g_prof_stop = nullptr;
-        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e == hipSuccess) ws = wait_stream(c, "profile");
+        if (ws) break;
         for (size_t i = 0; i < L && e == hipSuccess; ++i) {
             float ms = 0.0f;
             e = hipEventElapsedTime(&ms, e0[i], e1[i]);
@@ -1566,6 +1631,7 @@ int gemvq_profile(gemvq_ctx * c, const uint32_t * cmds, unsigned n, int reps, ge
         if (e0[i]) hipEventDestroy(e0[i]);
         if (e1[i]) hipEventDestroy(e1[i]);
     }
+    if (ws) return ws;
     if (e != hipSuccess) return fail(c, e, "profile");
     for (size_t i = 0; i < L && int(i) < max_out; ++i) {
         const auto d = describe(ls[i], pos);

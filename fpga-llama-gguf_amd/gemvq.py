@@ -28,7 +28,7 @@ GDN_WITH_GEMV, GDN_L2_QK, GDN_GATED, GDN_GATES, GDN_WITH_OUT, GDN_Z_SILU = 1, 2,
 NORM_L2, NORM_NO_WEIGHT, NORM_DEFER = 1, 2, 4
 SILU_MUL_SIGMOID = 1
 UNARY_SILU, UNARY_SIGMOID, UNARY_SOFTPLUS, UNARY_COPY = 1, 2, 3, 4
-EINVAL = -10000
+EINVAL, ETIMEDOUT, EUNUSABLE = -10000, -10001, -10002
 MAX_CMDS = 4096
 
 
@@ -172,6 +172,8 @@ def hip_lib() -> C.CDLL:
         _c_fn(lib, "gemvq_graph_replay", C.c_int, vp, C.c_int, C.c_int)
         _c_fn(lib, "gemvq_graph_destroy", C.c_int, vp, C.c_int)
         _c_fn(lib, "gemvq_sync", C.c_int, vp)
+        _c_fn(lib, "gemvq_set_wait_timeout", C.c_int, vp, C.c_uint)
+        _c_fn(lib, "gemvq_usable", C.c_int, vp)
         _c_fn(lib, "gemvq_last_launch_count", C.c_int, vp)
         _c_fn(lib, "gemvq_debug_blocksums", C.c_int, vp, vp, C.c_size_t)
         _c_fn(lib, "gemvq_graph_time", C.c_int, vp, C.c_int, C.c_int, C.POINTER(C.c_double))
@@ -359,6 +361,13 @@ class Context:
 
     def sync(self) -> None:
         self._check(self.lib.gemvq_sync(self.h), "sync")
+
+    def set_wait_timeout(self, ms: int) -> None:
+        """Bound of every wait for the device (a timed-out wait makes the context unusable)."""
+        self._check(self.lib.gemvq_set_wait_timeout(self.h, ms), "wait timeout")
+
+    def usable(self) -> bool:
+        return bool(self.lib.gemvq_usable(self.h))
 
     def launch_count(self) -> int:
         return self.lib.gemvq_last_launch_count(self.h)

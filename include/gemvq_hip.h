@@ -140,8 +140,19 @@ extern "C" {
 typedef struct gemvq_ctx gemvq_ctx;
 
 /* Status: 0 ok; > 0 the 1-based index of the first invalid command (nothing ran); GEMVQ_MAX_CMDS + 1 for a list
- * that is too long; < 0 a HIP error (negated hipError_t) or an argument error (GEMVQ_EINVAL). */
+ * that is too long; < 0 a HIP error (negated hipError_t), an argument error (GEMVQ_EINVAL), a wait for the device
+ * that passed its limit (GEMVQ_ETIMEDOUT), or a call on a context that a failed or timed-out device operation made
+ * unusable (GEMVQ_EUNUSABLE).
+ * Failure handling (replaces ggml-xrt.cpp:69-78, the GGML_XRT_WAIT_TIMEOUT_MS bound on every kernel wait, and the
+ * runtime_valid latch of ggml-xrt.cpp:1258-1264, 2761-2770): every wait for the device is bounded (default 180000
+ * ms, GEMVQ_WAIT_TIMEOUT_MS in the environment at create, or gemvq_set_wait_timeout). A HIP error from a launch, a
+ * copy or the stream, or a timed-out wait, latches the context unusable: every later call that would touch the
+ * device returns GEMVQ_EUNUSABLE (gemvq_last_error keeps the first failure) until gemvq_ctx_destroy, which waits for
+ * the device's outstanding work before it frees memory. Command lists rejected by validation (nothing launched) and
+ * argument errors do not latch. */
 #define GEMVQ_EINVAL (-10000)
+#define GEMVQ_ETIMEDOUT (-10001)
+#define GEMVQ_EUNUSABLE (-10002)
 
 /* Creates a context on HIP device `device` with an activation buffer of act_floats floats, a weight arena of
  * weight_bytes, and state_rows GDN state rows of 128 floats. Returns NULL on failure. */
@@ -182,6 +193,10 @@ int gemvq_graph_create(gemvq_ctx * ctx, const uint32_t * cmds, unsigned n_cmds, 
 int gemvq_graph_replay(gemvq_ctx * ctx, int graph, int times);
 int gemvq_graph_destroy(gemvq_ctx * ctx, int graph);
 int gemvq_sync(gemvq_ctx * ctx);
+/* The bound of every wait for the device, in milliseconds (> 0). */
+int gemvq_set_wait_timeout(gemvq_ctx * ctx, unsigned ms);
+/* 1 while the context accepts device work, 0 after a failed or timed-out device operation (or for NULL). */
+int gemvq_usable(const gemvq_ctx * ctx);
 /* Free and total HBM of a device (hipMemGetInfo); 0 or a negative HIP error. */
 int gemvq_device_memory(int device, size_t * free_bytes, size_t * total_bytes);
 

@@ -205,3 +205,15 @@ def test_activation_rounding_matches_roundf(tmp_path):
                     "round_check.c"), "-o", str(exe), "-lm"], check=True)
     n, bad = map(int, subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split())
     assert n == 2248146946 and bad == 0
+
+
+def test_wait_timeout_setting_is_validated(gq, libs, monkeypatch):
+    """The wait bound (ggml-xrt.cpp:69-78's GGML_XRT_WAIT_TIMEOUT_MS): a malformed GEMVQ_WAIT_TIMEOUT_MS fails the
+    create before any device call, with the reason; the setter rejects 0 and a NULL context; NULL is not usable."""
+    lib = gq.hip_lib()
+    for bad in ("0", "abc", "12x", "-5", ""):
+        monkeypatch.setenv("GEMVQ_WAIT_TIMEOUT_MS", bad)
+        assert not lib.gemvq_ctx_create(0, 1024, 0, 0), bad
+        assert b"GEMVQ_WAIT_TIMEOUT_MS" in lib.gemvq_last_error(None)
+    assert lib.gemvq_set_wait_timeout(None, 5) == gq.EINVAL
+    assert lib.gemvq_usable(None) == 0
