@@ -20,8 +20,9 @@
  * the parts the reference leaves on the CPU (attention core, embedding rows, greedy sampling) are listed below.
  *
  *   GEMV      [1, format | flags, rows, cols, w_off lo, w_off hi, x_off, y_off]
- *             format 2 Q4_0, 8 Q8_0, 13 Q5_K, 14 Q6_K; flags GEMVQ_GEMV_SWIGLU (0x100), GEMVQ_GEMV_CONV (0x200),
- *             GEMVQ_GEMV_ADD (0x400) as gemvqc16.h:31-45, and GEMVQ_GEMV_ARGMAX (0x800): the next command is an
+ *             format 2 Q4_0, 3 Q4_1 (Q8_1 activations), 8 Q8_0, 13 Q5_K, 14 Q6_K; flags GEMVQ_GEMV_SWIGLU
+ *             (0x100), GEMVQ_GEMV_CONV (0x200), GEMVQ_GEMV_ADD (0x400) as gemvqc16.h:31-45, and
+ *             GEMVQ_GEMV_ARGMAX (0x800): the next command is an
  *             ARGMAX over this GEMV's y (consumed; y is written), and GEMVQ_GEMV_SILU (0x1000): y = silu(W x) =
  *             v / (1 + e^-v) (the UNARY SiLU folded into the GEMV, no command consumed). Groups of up to 4 GEMVs with
  *             the same x_off, cols and format run as one pass; a group ends after a GEMV whose y overlaps x.
@@ -133,7 +134,7 @@ extern "C" {
 #define GEMVQ_MAX_COLS 16384u
 #define GEMVQ_MAX_CMDS 4096u
 /* Feature words (gemvqc16.h:126-134 layout, marker 0x6B51 / 0x6B52). */
-#define GEMVQ_FEATURES 0x6B51FFFBu
+#define GEMVQ_FEATURES 0x6B51FFFFu /* every format bit of the first word, Q4_1 (bit 2) included */
 #define GEMVQ_FEATURES2 0x6B52000Fu /* bit0 SILU_MUL sigmoid + strided g, bit1 ATTN/GET_ROWS/ARGMAX/NEXT_TOKEN,
                                        bit2 GEMM, bit3 ATTN and GET_ROWS n_tok */
 

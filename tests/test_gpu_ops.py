@@ -23,6 +23,8 @@ def test_features(gq, ctx):
     assert ctx.run([]) == 0
     f = ctx.read(0, 2, np.uint32)
     assert f[0] >> 16 == 0x6B51 and f[1] >> 16 == 0x6B52
+    # the format bits a planner checks before it offloads a type (ggml-xrt.cpp:341-375): Q5_K 1, Q6_K 2, Q4_1 4
+    assert f[0] & 7 == 7
     assert tuple(int(v) for v in f) == ctx.features()
 
 
