@@ -12,12 +12,13 @@
  *   - gemvq_features()       the n_cmds == 0 feature probe (gemvqc16.cpp:1076-1082, ggml-xrt.cpp:1284-1300).
  * Plain C types only; a context is not re-entrant (one host thread at a time, as the reference's backend mutex).
  *
- * Command list: GEMVQ_CMD_WORDS uint32 words per command, the opcodes and word layouts of gemvqc16.h:26-98 with
- * these differences: act offsets and lengths count floats and must be multiples of 16; a GEMV's w_off lo/hi is the
- * weight offset returned by gemvq_upload_weight (the matrix keeps its rows/cols/format from the upload and the
- * command must repeat them); GDN state rows index the state buffer (128 floats per row); there is no STATE_LOAD
- * prefetch need (the opcode is accepted and does nothing) and TRACE is accepted and does nothing. Opcodes added for
- * the parts the reference leaves on the CPU (attention core, embedding rows, greedy sampling) are listed below.
+ * Command list: GEMVQ_CMD_WORDS uint32 words per command, the opcodes and word layouts of gemvqc16.h:26-98, act
+ * offsets and lengths in floats and multiples of 16 as there (gemvqc16.h:24-25), with these differences: a GEMV's
+ * w_off lo/hi is the weight offset returned by gemvq_upload_weight (the matrix keeps its rows/cols/format from the
+ * upload and the command must repeat them); GDN state rows index the state buffer (128 floats per row); there is no
+ * STATE_LOAD prefetch need (the opcode is accepted and does nothing) and TRACE is accepted and does nothing. Opcodes
+ * added for the parts the reference leaves on the CPU (attention core, embedding rows, greedy sampling) are listed
+ * below.
  *
  *   GEMV      [1, format | flags, rows, cols, w_off lo, w_off hi, x_off, y_off]
  *             format 2 Q4_0, 3 Q4_1 (Q8_1 activations), 8 Q8_0, 13 Q5_K, 14 Q6_K; flags GEMVQ_GEMV_SWIGLU
