@@ -707,10 +707,10 @@ __device__ __forceinline__ void lane_partials(const Slot<TYPE, NU, PAIR> & R, in
     }
 }
 
-// The n (<= D) rows base, base + stride, ... of a chunk: the row totals are reduced together (lane group g holds row g), the
-// epilog runs once for all of them on the groups' first lanes, which store; CONV, whose operands sit in lanes 0-6
-// of ev[j], is finished row by row on lane 0. ev holds the rows' epilog operands, taken from the slots before
-// they were refilled.
+// The n (<= DS <= 4) rows base, base + stride, ... of a batch: the row totals are reduced together (lane group g holds
+// row g), the epilog runs once for all of them on the groups' first lanes, which store; CONV, whose operands sit in
+// lanes 0-6 of ev[j], is finished row by row on lane 0. ev holds the rows' epilog operands, taken from the slots
+// before they were refilled.
 template <int TYPE, int NU, bool PAIR, int EPI, int DS>
 __device__ __forceinline__ void finish_chunk(const GemvMember & m, bool argmax, int base, int stride, int n,
                                              const long long * p, const long long * p2, const float * ev, Ctx & c) {
@@ -772,35 +772,60 @@ __device__ __forceinline__ void finish_chunk(const GemvMember & m, bool argmax, 
     }
 }
 
-// The n rows w, w + S, w + 2 S, ... of one member (k-th row w + k S): slot j holds row k = kb + j; while more
-// than D rows remain, a slot is refilled with the row D further on as soon as its partial is formed
-// (unconditionally, so the waits stay exact); the last chunk only reduces.
+// Rows reduced and finished together: the partials of a batch of RB rows (RB/DS chunks of the DS rows in flight)
+// are kept and go through one cross-lane reduction and one epilog, whose cost is then shared by RB rows even when
+// fewer are in flight (finish_chunk takes at most 4 rows, and RB is a multiple of DS). Not for activations of more
+// than 8192 columns (NU >= 5): their larger per-lane activation and the batch's partials together pass 256 VGPRs
+// and halve the waves per SIMD.
+template <int DS, int NU>
+constexpr int batch_rows() { return DS >= 3 || NU >= 5 ? DS : 4; }
+
+// The n rows w, w + S, w + 2 S, ... of one member (k-th row w + k S): slot j holds row k = kb + i for the chunk of
+// rows i = ch DS + j of the batch starting at kb; a slot is refilled with the row DS further on as soon as its
+// partial is formed (unconditionally while a full batch follows, so the compiler's waits stay exact), and each
+// batch is reduced and finished once.
 template <int TYPE, int NU, bool PAIR, int EPI, int DS>
 __device__ __forceinline__ void run_rows(const GemvArgs & a, const GemvMember & m, int mi, int w, int S, int n,
                                          Slot<TYPE, NU, PAIR> * sl, const XB * xb, const XK * xk, Ctx & c) {
-
+    constexpr int RB = batch_rows<DS, NU>(), CH = RB / DS;
     const bool argmax = EPI == EPI_PLAIN && a.argmax_key != nullptr && mi == 0;
     int32_t * dbg = mi == 0 ? a.dbg : nullptr;
-    long long p[DS], p2[DS];
-    float ev[DS];
+    long long p[RB], p2[RB];
+    float ev[RB];
     int kb = 0;
-    for (; kb + DS < n; kb += DS) {
+    for (; kb + RB < n; kb += RB) {  // full batches with rows after them
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch)
+#pragma unroll
+            for (int j = 0; j < DS; ++j) {
+                const int i = ch * DS + j, k = kb + i;
+                p2[i] = 0;
+                lane_partials<TYPE, NU, PAIR, EPI>(sl[j], w + k * S, true, xb, xk, c, dbg, p[i], p2[i]);
+                ev[i] = sl[j].e;
+                load_slot<TYPE, NU, PAIR>(m, w + min(k + DS, n - 1) * S, c.lane, c.nb, c.nu, sl[j]);
+            }
+        finish_chunk<TYPE, NU, PAIR, EPI, RB>(m, argmax, w + kb * S, S, RB, p, p2, ev, c);
+    }
+    // the last batch (1 to RB rows): chunks past the last row are skipped, and a slot is refilled only for a chunk
+    // that has rows
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+        p[i] = p2[i] = 0;
+        ev[i] = 0.0f;
+    }
+#pragma unroll
+    for (int ch = 0; ch < CH; ++ch) {
+        if (ch > 0 && kb + ch * DS >= n) break;
 #pragma unroll
         for (int j = 0; j < DS; ++j) {
-            p2[j] = 0;
-            lane_partials<TYPE, NU, PAIR, EPI>(sl[j], w + (kb + j) * S, true, xb, xk, c, dbg, p[j], p2[j]);
-            ev[j] = sl[j].e;
-            load_slot<TYPE, NU, PAIR>(m, w + min(kb + DS + j, n - 1) * S, c.lane, c.nb, c.nu, sl[j]);
+            const int i = ch * DS + j, k = kb + i;
+            lane_partials<TYPE, NU, PAIR, EPI>(sl[j], w + k * S, k < n, xb, xk, c, dbg, p[i], p2[i]);
+            ev[i] = sl[j].e;
+            if (ch + 1 < CH && kb + (ch + 1) * DS < n)
+                load_slot<TYPE, NU, PAIR>(m, w + min(k + DS, n - 1) * S, c.lane, c.nb, c.nu, sl[j]);
         }
-        finish_chunk<TYPE, NU, PAIR, EPI, DS>(m, argmax, w + kb * S, S, DS, p, p2, ev, c);
     }
-#pragma unroll
-    for (int j = 0; j < DS; ++j) {
-        p2[j] = 0;
-        lane_partials<TYPE, NU, PAIR, EPI>(sl[j], w + (kb + j) * S, kb + j < n, xb, xk, c, dbg, p[j], p2[j]);
-        ev[j] = sl[j].e;
-    }
-    finish_chunk<TYPE, NU, PAIR, EPI, DS>(m, argmax, w + kb * S, S, min(DS, n - kb), p, p2, ev, c);
+    finish_chunk<TYPE, NU, PAIR, EPI, RB>(m, argmax, w + kb * S, S, min(RB, n - kb), p, p2, ev, c);
 }
 
 // The rows of a wave whose block terms could pass 2^53 LSB (see the kernel): one row at a time, each loaded, summed
