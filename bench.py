@@ -324,6 +324,37 @@ def configs(args) -> int:
 # ---------------------------------------------------------------------------------------------------------------
 # The batched GEMV (GEMM command) on the C5 layer shapes: M tokens per weight read, over rotated weight copies
 # (>= 512 MB) in one graph, against M single-token GEMVs of the same rows.
+def sequences(args) -> int:
+    """Lockstep decode of n sequences of the C5 model (gemvq_qwen35_batch_*): aggregate tokens/s over all of them.
+    Each sequence starts from its own 16-id prompt (consumed by the same steps); timed: --steps steps after the
+    prompts, every step one token per sequence. One JSON line per sequence count."""
+    counts = [int(v) for v in args.sequences.split(",")]
+    cfg = Q.Config(n_layer=args.layers, n_ctx=16 + args.warmup + args.steps + 8)
+    t = time.perf_counter()
+    blob = Q.generate(cfg, seed=0, threads=args.threads)
+    log(f"generated the synthetic model ({blob.data.size / 1e9:.2f} GB) in {time.perf_counter() - t:.1f} s")
+    wbytes = Q.weight_bytes(cfg)
+    for n in counts:
+        prompts = [Q.prompt_ids(cfg, 16, seed=100 + s) for s in range(n)]
+        with Q.BatchModel(blob, n) as bm:
+            bm.reset(prompts)
+            bm.step(15 + args.warmup)  # the prompts, then the untimed steps (captures the graph)
+            bm.sync()
+            t0 = time.perf_counter()
+            bm.step(args.steps)
+            bm.sync()
+            dt = time.perf_counter() - t0
+            launches = bm.ctx.launch_count()
+        tok_s = n * args.steps / dt
+        print(json.dumps({"sequences_decode": n, "tokens_per_s": round(tok_s, 1), "steps": args.steps,
+                          "ms_per_step": round(dt * 1e3 / args.steps, 4), "launches_per_step": launches,
+                          "weight_GBps_per_step": round(wbytes / (dt / args.steps) / 1e9, 1),
+                          "workload": "C5 model (32 layers, Q4_0 layers, Q6_K head: one GEMV per sequence), "
+                                      "16-id prompts then timed lockstep steps", "data": "synthetic"}), flush=True)
+        log(f"{n} sequences: {tok_s:.1f} tokens/s aggregate ({dt * 1e3 / args.steps:.3f} ms per step)")
+    return 0
+
+
 def batched(args) -> int:
     shapes = [("FFN gate/up pair 2x12288x4096 (+ norm)", 12288, 4096, True),
               ("FFN down 4096x12288 (+ residual)", 4096, 12288, False),
@@ -400,7 +431,11 @@ def main() -> int:
                     help="only time the single-op configurations C1-C4 (one JSON line each) and exit")
     ap.add_argument("--batched", action="store_true",
                     help="only time the batched GEMV on the C5 layer shapes at 1..32 tokens and exit")
+    ap.add_argument("--sequences", default="", metavar="N[,N...]",
+                    help="only time lockstep decode of N sequences of the C5 model (aggregate tokens/s) and exit")
     args = ap.parse_args()
+    if args.sequences:
+        return sequences(args)
     if args.batched:
         return batched(args)
     if args.copy_probe:

@@ -105,6 +105,7 @@ struct ConvArgs {
     int ch;
     int silu;
     int n_tok;  // token rows of x and y (ch floats apart), run in order: each token's window ends at its row
+    int seqs;   // nonzero: token t belongs to sequence t, whose window is at s_src / s_dst + 3 * ch * t
 };
 
 struct RopeArgs {
@@ -131,6 +132,8 @@ struct GdnArgs {
     int flags;
     int n_tok;             // tokens run in order on the same state
     int s_qkv, s_gb, s_y;  // row strides (floats) between tokens of q / k / v, of g / beta, of y
+    int seqs;              // nonzero: the tokens belong to n_tok sequences, token t on its own state rows (src and
+                           // dst + t * hv * 128 rows), all in one launch
 };
 
 // The DeltaNet step, its gated output norm and the ssm_out product in one launch (the reference's GDN_WITH_OUT,
@@ -185,6 +188,9 @@ struct AttnArgs {
     // head_dim; its partials and counters follow those of token t - 1 (part and counter hold n_tok sets).
     int n_tok;
     float * qr;           // n_tok > 1: normalized, rotated, fp16-rounded q rows [n_tok][n_head][head_dim]
+    // seq_ctx > 0: token t belongs to sequence t: its position is pos[16 t], and its keys and values are positions
+    // [t * seq_ctx, (t + 1) * seq_ctx) of the cache (n_ctx is then the capacity of one sequence, seq_ctx)
+    int seq_ctx;
 };
 
 struct GetRowsArgs {
@@ -203,6 +209,11 @@ struct NextTokenArgs {
     int n_prompt;
     int32_t * out;
     int max_pos;
+    // n_seq > 1: sequence t's key, token and position at key + 8 t (16 floats), tok + 16 t, pos + 16 t; its prompt
+    // (n_prompt_of[16 t] ids) at prompt + t * seq_cap and its token ids at out + t * seq_cap (max_pos = seq_cap)
+    int n_seq;
+    const int32_t * n_prompt_of;
+    int seq_cap;
 };
 
 // Batched GEMV (n_tok tokens per weight read): the activation rows are quantized once into Q8_0 blocks whose 32
@@ -275,7 +286,7 @@ hipError_t launch_gdn_out(const GdnOutArgs & a, int type, hipStream_t s);
 int gdn_out_parts(int rows);  // workgroups per head for an ssm_out of `rows` rows
 hipError_t launch_attn(const AttnArgs & a, hipStream_t s);
 hipError_t launch_get_rows(const GetRowsArgs & a, hipStream_t s);
-hipError_t launch_argmax(const float * x, int n, unsigned long long * key, hipStream_t s);
+hipError_t launch_argmax(const float * x, int n, unsigned long long * key, int rows, int stride, hipStream_t s);
 hipError_t launch_next_token(const NextTokenArgs & a, hipStream_t s);
 hipError_t launch_gemm_quant(const GemmQuantArgs & a, hipStream_t s);
 hipError_t launch_gemm(const GemmArgs & a, int type, hipStream_t s);

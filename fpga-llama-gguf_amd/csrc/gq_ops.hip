@@ -64,9 +64,18 @@ __global__ void ew_kernel(EwArgs a) {
 
 // ---- CONV opcode (gemvqc_ops.h:387-431): window [state (3), x], summed from t = 0; n_tok tokens in order, the
 // state moving one place per token ----
+// With seqs, token t is the one token of sequence t (grid y): its own window in, its own window out.
 __global__ void conv_kernel(ConvArgs a) {
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
     if (c >= a.ch) return;
+    if (a.seqs) {
+        const size_t t = blockIdx.y, so = 3 * size_t(a.ch) * t;
+        a.s_src += so;
+        a.s_dst += so;
+        a.x += t * size_t(a.ch);
+        a.y += t * size_t(a.ch);
+        a.n_tok = 1;
+    }
     float s0 = a.s_src[3 * c], s1 = a.s_src[3 * c + 1], s2 = a.s_src[3 * c + 2];
     const float w0 = a.w[4 * c], w1 = a.w[4 * c + 1], w2 = a.w[4 * c + 2], w3 = a.w[4 * c + 3];
     // every token's input is requested before the first output is stored (y may be x: a token's output replaces
@@ -164,8 +173,21 @@ __device__ __forceinline__ void gdn_token(const GdnArgs & a, const GdnIn & in, i
     }
 }
 
+// With seqs, grid y is the token: token t is the one token of sequence t on its own state rows.
 __global__ __launch_bounds__(128) void gdn_kernel(GdnArgs a) {
     constexpr int IT = GDN_IT;
+    if (a.seqs) {
+        const size_t t = blockIdx.y, so = size_t(a.hv) * 128 * 128 * t;
+        a.src += so;
+        a.dst += so;
+        a.q += t * size_t(a.s_qkv);
+        a.k += t * size_t(a.s_qkv);
+        a.v += t * size_t(a.s_qkv);
+        a.g += t * size_t(a.s_gb);
+        a.beta += t * size_t(a.s_gb);
+        a.y += t * size_t(a.s_y);
+        a.n_tok = 1;
+    }
     const int chunks = 128 / GDN_ROWS;
     const int h = blockIdx.x / chunks, chunk = blockIdx.x % chunks, kh = h % a.hk;
     const int l16 = threadIdx.x & 15, grp = threadIdx.x >> 4;  // 8 row groups
@@ -254,7 +276,7 @@ template <int HD>
 __global__ __launch_bounds__(ATT_T) void attn_append_kernel(AttnArgs a) {
     __shared__ float xs[HD];
     __shared__ float red[4];
-    const int s = blockIdx.x, t = blockIdx.y, pos = *a.pos + t;
+    const int s = blockIdx.x, t = blockIdx.y, pos = a.seq_ctx ? a.pos[16 * t] : *a.pos + t;
     if (pos < 0 || pos >= a.n_ctx) return;  // positions past the KV capacity are not stored
     const bool isq = s < a.n_head;
     const int h = isq ? s : s - a.n_head;
@@ -283,7 +305,8 @@ __global__ __launch_bounds__(ATT_T) void attn_append_kernel(AttnArgs a) {
     if (isq) {
         a.qr[(size_t(t) * a.n_head + h) * HD + e] = h2f(f2h(rv));
     } else {
-        const size_t off = (size_t(pos) * a.n_head_kv + h) * HD + e;
+        const size_t cpos = a.seq_ctx ? size_t(t) * a.seq_ctx + pos : size_t(pos);  // the token's sequence region
+        const size_t off = (cpos * a.n_head_kv + h) * HD + e;
         a.kc[off] = uint16_t(f2h(rv));
         a.vc[off] = uint16_t(f2h(vv));
     }
@@ -549,8 +572,11 @@ __global__ void get_rows_kernel(GetRowsArgs a) {
     }
 }
 
-__global__ __launch_bounds__(256) void argmax_kernel(const float * x, int n, unsigned long long * key) {
+// Grid y: row r of x (stride floats apart), its key at key + 8 r (16 floats).
+__global__ __launch_bounds__(256) void argmax_kernel(const float * x, int n, unsigned long long * key, int stride) {
     __shared__ unsigned long long red[4];
+    x += size_t(blockIdx.y) * stride;
+    key += size_t(blockIdx.y) * 8;
     unsigned long long best = 0;
     for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
         const unsigned long long k = argmax_key(x[i], uint32_t(i));
@@ -569,7 +595,19 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float * x, int n, uns
     }
 }
 
+// With n_seq > 1, thread t serves sequence t.
 __global__ void next_token_kernel(NextTokenArgs a) {
+    if (a.n_seq > 1) {
+        const int t = threadIdx.x;
+        if (t >= a.n_seq) return;
+        a.key += 8 * t;
+        a.tok += 16 * t;
+        a.pos += 16 * t;
+        a.prompt += size_t(t) * a.seq_cap;
+        a.out += size_t(t) * a.seq_cap;
+        a.n_prompt = a.n_prompt_of[16 * t];
+        a.max_pos = a.seq_cap;
+    }
     const int pos = *a.pos;
     const unsigned long long k = *a.key;
     int tok = int(0xffffffffu - uint32_t(k & 0xffffffffu));
@@ -595,7 +633,7 @@ hipError_t launch_ew(const EwArgs & a, hipStream_t s) {
 }
 
 hipError_t launch_conv(const ConvArgs & a, hipStream_t s) {
-    GQ_LAUNCH(conv_kernel, dim3((a.ch + 255) / 256), dim3(256), 0, s, a);
+    GQ_LAUNCH(conv_kernel, dim3((a.ch + 255) / 256, a.seqs ? a.n_tok : 1), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -607,7 +645,7 @@ hipError_t launch_rope(const RopeArgs & a, hipStream_t s) {
 }
 
 hipError_t launch_gdn(const GdnArgs & a, hipStream_t s) {
-    GQ_LAUNCH(gdn_kernel, dim3(a.hv * (128 / GDN_ROWS)), dim3(128), 0, s, a);
+    GQ_LAUNCH(gdn_kernel, dim3(a.hv * (128 / GDN_ROWS), a.seqs ? a.n_tok : 1), dim3(128), 0, s, a);
     return hipGetLastError();
 }
 
@@ -634,7 +672,14 @@ __global__ __launch_bounds__(ATT_T) void attn_group_kernel(AttnArgs a) {
     const int G = a.n_head / a.n_head_kv, b = blockIdx.x;
     const int u = (b / (8 * G)) * 8 + (b & 7), g = (b >> 3) % G;
     const int kvh = u % a.n_head_kv, chunk = u / a.n_head_kv, hq = kvh * G + g;
-    const int pos0 = *a.pos, tk0 = int(blockIdx.y) * ATTN_TG, tk1 = min(tk0 + ATTN_TG, a.n_tok);
+    // with sequences a group is one token, whose position is its own and whose keys and values are its sequence's
+    const int tg = a.seq_ctx ? 1 : ATTN_TG, tk0 = int(blockIdx.y) * tg, tk1 = min(tk0 + tg, a.n_tok);
+    const int pos0 = a.seq_ctx ? a.pos[16 * tk0] - tk0 : *a.pos;  // token t at pos0 + t
+    if (a.seq_ctx) {
+        const size_t ro = size_t(tk0) * a.seq_ctx * a.n_head_kv * HD;
+        a.kc += ro;
+        a.vc += ro;
+    }
     const int first = max(pos0 + tk0, 0), plast = min(pos0 + tk1 - 1, a.n_ctx - 1);  // the group's stored positions
     if (first > plast || chunk >= (plast + ATTN_CHUNK) / ATTN_CHUNK) return;
     const int tid = threadIdx.x, pc = tid % PER;
@@ -675,7 +720,8 @@ hipError_t launch_attn_hd(const AttnArgs & a, dim3 grid, hipStream_t s) {
         return hipGetLastError();
     }
     GQ_LAUNCH(attn_append_kernel<HD>, dim3(a.n_head + a.n_head_kv, grid.y), dim3(ATT_T), 0, s, a);
-    GQ_LAUNCH(attn_group_kernel<HD>, dim3(grid.x, (grid.y + ATTN_TG - 1) / ATTN_TG), dim3(ATT_T), 0, s, a);
+    const int tg = a.seq_ctx ? 1 : ATTN_TG;
+    GQ_LAUNCH(attn_group_kernel<HD>, dim3(grid.x, (grid.y + tg - 1) / tg), dim3(ATT_T), 0, s, a);
     return hipGetLastError();
 }
 
@@ -703,15 +749,15 @@ hipError_t launch_get_rows(const GetRowsArgs & a, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_argmax(const float * x, int n, unsigned long long * key, hipStream_t s) {
+hipError_t launch_argmax(const float * x, int n, unsigned long long * key, int rows, int stride, hipStream_t s) {
     int grid = (n + 255) / 256;
     grid = grid < 256 ? grid : 256;
-    GQ_LAUNCH(argmax_kernel, dim3(grid), dim3(256), 0, s, x, n, key);
+    GQ_LAUNCH(argmax_kernel, dim3(grid, rows), dim3(256), 0, s, x, n, key, stride);
     return hipGetLastError();
 }
 
 hipError_t launch_next_token(const NextTokenArgs & a, hipStream_t s) {
-    GQ_LAUNCH(next_token_kernel, dim3(1), dim3(1), 0, s, a);
+    GQ_LAUNCH(next_token_kernel, dim3(1), dim3(a.n_seq > 1 ? ((a.n_seq + 63) / 64) * 64 : 1), 0, s, a);
     return hipGetLastError();
 }
 

@@ -79,7 +79,7 @@ struct LGdnOut { GdnOutArgs a; int type; };
 struct LGated { GatedNormArgs a; };
 struct LAttn { AttnArgs a; };
 struct LRows { GetRowsArgs a; };
-struct LArgmax { const float * x; int n; unsigned long long * key; };
+struct LArgmax { const float * x; int n; unsigned long long * key; int rows, stride; };
 struct LNext { NextTokenArgs a; };
 struct LGemmQ { GemmQuantArgs a; };
 struct LGemm { GemmArgs a; int type; };
@@ -344,7 +344,7 @@ struct Compiler {
             case GEMVQ_OP_CONV: {
                 const uint64_t nt = (k[7] >> 16) ? (k[7] >> 16) : 1;
                 wr.push_back({k[4], k[4] + uint64_t(k[1]) * nt});
-                wr.push_back({k[6], k[6] + 3ull * k[1]});
+                wr.push_back({k[6], k[6] + 3ull * k[1] * ((k[7] & GEMVQ_CONV_SEQS) ? nt : 1)});
                 break;
             }
             case GEMVQ_OP_ROPE: wr.push_back({k[4], k[4] + uint64_t(k[5]) * k[6]}); break;
@@ -367,13 +367,15 @@ struct Compiler {
                 wr.push_back({k[7], k[7] + uint64_t(k[3]) * nt});
                 break;
             }
-            case GEMVQ_OP_ARGMAX: wr.push_back({k[3], k[3] + 2}); break;
-            case GEMVQ_OP_NEXT_TOKEN:
-                wr.push_back({k[1], k[1] + 2});
-                wr.push_back({k[2], k[2] + 1});
-                wr.push_back({k[3], k[3] + 1});
-                wr.push_back({k[6], c->act_floats});
+            case GEMVQ_OP_ARGMAX: wr.push_back({k[3], k[3] + 16ull * ((k[4] ? k[4] : 1) - 1) + 2}); break;
+            case GEMVQ_OP_NEXT_TOKEN: {
+                const uint64_t ns = (k[7] & 0xffu) > 1 ? (k[7] & 0xffu) : 1, sl = 16 * (ns - 1);
+                wr.push_back({k[1], k[1] + sl + 2});
+                wr.push_back({k[2], k[2] + sl + 1});
+                wr.push_back({k[3], k[3] + sl + 1});
+                wr.push_back({k[6], ns > 1 ? k[6] + uint64_t(k[7] >> 8) * ns : c->act_floats});
                 break;
+            }
             case GEMVQ_OP_GEMM:
                 if (k2) wr.push_back({k[7], k[7] + uint64_t(k2[2]) * (k2[0] ? k2[0] - 1 : 0) + k[2]});
                 step = 2;
@@ -605,9 +607,10 @@ struct Compiler {
                     !range(k[6], uint64_t(sg) * (ntok - 1) + hv) || !range(k[7], yz + hv * 128))
                     return reject(i, "GDN range");
                 const uint64_t src = k2[0], dst = k2[1];
-                if (src + uint64_t(hv) * 128 > c->state_rows || dst + uint64_t(hv) * 128 > c->state_rows)
-                    return reject(i, "GDN state rows");
-                if (src != dst && (src < dst + hv * 128ull && dst < src + hv * 128ull)) return reject(i, "GDN state overlap");
+                const bool seqs = flags & GEMVQ_GDN_SEQS;  // token t of sequence t on state rows + t hv 128
+                const uint64_t srows = uint64_t(hv) * 128 * (seqs ? ntok : 1);
+                if (src + srows > c->state_rows || dst + srows > c->state_rows) return reject(i, "GDN state rows");
+                if (src != dst && (src < dst + srows && dst < src + srows)) return reject(i, "GDN state overlap");
                 if (gates && (!range(k3[0], hv) || !range(k3[1], hv))) return reject(i, "GDN gates range");
                 if ((flags & GEMVQ_GDN_GATED) && (!range(k2[6], 128) || !range(k2[7], yz + hv * 128))) return reject(i, "GDN gated range");
                 GdnArgs a{};
@@ -630,6 +633,7 @@ struct Compiler {
                 a.s_qkv = int(sq);
                 a.s_gb = int(sg);
                 a.s_y = int(hv * 128);
+                a.seqs = int(seqs && ntok > 1);
                 const unsigned next = i + (gates ? 3 : 2);
                 uint32_t fy = 0, fres = 0;
                 if ((flags & GEMVQ_GDN_GATED) && (flags & GEMVQ_GDN_WITH_OUT) && ntok == 1 && !accp.on &&
@@ -681,11 +685,14 @@ struct Compiler {
             }
             case GEMVQ_OP_CONV: {
                 const uint32_t ch = k[1], ntok = (k[7] >> 16) ? (k[7] >> 16) : 1;  // packed token rows
+                const bool seqs = k[7] & GEMVQ_CONV_SEQS;  // token t of sequence t: windows packed, 3 ch apart
+                const uint64_t sw = 3ull * ch * (seqs ? ntok : 1);
                 if (ch == 0 || ch % 16 || ntok > GEMVQ_GEMM_MAX_TOK || !range(k[2], uint64_t(ch) * ntok) ||
-                    !range(k[3], 4ull * ch) || !range(k[4], uint64_t(ch) * ntok) || !range(k[5], 3ull * ch) ||
-                    !range(k[6], 3ull * ch))
+                    !range(k[3], 4ull * ch) || !range(k[4], uint64_t(ch) * ntok) || !range(k[5], sw) ||
+                    !range(k[6], sw))
                     return reject(i, "CONV range");
-                ConvArgs a{A(k[2]), A(k[3]), A(k[5]), A(k[6]), A(k[4]), int(ch), int(k[7] & 1), int(ntok)};
+                if (seqs && k[5] != k[6] && meet({k[5], k[5] + sw}, {k[6], k[6] + sw})) return reject(i, "CONV state overlap");
+                ConvArgs a{A(k[2]), A(k[3]), A(k[5]), A(k[6]), A(k[4]), int(ch), int(k[7] & 1), int(ntok), int(seqs)};
                 out.push_back(LConv{a});
                     spans.push_back({int(i), 1});
                 break;
@@ -717,10 +724,13 @@ struct Compiler {
                     return reject(i, "ATTN shape");
                 const uint32_t qstride = (flags & 1) ? 2 * hd : hd, ntok = (flags >> 16) & 0xffu ? (flags >> 16) & 0xffu : 1;
                 if (ntok > GEMVQ_GEMM_MAX_TOK) return reject(i, "ATTN tokens");
+                // token t of sequence t: position at pos + 16 t, the cache split into ntok equal regions
+                const bool seqs = (flags & GEMVQ_ATTN_SEQS) && ntok > 1;
+                if (seqs && (b.n_ctx % int(ntok) || !range(k[6], 16ull * (ntok - 1) + 1))) return reject(i, "ATTN sequences");
                 const uint64_t qt = uint64_t(nh) * qstride * (ntok - 1), kvt = uint64_t(nkv) * hd * ntok;  // packed tokens
                 if (!range(k[2], qt + uint64_t(qstride) * (nh - 1) + hd) || !range(k[4], uint64_t(nh) * hd * ntok) ||
                     !range(k[6], 1) || !range(k2[0], kvt) || !range(k2[1], kvt) || !range(k2[4], hd) ||
-                    !range(k2[5], hd) || k2[6] + uint64_t(b.n_ctx) * nrot > c->act_floats)
+                    !range(k2[5], hd) || k2[6] + uint64_t(seqs ? b.n_ctx / int(ntok) : b.n_ctx) * nrot > c->act_floats)
                     return reject(i, "ATTN range");
                 if ((flags & 1) && !range(k2[7], qt + uint64_t(2 * hd) * (nh - 1) + hd)) return reject(i, "ATTN gate range");
                 AttnArgs a{};
@@ -742,7 +752,8 @@ struct Compiler {
                 a.head_dim = int(hd);
                 a.n_rot = int(nrot);
                 a.q_stride = int(qstride);
-                a.n_ctx = b.n_ctx;
+                a.n_ctx = seqs ? b.n_ctx / int(ntok) : b.n_ctx;
+                a.seq_ctx = seqs ? a.n_ctx : 0;
                 a.scale = bits_f(k2[2]);
                 a.eps = bits_f(k2[3]);
                 a.n_tok = int(ntok);
@@ -773,12 +784,36 @@ struct Compiler {
                 break;
             }
             case GEMVQ_OP_ARGMAX: {
-                if (k[1] == 0 || !range(k[2], k[1]) || !range(k[3], 2)) return reject(i, "ARGMAX range");
-                out.push_back(LArgmax{A(k[2]), int(k[1]), reinterpret_cast<unsigned long long *>(A(k[3]))});
+                const uint32_t rows = k[4] ? k[4] : 1, stride = rows > 1 ? k[5] : 0;  // rows: keys 16 floats apart
+                if (k[1] == 0 || rows > GEMVQ_GEMM_MAX_TOK || (rows > 1 && (stride < k[1] || stride % 16)) ||
+                    !range(k[2], uint64_t(stride) * (rows - 1) + k[1]) || !range(k[3], 16ull * (rows - 1) + 2))
+                    return reject(i, "ARGMAX range");
+                out.push_back(LArgmax{A(k[2]), int(k[1]), reinterpret_cast<unsigned long long *>(A(k[3])), int(rows),
+                                      int(stride)});
                 spans.push_back({int(i), 1});
                 break;
             }
             case GEMVQ_OP_NEXT_TOKEN: {
+                const uint32_t ns = k[7] & 0xffu, cap = k[7] >> 8;  // sequences (2..): slots 16 floats apart
+                if (ns > 1) {
+                    const uint64_t sl = 16ull * (ns - 1);
+                    if (ns > GEMVQ_GEMM_MAX_TOK || cap == 0 || !range(k[1], sl + 2) || !range(k[2], sl + 1) ||
+                        !range(k[3], sl + 1) || !range(k[5], sl + 1) || !range(k[4], uint64_t(cap) * ns) ||
+                        !range(k[6], uint64_t(cap) * ns))
+                        return reject(i, "NEXT_TOKEN sequences");
+                    NextTokenArgs a{};
+                    a.key = reinterpret_cast<unsigned long long *>(A(k[1]));
+                    a.tok = reinterpret_cast<int32_t *>(A(k[2]));
+                    a.pos = reinterpret_cast<int32_t *>(A(k[3]));
+                    a.prompt = reinterpret_cast<const int32_t *>(A(k[4]));
+                    a.out = reinterpret_cast<int32_t *>(A(k[6]));
+                    a.n_seq = int(ns);
+                    a.n_prompt_of = reinterpret_cast<const int32_t *>(A(k[5]));
+                    a.seq_cap = int(cap);
+                    out.push_back(LNext{a});
+                    spans.push_back({int(i), 1});
+                    break;
+                }
                 if (!range(k[1], 2) || !range(k[2], 1) || !range(k[3], 1) || (k[5] && !range(k[4], k[5])) ||
                     !range(k[6], 1))
                     return reject(i, "NEXT_TOKEN range");
@@ -1155,7 +1190,7 @@ std::pair<std::string, uint64_t> describe(const Launch & l, int pos) {
     }
     if (auto * x = std::get_if<LRows>(&l))
         return {"get_rows_kernel", uint64_t(x->a.cols) * 4 + gguf_row_bytes(x->a.type, x->a.cols)};
-    if (auto * x = std::get_if<LArgmax>(&l)) return {"argmax_kernel", uint64_t(x->n) * 4};
+    if (auto * x = std::get_if<LArgmax>(&l)) return {"argmax_kernel", uint64_t(x->n) * 4 * uint64_t(x->rows)};
     if (auto * x = std::get_if<LGemmQ>(&l)) {
         const GemmQuantArgs & a = x->a;
         return {"gemm_quant_kernel", uint64_t(a.n_tok) * a.cols * (4 + 1) + uint64_t(a.n_tok) * (a.cols / 32) * 4 +
@@ -1187,7 +1222,7 @@ hipError_t issue(const std::vector<Launch> & ls, hipStream_t s) {
         else if (auto * x = std::get_if<LGated>(&l)) e = launch_gated_norm(x->a, s);
         else if (auto * x = std::get_if<LAttn>(&l)) e = launch_attn(x->a, s);
         else if (auto * x = std::get_if<LRows>(&l)) e = launch_get_rows(x->a, s);
-        else if (auto * x = std::get_if<LArgmax>(&l)) e = launch_argmax(x->x, x->n, x->key, s);
+        else if (auto * x = std::get_if<LArgmax>(&l)) e = launch_argmax(x->x, x->n, x->key, x->rows, x->stride, s);
         else if (auto * x = std::get_if<LNext>(&l)) e = launch_next_token(x->a, s);
         else if (auto * x = std::get_if<LGemmQ>(&l)) e = launch_gemm_quant(x->a, s);
         else if (auto * x = std::get_if<LGemm>(&l)) e = launch_gemm(x->a, x->type, s);

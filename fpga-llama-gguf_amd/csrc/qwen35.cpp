@@ -59,6 +59,11 @@ struct gemvq_qwen35 {
     uint32_t bh = 0, bqkv = 0, bcqkv = 0, bz = 0, bbeta = 0, balpha = 0, by = 0, bqg = 0, bk = 0, bv = 0, batt = 0,
              bffn = 0, bid = 0, bpos = 0;
     std::vector<int32_t> prompt_ids;
+    // lockstep decode of n_seq sequences (gemvq_qwen35_batch_create): per sequence, 16 floats apart, its key
+    // (skey), position (spos) and prompt length (slen); its prompt, token ids and logits in regions of n_ctx
+    // (n_vocab) floats; its conv windows, DeltaNet state rows and KV region follow those of the sequence before
+    int n_seq = 1;
+    uint32_t skey = 0, spos = 0, slen = 0, sprompt = 0, sout = 0, slogits = 0;
 };
 
 namespace {
@@ -89,9 +94,10 @@ size_t layout(gemvq_qwen35 & m, const gemvq_tensor_desc * tab, int n) {
         x.act_off = take(size_t(tab[i].ne0) * size_t(tab[i].ne1 > 0 ? tab[i].ne1 : 1));
     }
     const int ch = conv_ch(c), S = c.ssm_head_dim, hv = c.ssm_v_heads;
+    const size_t ns = size_t(m.n_seq);
     m.conv_state.assign(c.n_layer, 0);
     for (int il = 0; il < c.n_layer; ++il)
-        if (!is_attn(c, il)) m.conv_state[il] = take(size_t(ch) * 3);
+        if (!is_attn(c, il)) m.conv_state[il] = take(size_t(ch) * 3 * ns);
     m.rope = take(size_t(c.n_ctx) * c.n_rot);
     m.prompt = take(size_t(c.n_ctx));
     m.out = take(size_t(c.n_ctx) + 16);
@@ -124,6 +130,14 @@ size_t layout(gemvq_qwen35 & m, const gemvq_tensor_desc * tab, int n) {
     m.bffn = take(B * c.n_ff);
     m.bid = take(B * 16);
     m.bpos = take(16);
+    if (m.n_seq > 1) {
+        m.skey = take(ns * 16);
+        m.spos = take(ns * 16);
+        m.slen = take(ns * 16);
+        m.sprompt = take(ns * size_t(c.n_ctx));
+        m.sout = take(ns * size_t(c.n_ctx));
+        m.slogits = take(ns * size_t(c.n_vocab));
+    }
     return off;
 }
 
@@ -222,6 +236,56 @@ bool build_chunk(const gemvq_qwen35 & m, uint32_t ntok, std::vector<uint32_t> & 
         e.gemm(*W(p + "ffn_up.weight"), m.bh, E, m.bffn, F, ntok, 0, 0, 0, pn, eps);
         e.gemm(*W(p + "ffn_down.weight"), m.bffn, F, m.bh, E, ntok, GEMVQ_GEMV_ADD, m.bh, E);
     }
+    return true;
+}
+
+// One lockstep step of n_seq sequences, token t of sequence t: the chunk's GEMM projections over the n_seq token
+// rows; CONV, the DeltaNet step and attention in their sequences forms (each token on its own sequence's conv
+// window, state rows, KV region and position); the output norm and head per sequence; the argmax of every
+// sequence's logits and NEXT_TOKEN over all of them (the prompt token while one is left, else the argmax). Each
+// sequence's ids, logits, states and cache are those of a single-sequence decode of its prompt, bit for bit.
+bool build_batch(gemvq_qwen35 & m, std::string & err) {
+    const gemvq_qw_config & c = m.c;
+    const uint32_t B = uint32_t(m.n_seq);
+    std::vector<uint32_t> & w = m.cmds;
+    if (!build_chunk(m, B, w)) return false;
+    // the chunk list is one sequence's tokens in order; turn its CONV, GDN and ATTN into their sequences forms
+    const uint32_t hv = uint32_t(c.ssm_v_heads);
+    int slot = 0;
+    for (size_t i = 0; i < w.size(); i += GEMVQ_CMD_WORDS) {
+        uint32_t * k = &w[i];
+        if (k[0] == GEMVQ_OP_CONV) {
+            k[7] |= GEMVQ_CONV_SEQS;
+        } else if (k[0] == GEMVQ_OP_GDN) {
+            uint32_t * k2 = k + GEMVQ_CMD_WORDS;
+            const uint32_t row = uint32_t(slot++) * B * hv * 128u;  // the layer's rows of all sequences
+            k2[0] = k2[1] = row;
+            k2[3] |= GEMVQ_GDN_SEQS;
+            i += 2 * GEMVQ_CMD_WORDS;
+        } else if (k[0] == GEMVQ_OP_ATTN) {
+            k[6] = m.spos;
+            k[7] |= GEMVQ_ATTN_SEQS;
+            i += GEMVQ_CMD_WORDS;
+        } else if (k[0] == GEMVQ_OP_GEMM) {
+            i += GEMVQ_CMD_WORDS;
+        }
+    }
+    Emit e{w};
+    const T & onorm = m.t.at("output_norm.weight");
+    const T & head = m.t.at("output.weight");
+    const uint32_t E = uint32_t(c.n_embd), V = uint32_t(c.n_vocab);
+    const int ht = head.d->type;
+    if ((ht == T_Q4_0 || ht == T_Q4_1 || ht == T_Q8_0) && head.d->ne0 % 512 == 0) {
+        e.gemm(head, m.bh, E, m.slogits, V, B, 0, 0, 0, &onorm, c.eps);
+    } else {  // no batched form of the head's type: each sequence's row normed and multiplied on its own
+        for (uint32_t t = 0; t < B; ++t) {
+            e.cmd({GEMVQ_OP_RMSNORM, E, m.bh + t * E, onorm.act_off, m.xn, fb(c.eps), 1, GEMVQ_NORM_DEFER});
+            e.gemv(head, m.xn, m.slogits + t * V);
+        }
+    }
+    e.cmd({GEMVQ_OP_ARGMAX, V, m.slogits, m.skey, B, V});
+    e.cmd({GEMVQ_OP_NEXT_TOKEN, m.skey, m.bid, m.spos, m.sprompt, m.slen, m.sout, B | (uint32_t(c.n_ctx) << 8)});
+    (void)err;
     return true;
 }
 
@@ -328,9 +392,15 @@ extern "C" {
 
 int gemvq_qwen35_sizes(const gemvq_qw_config * cfg, const gemvq_tensor_desc * tab, int n, size_t * act_floats,
                        size_t * weight_bytes, size_t * state_rows) {
-    if (!cfg || !tab || n <= 0) return GEMVQ_EINVAL;
+    return gemvq_qwen35_batch_sizes(cfg, tab, n, 1, act_floats, weight_bytes, state_rows);
+}
+
+int gemvq_qwen35_batch_sizes(const gemvq_qw_config * cfg, const gemvq_tensor_desc * tab, int n, int n_seq,
+                             size_t * act_floats, size_t * weight_bytes, size_t * state_rows) {
+    if (!cfg || !tab || n <= 0 || n_seq < 1 || n_seq > int(GEMVQ_GEMM_MAX_TOK)) return GEMVQ_EINVAL;
     gemvq_qwen35 m;
     m.c = *cfg;
+    m.n_seq = n_seq;
     const size_t act = layout(m, tab, n);
     size_t wb = 0;
     for (int i = 0; i < n; ++i)
@@ -339,16 +409,26 @@ int gemvq_qwen35_sizes(const gemvq_qw_config * cfg, const gemvq_tensor_desc * ta
     for (int il = 0; il < cfg->n_layer; ++il) gdn_layers += !is_attn(*cfg, il);
     if (act_floats) *act_floats = act;
     if (weight_bytes) *weight_bytes = wb + 4096;
-    if (state_rows) *state_rows = size_t(gdn_layers) * cfg->ssm_v_heads * 128;
+    if (state_rows) *state_rows = size_t(gdn_layers) * cfg->ssm_v_heads * 128 * size_t(n_seq);
     return 0;
 }
 
 gemvq_qwen35 * gemvq_qwen35_create(gemvq_ctx * ctx, const gemvq_qw_config * cfg, const gemvq_tensor_desc * tab,
                                    int n, const uint8_t * blob) {
+    return gemvq_qwen35_batch_create(ctx, cfg, tab, n, blob, 1);
+}
+
+gemvq_qwen35 * gemvq_qwen35_batch_create(gemvq_ctx * ctx, const gemvq_qw_config * cfg, const gemvq_tensor_desc * tab,
+                                         int n, const uint8_t * blob, int n_seq) {
     if (!ctx || !cfg || !tab || !blob || n <= 0) return nullptr;
+    if (n_seq < 1 || n_seq > int(GEMVQ_GEMM_MAX_TOK)) {
+        set_err(ctx, "gemvq_qwen35_batch_create: 1 to GEMVQ_GEMM_MAX_TOK sequences");
+        return nullptr;
+    }
     auto * m = new gemvq_qwen35();
     m->ctx = ctx;
     m->c = *cfg;
+    m->n_seq = n_seq;
     const gemvq_qw_config & c = m->c;
     if (c.n_rot % 2 || c.n_rot > c.head_dim || c.ssm_head_dim != 128 || c.attn_interval <= 0 || c.n_ctx <= 0) {
         set_err(ctx, "gemvq_qwen35_create: unsupported configuration");
@@ -373,7 +453,7 @@ gemvq_qwen35 * gemvq_qwen35_create(gemvq_ctx * ctx, const gemvq_qw_config * cfg,
     m->kv.assign(c.n_layer, -1);
     for (int il = 0; il < c.n_layer; ++il) {
         if (!is_attn(c, il)) continue;
-        m->kv[il] = gemvq_kv_create(ctx, c.n_ctx, c.n_head_kv, c.head_dim);
+        m->kv[il] = gemvq_kv_create(ctx, c.n_ctx * n_seq, c.n_head_kv, c.head_dim);  // one region per sequence
         if (m->kv[il] < 0) {
             delete m;
             return nullptr;
@@ -392,12 +472,18 @@ gemvq_qwen35 * gemvq_qwen35_create(gemvq_ctx * ctx, const gemvq_qw_config * cfg,
         }
     }
     std::string err;
-    if (gemvq_act_write(ctx, m->rope, rope.data(), rope.size()) || !build_commands(*m, err)) {
+    m->can_batch = batchable(*m, m->batch_why);
+    if (n_seq > 1 && !m->can_batch) {
+        set_err(ctx, "gemvq_qwen35_batch_create: " + m->batch_why);
+        delete m;
+        return nullptr;
+    }
+    if (gemvq_act_write(ctx, m->rope, rope.data(), rope.size()) ||
+        !(n_seq > 1 ? build_batch(*m, err) : build_commands(*m, err))) {
         if (!err.empty()) set_err(ctx, err);
         delete m;
         return nullptr;
     }
-    m->can_batch = batchable(*m, m->batch_why);
     return m;  // the per-token graph is captured by the first gemvq_qwen35_step
 }
 
@@ -409,7 +495,7 @@ void gemvq_qwen35_destroy(gemvq_qwen35 * m) {
 }
 
 int gemvq_qwen35_reset(gemvq_qwen35 * m, const int32_t * prompt, int n) {
-    if (!m || !prompt || n < 1 || n > m->c.n_ctx) return GEMVQ_EINVAL;
+    if (!m || !prompt || n < 1 || n > m->c.n_ctx || m->n_seq > 1) return GEMVQ_EINVAL;
     gemvq_ctx * ctx = m->ctx;
     int st = gemvq_sync(ctx);
     if (!st) st = gemvq_state_clear(ctx);
@@ -440,7 +526,7 @@ int gemvq_qwen35_reset(gemvq_qwen35 * m, const int32_t * prompt, int n) {
 }
 
 int gemvq_qwen35_prefill(gemvq_qwen35 * m, int n) {
-    if (!m || n < 0) return GEMVQ_EINVAL;
+    if (!m || n < 0 || m->n_seq > 1) return GEMVQ_EINVAL;
     gemvq_ctx * ctx = m->ctx;
     if (n == 0) return 0;
     if (!m->can_batch) return set_err(ctx, "gemvq_qwen35_prefill: " + m->batch_why);
@@ -493,18 +579,59 @@ int gemvq_qwen35_step(gemvq_qwen35 * m, int n) {
 }
 
 int gemvq_qwen35_tokens(gemvq_qwen35 * m, int32_t * out, int n) {
-    if (!m || !out || n < 0 || n > m->c.n_ctx) return GEMVQ_EINVAL;
+    if (!m || !out || n < 0 || n > m->c.n_ctx || m->n_seq > 1) return GEMVQ_EINVAL;
     return gemvq_act_read(m->ctx, m->out, out, size_t(n));
 }
 
 int gemvq_qwen35_logits(gemvq_qwen35 * m, float * out) {
-    if (!m || !out) return GEMVQ_EINVAL;
+    if (!m || !out || m->n_seq > 1) return GEMVQ_EINVAL;
     return gemvq_act_read(m->ctx, m->logits, out, size_t(m->c.n_vocab));
 }
 
 int gemvq_qwen35_hidden(gemvq_qwen35 * m, float * out) {
-    if (!m || !out) return GEMVQ_EINVAL;
+    if (!m || !out || m->n_seq > 1) return GEMVQ_EINVAL;
     return gemvq_act_read(m->ctx, m->h, out, size_t(m->c.n_embd));
+}
+
+int gemvq_qwen35_batch_reset(gemvq_qwen35 * m, const int32_t * prompts, const int32_t * offsets) {
+    if (!m || !prompts || !offsets || m->n_seq < 2) return GEMVQ_EINVAL;
+    const gemvq_qw_config & c = m->c;
+    const int ns = m->n_seq, cap = c.n_ctx;
+    for (int s = 0; s < ns; ++s)
+        if (offsets[s + 1] - offsets[s] < 1 || offsets[s + 1] - offsets[s] > cap) return GEMVQ_EINVAL;
+    gemvq_ctx * ctx = m->ctx;
+    int st = gemvq_sync(ctx);
+    if (!st) st = gemvq_state_clear(ctx);
+    if (!st) st = gemvq_kv_clear(ctx);
+    std::vector<float> zeros(size_t(conv_ch(c)) * 3 * ns, 0.0f);
+    for (int il = 0; il < c.n_layer && !st; ++il)
+        if (!is_attn(c, il)) st = gemvq_act_write(ctx, m->conv_state[il], zeros.data(), zeros.size());
+    std::vector<int32_t> pr(size_t(ns) * cap, 0), out(size_t(ns) * cap, -1), slots(size_t(ns) * 16, 0),
+        len(size_t(ns) * 16, 0), ids(size_t(GEMVQ_GEMM_MAX_TOK) * 16, 0);
+    for (int s = 0; s < ns; ++s) {
+        const int n = offsets[s + 1] - offsets[s];
+        std::memcpy(&pr[size_t(s) * cap], prompts + offsets[s], size_t(n) * 4);
+        out[size_t(s) * cap] = prompts[offsets[s]];
+        len[size_t(s) * 16] = n;
+        ids[size_t(s) * 16] = prompts[offsets[s]];
+    }
+    if (!st) st = gemvq_act_write(ctx, m->sprompt, pr.data(), pr.size());
+    if (!st) st = gemvq_act_write(ctx, m->sout, out.data(), out.size());
+    if (!st) st = gemvq_act_write(ctx, m->slen, len.data(), len.size());
+    if (!st) st = gemvq_act_write(ctx, m->spos, slots.data(), slots.size());  // every position 0
+    if (!st) st = gemvq_act_write(ctx, m->skey, slots.data(), slots.size());
+    if (!st) st = gemvq_act_write(ctx, m->bid, ids.data(), ids.size());
+    return st;
+}
+
+int gemvq_qwen35_batch_tokens(gemvq_qwen35 * m, int seq, int32_t * out, int n) {
+    if (!m || !out || m->n_seq < 2 || seq < 0 || seq >= m->n_seq || n < 0 || n > m->c.n_ctx) return GEMVQ_EINVAL;
+    return gemvq_act_read(m->ctx, m->sout + size_t(seq) * m->c.n_ctx, out, size_t(n));
+}
+
+int gemvq_qwen35_batch_logits(gemvq_qwen35 * m, int seq, float * out) {
+    if (!m || !out || m->n_seq < 2 || seq < 0 || seq >= m->n_seq) return GEMVQ_EINVAL;
+    return gemvq_act_read(m->ctx, m->slogits + size_t(seq) * m->c.n_vocab, out, size_t(m->c.n_vocab));
 }
 
 int gemvq_qwen35_commands(gemvq_qwen35 * m, uint32_t * words, size_t n_words) {

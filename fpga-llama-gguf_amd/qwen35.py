@@ -194,6 +194,12 @@ def _lib():
         gq._c_fn(lib, "gemvq_qwen35_hidden", C.c_int, vp, vp)
         gq._c_fn(lib, "gemvq_qwen35_commands", C.c_int, vp, vp, C.c_size_t)
         gq._c_fn(lib, "gemvq_qwen35_graph", C.c_int, vp)
+        gq._c_fn(lib, "gemvq_qwen35_batch_sizes", C.c_int, vp, vp, C.c_int, C.c_int, C.POINTER(C.c_size_t),
+                 C.POINTER(C.c_size_t), C.POINTER(C.c_size_t))
+        gq._c_fn(lib, "gemvq_qwen35_batch_create", vp, vp, vp, vp, C.c_int, vp, C.c_int)
+        gq._c_fn(lib, "gemvq_qwen35_batch_reset", C.c_int, vp, vp, vp)
+        gq._c_fn(lib, "gemvq_qwen35_batch_tokens", C.c_int, vp, C.c_int, vp, C.c_int)
+        gq._c_fn(lib, "gemvq_qwen35_batch_logits", C.c_int, vp, C.c_int, vp)
         _fns = True
     return lib
 
@@ -287,3 +293,73 @@ class Model:
         self.reset(prompt)
         self.step(len(prompt) - 1 + n_gen)
         return self.tokens(len(prompt) + n_gen)
+
+
+class BatchModel:
+    """n_seq sequences decoded in lockstep on the GPU (include/gemvq_qwen35.h gemvq_qwen35_batch_*): one step
+    advances every sequence by one position, the layer projections reading each weight row once for all of them."""
+
+    def __init__(self, blob: Blob, n_seq: int, device: int = 0):
+        self.lib = _lib()
+        self.cfg = blob.cfg
+        self.n_seq = n_seq
+        self.cc = config_c(blob.cfg)
+        act, wb, st = C.c_size_t(), C.c_size_t(), C.c_size_t()
+        if self.lib.gemvq_qwen35_batch_sizes(C.byref(self.cc), blob.table, blob.n, n_seq, C.byref(act), C.byref(wb),
+                                             C.byref(st)):
+            raise gq.GemvqError("qwen35 batch sizes")
+        self.ctx = gq.Context(act_floats=act.value, weight_bytes=wb.value, state_rows=st.value, device=device)
+        self.h = self.lib.gemvq_qwen35_batch_create(self.ctx.h, C.byref(self.cc), blob.table, blob.n,
+                                                    blob.data.ctypes.data, n_seq)
+        if not self.h:
+            raise gq.GemvqError("qwen35 batch create: " + self.ctx.error())
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.gemvq_qwen35_destroy(self.h)
+            self.h = None
+        if getattr(self, "ctx", None):
+            self.ctx.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _ok(self, st, what):
+        if st:
+            raise gq.GemvqError(f"{what}: status {st}: {self.ctx.error()}")
+
+    def reset(self, prompts: list) -> None:
+        """One prompt (1..n_ctx ids) per sequence."""
+        assert len(prompts) == self.n_seq
+        flat = np.ascontiguousarray(np.concatenate([np.asarray(p, np.int32) for p in prompts]), np.int32)
+        offs = np.zeros(self.n_seq + 1, np.int32)
+        offs[1:] = np.cumsum([len(p) for p in prompts])
+        self._ok(self.lib.gemvq_qwen35_batch_reset(self.h, flat.ctypes.data, offs.ctypes.data), "batch reset")
+
+    def step(self, n: int = 1) -> None:
+        self._ok(self.lib.gemvq_qwen35_step(self.h, n), "batch step")
+
+    def sync(self) -> None:
+        self.ctx.sync()
+
+    def tokens(self, seq: int, n: int) -> np.ndarray:
+        out = np.empty(n, np.int32)
+        self._ok(self.lib.gemvq_qwen35_batch_tokens(self.h, seq, out.ctypes.data, n), "batch tokens")
+        return out
+
+    def logits(self, seq: int) -> np.ndarray:
+        out = np.empty(self.cfg.n_vocab, np.float32)
+        self._ok(self.lib.gemvq_qwen35_batch_logits(self.h, seq, out.ctypes.data), "batch logits")
+        return out
+
+    def commands(self) -> np.ndarray:
+        n = self.lib.gemvq_qwen35_commands(self.h, None, 0)
+        out = np.empty(n * 8, np.uint32)
+        self.lib.gemvq_qwen35_commands(self.h, out.ctypes.data, out.size)
+        return out.reshape(n, 8)
+
+    def graph(self) -> int:
+        return self.lib.gemvq_qwen35_graph(self.h)

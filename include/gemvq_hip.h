@@ -33,7 +33,9 @@
  *   ADD 3, SILU_MUL 4, MUL 5, UNARY 6, CONV 8, ROPE 10 as gemvqc16.h:52-59, 85-91; ROPE word 7 (pos_off): if
  *             nonzero, cs_off is a table of n_dims floats per position and the row is selected by the int32
  *             position stored at act[pos_off]. CONV word 7 bits 31:16 (0 or 1: one token): n_tok packed token
- *             rows of x and y run in order, each window ending at its token (up to GEMVQ_GEMM_MAX_TOK).
+ *             rows of x and y run in order, each window ending at its token (up to GEMVQ_GEMM_MAX_TOK); with word 7
+ *             bit1 (GEMVQ_CONV_SEQS) token t is the one token of sequence t instead, its window (3 * ch floats) at
+ *             the state offsets + 3 * ch * t.
  *   GDN       [7, H_v | H_k << 16, q_off, k_off, v_off, g_off, beta_off, y_off]
  *             + [src_row, dst_row, scale bits, flags, l2_eps bits, rms_eps bits, w_off, z_off]
  *             (+ [dt_off, a_off, n_tok, qkv_stride, gb_stride, 0, 0, 0] with GEMVQ_GDN_GATES) as gemvqc16.h:60-81;
@@ -50,6 +52,9 @@
  *             GEMVQ_GDN_Z_SILU (32): z_off already holds silu(z), the gated norm multiplies by it directly. A GDN with
  *             the gated norm followed by a Q4_0 / Q8_0 GEMV reading its y applies the norm in that GEMV's activation
  *             prologue (one launch less; y is still written).
+ *             GEMVQ_GDN_SEQS (64) with n_tok > 1: the tokens belong to n_tok sequences decoded in lockstep (no
+ *             counterpart in the reference): token t is the one token of sequence t and runs on its own state rows,
+ *             src_row / dst_row + t * H_v * 128, all tokens in one launch.
  *   ATTN      [12, n_head | n_head_kv << 16, q_off, kv, y_off, head_dim | n_rot << 16, pos_off, flags]
  *             + [k_off, v_off, scale bits, eps bits, qn_off, kn_off, cs_off, gate_off]
  *             One token of GQA attention (q head h reads KV head h / (n_head / n_head_kv)). q rows (head_dim floats)
@@ -62,14 +67,22 @@
  *             act[pos_off] + t, as n_tok one-token commands run in order (token t sees the keys of tokens < t), with
  *             packed rows: token t's q and gate rows start t * n_head * (q row stride) floats on, its k and v rows
  *             t * n_head_kv * head_dim, its output t * n_head * head_dim. Results are bit-identical to those commands.
+ *             flags bit1 (GEMVQ_ATTN_SEQS) with n_tok > 1: token t is the one token of sequence t of n_tok decoded in
+ *             lockstep (no counterpart in the reference): its position is act_i32[pos_off + 16 t], and KV buffer kv
+ *             (n_ctx a multiple of n_tok) holds the sequences in n_tok equal regions of n_ctx / n_tok positions, token
+ *             t storing and reading region t; each token's results are those of a one-token command on its region.
  *   GET_ROWS  [13, format | n_tok << 16, rows, cols, w_off lo, w_off hi, id_off, y_off]  y = dequantized row
  *             act_i32[id_off]; with n_tok (2..GEMVQ_GEMM_MAX_TOK) token t's id is act_i32[id_off + 16 t] and its row
  *             goes to y_off + t * cols.
- *   ARGMAX    [14, n, x_off, key_off, 0, 0, 0, 0]  max(packed key at act[key_off..+1]) with the first index of the
- *             maximum of x; the key must be cleared (NEXT_TOKEN does it).
+ *   ARGMAX    [14, n, x_off, key_off, rows, row_stride, 0, 0]  max(packed key at act[key_off..+1]) with the first
+ *             index of the maximum of x; the key must be cleared (NEXT_TOKEN does it). rows (0 or 1: one; at most
+ *             GEMVQ_GEMM_MAX_TOK): row r at x_off + r * row_stride, its key at key_off + 16 r.
  *   NEXT_TOKEN [15, key_off, tok_off, pos_off, prompt_off, n_prompt, out_off, 0]  token = argmax of the key, or
  *             the prompt token act_i32[prompt_off + pos + 1] while pos + 1 < n_prompt; act_i32[out_off + pos + 1]
  *             = token; act_i32[tok_off] = token; act_i32[pos_off] = pos + 1; the key is cleared.
+ *             Word 7 = n_seq | cap << 8 with n_seq > 1: n_seq sequences in lockstep, sequence s with its key, token
+ *             and position at key_off, tok_off, pos_off + 16 s, its prompt length at act_i32[n_prompt + 16 s] (word
+ *             5 is then an offset), its prompt at prompt_off + s * cap and its token ids at out_off + s * cap.
  *   FILL      [16, n, y_off, value bits, 0, 0, 0, 0]  y = value.
  *   GEMM      [17, format | flags, rows, cols, w_off lo, w_off hi, x_off, y_off]
  *             + [n_tok, x_stride, y_stride, res_off, res_stride, norm_w_off, eps bits, norm_flags]
@@ -128,6 +141,9 @@ extern "C" {
 #define GEMVQ_GDN_GATES 8u
 #define GEMVQ_GDN_WITH_OUT 16u
 #define GEMVQ_GDN_Z_SILU 32u
+#define GEMVQ_GDN_SEQS 64u
+#define GEMVQ_CONV_SEQS 2u
+#define GEMVQ_ATTN_SEQS 2u
 #define GEMVQ_NORM_L2 1u
 #define GEMVQ_NORM_NO_WEIGHT 2u
 #define GEMVQ_NORM_DEFER 4u

@@ -63,6 +63,26 @@ int gemvq_qwen35_hidden(gemvq_qwen35 * m, float * out);
 int gemvq_qwen35_commands(gemvq_qwen35 * m, uint32_t * words, size_t n_words);
 /* The captured graph id (for gemvq_graph_time); -1 before the first step. */
 int gemvq_qwen35_graph(gemvq_qwen35 * m);
+/* Lockstep decode of n_seq (2..GEMVQ_GEMM_MAX_TOK) sequences (the multi-sequence path the reference plans,
+ * ROADMAP.md:78-96; no counterpart in its code): every step reads each weight row once for all sequences (GEMM
+ * commands over their n_seq token rows), with CONV, the DeltaNet step and attention in their sequences forms, so
+ * each sequence keeps its own conv windows, state rows, KV region (n_ctx positions) and position, and its ids and
+ * logits are those of a single-sequence model decoding its prompt, bit for bit. Prompts are consumed by the same
+ * steps (a sequence takes its next prompt token while it has one, then its argmax). Layer projections must have a
+ * batched form (Q4_0 / Q4_1 / Q8_0, columns a multiple of 512); a head of another type runs one GEMV per sequence.
+ * gemvq_qwen35_batch_sizes gives the context sizes; gemvq_qwen35_step, _commands, _graph and _destroy apply to the
+ * batch model, the single-sequence _reset, _prefill, _tokens, _logits and _hidden return GEMVQ_EINVAL for it
+ * (gemvq_qwen35_batch_create with n_seq 1 is gemvq_qwen35_create). */
+int gemvq_qwen35_batch_sizes(const gemvq_qw_config * cfg, const gemvq_tensor_desc * table, int n_tensors, int n_seq,
+                             size_t * act_floats, size_t * weight_bytes, size_t * state_rows);
+gemvq_qwen35 * gemvq_qwen35_batch_create(gemvq_ctx * ctx, const gemvq_qw_config * cfg,
+                                         const gemvq_tensor_desc * table, int n_tensors, const uint8_t * blob,
+                                         int n_seq);
+/* Clears states and KV; sequence s gets prompts[offsets[s] .. offsets[s + 1]) (1..n_ctx ids) and position 0. */
+int gemvq_qwen35_batch_reset(gemvq_qwen35 * m, const int32_t * prompts, const int32_t * offsets);
+/* Sequence seq's token ids at positions 0 .. n - 1; its logits of the last step (n_vocab floats); synchronize. */
+int gemvq_qwen35_batch_tokens(gemvq_qwen35 * m, int seq, int32_t * out, int n);
+int gemvq_qwen35_batch_logits(gemvq_qwen35 * m, int seq, float * out);
 /* The per-token command list gemvq_qwen35_create would build, without a device: weights placed as
  * gemvq_upload_weight places them in table order, KV buffers numbered in layer order. Returns the number of commands
  * (words copied when n_words is large enough), or GEMVQ_EINVAL. */
