@@ -8,7 +8,7 @@ untimed and `--steps` timed greedy decode steps (one hipGraph replay each, token
 
 roofline: the dominant kernel (largest share of a token's device time), its algorithmic bytes (GGUF weights +
 fp32 vectors read and written once + state/KV traffic) over its measured duration, from device start/stop events
-of every kernel of one token (gemvq_profile). cpu_baseline: the oracle decoder in the reference's CPU arithmetic
+of every kernel of one token (gemvq_profile, the median over --profile-reps repetitions). cpu_baseline: the oracle decoder in the reference's CPU arithmetic
 (gemvq_ref.h: int8 block dots, here in AVX2, each row summed sequentially in FP32, double sums of squares) on the
 host, one thread per physical core, for up to 15 s (160 steps) of decode steps at the positions of the first timed GPU steps;
 the JSON names the CPU model, sockets, cores and SIMD extensions.
@@ -420,7 +420,8 @@ def main() -> int:
     ap.add_argument("--cpu-tokens", type=int, default=160, help="most decode steps timed for the CPU baseline (0: skip)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="time the CPU baseline samples for")
     ap.add_argument("--threads", type=int, default=min(16, os.cpu_count() or 1))
-    ap.add_argument("--profile-reps", type=int, default=3)
+    ap.add_argument("--profile-reps", type=int, default=9,
+                    help="repetitions of the per-kernel pass (each launch's median duration is reported)")
     ap.add_argument("--layers", type=int, default=32, help="(testing) fewer layers; the reported line is then invalid")
     ap.add_argument("--direct", action="store_true",
                     help="plain stream launches instead of graph replays (for tracing tools); slower per step")

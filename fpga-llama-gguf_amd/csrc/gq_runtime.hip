@@ -7,6 +7,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -1639,7 +1640,7 @@ int gemvq_profile(gemvq_ctx * c, const uint32_t * cmds, unsigned n, int reps, ge
         }
     const size_t L = ls.size();
     std::vector<hipEvent_t> e0(L), e1(L);
-    std::vector<double> sum(L, 0.0);
+    std::vector<std::vector<float>> ms_of(L);  // per launch, one duration per repetition
     hipError_t e = hipSuccess;
     int ws = 0;
     for (size_t i = 0; i < L && e == hipSuccess; ++i) {
@@ -1658,7 +1659,7 @@ int gemvq_profile(gemvq_ctx * c, const uint32_t * cmds, unsigned n, int reps, ge
         for (size_t i = 0; i < L && e == hipSuccess; ++i) {
             float ms = 0.0f;
             e = hipEventElapsedTime(&ms, e0[i], e1[i]);
-            sum[i] += ms;
+            ms_of[i].push_back(ms);
         }
     }
     g_prof_start = g_prof_stop = nullptr;
@@ -1676,7 +1677,11 @@ int gemvq_profile(gemvq_ctx * c, const uint32_t * cmds, unsigned n, int reps, ge
         o.first_cmd = spans[i].first;
         o.n_cmds = spans[i].second;
         o.bytes = d.second;
-        o.us = sum[i] * 1000.0 / reps;
+        // the median over the repetitions (a repetition slowed by something outside the launch does not move it)
+        std::vector<float> & v = ms_of[i];
+        std::sort(v.begin(), v.end());
+        const size_t h = v.size() / 2;
+        o.us = (v.size() % 2 ? double(v[h]) : 0.5 * (double(v[h - 1]) + double(v[h]))) * 1000.0;
     }
     return int(L);
 }

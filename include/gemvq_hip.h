@@ -232,8 +232,8 @@ int gemvq_graph_time(gemvq_ctx * ctx, int graph, int times, double * us_per_repl
 /* Profiling (the counterpart of the reference's TRACE opcode and XRT-TIMING totals, gemvqc16.h:92-98,
  * ggml-xrt.cpp:285-314, 1302-1397): runs a command list `reps` times, each kernel launched with device start/stop
  * events (hipExtLaunchKernelGGL), and reports per launch the kernel, the commands it executes, its algorithmic
- * bytes (GGUF-sized weights, fp32 vectors read and written once, state and KV cache traffic) and its average
- * duration. The list's side effects happen `reps` times. Returns the number of launches (>= 0) or a status. */
+ * bytes (GGUF-sized weights, fp32 vectors read and written once, state and KV cache traffic) and its median
+ * duration over the repetitions. The list's side effects happen `reps` times. Returns the number of launches (>= 0) or a status. */
 typedef struct {
     char name[40];
     int32_t first_cmd, n_cmds;
