@@ -9,6 +9,24 @@ hipError_t launch_gemv_q8_0(const GemvArgs & a, hipStream_t st);
 hipError_t launch_gemv_q5_k(const GemvArgs & a, hipStream_t st);
 hipError_t launch_gemv_q6_k(const GemvArgs & a, hipStream_t st);
 
+hipError_t launch_gemv_tok_q4_0(const TokArgs & a, hipStream_t st);
+hipError_t launch_gemv_tok_q8_0(const TokArgs & a, hipStream_t st);
+
+bool gemv_tok_ok(int type, int cols, int n_tok, bool pair) {
+    (void)pair;  // every instance has both member kinds
+    if ((type != T_Q4_0 && type != T_Q8_0) || cols <= 0 || cols % 32 || cols > GEMV_MAXK) return false;
+    const int nu = (cols / 32 + 63) / 64;
+    return n_tok >= 2 && n_tok <= TOK_MAX && (nu <= 2 || (nu <= 6 && n_tok == 2));
+}
+
+hipError_t launch_gemv_tok(const TokArgs & a, int type, hipStream_t st) {
+    bool pair = false;
+    for (int i = 0; i < a.n_members; ++i) pair = pair || a.m[i].epi == EPI_SWIGLU;
+    if (!gemv_tok_ok(type, a.cols, a.n_tok, pair) || a.n_members < 1 || a.n_members > 4 || (pair && a.n_members != 1))
+        return hipErrorInvalidValue;
+    return type == T_Q4_0 ? launch_gemv_tok_q4_0(a, st) : launch_gemv_tok_q8_0(a, st);
+}
+
 hipError_t launch_gemv(const GemvArgs & a, int type, hipStream_t st) {
     if (a.cols <= 0 || a.cols > GEMV_MAXK || a.total_tasks <= 0) return hipErrorInvalidValue;
     switch (type) {

@@ -163,17 +163,22 @@ __device__ __forceinline__ float quantize_half_core(const float * v, uint32_t * 
     return d;
 }
 
-__device__ __forceinline__ void quantize_half(const float * v, int item, bool valid, Lds & s) {
+// Stores into the quants xq, the words info (fp16 d | quant sum << 16) and the Q8_1 s values s1 of one vector.
+__device__ __forceinline__ void quantize_half(const float * v, int item, bool valid, int8_t * xq, uint32_t * info,
+                                              uint16_t * s1) {
     uint32_t packed[4];
     int sum;
     const float d = quantize_half_core(v, packed, sum);
     if (valid) {
-        *reinterpret_cast<uint4 *>(s.xq + size_t(item) * 16) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+        *reinterpret_cast<uint4 *>(xq + size_t(item) * 16) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
         if ((item & 1) == 0) {
-            s.info[item >> 1] = f2h(d) | (uint32_t(sum & 0xffff) << 16);
-            s.s1[item >> 1] = uint16_t(f2h(float(sum) * d));  // ggml quantize_row_q8_1: s = fp16(sum * d), FP32 d
+            info[item >> 1] = f2h(d) | (uint32_t(sum & 0xffff) << 16);
+            s1[item >> 1] = uint16_t(f2h(float(sum) * d));  // ggml quantize_row_q8_1: s = fp16(sum * d), FP32 d
         }
     }
+}
+__device__ __forceinline__ void quantize_half(const float * v, int item, bool valid, Lds & s) {
+    quantize_half(v, item, valid, s.xq, s.info, s.s1);
 }
 
 // Norm scale over the whole vector: tree over each item's 16 squares, pairwise over the 64 items of a wave, the 4
@@ -354,19 +359,24 @@ struct XK {  // one 64-weight unit (Q5_K / Q6_K)
 
 // Lanes past the last block hold a zero block (zero quants and scales), whose terms are exactly zero.
 template <int TYPE>
-__device__ __forceinline__ void load_xb(const Lds & s, int b, int nb, XB & x) {
+__device__ __forceinline__ void load_xb(const int8_t * xq, const uint32_t * info, const uint16_t * s1, int b, int nb,
+                                        XB & x) {
     const bool in = b < nb;
     b = in ? b : nb - 1;
-    const uint4 * p = reinterpret_cast<const uint4 *>(s.xq + size_t(b) * 32);
+    const uint4 * p = reinterpret_cast<const uint4 *>(xq + size_t(b) * 32);
     const uint4 lo = p[0], hi = p[1];
     x.q[0] = lo.x; x.q[1] = lo.y; x.q[2] = lo.z; x.q[3] = lo.w;
     x.q[4] = hi.x; x.q[5] = hi.y; x.q[6] = hi.z; x.q[7] = hi.w;
 #pragma unroll
     for (int i = 0; i < 8; ++i) x.q[i] = in ? x.q[i] : 0u;
-    const uint32_t inf = in ? s.info[b] : 0u;
+    const uint32_t inf = in ? info[b] : 0u;
     x.dx40 = h2f(inf & 0xffffu) * 1099511627776.0f;  // * 2^40
     x.sum = int(int16_t(inf >> 16));
-    x.sx40 = TYPE == T_Q4_1 && in ? h2f(s.s1[b]) * 1099511627776.0f : 0.0f;
+    x.sx40 = TYPE == T_Q4_1 && in ? h2f(s1[b]) * 1099511627776.0f : 0.0f;
+}
+template <int TYPE>
+__device__ __forceinline__ void load_xb(const Lds & s, int b, int nb, XB & x) {
+    load_xb<TYPE>(s.xq, s.info, s.s1, b, nb, x);
 }
 
 template <int TYPE>
@@ -979,7 +989,8 @@ constexpr int gemv_wg_per_cu(int nu) { return nu >= 5 && GEMV_WG_PER_CU > 2 ? 2 
 // on the device at once (every row is requested before the activation prologue ends); otherwise the resident waves,
 // shared in proportion to the rows, stream them. A slice's rows are dealt to its waves in turn, so the rows in flight
 // form one region of the slice.
-int plan_waves(GemvArgs & a, int cap_blocks, int ds) {
+template <typename Args>  // GemvArgs or TokArgs: n_members, m[i].rows, m[i].wave_begin, m[i].waves
+int plan_waves(Args & a, int cap_blocks, int ds) {
     const int cap_x = cap_blocks / 8 < 1 ? 1 : cap_blocks / 8;  // workgroups per XCD
     int need = 0;
     for (int i = 0; i < a.n_members; ++i) need += ((a.m[i].rows + 7) / 8 + ds - 1) / ds;

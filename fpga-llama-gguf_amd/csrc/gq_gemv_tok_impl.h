@@ -1,0 +1,295 @@
+#pragma once
+// The GEMM command for 2-4 tokens (TokArgs) on the single-token GEMV's structure: the same workgroups, XCD slices,
+// rows in flight and exact block terms as gemv_kernel, with every lane holding its activation blocks of all T
+// tokens in registers. A weight row is streamed and unpacked once and its block terms are formed for each token;
+// each token's row total is rounded once and goes through the member's epilog. The tokens are quantized in the
+// prologue of every workgroup, each exactly as the single-token prologue quantizes one vector (the same norm scale
+// tree and quantizer), so token t's output row is the single-token GEMV's (and the MFMA batched GEMV's) bit for
+// bit. It replaces a quantization launch plus a batched GEMV whose time is that of 16 tokens (one MFMA tile).
+#include "gq_gemv_impl.h"
+
+namespace gq {
+namespace {
+
+template <int T, int NU, int R>
+struct LdsTok {  // T quantized activations of at most 2048 NU columns
+    int8_t xq[T][2048 * NU];
+    uint32_t info[T][64 * NU];
+    uint16_t s1[T][64 * NU];
+    float red[T * R * NWAVES];
+};
+
+template <int T, int R>  // R rounds of NT 16-float items per token
+struct XT {
+    float v[T][R][16];
+    float w[R <= 2 ? R : 1][16];  // the norm weight (the activation again without one)
+};
+
+// Token t's items, and the norm weight's (R <= 2; wider rows read it when they use it), all issued together and
+// without branches.
+template <int T, int R>
+__device__ __forceinline__ void tok_fetch(const TokArgs & a, XT<T, R> & f) {
+    const int n16 = a.cols / 16;
+    const bool normw = a.norm && a.norm_w != nullptr;
+#pragma unroll
+    for (int g = 0; g < R; ++g) {
+        const int i = item_of(g, n16);
+#pragma unroll
+        for (int t = 0; t < T; ++t) load16(a.x + size_t(t) * a.x_stride + size_t(i) * 16, f.v[t][g]);
+        if constexpr (R <= 2) load16(normw ? a.norm_w + size_t(i) * 16 : a.x + size_t(i) * 16, f.w[g]);
+    }
+}
+
+// Each token as prologue_finish does one vector (XSRC_NORM or the raw rows): the canonical norm scale (a tree over
+// each item's 16 squares, pairwise over a wave's 64 items, the 4 waves of a round and the rounds), v = (x * scale)
+// * w, then Q8_0 (and the Q8_1 s) into the token's LDS rows.
+template <int T, int NU, int R>
+__device__ __forceinline__ void tok_finish(const TokArgs & a, XT<T, R> & f, LdsTok<T, NU, R> & s) {
+    const int n16 = a.cols / 16, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float sc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) sc[t] = 1.0f;
+    if (a.norm) {
+        float r[T * R];
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int g = 0; g < R; ++g) {
+                float sq[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) sq[j] = f.v[t][g][j] * f.v[t][g][j];
+                r[t * R + g] = int(threadIdx.x) + NT * g < n16 ? tree<16>(sq) : 0.0f;
+            }
+        pair_sum_lanes_n<64, T * R>(r);
+        if (lane == 0) {
+#pragma unroll
+            for (int k = 0; k < T * R; ++k) s.red[NWAVES * k + wave] = r[k];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            float rs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int g = 0; g < R; ++g) rs[g] = wave_tree(s.red + NWAVES * (t * R + g));
+            const float sum = R == 1 ? rs[0] : R == 2 ? rs[0] + rs[1] : (rs[0] + rs[1]) + (rs[2] + rs[3]);
+            sc[t] = a.norm_l2 ? 1.0f / fmaxf(sqrtf(sum), a.eps) : 1.0f / sqrtf(sum / float(a.cols) + a.eps);
+        }
+    }
+    const bool normw = a.norm && a.norm_w != nullptr;
+#pragma unroll
+    for (int g = 0; g < R; ++g) {
+        const int i = int(threadIdx.x) + NT * g;
+        float w[16];
+        if constexpr (R <= 2) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) w[j] = normw ? f.w[g][j] : 1.0f;
+        } else if (normw) {
+            load16(a.norm_w + size_t(item_of(g, n16)) * 16, w);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) w[j] = 1.0f;
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            float * v = f.v[t][g];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = (v[j] * sc[t]) * w[j];
+            quantize_half(v, i, i < n16, s.xq[t], s.info[t], s.s1[t]);
+        }
+    }
+}
+
+template <int TYPE, int NU, bool PAIR>
+struct TSlot {  // one row in flight: its blocks (of g and u for a SwiGLU pair) and the lane's epilog operand
+    WB wb[NU], wb2[PAIR ? NU : 1];
+    float e;  // ADD: the residual of row r for the lane group's token
+};
+
+// Loads of row r. Lane group g (of G groups of 64 / G lanes) takes token min(g, T - 1)'s epilog operand (a
+// member without a residual reads its own output row, unused), so no load sits behind a branch.
+template <int TYPE, int NU, bool PAIR, int T>
+__device__ __forceinline__ void load_tok_slot(const TokMember & m, int r, int lane, int nb, TSlot<TYPE, NU, PAIR> & o) {
+    constexpr int G = T == 2 ? 2 : 4, GW = 64 / G;
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+        const int b = lane + 64 * k, bb = b < nb ? b : nb - 1;
+        load_wb<TYPE>(m.w, size_t(r) * nb + bb, o.wb[k]);
+        if constexpr (PAIR) load_wb<TYPE>(m.w2, size_t(r) * nb + bb, o.wb2[k]);
+    }
+    const int g = lane / GW, tk = g < T ? g : T - 1;
+    o.e = m.res[size_t(tk) * m.res_stride + r];
+}
+
+// Row r's T token totals through one cross-lane reduction (lane group g ends with token g's), then the epilog as
+// finish_chunk forms it, stored by the groups' first lanes.
+template <int T, bool PAIR>
+__device__ __forceinline__ void finish_tok_row(const TokMember & m, int r, const long long * p, const long long * p2,
+                                               float ev, int lane) {
+    constexpr int G = T == 2 ? 2 : 4, GW = 64 / G;
+    long long pp[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) pp[j] = j < T ? p[j < T ? j : 0] : 0;
+    const long long tot = reduce_rows<G>(pp);
+    const int g = lane / GW;
+    const float v = fixed_to_float(tot);
+    float out = v;
+    if constexpr (PAIR) {
+        long long qq[G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) qq[j] = j < T ? p2[j < T ? j : 0] : 0;
+        const long long tot2 = reduce_rows<G>(qq);
+        out = (v / (1.0f + expf_(-v))) * fixed_to_float(tot2);  // gemvqc_ops.h:88-92
+    } else if (m.epi == EPI_ADD) {
+        out = v + ev;  // gemvqc16.cpp:282-301
+    } else if (m.epi == EPI_SILU) {
+        out = silu_(v);
+    }
+    if ((lane & (GW - 1)) == 0 && g < T) m.y[size_t(g) * m.y_stride + r] = out;
+}
+
+template <int TYPE, int NU, bool PAIR, int T, bool EXACT>
+__device__ __forceinline__ void tok_partials(const TSlot<TYPE, NU, PAIR> & sl, int r, int nb, const XB (*xb)[NU],
+                                             int lane, long long * p, long long * p2) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        p[t] = lane_blocks<TYPE, NU, EXACT>(sl.wb, r, true, nb, xb[t], lane, nullptr);
+        p2[t] = 0;
+        if constexpr (PAIR) p2[t] = lane_blocks<TYPE, NU, EXACT>(sl.wb2, r, true, nb, xb[t], lane, nullptr);
+    }
+}
+
+// The n rows w, w + S, ... of one member with DS in flight: a slot is refilled with the row DS further on as soon
+// as its partials are formed (unconditionally while rows follow, so the compiler's waits stay exact).
+template <int TYPE, int NU, bool PAIR, int T, int DS, bool EXACT>
+__device__ __forceinline__ void tok_rows(const TokMember & m, int w, int S, int n, TSlot<TYPE, NU, PAIR> * sl,
+                                         const XB (*xb)[NU], int lane, int nb) {
+    long long p[T], p2[T];
+    int k = 0;
+    for (; k + DS < n; k += DS) {
+#pragma unroll
+        for (int j = 0; j < DS; ++j) {
+            const int r = w + (k + j) * S;
+            tok_partials<TYPE, NU, PAIR, T, EXACT>(sl[j], r, nb, xb, lane, p, p2);
+            const float ev = sl[j].e;
+            load_tok_slot<TYPE, NU, PAIR, T>(m, w + min(k + j + DS, n - 1) * S, lane, nb, sl[j]);
+            finish_tok_row<T, PAIR>(m, r, p, p2, ev, lane);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < DS; ++j) {
+        if (k + j < n) {
+            const int r = w + (k + j) * S;
+            tok_partials<TYPE, NU, PAIR, T, EXACT>(sl[j], r, nb, xb, lane, p, p2);
+            finish_tok_row<T, PAIR>(m, r, p, p2, sl[j].e, lane);
+        }
+    }
+}
+
+// Rows in flight per wave: two for plain members of at most 4096 columns, one for SwiGLU pairs and wider rows
+// (whose T tokens' activation blocks already take most of the registers).
+template <int NU, bool PAIR>
+constexpr int tok_slots() { return PAIR || NU > 2 ? 1 : 2; }
+
+template <int TYPE, int NU, bool PAIR, int T>
+__global__ __launch_bounds__(NT) void gemv_tok_kernel(TokArgs a) {
+    constexpr int DS = tok_slots<NU, PAIR>();
+    constexpr int R = (128 * NU + NT - 1) / NT;  // rounds of NT activation items per token (cols <= 2048 NU)
+    __shared__ LdsTok<T, NU, R> s;
+    const int lane = threadIdx.x & 63, nb = a.cols / 32;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // workgroup b serves slice b % 8 of every member's rows (one XCD's L2), as gemv_kernel
+    const int xs = blockIdx.x & 7, lw = (blockIdx.x >> 3) * NWAVES + wave;
+    int mi = 0;
+#pragma unroll
+    for (int i = 1; i < 4; ++i)
+        if (i < a.n_members && lw >= a.m[i].wave_begin) mi = i;
+    const TokMember & m = a.m[mi];
+    const int s_lo = int((long long)xs * m.rows / 8), len = int((long long)(xs + 1) * m.rows / 8) - s_lo;
+    const int wv = lw - m.wave_begin, S = m.waves;
+    const int n = wv < S && wv < len ? (len - 1 - wv) / S + 1 : 0;  // waves past the last member have none
+    const int w = s_lo + wv;
+    XT<T, R> f;
+    tok_fetch<T, R>(a, f);              // the activations are requested first
+    __builtin_amdgcn_sched_barrier(0);  // and stay ahead of the weight loads
+    TSlot<TYPE, NU, PAIR> sl[DS];
+#pragma unroll
+    for (int j = 0; j < DS; ++j)
+        load_tok_slot<TYPE, NU, PAIR, T>(m, n > 0 ? w + min(j, n - 1) * S : m.rows - 1, lane, nb, sl[j]);
+    tok_finish<T, NU, R>(a, f, s);
+    __syncthreads();
+    XB xb[T][NU];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int k = 0; k < NU; ++k) load_xb<TYPE>(s.xq[t], s.info[t], s.s1[t], lane + 64 * k, nb, xb[t][k]);
+    // the single-token kernel's bound on a lane's FP64 partial (below 2^53 LSB), for every token: a wave where it
+    // could be passed sums its terms in two FP64 parts (EXACT)
+    bool big = false;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        float dsum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NU; ++k) dsum += fabsf(xb[t][k].dx40);
+        big = big || !(a.wbound[mi] * dsum < 4503599627370496.0f);
+    }
+    const bool exact = __builtin_amdgcn_ballot_w64(big) != 0;
+    if (n > 0) {
+        if (exact) tok_rows<TYPE, NU, PAIR, T, DS, true>(m, w, S, n, sl, xb, lane, nb);
+        else tok_rows<TYPE, NU, PAIR, T, DS, false>(m, w, S, n, sl, xb, lane, nb);
+    }
+}
+
+template <int TYPE, int NU, bool PAIR, int T>
+hipError_t launch_tok_typed(const TokArgs & a0, hipStream_t st) {
+    static const int cap = resident_blocks(gemv_tok_kernel<TYPE, NU, PAIR, T>, gemv_wg_per_cu(NU));
+    TokArgs a = a0;
+    for (int i = 0; i < a.n_members; ++i) {
+        TokMember & m = a.m[i];
+        if (m.epi != EPI_ADD) {  // the epilog operand load reads the member's own output rows
+            m.res = m.y;
+            m.res_stride = m.y_stride;
+        }
+        if (m.epi != EPI_SWIGLU) m.w2 = m.w;
+    }
+    const int grid = plan_waves(a, cap, tok_slots<NU, PAIR>());
+    GQ_LAUNCH((gemv_tok_kernel<TYPE, NU, PAIR, T>), dim3(grid), dim3(NT), 0, st, a);
+    return hipGetLastError();
+}
+
+// Instances: T = 2-4 tokens for rows of at most 4096 columns (NU <= 2), T = 2 up to 12288 columns (NU <= 6).
+constexpr bool tok_instance(int nu, int t) { return t >= 2 && t <= TOK_MAX && (nu <= 2 || (nu <= 6 && t == 2)); }
+
+template <int TYPE, int NU, int T>
+hipError_t launch_tok_nu_t(const TokArgs & a, hipStream_t st) {
+    if constexpr (tok_instance(NU, T)) {
+        return a.m[0].epi == EPI_SWIGLU ? launch_tok_typed<TYPE, NU, true, T>(a, st)
+                                        : launch_tok_typed<TYPE, NU, false, T>(a, st);
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int TYPE, int NU>
+hipError_t launch_tok_nu(const TokArgs & a, hipStream_t st) {
+    switch (a.n_tok) {
+    case 2: return launch_tok_nu_t<TYPE, NU, 2>(a, st);
+    case 3: return launch_tok_nu_t<TYPE, NU, 3>(a, st);
+    case 4: return launch_tok_nu_t<TYPE, NU, 4>(a, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <int TYPE>
+hipError_t launch_tok_type(const TokArgs & a, hipStream_t st) {
+    switch ((a.cols / 32 + 63) / 64) {
+    case 1: return launch_tok_nu<TYPE, 1>(a, st);
+    case 2: return launch_tok_nu<TYPE, 2>(a, st);
+    case 3: return launch_tok_nu<TYPE, 3>(a, st);
+    case 4: return launch_tok_nu<TYPE, 4>(a, st);
+    case 5: return launch_tok_nu<TYPE, 5>(a, st);
+    case 6: return launch_tok_nu<TYPE, 6>(a, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+}  // namespace gq

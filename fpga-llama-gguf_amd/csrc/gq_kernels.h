@@ -256,6 +256,29 @@ struct GemmArgs {
                                       // unknown, every round's terms are summed in int64)
 };
 
+// The GEMM command for 2-4 tokens on the single-token GEMV's structure: each lane keeps its activation blocks of
+// every token in registers, so each weight row is streamed and unpacked once for all of them, and the tokens are
+// quantized in the launch's own prologue (no separate quantization launch).
+constexpr int TOK_MAX = 4;
+struct TokMember {
+    WeightView w;       // matrix (g of a SwiGLU pair)
+    WeightView w2;      // u of a SwiGLU pair (the matrix again otherwise)
+    float * y;          // token t, row r at y[t * y_stride + r]
+    const float * res;  // ADD: res[t * res_stride + r]; otherwise y (read, not used)
+    int rows, y_stride, res_stride, epi;
+    int wave_begin, waves;  // set at launch, as GemvMember's
+};
+struct TokArgs {
+    const float * x;       // token t's row at x + t * x_stride
+    const float * norm_w;  // per-token RMS norm folded into the quantization: its weight (NULL: none)
+    float eps;
+    int norm, norm_l2;
+    int cols, n_tok, x_stride;
+    int n_members;
+    TokMember m[4];
+    float wbound[4];  // per member: the largest block term magnitude over |d_x| * 2^40
+};
+
 constexpr int GEMV_MAXK = 16384;  // GEMV columns at most
 constexpr int GEMM_MAX_TOK = 32;  // tokens of one batched GEMV (two tiles of 16)
 constexpr int ATTN_CHUNK = 64;
@@ -290,6 +313,9 @@ hipError_t launch_argmax(const float * x, int n, unsigned long long * key, int r
 hipError_t launch_next_token(const NextTokenArgs & a, hipStream_t s);
 hipError_t launch_gemm_quant(const GemmQuantArgs & a, hipStream_t s);
 hipError_t launch_gemm(const GemmArgs & a, int type, hipStream_t s);
+// Whether launch_gemv_tok has an instance for this weight type, width, token count and member kind (a SwiGLU pair).
+bool gemv_tok_ok(int type, int cols, int n_tok, bool pair);
+hipError_t launch_gemv_tok(const TokArgs & a, int type, hipStream_t s);
 
 // Layout helpers (host and device).
 __host__ __device__ inline size_t gguf_row_bytes(int type, int cols) {

@@ -84,8 +84,9 @@ struct LArgmax { const float * x; int n; unsigned long long * key; int rows, str
 struct LNext { NextTokenArgs a; };
 struct LGemmQ { GemmQuantArgs a; };
 struct LGemm { GemmArgs a; int type; };
+struct LTok { TokArgs a; int type; uint32_t x_off, x_len; };  // x_off, x_len: the token rows read (activation floats)
 using Launch = std::variant<LGemv, LNorm, LEw, LConv, LRope, LGdn, LGated, LAttn, LRows, LArgmax, LNext, LGemmQ, LGemm,
-                            LGdnOut>;
+                            LGdnOut, LTok>;
 
 }  // namespace
 
@@ -517,7 +518,7 @@ struct Compiler {
         {
             const uint32_t * k = cmds + size_t(i) * GEMVQ_CMD_WORDS;
             const uint32_t op = k[0];
-            if (op != GEMVQ_OP_GEMM) lastq.on = false;
+            if (op != GEMVQ_OP_GEMM) lastq.on = tok_open = false;
             switch (op) {
             case GEMVQ_OP_GEMV: {
                 unsigned used = 0;
@@ -901,6 +902,44 @@ struct Compiler {
         } else if (flags & GEMVQ_GEMV_SILU) {
             g.epi = EPI_SILU;
         }
+        const uint32_t x_len = xs * (ntok - 1) + cols;
+        const uint32_t y_off = uint32_t(g.y - c->act), y_len = uint32_t(g.y_stride) * (ntok - 1) + uint32_t(rows);
+        // 2-4 tokens: the small-token GEMV, which quantizes the rows in every workgroup's prologue, so no output may
+        // fall on the rows or the norm weight (other workgroups may still be reading them)
+        if (gemv_tok_ok(t, int(cols), int(ntok), g.epi == EPI_SWIGLU) && !(y_off < k[6] + x_len && k[6] < y_off + y_len) &&
+            !(normw && y_off < k2[5] + cols && k2[5] < y_off + y_len)) {
+            TokArgs ta{};
+            ta.x = A(k[6]);
+            ta.norm_w = normw ? A(k2[5]) : nullptr;
+            ta.eps = bits_f(k2[6]);
+            ta.norm = norm ? 1 : 0;
+            ta.norm_l2 = (nflags & GEMVQ_NORM_L2) ? 1 : 0;
+            ta.cols = int(cols);
+            ta.n_tok = int(ntok);
+            ta.x_stride = int(xs);
+            ta.n_members = 1;
+            ta.wbound[0] = g.wbound[0];
+            TokMember & m = ta.m[0];
+            m.w = g.w;
+            m.w2 = g.w2;
+            m.y = g.y;
+            m.res = g.res;
+            m.rows = rows;
+            m.y_stride = g.y_stride;
+            m.res_stride = g.res_stride;
+            m.epi = g.epi;
+            if (!merge_tok(ta, t, k[6], x_len, int(i), int(used))) {
+                out.push_back(LTok{ta, t, k[6], x_len});
+                spans.push_back({int(i), int(used)});
+            }
+            tok_open = true;
+            // the outputs end a reuse of the last batched GEMV's quantized rows if they fall on its rows or weight
+            const bool hits_x = y_off < lastq.x_off + lastq.x_len && lastq.x_off < y_off + y_len;
+            const uint32_t w_off = lastq.q.norm_w ? uint32_t(lastq.q.norm_w - c->act) : 0;
+            if (hits_x || (lastq.q.norm_w && y_off < w_off + lastq.q.cols && w_off < y_off + y_len)) lastq.on = false;
+            return true;
+        }
+        tok_open = false;
         GemmQuantArgs q{};
         q.x = A(k[6]);
         q.norm_w = normw ? A(k2[5]) : nullptr;
@@ -917,7 +956,6 @@ struct Compiler {
         g.q = c->gemm_q;
         g.d40 = c->gemm_d;
         g.s40 = c->gemm_s;
-        const uint32_t x_len = xs * (ntok - 1) + cols;
         const bool same = lastq.on && lastq.x_off == k[6] && lastq.x_len == x_len && lastq.q.n_tok == q.n_tok &&
                           lastq.q.cols == q.cols && lastq.q.x_stride == q.x_stride && lastq.q.norm == q.norm &&
                           lastq.q.norm_l2 == q.norm_l2 && lastq.q.norm_w == q.norm_w && lastq.q.eps == q.eps;
@@ -931,11 +969,43 @@ struct Compiler {
             spans.push_back({int(i), int(used)});
         }
         // outputs written over the quantized rows (or the norm weight) end the reuse
-        const uint32_t y_off = uint32_t(g.y - c->act), y_len = uint32_t(g.y_stride) * (ntok - 1) + uint32_t(rows);
         const bool hits_x = y_off < lastq.x_off + lastq.x_len && lastq.x_off < y_off + y_len;
         const uint32_t w_off = q.norm_w ? uint32_t(q.norm_w - c->act) : 0;
         const bool hits_w = q.norm_w && y_off < w_off + cols && w_off < y_off + y_len;
         if (hits_x || hits_w) lastq.on = false;
+        return true;
+    }
+
+    // A small-token GEMM right after another on the same rows (the same token count, stride and norm) joins its launch
+    // as a further member (up to four, none a SwiGLU pair), under the rules of merge_gemm; no member writes the rows
+    // or the norm weight (checked before).
+    bool tok_open = false;  // the last command was a GEMM that made or joined the last launch, an LTok
+    bool merge_tok(const TokArgs & g, int t, uint32_t x_off, uint32_t x_len, int i, int used) {
+        auto * p = out.empty() || !tok_open ? nullptr : std::get_if<LTok>(&out.back());
+        if (!p || p->type != t || p->x_off != x_off || p->x_len != x_len || p->a.n_members >= 4 ||
+            p->a.m[0].epi == EPI_SWIGLU || g.m[0].epi == EPI_SWIGLU || p->a.n_tok != g.n_tok || p->a.cols != g.cols ||
+            p->a.x_stride != g.x_stride || p->a.norm != g.norm || p->a.norm_l2 != g.norm_l2 || p->a.norm_w != g.norm_w ||
+            p->a.eps != g.eps)
+            return false;
+        struct R { uint64_t lo, hi; };
+        auto span = [&](const float * base, int stride, int rows) {
+            const uint64_t lo = uint64_t(base - c->act);
+            return R{lo, lo + uint64_t(stride) * uint64_t(g.n_tok - 1) + uint64_t(rows)};
+        };
+        auto meet = [](R x, R y) { return x.lo < y.hi && y.lo < x.hi; };
+        const TokMember & nm = g.m[0];
+        const R ny = span(nm.y, nm.y_stride, nm.rows);
+        const bool nres = nm.epi == EPI_ADD;
+        const R nr = nres ? span(nm.res, nm.res_stride, nm.rows) : R{0, 0};
+        for (int m = 0; m < p->a.n_members; ++m) {
+            const TokMember & o = p->a.m[m];
+            const R y = span(o.y, o.y_stride, o.rows);
+            const R res = o.epi == EPI_ADD ? span(o.res, o.res_stride, o.rows) : R{0, 0};
+            if (meet(ny, y) || (o.epi == EPI_ADD && meet(ny, res)) || (nres && meet(nr, y))) return false;
+        }
+        p->a.wbound[p->a.n_members] = g.wbound[0];
+        p->a.m[p->a.n_members++] = nm;
+        spans.back().second = i + used - spans.back().first;
         return true;
     }
 
@@ -1208,6 +1278,16 @@ std::pair<std::string, uint64_t> describe(const Launch & l, int pos) {
         const uint64_t act = uint64_t(a.n_tok) * (a.cols + (a.cols / 32) * 4);
         return {"gemm_kernel<" + std::to_string(x->type) + ">", w + act + out};
     }
+    if (auto * x = std::get_if<LTok>(&l)) {
+        const TokArgs & a = x->a;
+        uint64_t w = 0, out = 0;
+        for (int m = 0; m < a.n_members; ++m) {
+            w += uint64_t(a.m[m].rows) * gguf_row_bytes(x->type, a.cols) * (a.m[m].epi == EPI_SWIGLU ? 2 : 1);
+            out += uint64_t(a.n_tok) * a.m[m].rows * 4 * (a.m[m].epi == EPI_ADD ? 2 : 1);
+        }
+        const uint64_t act = uint64_t(a.n_tok) * a.cols * 4 + (a.norm_w ? uint64_t(a.cols) * 4 : 0);
+        return {"gemv_tok_kernel<" + std::to_string(x->type) + "," + std::to_string(a.n_tok) + ">", w + act + out};
+    }
     return {"next_token_kernel", 32};
 }
 
@@ -1228,6 +1308,7 @@ hipError_t issue(const std::vector<Launch> & ls, hipStream_t s) {
         else if (auto * x = std::get_if<LGemmQ>(&l)) e = launch_gemm_quant(x->a, s);
         else if (auto * x = std::get_if<LGemm>(&l)) e = launch_gemm(x->a, x->type, s);
         else if (auto * x = std::get_if<LGdnOut>(&l)) e = launch_gdn_out(x->a, x->type, s);
+        else if (auto * x = std::get_if<LTok>(&l)) e = launch_gemv_tok(x->a, x->type, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

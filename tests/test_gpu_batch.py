@@ -3,7 +3,8 @@ sequence by one position with each layer's weight rows read once for all of them
 step and attention in their sequences forms. Every sequence must equal a single-sequence decode of its own prompt
 bit for bit: its token ids over the prompt and the generation, and its last logits. Prompts of different lengths
 (sequences switch from prompt tokens to generated ones at different steps), a K-quant head (one GEMV per sequence)
-and a Q8_0 head (one GEMM over all sequences), up to the largest batch."""
+and a Q8_0 head (one GEMM over all sequences), up to the largest batch; 2-4 sequences run their projections as
+small-token GEMVs, 5 and more as MFMA batched GEMVs."""
 import numpy as np
 import pytest
 
@@ -25,7 +26,8 @@ def small(n_layer=4, n_ctx=48):
                          head_dim=128, n_rot=32, ssm_k_heads=2, ssm_v_heads=4, n_ctx=n_ctx)
 
 
-@pytest.mark.parametrize("n_seq,head,steps", [(4, "q6_k", 20), (5, "q8_0", 16), (32, "q6_k", 6)])
+@pytest.mark.parametrize("n_seq,head,steps", [(2, "q8_0", 14), (3, "q6_k", 12), (4, "q6_k", 20), (5, "q8_0", 16),
+                                             (32, "q6_k", 6)])
 def test_lockstep_sequences_equal_single_decodes(gq, q35, n_seq, head, steps):
     cfg = small()
     types = {"output.weight": gq.Q8_0} if head == "q8_0" else None

@@ -1,7 +1,8 @@
 """The batched GEMV (GEMM command) on the GPU through the C ABI. Every token's output row must equal, bit for bit, the
 oracle's single-token GEMV of that token's row and the GPU's own GEMV command on it: the same activation quantizer,
 the same exact block terms, the same epilogs, only the block sums come from int8 MFMAs. Covered: Q4_0, Q4_1 and Q8_0;
-1, 5, 16, 17, 20 and 32 tokens (one and two token tiles, padding tokens); row counts that are not a multiple of the
+1, 5, 16, 17, 20 and 32 tokens (one and two token tiles, padding tokens; 2-4 tokens run as a small-token GEMV,
+tests/test_gpu_gemm_tok.py); row counts that are not a multiple of the
 16-row tile; 2560, 4096 and 12288 columns; strided rows; the SwiGLU pair, residual ADD and SiLU epilogs; the folded
 per-token RMS norm (with and without weight, L2); output rows over the input rows; invalid commands."""
 import numpy as np
@@ -261,7 +262,9 @@ def test_gemm_reuses_quantized_rows_until_overwritten(gq, orc, ctx):
 def test_gemm_group_of_members(gq, orc, ctx, ntok):
     """Consecutive GEMMs of one format on the same quantized rows run as one launch (up to four members, each with its
     own rows, output and epilog; rows that are not whole 16-row tiles); an output that overlaps an earlier member's
-    output or feeds its residual starts a new launch, so the commands' order still decides the result."""
+    output or feeds its residual starts a new launch, so the commands' order still decides the result. With 3 tokens
+    the groups are small-token GEMV launches, which quantize the rows themselves (no quantization launch)."""
+    q = 0 if ntok <= 4 else 1  # the quantization launch of the MFMA path
     cols, eps = 1024, 1e-6
     shapes = [(100, gq.GEMV_SILU), (33, 0), (512, gq.GEMV_ADD), (16, 0), (48, 0)]
     ws = [gq.matrix(2, r, cols, 8, 60 + j, std=0.02) for j, (r, _) in enumerate(shapes)]
@@ -295,7 +298,7 @@ def test_gemm_group_of_members(gq, orc, ctx, ntok):
         return v
 
     assert ctx.run(sum((cmd(j, Y[j]) for j in range(5)), [])) == 0, ctx.error()
-    assert ctx.launch_count() == 3  # one quantization, a group of four, then the fifth member's own launch
+    assert ctx.launch_count() == q + 2  # (the quantization,) a group of four, then the fifth member's own launch
     for j, (r, _) in enumerate(shapes):
         got = ctx.read(Y[j], ntok * up16(r)).reshape(ntok, up16(r))[:, :r]
         for t in range(ntok):
@@ -303,7 +306,7 @@ def test_gemm_group_of_members(gq, orc, ctx, ntok):
     # the second output overlaps the first's (rows 48..80 of every token): two launches, the later command's values
     # win where they overlap
     assert ctx.run(cmd(0, Y[0]) + cmd(1, Y[0] + 48, ys=112)) == 0, ctx.error()
-    assert ctx.launch_count() == 3
+    assert ctx.launch_count() == q + 2
     got = ctx.read(Y[0], ntok * 112).reshape(ntok, 112)[:, :100]
     for t in range(ntok):
         first = want(0, t)
@@ -313,7 +316,7 @@ def test_gemm_group_of_members(gq, orc, ctx, ntok):
     # a member whose residual is an earlier member's output (rows 0..15 of every token): a new launch that adds the
     # new values
     assert ctx.run(cmd(3, RES, ys=512) + cmd(2, Y[2])) == 0, ctx.error()
-    assert ctx.launch_count() == 3
+    assert ctx.launch_count() == q + 2
     got = ctx.read(Y[2], ntok * 512).reshape(ntok, 512)
     for t in range(ntok):
         r16 = want(3, t)
