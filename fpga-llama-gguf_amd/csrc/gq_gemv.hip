@@ -11,12 +11,21 @@ hipError_t launch_gemv_q6_k(const GemvArgs & a, hipStream_t st);
 
 hipError_t launch_gemv_tok_q4_0(const TokArgs & a, hipStream_t st);
 hipError_t launch_gemv_tok_q8_0(const TokArgs & a, hipStream_t st);
+hipError_t launch_gemv_tok_q5_k(const TokArgs & a, hipStream_t st);
+hipError_t launch_gemv_tok_q6_k(const TokArgs & a, hipStream_t st);
 
+// The instances of gq_gemv_tok_impl.h: Q4_0 / Q8_0 with 2-4 tokens up to 4096 columns and 2 up to 12288 (SwiGLU
+// pairs included); Q5_K / Q6_K with 1-4 tokens up to 4096 columns and 1-2 up to 12288 (no pairs).
 bool gemv_tok_ok(int type, int cols, int n_tok, bool pair) {
-    (void)pair;  // every instance has both member kinds
-    if ((type != T_Q4_0 && type != T_Q8_0) || cols <= 0 || cols % 32 || cols > GEMV_MAXK) return false;
+    if (cols <= 0 || cols > GEMV_MAXK || n_tok < 1 || n_tok > TOK_MAX) return false;
+    if (type == T_Q5_K || type == T_Q6_K) {
+        if (pair || cols % 256) return false;
+        const int nu = (cols / 64 + 63) / 64;
+        return nu == 1 || (nu <= 3 && n_tok <= 2);
+    }
+    if ((type != T_Q4_0 && type != T_Q8_0) || cols % 32) return false;
     const int nu = (cols / 32 + 63) / 64;
-    return n_tok >= 2 && n_tok <= TOK_MAX && (nu <= 2 || (nu <= 6 && n_tok == 2));
+    return n_tok >= 2 && (nu <= 2 || (nu <= 6 && n_tok == 2));
 }
 
 hipError_t launch_gemv_tok(const TokArgs & a, int type, hipStream_t st) {
@@ -24,7 +33,12 @@ hipError_t launch_gemv_tok(const TokArgs & a, int type, hipStream_t st) {
     for (int i = 0; i < a.n_members; ++i) pair = pair || a.m[i].epi == EPI_SWIGLU;
     if (!gemv_tok_ok(type, a.cols, a.n_tok, pair) || a.n_members < 1 || a.n_members > 4 || (pair && a.n_members != 1))
         return hipErrorInvalidValue;
-    return type == T_Q4_0 ? launch_gemv_tok_q4_0(a, st) : launch_gemv_tok_q8_0(a, st);
+    switch (type) {
+    case T_Q4_0: return launch_gemv_tok_q4_0(a, st);
+    case T_Q8_0: return launch_gemv_tok_q8_0(a, st);
+    case T_Q5_K: return launch_gemv_tok_q5_k(a, st);
+    default: return launch_gemv_tok_q6_k(a, st);
+    }
 }
 
 hipError_t launch_gemv(const GemvArgs & a, int type, hipStream_t st) {

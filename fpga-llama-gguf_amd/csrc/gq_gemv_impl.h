@@ -287,15 +287,18 @@ __device__ __forceinline__ void prologue_finish(const GemvArgs & a, XF<R, XS> & 
 
 // Q8_K of the activation (gemvq_ref.h:62-81): one wave per 256-block, 4 values per lane; the signed value of the
 // largest magnitude at the first index; bsums per 16.
-__device__ void quantize_q8_K(const GemvArgs & a, float scale, Lds & s) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nsb = a.cols / 256;
+// x: cols floats; with norm, v = (x * scale) * w (w = norm_w, or 1 without one) before quantizing. Writes the quants
+// xq, the bsums bs and the FP32 d bits info of each super-block.
+__device__ void quantize_q8_K(const float * x, int cols, bool norm, const float * norm_w, float scale, int8_t * xq,
+                              int16_t * bs, uint32_t * info) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nsb = cols / 256;
     for (int sb = wave; sb < nsb; sb += NWAVES) {
         const int base = sb * 256 + lane * 4;
-        const float4 t = *reinterpret_cast<const float4 *>(a.x + base);
+        const float4 t = *reinterpret_cast<const float4 *>(x + base);
         float v[4] = {t.x, t.y, t.z, t.w};
-        if (a.xsrc == XSRC_NORM) {
-            if (a.norm_w) {
-                const float4 w = *reinterpret_cast<const float4 *>(a.norm_w + base);
+        if (norm) {
+            if (norm_w) {
+                const float4 w = *reinterpret_cast<const float4 *>(norm_w + base);
                 v[0] = (v[0] * scale) * w.x;
                 v[1] = (v[1] * scale) * w.y;
                 v[2] = (v[2] * scale) * w.z;
@@ -336,12 +339,15 @@ __device__ void quantize_q8_K(const GemvArgs & a, float scale, Lds & s) {
             }
             d = 1.0f / iscale;
         }
-        *reinterpret_cast<uint32_t *>(s.xq + base) = packed;
+        *reinterpret_cast<uint32_t *>(xq + base) = packed;
         part += __shfl_xor(part, 1, WAVE);
         part += __shfl_xor(part, 2, WAVE);
-        if ((lane & 3) == 0) s.bs[sb * 16 + (lane >> 2)] = int16_t(part);
-        if (lane == 0) s.info[sb] = __float_as_uint(d);
+        if ((lane & 3) == 0) bs[sb * 16 + (lane >> 2)] = int16_t(part);
+        if (lane == 0) info[sb] = __float_as_uint(d);
     }
+}
+__device__ void quantize_q8_K(const GemvArgs & a, float scale, Lds & s) {
+    quantize_q8_K(a.x, a.cols, a.xsrc == XSRC_NORM, a.norm_w, scale, s.xq, s.bs, s.info);
 }
 
 // ---- per-lane activation slices ----
@@ -380,7 +386,8 @@ __device__ __forceinline__ void load_xb(const Lds & s, int b, int nb, XB & x) {
 }
 
 template <int TYPE>
-__device__ __forceinline__ void load_xk(const Lds & s, int u, int nu, XK & x) {
+__device__ __forceinline__ void load_xk(const int8_t * xq, const int16_t * bsv, const uint32_t * info, int u, int nu,
+                                        XK & x) {
     u = u < nu ? u : nu - 1;
     const int sb = u >> 2, part = u & 3;
     int off0, off1, g0, g1;
@@ -396,20 +403,24 @@ __device__ __forceinline__ void load_xk(const Lds & s, int u, int nu, XK & x) {
         g0 = (64 * part) / 16;
         g1 = g0 + 2;
     }
-    const uint4 * p0 = reinterpret_cast<const uint4 *>(s.xq + off0);
-    const uint4 * p1 = reinterpret_cast<const uint4 *>(s.xq + off1);
+    const uint4 * p0 = reinterpret_cast<const uint4 *>(xq + off0);
+    const uint4 * p1 = reinterpret_cast<const uint4 *>(xq + off1);
     const uint4 a0 = p0[0], a1 = p0[1], b0 = p1[0], b1 = p1[1];
     x.q[0] = a0.x; x.q[1] = a0.y; x.q[2] = a0.z; x.q[3] = a0.w;
     x.q[4] = a1.x; x.q[5] = a1.y; x.q[6] = a1.z; x.q[7] = a1.w;
     x.q[8] = b0.x; x.q[9] = b0.y; x.q[10] = b0.z; x.q[11] = b0.w;
     x.q[12] = b1.x; x.q[13] = b1.y; x.q[14] = b1.z; x.q[15] = b1.w;
-    x.bs[0] = s.bs[sb * 16 + g0];
-    x.bs[1] = s.bs[sb * 16 + g0 + 1];
-    x.bs[2] = s.bs[sb * 16 + g1];
-    x.bs[3] = s.bs[sb * 16 + g1 + 1];
-    const float d = __uint_as_float(s.info[sb]);
+    x.bs[0] = bsv[sb * 16 + g0];
+    x.bs[1] = bsv[sb * 16 + g0 + 1];
+    x.bs[2] = bsv[sb * 16 + g1];
+    x.bs[3] = bsv[sb * 16 + g1 + 1];
+    const float d = __uint_as_float(info[sb]);
     float_parts(d, x.m, x.e);
     x.neg = d < 0.0f;
+}
+template <int TYPE>
+__device__ __forceinline__ void load_xk(const Lds & s, int u, int nu, XK & x) {
+    load_xk<TYPE>(s.xq, s.bs, s.info, u, nu, x);
 }
 
 // ---- weight loads and unit dots ----

@@ -1,21 +1,27 @@
 #pragma once
-// The GEMM command for 2-4 tokens (TokArgs) on the single-token GEMV's structure: the same workgroups, XCD slices,
-// rows in flight and exact block terms as gemv_kernel, with every lane holding its activation blocks of all T
-// tokens in registers. A weight row is streamed and unpacked once and its block terms are formed for each token;
-// each token's row total is rounded once and goes through the member's epilog. The tokens are quantized in the
-// prologue of every workgroup, each exactly as the single-token prologue quantizes one vector (the same norm scale
-// tree and quantizer), so token t's output row is the single-token GEMV's (and the MFMA batched GEMV's) bit for
-// bit. It replaces a quantization launch plus a batched GEMV whose time is that of 16 tokens (one MFMA tile).
+// The GEMM command for 1-4 tokens (TokArgs) on the single-token GEMV's structure: the same workgroups, XCD slices,
+// rows in flight and exact block (K-quant super-block) terms as gemv_kernel, with every lane holding its activation
+// blocks (units) of all T tokens in registers. A weight row is streamed and unpacked once and its block terms are
+// formed for each token; each token's row total is rounded once and goes through the member's epilog. The tokens
+// are quantized in the prologue of every workgroup, each exactly as the single-token prologue quantizes one vector
+// (the same norm scale tree and quantizer), so token t's output row is the single-token GEMV's (and the MFMA
+// batched GEMV's) bit for bit. For Q4_0 / Q8_0 it replaces a quantization launch plus a batched GEMV whose time is
+// that of 16 tokens (one MFMA tile); for the K-quants, which have no MFMA form, one GEMV per token.
 #include "gq_gemv_impl.h"
 
 namespace gq {
 namespace {
 
-template <int T, int NU, int R>
-struct LdsTok {  // T quantized activations of at most 2048 NU columns
-    int8_t xq[T][2048 * NU];
-    uint32_t info[T][64 * NU];
-    uint16_t s1[T][64 * NU];
+template <bool KQ, int NU>
+constexpr int tok_cols() { return (KQ ? 4096 : 2048) * NU; }  // columns at most: 64 NU blocks or units per row
+
+template <int T, int NU, int R, bool KQ>
+struct LdsTok {  // T quantized activations: Q8_0 (d | sum words, Q8_1 s) or Q8_K (d bits per super-block, bsums)
+    static constexpr int C = tok_cols<KQ, NU>();
+    int8_t xq[T][C];
+    uint32_t info[T][KQ ? C / 256 : C / 32];
+    uint16_t s1[T][KQ ? 1 : C / 32];
+    int16_t bs[T][KQ ? C / 16 : 1];
     float red[T * R * NWAVES];
 };
 
@@ -40,11 +46,12 @@ __device__ __forceinline__ void tok_fetch(const TokArgs & a, XT<T, R> & f) {
     }
 }
 
-// Each token as prologue_finish does one vector (XSRC_NORM or the raw rows): the canonical norm scale (a tree over
-// each item's 16 squares, pairwise over a wave's 64 items, the 4 waves of a round and the rounds), v = (x * scale)
-// * w, then Q8_0 (and the Q8_1 s) into the token's LDS rows.
-template <int T, int NU, int R>
-__device__ __forceinline__ void tok_finish(const TokArgs & a, XT<T, R> & f, LdsTok<T, NU, R> & s) {
+// Each token as the single-token prologue does one vector (XSRC_NORM or the raw rows): the canonical norm scale (a
+// tree over each item's 16 squares, pairwise over a wave's 64 items, the 4 waves of a round and the rounds), then
+// Q8_0 (and the Q8_1 s) of v = (x * scale) * w into the token's LDS rows, or for K-quant weights Q8_K of the same v
+// (quantize_q8_K, which reads the row again in its own layout).
+template <int T, int NU, int R, bool KQ>
+__device__ __forceinline__ void tok_finish(const TokArgs & a, XT<T, R> & f, LdsTok<T, NU, R, KQ> & s) {
     const int n16 = a.cols / 16, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float sc[T];
 #pragma unroll
@@ -75,6 +82,12 @@ __device__ __forceinline__ void tok_finish(const TokArgs & a, XT<T, R> & f, LdsT
             sc[t] = a.norm_l2 ? 1.0f / fmaxf(sqrtf(sum), a.eps) : 1.0f / sqrtf(sum / float(a.cols) + a.eps);
         }
     }
+    if constexpr (KQ) {
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+            quantize_q8_K(a.x + size_t(t) * a.x_stride, a.cols, a.norm != 0, a.norm_w, sc[t], s.xq[t], s.bs[t], s.info[t]);
+        return;
+    }
     const bool normw = a.norm && a.norm_w != nullptr;
 #pragma unroll
     for (int g = 0; g < R; ++g) {
@@ -99,22 +112,38 @@ __device__ __forceinline__ void tok_finish(const TokArgs & a, XT<T, R> & f, LdsT
     }
 }
 
+template <int T>
+constexpr int tok_groups() { return T == 1 ? 1 : T == 2 ? 2 : 4; }  // lane groups of a row's reduction
+
 template <int TYPE, int NU, bool PAIR>
-struct TSlot {  // one row in flight: its blocks (of g and u for a SwiGLU pair) and the lane's epilog operand
-    WB wb[NU], wb2[PAIR ? NU : 1];
+struct TSlot {  // one row in flight: its blocks (of g and u for a SwiGLU pair) or K-quant units, and the lane's
+                // epilog operand
+    static constexpr bool KQ = TYPE == T_Q5_K || TYPE == T_Q6_K;
+    WB wb[KQ ? 1 : NU], wb2[(KQ || !PAIR) ? 1 : NU];
+    WK wk[KQ ? NU : 1];
     float e;  // ADD: the residual of row r for the lane group's token
 };
 
 // Loads of row r. Lane group g (of G groups of 64 / G lanes) takes token min(g, T - 1)'s epilog operand (a
 // member without a residual reads its own output row, unused), so no load sits behind a branch.
 template <int TYPE, int NU, bool PAIR, int T>
-__device__ __forceinline__ void load_tok_slot(const TokMember & m, int r, int lane, int nb, TSlot<TYPE, NU, PAIR> & o) {
-    constexpr int G = T == 2 ? 2 : 4, GW = 64 / G;
+__device__ __forceinline__ void load_tok_slot(const TokMember & m, int r, int lane, int nb, int nu,
+                                              TSlot<TYPE, NU, PAIR> & o) {
+    constexpr int G = tok_groups<T>(), GW = 64 / G;
+    if constexpr (TSlot<TYPE, NU, PAIR>::KQ) {
+        const int nsb = nu >> 2;
 #pragma unroll
-    for (int k = 0; k < NU; ++k) {
-        const int b = lane + 64 * k, bb = b < nb ? b : nb - 1;
-        load_wb<TYPE>(m.w, size_t(r) * nb + bb, o.wb[k]);
-        if constexpr (PAIR) load_wb<TYPE>(m.w2, size_t(r) * nb + bb, o.wb2[k]);
+        for (int k = 0; k < NU; ++k) {
+            const int u0 = lane + 64 * k, u = u0 < nu ? u0 : nu - 1;
+            load_wk<TYPE>(m.w, size_t(r) * nsb + (u >> 2), u & 3, o.wk[k]);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < NU; ++k) {
+            const int b = lane + 64 * k, bb = b < nb ? b : nb - 1;
+            load_wb<TYPE>(m.w, size_t(r) * nb + bb, o.wb[k]);
+            if constexpr (PAIR) load_wb<TYPE>(m.w2, size_t(r) * nb + bb, o.wb2[k]);
+        }
     }
     const int g = lane / GW, tk = g < T ? g : T - 1;
     o.e = m.res[size_t(tk) * m.res_stride + r];
@@ -125,7 +154,7 @@ __device__ __forceinline__ void load_tok_slot(const TokMember & m, int r, int la
 template <int T, bool PAIR>
 __device__ __forceinline__ void finish_tok_row(const TokMember & m, int r, const long long * p, const long long * p2,
                                                float ev, int lane) {
-    constexpr int G = T == 2 ? 2 : 4, GW = 64 / G;
+    constexpr int G = tok_groups<T>(), GW = 64 / G;
     long long pp[G];
 #pragma unroll
     for (int j = 0; j < G; ++j) pp[j] = j < T ? p[j < T ? j : 0] : 0;
@@ -148,13 +177,18 @@ __device__ __forceinline__ void finish_tok_row(const TokMember & m, int r, const
 }
 
 template <int TYPE, int NU, bool PAIR, int T, bool EXACT>
-__device__ __forceinline__ void tok_partials(const TSlot<TYPE, NU, PAIR> & sl, int r, int nb, const XB (*xb)[NU],
-                                             int lane, long long * p, long long * p2) {
+__device__ __forceinline__ void tok_partials(const TSlot<TYPE, NU, PAIR> & sl, int r, int nb, int nu,
+                                             const XB (*xb)[NU], const XK (*xk)[NU], int lane, long long * p,
+                                             long long * p2) {
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-        p[t] = lane_blocks<TYPE, NU, EXACT>(sl.wb, r, true, nb, xb[t], lane, nullptr);
         p2[t] = 0;
-        if constexpr (PAIR) p2[t] = lane_blocks<TYPE, NU, EXACT>(sl.wb2, r, true, nb, xb[t], lane, nullptr);
+        if constexpr (TSlot<TYPE, NU, PAIR>::KQ) {
+            p[t] = lane_units<TYPE, NU>(sl.wk, r, true, nu, xk[t], lane, nullptr);
+        } else {
+            p[t] = lane_blocks<TYPE, NU, EXACT>(sl.wb, r, true, nb, xb[t], lane, nullptr);
+            if constexpr (PAIR) p2[t] = lane_blocks<TYPE, NU, EXACT>(sl.wb2, r, true, nb, xb[t], lane, nullptr);
+        }
     }
 }
 
@@ -162,16 +196,16 @@ __device__ __forceinline__ void tok_partials(const TSlot<TYPE, NU, PAIR> & sl, i
 // as its partials are formed (unconditionally while rows follow, so the compiler's waits stay exact).
 template <int TYPE, int NU, bool PAIR, int T, int DS, bool EXACT>
 __device__ __forceinline__ void tok_rows(const TokMember & m, int w, int S, int n, TSlot<TYPE, NU, PAIR> * sl,
-                                         const XB (*xb)[NU], int lane, int nb) {
+                                         const XB (*xb)[NU], const XK (*xk)[NU], int lane, int nb, int nu) {
     long long p[T], p2[T];
     int k = 0;
     for (; k + DS < n; k += DS) {
 #pragma unroll
         for (int j = 0; j < DS; ++j) {
             const int r = w + (k + j) * S;
-            tok_partials<TYPE, NU, PAIR, T, EXACT>(sl[j], r, nb, xb, lane, p, p2);
+            tok_partials<TYPE, NU, PAIR, T, EXACT>(sl[j], r, nb, nu, xb, xk, lane, p, p2);
             const float ev = sl[j].e;
-            load_tok_slot<TYPE, NU, PAIR, T>(m, w + min(k + j + DS, n - 1) * S, lane, nb, sl[j]);
+            load_tok_slot<TYPE, NU, PAIR, T>(m, w + min(k + j + DS, n - 1) * S, lane, nb, nu, sl[j]);
             finish_tok_row<T, PAIR>(m, r, p, p2, ev, lane);
         }
     }
@@ -179,23 +213,24 @@ __device__ __forceinline__ void tok_rows(const TokMember & m, int w, int S, int 
     for (int j = 0; j < DS; ++j) {
         if (k + j < n) {
             const int r = w + (k + j) * S;
-            tok_partials<TYPE, NU, PAIR, T, EXACT>(sl[j], r, nb, xb, lane, p, p2);
+            tok_partials<TYPE, NU, PAIR, T, EXACT>(sl[j], r, nb, nu, xb, xk, lane, p, p2);
             finish_tok_row<T, PAIR>(m, r, p, p2, sl[j].e, lane);
         }
     }
 }
 
-// Rows in flight per wave: two for plain members of at most 4096 columns, one for SwiGLU pairs and wider rows
-// (whose T tokens' activation blocks already take most of the registers).
-template <int NU, bool PAIR>
-constexpr int tok_slots() { return PAIR || NU > 2 ? 1 : 2; }
+// Rows in flight per wave: two for plain members of at most 4096 columns (Q4_0 / Q8_0), one for SwiGLU pairs, wider
+// rows and K-quant units (whose T tokens' activations already take most of the registers).
+template <int TYPE, int NU, bool PAIR>
+constexpr int tok_slots() { return PAIR || NU > 2 || TYPE == T_Q5_K || TYPE == T_Q6_K ? 1 : 2; }
 
 template <int TYPE, int NU, bool PAIR, int T>
 __global__ __launch_bounds__(NT) void gemv_tok_kernel(TokArgs a) {
-    constexpr int DS = tok_slots<NU, PAIR>();
-    constexpr int R = (128 * NU + NT - 1) / NT;  // rounds of NT activation items per token (cols <= 2048 NU)
-    __shared__ LdsTok<T, NU, R> s;
-    const int lane = threadIdx.x & 63, nb = a.cols / 32;
+    constexpr bool KQ = TYPE == T_Q5_K || TYPE == T_Q6_K;
+    constexpr int DS = tok_slots<TYPE, NU, PAIR>();
+    constexpr int R = (tok_cols<KQ, NU>() / 16 + NT - 1) / NT;  // rounds of NT activation items per token
+    __shared__ LdsTok<T, NU, R, KQ> s;
+    const int lane = threadIdx.x & 63, nb = a.cols / 32, nu = a.cols / 64;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // workgroup b serves slice b % 8 of every member's rows (one XCD's L2), as gemv_kernel
     const int xs = blockIdx.x & 7, lw = (blockIdx.x >> 3) * NWAVES + wave;
@@ -214,28 +249,37 @@ __global__ __launch_bounds__(NT) void gemv_tok_kernel(TokArgs a) {
     TSlot<TYPE, NU, PAIR> sl[DS];
 #pragma unroll
     for (int j = 0; j < DS; ++j)
-        load_tok_slot<TYPE, NU, PAIR, T>(m, n > 0 ? w + min(j, n - 1) * S : m.rows - 1, lane, nb, sl[j]);
-    tok_finish<T, NU, R>(a, f, s);
+        load_tok_slot<TYPE, NU, PAIR, T>(m, n > 0 ? w + min(j, n - 1) * S : m.rows - 1, lane, nb, nu, sl[j]);
+    tok_finish<T, NU, R, KQ>(a, f, s);
     __syncthreads();
-    XB xb[T][NU];
+    XB xb[T][NU];  // (only the arrays of the weight kind are used; the other is removed by the compiler)
+    XK xk[T][NU];
+    bool exact = false;
+    if constexpr (KQ) {  // super-block terms are summed in int64
 #pragma unroll
-    for (int t = 0; t < T; ++t)
+        for (int t = 0; t < T; ++t)
 #pragma unroll
-        for (int k = 0; k < NU; ++k) load_xb<TYPE>(s.xq[t], s.info[t], s.s1[t], lane + 64 * k, nb, xb[t][k]);
-    // the single-token kernel's bound on a lane's FP64 partial (below 2^53 LSB), for every token: a wave where it
-    // could be passed sums its terms in two FP64 parts (EXACT)
-    bool big = false;
+            for (int k = 0; k < NU; ++k) load_xk<TYPE>(s.xq[t], s.bs[t], s.info[t], lane + 64 * k, nu, xk[t][k]);
+    } else {
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-        float dsum = 0.0f;
+        for (int t = 0; t < T; ++t)
 #pragma unroll
-        for (int k = 0; k < NU; ++k) dsum += fabsf(xb[t][k].dx40);
-        big = big || !(a.wbound[mi] * dsum < 4503599627370496.0f);
+            for (int k = 0; k < NU; ++k) load_xb<TYPE>(s.xq[t], s.info[t], s.s1[t], lane + 64 * k, nb, xb[t][k]);
+        // the single-token kernel's bound on a lane's FP64 partial (below 2^53 LSB), for every token: a wave where
+        // it could be passed sums its terms in two FP64 parts (EXACT)
+        bool big = false;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            float dsum = 0.0f;
+#pragma unroll
+            for (int k = 0; k < NU; ++k) dsum += fabsf(xb[t][k].dx40);
+            big = big || !(a.wbound[mi] * dsum < 4503599627370496.0f);
+        }
+        exact = __builtin_amdgcn_ballot_w64(big) != 0;
     }
-    const bool exact = __builtin_amdgcn_ballot_w64(big) != 0;
     if (n > 0) {
-        if (exact) tok_rows<TYPE, NU, PAIR, T, DS, true>(m, w, S, n, sl, xb, lane, nb);
-        else tok_rows<TYPE, NU, PAIR, T, DS, false>(m, w, S, n, sl, xb, lane, nb);
+        if (!KQ && exact) tok_rows<TYPE, NU, PAIR, T, DS, true>(m, w, S, n, sl, xb, xk, lane, nb, nu);
+        else tok_rows<TYPE, NU, PAIR, T, DS, false>(m, w, S, n, sl, xb, xk, lane, nb, nu);
     }
 }
 
@@ -251,19 +295,26 @@ hipError_t launch_tok_typed(const TokArgs & a0, hipStream_t st) {
         }
         if (m.epi != EPI_SWIGLU) m.w2 = m.w;
     }
-    const int grid = plan_waves(a, cap, tok_slots<NU, PAIR>());
+    const int grid = plan_waves(a, cap, tok_slots<TYPE, NU, PAIR>());
     GQ_LAUNCH((gemv_tok_kernel<TYPE, NU, PAIR, T>), dim3(grid), dim3(NT), 0, st, a);
     return hipGetLastError();
 }
 
-// Instances: T = 2-4 tokens for rows of at most 4096 columns (NU <= 2), T = 2 up to 12288 columns (NU <= 6).
-constexpr bool tok_instance(int nu, int t) { return t >= 2 && t <= TOK_MAX && (nu <= 2 || (nu <= 6 && t == 2)); }
+// Instances (gemv_tok_ok states the same): Q4_0 / Q8_0 (NU blocks of 32 per lane) T = 2-4 tokens for rows of at
+// most 4096 columns (NU <= 2) and T = 2 up to 12288 (NU <= 6), with SwiGLU pairs; Q5_K / Q6_K (NU units of 64 per
+// lane) T = 1-4 up to 4096 columns and T = 1-2 up to 12288, without pairs.
+template <int TYPE>
+constexpr bool tok_instance(int nu, int t) {
+    if constexpr (TYPE == T_Q5_K || TYPE == T_Q6_K) return t >= 1 && t <= TOK_MAX && (nu == 1 || (nu <= 3 && t <= 2));
+    return t >= 2 && t <= TOK_MAX && (nu <= 2 || (nu <= 6 && t == 2));
+}
 
 template <int TYPE, int NU, int T>
 hipError_t launch_tok_nu_t(const TokArgs & a, hipStream_t st) {
-    if constexpr (tok_instance(NU, T)) {
-        return a.m[0].epi == EPI_SWIGLU ? launch_tok_typed<TYPE, NU, true, T>(a, st)
-                                        : launch_tok_typed<TYPE, NU, false, T>(a, st);
+    constexpr bool KQ = TYPE == T_Q5_K || TYPE == T_Q6_K;
+    if constexpr (tok_instance<TYPE>(NU, T)) {
+        if (a.m[0].epi != EPI_SWIGLU) return launch_tok_typed<TYPE, NU, false, T>(a, st);
+        if constexpr (!KQ) return launch_tok_typed<TYPE, NU, true, T>(a, st);
     }
     return hipErrorInvalidValue;
 }
@@ -271,6 +322,7 @@ hipError_t launch_tok_nu_t(const TokArgs & a, hipStream_t st) {
 template <int TYPE, int NU>
 hipError_t launch_tok_nu(const TokArgs & a, hipStream_t st) {
     switch (a.n_tok) {
+    case 1: return launch_tok_nu_t<TYPE, NU, 1>(a, st);
     case 2: return launch_tok_nu_t<TYPE, NU, 2>(a, st);
     case 3: return launch_tok_nu_t<TYPE, NU, 3>(a, st);
     case 4: return launch_tok_nu_t<TYPE, NU, 4>(a, st);
@@ -280,7 +332,8 @@ hipError_t launch_tok_nu(const TokArgs & a, hipStream_t st) {
 
 template <int TYPE>
 hipError_t launch_tok_type(const TokArgs & a, hipStream_t st) {
-    switch ((a.cols / 32 + 63) / 64) {
+    constexpr bool KQ = TYPE == T_Q5_K || TYPE == T_Q6_K;
+    switch ((a.cols / (KQ ? 64 : 32) + 63) / 64) {
     case 1: return launch_tok_nu<TYPE, 1>(a, st);
     case 2: return launch_tok_nu<TYPE, 2>(a, st);
     case 3: return launch_tok_nu<TYPE, 3>(a, st);

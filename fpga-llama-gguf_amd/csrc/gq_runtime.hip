@@ -853,10 +853,13 @@ struct Compiler {
         const uint32_t * k = cmds + size_t(i) * GEMVQ_CMD_WORDS, * k2 = k + GEMVQ_CMD_WORDS;
         const int t = int(k[1] & 0xffu), rows = int(k[2]);
         const uint32_t flags = k[1] & ~0xffu, cols = k[3], ntok = k2[0], xs = k2[1], ys = k2[2], nflags = k2[7];
-        if (t != T_Q4_0 && t != T_Q4_1 && t != T_Q8_0) return reject(i, "GEMM format (Q4_0, Q4_1 or Q8_0)");
+        const bool kq = t == T_Q5_K || t == T_Q6_K;  // no MFMA form: launches of up to 4 tokens of the small-token GEMV
+        if (t != T_Q4_0 && t != T_Q4_1 && t != T_Q8_0 && !kq) return reject(i, "GEMM format (Q4_0, Q4_1, Q8_0, Q5_K or Q6_K)");
         if (rows <= 0 || cols == 0 || cols % 512 || cols > GEMVQ_MAX_COLS) return reject(i, "GEMM shape (cols a multiple of 512)");
         if (flags & ~(GEMVQ_GEMV_SWIGLU | GEMVQ_GEMV_ADD | GEMVQ_GEMV_SILU) || __builtin_popcount(flags) > 1)
             return reject(i, "GEMM flags");
+        if (kq && ((flags & GEMVQ_GEMV_SWIGLU) || !gemv_tok_ok(t, int(cols), 1, false)))
+            return reject(i, "GEMM on K-quant weights: no SwiGLU pair, at most 12288 columns");
         if (ntok < 1 || ntok > GEMVQ_GEMM_MAX_TOK) return reject(i, "GEMM token count");
         if (xs % 16 || xs < cols || ys % 16 || ys < uint32_t(rows)) return reject(i, "GEMM strides");
         const uint64_t woff = uint64_t(k[4]) | (uint64_t(k[5]) << 32);
@@ -904,35 +907,41 @@ struct Compiler {
         }
         const uint32_t x_len = xs * (ntok - 1) + cols;
         const uint32_t y_off = uint32_t(g.y - c->act), y_len = uint32_t(g.y_stride) * (ntok - 1) + uint32_t(rows);
-        // 2-4 tokens: the small-token GEMV, which quantizes the rows in every workgroup's prologue, so no output may
-        // fall on the rows or the norm weight (other workgroups may still be reading them)
-        if (gemv_tok_ok(t, int(cols), int(ntok), g.epi == EPI_SWIGLU) && !(y_off < k[6] + x_len && k[6] < y_off + y_len) &&
-            !(normw && y_off < k2[5] + cols && k2[5] < y_off + y_len)) {
-            TokArgs ta{};
-            ta.x = A(k[6]);
-            ta.norm_w = normw ? A(k2[5]) : nullptr;
-            ta.eps = bits_f(k2[6]);
-            ta.norm = norm ? 1 : 0;
-            ta.norm_l2 = (nflags & GEMVQ_NORM_L2) ? 1 : 0;
-            ta.cols = int(cols);
-            ta.n_tok = int(ntok);
-            ta.x_stride = int(xs);
-            ta.n_members = 1;
-            ta.wbound[0] = g.wbound[0];
-            TokMember & m = ta.m[0];
-            m.w = g.w;
-            m.w2 = g.w2;
-            m.y = g.y;
-            m.res = g.res;
-            m.rows = rows;
-            m.y_stride = g.y_stride;
-            m.res_stride = g.res_stride;
-            m.epi = g.epi;
-            if (!merge_tok(ta, t, k[6], x_len, int(i), int(used))) {
-                out.push_back(LTok{ta, t, k[6], x_len});
-                spans.push_back({int(i), int(used)});
+        // 2-4 tokens (K-quants: any count, in launches of up to 4): the small-token GEMV, which quantizes the rows in
+        // every workgroup's prologue, so no output may fall on the rows or the norm weight (other workgroups may still
+        // be reading them)
+        const bool over = (y_off < k[6] + x_len && k[6] < y_off + y_len) || (normw && y_off < k2[5] + cols && k2[5] < y_off + y_len);
+        if (kq && over) return reject(i, "GEMM on K-quant weights: the output falls on the input rows or the norm weight");
+        if (kq || (!over && gemv_tok_ok(t, int(cols), int(ntok), g.epi == EPI_SWIGLU))) {
+            const uint32_t cs = kq ? (gemv_tok_ok(t, int(cols), TOK_MAX, false) ? TOK_MAX : 2) : ntok;  // tokens a launch
+            for (uint32_t c0 = 0; c0 < ntok; c0 += cs) {
+                const uint32_t nt = std::min(cs, ntok - c0);
+                TokArgs ta{};
+                ta.x = A(k[6]) + size_t(c0) * xs;
+                ta.norm_w = normw ? A(k2[5]) : nullptr;
+                ta.eps = bits_f(k2[6]);
+                ta.norm = norm ? 1 : 0;
+                ta.norm_l2 = (nflags & GEMVQ_NORM_L2) ? 1 : 0;
+                ta.cols = int(cols);
+                ta.n_tok = int(nt);
+                ta.x_stride = int(xs);
+                ta.n_members = 1;
+                ta.wbound[0] = g.wbound[0];
+                TokMember & m = ta.m[0];
+                m.w = g.w;
+                m.w2 = g.w2;
+                m.y = g.y + size_t(c0) * g.y_stride;
+                m.res = g.res ? g.res + size_t(c0) * g.res_stride : nullptr;
+                m.rows = rows;
+                m.y_stride = g.y_stride;
+                m.res_stride = g.res_stride;
+                m.epi = g.epi;
+                if (!(nt == ntok && merge_tok(ta, t, k[6], x_len, int(i), int(used)))) {
+                    out.push_back(LTok{ta, t, uint32_t(k[6] + c0 * xs), xs * (nt - 1) + cols});
+                    spans.push_back({int(i), int(used)});
+                }
             }
-            tok_open = true;
+            tok_open = cs >= ntok;  // a later GEMM on the same rows may join a launch that holds all of them
             // the outputs end a reuse of the last batched GEMV's quantized rows if they fall on its rows or weight
             const bool hits_x = y_off < lastq.x_off + lastq.x_len && lastq.x_off < y_off + y_len;
             const uint32_t w_off = lastq.q.norm_w ? uint32_t(lastq.q.norm_w - c->act) : 0;

@@ -20,7 +20,7 @@
 
 namespace {
 
-constexpr int F32 = 0, T_Q4_0 = 2, T_Q4_1 = 3, T_Q8_0 = 8;  // ggml type ids
+constexpr int F32 = 0, T_Q4_0 = 2, T_Q4_1 = 3, T_Q8_0 = 8, T_Q5_K = 13, T_Q6_K = 14;  // ggml type ids
 
 uint32_t fb(float f) {
     uint32_t b;
@@ -275,7 +275,8 @@ bool build_batch(gemvq_qwen35 & m, std::string & err) {
     const T & head = m.t.at("output.weight");
     const uint32_t E = uint32_t(c.n_embd), V = uint32_t(c.n_vocab);
     const int ht = head.d->type;
-    if ((ht == T_Q4_0 || ht == T_Q4_1 || ht == T_Q8_0) && head.d->ne0 % 512 == 0) {
+    if ((ht == T_Q4_0 || ht == T_Q4_1 || ht == T_Q8_0 || ((ht == T_Q5_K || ht == T_Q6_K) && head.d->ne0 <= 12288)) &&
+        head.d->ne0 % 512 == 0) {
         e.gemm(head, m.bh, E, m.slogits, V, B, 0, 0, 0, &onorm, c.eps);
     } else {  // no batched form of the head's type: each sequence's row normed and multiplied on its own
         for (uint32_t t = 0; t < B; ++t) {

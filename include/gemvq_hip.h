@@ -90,13 +90,15 @@
  *             kernel): n_tok (1..GEMVQ_GEMM_MAX_TOK) token rows read each weight row once. Token t's input row is at
  *             x_off + t * x_stride and its output row at y_off + t * y_stride; each output row equals, bit for bit,
  *             what a GEMV command on that token row writes. Format 2 Q4_0, 3 Q4_1 or 8 Q8_0, cols a multiple of
- *             512.
+ *             512; or 13 Q5_K or 14 Q6_K with cols a multiple of 512 up to 12288, no SwiGLU pair, and y not over x
+ *             or the norm weight (these run in launches of up to 4 tokens, each reading the weights once).
  *             flags: GEMVQ_GEMV_SWIGLU (the next command is the u GEMM with the same format, rows, cols, x_off,
  *             n_tok, x_stride and norm words and no flags; y = silu(g) * u goes to the u command's y_off /
  *             y_stride), GEMVQ_GEMV_ADD (y = W x + res, token t's residual at res_off + t * res_stride) or
  *             GEMVQ_GEMV_SILU. norm_flags GEMVQ_NORM_DEFER: every token row is RMS-normalized first (weight at
  *             norm_w_off unless GEMVQ_NORM_NO_WEIGHT, GEMVQ_NORM_L2 for the L2 norm, eps), as a deferred RMSNORM
- *             before a GEMV. The rows are read before any output is written, so y may overlap x.
+ *             before a GEMV. The rows are read before any output is written, so y may overlap x (K-quant
+ *             formats excepted).
  *             Consecutive GEMMs of one format on the same rows and norm words quantize the rows once and run as one
  *             launch of up to four members, unless one is a SwiGLU pair or a member's output overlaps an earlier
  *             member's output or residual; the results are those of the commands one by one.

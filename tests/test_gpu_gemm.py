@@ -214,7 +214,8 @@ def test_gemm_invalid_commands_rejected(gq, ctx):
     good = gq.gemm(2, 64, 1024, off, 0, 65536, 4, 1024, 64)
     assert ctx.run(good) == 0, ctx.error()
     bad = [
-        gq.gemm(14, 64, 1024, ok, 0, 65536, 4, 1024, 64),                         # K-quant weights
+        gq.gemm(14, 64, 1024, ok, 0, 65536, 4, 1024, 64, gq.GEMV_SWIGLU),         # K-quant SwiGLU pair
+        gq.gemm(14, 64, 1024, ok, 0, 0, 4, 1024, 64),                             # K-quant output over its rows
         gq.gemm(2, 64, 1024, off, 0, 65536, 0, 1024, 64),                         # no tokens
         gq.gemm(2, 64, 1024, off, 0, 65536, gq.GEMM_MAX_TOK + 1, 1024, 64),       # too many tokens
         gq.gemm(2, 64, 1024, off, 0, 65536, 4, 1000, 64),                         # stride below cols

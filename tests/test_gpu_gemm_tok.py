@@ -5,7 +5,8 @@ that row and the GPU's own GEMV command on it. Covered: Q4_0 and Q8_0; 2, 3 and 
 (fewer blocks than lanes, one to six blocks per lane); row counts that are not a multiple of the 8 slices; strided
 rows; the SwiGLU pair, residual ADD and SiLU epilogs; the folded per-token norm (with weight, L2 without); block
 terms past 2^53 LSB; the routing (one launch here, the quantization and MFMA launches for Q4_1, for 3 tokens of 12288
-columns and for an output over the input rows)."""
+columns and for an output over the input rows). Q5_K and Q6_K (no MFMA form) run any token count in launches of up
+to 4 tokens (2 above 4096 columns), each reading the weights once."""
 import numpy as np
 import pytest
 
@@ -131,3 +132,62 @@ def test_tok_routing(gq, orc, ctx):
         y = ctx.read(Y, ntok * rows).reshape(ntok, rows)
         for t in range(ntok):
             assert_bits(y[t], orc.fx_gemv(fmt, w, x[t * cols:(t + 1) * cols], rows, cols), f"fmt {fmt} token {t}")
+
+
+@pytest.mark.parametrize("fmt", [13, 14])
+@pytest.mark.parametrize("rows,cols,ntok", [(1000, 4096, 1), (333, 4096, 4), (1000, 4096, 9), (700, 12288, 3),
+                                            (256, 2048, 6)])
+def test_tok_k_quant_rows(gq, orc, ctx, fmt, rows, cols, ntok):
+    xs, ys = cols + 16, up16(rows) + 16
+    w = gq.matrix(fmt, rows, cols, 5, 30 + fmt, std=0.02)
+    off = ctx.upload(fmt, rows, cols, w)
+    x = gq.normal(5, 31, ntok * xs) * 2.0
+    X, Y, Y1 = 0, up16(ntok * xs), up16(ntok * xs) + up16(ntok * ys)
+    ctx.write(X, x)
+    print(f"[gemm tok] k-quant fmt {fmt} rows {rows} cols {cols} tokens {ntok}", flush=True)
+    assert ctx.run(gq.gemm(fmt, rows, cols, off, X, Y, ntok, xs, ys)) == 0, ctx.error()
+    per = 4 if cols <= 4096 else 2
+    assert ctx.launch_count() == (ntok + per - 1) // per
+    y = ctx.read(Y, ntok * ys).reshape(ntok, ys)[:, :rows]
+    for t in range(ntok):
+        want = orc.fx_gemv(fmt, w, x[t * xs:t * xs + cols], rows, cols)
+        assert_bits(y[t], want, f"token {t}")
+        if t in (0, ntok - 1):
+            assert ctx.run(gq.gemv(fmt, rows, cols, off, X + t * xs, Y1)) == 0, ctx.error()
+            assert_bits(ctx.read(Y1, rows), y[t], f"GEMV command, token {t}")
+
+
+@pytest.mark.parametrize("ntok", [3, 6])
+def test_tok_k_quant_norm_and_epilogs(gq, orc, ctx, ntok):
+    fmt, rows, cols, eps = 14, 1504, 4096, 1e-6
+    w = gq.matrix(fmt, rows, cols, 6, 50, std=0.02)
+    off = ctx.upload(fmt, rows, cols, w)
+    x = gq.normal(6, 51, ntok * cols) * 3.0
+    nw = gq.uniform(6, 52, cols, 0.5, 1.5)
+    res = gq.normal(6, 53, ntok * rows)
+    X, NW, RES, Y = 0, 1 << 16, 1 << 17, 1 << 18
+    ctx.write(X, x)
+    ctx.write(NW, nw)
+    ctx.write(RES, res)
+    xn = [orc.rownorm(x[t * cols:(t + 1) * cols], nw, cols, 1, eps) for t in range(ntok)]
+    v = [orc.fx_gemv(fmt, w, r, rows, cols) for r in xn]
+    norm = dict(norm_w=NW, eps=eps, norm_flags=gq.NORM_DEFER)
+    print(f"[gemm tok] k-quant norm and epilogs, tokens {ntok}", flush=True)
+    assert ctx.run(gq.gemm(fmt, rows, cols, off, X, Y, ntok, cols, rows, **norm)) == 0, ctx.error()
+    y = ctx.read(Y, ntok * rows).reshape(ntok, rows)
+    for t in range(ntok):
+        assert_bits(y[t], v[t], f"norm token {t}")
+    assert ctx.run(gq.gemm(fmt, rows, cols, off, X, Y, ntok, cols, rows, gq.GEMV_ADD, RES, rows, **norm)) == 0, ctx.error()
+    y = ctx.read(Y, ntok * rows).reshape(ntok, rows)
+    for t in range(ntok):
+        assert_bits(y[t], v[t] + res[t * rows:(t + 1) * rows], f"add token {t}")
+    assert ctx.run(gq.gemm(fmt, rows, cols, off, X, Y, ntok, cols, rows, gq.GEMV_SILU, **norm)) == 0, ctx.error()
+    y = ctx.read(Y, ntok * rows).reshape(ntok, rows)
+    for t in range(ntok):
+        assert_bits(y[t], orc.unary(v[t], 1), f"silu token {t}")
+    assert ctx.run(gq.gemm(fmt, rows, cols, off, X, Y, ntok, cols, rows, eps=eps,
+                           norm_flags=gq.NORM_DEFER | gq.NORM_L2 | gq.NORM_NO_WEIGHT)) == 0, ctx.error()
+    y = ctx.read(Y, ntok * rows).reshape(ntok, rows)
+    for t in range(ntok):
+        xl2 = orc.rownorm(x[t * cols:(t + 1) * cols], None, cols, 1, eps, gq.NORM_L2 | gq.NORM_NO_WEIGHT)
+        assert_bits(y[t], orc.fx_gemv(fmt, w, xl2, rows, cols), f"l2 token {t}")
