@@ -28,7 +28,11 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # packed FP32 instructions are disabled (they are avoided on this hardware).
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fno-fast-math",
              "-Wno-unused-value", "-Wno-unused-result",
-             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I" + INCLUDE, "-I" + CSRC]
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             # leading scalar kernel arguments arrive in SGPRs (kernel argument preloading, gfx940 and later; the
+             # code object keeps a prologue that loads them where the firmware does not)
+             "-mllvm", "-amdgpu-kernarg-preload-count=16",
+             "-I" + INCLUDE, "-I" + CSRC]
 
 
 def _run(cmd: list[str]) -> None:

@@ -28,6 +28,17 @@ struct Lds {
     unsigned long long key[NWAVES];
 };
 
+// The fields the prologue's first loads need, passed as leading scalar kernel arguments (ahead of GemvArgs, which
+// is read through the kernel argument segment) so that they can arrive in SGPRs with the wave instead of through a
+// dependent scalar load before the activation can be requested.
+struct GemvHot {
+    const float * x;
+    const float * norm_w;
+    const float * gate_z;
+    int cols;
+    int xsrc;
+};
+
 // Pairwise tree over the workgroup's per-wave values (NWAVES, a power of two, consecutive).
 __device__ __forceinline__ float wave_tree(const float * r) {
     float t[NWAVES];
@@ -108,13 +119,13 @@ __device__ __forceinline__ int item_of(int g, int n16) {
 // Every load is unconditional (an operand a source does not use is read from the activation itself), so the loads
 // cannot be moved into the branches that use them, behind the weight loads.
 template <int R, int XS>
-__device__ __forceinline__ void prologue_fetch(const GemvArgs & a, XF<R, XS> & f) {
-    const int n16 = a.cols / 16;
-    const bool normw = (XS == XS_ACC || a.xsrc == XSRC_NORM) && a.norm_w != nullptr;  // ACC instances: always a norm
+__device__ __forceinline__ void prologue_fetch(const GemvHot & h, const GemvArgs & a, XF<R, XS> & f) {
+    const int n16 = h.cols / 16;
+    const bool normw = (XS == XS_ACC || h.xsrc == XSRC_NORM) && h.norm_w != nullptr;  // ACC instances: always a norm
 #pragma unroll
     for (int g = 0; g < R; ++g) {
         const int i = item_of(g, n16);
-        const float * xi = a.x + size_t(i) * 16;
+        const float * xi = h.x + size_t(i) * 16;
         load16(xi, f.v[g]);
         if constexpr (XS == XS_ACC) {
             const u64x2 * ap = reinterpret_cast<const u64x2 *>(a.acc + size_t(i) * 16);
@@ -126,10 +137,10 @@ __device__ __forceinline__ void prologue_fetch(const GemvArgs & a, XF<R, XS> & f
             }
         }
         if constexpr (XS == XS_GATED) {
-            load16(a.gate_z + size_t(i) * 16, f.z[g]);
-            load16(a.norm_w + size_t(i & 7) * 16, f.w[g]);
+            load16(h.gate_z + size_t(i) * 16, f.z[g]);
+            load16(h.norm_w + size_t(i & 7) * 16, f.w[g]);
         } else if constexpr (R <= 2) {
-            load16(normw ? a.norm_w + size_t(i) * 16 : xi, f.w[g]);
+            load16(normw ? h.norm_w + size_t(i) * 16 : xi, f.w[g]);
         }
     }
 }
@@ -345,9 +356,6 @@ __device__ void quantize_q8_K(const float * x, int cols, bool norm, const float 
         if ((lane & 3) == 0) bs[sb * 16 + (lane >> 2)] = int16_t(part);
         if (lane == 0) info[sb] = __float_as_uint(d);
     }
-}
-__device__ void quantize_q8_K(const GemvArgs & a, float scale, Lds & s) {
-    quantize_q8_K(a.x, a.cols, a.xsrc == XSRC_NORM, a.norm_w, scale, s.xq, s.bs, s.info);
 }
 
 // ---- per-lane activation slices ----
@@ -869,31 +877,37 @@ __device__ __forceinline__ void exact_rows(const GemvArgs & a, const GemvMember 
 // Waves are assigned to members in order: member i owns the global waves wave_begin .. wave_begin + waves - 1;
 // waves past the last member only take part in the prologue.
 template <int TYPE, int NU, bool PAIR, int XS, int DS>
-__global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(NT) void gemv_kernel(const float * x, const float * norm_w, const float * gate_z, int cols,
+                                                  int xsrc, int n_members, int wb1, int wb2, int wb3, GemvArgs a) {
     __shared__ Lds s;
     constexpr bool KQ = TYPE == T_Q5_K || TYPE == T_Q6_K;
-
+    // Leading scalar arguments: preloaded into SGPRs where the firmware supports it, so the activation loads and the
+    // member choice wait for no load of the kernel argument segment.
+    const GemvHot h{x, norm_w, gate_z, cols, xsrc};
     constexpr int RX = KQ ? 1 : (128 * NU + NT - 1) / NT;  // rounds of 16 NT activation floats (cols <= 2048 NU)
+    XF<RX, XS> xf;
+    if constexpr (!KQ) prologue_fetch<RX, XS>(h, a, xf);  // the activation is requested first
+    __builtin_amdgcn_sched_barrier(0);                    // and stays ahead of the member lookup and weight loads
     Ctx c;
     c.lane = threadIdx.x & 63;
-    c.nb = a.cols / 32;
-    c.nu = a.cols / 64;
+    c.nb = h.cols / 32;
+    c.nu = h.cols / 64;
     c.best = 0;
     c.exact = false;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: member fields load as scalars
     // Workgroup b serves slice b % 8 of every member's rows (workgroups are dealt to the XCDs in turn, so a slice's
     // rows stream through one XCD's L2; placement only affects speed, never which rows run).
     const int xs = blockIdx.x & 7, lw = (blockIdx.x >> 3) * NWAVES + wave;  // slice, wave index within it
-    int mi = 0;
-#pragma unroll
-    for (int i = 1; i < 4; ++i)
-        if (i < a.n_members && lw >= a.m[i].wave_begin) mi = i;
+    // member i owns the waves from its wave_begin (wb1..wb3 = a.m[1..3].wave_begin)
+    const int mi = n_members > 3 && lw >= wb3 ? 3 : n_members > 2 && lw >= wb2 ? 2 : n_members > 1 && lw >= wb1 ? 1 : 0;
     const GemvMember & m = a.m[mi];
     const int s_lo = int((long long)xs * m.rows / 8), len = int((long long)(xs + 1) * m.rows / 8) - s_lo;
-    const int wv = lw - m.wave_begin, S = m.waves;                  // rows s_lo + wv, s_lo + wv + S, ... of the slice
-    const int n = wv < S && wv < len ? (len - 1 - wv) / S + 1 : 0;  // waves past the last member have none
+    const int wv = lw - m.wave_begin, S = m.waves;  // rows s_lo + wv, s_lo + wv + S, ... of the slice
+    // waves past the last member have none; computed without a branch, so that the member's remaining fields are
+    // loaded in the same round as these
+    const int q = int(unsigned(max(len - 1 - wv, 0)) / unsigned(max(S, 1)));
+    const int n = wv < S && wv < len ? q + 1 : 0;
     const int w = s_lo + wv;
-    XF<RX, XS> xf;
     // ACC: the fused step's new state rows, copied from the shadow rows into the state (one float4 per thread of
     // the grid in turn); the first is requested with the activation and stored once the prologue is done
     const int cp_i = int(blockIdx.x) * NT + int(threadIdx.x), cp_s = int(gridDim.x) * NT;
@@ -901,15 +915,13 @@ __global__ __launch_bounds__(NT) void gemv_kernel(GemvArgs a) {
     if constexpr (XS == XS_ACC) {
         if (cp_i < a.cp_n) cp_v = a.cp_src[cp_i];
     }
-    if constexpr (!KQ) prologue_fetch<RX, XS>(a, xf);  // the activation is requested first
-    __builtin_amdgcn_sched_barrier(0);                    // and stays ahead of the weight loads
     Slot<TYPE, NU, PAIR> sl[DS];  // the first D rows (a wave without rows reloads the member's last row)
 #pragma unroll
     for (int j = 0; j < DS; ++j)
         load_slot<TYPE, NU, PAIR>(m, n > 0 ? w + min(j, n - 1) * S : m.rows - 1, c.lane, c.nb, c.nu, sl[j]);
     if constexpr (KQ) {
-        const float scale = a.xsrc == XSRC_NORM ? block_norm_scale(a.x, a.cols, a.norm_eps, a.norm_l2, s) : 1.0f;
-        quantize_q8_K(a, scale, s);
+        const float scale = h.xsrc == XSRC_NORM ? block_norm_scale(h.x, h.cols, a.norm_eps, a.norm_l2, s) : 1.0f;
+        quantize_q8_K(h.x, h.cols, h.xsrc == XSRC_NORM, h.norm_w, scale, s.xq, s.bs, s.info);
     } else {
         prologue_finish<RX, XS>(a, xf, s);
     }
@@ -1047,7 +1059,9 @@ hipError_t launch_typed(const GemvArgs & a0, hipStream_t st) {
     GemvArgs a = a0;
     for (int i = 0; i < a.n_members; ++i) epilog_operands(a.m[i]);
     const int grid = plan_waves(a, cap, DS);
-    GQ_LAUNCH((gemv_kernel<TYPE, NU, PAIR, XS, DS>), dim3(grid), dim3(NT), 0, st, a);
+    GQ_LAUNCH((gemv_kernel<TYPE, NU, PAIR, XS, DS>), dim3(grid), dim3(NT), 0, st, a.x, a.norm_w, a.gate_z, a.cols,
+              a.xsrc, a.n_members, a.n_members > 1 ? a.m[1].wave_begin : 0, a.n_members > 2 ? a.m[2].wave_begin : 0,
+              a.n_members > 3 ? a.m[3].wave_begin : 0, a);
     return hipGetLastError();
 }
 
