@@ -901,6 +901,12 @@ __global__ __launch_bounds__(NT) void gemv_kernel(const float * x, const float *
     // member i owns the waves from its wave_begin (wb1..wb3 = a.m[1..3].wave_begin)
     const int mi = n_members > 3 && lw >= wb3 ? 3 : n_members > 2 && lw >= wb2 ? 2 : n_members > 1 && lw >= wb1 ? 1 : 0;
     const GemvMember & m = a.m[mi];
+    // The member fields that the first weight and epilog operand loads need, requested in one round of scalar loads
+    // (left to itself the compiler waits for the row count before it requests the rest); later reads of the same
+    // fields reuse these registers.
+    asm volatile("" ::"s"(m.rows), "s"(m.wave_begin), "s"(m.waves), "s"(m.w.a), "s"(m.w.b), "s"(m.w.c), "s"(m.w2.a),
+                 "s"(m.w2.b), "s"(m.w2.c), "s"(m.ea), "s"(m.eb), "s"(m.e_sa), "s"(m.e_sb), "s"(m.e_split),
+                 "s"(m.e_lane));
     const int s_lo = int((long long)xs * m.rows / 8), len = int((long long)(xs + 1) * m.rows / 8) - s_lo;
     const int wv = lw - m.wave_begin, S = m.waves;  // rows s_lo + wv, s_lo + wv + S, ... of the slice
     // waves past the last member have none; computed without a branch, so that the member's remaining fields are
