@@ -173,10 +173,23 @@ __device__ __forceinline__ void gdn_token(const GdnArgs & a, const GdnIn & in, i
     }
 }
 
-// With seqs, grid y is the token: token t is the one token of sequence t on its own state rows.
-__global__ __launch_bounds__(128) void gdn_kernel(GdnArgs a) {
+// With SEQS (args.seqs), grid y is the token: token t is the one token of sequence t on its own state rows.
+// The state rows, the first token's inputs and the key head count are leading scalar arguments (preloaded into SGPRs
+// where the firmware supports it), so without SEQS the state and input loads wait for no load of the argument
+// segment.
+template <bool SEQS>
+__global__ __launch_bounds__(128) void gdn_kernel(const float * src, const float * q, const float * k, const float * v,
+                                                  const float * g, const float * beta, int hk, GdnArgs args) {
     constexpr int IT = GDN_IT;
-    if (a.seqs) {
+    GdnArgs a = args;
+    a.src = src;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.g = g;
+    a.beta = beta;
+    a.hk = hk;
+    if constexpr (SEQS) {
         const size_t t = blockIdx.y, so = size_t(a.hv) * 128 * 128 * t;
         a.src += so;
         a.dst += so;
@@ -202,17 +215,17 @@ __global__ __launch_bounds__(128) void gdn_kernel(GdnArgs a) {
         x[it][0] = s0.x; x[it][1] = s0.y; x[it][2] = s0.z; x[it][3] = s0.w;
         x[it][4] = s1.x; x[it][5] = s1.y; x[it][6] = s1.z; x[it][7] = s1.w;
     }
+    // a ring of three token inputs: token tk + 2 is requested before token tk runs (uniform branches: only tokens
+    // that exist are loaded); the first token's are requested before the gate parameters
+    GdnIn r0, r1, r2;
+    gdn_load(a, 0, h, kh, chunk, l16, grp, r0);
+    const int n = a.n_tok;
+    if (n > 1) gdn_load(a, 1, h, kh, chunk, l16, grp, r1);
     float dtv = 0.0f, av = 0.0f;
     if (a.flags & 8) {
         dtv = a.dt[h];
         av = a.a[h];
     }
-    // a ring of three token inputs: token tk + 2 is requested before token tk runs (uniform branches: only tokens
-    // that exist are loaded)
-    const int n = a.n_tok;
-    GdnIn r0, r1, r2;
-    gdn_load(a, 0, h, kh, chunk, l16, grp, r0);
-    if (n > 1) gdn_load(a, 1, h, kh, chunk, l16, grp, r1);
     for (int tk = 0; tk < n; tk += 3) {
         if (tk + 2 < n) gdn_load(a, tk + 2, h, kh, chunk, l16, grp, r2);
         gdn_token(a, r0, tk, h, chunk, l16, grp, dtv, av, x);
@@ -445,8 +458,20 @@ __device__ __forceinline__ void attn_token(const AttnArgs & a, const uint4 (&kr)
     if (tid == 0) a.counter[th] = 0u;
 }
 
+// The position, the q rows, the cache and the head counts are leading scalar arguments (preloaded into SGPRs where
+// the firmware supports it): the position and q loads wait for no load of the argument segment.
 template <int HD>
-__global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(ATT_T) void attn_kernel(const int32_t * pos_p, const float * q, uint16_t * kc, uint16_t * vc,
+                                                     int n_head, int n_head_kv, int q_stride, int n_ctx, AttnArgs args) {
+    AttnArgs a = args;
+    a.pos = pos_p;
+    a.q = q;
+    a.kc = kc;
+    a.vc = vc;
+    a.n_head = n_head;
+    a.n_head_kv = n_head_kv;
+    a.q_stride = q_stride;
+    a.n_ctx = n_ctx;
     constexpr int PER = HD / 8;                    // 16-byte pieces per row
     constexpr int RPP = ATT_T / PER;               // rows per pass
     constexpr int NP = (ATTN_CHUNK + RPP - 1) / RPP;  // passes
@@ -536,8 +561,10 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(AttnArgs a) {
 }
 
 // ---- embedding rows (ggml dequantize_row_*) ----
-__global__ void get_rows_kernel(GetRowsArgs a) {
-    const int id = a.id[16 * blockIdx.y];
+// The ids are a leading scalar argument (preloaded into SGPRs where the firmware supports it): the id load waits for
+// no load of the argument segment.
+__global__ void get_rows_kernel(const int32_t * ids, GetRowsArgs a) {
+    const int id = ids[16 * blockIdx.y];
     if (id < 0 || id >= a.rows) return;
     float * const yt = a.y + size_t(blockIdx.y) * a.cols;  // this token's row
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < a.cols; i += gridDim.x * blockDim.x) {
@@ -645,7 +672,12 @@ hipError_t launch_rope(const RopeArgs & a, hipStream_t s) {
 }
 
 hipError_t launch_gdn(const GdnArgs & a, hipStream_t s) {
-    GQ_LAUNCH(gdn_kernel, dim3(a.hv * (128 / GDN_ROWS), a.seqs ? a.n_tok : 1), dim3(128), 0, s, a);
+    if (a.seqs)
+        GQ_LAUNCH(gdn_kernel<true>, dim3(a.hv * (128 / GDN_ROWS), a.n_tok), dim3(128), 0, s, a.src, a.q, a.k, a.v, a.g,
+                  a.beta, a.hk, a);
+    else
+        GQ_LAUNCH(gdn_kernel<false>, dim3(a.hv * (128 / GDN_ROWS), 1), dim3(128), 0, s, a.src, a.q, a.k, a.v, a.g,
+                  a.beta, a.hk, a);
     return hipGetLastError();
 }
 
@@ -716,7 +748,8 @@ __global__ __launch_bounds__(ATT_T) void attn_group_kernel(AttnArgs a) {
 template <int HD>
 hipError_t launch_attn_hd(const AttnArgs & a, dim3 grid, hipStream_t s) {
     if (grid.y == 1) {
-        GQ_LAUNCH(attn_kernel<HD>, grid, dim3(ATT_T), 0, s, a);
+        GQ_LAUNCH(attn_kernel<HD>, grid, dim3(ATT_T), 0, s, a.pos, a.q, a.kc, a.vc, a.n_head, a.n_head_kv, a.q_stride,
+                  a.n_ctx, a);
         return hipGetLastError();
     }
     GQ_LAUNCH(attn_append_kernel<HD>, dim3(a.n_head + a.n_head_kv, grid.y), dim3(ATT_T), 0, s, a);
@@ -745,7 +778,7 @@ hipError_t launch_attn(const AttnArgs & a, hipStream_t s) {
 }
 
 hipError_t launch_get_rows(const GetRowsArgs & a, hipStream_t s) {
-    GQ_LAUNCH(get_rows_kernel, dim3((a.cols + 255) / 256, a.n_tok > 1 ? a.n_tok : 1), dim3(256), 0, s, a);
+    GQ_LAUNCH(get_rows_kernel, dim3((a.cols + 255) / 256, a.n_tok > 1 ? a.n_tok : 1), dim3(256), 0, s, a.id, a);
     return hipGetLastError();
 }
 
