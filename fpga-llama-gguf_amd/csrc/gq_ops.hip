@@ -325,6 +325,14 @@ __global__ __launch_bounds__(ATT_T) void attn_append_kernel(AttnArgs a) {
     }
 }
 
+// Chunk partials: agent-scope atomic accesses (coherent across the XCDs' L2 caches).
+__device__ __forceinline__ void part_store(float * p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float part_load(const float * p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Steps 3-5 of one token on a loaded chunk (rows t0 .. t0 + nt - 1): kr holds the chunk's key pieces, vs its values,
 // qs[0] the rounded q and, with NEW, qs[1] the new key of row pos; the partials go to set th, and the workgroup that
 // completes the set's nc chunks combines them into the output row (and clears the set's counter).
@@ -380,18 +388,21 @@ __device__ __forceinline__ void attn_token(const AttnArgs & a, const uint4 (&kr)
             o += p * h2f(vs[i * HD + e]);
         }
         float * pp = a.part + (size_t(th) * nchmax + chunk) * pstride;
-        pp[2 + e] = o;
+        part_store(pp + 2 + e, o);
         if (e == 0) {
-            pp[0] = mx;
-            pp[1] = l;
+            part_store(pp, mx);
+            part_store(pp + 1, l);
         }
     }
+    // The partials are agent-scope atomic stores, coherent across the XCDs without an L2 writeback; every thread
+    // waits until its stores have completed before the barrier, so the counter update that follows it is ordered
+    // after all of them (a release without the writeback of the whole L2 that a release fence performs). The last
+    // workgroup's partial loads are agent-scope atomic loads issued after its counter update returned, so they need
+    // no acquire fence (no L2 invalidation) either.
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (tid == 0) {  // the partials are released (agent scope) by the counter update; the last workgroup acquires
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        last = atomicAdd(a.counter + th, 1u) == unsigned(nc - 1);
-        if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    }
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(a.counter + th, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == unsigned(nc - 1);
     __syncthreads();
     if (!last) return;
     // ---- 5. combine (last workgroup of the q head): M over every chunk, then L and O in chunk order, MAXCH
@@ -401,15 +412,15 @@ __device__ __forceinline__ void attn_token(const AttnArgs & a, const uint4 (&kr)
     float ov[CMB];
     float mc = -__builtin_inff(), lc = 0.0f;
     if (wave == 0 && lane < nr0) {
-        mc = __builtin_nontemporal_load(pk + size_t(lane) * pstride);
-        lc = __builtin_nontemporal_load(pk + size_t(lane) * pstride + 1);
+        mc = part_load(pk + size_t(lane) * pstride);
+        lc = part_load(pk + size_t(lane) * pstride + 1);
     }
 #pragma unroll
-    for (int c = 0; c < CMB; ++c) ov[c] = c < nc ? __builtin_nontemporal_load(pk + size_t(c) * pstride + 2 + e) : 0.0f;
+    for (int c = 0; c < CMB; ++c) ov[c] = c < nc ? part_load(pk + size_t(c) * pstride + 2 + e) : 0.0f;
     if (wave == 0) {
         float M = mc;
         for (int r0 = MAXCH; r0 < nc; r0 += MAXCH)  // contexts past MAXCH chunks: the later rounds' maxima
-            M = fmaxf(M, r0 + lane < nc ? __builtin_nontemporal_load(pk + size_t(r0 + lane) * pstride) : -__builtin_inff());
+            M = fmaxf(M, r0 + lane < nc ? part_load(pk + size_t(r0 + lane) * pstride) : -__builtin_inff());
 #pragma unroll
         for (int st = 32; st >= 1; st >>= 1) M = fmaxf(M, __shfl_xor(M, st, WAVE));
         if (lane < nr0) {
@@ -434,20 +445,20 @@ __device__ __forceinline__ void attn_token(const AttnArgs & a, const uint4 (&kr)
             if (c0 >= rn) break;
 #pragma unroll
             for (int c = 0; c < CMB; ++c)
-                ov[c] = c0 + c < rn ? __builtin_nontemporal_load(pk + size_t(r0 + c0 + c) * pstride + 2 + e) : 0.0f;
+                ov[c] = c0 + c < rn ? part_load(pk + size_t(r0 + c0 + c) * pstride + 2 + e) : 0.0f;
         }
         r0 += MAXCH;
         if (r0 >= nc) break;
         const int rn2 = min(MAXCH, nc - r0);
         __syncthreads();  // every thread has read this round's f_c and l_c
         if (wave == 0 && lane < rn2) {
-            const float m2 = __builtin_nontemporal_load(pk + size_t(r0 + lane) * pstride);
+            const float m2 = part_load(pk + size_t(r0 + lane) * pstride);
             fcs[lane] = expf_(m2 - mx);
-            lcs[lane] = __builtin_nontemporal_load(pk + size_t(r0 + lane) * pstride + 1);
+            lcs[lane] = part_load(pk + size_t(r0 + lane) * pstride + 1);
         }
 #pragma unroll
         for (int c = 0; c < CMB; ++c)
-            ov[c] = c < rn2 ? __builtin_nontemporal_load(pk + size_t(r0 + c) * pstride + 2 + e) : 0.0f;
+            ov[c] = c < rn2 ? part_load(pk + size_t(r0 + c) * pstride + 2 + e) : 0.0f;
         __syncthreads();
     }
     if (el) {
