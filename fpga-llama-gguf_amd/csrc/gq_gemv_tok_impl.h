@@ -25,6 +25,12 @@ struct LdsTok {  // T quantized activations: Q8_0 (d | sum words, Q8_1 s) or Q8_
     float red[T * R * NWAVES];
 };
 
+struct TokHot {
+    const float * x;
+    const float * norm_w;
+    int cols, x_stride, norm;
+};
+
 template <int T, int R>  // R rounds of NT 16-float items per token
 struct XT {
     float v[T][R][16];
@@ -33,16 +39,17 @@ struct XT {
 
 // Token t's items, and the norm weight's (R <= 2; wider rows read it when they use it), all issued together and
 // without branches.
+// h: the preloaded leading kernel arguments (the rows, the norm weight, the columns, the row stride, the norm flag).
 template <int T, int R>
-__device__ __forceinline__ void tok_fetch(const TokArgs & a, XT<T, R> & f) {
-    const int n16 = a.cols / 16;
-    const bool normw = a.norm && a.norm_w != nullptr;
+__device__ __forceinline__ void tok_fetch(const TokHot & h, XT<T, R> & f) {
+    const int n16 = h.cols / 16;
+    const bool normw = h.norm && h.norm_w != nullptr;
 #pragma unroll
     for (int g = 0; g < R; ++g) {
         const int i = item_of(g, n16);
 #pragma unroll
-        for (int t = 0; t < T; ++t) load16(a.x + size_t(t) * a.x_stride + size_t(i) * 16, f.v[t][g]);
-        if constexpr (R <= 2) load16(normw ? a.norm_w + size_t(i) * 16 : a.x + size_t(i) * 16, f.w[g]);
+        for (int t = 0; t < T; ++t) load16(h.x + size_t(t) * h.x_stride + size_t(i) * 16, f.v[t][g]);
+        if constexpr (R <= 2) load16(normw ? h.norm_w + size_t(i) * 16 : h.x + size_t(i) * 16, f.w[g]);
     }
 }
 
@@ -224,28 +231,34 @@ __device__ __forceinline__ void tok_rows(const TokMember & m, int w, int S, int 
 template <int TYPE, int NU, bool PAIR>
 constexpr int tok_slots() { return PAIR || NU > 2 || TYPE == T_Q5_K || TYPE == T_Q6_K ? 1 : 2; }
 
+// The activation rows, norm weight, columns, row stride, norm flag, member count and the members' first waves are
+// leading scalar arguments (preloaded into SGPRs where the firmware supports it), so the activation loads and the
+// member choice wait for no load of the argument segment.
 template <int TYPE, int NU, bool PAIR, int T>
-__global__ __launch_bounds__(NT) void gemv_tok_kernel(TokArgs a) {
+__global__ __launch_bounds__(NT) void gemv_tok_kernel(const float * x, const float * norm_w, int cols, int x_stride,
+                                                      int norm, int n_members, int wb1, int wb2, int wb3, TokArgs a) {
     constexpr bool KQ = TYPE == T_Q5_K || TYPE == T_Q6_K;
     constexpr int DS = tok_slots<TYPE, NU, PAIR>();
     constexpr int R = (tok_cols<KQ, NU>() / 16 + NT - 1) / NT;  // rounds of NT activation items per token
     __shared__ LdsTok<T, NU, R, KQ> s;
-    const int lane = threadIdx.x & 63, nb = a.cols / 32, nu = a.cols / 64;
+    XT<T, R> f;
+    tok_fetch<T, R>(TokHot{x, norm_w, cols, x_stride, norm}, f);  // the activations are requested first
+    __builtin_amdgcn_sched_barrier(0);  // and stay ahead of the member lookup and the weight loads
+    const int lane = threadIdx.x & 63, nb = cols / 32, nu = cols / 64;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // workgroup b serves slice b % 8 of every member's rows (one XCD's L2), as gemv_kernel
     const int xs = blockIdx.x & 7, lw = (blockIdx.x >> 3) * NWAVES + wave;
-    int mi = 0;
-#pragma unroll
-    for (int i = 1; i < 4; ++i)
-        if (i < a.n_members && lw >= a.m[i].wave_begin) mi = i;
+    const int mi = n_members > 3 && lw >= wb3 ? 3 : n_members > 2 && lw >= wb2 ? 2 : n_members > 1 && lw >= wb1 ? 1 : 0;
     const TokMember & m = a.m[mi];
+    // the member fields that the first weight and epilog operand loads need, requested in one round of scalar loads
+    asm volatile("" ::"s"(m.rows), "s"(m.wave_begin), "s"(m.waves), "s"(m.w.a), "s"(m.w.b), "s"(m.w.c), "s"(m.w2.a),
+                 "s"(m.w2.b), "s"(m.w2.c), "s"(m.res), "s"(m.res_stride));
     const int s_lo = int((long long)xs * m.rows / 8), len = int((long long)(xs + 1) * m.rows / 8) - s_lo;
     const int wv = lw - m.wave_begin, S = m.waves;
-    const int n = wv < S && wv < len ? (len - 1 - wv) / S + 1 : 0;  // waves past the last member have none
+    // computed without a branch, so that the member's remaining fields are loaded in the same round as these
+    const int q = int(unsigned(max(len - 1 - wv, 0)) / unsigned(max(S, 1)));
+    const int n = wv < S && wv < len ? q + 1 : 0;  // waves past the last member have none
     const int w = s_lo + wv;
-    XT<T, R> f;
-    tok_fetch<T, R>(a, f);              // the activations are requested first
-    __builtin_amdgcn_sched_barrier(0);  // and stay ahead of the weight loads
     TSlot<TYPE, NU, PAIR> sl[DS];
 #pragma unroll
     for (int j = 0; j < DS; ++j)
@@ -296,7 +309,9 @@ hipError_t launch_tok_typed(const TokArgs & a0, hipStream_t st) {
         if (m.epi != EPI_SWIGLU) m.w2 = m.w;
     }
     const int grid = plan_waves(a, cap, tok_slots<TYPE, NU, PAIR>());
-    GQ_LAUNCH((gemv_tok_kernel<TYPE, NU, PAIR, T>), dim3(grid), dim3(NT), 0, st, a);
+    GQ_LAUNCH((gemv_tok_kernel<TYPE, NU, PAIR, T>), dim3(grid), dim3(NT), 0, st, a.x, a.norm_w, a.cols, a.x_stride,
+              a.norm, a.n_members, a.n_members > 1 ? a.m[1].wave_begin : 0, a.n_members > 2 ? a.m[2].wave_begin : 0,
+              a.n_members > 3 ? a.m[3].wave_begin : 0, a);
     return hipGetLastError();
 }
 
