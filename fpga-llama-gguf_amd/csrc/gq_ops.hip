@@ -277,6 +277,9 @@ __global__ __launch_bounds__(64) void gated_norm_kernel(GatedNormArgs a) {
 //      f_c = e^(m_c - M), L = sum l_c f_c and O = sum o_c f_c in chunk order, and writes O / L times the sigmoid
 //      of the gate.
 constexpr int ATT_T = 256;
+// 16 bytes of keys or values: a native vector, which the compiler keeps in registers (HIP's uint4 struct kept the
+// chunk's arrays out of SROA, in scratch)
+typedef unsigned kv16 __attribute__((ext_vector_type(4)));
 constexpr int MAXCH = 64;  // chunks a combine round handles (wave 0's lanes)
 constexpr int CMB = 32;    // chunks per load round of the combine (each round is a dependent load)
 
@@ -333,13 +336,13 @@ __device__ __forceinline__ float part_load(const float * p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Steps 3-5 of one token on a loaded chunk (rows t0 .. t0 + nt - 1): kr holds the chunk's key pieces, vs its values,
-// qs[0] the rounded q and, with NEW, qs[1] the new key of row pos; the partials go to set th, and the workgroup that
-// completes the set's nc chunks combines them into the output row (and clears the set's counter).
+// Steps 3-4 of one token on a loaded chunk (rows t0 .. t0 + nt - 1): kr holds the chunk's key pieces, vs its values,
+// qs[0] the rounded q and, with NEW, qs[1] the new key of row pos. Leaves the chunk max in mx and gives thread e
+// (< HD) the chunk's sums l and o over its positions in order.
 template <int HD, bool NEW>
-__device__ __forceinline__ void attn_token(const AttnArgs & a, const uint4 (&kr)[(ATTN_CHUNK + ATT_T / (HD / 8) - 1) / (ATT_T / (HD / 8))],
-                                           const uint16_t * vs, const float (*qs)[HD], float * pr, float & mx, float * fcs,
-                                           float * lcs, int & last, int pos, int t0, int chunk, int th, int nt, int nc, float gt) {
+__device__ __forceinline__ void attn_chunk(const AttnArgs & a, const kv16 (&kr)[(ATTN_CHUNK + ATT_T / (HD / 8) - 1) / (ATT_T / (HD / 8))],
+                                           const uint16_t * vs, const float (*qs)[HD], float * pr, float & mx, int pos,
+                                           int t0, int nt, float & o, float & l) {
     constexpr int PER = HD / 8, RPP = ATT_T / PER, NP = (ATTN_CHUNK + RPP - 1) / RPP;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, pc = tid % PER;
     const bool el = tid < HD;
@@ -378,15 +381,31 @@ __device__ __forceinline__ void attn_token(const AttnArgs & a, const uint4 (&kr)
         if (lane == 0) mx = m;
     }
     __syncthreads();
-    const int pstride = 2 + HD, nchmax = (a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
+    o = 0.0f;
+    l = 0.0f;
     if (el) {
-        float o = 0.0f, l = 0.0f;
 #pragma unroll 8
         for (int i = 0; i < nt; ++i) {
             const float p = pr[i];
             l += p;
             o += p * h2f(vs[i * HD + e]);
         }
+    }
+}
+
+// Steps 3-5 of one token on a loaded chunk (as attn_chunk); the partials go to set th, and the workgroup that
+// completes the set's nc chunks combines them into the output row (and clears the set's counter).
+template <int HD, bool NEW>
+__device__ __forceinline__ void attn_token(const AttnArgs & a, const kv16 (&kr)[(ATTN_CHUNK + ATT_T / (HD / 8) - 1) / (ATT_T / (HD / 8))],
+                                           const uint16_t * vs, const float (*qs)[HD], float * pr, float & mx, float * fcs,
+                                           float * lcs, int & last, int pos, int t0, int chunk, int th, int nt, int nc, float gt) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool el = tid < HD;
+    const int e = el ? tid : 0;
+    float o, l;
+    attn_chunk<HD, NEW>(a, kr, vs, qs, pr, mx, pos, t0, nt, o, l);
+    const int pstride = 2 + HD, nchmax = (a.n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
+    if (el) {
         float * pp = a.part + (size_t(th) * nchmax + chunk) * pstride;
         part_store(pp + 2 + e, o);
         if (e == 0) {
@@ -505,13 +524,13 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(const int32_t * pos_p, cons
     const bool has_new = chunk == nc - 1;  // this chunk holds pos
     const float * qrow = a.q + size_t(hq) * a.q_stride;
     // ---- 1. loads ----
-    uint4 kr[NP], vr[NP];  // rows past the chunk re-read its last row (stored memory); they are not used
+    kv16 kr[NP], vr[NP];  // rows past the chunk re-read its last row (stored memory); they are not used
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
         const int ti = min(tid / PER + j * RPP, nt - 1);
         const size_t off = (size_t(t0 + ti) * a.n_head_kv + kvh) * HD + pc * 8;
-        kr[j] = *reinterpret_cast<const uint4 *>(a.kc + off);
-        vr[j] = *reinterpret_cast<const uint4 *>(a.vc + off);
+        kr[j] = *reinterpret_cast<const kv16 *>(a.kc + off);
+        vr[j] = *reinterpret_cast<const kv16 *>(a.vc + off);
     }
     const bool el = tid < HD;
     const int e = el ? tid : 0;  // element of the head this thread holds
@@ -528,7 +547,7 @@ __global__ __launch_bounds__(ATT_T) void attn_kernel(const int32_t * pos_p, cons
 #pragma unroll
     for (int j = 0; j < NP; ++j) {  // values to LDS (the row of pos is overwritten with the new value below)
         const int ti = tid / PER + j * RPP;
-        if (ti < nt) *reinterpret_cast<uint4 *>(vs + ti * HD + pc * 8) = vr[j];
+        if (ti < nt) *reinterpret_cast<kv16 *>(vs + ti * HD + pc * 8) = vr[j];
     }
     // ---- 2. norms (pairwise over head_dim), RoPE, fp16 rounding ----
     {
@@ -727,18 +746,18 @@ __global__ __launch_bounds__(ATT_T) void attn_group_kernel(AttnArgs a) {
     if (first > plast || chunk >= (plast + ATTN_CHUNK) / ATTN_CHUNK) return;
     const int tid = threadIdx.x, pc = tid % PER;
     const int t0 = chunk * ATTN_CHUNK, ntmax = min(ATTN_CHUNK, plast + 1 - t0);
-    uint4 kr[NP], vr[NP];  // rows past ntmax re-read row ntmax - 1; they are not used
+    kv16 kr[NP], vr[NP];  // rows past ntmax re-read row ntmax - 1; they are not used
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
         const int ti = min(tid / PER + j * RPP, ntmax - 1);
         const size_t off = (size_t(t0 + ti) * a.n_head_kv + kvh) * HD + pc * 8;
-        kr[j] = *reinterpret_cast<const uint4 *>(a.kc + off);
-        vr[j] = *reinterpret_cast<const uint4 *>(a.vc + off);
+        kr[j] = *reinterpret_cast<const kv16 *>(a.kc + off);
+        vr[j] = *reinterpret_cast<const kv16 *>(a.vc + off);
     }
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
         const int ti = tid / PER + j * RPP;
-        if (ti < ntmax) *reinterpret_cast<uint4 *>(vs + ti * HD + pc * 8) = vr[j];
+        if (ti < ntmax) *reinterpret_cast<kv16 *>(vs + ti * HD + pc * 8) = vr[j];
     }
     const bool el = tid < HD;
     const int e = el ? tid : 0;
