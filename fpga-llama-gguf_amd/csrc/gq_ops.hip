@@ -328,7 +328,13 @@ __global__ __launch_bounds__(ATT_T) void attn_append_kernel(AttnArgs a) {
     }
 }
 
-// Chunk partials: agent-scope atomic accesses (coherent across the XCDs' L2 caches).
+// Chunk partials: agent-scope atomic accesses (coherent across the XCDs' L2 caches). The combine orders them with a
+// wait for the stores' completion (s_waitcnt 0) before the counter update: on gfx9 vector stores are counted in
+// vmcnt, so that wait covers them. Later architectures count stores separately (vscnt), which s_waitcnt 0 does not
+// wait for, so the code is restricted to the gfx9 CDNA parts it was written for.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__) && !defined(__gfx942__)
+#error "the attention combine relies on gfx9 store counting (vmcnt); build for gfx950 (or gfx942)"
+#endif
 __device__ __forceinline__ void part_store(float * p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -668,7 +674,9 @@ __global__ void next_token_kernel(NextTokenArgs a) {
     const int pos = *a.pos;
     const unsigned long long k = *a.key;
     int tok = int(0xffffffffu - uint32_t(k & 0xffffffffu));
-    if (pos + 1 < a.n_prompt) tok = a.prompt[pos + 1];
+    // a sequence's prompt occupies at most its seq_cap slots, whatever its length word says
+    const int plim = a.n_seq > 1 ? min(a.n_prompt, a.seq_cap) : a.n_prompt;
+    if (pos + 1 < plim) tok = a.prompt[pos + 1];
     if (pos + 1 < a.max_pos) a.out[pos + 1] = tok;
     *a.tok = tok;
     *a.pos = pos + 1;

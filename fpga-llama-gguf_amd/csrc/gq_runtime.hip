@@ -159,6 +159,10 @@ int wait_stream(gemvq_ctx * c, const char * what) {
     }
 }
 
+// Host copies of pageable memory run synchronously behind the work already queued on the stream, outside any
+// bound: every such copy first waits (bounded) for that work, so the copy itself has nothing to wait behind.
+int drain(gemvq_ctx * c, const char * what) { return wait_stream(c, what); }
+
 int einval(gemvq_ctx * c, const std::string & what) {
     if (c) c->err = what;
     return GEMVQ_EINVAL;
@@ -433,6 +437,9 @@ struct Compiler {
         if (g[0] != GEMVQ_OP_GEMV || (g[1] & ~0xffu) != GEMVQ_GEMV_ADD || (t != T_Q4_0 && t != T_Q8_0) || g[6] != gy ||
             g[3] != cols || rows > 4096 || gdn_out_parts(int(rows)) == 0 || !weight(woff, t, int(rows), int(cols)))
             return false;
+        // each fused pair clears the other accumulator's first `rows` entries for the next pair, so every pair of a
+        // list must have the same row count (else a later pair could add onto sums a wider pair left behind)
+        if (accn > 0 && rows != acc_rows) return false;
         if (e[0] != GEMVQ_OP_ADD || e[1] != rows || (e[2] != g[7] && e[3] != g[7])) return false;
         res = e[2] == g[7] ? e[3] : e[2];
         y = e[4];
@@ -497,11 +504,13 @@ struct Compiler {
             const unsigned at = i;
             if (!compile_one(cmds, n, i)) return false;
             // a command that overwrote the row or the weight of a pending deferred norm: a later GEMV on the norm
-            // reads a snapshot computed before that command
+            // reads a snapshot computed before that command. A command that added no launch joined the last one
+            // (a GEMM merged into the previous GEMM's launch), which then does the writing: the snapshot goes
+            // before that launch.
             if (defer.on && !defer.snap && defer.dirty < 0) {
                 std::vector<Rng> wr;
                 cmd_writes(cmds, n, at, i - at, wr);
-                if (meet_any(wr, defer_ranges())) defer.dirty = long(before);
+                if (meet_any(wr, defer_ranges())) defer.dirty = long(out.size() == before && before > 0 ? before - 1 : before);
             }
         }
         if (accp.on) return reject(n - 1, "internal: a fused DeltaNet output was not consumed");
@@ -1481,6 +1490,7 @@ int gemvq_act_write(gemvq_ctx * c, size_t off, const void * src, size_t n) {
     if (!c || !src || off + n > c->act_floats) return einval(c, "gemvq_act_write: range");
     if (!c->usable) return unusable(c);
     hipSetDevice(c->device);
+    if (const int w = drain(c, "act write")) return w;
     hipError_t e = hipMemcpyAsync(c->act + off, src, n * 4, hipMemcpyHostToDevice, c->stream);
     return e == hipSuccess ? wait_stream(c, "act write") : fail(c, e, "act write");
 }
@@ -1489,6 +1499,7 @@ int gemvq_act_read(gemvq_ctx * c, size_t off, void * dst, size_t n) {
     if (!c || !dst || off + n > c->act_floats) return einval(c, "gemvq_act_read: range");
     if (!c->usable) return unusable(c);
     hipSetDevice(c->device);
+    if (const int w = drain(c, "act read")) return w;
     hipError_t e = hipMemcpyAsync(dst, c->act + off, n * 4, hipMemcpyDeviceToHost, c->stream);
     return e == hipSuccess ? wait_stream(c, "act read") : fail(c, e, "act read");
 }
@@ -1497,6 +1508,7 @@ int gemvq_state_write(gemvq_ctx * c, size_t row, const float * src, size_t rows)
     if (!c || !src || row + rows > c->state_rows) return einval(c, "gemvq_state_write: range");
     if (!c->usable) return unusable(c);
     hipSetDevice(c->device);
+    if (const int w = drain(c, "state write")) return w;
     hipError_t e = hipMemcpyAsync(c->state + row * 128, src, rows * 512, hipMemcpyHostToDevice, c->stream);
     return e == hipSuccess ? wait_stream(c, "state write") : fail(c, e, "state write");
 }
@@ -1505,6 +1517,7 @@ int gemvq_state_read(gemvq_ctx * c, size_t row, float * dst, size_t rows) {
     if (!c || !dst || row + rows > c->state_rows) return einval(c, "gemvq_state_read: range");
     if (!c->usable) return unusable(c);
     hipSetDevice(c->device);
+    if (const int w = drain(c, "state read")) return w;
     hipError_t e = hipMemcpyAsync(dst, c->state + row * 128, rows * 512, hipMemcpyDeviceToHost, c->stream);
     return e == hipSuccess ? wait_stream(c, "state read") : fail(c, e, "state read");
 }
@@ -1558,6 +1571,7 @@ int gemvq_kv_read(gemvq_ctx * c, int kv, int pos0, int npos, uint16_t * k, uint1
     if (pos0 < 0 || npos < 0 || pos0 + npos > b.n_ctx) return einval(c, "gemvq_kv_read: range");
     hipSetDevice(c->device);
     const size_t row = size_t(b.n_head_kv) * b.head_dim, off = size_t(pos0) * row, n = size_t(npos) * row;
+    if (const int w = drain(c, "kv read")) return w;
     hipError_t e = hipSuccess;
     if (k) e = hipMemcpyAsync(k, b.k + off, n * 2, hipMemcpyDeviceToHost, c->stream);
     if (e == hipSuccess && v) e = hipMemcpyAsync(v, b.v + off, n * 2, hipMemcpyDeviceToHost, c->stream);

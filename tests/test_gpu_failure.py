@@ -43,3 +43,24 @@ def test_timed_out_wait_latches_the_context(gq, orc):
         ref = orc.fx_gemv(gq.Q4_0, w2, x2, r2, c2s)
         assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
         assert c2.usable()
+
+
+def test_host_read_after_long_work_is_bounded(gq):
+    """A read of the activation buffer behind work that outlasts the wait bound returns GEMVQ_ETIMEDOUT (the copy
+    waits, bounded, for the queued work before it is issued) and latches the context."""
+    rows, cols = 8192, 16384
+    w = gq.matrix(gq.Q4_0, rows, cols, seed=0, stream=7, std=0.02)
+    x = gq.normal(0, 8, cols)
+    ctx = gq.Context(act_floats=1 << 16, weight_bytes=1 << 27)
+    off = ctx.upload(gq.Q4_0, rows, cols, w)
+    ctx.write(0, x)
+    g = ctx.graph(gq.gemv(gq.Q4_0, rows, cols, off, 0, cols) * 200)
+    ctx.set_wait_timeout(1)
+    print("[failure] act read behind 5 replays of 200 GEMVs of 75.5 MB against a 1 ms wait", flush=True)
+    ctx.replay(g, 5)
+    dst = np.zeros(16, np.float32)
+    st = ctx.lib.gemvq_act_read(ctx.h, 0, dst.ctypes.data_as(gq.C.c_void_p), 16)
+    assert st == gq.ETIMEDOUT, st
+    assert not ctx.usable()
+    assert "act read" in ctx.error()
+    ctx.close()  # waits for the replays, which end normally

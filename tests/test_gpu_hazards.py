@@ -119,3 +119,37 @@ def test_deferred_norm_weight_overwritten_by_a_member(env):
     b = run_state(ctx, x, r, nw, stored, True)
     assert np.array_equal(bits(a[8192:8192 + ROWS]), bits(b[8192:8192 + ROWS]))
     assert np.array_equal(bits(a[20480:20480 + ROWS]), bits(b[20480:20480 + ROWS]))
+
+
+def test_deferred_norm_row_overwritten_by_a_merged_gemm(env):
+    """A deferred RMSNORM, then two batched GEMVs on the same token rows that share one launch, the second writing
+    over the norm's input row, then a GEMV on the norm. The merged launch is the one that overwrites the row, so
+    the norm's row must be fixed before it: the GEMV reads the row as it was when the norm ran. Expected: the norm
+    stored (not deferred) and the commands run one by one."""
+    gq, ctx, offs, x, r, nw = env
+    ntok = 8  # the MFMA batched GEMV (more than 4 tokens), whose launches merge consecutive GEMMs on the same rows
+    rows_x = gq.normal(11, 13, ntok * COLS)
+    deferred = [gq.rmsnorm(COLS, 0, 8192, 12288, 1e-6, flags=gq.NORM_DEFER),
+                gq.gemm(gq.Q4_0, ROWS, COLS, offs[2], 32768, 40960, ntok, COLS, ROWS),
+                gq.gemm(gq.Q4_0, ROWS, COLS, offs[3], 32768, 0, ntok, COLS, ROWS),
+                gq.gemv(gq.Q4_0, ROWS, COLS, offs[0], 12288, 20480)]
+    stored = [gq.rmsnorm(COLS, 0, 8192, 12288, 1e-6)] + deferred[1:]
+
+    def state(cmds, one_by_one):
+        ctx.write(0, np.zeros(1 << 16, np.float32))
+        ctx.write(0, x)
+        ctx.write(8192, nw)
+        ctx.write(32768, rows_x)
+        if one_by_one:
+            for c in cmds:
+                assert ctx.run(c) == 0, ctx.error()
+        else:
+            assert ctx.run([w for c in cmds for w in c]) == 0, ctx.error()
+        return ctx.read(0, 1 << 16)
+
+    a = state(deferred, False)
+    assert ctx.launch_count() == 4  # quantization, the norm's snapshot, the two GEMMs as one launch, the GEMV
+    b = state(stored, True)
+    assert np.array_equal(bits(a[20480:20480 + ROWS]), bits(b[20480:20480 + ROWS]))
+    assert np.array_equal(bits(a[:ntok * ROWS]), bits(b[:ntok * ROWS]))  # the second GEMM's output
+    assert np.array_equal(bits(a[40960:40960 + ntok * ROWS]), bits(b[40960:40960 + ntok * ROWS]))
