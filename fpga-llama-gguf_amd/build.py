@@ -21,7 +21,7 @@ HIP_LIB = os.path.join(PKG, "libgemvq_hip.so")
 SYNTH_LIB = os.path.join(PKG, "libgemvq_synth.so")
 
 HIP_SOURCES = ["gq_gemv.hip", "gq_gemv_q4_0.hip", "gq_gemv_q4_1.hip", "gq_gemv_q8_0.hip", "gq_gemv_kq.hip",
-               "gq_gemv_tok_q4_0.hip", "gq_gemv_tok_q8_0.hip", "gq_gemv_tok_kq.hip", "gq_gemm.hip", "gq_ops.hip", "gq_gdn_out.hip",
+               "gq_gemv_tok_q4_0.hip", "gq_gemv_tok_q8_0.hip", "gq_gemv_tok_kq.hip", "gq_gemm.hip", "gq_ops.hip", "gq_gdn_out.hip", "gq_ref.hip", "gq_ref_gemv.hip",
                "gq_runtime.hip", "gq_static.hip", "qwen35.cpp", "gguf.cpp", "gq_ggml.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -ffp-contract=off: no multiply-add is fused unless written as fmaf (results are reproduced bit for bit on the CPU);

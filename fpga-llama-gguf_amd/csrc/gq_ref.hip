@@ -1,0 +1,309 @@
+// Reference-arithmetic kernels other than the GEMV (see gq_ref.h): row norms, the element-wise ops that evaluate exp
+// or log, the conv, the DeltaNet step and its gated output norm, attention, and the exhaustive hash of the
+// correctly rounded exp / log. They favour the reference's operation order over speed; the mode exists to give the
+// reference CPU path's results on the GPU.
+#include "gemvq_hip.h"
+#include "gq_ref.h"
+#include "gq_refmath.h"
+
+namespace gq {
+namespace {
+
+// ---- RMSNORM rows (gemvq_ref.h:309-324): one workgroup of 256 per row ----
+__global__ __launch_bounds__(256) void norm_ref_kernel(NormArgs a) {
+    __shared__ double red[4];
+    const int r = blockIdx.x, tid = threadIdx.x;
+    const float * x = a.x + size_t(r) * a.stride;
+    const int l2 = a.flags & 1;
+    const float v = ref_norm_value(x, a.n, l2, red);
+    const float s = l2 ? 1.0f / fmaxf(sqrtf(v), a.eps) : 1.0f / sqrtf(v + a.eps);
+    float * y = a.y + size_t(r) * a.n;
+    for (int i = tid; i < a.n; i += 256) y[i] = (a.flags & 2) ? x[i] * s : (x[i] * s) * a.w[i];
+}
+
+// ---- element-wise ops (gemvq_ref.h:297-342), exp / log correctly rounded ----
+__global__ void ew_ref_kernel(EwArgs a) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += gridDim.x * blockDim.x) {
+        const float av = a.op == EW_FILL ? 0.0f : a.row ? a.a[size_t(i / a.row) * a.stride + i % a.row] : a.a[i];
+        float r;
+        switch (a.op) {
+        case EW_ADD: r = av + a.b[i]; break;
+        case EW_MUL: r = av * a.b[i]; break;
+        case EW_SILU_MUL: r = av / (1.0f + cr::expf(-av)) * a.b[i]; break;
+        case EW_SIGMOID_MUL: r = 1.0f / (1.0f + cr::expf(-av)) * a.b[i]; break;
+        case EW_SILU: r = cr::silu(av); break;
+        case EW_SIGMOID: r = cr::sigmoid(av); break;
+        case EW_SOFTPLUS: r = cr::softplus(av); break;
+        case EW_COPY: r = av; break;
+        default: r = a.value; break;
+        }
+        a.y[i] = r;
+    }
+}
+
+// ---- CONV, one token (gemvq_ref.h:344-358): window [state (3), x] summed from t = 0 ----
+__global__ void conv_ref_kernel(ConvArgs a, int tok) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= a.ch) return;
+    const size_t so = 3 * size_t(a.ch) * size_t(tok);
+    // tokens of one sequence run in order on the same window; sequences each have their own
+    const float * src = a.seqs ? a.s_src + so : tok == 0 ? a.s_src : a.s_dst;
+    float * dst = a.seqs ? a.s_dst + so : a.s_dst;
+    const float x = a.x[size_t(tok) * a.ch + c];
+    const float s0 = src[3 * c], s1 = src[3 * c + 1], s2 = src[3 * c + 2];
+    float sum = 0.0f;
+    sum += s0 * a.w[4 * c];
+    sum += s1 * a.w[4 * c + 1];
+    sum += s2 * a.w[4 * c + 2];
+    sum += x * a.w[4 * c + 3];
+    a.y[size_t(tok) * a.ch + c] = a.silu ? cr::silu(sum) : sum;
+    dst[3 * c] = s1;
+    dst[3 * c + 1] = s2;
+    dst[3 * c + 2] = x;
+}
+
+// ---- DeltaNet step, one token (gemvq_ref.h:360-397 with ggml's L2_NORM and gate ops around it,
+// ggml-xrt.cpp:1977-2000): workgroup = value head h, thread j = state row j ----
+__global__ __launch_bounds__(128) void gdn_ref_kernel(GdnArgs a, int tok) {
+    __shared__ float qs[128], ks[128], sc[2];
+    const int h = blockIdx.x, j = threadIdx.x, kh = h % a.hk;
+    const float * q = a.q + size_t(tok) * a.s_qkv + kh * 128;
+    const float * k = a.k + size_t(tok) * a.s_qkv + kh * 128;
+    const float * v = a.v + size_t(tok) * a.s_qkv + h * 128;
+    const size_t so = a.seqs ? size_t(tok) * a.hv * 128 * 128 : 0;
+    const float * src = a.seqs ? a.src + so : tok == 0 ? a.src : a.dst;
+    float * dst = a.dst + so;
+    if (a.flags & GEMVQ_GDN_L2_QK) {  // ggml_l2_norm of q and k: 1 / max(sqrt(sum of squares), eps)
+        if (j == 0 || j == 64) {
+            const float * p = j == 0 ? q : k;
+            double sum = 0.0;
+            for (int i = 0; i < 128; ++i) {
+                const float sq = p[i] * p[i];
+                sum += double(sq);
+            }
+            sc[j >> 6] = 1.0f / fmaxf(sqrtf(float(sum)), a.l2_eps);
+        }
+        __syncthreads();
+        qs[j] = q[j] * sc[0];
+        ks[j] = k[j] * sc[1];
+    } else {
+        qs[j] = q[j];
+        ks[j] = k[j];
+    }
+    float g = a.g[size_t(tok) * a.s_gb + h], beta = a.beta[size_t(tok) * a.s_gb + h];
+    if (a.flags & GEMVQ_GDN_GATES) {  // beta = sigmoid(b), g = softplus(alpha + dt) * a
+        g = cr::softplus(g + a.dt[h]) * a.a[h];
+        beta = cr::sigmoid(beta);
+    }
+    const float decay = cr::expf(g);
+    const size_t row = (size_t(h) * 128 + j) * 128;
+    float s[128];
+#pragma unroll
+    for (int i = 0; i < 128; i += 4) {
+        const float4 t = *reinterpret_cast<const float4 *>(src + row + i);
+        s[i] = t.x;
+        s[i + 1] = t.y;
+        s[i + 2] = t.z;
+        s[i + 3] = t.w;
+    }
+    __syncthreads();
+    float dot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 128; ++i) {
+        s[i] = s[i] * decay;
+        dot += s[i] * ks[i];
+    }
+    const float delta = (v[j] - dot) * beta;
+    float out = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 128; ++i) {
+        s[i] += ks[i] * delta;
+        out += s[i] * qs[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 128; i += 4) *reinterpret_cast<float4 *>(dst + row + i) = make_float4(s[i], s[i + 1], s[i + 2], s[i + 3]);
+    a.y[size_t(tok) * a.s_y + h * 128 + j] = out * a.scale;
+}
+
+// ---- gated output norm per head of 128 (RMS_NORM -> MUL weight -> MUL SILU(z), ggml-xrt.cpp:1952-1975) ----
+__global__ __launch_bounds__(128) void gated_norm_ref_kernel(GatedNormArgs a) {
+    __shared__ float sc;
+    const int h = blockIdx.x, j = threadIdx.x;
+    float * y = a.y + size_t(h) * 128;
+    const float yv = y[j];
+    if (j == 0) {
+        double sum = 0.0;
+        for (int i = 0; i < 128; ++i) {
+            const float sq = y[i] * y[i];
+            sum += double(sq);
+        }
+        sc = 1.0f / sqrtf(float(sum / 128.0) + a.eps);
+    }
+    __syncthreads();
+    const float z = a.z[size_t(h) * 128 + j];
+    y[j] = ((yv * sc) * a.w[j]) * (a.z_silu ? z : cr::silu(z));
+}
+
+// ---- attention, one token ----
+// The token's position, and the cache it stores into and reads (its sequence's region with sequences).
+struct AttnTok {
+    int pos;
+    uint16_t * kc;
+    uint16_t * vc;
+};
+__device__ inline AttnTok attn_tok(const AttnArgs & a, int tok) {
+    AttnTok t;
+    t.pos = a.seq_ctx ? a.pos[16 * tok] : *a.pos + tok;
+    const size_t ro = a.seq_ctx ? size_t(tok) * a.seq_ctx * a.n_head_kv * a.head_dim : 0;
+    t.kc = a.kc + ro;
+    t.vc = a.vc + ro;
+    return t;
+}
+
+// Workgroup s < n_head: q head s, normalized (RMS, weight), rotated (NEOX) and rounded to fp16 into qr; the others:
+// the new key of KV head s - n_head, normalized and rotated, and the value, stored as fp16 at the position.
+__global__ __launch_bounds__(256) void attn_ref_append_kernel(AttnArgs a, int tok) {
+    __shared__ float xs[256], scs;
+    const AttnTok t = attn_tok(a, tok);
+    if (t.pos < 0 || t.pos >= a.n_ctx) return;  // positions past the KV capacity are not stored
+    const int s = blockIdx.x, hd = a.head_dim, e = threadIdx.x, half = a.n_rot / 2;
+    const bool isq = s < a.n_head;
+    const int h = isq ? s : s - a.n_head;
+    const float * x = isq ? a.q + size_t(tok) * a.n_head * a.q_stride + size_t(h) * a.q_stride
+                          : a.k + (size_t(tok) * a.n_head_kv + h) * hd;
+    if (e == 0) {
+        double sum = 0.0;
+        for (int i = 0; i < hd; ++i) {
+            const float sq = x[i] * x[i];
+            sum += double(sq);
+        }
+        scs = 1.0f / sqrtf(float(sum / double(hd)) + a.eps);
+    }
+    __syncthreads();
+    if (e < hd) xs[e] = (x[e] * scs) * (isq ? a.qn[e] : a.kn[e]);
+    __syncthreads();
+    if (e >= hd) return;
+    const float * cs = a.cs + size_t(t.pos) * a.n_rot;
+    const int pi = e < half ? e : e - half;
+    float rv = xs[e];
+    if (e < half) rv = xs[pi] * cs[2 * pi] - xs[pi + half] * cs[2 * pi + 1];
+    else if (e < a.n_rot) rv = xs[pi] * cs[2 * pi + 1] + xs[pi + half] * cs[2 * pi];
+    if (isq) {
+        a.qr[size_t(h) * hd + e] = h2f(f2h(rv));
+    } else {
+        const size_t off = (size_t(t.pos) * a.n_head_kv + h) * hd + e;
+        t.kc[off] = uint16_t(f2h(rv));
+        t.vc[off] = uint16_t(f2h(a.v[(size_t(tok) * a.n_head_kv + h) * hd + e]));
+    }
+}
+
+// Workgroup = q head: scores over positions 0 .. pos (a thread per position, the F16 dot summed in double), the max,
+// e^(s - max) and their sum in order (thread 0), the fp16 probabilities, then thread d sums p * v[d] over the
+// positions in order. sp: n_ctx floats per q head of scratch.
+__global__ __launch_bounds__(256) void attn_ref_kernel(AttnArgs a, int tok) {
+    __shared__ float qv[256], red[4], inv;
+    const AttnTok t = attn_tok(a, tok);
+    if (t.pos < 0 || t.pos >= a.n_ctx) return;
+    const int h = blockIdx.x, hd = a.head_dim, tid = threadIdx.x, n = t.pos + 1;
+    const int kvh = h / (a.n_head / a.n_head_kv);
+    float * sp = a.part + size_t(h) * a.n_ctx;
+    if (tid < hd) qv[tid] = a.qr[size_t(h) * hd + tid];
+    __syncthreads();
+    float mx = -__builtin_inff();
+    for (int p = tid; p < n; p += 256) {
+        const uint16_t * kr = t.kc + (size_t(p) * a.n_head_kv + kvh) * hd;
+        double acc = 0.0;
+        for (int d = 0; d < hd; ++d) {
+            const float pr = qv[d] * h2f(kr[d]);
+            acc += double(pr);
+        }
+        const float sc = float(acc) * a.scale;
+        sp[p] = sc;
+        mx = fmaxf(mx, sc);
+    }
+#pragma unroll
+    for (int st = 32; st >= 1; st >>= 1) mx = fmaxf(mx, __shfl_xor(mx, st, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int p = tid; p < n; p += 256) sp[p] = cr::expf(sp[p] - mx);
+    __syncthreads();
+    if (tid == 0) {
+        double sum = 0.0;
+        for (int p = 0; p < n; ++p) sum += double(sp[p]);
+        inv = float(1.0 / sum);
+    }
+    __syncthreads();
+    for (int p = tid; p < n; p += 256) sp[p] = h2f(f2h(sp[p] * inv));
+    __syncthreads();
+    if (tid >= hd) return;
+    double acc = 0.0;
+    for (int p = 0; p < n; ++p) {
+        const float pv = h2f(t.vc[(size_t(p) * a.n_head_kv + kvh) * hd + tid]) * sp[p];
+        acc += double(pv);
+    }
+    float o = float(acc);
+    if (a.gate) o = cr::sigmoid(a.gate[size_t(tok) * a.n_head * a.q_stride + size_t(h) * 2 * hd + tid]) * o;
+    a.y[(size_t(tok) * a.n_head + h) * hd + tid] = o;
+}
+
+// ---- exhaustive hash of the correctly rounded exp / log (block b: inputs b 2^20 .. b 2^20 + 2^20 - 1) ----
+__global__ __launch_bounds__(256) void crmath_hash_kernel(int fn, unsigned long long * hashes) {
+    __shared__ unsigned long long red[4];
+    const uint32_t blk = blockIdx.x;
+    unsigned long long h = 0;
+    for (uint32_t i = threadIdx.x; i < (1u << 20); i += 256) {
+        const float x = cr::bitsf((blk << 20) | i);
+        const float y = fn == 0 ? cr::expf(x) : cr::logf(x);
+        const uint32_t yb = y != y ? 0x7fc00000u : cr::fbits(y);
+        h += (unsigned long long)yb * (2ull * i + 1ull);
+    }
+#pragma unroll
+    for (int st = 32; st >= 1; st >>= 1) h += (unsigned long long)shfl_xor_i64((long long)h, st);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = h;
+    __syncthreads();
+    if (threadIdx.x == 0) hashes[blk] = red[0] + red[1] + red[2] + red[3];
+}
+
+}  // namespace
+
+hipError_t launch_norm_ref(const NormArgs & a, hipStream_t s) {
+    GQ_LAUNCH(norm_ref_kernel, dim3(a.rows), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_ew_ref(const EwArgs & a, hipStream_t s) {
+    int grid = (a.n + 255) / 256;
+    grid = grid < 1024 ? grid : 1024;
+    GQ_LAUNCH(ew_ref_kernel, dim3(grid), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv_ref(const ConvArgs & a, int tok, hipStream_t s) {
+    GQ_LAUNCH(conv_ref_kernel, dim3((a.ch + 255) / 256), dim3(256), 0, s, a, tok);
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn_ref(const GdnArgs & a, int tok, hipStream_t s) {
+    GQ_LAUNCH(gdn_ref_kernel, dim3(a.hv), dim3(128), 0, s, a, tok);
+    return hipGetLastError();
+}
+
+hipError_t launch_gated_norm_ref(const GatedNormArgs & a, hipStream_t s) {
+    GQ_LAUNCH(gated_norm_ref_kernel, dim3(a.heads), dim3(128), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_ref(const AttnArgs & a, int tok, hipStream_t s) {
+    if (a.head_dim > 256 || a.n_head % a.n_head_kv) return hipErrorInvalidValue;
+    GQ_LAUNCH(attn_ref_append_kernel, dim3(a.n_head + a.n_head_kv), dim3(256), 0, s, a, tok);
+    GQ_LAUNCH(attn_ref_kernel, dim3(a.n_head), dim3(256), 0, s, a, tok);
+    return hipGetLastError();
+}
+
+hipError_t launch_crmath_hash(int fn, unsigned long long * hashes, hipStream_t s) {
+    hipLaunchKernelGGL(crmath_hash_kernel, dim3(4096), dim3(256), 0, s, fn, hashes);
+    return hipGetLastError();
+}
+
+}  // namespace gq

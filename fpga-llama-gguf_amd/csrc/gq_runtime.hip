@@ -4,6 +4,8 @@
 // hipGraph capture and replay of per-token lists. C ABI in include/gemvq_hip.h.
 #include "gemvq_hip.h"
 #include "gq_kernels.h"
+#include "gq_ref.h"
+#include "gq_refmath.h"
 
 #include <hip/hip_runtime.h>
 
@@ -70,15 +72,17 @@ struct KvBuf {
     int n_ctx = 0, n_head_kv = 0, head_dim = 0;
 };
 
-struct LGemv { GemvArgs a; int type; };
-struct LNorm { NormArgs a; };
-struct LEw { EwArgs a; };
-struct LConv { ConvArgs a; };
+// ref: the launch runs in the reference arithmetic (gq_ref.h); tok: the one token of a CONV, GDN or ATTN command
+// that such a launch runs (the command's tokens run as launches in order)
+struct LGemv { GemvArgs a; int type; int ref = 0; };
+struct LNorm { NormArgs a; int ref = 0; };
+struct LEw { EwArgs a; int ref = 0; };
+struct LConv { ConvArgs a; int ref = 0, tok = 0; };
 struct LRope { RopeArgs a; };
-struct LGdn { GdnArgs a; };
+struct LGdn { GdnArgs a; int ref = 0, tok = 0; };
 struct LGdnOut { GdnOutArgs a; int type; };
-struct LGated { GatedNormArgs a; };
-struct LAttn { AttnArgs a; };
+struct LGated { GatedNormArgs a; int ref = 0; };
+struct LAttn { AttnArgs a; int ref = 0, tok = 0; };
 struct LRows { GetRowsArgs a; };
 struct LArgmax { const float * x; int n; unsigned long long * key; int rows, stride; };
 struct LNext { NextTokenArgs a; };
@@ -115,6 +119,8 @@ struct gemvq_ctx {
     int8_t * gemm_q = nullptr;    // a batched GEMV's quantized activation rows (GEMM_MAX_TOK x GEMV_MAXK)
     float * gemm_d = nullptr;     // and their block scales
     float * gemm_s = nullptr;     // and their Q8_1 block sums (for Q4_1 weights)
+    float * ref_x = nullptr;      // the reference arithmetic's copy of a GEMM's token rows and norm weight
+    int arith = GEMVQ_ARITH_CANONICAL;  // the arithmetic lists are compiled in (gemvq_set_arith)
     int last_launches = 0;
     std::string err;
     // Failure handling (ggml-xrt.cpp:69-78, 1258-1264, 2761-2770): every wait for the device is bounded by wait_ms;
@@ -281,6 +287,8 @@ struct Compiler {
     std::string why;
 
     bool range(uint32_t off, uint64_t n) const { return off % 16 == 0 && uint64_t(off) + n <= c->act_floats; }
+    // the list is compiled in the reference arithmetic (gq_ref.h): no fused forms whose arithmetic differs from it
+    int ref() const { return c->arith == GEMVQ_ARITH_REFERENCE ? 1 : 0; }
     float * A(uint32_t off) const { return c->act + off; }
 
     bool reject(unsigned i, const std::string & w) {
@@ -489,7 +497,7 @@ struct Compiler {
     void snapshot_defer(size_t at, int cmd) {
         NormArgs a{A(defer.x), (defer.flags & GEMVQ_NORM_NO_WEIGHT) ? nullptr : A(defer.w), c->dsnap, int(defer.n), 1,
                    int(defer.n), defer.eps, int(defer.flags & 3)};
-        out.insert(out.begin() + long(at), LNorm{a});
+        out.insert(out.begin() + long(at), LNorm{a, ref()});
         spans.insert(spans.begin() + long(at), {cmd, 1});
         defer.snap = true;
     }
@@ -556,7 +564,7 @@ struct Compiler {
                 } else {
                     NormArgs a{A(k[2]), (flags & GEMVQ_NORM_NO_WEIGHT) ? nullptr : A(k[3]), A(k[4]), int(nn), int(rows),
                                int(st), bits_f(k[5]), int(flags & 3)};
-                    out.push_back(LNorm{a});
+                    out.push_back(LNorm{a, ref()});
                     spans.push_back({int(i), 1});
                 }
                 break;
@@ -581,7 +589,7 @@ struct Compiler {
                 }
                 EwArgs a{A(k[2]), A(k[3]), A(k[4]), int(nn), int(row), int(stride),
                          (k[5] & GEMVQ_SILU_MUL_SIGMOID) ? EW_SIGMOID_MUL : EW_SILU_MUL, 0.0f};
-                out.push_back(LEw{a});
+                out.push_back(LEw{a, ref()});
                     spans.push_back({int(i), 1});
                 break;
             }
@@ -596,7 +604,7 @@ struct Compiler {
                 }
                 const int ops[5] = {0, EW_SILU, EW_SIGMOID, EW_SOFTPLUS, EW_COPY};
                 EwArgs a{A(k[2]), nullptr, A(k[4]), int(nn), int(row), int(stride), ops[kind], 0.0f};
-                out.push_back(LEw{a});
+                out.push_back(LEw{a, ref()});
                     spans.push_back({int(i), 1});
                 break;
             }
@@ -647,6 +655,20 @@ struct Compiler {
                 a.seqs = int(seqs && ntok > 1);
                 const unsigned next = i + (gates ? 3 : 2);
                 uint32_t fy = 0, fres = 0;
+                if (ref()) {  // the tokens one launch each, in order; then the gated norm of all of them
+                    for (uint32_t t = 0; t < ntok; ++t) {
+                        out.push_back(LGdn{a, 1, int(t)});
+                        spans.push_back({int(i), gates ? 3 : 2});
+                    }
+                    if (flags & GEMVQ_GDN_GATED) {
+                        GatedNormArgs g{A(k[7]), A(k2[7]), A(k2[6]), int(hv * ntok), bits_f(k2[5]),
+                                        int(bool(flags & GEMVQ_GDN_Z_SILU))};
+                        out.push_back(LGated{g, 1});
+                        spans.push_back({int(i), gates ? 3 : 2});
+                    }
+                    i = next;
+                    return true;
+                }
                 if ((flags & GEMVQ_GDN_GATED) && (flags & GEMVQ_GDN_WITH_OUT) && ntok == 1 && !accp.on &&
                     fuse_out(cmds, n, next, k[7], hv * 128, fy, fres)) {
                     // asked for with GEMVQ_GDN_WITH_OUT: the step, the gated norm and ssm_out in one launch; the GEMV
@@ -704,7 +726,15 @@ struct Compiler {
                     return reject(i, "CONV range");
                 if (seqs && k[5] != k[6] && meet({k[5], k[5] + sw}, {k[6], k[6] + sw})) return reject(i, "CONV state overlap");
                 ConvArgs a{A(k[2]), A(k[3]), A(k[5]), A(k[6]), A(k[4]), int(ch), int(k[7] & 1), int(ntok), int(seqs)};
-                out.push_back(LConv{a});
+                if (ref()) {  // the tokens one launch each, in order
+                    for (uint32_t t = 0; t + 1 < ntok; ++t) {
+                        out.push_back(LConv{a, 1, int(t)});
+                        spans.push_back({int(i), 1});
+                    }
+                    out.push_back(LConv{a, 1, int(ntok - 1)});
+                } else {
+                    out.push_back(LConv{a});
+                }
                     spans.push_back({int(i), 1});
                 break;
             }
@@ -769,8 +799,15 @@ struct Compiler {
                 a.eps = bits_f(k2[3]);
                 a.n_tok = int(ntok);
                 a.qr = b.qr;
-                out.push_back(LAttn{a});
-                spans.push_back({int(i), 2});
+                if (ref()) {  // the tokens one launch pair each, in order
+                    for (uint32_t t = 0; t < ntok; ++t) {
+                        out.push_back(LAttn{a, 1, int(t)});
+                        spans.push_back({int(i), 2});
+                    }
+                } else {
+                    out.push_back(LAttn{a});
+                    spans.push_back({int(i), 2});
+                }
                 i += 2;
                 return true;
             }
@@ -920,7 +957,8 @@ struct Compiler {
         // every workgroup's prologue, so no output may fall on the rows or the norm weight (other workgroups may still
         // be reading them)
         const bool over = (y_off < k[6] + x_len && k[6] < y_off + y_len) || (normw && y_off < k2[5] + cols && k2[5] < y_off + y_len);
-        if (kq && over) return reject(i, "GEMM on K-quant weights: the output falls on the input rows or the norm weight");
+        if (kq && over && !ref()) return reject(i, "GEMM on K-quant weights: the output falls on the input rows or the norm weight");
+        if (ref()) return gemm_ref(g, t, k, k2, over, normw, i, used);
         if (kq || (!over && gemv_tok_ok(t, int(cols), int(ntok), g.epi == EPI_SWIGLU))) {
             const uint32_t cs = kq ? (gemv_tok_ok(t, int(cols), TOK_MAX, false) ? TOK_MAX : 2) : ntok;  // tokens a launch
             for (uint32_t c0 = 0; c0 < ntok; c0 += cs) {
@@ -991,6 +1029,54 @@ struct Compiler {
         const uint32_t w_off = q.norm_w ? uint32_t(q.norm_w - c->act) : 0;
         const bool hits_w = q.norm_w && y_off < w_off + cols && w_off < y_off + y_len;
         if (hits_x || hits_w) lastq.on = false;
+        return true;
+    }
+
+    // The reference arithmetic has no batched form: token t of a GEMM runs as the GEMV command on its row (with the
+    // per-token norm as a deferred norm), one launch each. An output that falls on the token rows or the norm weight
+    // would change what a later token reads, so those are copied first (as the batched kernels read them all before
+    // writing).
+    bool gemm_ref(const GemmArgs & g, int t, const uint32_t * k, const uint32_t * k2, bool over, bool normw, unsigned i,
+                  unsigned used) {
+        const uint32_t cols = k[3], ntok = k2[0], xs = k2[1], nflags = k2[7];
+        const float * x = A(k[6]);
+        size_t xstride = xs;
+        const float * nw = normw ? A(k2[5]) : nullptr;
+        if (over) {
+            EwArgs cp{x, nullptr, c->ref_x, int(cols * ntok), int(cols), int(xs), EW_COPY, 0.0f};
+            out.push_back(LEw{cp});
+            spans.push_back({int(i), int(used)});
+            x = c->ref_x;
+            xstride = cols;
+            if (nw) {
+                EwArgs cw{nw, nullptr, c->ref_x + size_t(GEMM_MAX_TOK) * GEMV_MAXK, int(cols), 0, 0, EW_COPY, 0.0f};
+                out.push_back(LEw{cw});
+                spans.push_back({int(i), int(used)});
+                nw = c->ref_x + size_t(GEMM_MAX_TOK) * GEMV_MAXK;
+            }
+        }
+        for (uint32_t tk = 0; tk < ntok; ++tk) {
+            GemvArgs a{};
+            a.x = x + tk * xstride;
+            a.cols = int(cols);
+            a.xsrc = (nflags & GEMVQ_NORM_DEFER) ? XSRC_NORM : XSRC_RAW;
+            a.norm_w = nw;
+            a.norm_eps = bits_f(k2[6]);
+            a.norm_l2 = (nflags & GEMVQ_NORM_L2) ? 1 : 0;
+            a.n_members = 1;
+            a.total_tasks = g.rows;
+            GemvMember & m = a.m[0];
+            m.w = g.w;
+            m.w2 = g.w2;
+            m.rows = g.rows;
+            m.epi = g.epi;
+            m.y = g.y + size_t(tk) * g.y_stride;
+            m.res = g.res ? g.res + size_t(tk) * g.res_stride : nullptr;
+            a.wbound[0] = g.wbound[0];
+            out.push_back(LGemv{a, t, 1});
+            spans.push_back({int(i), int(used)});
+        }
+        lastq.on = tok_open = false;
         return true;
     }
 
@@ -1215,6 +1301,7 @@ struct Compiler {
             spans.push_back({int(i0), 1});
             a.x = c->xsnap;
         }
+        if (c->dbg_dst && !c->dbg_used && ref()) return reject(i0, "debug block sums are not written in the reference arithmetic");
         if (c->dbg_dst && !c->dbg_used) {
             const Weight * w0 = &c->weights[uint64_t(cmds[size_t(i0) * GEMVQ_CMD_WORDS + 4]) |
                                             (uint64_t(cmds[size_t(i0) * GEMVQ_CMD_WORDS + 5]) << 32)];
@@ -1224,7 +1311,7 @@ struct Compiler {
             a.dbg = c->dbg;
             c->dbg_used = true;
         }
-        out.push_back(LGemv{a, type});
+        out.push_back(LGemv{a, type, ref()});
         spans.push_back({int(i0), int(i - i0)});
         used = i - i0;
         return true;
@@ -1249,20 +1336,23 @@ std::pair<std::string, uint64_t> describe(const Launch & l, int pos) {
             if (m.epi == EPI_ADD) b += rows * 4;
             if (m.epi == EPI_CONV) b += rows * 40;
         }
-        return {"gemv_kernel<" + std::to_string(g->type) + "," + std::to_string(nu) + ">", b};
+        return {std::string(g->ref ? "gemv_ref_kernel<" : "gemv_kernel<") + std::to_string(g->type) + "," + std::to_string(nu) + ">", b};
     }
     if (auto * x = std::get_if<LNorm>(&l))
-        return {"norm_kernel", uint64_t(x->a.n) * x->a.rows * 8 + (x->a.w ? uint64_t(x->a.n) * 4 : 0)};
+        return {x->ref ? "norm_ref_kernel" : "norm_kernel", uint64_t(x->a.n) * x->a.rows * 8 + (x->a.w ? uint64_t(x->a.n) * 4 : 0)};
     if (auto * x = std::get_if<LEw>(&l))
-        return {"ew_kernel", uint64_t(x->a.n) * 4 * (x->a.op == EW_FILL ? 1 : x->a.b ? 3 : 2)};
-    if (auto * x = std::get_if<LConv>(&l)) return {"conv_kernel", uint64_t(x->a.ch) * (40 + 8 * x->a.n_tok)};
+        return {x->ref ? "ew_ref_kernel" : "ew_kernel", uint64_t(x->a.n) * 4 * (x->a.op == EW_FILL ? 1 : x->a.b ? 3 : 2)};
+    if (auto * x = std::get_if<LConv>(&l))
+        return {x->ref ? "conv_ref_kernel" : "conv_kernel", uint64_t(x->a.ch) * (40 + 8 * (x->ref ? 1 : x->a.n_tok))};
     if (auto * x = std::get_if<LRope>(&l))
         return {"rope_kernel", uint64_t(x->a.ne0) * x->a.rows * 8 + uint64_t(x->a.n_dims) * 4};
     if (auto * x = std::get_if<LGdn>(&l)) {
         const uint64_t hv = uint64_t(x->a.hv), hk = uint64_t(x->a.hk);
-        return {"gdn_kernel", 2 * hv * 128 * 128 * 4 + ((2 * hk + 2 * hv) * 128 * 4 + hv * 16) * uint64_t(x->a.n_tok)};
+        return {x->ref ? "gdn_ref_kernel" : "gdn_kernel",
+                2 * hv * 128 * 128 * 4 + ((2 * hk + 2 * hv) * 128 * 4 + hv * 16) * uint64_t(x->ref ? 1 : x->a.n_tok)};
     }
-    if (auto * x = std::get_if<LGated>(&l)) return {"gated_norm_kernel", uint64_t(x->a.heads) * 128 * 12 + 512};
+    if (auto * x = std::get_if<LGated>(&l))
+        return {x->ref ? "gated_norm_ref_kernel" : "gated_norm_kernel", uint64_t(x->a.heads) * 128 * 12 + 512};
     if (auto * x = std::get_if<LGdnOut>(&l)) {
         const GdnOutArgs & o = x->a;
         const uint64_t hv = uint64_t(o.g.hv), hk = uint64_t(o.g.hk), rows = uint64_t(o.rows);
@@ -1272,10 +1362,10 @@ std::pair<std::string, uint64_t> describe(const Launch & l, int pos) {
     }
     if (auto * x = std::get_if<LAttn>(&l)) {
         const AttnArgs & a = x->a;
-        const uint64_t nt = uint64_t(a.n_tok > 1 ? a.n_tok : 1);  // token t reads positions 0 .. pos + t
+        const uint64_t nt = uint64_t(a.n_tok > 1 && !x->ref ? a.n_tok : 1);  // token t reads positions 0 .. pos + t
         const uint64_t kv = (uint64_t(pos + 1) * nt + nt * (nt - 1) / 2) * a.n_head_kv * a.head_dim * 2 * 2;
         const uint64_t vec = (uint64_t(a.n_head) * a.head_dim * 4 * (a.gate ? 3 : 2) + uint64_t(a.n_head_kv) * a.head_dim * 8) * nt;
-        return {"attn_kernel", kv + vec};
+        return {x->ref ? "attn_ref_kernel" : "attn_kernel", kv + vec};
     }
     if (auto * x = std::get_if<LRows>(&l))
         return {"get_rows_kernel", uint64_t(x->a.cols) * 4 + gguf_row_bytes(x->a.type, x->a.cols)};
@@ -1312,14 +1402,14 @@ std::pair<std::string, uint64_t> describe(const Launch & l, int pos) {
 hipError_t issue(const std::vector<Launch> & ls, hipStream_t s) {
     for (const Launch & l : ls) {
         hipError_t e = hipSuccess;
-        if (auto * g = std::get_if<LGemv>(&l)) e = launch_gemv(g->a, g->type, s);
-        else if (auto * x = std::get_if<LNorm>(&l)) e = launch_norm(x->a, s);
-        else if (auto * x = std::get_if<LEw>(&l)) e = launch_ew(x->a, s);
-        else if (auto * x = std::get_if<LConv>(&l)) e = launch_conv(x->a, s);
+        if (auto * g = std::get_if<LGemv>(&l)) e = g->ref ? launch_gemv_ref(g->a, g->type, s) : launch_gemv(g->a, g->type, s);
+        else if (auto * x = std::get_if<LNorm>(&l)) e = x->ref ? launch_norm_ref(x->a, s) : launch_norm(x->a, s);
+        else if (auto * x = std::get_if<LEw>(&l)) e = x->ref ? launch_ew_ref(x->a, s) : launch_ew(x->a, s);
+        else if (auto * x = std::get_if<LConv>(&l)) e = x->ref ? launch_conv_ref(x->a, x->tok, s) : launch_conv(x->a, s);
         else if (auto * x = std::get_if<LRope>(&l)) e = launch_rope(x->a, s);
-        else if (auto * x = std::get_if<LGdn>(&l)) e = launch_gdn(x->a, s);
-        else if (auto * x = std::get_if<LGated>(&l)) e = launch_gated_norm(x->a, s);
-        else if (auto * x = std::get_if<LAttn>(&l)) e = launch_attn(x->a, s);
+        else if (auto * x = std::get_if<LGdn>(&l)) e = x->ref ? launch_gdn_ref(x->a, x->tok, s) : launch_gdn(x->a, s);
+        else if (auto * x = std::get_if<LGated>(&l)) e = x->ref ? launch_gated_norm_ref(x->a, s) : launch_gated_norm(x->a, s);
+        else if (auto * x = std::get_if<LAttn>(&l)) e = x->ref ? launch_attn_ref(x->a, x->tok, s) : launch_attn(x->a, s);
         else if (auto * x = std::get_if<LRows>(&l)) e = launch_get_rows(x->a, s);
         else if (auto * x = std::get_if<LArgmax>(&l)) e = launch_argmax(x->x, x->n, x->key, x->rows, x->stride, s);
         else if (auto * x = std::get_if<LNext>(&l)) e = launch_next_token(x->a, s);
@@ -1384,6 +1474,7 @@ gemvq_ctx * gemvq_ctx_create(int device, size_t act_floats, size_t weight_bytes,
     if (e == hipSuccess) e = hipMalloc(&c->gemm_q, size_t(GEMM_MAX_TOK) * GEMV_MAXK);
     if (e == hipSuccess) e = hipMalloc(&c->gemm_d, size_t(GEMM_MAX_TOK) * (GEMV_MAXK / 32) * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&c->gemm_s, size_t(GEMM_MAX_TOK) * (GEMV_MAXK / 32) * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&c->ref_x, size_t(GEMM_MAX_TOK + 1) * GEMV_MAXK * sizeof(float));
     if (e == hipSuccess && state_rows) e = hipMemset(c->state, 0, state_rows * 128 * sizeof(float));
     if (e != hipSuccess) {
         g_create_error = std::string("gemvq_ctx_create: ") + hipGetErrorString(e);
@@ -1423,6 +1514,7 @@ void gemvq_ctx_destroy(gemvq_ctx * c) {
     hipFree(c->gemm_q);
     hipFree(c->gemm_d);
     hipFree(c->gemm_s);
+    hipFree(c->ref_x);
     hipFree(c->dbg);
     if (c->stream) hipStreamDestroy(c->stream);
     delete c;
@@ -1692,6 +1784,38 @@ int gemvq_set_wait_timeout(gemvq_ctx * c, unsigned ms) {
 int gemvq_usable(const gemvq_ctx * c) { return c && c->usable ? 1 : 0; }
 
 int gemvq_last_launch_count(const gemvq_ctx * c) { return c ? c->last_launches : -1; }
+
+int gemvq_set_arith(gemvq_ctx * c, int arith) {
+    if (!c || (arith != GEMVQ_ARITH_CANONICAL && arith != GEMVQ_ARITH_REFERENCE)) return einval(c, "gemvq_set_arith: mode");
+    c->arith = arith;
+    return 0;
+}
+
+int gemvq_arith(const gemvq_ctx * c) { return c ? c->arith : GEMVQ_EINVAL; }
+
+float gemvq_cr_expf(float x) { return cr::expf(x); }
+float gemvq_cr_logf(float x) { return cr::logf(x); }
+
+int gemvq_crmath_hash(gemvq_ctx * c, int fn, uint64_t * hashes) {
+    if (!c || !hashes || (fn != 0 && fn != 1)) return einval(c, "gemvq_crmath_hash: arguments");
+    if (!c->usable) return unusable(c);
+    hipSetDevice(c->device);
+    unsigned long long * d = nullptr;
+    hipError_t e = hipMalloc(&d, 4096 * 8);
+    if (e != hipSuccess) return fail(c, e, "crmath hash");
+    e = launch_crmath_hash(fn, d, c->stream);
+    if (e != hipSuccess) {
+        hipFree(d);
+        return fail(c, e, "crmath hash");
+    }
+    int st = wait_stream(c, "crmath hash");
+    if (!st) {
+        e = hipMemcpy(hashes, d, 4096 * 8, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) st = fail(c, e, "crmath hash copy");
+    }
+    hipFree(d);
+    return st;
+}
 
 int gemvq_debug_blocksums(gemvq_ctx * c, int32_t * dst, size_t n) {
     if (!c || !dst || n == 0) return einval(c, "gemvq_debug_blocksums: arguments");

@@ -643,6 +643,17 @@ int gemvq_qwen35_commands(gemvq_qwen35 * m, uint32_t * words, size_t n_words) {
 
 int gemvq_qwen35_graph(gemvq_qwen35 * m) { return m ? m->graph : -1; }
 
+int gemvq_qwen35_set_arith(gemvq_qwen35 * m, int arith) {
+    if (!m) return GEMVQ_EINVAL;
+    const int st = gemvq_set_arith(m->ctx, arith);
+    if (st) return st;
+    // the captured graphs hold the kernels of the arithmetic they were compiled in: capture again on next use
+    if (m->graph >= 0) gemvq_graph_destroy(m->ctx, m->graph);
+    if (m->chunk_graph >= 0) gemvq_graph_destroy(m->ctx, m->chunk_graph);
+    m->graph = m->chunk_graph = -1;
+    return 0;
+}
+
 }  // extern "C"
 
 extern "C" int gemvq_qwen35_dry_commands(const gemvq_qw_config * cfg, const gemvq_tensor_desc * tab, int n,

@@ -29,6 +29,7 @@ NORM_L2, NORM_NO_WEIGHT, NORM_DEFER = 1, 2, 4
 SILU_MUL_SIGMOID = 1
 UNARY_SILU, UNARY_SIGMOID, UNARY_SOFTPLUS, UNARY_COPY = 1, 2, 3, 4
 EINVAL, ETIMEDOUT, EUNUSABLE = -10000, -10001, -10002
+ARITH_CANONICAL, ARITH_REFERENCE = 0, 1
 MAX_CMDS = 4096
 
 
@@ -177,6 +178,11 @@ def hip_lib() -> C.CDLL:
         _c_fn(lib, "gemvq_last_launch_count", C.c_int, vp)
         _c_fn(lib, "gemvq_debug_blocksums", C.c_int, vp, vp, C.c_size_t)
         _c_fn(lib, "gemvq_graph_time", C.c_int, vp, C.c_int, C.c_int, C.POINTER(C.c_double))
+        _c_fn(lib, "gemvq_set_arith", C.c_int, vp, C.c_int)
+        _c_fn(lib, "gemvq_arith", C.c_int, vp)
+        _c_fn(lib, "gemvq_cr_expf", C.c_float, C.c_float)
+        _c_fn(lib, "gemvq_cr_logf", C.c_float, C.c_float)
+        _c_fn(lib, "gemvq_crmath_hash", C.c_int, vp, C.c_int, u64p)
         _hip = lib
     return _hip
 
@@ -371,6 +377,20 @@ class Context:
 
     def launch_count(self) -> int:
         return self.lib.gemvq_last_launch_count(self.h)
+
+    def set_arith(self, arith: int) -> None:
+        """Arithmetic of the lists compiled from now on: ARITH_CANONICAL (default) or ARITH_REFERENCE (the reference's
+        CPU arithmetic, gemvq_hip.h)."""
+        self._check(self.lib.gemvq_set_arith(self.h, arith), "set arith")
+
+    def arith(self) -> int:
+        return self.lib.gemvq_arith(self.h)
+
+    def crmath_hash(self, fn: int) -> np.ndarray:
+        """The device's correctly rounded exp (fn 0) or log (fn 1) over every binary32 input, as 4096 block hashes."""
+        out = np.zeros(4096, dtype=np.uint64)
+        self._check(self.lib.gemvq_crmath_hash(self.h, fn, out.ctypes.data_as(C.POINTER(C.c_uint64))), "crmath hash")
+        return out
 
     def debug_blocksums(self, out: np.ndarray) -> None:
         assert out.dtype == np.int32 and out.flags["C_CONTIGUOUS"]

@@ -194,6 +194,7 @@ def _lib():
         gq._c_fn(lib, "gemvq_qwen35_hidden", C.c_int, vp, vp)
         gq._c_fn(lib, "gemvq_qwen35_commands", C.c_int, vp, vp, C.c_size_t)
         gq._c_fn(lib, "gemvq_qwen35_graph", C.c_int, vp)
+        gq._c_fn(lib, "gemvq_qwen35_set_arith", C.c_int, vp, C.c_int)
         gq._c_fn(lib, "gemvq_qwen35_batch_sizes", C.c_int, vp, vp, C.c_int, C.c_int, C.POINTER(C.c_size_t),
                  C.POINTER(C.c_size_t), C.POINTER(C.c_size_t))
         gq._c_fn(lib, "gemvq_qwen35_batch_create", vp, vp, vp, vp, C.c_int, vp, C.c_int)
@@ -287,6 +288,10 @@ class Model:
 
     def graph(self) -> int:
         return self.lib.gemvq_qwen35_graph(self.h)
+
+    def set_arith(self, arith: int) -> None:
+        """gq.ARITH_REFERENCE: the following steps and prefills in the reference's CPU arithmetic (gemvq_hip.h)."""
+        self._ok(self.lib.gemvq_qwen35_set_arith(self.h, arith), "set arith")
 
     def generate(self, prompt: np.ndarray, n_gen: int) -> np.ndarray:
         """Greedy decode: the prompt token by token, then n_gen generated tokens; returns all ids."""

@@ -245,6 +245,30 @@ typedef struct {
 int gemvq_profile(gemvq_ctx * ctx, const uint32_t * cmds, unsigned n_cmds, int reps, gemvq_launch_stat * out,
                   int max_out);
 
+/* Arithmetic of the lists compiled after the call (graphs keep the arithmetic they were captured in).
+ * GEMVQ_ARITH_CANONICAL (default): the reference kernel's fixed-point GEMV rows (each block term exact and floored to
+ * 2^-40, summed exactly, rounded once; fpga/src/gemvqw_engine.h:352-445) and pairwise-tree FP32 reductions.
+ * GEMVQ_ARITH_REFERENCE: the reference's CPU path (fpga/src/gemvq_ref.h), as its ggml backend checks the kernel
+ * against it (the XRT-VERIFY mode, ggml-xrt.cpp:1153-1202): GEMV rows as FP32 block terms added in block order (the
+ * K-quants' eight FP32 partial sums), norm sums of FP32 squares in double in index order, the DeltaNet step's dots in
+ * order, attention with double sums (ggml's CPU path), and correctly rounded exp / log (gemvq_cr_expf / _logf) where
+ * the reference calls libm. Every command keeps its meaning; the fused forms whose arithmetic differs (the gated norm
+ * in the next GEMV's prologue, GEMVQ_GDN_WITH_OUT) run unfused, a GEMM runs token by token as GEMV commands, and
+ * CONV, GDN and ATTN with several tokens run token by token. Debug block sums are not written in this mode.
+ * Returns 0 or GEMVQ_EINVAL. */
+#define GEMVQ_ARITH_CANONICAL 0
+#define GEMVQ_ARITH_REFERENCE 1
+int gemvq_set_arith(gemvq_ctx * ctx, int arith);
+int gemvq_arith(const gemvq_ctx * ctx);
+/* The reference arithmetic's exp and log on the host: the binary32 value nearest to e^x / log x (ties to even), the
+ * same code the device evaluates. */
+float gemvq_cr_expf(float x);
+float gemvq_cr_logf(float x);
+/* Test hook: the device's correctly rounded exp (fn 0) or log (fn 1) over every binary32 input, as 4096 block
+ * hashes (block b: the inputs with bits b 2^20 .. b 2^20 + 2^20 - 1; hash = sum mod 2^64 of bits(f(x)) (2 i + 1) over
+ * the block's i, NaN results as 0x7fc00000). Synchronous; 0 or a negative status. */
+int gemvq_crmath_hash(gemvq_ctx * ctx, int fn, uint64_t * hashes);
+
 /* No counterpart in the reference: for callers that cannot allocate device memory (code under hipGraph capture,
  * serving loops, harnesses that forbid hipMalloc). The batched GEMV of the GEMM command (plain epilog) on
  * caller-owned device memory, allocating nothing: y[t * y_stride + r] = row r of the matrix times token row t of x

@@ -63,6 +63,10 @@ int gemvq_qwen35_hidden(gemvq_qwen35 * m, float * out);
 int gemvq_qwen35_commands(gemvq_qwen35 * m, uint32_t * words, size_t n_words);
 /* The captured graph id (for gemvq_graph_time); -1 before the first step. */
 int gemvq_qwen35_graph(gemvq_qwen35 * m);
+/* The arithmetic of the model's steps and prefill from now on (gemvq_set_arith on its context; the graphs are
+ * captured again): GEMVQ_ARITH_REFERENCE decodes with the tokens and logits of the reference's CPU path. The
+ * states carry over. 0 or GEMVQ_EINVAL. */
+int gemvq_qwen35_set_arith(gemvq_qwen35 * m, int arith);
 /* Lockstep decode of n_seq (2..GEMVQ_GEMM_MAX_TOK) sequences (the multi-sequence path the reference plans,
  * ROADMAP.md:78-96; no counterpart in its code): every step reads each weight row once for all sequences (GEMM
  * commands over their n_seq token rows), with CONV, the DeltaNet step and attention in their sequences forms, so

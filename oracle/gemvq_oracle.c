@@ -626,31 +626,50 @@ void orc_unary(const float * x, int n, int kind, float * y) {
     }
 }
 
-/* gemvq_ref.h:333-342 with libm exp/log. */
-void orc_ref_unary(const float * x, int n, int kind, float * y) {
+/* The exp and log of the reference arithmetic: the host's libm (the compiled reference path, for the golden
+ * vectors) or the correctly rounded functions (the reference-arithmetic decoder, which the GPU reproduces). */
+typedef struct {
+    float (*exp)(float);
+    float (*log)(float);
+} orc_math;
+static const orc_math MATH_LIBM = {expf, logf};
+static const orc_math MATH_CR = {orc_cr_expf, orc_cr_logf};
+
+/* gemvq_ref.h:333-342. */
+static void ref_unary(const float * x, int n, int kind, float * y, const orc_math * mt) {
     for (int i = 0; i < n; ++i) {
         const float v = x[i];
-        y[i] = kind == 1 ? v / (1.0f + expf(-v)) : kind == 2 ? 1.0f / (1.0f + expf(-v))
-             : kind == 3 ? (v > 20.0f ? v : logf(1.0f + expf(v))) : v;
+        y[i] = kind == 1 ? v / (1.0f + mt->exp(-v)) : kind == 2 ? 1.0f / (1.0f + mt->exp(-v))
+             : kind == 3 ? (v > 20.0f ? v : mt->log(1.0f + mt->exp(v))) : v;
     }
+}
+void orc_ref_unary(const float * x, int n, int kind, float * y) { ref_unary(x, n, kind, y, &MATH_LIBM); }
+void orc_ref_unary_cr(const float * x, int n, int kind, float * y) { ref_unary(x, n, kind, y, &MATH_CR); }
+
+/* gemvq_ref.h:303-307: y = g / (1 + e^-g) * u */
+void orc_ref_silu_mul_cr(const float * g, const float * u, int n, float * y) {
+    for (int i = 0; i < n; ++i) y[i] = g[i] / (1.0f + orc_cr_expf(-g[i])) * u[i];
 }
 
 /* CONV (gemvq_ref.h:346-358, gemvqc_ops.h:135-144, 387-431): window [state_c (3), x_c], summed from t = 0. */
 static void conv_impl(const float * state, const float * x, const float * w, int ch, int silu, float * y,
-                      float * new_state, int canonical) {
+                      float * new_state, const orc_math * mt) {
     for (int c = 0; c < ch; ++c) {
         const float in[4] = {state[c * 3], state[c * 3 + 1], state[c * 3 + 2], x[c]};
         float sum = 0.0f;
         for (int t = 0; t < 4; ++t) sum += in[t] * w[c * 4 + t];
-        y[c] = silu ? (canonical ? orc_silu(sum) : sum / (1.0f + expf(-sum))) : sum;
+        y[c] = silu ? (mt ? sum / (1.0f + mt->exp(-sum)) : orc_silu(sum)) : sum;
         for (int t = 0; t < 3; ++t) new_state[c * 3 + t] = in[t + 1];
     }
 }
 void orc_conv(const float * state, const float * x, const float * w, int ch, int silu, float * y, float * ns) {
-    conv_impl(state, x, w, ch, silu, y, ns, 1);
+    conv_impl(state, x, w, ch, silu, y, ns, NULL);
 }
 void orc_ref_conv(const float * state, const float * x, const float * w, int ch, int silu, float * y, float * ns) {
-    conv_impl(state, x, w, ch, silu, y, ns, 0);
+    conv_impl(state, x, w, ch, silu, y, ns, &MATH_LIBM);
+}
+void orc_ref_conv_cr(const float * state, const float * x, const float * w, int ch, int silu, float * y, float * ns) {
+    conv_impl(state, x, w, ch, silu, y, ns, &MATH_CR);
 }
 
 /* ROPE (gemvqc_ops.h:275-312): NEOX pairs (i, i + n_dims / 2); cs holds cos, sin of pair i at 2i, 2i + 1. */
@@ -676,14 +695,14 @@ void orc_ref_gdn(float * state, const float * q, const float * k, const float * 
 }
 
 /* The value heads are independent, so they split over threads without changing any result. */
-void orc_ref_gdn_mt(float * state, const float * q, const float * k, const float * v, const float * g,
+static void ref_gdn(float * state, const float * q, const float * k, const float * v, const float * g,
                     const float * beta, int hv, int hk, float scale, float * y, double * y_mag, double * s_mag,
-                    int n_threads) {
+                    int n_threads, const orc_math * mt) {
     const int S = 128;
 #pragma omp parallel for schedule(static) num_threads(n_threads > 0 ? n_threads : 1)
     for (int h = 0; h < hv; ++h) {
         const float * qh = q + (h % hk) * S, * kh = k + (h % hk) * S;
-        const float decay = expf(g[h]);
+        const float decay = mt->exp(g[h]);
         for (int j = 0; j < S; ++j) {
             float * row = &state[((size_t)h * S + j) * S];
             double dmag = 0.0;
@@ -707,6 +726,15 @@ void orc_ref_gdn_mt(float * state, const float * q, const float * k, const float
             if (y_mag) y_mag[h * S + j] = omag * scale;
         }
     }
+}
+void orc_ref_gdn_mt(float * state, const float * q, const float * k, const float * v, const float * g,
+                    const float * beta, int hv, int hk, float scale, float * y, double * y_mag, double * s_mag,
+                    int n_threads) {
+    ref_gdn(state, q, k, v, g, beta, hv, hk, scale, y, y_mag, s_mag, n_threads, &MATH_LIBM);
+}
+void orc_ref_gdn_cr_mt(float * state, const float * q, const float * k, const float * v, const float * g,
+                       const float * beta, int hv, int hk, float scale, float * y, int n_threads) {
+    ref_gdn(state, q, k, v, g, beta, hv, hk, scale, y, NULL, NULL, n_threads, &MATH_CR);
 }
 
 /* Canonical fused step: the GDN opcode (gemvqc16.h:60-81) with the input load of gemvqc_gdn.h:223-281, the step of
@@ -834,8 +862,8 @@ void orc_ref_attn(const float * q, const uint16_t * kc, const uint16_t * vc, int
     orc_ref_attn_mt(q, kc, vc, nh, nkvh, hd, n_kv, scale, out, 1);
 }
 
-void orc_ref_attn_mt(const float * q, const uint16_t * kc, const uint16_t * vc, int nh, int nkvh, int hd, int n_kv,
-                     float scale, float * out, int n_threads) {
+static void ref_attn(const float * q, const uint16_t * kc, const uint16_t * vc, int nh, int nkvh, int hd, int n_kv,
+                     float scale, float * out, int n_threads, const orc_math * mt) {
     const int group = nh / nkvh;
 #pragma omp parallel for schedule(static) num_threads(n_threads > 0 ? n_threads : 1)
     for (int h = 0; h < nh; ++h) {
@@ -854,7 +882,7 @@ void orc_ref_attn_mt(const float * q, const uint16_t * kc, const uint16_t * vc, 
         }
         double sum = 0.0;
         for (int t = 0; t < n_kv; ++t) {
-            const float e = expf(s[t] - mx);
+            const float e = mt->exp(s[t] - mx);
             sum += (double)e;
             s[t] = e;
         }
@@ -867,6 +895,14 @@ void orc_ref_attn_mt(const float * q, const uint16_t * kc, const uint16_t * vc, 
         }
         free(q16); free(s); free(p16);
     }
+}
+void orc_ref_attn_mt(const float * q, const uint16_t * kc, const uint16_t * vc, int nh, int nkvh, int hd, int n_kv,
+                     float scale, float * out, int n_threads) {
+    ref_attn(q, kc, vc, nh, nkvh, hd, n_kv, scale, out, n_threads, &MATH_LIBM);
+}
+void orc_ref_attn_cr_mt(const float * q, const uint16_t * kc, const uint16_t * vc, int nh, int nkvh, int hd, int n_kv,
+                        float scale, float * out, int n_threads) {
+    ref_attn(q, kc, vc, nh, nkvh, hd, n_kv, scale, out, n_threads, &MATH_CR);
 }
 
 /* ggml dequantize_row_q6_K: y = d * sc * q evaluated as (d * sc) * q. */

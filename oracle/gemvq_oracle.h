@@ -39,6 +39,18 @@ float orc_softplus(float x);
 float orc_pair_sum(const float * a, int n);
 size_t orc_row_bytes(int fmt, int cols);
 
+/* ---- correctly rounded exp and log (orc_crmath.c): the binary32 value nearest to e^x / log x ---- */
+float orc_cr_expf(float x);
+float orc_cr_logf(float x);
+/* Exhaustive checks over every binary32 input (orc_crcheck.c); fn 0 exp, 1 log. out: [0] inputs where orc_cr_* is
+ * not the correctly rounded result, [1] inputs where the host libm (expf / logf) differs from orc_cr_*, [2] inputs
+ * the 80-bit reference left to quad precision, [3] inputs off the special cases. */
+void orc_crmath_check(int fn, int n_threads, uint64_t out[4]);
+/* Inputs where other() differs from orc_cr_* (NaN equals NaN). */
+uint64_t orc_crmath_compare(int fn, float (*other)(float), int n_threads);
+/* hashes[b], b < 4096: sum mod 2^64 over i < 2^20 of bits(f(bits b 2^20 + i)) (2 i + 1), NaN as 0x7fc00000. */
+void orc_crmath_hash(int fn, uint64_t * hashes, int n_threads);
+
 /* ---- activation quantizers (gemvq_ref.h:62-81, 236-245) ---- */
 /* Q8_0: per 32 values d_bits = fp16(amax / 127), q = roundf(x * (1 / (amax / 127))). */
 void orc_quantize_q8_0(const float * x, int n, int8_t * q, uint16_t * d_bits);
@@ -79,6 +91,10 @@ void orc_conv(const float * state, const float * x, const float * w, int ch, int
 void orc_rope(const float * x, const float * cs, int n_dims, int ne0, int rows, float * y);
 void orc_ref_conv(const float * state, const float * x, const float * w, int ch, int silu, float * y, float * new_state);
 void orc_ref_unary(const float * x, int n, int kind, float * y);
+/* The same with the correctly rounded exp / log in place of libm's (the reference-arithmetic decoder). */
+void orc_ref_conv_cr(const float * state, const float * x, const float * w, int ch, int silu, float * y, float * new_state);
+void orc_ref_unary_cr(const float * x, int n, int kind, float * y);
+void orc_ref_silu_mul_cr(const float * g, const float * u, int n, float * y);
 
 /* ---- Gated DeltaNet step ---- */
 /* Reference (gemvq_ref.h:363-397): state [hv][128][128] in place, q/k [hk][128], v [hv][128], g, beta [hv] (g is
@@ -88,6 +104,8 @@ void orc_ref_gdn(float * state, const float * q, const float * k, const float * 
 void orc_ref_gdn_mt(float * state, const float * q, const float * k, const float * v, const float * g,
                     const float * beta, int hv, int hk, float scale, float * y, double * y_mag, double * s_mag,
                     int n_threads);
+void orc_ref_gdn_cr_mt(float * state, const float * q, const float * k, const float * v, const float * g,
+                       const float * beta, int hv, int hk, float scale, float * y, int n_threads);
 /* Canonical fused step (GDN opcode): flags bit1 L2-normalize q/k (l2_eps), bit2 gated output norm
  * (rms_eps, w[128], z[hv*128]), bit3 gates from raw projections (beta = sigmoid(b), g = softplus(a_raw + dt) * a),
  * bit5 z already holds silu(z).
@@ -112,6 +130,8 @@ void orc_ref_attn(const float * q, const uint16_t * kc, const uint16_t * vc, int
                   float scale, float * out);
 void orc_ref_attn_mt(const float * q, const uint16_t * kc, const uint16_t * vc, int nh, int nkvh, int hd, int n_kv,
                      float scale, float * out, int n_threads);
+void orc_ref_attn_cr_mt(const float * q, const uint16_t * kc, const uint16_t * vc, int nh, int nkvh, int hd, int n_kv,
+                        float scale, float * out, int n_threads);
 
 /* ---- Q6_K row dequantize (ggml dequantize_row_q6_K) and argmax ---- */
 void orc_dequant_row_q6_K(const uint8_t * row, int cols, float * y);

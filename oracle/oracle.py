@@ -93,6 +93,17 @@ def orc() -> C.CDLL:
         _fn(lib, "orc_gdn_mt", None, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i, i, fl, fl, fl, i, vp, i)
         _fn(lib, "orc_attn_mt", None, vp, vp, vp, i, i, i, i, fl, vp, i)
         _fn(lib, "orc_ref_attn", None, vp, vp, vp, i, i, i, i, fl, vp)
+        for n in ("orc_cr_expf", "orc_cr_logf"):
+            _fn(lib, n, fl, fl)
+        u64p = C.POINTER(C.c_uint64)
+        _fn(lib, "orc_crmath_check", None, i, i, u64p)
+        _fn(lib, "orc_crmath_compare", C.c_uint64, i, vp, i)
+        _fn(lib, "orc_crmath_hash", None, i, u64p, i)
+        _fn(lib, "orc_ref_unary_cr", None, vp, i, i, vp)
+        _fn(lib, "orc_ref_conv_cr", None, vp, vp, vp, i, i, vp, vp)
+        _fn(lib, "orc_ref_silu_mul_cr", None, vp, vp, i, vp)
+        _fn(lib, "orc_ref_gdn_cr_mt", None, vp, vp, vp, vp, vp, vp, i, i, fl, vp, i)
+        _fn(lib, "orc_ref_attn_cr_mt", None, vp, vp, vp, i, i, i, i, fl, vp, i)
         _orc = lib
     return _orc
 
@@ -195,6 +206,15 @@ def rownorm(x: np.ndarray, w: np.ndarray | None, n: int, rows: int, eps: float, 
     return y
 
 
+def ref_rownorm(x: np.ndarray, w: np.ndarray | None, n: int, rows: int, eps: float, flags: int = 0):
+    """The reference's row norm (gemvq_ref.h:309-324): the FP32 squares summed in double in order; packed rows."""
+    x = np.ascontiguousarray(x, F)
+    w = np.ascontiguousarray(w, F) if w is not None else np.zeros(n, F)
+    y = np.empty(n * rows, F)
+    orc().orc_ref_rownorm(_p(x), _p(w), n, rows, eps, flags, _p(y))
+    return y
+
+
 def pair_sum(a: np.ndarray) -> float:
     a = np.ascontiguousarray(a, F)
     return float(orc().orc_pair_sum(_p(a), a.size))
@@ -255,6 +275,64 @@ def attn(q, kc, vc, nh, nkvh, hd, n_kv, scale, threads: int = 1, reference: bool
     return out
 
 
+def crmath_check(fn: int, threads: int = 0) -> dict:
+    """Exhaustive check of the correctly rounded exp (fn 0) / log (fn 1) over every binary32 input."""
+    out = (C.c_uint64 * 4)()
+    orc().orc_crmath_check(fn, threads or min(16, os.cpu_count() or 1), out)
+    return {"misrounded": int(out[0]), "libm_differs": int(out[1]), "quad_decided": int(out[2]), "inputs": int(out[3])}
+
+
+def crmath_compare(fn: int, func_ptr: int, threads: int = 0) -> int:
+    """Inputs (of all 2^32) where the float(float) function at func_ptr differs from the oracle's exp / log."""
+    return int(orc().orc_crmath_compare(fn, func_ptr, threads or min(16, os.cpu_count() or 1)))
+
+
+def crmath_hash(fn: int, threads: int = 0) -> np.ndarray:
+    out = np.zeros(4096, np.uint64)
+    orc().orc_crmath_hash(fn, out.ctypes.data_as(C.POINTER(C.c_uint64)), threads or min(16, os.cpu_count() or 1))
+    return out
+
+
+def ref_unary_cr(x, kind):
+    x = np.ascontiguousarray(x, F)
+    y = np.empty_like(x)
+    orc().orc_ref_unary_cr(_p(x), x.size, kind, _p(y))
+    return y
+
+
+def ref_silu_mul_cr(g, u):
+    g, u = np.ascontiguousarray(g, F), np.ascontiguousarray(u, F)
+    y = np.empty_like(g)
+    orc().orc_ref_silu_mul_cr(_p(g), _p(u), g.size, _p(y))
+    return y
+
+
+def ref_conv_cr(state, x, w, silu=True):
+    state, x, w = (np.ascontiguousarray(t, F) for t in (state, x, w))
+    y = np.empty(x.size, F)
+    ns = np.empty(3 * x.size, F)
+    orc().orc_ref_conv_cr(_p(state), _p(x), _p(w), x.size, 1 if silu else 0, _p(y), _p(ns))
+    return y, ns
+
+
+def ref_gdn_cr(state, q, k, v, g, beta, hv, hk, scale, threads: int = 1):
+    """The reference DeltaNet step (gemvq_ref.h:360-397) with the correctly rounded exp: g is the log decay, beta
+    the gate. Returns y and the new state."""
+    st = np.ascontiguousarray(state, F).copy()
+    args = [np.ascontiguousarray(t, F) for t in (q, k, v, g, beta)]
+    y = np.empty(hv * 128, F)
+    orc().orc_ref_gdn_cr_mt(_p(st), *[_p(t) for t in args], hv, hk, scale, _p(y), threads)
+    return y, st
+
+
+def ref_attn_cr(q, kc, vc, nh, nkvh, hd, n_kv, scale, threads: int = 1):
+    q = np.ascontiguousarray(q, F)
+    out = np.empty(nh * hd, F)
+    kc, vc = np.ascontiguousarray(kc, np.uint16), np.ascontiguousarray(vc, np.uint16)
+    orc().orc_ref_attn_cr_mt(_p(q), _p(kc), _p(vc), nh, nkvh, hd, n_kv, scale, _p(out), threads)
+    return out
+
+
 def dequant_row_q6_K(row: np.ndarray, cols: int) -> np.ndarray:
     y = np.empty(cols, F)
     orc().orc_dequant_row_q6_K(_p(np.ascontiguousarray(row, np.uint8)), cols, _p(y))
@@ -266,7 +344,7 @@ def f2h(x: np.ndarray) -> np.ndarray:
     return np.array([o.orc_float_to_half(float(v)) for v in np.asarray(x, F).ravel()], np.uint16)
 
 
-MODE_CANONICAL, MODE_REFERENCE = 0, 1
+MODE_CANONICAL, MODE_REFERENCE, MODE_REFERENCE_LIBM = 0, 1, 2
 FAULT_ATTN_RESIDUAL, FAULT_QGATE_SWAP, FAULT_GATES_SWAP, FAULT_FFN_SWAP, FAULT_ROPE_K, FAULT_SSM_RESIDUAL = range(1, 7)
 
 

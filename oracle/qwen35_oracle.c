@@ -5,9 +5,11 @@
  * and attention run token by token in order. Two arithmetics:
  *   ORC_MODE_CANONICAL  the arithmetic the GPU reproduces bit for bit (gemvq_oracle.c's canonical ops);
  *   ORC_MODE_REFERENCE  the reference's CPU arithmetic: gemvq_ref.h's sequential FP32 GEMV rows, sums of squares in
- *                       double, libm exp/log (gemvq_ref.h:94-358), composed as ggml's graph composes them
- *                       (ggml-xrt.cpp:1944-1992: L2_NORM of q and k, SIGMOID(beta), MUL(SOFTPLUS(ADD(alpha, dt)),
- *                       a), RMS_NORM rows of 128 -> MUL weight -> MUL SILU(z)); attention as orc_ref_attn. */
+ *                       double (gemvq_ref.h:94-358), composed as ggml's graph composes them (ggml-xrt.cpp:1944-1992:
+ *                       L2_NORM of q and k, SIGMOID(beta), MUL(SOFTPLUS(ADD(alpha, dt)), a), RMS_NORM rows of 128 ->
+ *                       MUL weight -> MUL SILU(z)); attention as orc_ref_attn; exp and log correctly rounded
+ *                       (orc_crmath.c), the functions the GPU's reference-arithmetic mode evaluates;
+ *   ORC_MODE_REFERENCE_LIBM  the same with the host libm's expf / logf, as the compiled reference path calls them. */
 #include "qwen35_oracle.h"
 #include "gemvq_oracle.h"
 #include "orc_fast.h"
@@ -157,7 +159,7 @@ void orc_model_destroy(void * mp) {
 
 int orc_model_set_mode(void * mp, int mode) {
     orc_model * m = (orc_model *)mp;
-    if (!m || (mode != ORC_MODE_CANONICAL && mode != ORC_MODE_REFERENCE)) return -1;
+    if (!m || (mode != ORC_MODE_CANONICAL && mode != ORC_MODE_REFERENCE && mode != ORC_MODE_REFERENCE_LIBM)) return -1;
     m->mode = mode;
     return 0;
 }
@@ -198,7 +200,8 @@ int orc_model_reset(void * mp) {
  * all tokens; rows split over the threads (a row's result does not depend on the split). */
 static void gemm(orc_model * m, const orc_t * w, const float * X, int xs, int T, float * Y, int ys) {
     const int rows = w->rows, cols = w->cols, fmt = w->type;
-    if (m->mode == ORC_MODE_REFERENCE && !orc_fast_supported(fmt)) {
+    const int fmode = m->mode == ORC_MODE_CANONICAL ? 0 : 1;  /* orc_fast: 0 canonical rows, 1 sequential FP32 rows */
+    if (fmode && !orc_fast_supported(fmt)) {
         for (int t = 0; t < T; ++t) orc_ref_gemv(fmt, (const uint8_t *)w->data, X + (size_t)t * xs, rows, cols, Y + (size_t)t * ys, NULL);
         return;
     }
@@ -214,7 +217,7 @@ static void gemm(orc_model * m, const orc_t * w, const float * X, int xs, int T,
     for (int cidx = 0; cidx < nchunks; ++cidx) {
         const int r0 = cidx * chunk, r1 = r0 + chunk < rows ? r0 + chunk : rows;
         float tmp[CHUNK * 16];
-        orc_fast_rows_multi(m->mode, fmt, (const uint8_t *)w->data, ap, T, r0, r1, tmp, 16);
+        orc_fast_rows_multi(fmode, fmt, (const uint8_t *)w->data, ap, T, r0, r1, tmp, 16);
         for (int t = 0; t < T; ++t) memcpy(Y + (size_t)t * ys + r0, tmp + 16 * t, sizeof(float) * (size_t)(r1 - r0));
     }
     for (int t = 0; t < T; ++t) orc_act_free(&acts[t]);
@@ -222,13 +225,14 @@ static void gemm(orc_model * m, const orc_t * w, const float * X, int xs, int T,
 
 /* RMS norm of one row with weight (canonical pairwise tree, or ggml's double sum of float squares). */
 static void rmsnorm(const orc_model * m, const float * x, const orc_t * w, int n, float * y) {
-    if (m->mode == ORC_MODE_REFERENCE) orc_ref_rownorm(x, (const float *)w->data, n, 1, m->c.eps, 0, y);
+    if (m->mode != ORC_MODE_CANONICAL) orc_ref_rownorm(x, (const float *)w->data, n, 1, m->c.eps, 0, y);
     else orc_rownorm(x, (const float *)w->data, n, 1, 0, m->c.eps, 0, y);
 }
 
 static float unary1(const orc_model * m, float v, int kind) {
     float y;
-    if (m->mode == ORC_MODE_REFERENCE) orc_ref_unary(&v, 1, kind, &y);
+    if (m->mode == ORC_MODE_REFERENCE) orc_ref_unary_cr(&v, 1, kind, &y);
+    else if (m->mode == ORC_MODE_REFERENCE_LIBM) orc_ref_unary(&v, 1, kind, &y);
     else orc_unary(&v, 1, kind, &y);
     return y;
 }
@@ -240,7 +244,7 @@ static void attn_layer(orc_model * m, int il, int T, int pos0) {
     const orc_qw_config * c = &m->c;
     orc_layer * L = &m->layers[il];
     const int E = c->n_embd, hd = c->head_dim, nh = c->n_head, nkv = c->n_head_kv, B = m->big;
-    const int ref = m->mode == ORC_MODE_REFERENCE;
+    const int ref = m->mode != ORC_MODE_CANONICAL, cr = m->mode == ORC_MODE_REFERENCE;
     float * qg = m->b1, * kk = m->b2, * vv = m->b3;
     gemm(m, &L->wq, m->xn, B, T, qg, B);
     gemm(m, &L->wk, m->xn, B, T, kk, B);
@@ -275,7 +279,8 @@ static void attn_layer(orc_model * m, int il, int T, int pos0) {
             vc[i] = orc_float_to_half(vt[i]);
         }
         const float scale = 1.0f / sqrtf((float)hd);
-        if (ref) orc_ref_attn_mt(qn, m->kcache[il], m->vcache[il], nh, nkv, hd, pos + 1, scale, att, m->n_threads);
+        if (cr) orc_ref_attn_cr_mt(qn, m->kcache[il], m->vcache[il], nh, nkv, hd, pos + 1, scale, att, m->n_threads);
+        else if (ref) orc_ref_attn_mt(qn, m->kcache[il], m->vcache[il], nh, nkv, hd, pos + 1, scale, att, m->n_threads);
         else orc_attn_mt(qn, m->kcache[il], m->vcache[il], nh, nkv, hd, pos + 1, scale, att, m->n_threads);
         /* output gate: sigmoid(gate) * att */
         float * o = xo + (size_t)t * B;
@@ -302,7 +307,7 @@ static void gdn_layer(orc_model * m, int il, int T) {
     orc_layer * L = &m->layers[il];
     const int E = c->n_embd, S = c->ssm_head_dim, hk = c->ssm_k_heads, hv = c->ssm_v_heads, B = m->big;
     const int ch = conv_channels(c);
-    const int ref = m->mode == ORC_MODE_REFERENCE;
+    const int ref = m->mode != ORC_MODE_CANONICAL, cr = m->mode == ORC_MODE_REFERENCE;
     float * qkv = m->b1, * z = m->b2, * ba = m->b3;  /* ba row: beta [hv] then alpha at + 64 */
     gemm(m, &L->qkv, m->xn, B, T, qkv, B);
     gemm(m, &L->z, m->xn, B, T, z, B);
@@ -316,7 +321,9 @@ static void gdn_layer(orc_model * m, int il, int T) {
         const float * bt = ba + (size_t)t * B, * at = bt + (hv + 63) / 64 * 64;
         const float * braw = m->fault == ORC_FAULT_GATES_SWAP ? at : bt, * araw = m->fault == ORC_FAULT_GATES_SWAP ? bt : at;
         float * yt = y + (size_t)t * B;
-        if (ref) {
+        if (cr) {
+            orc_ref_conv_cr(m->conv_state[il], qkv + (size_t)t * B, (const float *)L->conv1d.data, ch, 1, cy, ns);
+        } else if (ref) {
             orc_ref_conv(m->conv_state[il], qkv + (size_t)t * B, (const float *)L->conv1d.data, ch, 1, cy, ns);
         } else {
             orc_conv(m->conv_state[il], qkv + (size_t)t * B, (const float *)L->conv1d.data, ch, 1, cy, ns);
@@ -334,8 +341,12 @@ static void gdn_layer(orc_model * m, int il, int T) {
                 g[h] = unary1(m, araw[h] + dt[h], 3) * av[h];
             }
             float * yr = (float *)malloc(sizeof(float) * (size_t)hv * S);
-            orc_ref_gdn_mt(m->ssm_state[il], qn, kn, cy + 2 * hk * S, g, be, hv, hk, 1.0f / sqrtf((float)S), yr, NULL, NULL,
-                           m->n_threads);
+            if (cr)
+                orc_ref_gdn_cr_mt(m->ssm_state[il], qn, kn, cy + 2 * hk * S, g, be, hv, hk, 1.0f / sqrtf((float)S), yr,
+                                  m->n_threads);
+            else
+                orc_ref_gdn_mt(m->ssm_state[il], qn, kn, cy + 2 * hk * S, g, be, hv, hk, 1.0f / sqrtf((float)S), yr, NULL,
+                               NULL, m->n_threads);
             orc_ref_rownorm(yr, wn, S, hv, c->eps, 0, yt);
             for (int i = 0; i < hv * S; ++i) yt[i] = yt[i] * unary1(m, z[(size_t)t * B + i], 1);
             free(qn); free(kn); free(g); free(be); free(yr);
@@ -378,7 +389,9 @@ static int run_chunk(orc_model * m, const int32_t * tok, int T, int pos0, int lo
         for (int t = 0; t < T; ++t) {
             float * g = m->b1 + (size_t)t * B, * u = m->b2 + (size_t)t * B, * o = m->b3 + (size_t)t * B;
             if (m->mode == ORC_MODE_REFERENCE) {
-                for (int i = 0; i < c->n_ff; ++i) o[i] = g[i] / (1.0f + expf(-g[i])) * u[i];  /* gemvq_ref.h:303-307 */
+                orc_ref_silu_mul_cr(g, u, c->n_ff, o);  /* gemvq_ref.h:303-307 */
+            } else if (m->mode == ORC_MODE_REFERENCE_LIBM) {
+                for (int i = 0; i < c->n_ff; ++i) o[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
             } else {
                 orc_silu_mul(g, u, c->n_ff, 0, o);
             }

@@ -29,8 +29,9 @@ typedef struct {
 void * orc_model_create(const orc_qw_config * cfg, const orc_tensor_desc * table, int n_tensors, const uint8_t * blob,
                         int n_threads);
 /* Arithmetic of the following tokens (the states carry over): the canonical one the GPU reproduces bit for bit
- * (default), or the reference's sequential FP32 rows, double sums of squares and libm exp/log. */
-enum { ORC_MODE_CANONICAL = 0, ORC_MODE_REFERENCE = 1 };
+ * (default); the reference's sequential FP32 rows and double sums of squares with correctly rounded exp / log (the
+ * GPU's reference-arithmetic mode reproduces it bit for bit); or the same with the host libm's expf / logf. */
+enum { ORC_MODE_CANONICAL = 0, ORC_MODE_REFERENCE = 1, ORC_MODE_REFERENCE_LIBM = 2 };
 int orc_model_set_mode(void * model, int mode);
 /* Planted wiring mistakes, for tests that show the independent checks catch them (0: none). */
 enum {
