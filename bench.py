@@ -143,7 +143,8 @@ def cpu_baseline(blob, cfg, tokens, pos0: int, max_tokens: int, seconds: float, 
         os.sched_setaffinity(0, old)
     return {"value": round(n / dt, 4), "unit": "tokens/s", "cores": len(cpus), "kind": "port",
             "arithmetic": "the reference's CPU arithmetic (gemvq_ref.h: int8 block dot products, each row summed "
-                          "sequentially in FP32, sums of squares in double, libm exp); the int8 dots in AVX2",
+                          "sequentially in FP32, sums of squares in double; exp / log correctly rounded, as the "
+                          "GPU's reference mode evaluates them); the int8 dots in AVX2",
             "cpu": cpu_info(),
             "sample": f"{n} decode steps of the same 9B-shape model at positions {pos0 + 1}..{pos0 + n} with the ids "
                       f"the GPU generated there, from an empty state (a step's work depends on its position, not on "
@@ -422,6 +423,8 @@ def main() -> int:
     ap.add_argument("--threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--profile-reps", type=int, default=9,
                     help="repetitions of the per-kernel pass (each launch's median duration is reported)")
+    ap.add_argument("--ref-steps", type=int, default=32,
+                    help="decode steps timed in the reference arithmetic after the profile (0: skip)")
     ap.add_argument("--layers", type=int, default=32, help="(testing) fewer layers; the reported line is then invalid")
     ap.add_argument("--direct", action="store_true",
                     help="plain stream launches instead of graph replays (for tracing tools); slower per step")
@@ -448,7 +451,7 @@ def main() -> int:
               f"(the multi-GPU sharding is a design note, not code)", file=sys.stderr)
         return 2
 
-    slack = args.profile_reps + 16
+    slack = args.profile_reps + args.ref_steps + 20
     cfg = Q.Config(n_layer=args.layers, n_ctx=args.prompt + args.warmup + args.steps + slack)
     t = time.perf_counter()
     blob = Q.generate(cfg, seed=0, threads=args.threads)
@@ -525,6 +528,24 @@ def main() -> int:
     dom_name, dom = max(agg.items(), key=lambda kv: kv[1]["us"])
     achieved = dom["bytes"] / dom["us"] / 1e3  # GB/s
     traffic, traffic_src = measured_traffic(dom_name)
+    ref = None
+    if args.ref_steps > 0 and not args.direct:
+        # the same model continuing in the reference arithmetic (gemvq_set_arith): bit-identical to the reference's
+        # CPU path, not the timed workload
+        m.set_arith(gq.ARITH_REFERENCE)
+        m.step(2)  # captures the graph
+        m.sync()
+        t = time.perf_counter()
+        m.step(args.ref_steps)
+        m.sync()
+        t_ref = time.perf_counter() - t
+        ref = {"tokens_per_s": round(args.ref_steps / t_ref, 1), "steps": args.ref_steps,
+               "vs_canonical": round(args.ref_steps / t_ref / tok_s, 3),
+               "what": "the same decode in the reference arithmetic (the reference CPU path's sequential FP32 rows, "
+                       "double norm sums, in-order DeltaNet dots, double-sum attention, correctly rounded exp / "
+                       "log; its tokens equal the CPU reference decoder's bit for bit), graph replays after the "
+                       "profile pass"}
+        log(f"reference arithmetic: {ref['tokens_per_s']} tok/s ({ref['vs_canonical']} of the canonical rate)")
     m.close()
 
     cpu = None
@@ -559,6 +580,7 @@ def main() -> int:
             "token_device_us": round(tot_us, 1),
             "launches_per_token": len(stats),
             "prompt_prefill": prefill,
+            "reference_arithmetic": ref,
         },
         "roofline": {
             "bound": "hbm",

@@ -154,7 +154,8 @@ struct gqg_backend {
     std::map<std::string, KvPair> kv_layers;  // layer suffix -> device cache
     struct Io { const void * host; uint32_t off; size_t floats; };
     struct Plan {
-        std::vector<uint64_t> key;
+        std::vector<uint64_t> sig;  // the split's structural signature (signature_of) and its hash
+        uint64_t hash = 0;
         std::vector<uint32_t> words;
         std::vector<Io> in, out;  // host data copied in before, results copied back after the run
         std::vector<std::pair<const int64_t *, const int32_t *>> pos_checks;  // KV row == position
@@ -266,53 +267,17 @@ bool rope_table(gqg_backend * b, int n_dims, float base, int64_t n_ctx, uint32_t
     return true;
 }
 
-// ---- the analysis of a split (xrt_qc_build_plan's roles) ----
-
-struct Analysis {
-    std::unordered_map<const gqg_tensor *, int> index, readers, last_use;
-    std::unordered_set<const gqg_tensor *> skip;
-    struct Conv { const gqg_tensor * get_rows, * concat, * cpy, * conv, * x; };
-    std::unordered_map<const gqg_tensor *, Conv> conv_of_silu;          // SILU node -> its conv
-    std::unordered_map<const gqg_tensor *, const gqg_tensor *> conv_src;  // qkv GEMV -> the conv's SILU
-    struct Gdn {
-        const gqg_tensor * get_rows = nullptr, * cpy = nullptr;
-        bool l2 = false;
-        float l2_eps = 0, rms_eps = 0;
-        const gqg_tensor * out = nullptr, * w = nullptr, * z = nullptr;  // gated norm (z: silu(z) with z_silu)
-        bool z_silu = false;
-        const gqg_tensor * alpha = nullptr, * beta = nullptr, * dt = nullptr, * a = nullptr;
-    };
-    std::unordered_map<const gqg_tensor *, Gdn> gdns;
-    std::unordered_map<const gqg_tensor *, const gqg_tensor *> silu_epilog;  // GEMV -> the SILU node it writes
-    std::unordered_map<const gqg_tensor *, std::pair<const gqg_tensor *, const gqg_tensor *>> swiglus;
-    std::unordered_set<const gqg_tensor *> add_src, defer_ok;
-    struct Attn {
-        const gqg_tensor * qfull, * kcur, * vcur, * qn, * kn, * fa, * kstore, * vstore, * pos, * kidx;
-        float eps, scale, base;
-        int n_rot, n_head, n_head_kv, head_dim;
-        std::string layer;
-    };
-    std::unordered_map<const gqg_tensor *, Attn> attn;  // gated output MUL -> its attention
-    int readers_of(const gqg_tensor * t) const {
-        const auto it = readers.find(t);
-        return it == readers.end() ? 0 : it->second;
-    }
-};
+// ---- the fusion plan of a split ----
+//
+// A reader index of the split (for every data root, the non-view nodes that read it, through which operand), then
+// one pass over the nodes from the last to the first. Each fused form is anchored at the node that consumes its
+// chain: the conv's SSM_CONV, the DeltaNet step, the attention, the GLU of a SwiGLU pair, a GEMV (for the ADD that
+// reads it), a norm (for the GEMVs that read it). Walking backwards, every consumer has settled what it absorbs
+// before its producers are visited, so a GEMV or a norm decides its own fusion against the final set of absorbed
+// nodes. The conditions are the ones the reference kernel's fused forms need (gemvqc16.h; the reference's planner
+// decides the same forms, ggml-xrt.cpp:1813-2110).
 
 bool unfused_output(const gqg_tensor * t) { return (t->flags & (GQG_FLAG_OUTPUT | GQG_FLAG_SPLIT_OUTPUT)) == 0; }
-
-// The single non-view reader of t's data in the split, or nullptr.
-const gqg_tensor * single_reader(const gqg_cgraph * g, const Analysis & A, const gqg_tensor * t) {
-    const auto it = A.readers.find(t);
-    if (it == A.readers.end() || it->second != 1 || !unfused_output(t)) return nullptr;
-    for (int i = 0; i < g->n_nodes; ++i) {
-        const gqg_tensor * m = g->nodes[i];
-        if (is_view(m)) continue;
-        for (const gqg_tensor * s : m->src)
-            if (s && root_of(s) == t) return m;
-    }
-    return nullptr;
-}
 
 // Through views to the computing node.
 const gqg_tensor * through_views(const gqg_tensor * t) {
@@ -320,296 +285,422 @@ const gqg_tensor * through_views(const gqg_tensor * t) {
     return t;
 }
 
-bool analyse(const gqg_cgraph * g, Analysis & A, std::string & err) {
-    const int n = g->n_nodes;
-    for (int i = 0; i < n; ++i) A.index[g->nodes[i]] = i;
-    for (int i = 0; i < n; ++i) {
-        const gqg_tensor * m = g->nodes[i];
-        if (is_view(m)) continue;
-        std::unordered_set<const gqg_tensor *> roots;
-        for (const gqg_tensor * s : m->src)
-            if (s) roots.insert(root_of(s));
-        for (const gqg_tensor * r : roots) {
-            ++A.readers[r];
-            A.last_use[r] = i;
-        }
-    }
-    const std::unordered_set<const gqg_tensor *> nodes(g->nodes, g->nodes + n);
-    const auto rd = [&](const gqg_tensor * t) {
-        const auto it = A.readers.find(t);
-        return it == A.readers.end() ? 0 : it->second;
+struct ReaderIndex {
+    struct Read {
+        const gqg_tensor * node;  // the reading node
+        int slot;                 // its operand index
+        const gqg_tensor * via;   // the operand as the node names it (the root or a view of it)
     };
-    const auto single = [&](const gqg_tensor * t) { return single_reader(g, A, t); };
-    // conv: SILU(SSM_CONV(CONCAT(state rows, qkv^T), kernel)) and the CPY of the window's last 3 columns
-    for (int i = 0; i < n; ++i) {
-        const gqg_tensor * c = g->nodes[i];
-        if (c->op != GQG_OP_SSM_CONV) continue;
-        Analysis::Conv cv{};
-        cv.conv = c;
-        cv.concat = c->src[0];
-        cv.get_rows = cv.concat && cv.concat->op == GQG_OP_CONCAT ? rs_rows(cv.concat->src[0]) : nullptr;
-        cv.x = cv.concat ? cv.concat->src[1] : nullptr;
-        const gqg_tensor * silu = nullptr;
-        for (int j = 0; j < n; ++j) {
-            const gqg_tensor * m = g->nodes[j];
-            if (m->op == GQG_OP_CPY && m->src[0]->view_src == cv.concat && in_buf(m->src[1], GQG_BUF_RS)) cv.cpy = m;
-            if (unary_kind(m) == 1 && m->src[0] == c) silu = m;
-        }
-        if (!cv.get_rows || !cv.cpy || cv.cpy->src[0]->view_offs != 4 || !silu || !f32_weight(c->src[1]) ||
-            c->ne[0] % 16 || cv.concat->ne[0] != 4 || cv.concat->ne[1] != c->ne[0]) {
-            err = std::string("unexpected conv graph around ") + c->name;
-            return false;
-        }
-        A.conv_of_silu[silu] = cv;
-        A.skip.insert({cv.get_rows, cv.concat, cv.cpy, c});
-        const gqg_tensor * x = root_of(cv.x);
-        if (x->op == GQG_OP_MUL_MAT && nodes.count(x) && rd(x) == 1 && unfused_output(x) && x->ne[0] == c->ne[0])
-            A.conv_src[x] = silu;
-    }
-    // GDN: the state rows, the new state's CPY, L2 norms of q and k, the gated norm, the gates
-    for (int i = 0; i < n; ++i) {
-        const gqg_tensor * node = g->nodes[i];
-        if (node->op != GQG_OP_GATED_DELTA_NET) continue;
-        Analysis::Gdn p;
-        p.get_rows = rs_rows(node->src[5]);
-        const int64_t hv = node->src[2]->ne[1];
-        const size_t y_bytes = size_t(hv) * HEAD * 4;
-        for (int j = 0; j < n; ++j) {
-            const gqg_tensor * m = g->nodes[j];
-            if (m->op == GQG_OP_CPY && m->src[0]->view_src == node && m->src[0]->view_offs == y_bytes &&
-                in_buf(m->src[1], GQG_BUF_RS))
-                p.cpy = m;
-        }
-        if (!p.get_rows || !p.cpy) {
-            err = std::string("unexpected GDN graph around ") + node->name;
-            return false;
-        }
-        A.skip.insert({p.get_rows, p.cpy});
-        const gqg_tensor * q = node->src[0], * k = node->src[1];
-        if (q->op == GQG_OP_L2_NORM && k->op == GQG_OP_L2_NORM && single(q) == node && single(k) == node &&
-            contiguous(q->src[0]) && contiguous(k->src[0]) && q->op_params[0] == k->op_params[0]) {
-            p.l2 = true;
-            p.l2_eps = pf(q, 0);
-            A.skip.insert({q, k});
-        }
-        // y -> RMS_NORM rows of 128 -> MUL weight -> MUL SILU(z); the node is read by that norm and the CPY only
-        const gqg_tensor * r = nullptr;
-        for (int j = 0; j < n; ++j) {
-            const gqg_tensor * m = g->nodes[j];
-            if (m->op == GQG_OP_RMS_NORM && root_of(m->src[0]) == node && m->src[0]->view_offs == 0 && m->ne[0] == HEAD &&
-                nel(m) == nel(node->src[2]))
-                r = m;
-        }
-        const gqg_tensor * m1 = r ? single(r) : nullptr;
-        const gqg_tensor * m2 = m1 && m1->op == GQG_OP_MUL && m1->src[0] == r ? single(m1) : nullptr;
-        const gqg_tensor * w = m1 ? m1->src[1] : nullptr;
-        const gqg_tensor * sl = m2 && m2->op == GQG_OP_MUL && m2->src[0] == m1 ? m2->src[1] : nullptr;
-        if (r && rd(node) == 2 && w && f32_weight(w) && nel(w) == HEAD && sl && unary_kind(sl) == 1 && single(sl) == m2 &&
-            nel(sl) == nel(m2) && nel(m2) == nel(r) && contiguous(sl->src[0]) && contiguous(m2)) {
-            p.out = m2;
-            p.w = w;
-            p.rms_eps = pf(r, 0);
-            A.skip.insert({r, m1, m2});
-            // z = silu(GEMV): the GEMV writes silu(z) once (its SiLU epilog) and the step multiplies by it directly
-            const gqg_tensor * zm = root_of(sl->src[0]);
-            if (zm->op == GQG_OP_MUL_MAT && nodes.count(zm) && rd(zm) == 1 && unfused_output(zm) &&
-                sl->src[0]->data == zm->data && nel(zm) == nel(sl)) {
-                A.silu_epilog[zm] = sl;
-                p.z = sl;
-                p.z_silu = true;
-            } else {
-                p.z = sl->src[0];
-            }
-            A.skip.insert(sl);
-        }
-        // gates: SIGMOID(beta raw) and MUL(SOFTPLUS(ADD(alpha raw, dt)), a), each read once; dt and a weights
-        const gqg_tensor * sg = root_of(node->src[4]), * ml = root_of(node->src[3]);
-        const auto w_hv = [&](const gqg_tensor * x) { return x && f32_weight(x) && nel(x) == hv; };
-        const auto raw = [&](const gqg_tensor * x) { return x->type == GQG_TYPE_F32 && contiguous(x) && nel(x) == hv; };
-        if (unary_kind(sg) == 2 && single(sg) == node && ml->op == GQG_OP_MUL && single(ml) == node && raw(sg->src[0])) {
-            const int si = ml->src[0]->op == GQG_OP_UNARY ? 0 : 1;
-            const gqg_tensor * sp = ml->src[si], * a = ml->src[1 - si];
-            const gqg_tensor * ad = unary_kind(sp) == 3 && single(sp) == ml ? sp->src[0] : nullptr;
-            if (ad && ad->op == GQG_OP_ADD && single(ad) == sp && w_hv(a)) {
-                const int di = w_hv(ad->src[1]) ? 1 : 0;
-                if (w_hv(ad->src[di]) && raw(ad->src[1 - di])) {
-                    p.beta = sg->src[0];
-                    p.alpha = ad->src[1 - di];
-                    p.dt = ad->src[di];
-                    p.a = a;
-                    A.skip.insert({sg, ml, sp, ad});
-                }
-            }
-        }
-        A.gdns[node] = p;
-    }
-    // one-token gated attention ending in MUL(RESHAPE(FLASH_ATTN_EXT), SIGMOID(CONT(gate rows of q)))
-    for (int i = 0; i < n; ++i) {
-        const gqg_tensor * fa = g->nodes[i];
-        if (fa->op != GQG_OP_FLASH_ATTN_EXT) continue;
-        Analysis::Attn at{};
-        at.fa = fa;
-        at.scale = pf(fa, 0);
-        const gqg_tensor * qr = through_views(fa->src[0]);  // ROPE(MUL(RMS_NORM(q rows), qn))
-        const gqg_tensor * kc = root_of(fa->src[1]), * vc = root_of(fa->src[2]);
-        const auto chain = [&](const gqg_tensor * rope, const gqg_tensor *& raw, const gqg_tensor *& w, float & eps) {
-            if (!rope || rope->op != GQG_OP_ROPE) return false;
-            const gqg_tensor * mu = rope->src[0];
-            if (!mu || mu->op != GQG_OP_MUL || !mu->src[0] || mu->src[0]->op != GQG_OP_RMS_NORM || !f32_weight(mu->src[1]))
-                return false;
-            raw = mu->src[0]->src[0];
-            w = mu->src[1];
-            eps = pf(mu->src[0], 0);
-            return true;
-        };
-        const gqg_tensor * qrows = nullptr, * krows = nullptr;
-        float qeps = 0, keps = 0;
-        bool ok = in_buf(kc, GQG_BUF_KV) && in_buf(vc, GQG_BUF_KV) && chain(qr, qrows, at.qn, qeps);
-        // the stores of k and v into the caches this attention reads
-        for (int j = 0; ok && j < n; ++j) {
-            const gqg_tensor * m = g->nodes[j];
-            if (m->op != GQG_OP_SET_ROWS) continue;
-            if (root_of(m->src[0]) == kc) at.kstore = m;
-            if (root_of(m->src[0]) == vc) at.vstore = m;
-        }
-        ok = ok && at.kstore && at.vstore && chain(through_views(at.kstore->src[1]), krows, at.kn, keps) && qeps == keps;
-        if (ok) {
-            at.eps = qeps;
-            at.qfull = root_of(qrows);
-            at.kcur = root_of(krows);
-            at.vcur = root_of(at.vstore->src[1]);
-            at.head_dim = int(qrows->ne[0]);
-            at.n_head = int(qrows->ne[1]);
-            at.n_head_kv = int(krows->ne[1] > 1 ? krows->ne[1] : nel(krows) / at.head_dim);
-            at.n_rot = qr->op_params[1];
-            at.base = pf(qr, 5);
-            at.pos = qr->src[1];
-            at.kidx = at.kstore->src[2];
-            const gqg_tensor * kr = through_views(at.kstore->src[1]);
-            ok = at.qfull->op == GQG_OP_MUL_MAT && at.kcur->op == GQG_OP_MUL_MAT && at.vcur->op == GQG_OP_MUL_MAT &&
-                 qrows->view_offs == 0 && qrows->nb[1] == size_t(2 * at.head_dim) * 4 && qrows->nb[0] == 4 &&
-                 nel(at.qfull) == int64_t(2) * at.head_dim * at.n_head && nel(at.vcur) == nel(at.kcur) &&
-                 qr->op_params[2] == GQG_ROPE_TYPE_NEOX && kr->op_params[2] == GQG_ROPE_TYPE_NEOX &&
-                 kr->op_params[1] == at.n_rot && pf(kr, 5) == at.base && kr->src[1] == at.pos && pf(qr, 6) == 1.0f &&
-                 pf(qr, 7) == 0.0f && pf(qr, 8) == 1.0f && at.pos->type == GQG_TYPE_I32 && nel(at.pos) == 1 &&
-                 at.kidx->type == GQG_TYPE_I64 && nel(at.kidx) == 1 && at.vstore->src[2] == at.kidx;
-        }
-        // the gate: MUL(view of the output, SIGMOID(CONT(q rows at offset head_dim))) reading the output alone
-        const gqg_tensor * mul = nullptr;
-        for (int j = 0; ok && j < n; ++j) {
-            const gqg_tensor * m = g->nodes[j];
-            if (m->op == GQG_OP_MUL && root_of(m->src[0]) == fa) mul = m;
-        }
-        const gqg_tensor * sg = mul ? mul->src[1] : nullptr;
-        const gqg_tensor * gv = sg && unary_kind(sg) == 2 && sg->src[0]->op == GQG_OP_CONT ? sg->src[0]->src[0] : nullptr;
-        ok = ok && mul && gv && root_of(gv) == at.qfull && gv->view_offs == size_t(at.head_dim) * 4 &&
-             gv->nb[1] == size_t(2 * at.head_dim) * 4 && nel(mul) == int64_t(at.n_head) * at.head_dim &&
-             A.readers[fa] == 1 && unfused_output(fa);
-        if (!ok) {
-            err = std::string("unexpected attention graph around ") + fa->name;
-            return false;
-        }
-        const std::string kn = root_of(at.kstore->src[0])->name;
-        at.layer = kn.size() > 7 ? kn.substr(7) : kn;  // cache_k_l<N>
-        A.attn[mul] = at;
-        const gqg_tensor * kr = through_views(at.kstore->src[1]);
-        const gqg_tensor * fused[] = {qr, qr->src[0], qr->src[0]->src[0], kr, kr->src[0], kr->src[0]->src[0],
-                                      at.kstore, at.vstore, fa, sg, sg->src[0]};
-        A.skip.insert(std::begin(fused), std::end(fused));
-    }
-    // SwiGLU pairs: GLU(gate, up) of two GEMVs on the same row, each read by the GLU alone
-    for (int i = 0; i < n; ++i) {
-        const gqg_tensor * m = g->nodes[i];
-        if (m->op != GQG_OP_GLU || m->op_params[0] != GQG_GLU_SWIGLU || m->op_params[1] != 0) continue;
-        const gqg_tensor * gt = m->src[0], * ut = m->src[1];
-        const auto fusable = [&](const gqg_tensor * x) {
-            return x && x->op == GQG_OP_MUL_MAT && nodes.count(x) && rd(x) == 1 && unfused_output(x);
-        };
-        if (fusable(gt) && fusable(ut) && gt->src[1]->data == ut->src[1]->data && gt->src[0]->ne[0] == ut->src[0]->ne[0] &&
-            gt->ne[0] == ut->ne[0] && gt->ne[0] == m->ne[0] && gt->src[0]->type == ut->src[0]->type) {
-            A.swiglus[m] = {gt, ut};
-            A.skip.insert({gt, ut});
-        }
-    }
-    // ADD epilogs: a GEMV read only by an ADD of the same length whose other operand exists before the GEMV
-    for (int i = 0; i < n; ++i) {
-        const gqg_tensor * add = g->nodes[i];
-        if (add->op != GQG_OP_ADD || A.skip.count(add)) continue;
-        for (int s = 0; s < 2; ++s) {
-            const gqg_tensor * m = root_of(add->src[s]), * r = root_of(add->src[1 - s]);
-            const auto im = A.index.find(m), ir = A.index.find(r);
-            if (m->op == GQG_OP_MUL_MAT && im != A.index.end() && !A.skip.count(m) && !A.silu_epilog.count(m) &&
-                !A.conv_src.count(m) && rd(m) == 1 && unfused_output(m) && add->src[s]->data == m->data &&
-                nel(m) == nel(add) && m->ne[0] >= 256 && m->ne[0] % 16 == 0 &&
-                (ir == A.index.end() || ir->second < im->second)) {
-                A.add_src.insert(m);
-                break;
+    std::unordered_map<const gqg_tensor *, std::vector<Read>> reads;  // data root -> its reads, in node order
+    std::unordered_map<const gqg_tensor *, int> nodes_reading;        // data root -> distinct nodes reading it
+    std::unordered_map<const gqg_tensor *, int> at;                   // node -> position in the split
+
+    void build(const gqg_cgraph * g) {
+        for (int i = 0; i < g->n_nodes; ++i) at[g->nodes[i]] = i;
+        for (int i = 0; i < g->n_nodes; ++i) {
+            const gqg_tensor * m = g->nodes[i];
+            if (is_view(m)) continue;
+            for (int k = 0; k < GQG_MAX_SRC; ++k) {
+                if (!m->src[k]) continue;
+                const gqg_tensor * r = root_of(m->src[k]);
+                auto & v = reads[r];
+                bool seen = false;
+                for (const Read & x : v) seen = seen || x.node == m;
+                if (!seen) ++nodes_reading[r];
+                v.push_back({m, k, m->src[k]});
             }
         }
     }
-    // norm rows read only by GEMVs of this split stay unwritten (deferred RMSNORM)
-    std::unordered_map<const gqg_tensor *, bool> only_gemv;
-    for (int i = 0; i < n; ++i) {
-        const gqg_tensor * m = g->nodes[i];
-        if (is_view(m)) continue;
-        for (const gqg_tensor * s : m->src) {
-            if (!s) continue;
-            const gqg_tensor * r = root_of(s);
-            const bool ok = m->op == GQG_OP_MUL_MAT && m->src[1] == s;
-            const auto it = only_gemv.find(r);
-            only_gemv[r] = (it == only_gemv.end() || it->second) && ok;
-        }
+    int readers(const gqg_tensor * r) const {
+        const auto it = nodes_reading.find(r);
+        return it == nodes_reading.end() ? 0 : it->second;
     }
-    for (const auto & e : only_gemv) {
-        const gqg_tensor * r = e.first;
-        if (e.second && (r->op == GQG_OP_RMS_NORM || r->op == GQG_OP_MUL) && unfused_output(r) && nel(r) == r->ne[0] &&
-            r->ne[0] % 16 == 0 && r->ne[0] <= 16384 && !A.skip.count(r))
-            A.defer_ok.insert(r);
+    // the node that alone reads root r, when r is no graph or split output (its value is then needed only there)
+    const gqg_tensor * sole(const gqg_tensor * r) const {
+        if (readers(r) != 1 || !unfused_output(r)) return nullptr;
+        return reads.at(r).front().node;
+    }
+    // the first read of root r that pred accepts
+    template <typename P>
+    const Read * first(const gqg_tensor * r, P pred) const {
+        const auto it = reads.find(r);
+        if (it == reads.end()) return nullptr;
+        for (const Read & x : it->second)
+            if (pred(x)) return &x;
+        return nullptr;
+    }
+    bool in_split(const gqg_tensor * t) const { return at.count(t) != 0; }
+};
+
+// The one-token conv chain (gemvqc16.cpp:161-190, 244-281): the state's window row, CONCAT with the input, SSM_CONV,
+// and the CPY of the new window back into the state.
+struct ConvChain {
+    const gqg_tensor * state_rows = nullptr, * window = nullptr, * store = nullptr, * conv = nullptr, * input = nullptr;
+};
+// The DeltaNet step with what the GDN command folds into it (gemvqc16.h:60-81, gemvqc_gdn.h).
+struct DeltaStep {
+    const gqg_tensor * state_rows = nullptr, * store = nullptr;
+    bool l2 = false;
+    float l2_eps = 0.0f, rms_eps = 0.0f;
+    const gqg_tensor * gated = nullptr, * norm_w = nullptr, * gate = nullptr;  // gated norm output, its weight, z
+    bool gate_silu = false;                                                      // gate holds silu(z)
+    const gqg_tensor * alpha = nullptr, * beta = nullptr, * dt = nullptr, * a = nullptr;  // raw gates
+};
+// One-token gated attention: the q (+ gate) / k / v projections, the norms, RoPE, the cache stores and the output.
+struct AttnChain {
+    const gqg_tensor * q_proj = nullptr, * k_proj = nullptr, * v_proj = nullptr, * q_norm_w = nullptr,
+                     * k_norm_w = nullptr, * fa = nullptr, * k_store = nullptr, * v_store = nullptr, * pos = nullptr,
+                     * k_row = nullptr;
+    float eps = 0.0f, scale = 0.0f, base = 0.0f;
+    int n_rot = 0, n_head = 0, n_head_kv = 0, head_dim = 0;
+    std::string layer;
+};
+
+struct FusionPlan {
+    ReaderIndex ix;
+    std::unordered_set<const gqg_tensor *> absorbed;  // nodes computed inside another node's command
+    std::unordered_map<const gqg_tensor *, ConvChain> conv_by_silu;            // the SiLU closing a conv chain
+    std::unordered_map<const gqg_tensor *, const gqg_tensor *> conv_input_gemv;  // GEMV -> SiLU of the conv it feeds
+    std::unordered_map<const gqg_tensor *, DeltaStep> steps;                     // GATED_DELTA_NET nodes
+    std::unordered_map<const gqg_tensor *, const gqg_tensor *> silu_written;     // GEMV -> the SiLU it writes
+    std::unordered_map<const gqg_tensor *, std::pair<const gqg_tensor *, const gqg_tensor *>> glu_pairs;  // GLU -> g, u
+    std::unordered_set<const gqg_tensor *> add_epilog;   // GEMVs whose one reader, an ADD, becomes their epilog
+    std::unordered_set<const gqg_tensor *> adds_taken;   // those ADDs
+    std::unordered_set<const gqg_tensor *> deferred;     // norm rows read only by GEMVs (never written)
+    std::unordered_map<const gqg_tensor *, AttnChain> attn_by_gate;  // the gate MUL closing an attention
+    int readers(const gqg_tensor * t) const { return ix.readers(t); }
+    void absorb(std::initializer_list<const gqg_tensor *> ts) { absorbed.insert(ts); }
+};
+
+bool match_conv(FusionPlan & F, const gqg_tensor * c, std::string & err) {
+    ConvChain cc;
+    cc.conv = c;
+    cc.window = c->src[0];
+    const bool concat = cc.window && cc.window->op == GQG_OP_CONCAT;
+    if (concat) {
+        cc.state_rows = rs_rows(cc.window->src[0]);
+        cc.input = cc.window->src[1];
+        // the new window: the last three columns of the concatenation (a view one float in) copied into the state
+        const auto * st = F.ix.first(cc.window, [](const ReaderIndex::Read & r) {
+            return r.node->op == GQG_OP_CPY && r.slot == 0 && r.via->view_offs == 4 && in_buf(r.node->src[1], GQG_BUF_RS);
+        });
+        cc.store = st ? st->node : nullptr;
+    }
+    const auto * sr = F.ix.first(c, [c](const ReaderIndex::Read & r) { return unary_kind(r.node) == 1 && r.node->src[0] == c; });
+    const gqg_tensor * silu = sr ? sr->node : nullptr;
+    if (!concat || !cc.state_rows || !cc.store || !silu || !f32_weight(c->src[1]) || c->ne[0] % 16 ||
+        cc.window->ne[0] != 4 || cc.window->ne[1] != c->ne[0]) {
+        err = std::string("conv ") + c->name + ": not the state-window CONCAT, SSM_CONV, SiLU and state CPY of one token";
+        return false;
+    }
+    F.conv_by_silu[silu] = cc;
+    F.absorb({cc.state_rows, cc.window, cc.store, c});
+    // its input straight from a GEMV of this split that nothing else reads: the CONV becomes that GEMV's epilog
+    const gqg_tensor * x = root_of(cc.input);
+    if (x->op == GQG_OP_MUL_MAT && F.ix.in_split(x) && F.ix.sole(x) && x->ne[0] == c->ne[0]) F.conv_input_gemv[x] = silu;
+    return true;
+}
+
+// The gated output norm after the step: RMS_NORM over rows of 128 of the step's output -> MUL by a 128-float weight ->
+// MUL by SILU(z), each read by the next alone; the step read by that norm and its state CPY only.
+void match_gated_norm(FusionPlan & F, const gqg_tensor * node, DeltaStep & p) {
+    const gqg_tensor * v = node->src[2];
+    const auto * nr = F.ix.first(node, [&](const ReaderIndex::Read & r) {
+        const gqg_tensor * m = r.node;
+        return m->op == GQG_OP_RMS_NORM && r.slot == 0 && r.via->view_offs == 0 && m->ne[0] == HEAD && nel(m) == nel(v);
+    });
+    const gqg_tensor * norm = nr ? nr->node : nullptr;
+    if (!norm || F.readers(node) != 2) return;
+    const gqg_tensor * mw = F.ix.sole(norm);
+    if (!mw || mw->op != GQG_OP_MUL || mw->src[0] != norm) return;
+    const gqg_tensor * mz = F.ix.sole(mw);
+    if (!mz || mz->op != GQG_OP_MUL || mz->src[0] != mw) return;
+    const gqg_tensor * w = mw->src[1], * sl = mz->src[1];
+    if (!f32_weight(w) || nel(w) != HEAD || unary_kind(sl) != 1 || F.ix.sole(sl) != mz || nel(sl) != nel(mz) ||
+        nel(mz) != nel(norm) || !contiguous(sl->src[0]) || !contiguous(mz))
+        return;
+    p.gated = mz;
+    p.norm_w = w;
+    p.rms_eps = pf(norm, 0);
+    F.absorb({norm, mw, mz, sl});
+    // z = silu(GEMV output) where that GEMV feeds the SiLU alone: the GEMV writes silu(z) (its SiLU epilog) once
+    const gqg_tensor * zg = root_of(sl->src[0]);
+    if (zg->op == GQG_OP_MUL_MAT && F.ix.in_split(zg) && F.ix.sole(zg) && sl->src[0]->data == zg->data && nel(zg) == nel(sl)) {
+        F.silu_written[zg] = sl;
+        p.gate = sl;
+        p.gate_silu = true;
+    } else {
+        p.gate = sl->src[0];
+    }
+}
+
+// The gates: SIGMOID(beta raw) and MUL(SOFTPLUS(ADD(alpha raw, dt)), a), every link read by the next alone, dt and a
+// weights of one float per value head.
+void match_gates(FusionPlan & F, const gqg_tensor * node, DeltaStep & p) {
+    const int64_t hv = node->src[2]->ne[1];
+    const gqg_tensor * sig = root_of(node->src[4]), * mul = root_of(node->src[3]);
+    const auto head_weight = [hv](const gqg_tensor * x) { return x && f32_weight(x) && nel(x) == hv; };
+    const auto head_row = [hv](const gqg_tensor * x) { return x->type == GQG_TYPE_F32 && contiguous(x) && nel(x) == hv; };
+    if (unary_kind(sig) != 2 || F.ix.sole(sig) != node || mul->op != GQG_OP_MUL || F.ix.sole(mul) != node ||
+        !head_row(sig->src[0]))
+        return;
+    const bool sp_first = mul->src[0]->op == GQG_OP_UNARY;
+    const gqg_tensor * sp = mul->src[sp_first ? 0 : 1], * a = mul->src[sp_first ? 1 : 0];
+    if (unary_kind(sp) != 3 || F.ix.sole(sp) != mul || !head_weight(a)) return;
+    const gqg_tensor * add = sp->src[0];
+    if (add->op != GQG_OP_ADD || F.ix.sole(add) != sp) return;
+    const bool dt_second = head_weight(add->src[1]);
+    const gqg_tensor * dt = add->src[dt_second ? 1 : 0], * alpha = add->src[dt_second ? 0 : 1];
+    if (!head_weight(dt) || !head_row(alpha)) return;
+    p.beta = sig->src[0];
+    p.alpha = alpha;
+    p.dt = dt;
+    p.a = a;
+    F.absorb({sig, mul, sp, add});
+}
+
+bool match_step(FusionPlan & F, const gqg_tensor * node, std::string & err) {
+    DeltaStep p;
+    p.state_rows = rs_rows(node->src[5]);
+    const size_t y_bytes = size_t(node->src[2]->ne[1]) * HEAD * 4;  // the new state follows the outputs
+    const auto * st = F.ix.first(node, [y_bytes](const ReaderIndex::Read & r) {
+        return r.node->op == GQG_OP_CPY && r.slot == 0 && r.via->view_offs == y_bytes && in_buf(r.node->src[1], GQG_BUF_RS);
+    });
+    p.store = st ? st->node : nullptr;
+    if (!p.state_rows || !p.store) {
+        err = std::string("DeltaNet step ") + node->name + ": no state row read from, or new state copied to, a state buffer";
+        return false;
+    }
+    F.absorb({p.state_rows, p.store});
+    const gqg_tensor * q = node->src[0], * k = node->src[1];
+    if (q->op == GQG_OP_L2_NORM && k->op == GQG_OP_L2_NORM && F.ix.sole(q) == node && F.ix.sole(k) == node &&
+        contiguous(q->src[0]) && contiguous(k->src[0]) && q->op_params[0] == k->op_params[0]) {
+        p.l2 = true;
+        p.l2_eps = pf(q, 0);
+        F.absorb({q, k});
+    }
+    match_gated_norm(F, node, p);
+    match_gates(F, node, p);
+    F.steps[node] = p;
+    return true;
+}
+
+// ROPE(MUL(RMS_NORM(rows), weight)) -> the rows, the weight and the norm's eps
+bool rope_of_norm(const gqg_tensor * rope, const gqg_tensor *& rows, const gqg_tensor *& w, float & eps) {
+    if (!rope || rope->op != GQG_OP_ROPE) return false;
+    const gqg_tensor * mw = rope->src[0];
+    if (!mw || mw->op != GQG_OP_MUL || !mw->src[0] || mw->src[0]->op != GQG_OP_RMS_NORM || !f32_weight(mw->src[1]))
+        return false;
+    rows = mw->src[0]->src[0];
+    w = mw->src[1];
+    eps = pf(mw->src[0], 0);
+    return true;
+}
+
+bool match_attention(FusionPlan & F, const gqg_tensor * fa, std::string & err) {
+    AttnChain at;
+    at.fa = fa;
+    at.scale = pf(fa, 0);
+    const gqg_tensor * kc = root_of(fa->src[1]), * vc = root_of(fa->src[2]);
+    const gqg_tensor * qrope = through_views(fa->src[0]);
+    const gqg_tensor * qrows = nullptr, * krows = nullptr;
+    float qeps = 0.0f, keps = 0.0f;
+    const auto store_into = [&](const gqg_tensor * cache) {
+        const auto * r = F.ix.first(cache, [cache](const ReaderIndex::Read & x) {
+            return x.node->op == GQG_OP_SET_ROWS && x.slot == 0 && root_of(x.node->src[0]) == cache;
+        });
+        return r ? r->node : nullptr;
+    };
+    bool ok = in_buf(kc, GQG_BUF_KV) && in_buf(vc, GQG_BUF_KV) && rope_of_norm(qrope, qrows, at.q_norm_w, qeps);
+    if (ok) {
+        at.k_store = store_into(kc);
+        at.v_store = store_into(vc);
+    }
+    const gqg_tensor * krope = ok && at.k_store ? through_views(at.k_store->src[1]) : nullptr;
+    ok = ok && at.v_store && rope_of_norm(krope, krows, at.k_norm_w, keps) && qeps == keps;
+    if (ok) {
+        at.eps = qeps;
+        at.q_proj = root_of(qrows);
+        at.k_proj = root_of(krows);
+        at.v_proj = root_of(at.v_store->src[1]);
+        at.head_dim = int(qrows->ne[0]);
+        at.n_head = int(qrows->ne[1]);
+        at.n_head_kv = int(krows->ne[1] > 1 ? krows->ne[1] : nel(krows) / at.head_dim);
+        at.n_rot = qrope->op_params[1];
+        at.base = pf(qrope, 5);
+        at.pos = qrope->src[1];
+        at.k_row = at.k_store->src[2];
+        const bool neox = qrope->op_params[2] == GQG_ROPE_TYPE_NEOX && krope->op_params[2] == GQG_ROPE_TYPE_NEOX;
+        const bool same_rope = krope->op_params[1] == at.n_rot && pf(krope, 5) == at.base && krope->src[1] == at.pos;
+        const bool plain_rope = pf(qrope, 6) == 1.0f && pf(qrope, 7) == 0.0f && pf(qrope, 8) == 1.0f;  // no YaRN
+        const bool q_gate_rows = qrows->view_offs == 0 && qrows->nb[0] == 4 && qrows->nb[1] == size_t(2 * at.head_dim) * 4 &&
+                                 nel(at.q_proj) == int64_t(2) * at.head_dim * at.n_head;
+        ok = at.q_proj->op == GQG_OP_MUL_MAT && at.k_proj->op == GQG_OP_MUL_MAT && at.v_proj->op == GQG_OP_MUL_MAT &&
+             nel(at.v_proj) == nel(at.k_proj) && q_gate_rows && neox && same_rope && plain_rope &&
+             at.pos->type == GQG_TYPE_I32 && nel(at.pos) == 1 && at.k_row->type == GQG_TYPE_I64 && nel(at.k_row) == 1 &&
+             at.v_store->src[2] == at.k_row;
+    }
+    // the output gate: MUL(the output, SIGMOID(CONT(the gate rows of q, head_dim floats in))), the output read there alone
+    const auto * gr = ok ? F.ix.first(fa, [fa](const ReaderIndex::Read & r) {
+        return r.node->op == GQG_OP_MUL && root_of(r.node->src[0]) == fa;
+    }) : nullptr;
+    const gqg_tensor * gmul = gr ? gr->node : nullptr;
+    const gqg_tensor * sig = gmul ? gmul->src[1] : nullptr;
+    const gqg_tensor * grow = sig && unary_kind(sig) == 2 && sig->src[0]->op == GQG_OP_CONT ? sig->src[0]->src[0] : nullptr;
+    ok = ok && gmul && grow && root_of(grow) == at.q_proj && grow->view_offs == size_t(at.head_dim) * 4 &&
+         grow->nb[1] == size_t(2 * at.head_dim) * 4 && nel(gmul) == int64_t(at.n_head) * at.head_dim &&
+         F.readers(fa) == 1 && unfused_output(fa);
+    if (!ok) {
+        err = std::string("attention ") + fa->name + ": not the one-token gated attention of a KV buffer of this backend";
+        return false;
+    }
+    const std::string cname = root_of(at.k_store->src[0])->name;  // cache_k_l<N>: the layer is what follows cache_k_
+    at.layer = cname.size() > 7 ? cname.substr(7) : cname;
+    F.attn_by_gate[gmul] = at;
+    F.absorb({qrope, qrope->src[0], qrope->src[0]->src[0], krope, krope->src[0], krope->src[0]->src[0], at.k_store,
+              at.v_store, fa, sig, sig->src[0]});
+    return true;
+}
+
+// GLU(g, u) of two GEMVs on the same row, each read by the GLU alone: a SwiGLU pair (gemvqc16.cpp:224-243).
+void match_glu(FusionPlan & F, const gqg_tensor * m) {
+    if (m->op_params[0] != GQG_GLU_SWIGLU || m->op_params[1] != 0) return;
+    const gqg_tensor * g = m->src[0], * u = m->src[1];
+    const auto lone_gemv = [&](const gqg_tensor * x) {
+        return x && x->op == GQG_OP_MUL_MAT && F.ix.in_split(x) && F.ix.sole(x) == m;
+    };
+    if (!lone_gemv(g) || !lone_gemv(u) || g->src[1]->data != u->src[1]->data || g->src[0]->ne[0] != u->src[0]->ne[0] ||
+        g->ne[0] != u->ne[0] || g->ne[0] != m->ne[0] || g->src[0]->type != u->src[0]->type)
+        return;
+    F.glu_pairs[m] = {g, u};
+    F.absorb({g, u});
+}
+
+// A GEMV read only by an ADD of its own length, whose other operand exists before the GEMV runs: the ADD becomes the
+// GEMV's epilog (gemvqc16.cpp:282-301). The GEMV's place in the row must be the ADD operand itself.
+void match_add_epilog(FusionPlan & F, const gqg_tensor * m) {
+    if (F.silu_written.count(m) || F.conv_input_gemv.count(m)) return;
+    const gqg_tensor * add = F.ix.sole(m);
+    if (!add || add->op != GQG_OP_ADD || F.absorbed.count(add) || F.adds_taken.count(add)) return;
+    if (nel(m) != nel(add) || m->ne[0] < 256 || m->ne[0] % 16) return;
+    for (int s = 0; s < 2; ++s) {
+        if (root_of(add->src[s]) != m || add->src[s]->data != m->data) continue;
+        const gqg_tensor * other = root_of(add->src[1 - s]);
+        if (other == m || (F.ix.in_split(other) && F.ix.at.at(other) > F.ix.at.at(m))) return;
+        F.add_epilog.insert(m);
+        F.adds_taken.insert(add);
+        return;
+    }
+}
+
+// A norm row (RMS_NORM, or the MUL by its weight) that only GEMVs of this split read, as their activation: the
+// deferred RMSNORM (gemvqc16.h:46-51), folded into their quantization and never written.
+void match_deferred(FusionPlan & F, const gqg_tensor * r) {
+    if (!unfused_output(r) || nel(r) != r->ne[0] || r->ne[0] % 16 || r->ne[0] > 16384) return;
+    const auto it = F.ix.reads.find(r);
+    if (it == F.ix.reads.end() || it->second.empty()) return;
+    for (const auto & x : it->second)
+        if (x.node->op != GQG_OP_MUL_MAT || x.slot != 1) return;
+    F.deferred.insert(r);
+}
+
+bool plan_fusions(const gqg_cgraph * g, FusionPlan & F, std::string & err) {
+    F.ix.build(g);
+    for (int i = g->n_nodes - 1; i >= 0; --i) {
+        const gqg_tensor * t = g->nodes[i];
+        if (is_view(t) || F.absorbed.count(t)) continue;
+        switch (t->op) {
+        case GQG_OP_SSM_CONV:
+            if (!match_conv(F, t, err)) return false;
+            break;
+        case GQG_OP_GATED_DELTA_NET:
+            if (!match_step(F, t, err)) return false;
+            break;
+        case GQG_OP_FLASH_ATTN_EXT:
+            if (!match_attention(F, t, err)) return false;
+            break;
+        case GQG_OP_GLU: match_glu(F, t); break;
+        case GQG_OP_MUL_MAT: match_add_epilog(F, t); break;
+        case GQG_OP_RMS_NORM:
+        case GQG_OP_MUL: match_deferred(F, t); break;
+        default: break;
+        }
     }
     return true;
 }
 
-// ---- the plan key (ggml-xrt.cpp:2133-2160's fields) ----
+// ---- the plan cache key: a structural signature of the split ----
+// Every node contributes its operation, types, flags, buffer, shape, strides, parameters, data address and view
+// offset, and for each operand (and its view source) a reference: the producing node's position in the split, or an
+// entry of a table of the tensors read from outside the split (weights, inputs, states), each described once with
+// the same fields, its name and its own address (weights are uploaded once per tensor). A state GET_ROWS adds the
+// row it selects (the command's state rows depend on it). Plans are found by a 64-bit mix of the signature and
+// confirmed by comparing it whole.
+struct Signature {
+    std::vector<uint64_t> words;
+    uint64_t hash = 0;
+};
 
-void key_tensor(std::vector<uint64_t> & key, const gqg_tensor * t) {
-    key.push_back(uint64_t(reinterpret_cast<uintptr_t>(t)));
-    if (!t) return;
-    key.push_back(uint64_t(reinterpret_cast<uintptr_t>(t->data)));
-    key.push_back(uint64_t(reinterpret_cast<uintptr_t>(t->view_src)));
-    key.push_back(uint64_t(t->view_offs));
-    key.push_back(uint64_t(uint32_t(t->op)) | (uint64_t(uint32_t(t->type)) << 16) | (uint64_t(uint32_t(t->flags)) << 32) |
-                  (uint64_t(uint32_t(t->buffer)) << 56));
-    for (int d = 0; d < GQG_MAX_DIMS; ++d) {
-        key.push_back(uint64_t(t->ne[d]));
-        key.push_back(uint64_t(t->nb[d]));
-    }
-    for (int k = 0; k < GQG_MAX_OP_PARAMS; ++k) key.push_back(uint64_t(uint32_t(t->op_params[k])));
+uint64_t mix64(uint64_t h) {  // a finalizer with full avalanche (the SplitMix64 one)
+    h ^= h >> 30;
+    h *= 0xbf58476d1ce4e5b9ull;
+    h ^= h >> 27;
+    h *= 0x94d049bb133111ebull;
+    return h ^ (h >> 31);
 }
 
-void plan_key(const gqg_cgraph * g, std::vector<uint64_t> & key) {
-    key.clear();
-    key.push_back(uint64_t(g->n_nodes));
-    const std::unordered_set<const gqg_tensor *> nodes(g->nodes, g->nodes + g->n_nodes);
-    const auto outside = [&](const gqg_tensor * t) {
-        if (t && !nodes.count(t)) key_tensor(key, t);
-    };
-    for (int i = 0; i < g->n_nodes; ++i) {
-        const gqg_tensor * node = g->nodes[i];
-        key_tensor(key, node);
-        int ns = GQG_MAX_SRC;
-        while (ns > 0 && !node->src[ns - 1]) --ns;
-        key.push_back(uint64_t(ns));
-        for (int k = 0; k < ns; ++k) {
-            const gqg_tensor * s = node->src[k];
-            key.push_back(uint64_t(reinterpret_cast<uintptr_t>(s)));
-            outside(s);
-            if (s) outside(s->view_src);
-        }
-        outside(node->view_src);
-        // the sequence row a state GET_ROWS selects decides the command's state rows
-        if (node->op == GQG_OP_GET_ROWS && in_buf(node->src[0], GQG_BUF_RS) && node->src[1]->data)
-            key.push_back(uint64_t(uint32_t(*static_cast<const int32_t *>(node->src[1]->data))));
+struct SignatureBuilder {
+    const ReaderIndex & ix;
+    std::vector<uint64_t> & w;
+    std::unordered_map<const gqg_tensor *, uint64_t> outside;
+    std::vector<const gqg_tensor *> outside_order;
+
+    uint64_t ref(const gqg_tensor * t) {
+        if (!t) return 0;
+        const auto n = ix.at.find(t);
+        if (n != ix.at.end()) return (1ull << 62) | uint64_t(n->second);
+        const auto o = outside.find(t);
+        if (o != outside.end()) return o->second;
+        const uint64_t id = (2ull << 62) | uint64_t(outside.size());
+        outside[t] = id;
+        outside_order.push_back(t);
+        return id;
     }
+    void fields(const gqg_tensor * t) {
+        w.push_back(uint64_t(uint32_t(t->op)) | uint64_t(uint32_t(t->type)) << 16 | uint64_t(uint32_t(t->buffer)) << 32 |
+                    uint64_t(uint32_t(t->flags) & 0xffffu) << 48);
+        for (int d = 0; d < GQG_MAX_DIMS; ++d) w.push_back(uint64_t(t->ne[d]) ^ (uint64_t(t->nb[d]) << 40) ^ (uint64_t(t->nb[d]) >> 24));
+        for (int k = 0; k < GQG_MAX_OP_PARAMS; k += 2)
+            w.push_back(uint64_t(uint32_t(t->op_params[k])) | uint64_t(uint32_t(t->op_params[k + 1])) << 32);
+        w.push_back(uint64_t(reinterpret_cast<uintptr_t>(t->data)));
+        w.push_back(uint64_t(t->view_offs));
+        w.push_back(ref(t->view_src));
+    }
+};
+
+void signature_of(const gqg_cgraph * g, const ReaderIndex & ix, Signature & s) {
+    s.words.clear();
+    SignatureBuilder b{ix, s.words, {}, {}};
+    s.words.push_back(uint64_t(g->n_nodes));
+    for (int i = 0; i < g->n_nodes; ++i) {
+        const gqg_tensor * t = g->nodes[i];
+        b.fields(t);
+        for (int k = 0; k < GQG_MAX_SRC; ++k) s.words.push_back(b.ref(t->src[k]));
+        if (t->op == GQG_OP_GET_ROWS && in_buf(t->src[0], GQG_BUF_RS) && t->src[1]->data)
+            s.words.push_back(uint64_t(uint32_t(*static_cast<const int32_t *>(t->src[1]->data))));
+    }
+    // the outside tensors, in order of first reference (describing one may add its view source)
+    for (size_t i = 0; i < b.outside_order.size(); ++i) {
+        const gqg_tensor * t = b.outside_order[i];
+        s.words.push_back(uint64_t(reinterpret_cast<uintptr_t>(t)));
+        b.fields(t);
+        uint64_t nh = 0xcbf29ce484222325ull;  // FNV-1a of the name
+        for (const char * c = t->name; *c && c < t->name + sizeof(t->name); ++c) nh = (nh ^ uint8_t(*c)) * 0x100000001b3ull;
+        s.words.push_back(nh);
+    }
+    uint64_t h = 0x9e3779b97f4a7c15ull;
+    for (uint64_t v : s.words) h = mix64(h ^ v);
+    s.hash = h;
 }
 
 // ---- emission ----
@@ -617,7 +708,7 @@ void plan_key(const gqg_cgraph * g, std::vector<uint64_t> & key) {
 struct Emitter {
     gqg_backend * b;
     const gqg_cgraph * g;
-    const Analysis & A;
+    const FusionPlan & F;
     gqg_backend::Plan & P;
     std::string err;
     size_t used = 64;  // transient region bump pointer
@@ -751,7 +842,7 @@ struct Emitter {
         const int n = g->n_nodes;
         for (int i = 0; i < n; ++i) {
             const gqg_tensor * node = g->nodes[i];
-            if (is_view(node) || A.skip.count(node) || nel(node) == 0) continue;
+            if (is_view(node) || F.absorbed.count(node) || nel(node) == 0) continue;
             const size_t ne = size_t(nel(node));
             const gqg_tensor * a = node->src[0], * bsrc = node->src[1];
             const gqg_tensor * next = i + 1 < n ? g->nodes[i + 1] : nullptr;
@@ -764,11 +855,11 @@ struct Emitter {
                 if (root_of(bsrc) != last_deferred) undefer(root_of(bsrc));
                 uint32_t x, y;
                 if (!operand(bsrc, size_t(a->ne[0]), x)) return false;
-                const auto se = A.silu_epilog.find(node);
-                if (!output(se != A.silu_epilog.end() ? se->second : node, y)) return false;
-                if (A.add_src.count(node)) add_at[node] = P.words.size();
-                if (A.conv_src.count(node)) conv_at[node] = P.words.size();
-                if (!gemv(node, x, y, se != A.silu_epilog.end() ? GEMVQ_GEMV_SILU : 0u)) return false;
+                const auto se = F.silu_written.find(node);
+                if (!output(se != F.silu_written.end() ? se->second : node, y)) return false;
+                if (F.add_epilog.count(node)) add_at[node] = P.words.size();
+                if (F.conv_input_gemv.count(node)) conv_at[node] = P.words.size();
+                if (!gemv(node, x, y, se != F.silu_written.end() ? GEMVQ_GEMV_SILU : 0u)) return false;
                 break;
             }
             case GQG_OP_RMS_NORM:
@@ -776,9 +867,9 @@ struct Emitter {
             case GQG_OP_MUL: {
                 const gqg_tensor * norm = node->op == GQG_OP_MUL ? a : node;
                 const bool weight_mul = node->op == GQG_OP_MUL && a->op == GQG_OP_RMS_NORM && i > 0 && g->nodes[i - 1] == a &&
-                                        A.readers_of(a) == 1 && nel(bsrc) == node->ne[0] && f32_weight(bsrc);
+                                        F.readers(a) == 1 && nel(bsrc) == node->ne[0] && f32_weight(bsrc);
                 if (node->op == GQG_OP_RMS_NORM && next && next->op == GQG_OP_MUL && next->src[0] == node &&
-                    A.readers_of(node) == 1 && nel(next->src[1]) == node->ne[0] && f32_weight(next->src[1]))
+                    F.readers(node) == 1 && nel(next->src[1]) == node->ne[0] && f32_weight(next->src[1]))
                     break;  // emitted with the weight MUL
                 if (node->op != GQG_OP_MUL || weight_mul) {
                     const uint32_t row = uint32_t(norm->ne[0]), rows = uint32_t(ne / row);
@@ -794,7 +885,7 @@ struct Emitter {
                     if (!operand(nx, span, x) || (weight_mul && !operand(bsrc, row, w)) || !output(node, y)) return false;
                     const uint32_t flags = (norm->op == GQG_OP_L2_NORM ? GEMVQ_NORM_L2 : 0u) |
                                            (weight_mul ? 0u : GEMVQ_NORM_NO_WEIGHT);
-                    const bool defer = rows == 1 && !strided && A.defer_ok.count(node);
+                    const bool defer = rows == 1 && !strided && F.deferred.count(node);
                     if (defer) {
                         deferred_at[node] = P.words.size();
                         last_deferred = node;
@@ -807,8 +898,8 @@ struct Emitter {
                     err = std::string("broadcast MUL ") + node->name + " is not the weight of the preceding norm";
                     return false;
                 }
-                const auto at = A.attn.find(node);
-                if (at != A.attn.end()) {
+                const auto at = F.attn_by_gate.find(node);
+                if (at != F.attn_by_gate.end()) {
                     if (!attention(node, at->second)) return false;
                     break;
                 }
@@ -823,8 +914,8 @@ struct Emitter {
             }
             case GQG_OP_ADD:
             case GQG_OP_GLU: {
-                const auto sw = A.swiglus.find(node);
-                if (sw != A.swiglus.end()) {
+                const auto sw = F.glu_pairs.find(node);
+                if (sw != F.glu_pairs.end()) {
                     const gqg_tensor * gt = sw->second.first, * ut = sw->second.second, * x = gt->src[1];
                     if (!quant_type(gt->src[0]->type) || !token_row(x)) {
                         err = std::string("SwiGLU pair ") + node->name + ": not quantized GEMVs on one row";
@@ -861,8 +952,8 @@ struct Emitter {
                 break;
             }
             case GQG_OP_UNARY: {
-                const auto cv = A.conv_of_silu.find(node);
-                if (cv != A.conv_of_silu.end()) {
+                const auto cv = F.conv_by_silu.find(node);
+                if (cv != F.conv_by_silu.end()) {
                     if (!conv(node, cv->second)) return false;
                     break;
                 }
@@ -872,11 +963,11 @@ struct Emitter {
                     return false;
                 }
                 if ((kind == 1 || kind == 2) && next && next->op == GQG_OP_MUL && next->src[1] == node &&
-                    next->src[0] != node && A.readers_of(node) == 1 && nel(next) == nel(node) && token_row(a)) {
+                    next->src[0] != node && F.readers(node) == 1 && nel(next) == nel(node) && token_row(a)) {
                     (kind == 1 ? fused_silu : fused_sigmoid).insert(node);  // emitted with the MUL
                     break;
                 }
-                const gqg_tensor * x = a->op == GQG_OP_CONT && strided_rows(a->src[0]) && A.readers_of(a) == 1 ? a->src[0] : a;
+                const gqg_tensor * x = a->op == GQG_OP_CONT && strided_rows(a->src[0]) && F.readers(a) == 1 ? a->src[0] : a;
                 const bool strided = x != a;
                 if (!strided && !token_row(x)) {
                     err = std::string("UNARY ") + node->name + ": input rows";
@@ -901,7 +992,7 @@ struct Emitter {
                 break;
             }
             case GQG_OP_GATED_DELTA_NET:
-                if (!gdn(node, A.gdns.at(node))) return false;
+                if (!gdn(node, F.steps.at(node))) return false;
                 break;
             case GQG_OP_GET_ROWS: {
                 const gqg_tensor * w = a, * ids = bsrc;
@@ -933,16 +1024,16 @@ struct Emitter {
         return true;
     }
 
-    bool conv(const gqg_tensor * silu, const Analysis::Conv & cv) {
+    bool conv(const gqg_tensor * silu, const ConvChain & cv) {
         const uint32_t ch = uint32_t(cv.conv->ne[0]);
         bool st;
         size_t s_src, s_dst;
-        if (!rs_at(cv.get_rows, state_row(cv.get_rows), st, s_src) || !rs_at(cv.cpy->src[1], cv.cpy->src[1]->data, st, s_dst))
+        if (!rs_at(cv.state_rows, state_row(cv.state_rows), st, s_src) || !rs_at(cv.store->src[1], cv.store->src[1]->data, st, s_dst))
             return false;
         uint32_t xo, wo, y;
-        if (!operand(cv.x, ch, xo) || !operand(cv.conv->src[1], size_t(ch) * 4, wo) || !output(silu, y)) return false;
+        if (!operand(cv.input, ch, xo) || !operand(cv.conv->src[1], size_t(ch) * 4, wo) || !output(silu, y)) return false;
         const uint32_t cmd[GEMVQ_CMD_WORDS] = {GEMVQ_OP_CONV, ch, xo, wo, y, uint32_t(s_src), uint32_t(s_dst), 1u};
-        const auto it = conv_at.find(root_of(cv.x));
+        const auto it = conv_at.find(root_of(cv.input));
         if (it != conv_at.end() && P.words[it->second + 7] == xo) {
             P.words[it->second + 1] |= GEMVQ_GEMV_CONV;  // the CONV right behind the GEMV of its input
             insert_after(it->second, cmd);
@@ -953,12 +1044,12 @@ struct Emitter {
         return true;
     }
 
-    bool gdn(const gqg_tensor * node, const Analysis::Gdn & p) {
+    bool gdn(const gqg_tensor * node, const DeltaStep & p) {
         const gqg_tensor * q = node->src[0], * k = node->src[1], * v = node->src[2];
         const uint32_t hv = uint32_t(v->ne[1]), hk = uint32_t(q->ne[1]);
         bool st_src, st_dst;
         size_t src_row, dst_row;
-        if (!rs_at(p.get_rows, state_row(p.get_rows), st_src, src_row) || !rs_at(p.cpy->src[1], p.cpy->src[1]->data, st_dst, dst_row))
+        if (!rs_at(p.state_rows, state_row(p.state_rows), st_src, src_row) || !rs_at(p.store->src[1], p.store->src[1]->data, st_dst, dst_row))
             return false;
         if (!st_src || !st_dst) {
             err = std::string("GDN state of ") + node->name + " is not on state rows";
@@ -971,11 +1062,11 @@ struct Emitter {
         if (!operand(qi, size_t(hk) * HEAD, qo) || !operand(ki, size_t(hk) * HEAD, ko) || !operand(v, size_t(hv) * HEAD, vo) ||
             !operand(gi, hv, go) || !operand(bi, hv, bo))
             return false;
-        if (p.out && (!operand(p.w, HEAD, wo) || !operand(p.z, size_t(hv) * HEAD, zo))) return false;
+        if (p.gated && (!operand(p.norm_w, HEAD, wo) || !operand(p.gate, size_t(hv) * HEAD, zo))) return false;
         if (gates && (!operand(p.dt, hv, dto) || !operand(p.a, hv, ao))) return false;
-        if (!output(p.out ? p.out : node, y)) return false;
-        const uint32_t flags = (p.l2 ? GEMVQ_GDN_L2_QK : 0u) | (p.out ? GEMVQ_GDN_GATED : 0u) | (gates ? GEMVQ_GDN_GATES : 0u) |
-                               (p.z_silu ? GEMVQ_GDN_Z_SILU : 0u);
+        if (!output(p.gated ? p.gated : node, y)) return false;
+        const uint32_t flags = (p.l2 ? GEMVQ_GDN_L2_QK : 0u) | (p.gated ? GEMVQ_GDN_GATED : 0u) | (gates ? GEMVQ_GDN_GATES : 0u) |
+                               (p.gate_silu ? GEMVQ_GDN_Z_SILU : 0u);
         push({GEMVQ_OP_GDN, hv | (hk << 16), qo, ko, vo, go, bo, y});
         push({uint32_t(src_row), uint32_t(dst_row), fbits(1.0f / std::sqrt(float(HEAD))), flags, fbits(p.l2_eps),
               fbits(p.rms_eps), wo, zo});
@@ -983,7 +1074,7 @@ struct Emitter {
         return true;
     }
 
-    bool attention(const gqg_tensor * mul, const Analysis::Attn & at) {
+    bool attention(const gqg_tensor * mul, const AttnChain & at) {
         // the layer's device KV cache: created on first use with the cache's size
         auto & kvp = b->kv_layers[at.layer];
         const int64_t n_ctx = root_of(at.fa->src[1])->ne[1];
@@ -1000,13 +1091,13 @@ struct Emitter {
             kvp.n_ctx = n_ctx;
         }
         uint32_t qo, ko, vo, qno, kno, po, cs, y;
-        if (!operand(at.qfull, size_t(2) * at.head_dim * at.n_head, qo) ||
-            !operand(at.kcur, size_t(at.n_head_kv) * at.head_dim, ko) ||
-            !operand(at.vcur, size_t(at.n_head_kv) * at.head_dim, vo) || !operand(at.qn, at.head_dim, qno) ||
-            !operand(at.kn, at.head_dim, kno) || !operand(at.pos, 1, po) ||
+        if (!operand(at.q_proj, size_t(2) * at.head_dim * at.n_head, qo) ||
+            !operand(at.k_proj, size_t(at.n_head_kv) * at.head_dim, ko) ||
+            !operand(at.v_proj, size_t(at.n_head_kv) * at.head_dim, vo) || !operand(at.q_norm_w, at.head_dim, qno) ||
+            !operand(at.k_norm_w, at.head_dim, kno) || !operand(at.pos, 1, po) ||
             !rope_table(b, at.n_rot, at.base, kvp.n_ctx, cs, err) || !output(mul, y))
             return false;
-        P.pos_checks.push_back({static_cast<const int64_t *>(at.kidx->data), static_cast<const int32_t *>(at.pos->data)});
+        P.pos_checks.push_back({static_cast<const int64_t *>(at.k_row->data), static_cast<const int32_t *>(at.pos->data)});
         push({GEMVQ_OP_ATTN, uint32_t(at.n_head) | (uint32_t(at.n_head_kv) << 16), qo, uint32_t(kvp.kv), y,
               uint32_t(at.head_dim) | (uint32_t(at.n_rot) << 16), po, 1u});
         push({ko, vo, fbits(at.scale), fbits(at.eps), qno, kno, cs, qo + uint32_t(at.head_dim)});
@@ -1080,9 +1171,9 @@ bool build(gqg_backend * b, const gqg_cgraph * g, gqg_backend::Plan & P, std::st
             err = std::string("node ") + g->nodes[i]->name + " is not supported";
             return false;
         }
-    Analysis A;
-    if (!analyse(g, A, err)) return false;
-    Emitter E{b, g, A, P};
+    FusionPlan F;
+    if (!plan_fusions(g, F, err)) return false;
+    Emitter E{b, g, F, P};
     if (!E.run()) {
         err = E.err;
         return false;
@@ -1095,16 +1186,19 @@ bool build(gqg_backend * b, const gqg_cgraph * g, gqg_backend::Plan & P, std::st
 }
 
 gqg_backend::Plan * get_plan(gqg_backend * b, const gqg_cgraph * g, std::string & err) {
-    static thread_local std::vector<uint64_t> key;
-    plan_key(g, key);
+    ReaderIndex ix;
+    for (int i = 0; i < g->n_nodes; ++i) ix.at[g->nodes[i]] = i;
+    Signature sig;
+    signature_of(g, ix, sig);
     for (auto & p : b->plans)
-        if (p->key == key) {
+        if (p->hash == sig.hash && p->sig == sig.words) {
             ++b->reused;
             return p.get();
         }
     auto P = std::make_unique<gqg_backend::Plan>();
     if (!build(b, g, *P, err)) return nullptr;
-    P->key = key;
+    P->sig = std::move(sig.words);
+    P->hash = sig.hash;
     ++b->built;
     if (b->plans.size() >= 64) {  // a decode token has a few splits; bound the cache
         for (auto & p : b->plans)
@@ -1193,6 +1287,18 @@ int gqg_graph_compute(gqg_backend * b, gqg_cgraph * g) {
     if (ok) return GQG_STATUS_SUCCESS;
     b->valid = false;  // a failed list leaves the device state unknown (ggml-xrt.cpp:2761-2770)
     return fail(b, err);
+}
+
+int gqg_graph_io(gqg_backend * b, gqg_cgraph * g, const void ** ins, const void ** outs, size_t cap, int counts[2]) {
+    if (!b || !g || g->n_nodes <= 0 || !counts) return fail(b, "gqg_graph_io: arguments");
+    std::string err;
+    gqg_backend::Plan * P = get_plan(b, g, err);
+    if (!P) return fail(b, err);
+    counts[0] = int(P->in.size());
+    counts[1] = int(P->out.size());
+    for (size_t i = 0; ins && i < P->in.size() && i < cap; ++i) ins[i] = P->in[i].host;
+    for (size_t i = 0; outs && i < P->out.size() && i < cap; ++i) outs[i] = P->out[i].host;
+    return 0;
 }
 
 void gqg_plan_stats(const gqg_backend * b, uint64_t out[2]) {

@@ -255,6 +255,7 @@ def lib():
         gq._c_fn(L, "gqg_graph_compute", C.c_int, vp, P(CGraph))
         gq._c_fn(L, "gqg_graph_plan", C.c_int, vp, P(CGraph), P(C.c_uint32), C.c_size_t)
         gq._c_fn(L, "gqg_plan_stats", None, vp, P(C.c_uint64))
+        gq._c_fn(L, "gqg_graph_io", C.c_int, vp, P(CGraph), P(vp), P(vp), C.c_size_t, P(C.c_int))
         gq._c_fn(L, "gqg_rs_buffer_alloc", vp, vp, C.c_size_t)
         gq._c_fn(L, "gqg_kv_buffer_alloc", vp, vp, C.c_size_t)
         gq._c_fn(L, "gqg_buffer_base", vp, vp)
@@ -306,6 +307,14 @@ class Backend:
 
     def compute(self, g: CGraph) -> int:
         return self.L.gqg_graph_compute(self.h, C.byref(g))
+
+    def io(self, g: CGraph, cap: int = 256) -> tuple[list[int], list[int]]:
+        """The host data addresses the split's plan copies in and copies back."""
+        ins, outs = (C.c_void_p * cap)(), (C.c_void_p * cap)()
+        counts = (C.c_int * 2)()
+        if self.L.gqg_graph_io(self.h, C.byref(g), ins, outs, cap, counts) != 0:
+            raise RuntimeError(f"io: {self.error()}")
+        return [ins[i] for i in range(min(counts[0], cap))], [outs[i] for i in range(min(counts[1], cap))]
 
     def stats(self) -> tuple[int, int]:
         out = (C.c_uint64 * 2)()

@@ -134,6 +134,42 @@ class Qwen35Graph:
         G.expand(self.logits_t)
         self.cgraph = G.cgraph()
 
+    def layer_splits(self) -> list[ir.CGraph]:
+        """The token's nodes as one split per layer (the embedding rows with layer 0, the output norm and head after
+        the last layer), the way ggml's scheduler cuts a graph into splits: a tensor that a later split reads is
+        flagged GGML_TENSOR_FLAG_SPLIT_OUTPUT (the reference's scheduler patch 0002), so its split copies it back to
+        the host and the later split copies it in. Returns the splits' graphs, in order."""
+        nodes, cfg = self.G.nodes, self.cfg
+        names = [t.name.decode() for t in nodes]
+        starts = [0] + [names.index(f"norm-{il}") for il in range(1, cfg.n_layer)]
+        starts.append(names.index(f"l_out-{cfg.n_layer - 1}") + 1)
+        bounds = list(zip(starts, starts[1:] + [len(nodes)]))
+        split_of = {}
+        for k, (a, b) in enumerate(bounds):
+            for t in nodes[a:b]:
+                split_of[C.addressof(t)] = k
+        root = lambda t: t.view_src.contents if t.view_src else t
+        for k, (a, b) in enumerate(bounds):
+            for t in nodes[a:b]:
+                for i in range(10):
+                    if not t.src[i]:
+                        continue
+                    r = root(t.src[i].contents)
+                    kr = split_of.get(C.addressof(r))
+                    if kr is not None and kr < k:
+                        r.flags |= ir.FLAG_SPLIT_OUTPUT
+        self.splits = [self.G.cgraph(nodes[a:b]) for a, b in bounds]
+        return self.splits
+
+    def step_splits(self, tok: int, pos: int) -> np.ndarray:
+        """One token through the backend split by split (layer_splits); returns the logits."""
+        self.set_token(tok, pos)
+        for k, g in enumerate(self.splits):
+            st = self.backend.compute(g)
+            if st != 0:
+                raise RuntimeError(f"graph_compute of split {k}: {st}: {self.backend.error()}")
+        return self.G.host(self.logits_t).copy()
+
     def _init(self, t: ir.Tensor) -> None:
         buf = self.rs if t.name.startswith(b"cache_s") or t.name.startswith(b"cache_r") else self.kvb
         if self.backend.L.gqg_buffer_init_tensor(buf, C.byref(t)) != 0:

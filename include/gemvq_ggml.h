@@ -23,10 +23,11 @@
  *   - GET_ROWS of a quantized weight by I32 ids: GET_ROWS; RMS_NORM, MUL, ADD, UNARY (SILU, SIGMOID, SOFTPLUS), CONT
  *     of strided rows, ROPE: their commands.
  * Every split compiles to one command list, run as a captured hipGraph: the plan (the list, where every input and
- * output sits in the activation buffer, what is copied back) is cached under the exact identity of the split (the
- * reference's plan key, ggml-xrt.cpp:2133-2188) and the graph is replayed when the same split comes again. An
- * output is copied back to its host tensor only when it is a graph output, a split output, or a later node of the
- * split reads it (the reference's readback filter, :1399-1478).
+ * output sits in the activation buffer, what is copied back) is cached under a structural signature of the split
+ * (every node's fields, its operands as node positions or outside tensors; the role of the reference's plan key,
+ * ggml-xrt.cpp:2133-2188) and the graph is replayed when the same split comes again. An
+ * output is copied back to its host tensor only when it is a graph output or a split output (the reference's
+ * readback filter, :1399-1478).
  *
  * Errors: a failed call latches the backend invalid; every later compute returns GQG_STATUS_FAILED
  * (ggml-xrt.cpp:2747-2770). Status values are ggml's (GGML_STATUS_*). */
@@ -117,6 +118,10 @@ int gqg_graph_compute(gqg_backend * b, gqg_cgraph * graph);
 int gqg_graph_plan(gqg_backend * b, gqg_cgraph * graph, uint32_t * words, size_t cap);
 /* Plan cache counters: plans built, plans reused. */
 void gqg_plan_stats(const gqg_backend * b, uint64_t out[2]);
+/* The host data a split's plan copies in before its run (ins) and copies back after it (outs: the readback filter,
+ * ggml-xrt.cpp:1399-1478): counts[0] and counts[1] receive how many, and up to cap of each are stored. Plans (or reuses)
+ * the split; returns 0 or a negative GQG_STATUS. */
+int gqg_graph_io(gqg_backend * b, gqg_cgraph * graph, const void ** ins, const void ** outs, size_t cap, int counts[2]);
 
 /* Recurrent-state buffer type (ggml-xrt.cpp:562-611; ggml_backend_xrt_rs_buffer_type): a host address range
  * reserved without access rights; gqg_rs_init_tensor places a tensor named cache_s_l* on state rows (128 floats a

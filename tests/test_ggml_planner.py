@@ -206,3 +206,35 @@ def test_registration_table():
 
     reg = C.cast(L.gqg_backend_get_reg(), C.POINTER(Reg)).contents
     assert reg.name == b"GEMVQ" and reg.device_type == 2 and reg.get_description and reg.get_memory
+
+
+def test_per_layer_splits_copy_only_split_outputs(tiny_blob):
+    """The token cut into one split per layer (and the head): every split compiles, each copies back exactly the
+    tensors flagged as split outputs or graph outputs (the residual stream it hands on, the logits), and copies in
+    the previous split's residual and the token's host inputs (the reference's readback filter and flush,
+    ggml-xrt.cpp:1399-1478); the plans are reused for the next token."""
+    cfg = tiny_blob.cfg
+    with dry_backend(tiny_blob) as b:
+        g = qwen35_ggml.Qwen35Graph(tiny_blob, b)
+        try:
+            splits = g.layer_splits()
+            assert len(splits) == cfg.n_layer + 1
+            names = {}
+            for t in g.G.tensors:
+                names[t.data] = t
+            produced = []
+            for k, sg in enumerate(splits):
+                ins, outs = b.io(sg)
+                flagged = [sg.nodes[i].contents for i in range(sg.n_nodes)]
+                want_out = {t.data for t in flagged if t.flags & (ir.FLAG_SPLIT_OUTPUT | ir.FLAG_OUTPUT) and not t.view_src}
+                assert set(outs) == want_out, (k, [names[o].name for o in outs])
+                assert len(outs) == 1  # the residual it hands on, or the logits
+                if k > 0:
+                    assert produced[-1] in ins, k  # the previous split's residual comes back in
+                produced.extend(outs)
+            built = b.stats()[0]
+            for sg in splits:  # the next token: every split's plan again
+                b.plan(sg)
+            assert b.stats()[0] == built
+        finally:
+            g.close()

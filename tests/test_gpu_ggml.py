@@ -73,3 +73,37 @@ def test_state_buffer_io(gq):
         assert np.array_equal(part, sv[128 * 128:128 * 128 + 128])
         assert b.L.gqg_buffer_get(buf, C.byref(s), part.ctypes.data, 4, 512) != 0  # not a whole row
         b.L.gqg_buffer_free(buf)
+
+
+def test_ggml_graph_in_per_layer_splits_matches_oracle(gq, orc):
+    """The token as one split per layer and a head split (the residual stream flagged as a split output at every
+    boundary, copied back to the host by one split and in by the next, ggml-xrt.cpp:1399-1478): greedy tokens and
+    every step's logits identical to the oracle decoder, each split's plan built once and replayed."""
+    import ggml_ir as ir
+    import qwen35
+    import qwen35_ggml
+
+    cfg = qwen35.tiny(n_layer=8, n_ctx=64)
+    blob = qwen35.generate(cfg, seed=6)
+    prompt = qwen35.prompt_ids(cfg, 5, seed=6)
+    n_gen = 8
+    om = orc.Model(qwen35.config_c(cfg), blob.table, blob.n, blob.data)
+    want = om.generate(prompt, n_gen)
+    lo = np.empty(cfg.n_vocab, np.float32)
+    om2 = orc.Model(qwen35.config_c(cfg), blob.table, blob.n, blob.data)
+    rows = sum(not cfg.is_attn(i) for i in range(cfg.n_layer)) * cfg.ssm_v_heads * 128
+    with ir.Backend(act_floats=1 << 21, weight_bytes=blob.data.size + (1 << 20), state_rows=rows) as b:
+        g = qwen35_ggml.Qwen35Graph(blob, b)
+        try:
+            splits = g.layer_splits()
+            toks = [int(prompt[0])]
+            for pos in range(len(prompt) - 1 + n_gen):
+                print(f"[ggml splits] position {pos}", flush=True)
+                logits = g.step_splits(toks[pos], pos)
+                om2.decode(int(want[pos]), pos, lo)
+                assert np.array_equal(logits.view(np.uint32), lo.view(np.uint32)), f"logits at position {pos}"
+                toks.append(int(prompt[pos + 1]) if pos + 1 < len(prompt) else int(np.argmax(logits)))
+            assert np.array_equal(np.array(toks, np.int32), want)
+            assert b.stats()[0] == len(splits)
+        finally:
+            g.close()
