@@ -52,7 +52,7 @@ def build_hip() -> str:
         list(ex.map(lambda so: _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, so[0]), "-o", so[1]]),
                     zip(HIP_SOURCES, objs)))
     tmp = HIP_LIB + ".tmp"
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp])
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,-soname,libgemvq_hip.so", *objs, "-o", tmp])
     os.replace(tmp, HIP_LIB)
     return HIP_LIB
 

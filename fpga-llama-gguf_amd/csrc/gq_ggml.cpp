@@ -1231,10 +1231,7 @@ gqg_backend * gqg_backend_init(const gqg_params * params) {
 
 void gqg_backend_free(gqg_backend * b) {
     if (!b) return;
-    for (gqg_buffer * buf : b->buffers) {
-        munmap(buf->base, buf->size);
-        delete buf;
-    }
+    for (gqg_buffer * buf : b->buffers) buf->owner = nullptr;  // detached: only gqg_buffer_free works on them now
     if (b->ctx) gemvq_ctx_destroy(b->ctx);
     if (g_active == b) g_active = nullptr;
     delete b;
@@ -1325,7 +1322,7 @@ gqg_buffer * gqg_kv_buffer_alloc(gqg_backend * b, size_t size) { return buffer_a
 void * gqg_buffer_base(const gqg_buffer * buf) { return buf ? buf->base : nullptr; }
 
 int gqg_buffer_init_tensor(gqg_buffer * buf, gqg_tensor * t) {
-    if (!buf || !t) return GQG_STATUS_FAILED;
+    if (!buf || !t || !buf->owner) return GQG_STATUS_FAILED;
     if (t->view_src) return GQG_STATUS_SUCCESS;
     gqg_backend * b = buf->owner;
     const auto * p = static_cast<const uint8_t *>(t->data);
@@ -1356,7 +1353,7 @@ int gqg_buffer_init_tensor(gqg_buffer * buf, gqg_tensor * t) {
 }
 
 static int buffer_io(gqg_buffer * buf, const gqg_tensor * t, void * data, size_t offset, size_t size, bool to_dev) {
-    if (!buf || !t) return GQG_STATUS_FAILED;
+    if (!buf || !t || !buf->owner) return GQG_STATUS_FAILED;
     gqg_backend * b = buf->owner;
     if (buf->kind != GQG_BUF_RS) return fail(b, "KV buffers are written by attention commands only");
     const gqg_buffer::Entry * e = buf->find(static_cast<const uint8_t *>(t->data) + offset);
@@ -1385,7 +1382,7 @@ int gqg_buffer_get(gqg_buffer * buf, const gqg_tensor * t, void * data, size_t o
 }
 
 int gqg_buffer_clear(gqg_buffer * buf, uint8_t value) {
-    if (!buf) return GQG_STATUS_FAILED;
+    if (!buf || !buf->owner) return GQG_STATUS_FAILED;
     gqg_backend * b = buf->owner;
     if (b->dry()) return GQG_STATUS_SUCCESS;
     if (buf->kind == GQG_BUF_KV) {
@@ -1403,9 +1400,10 @@ int gqg_buffer_clear(gqg_buffer * buf, uint8_t value) {
 
 void gqg_buffer_free(gqg_buffer * buf) {
     if (!buf) return;
-    gqg_backend * b = buf->owner;
-    auto & v = b->buffers;
-    v.erase(std::remove(v.begin(), v.end(), buf), v.end());
+    if (gqg_backend * b = buf->owner) {
+        auto & v = b->buffers;
+        v.erase(std::remove(v.begin(), v.end(), buf), v.end());
+    }
     munmap(buf->base, buf->size);
     delete buf;
 }

@@ -277,11 +277,15 @@ class Backend:
         self.h = self.L.gqg_backend_init(C.byref(Params(device, act_floats, weight_bytes, state_rows, int(dry))))
         if not self.h:
             raise RuntimeError("gqg_backend_init failed (one backend per process)")
+        self.buffers: list[int] = []
 
     def close(self):
         if self.h:
-            self.L.gqg_backend_free(self.h)
+            self.L.gqg_backend_free(self.h)  # buffers still held are detached, then freed here
             self.h = None
+        for b in self.buffers:
+            self.L.gqg_buffer_free(b)
+        self.buffers = []
 
     def __enter__(self):
         return self
@@ -325,4 +329,10 @@ class Backend:
         b = (self.L.gqg_rs_buffer_alloc if kind == BUF_RS else self.L.gqg_kv_buffer_alloc)(self.h, size)
         if not b:
             raise RuntimeError("buffer alloc failed")
+        self.buffers.append(b)
         return b
+
+    def free_buffer(self, b: int) -> None:
+        if b in self.buffers:
+            self.buffers.remove(b)
+            self.L.gqg_buffer_free(b)

@@ -197,5 +197,5 @@ class Qwen35Graph:
     def close(self) -> None:
         for b in (getattr(self, "rs", None), getattr(self, "kvb", None)):
             if b:
-                self.backend.L.gqg_buffer_free(b)
+                self.backend.free_buffer(b)
         self.rs = self.kvb = None

@@ -208,6 +208,28 @@ def test_registration_table():
     assert reg.name == b"GEMVQ" and reg.device_type == 2 and reg.get_description and reg.get_memory
 
 
+def test_buffer_outlives_its_backend():
+    """A ggml context may free its backend before the buffers of its caches: the buffers are then detached, refuse
+    every access, and are still freed by gqg_buffer_free (the memory is reserved, never touched)."""
+    L = ir.lib()
+    b = ir.Backend(act_floats=1 << 16, weight_bytes=1 << 20, state_rows=2 * 128, dry=True)
+    buf = L.gqg_rs_buffer_alloc(b.h, 2 * 128 * 512)
+    base = L.gqg_buffer_base(buf)
+    G = ir.Graph()
+    s = G.at(ir.F32, [2 * 128 * 128], base, "cache_s_l0")
+    assert L.gqg_buffer_init_tensor(buf, C.byref(s)) == 0
+    row = np.zeros(128, np.float32)
+    assert L.gqg_buffer_get(buf, C.byref(s), row.ctypes.data, 0, 512) == 0  # dry: accepted, nothing moves
+    b.close()
+    assert L.gqg_buffer_get(buf, C.byref(s), row.ctypes.data, 0, 512) != 0
+    assert L.gqg_buffer_set(buf, C.byref(s), row.ctypes.data, 0, 512) != 0
+    assert L.gqg_buffer_clear(buf, 0) != 0
+    assert L.gqg_buffer_init_tensor(buf, C.byref(s)) != 0
+    L.gqg_buffer_free(buf)
+    with ir.Backend(act_floats=1 << 16, weight_bytes=1 << 20, state_rows=128, dry=True):
+        pass  # the process's one backend slot is free again
+
+
 def test_per_layer_splits_copy_only_split_outputs(tiny_blob):
     """The token cut into one split per layer (and the head): every split compiles, each copies back exactly the
     tensors flagged as split outputs or graph outputs (the residual stream it hands on, the logits), and copies in
