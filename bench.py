@@ -34,11 +34,6 @@ METRIC = "decode tokens/s (9B-shape Q4_0, batch 1); GEMV HBM GB/s vs 8 TB/s peak
 HBM_PEAK_GBPS = 8000.0
 
 
-class LaunchStat(C.Structure):
-    _fields_ = [("name", C.c_char * 40), ("first_cmd", C.c_int32), ("n_cmds", C.c_int32), ("bytes", C.c_uint64),
-                ("us", C.c_double)]
-
-
 def measured_traffic(kernel: str) -> tuple[int | None, str | None]:
     """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, each
     scaled by the same counter on a copy kernel of known size), if that kernel was measured."""
@@ -57,16 +52,7 @@ def log(msg: str) -> None:
 
 
 def profile(ctx: gq.Context, cmds: np.ndarray, reps: int) -> list[dict]:
-    lib = gq.hip_lib()
-    lib.gemvq_profile.restype = C.c_int
-    lib.gemvq_profile.argtypes = [C.c_void_p, C.POINTER(C.c_uint32), C.c_uint, C.c_int, C.c_void_p, C.c_int]
-    w = np.ascontiguousarray(cmds.ravel(), np.uint32)
-    out = (LaunchStat * 4096)()
-    n = lib.gemvq_profile(ctx.h, w.ctypes.data_as(C.POINTER(C.c_uint32)), w.size // 8, reps, out, 4096)
-    if n < 0:
-        raise gq.GemvqError(f"profile: {n}: {ctx.error()}")
-    return [dict(name=out[i].name.decode(), first=out[i].first_cmd, bytes=int(out[i].bytes), us=out[i].us)
-            for i in range(n)]
+    return ctx.profile(np.ascontiguousarray(cmds.ravel(), np.uint32), reps)
 
 
 def cpu_info() -> dict:

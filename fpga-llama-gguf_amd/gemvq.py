@@ -137,6 +137,11 @@ _hip = None
 _synth = None
 
 
+class LaunchStat(C.Structure):  # gemvq_launch_stat
+    _fields_ = [("name", C.c_char * 40), ("first_cmd", C.c_int32), ("n_cmds", C.c_int32), ("bytes", C.c_uint64),
+                ("us", C.c_double)]
+
+
 def _c_fn(lib, name, res, *args):
     f = getattr(lib, name)
     f.restype = res
@@ -179,6 +184,7 @@ def hip_lib() -> C.CDLL:
         _c_fn(lib, "gemvq_debug_blocksums", C.c_int, vp, vp, C.c_size_t)
         _c_fn(lib, "gemvq_graph_time", C.c_int, vp, C.c_int, C.c_int, C.POINTER(C.c_double))
         _c_fn(lib, "gemvq_set_arith", C.c_int, vp, C.c_int)
+        _c_fn(lib, "gemvq_profile", C.c_int, vp, C.POINTER(C.c_uint32), C.c_uint, C.c_int, C.c_void_p, C.c_int)
         _c_fn(lib, "gemvq_arith", C.c_int, vp)
         _c_fn(lib, "gemvq_cr_expf", C.c_float, C.c_float)
         _c_fn(lib, "gemvq_cr_logf", C.c_float, C.c_float)
@@ -385,6 +391,17 @@ class Context:
 
     def arith(self) -> int:
         return self.lib.gemvq_arith(self.h)
+
+    def profile(self, cmds, reps: int = 1) -> list[dict]:
+        """The launches the list compiles to, each timed on the stream with HIP events (gemvq_profile: the median
+        over reps repetitions of the list): name, first command, HBM bytes (algorithmic), microseconds."""
+        w, n = self._words(cmds)
+        out = (LaunchStat * 4096)()
+        got = self.lib.gemvq_profile(self.h, w.ctypes.data_as(C.POINTER(C.c_uint32)), n, reps, out, 4096)
+        if got < 0:
+            raise GemvqError(f"profile: {got}: {self.error()}")
+        return [dict(name=out[i].name.decode(), first=out[i].first_cmd, bytes=int(out[i].bytes), us=out[i].us)
+                for i in range(got)]
 
     def crmath_hash(self, fn: int) -> np.ndarray:
         """The device's correctly rounded exp (fn 0) or log (fn 1) over every binary32 input, as 4096 block hashes."""

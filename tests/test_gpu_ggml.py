@@ -72,7 +72,7 @@ def test_state_buffer_io(gq):
         assert b.L.gqg_buffer_get(buf, C.byref(s), part.ctypes.data, 128 * 512, 512) == 0, b.error()
         assert np.array_equal(part, sv[128 * 128:128 * 128 + 128])
         assert b.L.gqg_buffer_get(buf, C.byref(s), part.ctypes.data, 4, 512) != 0  # not a whole row
-        b.L.gqg_buffer_free(buf)
+        b.free_buffer(buf)
 
 
 def test_ggml_graph_in_per_layer_splits_matches_oracle(gq, orc):
