@@ -103,13 +103,23 @@ def one_cpu_per_core(n: int) -> list[int]:
     return out
 
 
+def simd_name(oracle) -> str:
+    """The fast rows' SIMD level on this host (AVX-512 VNNI for Q4_0 / Q4_1 / Q8_0 block sums where the CPU has it)."""
+    return ("AVX-512 VNNI (Q4_0 / Q4_1 / Q8_0 blocks, 16 at a time) and AVX2 (Q6_K)"
+            if oracle.orc().orc_fast_simd() == oracle.SIMD_AVX512_VNNI else "AVX2")
+
+
+def pin_openmp(cpus: list[int]) -> None:
+    """One OpenMP thread per listed CPU, bound in order (the oracle's runtime reads these when it loads)."""
+    os.environ["OMP_PLACES"] = ",".join(f"{{{c}}}" for c in cpus)
+    os.environ["OMP_PROC_BIND"] = "close"
+
+
 def cpu_baseline(blob, cfg, tokens, pos0: int, max_tokens: int, seconds: float, threads: int) -> dict:
     """The oracle decoder in the reference's CPU arithmetic on the host: decode steps at the positions (and with the
     token ids) of the first timed GPU steps, until `seconds` have passed or max_tokens steps ran."""
     cpus = one_cpu_per_core(threads)
-    # one OpenMP thread per physical core, bound in order (the oracle's runtime reads these when it loads)
-    os.environ["OMP_PLACES"] = ",".join(f"{{{c}}}" for c in cpus)
-    os.environ["OMP_PROC_BIND"] = "close"
+    pin_openmp(cpus)
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle  # noqa: E402  (the CPU baseline leg only)
 
@@ -130,7 +140,7 @@ def cpu_baseline(blob, cfg, tokens, pos0: int, max_tokens: int, seconds: float, 
     return {"value": round(n / dt, 4), "unit": "tokens/s", "cores": len(cpus), "kind": "port",
             "arithmetic": "the reference's CPU arithmetic (gemvq_ref.h: int8 block dot products, each row summed "
                           "sequentially in FP32, sums of squares in double; exp / log correctly rounded, as the "
-                          "GPU's reference mode evaluates them); the int8 dots in AVX2",
+                          "GPU's reference mode evaluates them); the int8 dots in " + simd_name(oracle),
             "cpu": cpu_info(),
             "sample": f"{n} decode steps of the same 9B-shape model at positions {pos0 + 1}..{pos0 + n} with the ids "
                       f"the GPU generated there, from an empty state (a step's work depends on its position, not on "
@@ -155,7 +165,7 @@ def copy_probe(mib: int) -> int:
 # ---------------------------------------------------------------------------------------------------------------
 # C1-C4: the single-op configurations, each timed over rotated weight copies (>= 512 MB, twice the 256 MB
 # memory-side cache) inside one graph, and as single launches; the oracle on the host on the same bytes.
-def _cfg_units(seed: int = 0):
+def _cfg_units(threads: int = 1, seed: int = 0):
     """[(name, description, algorithmic bytes per unit, rotated copies, setup(ctx) -> builder(copy) -> commands,
     cpu(oracle) -> (function, args[, scale]))]."""
     units = []
@@ -173,7 +183,7 @@ def _cfg_units(seed: int = 0):
         ctx.write(16384, x1)  # consecutive copies read different (equal) x: each is its own launch, not a group
         return lambda i: gq.gemv(gq.Q4_0, R1, K1, offs[i], 16384 * (i & 1), 4096)
     units.append(("C1", "Q4_0 GEMV 9728x2560", w1.size + 4 * K1 + 4 * R1, C1_COPIES, c1,
-                  lambda orc: (orc.fx_gemv, (gq.Q4_0, w1, x1, R1, K1))))
+                  lambda orc: (orc.fast_gemv, (1, gq.Q4_0, w1, x1, R1, K1, threads))))
 
     # C2: norm + SwiGLU gate/up (Q8_0 [9728 x 2560] x 2) + down (Q8_0 [2560 x 9728]) + residual
     E, F = 2560, 9728
@@ -197,8 +207,9 @@ def _cfg_units(seed: int = 0):
     def c2_cpu(orc):
         def run():
             xn = orc.rownorm(x2, nw2, E, 1, 1e-6)
-            act = orc.silu_mul(orc.fx_gemv(gq.Q8_0, wg, xn, F, E), orc.fx_gemv(gq.Q8_0, wu, xn, F, E))
-            return orc.fx_gemv(gq.Q8_0, wd, act, E, F) + r2
+            act = orc.silu_mul(orc.fast_gemv(1, gq.Q8_0, wg, xn, F, E, threads),
+                               orc.fast_gemv(1, gq.Q8_0, wu, xn, F, E, threads))
+            return orc.fast_gemv(1, gq.Q8_0, wd, act, E, F, threads) + r2
         return run, ()
 
     units.append(("C2", "RMSNorm + Q8_0 SwiGLU gate/up 2x9728x2560 + down 2560x9728 + residual",
@@ -224,9 +235,10 @@ def _cfg_units(seed: int = 0):
 
     sl = 16384  # the CPU times a row slice of the head and scales it
     units.append(("C3 head", "Q6_K GEMV 151936x4096", wh.size + 4 * D3 + 4 * V, 2, c3h,
-                  lambda orc: (orc.fx_gemv, (gq.Q6_K, wh[:sl * gq.row_bytes(gq.Q6_K, D3)], x3, sl, D3), V / sl)))
+                  lambda orc: (orc.fast_gemv, (1, gq.Q6_K, wh[:sl * gq.row_bytes(gq.Q6_K, D3)], x3, sl, D3, threads),
+                               V / sl)))
     units.append(("C3 Q5_K", "Q5_K GEMV 12288x4096", w5.size + 4 * D3 + 4 * 12288, 16, c35,
-                  lambda orc: (orc.fx_gemv, (gq.Q5_K, w5, x3, 12288, D3))))
+                  lambda orc: (orc.fast_gemv, (1, gq.Q5_K, w5, x3, 12288, D3, threads))))
 
     # C4: conv over 8192 channels (3x8192 cache, 4x8192 kernel), the GDN step (32 value / 16 key heads, L2 q/k,
     # gates, gated norm) and ssm_out Q4_0 [4096 x 4096] + residual
@@ -265,7 +277,7 @@ def _cfg_units(seed: int = 0):
             yc, _ = orc.conv(cst, qkv, cw)
             y, _ = orc.gdn(state, yc[:Hk * S], yc[Hk * S:2 * Hk * S], yc[2 * Hk * S:], ba[Hv:], ba[:Hv], Hv, Hk,
                            float(1 / np.sqrt(S)), gq.GDN_L2_QK | gq.GDN_GATED | gq.GDN_GATES, dt, av, z, sw)
-            return orc.fx_gemv(gq.Q4_0, wo, y, 4096, Hv * S)
+            return orc.fast_gemv(1, gq.Q4_0, wo, y, 4096, Hv * S, threads)
         return run, ()
 
     units.append(("C4", "conv 8192 ch + GDN step (32 heads) + gated norm + ssm_out Q4_0 4096x4096 + residual",
@@ -274,10 +286,12 @@ def _cfg_units(seed: int = 0):
 
 
 def configs(args) -> int:
+    cpus = one_cpu_per_core(args.threads)
+    pin_openmp(cpus)
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle  # noqa: E402  (the CPU baseline only)
 
-    for name, desc, nbytes, copies, setup, cpu in _cfg_units():
+    for name, desc, nbytes, copies, setup, cpu in _cfg_units(len(cpus)):
         ctx = gq.Context(act_floats=1 << 21, weight_bytes=1_100_000_000, state_rows=48 * 32 * 128)
         build = setup(ctx)
         cmds = sum((build(i) for i in range(copies)), [])
@@ -293,17 +307,26 @@ def configs(args) -> int:
         spec = cpu(oracle)
         fn, fargs = spec[0], spec[1]
         scale = spec[2] if len(spec) > 2 else 1.0
-        fn(*fargs)
-        t0 = time.perf_counter()
-        fn(*fargs)
-        t_cpu = (time.perf_counter() - t0) * scale
+        old = os.sched_getaffinity(0)
+        os.sched_setaffinity(0, cpus)
+        try:
+            fn(*fargs)
+            n_cpu, t0 = 0, time.perf_counter()
+            while n_cpu == 0 or time.perf_counter() - t0 < 0.25:  # short units: average over 0.25 s of calls
+                fn(*fargs)
+                n_cpu += 1
+            t_cpu = (time.perf_counter() - t0) / n_cpu * scale
+        finally:
+            os.sched_setaffinity(0, old)
         line = {"config": name, "what": desc, "algorithmic_bytes": nbytes, "copies_rotated": copies,
                 "graph_us_per_unit": round(t_graph, 3), "graph_launches_per_unit": launches / copies,
                 "graph_GBps": round(nbytes / t_graph / 1e3, 1),
                 "graph_frac_of_8TBps": round(nbytes / t_graph / 1e3 / HBM_PEAK_GBPS, 4),
                 "single_launch_device_us": round(t_single, 3), "launches_per_unit": len(stats),
                 "cpu_oracle_s": round(t_cpu, 4), "cpu_GBps": round(nbytes / t_cpu / 1e9, 2),
-                "cpu_kind": "port (oracle, one thread)"}
+                "cpu_kind": f"port (the oracle in the reference's CPU arithmetic: GEMV rows summed sequentially in "
+                            f"FP32, int8 dots in {simd_name(oracle)}; rows split over {len(cpus)} threads, one per "
+                            f"physical core, CPUs {cpus[0]}..{cpus[-1]})", "cpu_cores": len(cpus)}
         print(json.dumps(line), flush=True)
     return 0
 

@@ -90,6 +90,9 @@ def orc() -> C.CDLL:
         _fn(lib, "orc_model_prefill", i, vp, vp, i, i)
         _fn(lib, "orc_model_generate", i, vp, vp, i, i, vp, vp)
         _fn(lib, "orc_fast_gemv", None, i, i, vp, vp, i, i, vp)
+        _fn(lib, "orc_fast_gemv_mt", None, i, i, vp, vp, i, i, vp, i)
+        _fn(lib, "orc_fast_simd", i)
+        _fn(lib, "orc_fast_set_simd", i, i)
         _fn(lib, "orc_gdn_mt", None, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i, i, fl, fl, fl, i, vp, i)
         _fn(lib, "orc_attn_mt", None, vp, vp, vp, i, i, i, i, fl, vp, i)
         _fn(lib, "orc_ref_attn", None, vp, vp, vp, i, i, i, i, fl, vp)
@@ -185,11 +188,31 @@ def fx_gemv(t: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int, blocksum
     return (y, bs, acc) if blocksums else y
 
 
-def fast_gemv(mode: int, t: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int) -> np.ndarray:
-    """The decoder's SIMD rows: mode 0 canonical (= fx_gemv), 1 reference (= ref_gemv)."""
+SIMD_AVX2, SIMD_AVX512_VNNI = 0, 1
+
+
+def simd_levels() -> list[int]:
+    """The fast rows' SIMD levels this host runs (AVX2 always; AVX-512 VNNI where the CPU has it)."""
+    L = orc()
+    prev = L.orc_fast_simd()
+    top = L.orc_fast_set_simd(SIMD_AVX512_VNNI)
+    L.orc_fast_set_simd(prev)
+    return list(range(top + 1))
+
+
+def set_simd(level: int) -> int:
+    return orc().orc_fast_set_simd(level)
+
+
+def fast_gemv(mode: int, t: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int, threads: int = 1) -> np.ndarray:
+    """The decoder's SIMD rows: mode 0 canonical (= fx_gemv), 1 reference (= ref_gemv); rows split over threads."""
     x = np.ascontiguousarray(x, F)
     y = np.empty(rows, F)
-    orc().orc_fast_gemv(mode, t, _p(np.ascontiguousarray(w, np.uint8)), _p(x), rows, cols, _p(y))
+    wp = _p(np.ascontiguousarray(w, np.uint8))
+    if threads > 1:
+        orc().orc_fast_gemv_mt(mode, t, wp, _p(x), rows, cols, _p(y), threads)
+    else:
+        orc().orc_fast_gemv(mode, t, wp, _p(x), rows, cols, _p(y))
     return y
 
 

@@ -25,6 +25,11 @@ typedef struct {
     float * dxf, * sxf;
 } orc_act;
 
+/* SIMD level of the fast rows: the highest the host supports unless lowered (returns the level in effect). */
+enum { ORC_SIMD_AVX2 = 0, ORC_SIMD_AVX512_VNNI = 1 };
+int orc_fast_simd(void);
+int orc_fast_set_simd(int level);
+
 void orc_act_init(orc_act * a, int weight_fmt, const float * x, int cols);
 void orc_act_free(orc_act * a);
 int orc_fast_supported(int fmt);
@@ -35,6 +40,9 @@ void orc_fast_rows_multi(int mode, int fmt, const uint8_t * w, const orc_act * c
                          float * y, size_t ys);
 /* Quantizes x and runs every row (the pinning entry point of the tests). */
 void orc_fast_gemv(int mode, int fmt, const uint8_t * w, const float * x, int rows, int cols, float * y);
+/* The same with the rows split over n_threads OpenMP threads (placement from OMP_PLACES / OMP_PROC_BIND). */
+void orc_fast_gemv_mt(int mode, int fmt, const uint8_t * w, const float * x, int rows, int cols, float * y,
+                      int n_threads);
 
 #ifdef __cplusplus
 }

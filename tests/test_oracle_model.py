@@ -33,7 +33,20 @@ def q35():
     return qwen35
 
 
-def test_fast_rows_match_scalar_oracle(orc, gq):
+@pytest.mark.parametrize("simd", [0, 1])
+def test_fast_rows_match_scalar_oracle(orc, gq, simd):
+    """The decoder's SIMD rows (AVX2, and AVX-512 VNNI on hosts that have it) equal the scalar oracle bit for bit."""
+    if simd not in orc.simd_levels():
+        pytest.skip("this host has no AVX-512 VNNI")
+    prev = orc.orc().orc_fast_simd()
+    assert orc.set_simd(simd) == simd
+    try:
+        _fast_rows_match(orc, gq)
+    finally:
+        orc.set_simd(prev)
+
+
+def _fast_rows_match(orc, gq):
     rng = np.random.default_rng(7)
     for t in (gq.Q4_0, gq.Q4_1, gq.Q8_0, gq.Q5_K, gq.Q6_K):
         rows, cols = 48, 2048
