@@ -285,12 +285,17 @@ def _cfg_units(threads: int = 1, seed: int = 0):
     return units
 
 
+CPU_REPS = 15  # cold-cache calls per unit on the CPU; the median is reported
+CPU_FLUSH_BYTES = 1 << 30  # read between calls, larger than any host's last-level cache
+
+
 def configs(args) -> int:
     cpus = one_cpu_per_core(args.threads)
     pin_openmp(cpus)
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle  # noqa: E402  (the CPU baseline only)
 
+    flush = np.ones(CPU_FLUSH_BYTES // 8)
     for name, desc, nbytes, copies, setup, cpu in _cfg_units(len(cpus)):
         ctx = gq.Context(act_floats=1 << 21, weight_bytes=1_100_000_000, state_rows=48 * 32 * 128)
         build = setup(ctx)
@@ -311,11 +316,13 @@ def configs(args) -> int:
         os.sched_setaffinity(0, cpus)
         try:
             fn(*fargs)
-            n_cpu, t0 = 0, time.perf_counter()
-            while n_cpu == 0 or time.perf_counter() - t0 < 0.25:  # short units: average over 0.25 s of calls
+            times = []
+            for _ in range(CPU_REPS):
+                flush.sum()  # untimed: evicts the unit's bytes from the host caches, as the GPU's rotated copies do
+                t0 = time.perf_counter()
                 fn(*fargs)
-                n_cpu += 1
-            t_cpu = (time.perf_counter() - t0) / n_cpu * scale
+                times.append(time.perf_counter() - t0)
+            t_cpu = float(np.median(times)) * scale
         finally:
             os.sched_setaffinity(0, old)
         line = {"config": name, "what": desc, "algorithmic_bytes": nbytes, "copies_rotated": copies,
@@ -326,7 +333,9 @@ def configs(args) -> int:
                 "cpu_oracle_s": round(t_cpu, 4), "cpu_GBps": round(nbytes / t_cpu / 1e9, 2),
                 "cpu_kind": f"port (the oracle in the reference's CPU arithmetic: GEMV rows summed sequentially in "
                             f"FP32, int8 dots in {simd_name(oracle)}; rows split over {len(cpus)} threads, one per "
-                            f"physical core, CPUs {cpus[0]}..{cpus[-1]})", "cpu_cores": len(cpus)}
+                            f"physical core, CPUs {cpus[0]}..{cpus[-1]}; median of {CPU_REPS} calls, each after reading "
+                            f"{CPU_FLUSH_BYTES >> 20} MiB to evict the unit's bytes from the caches)",
+                "cpu_cores": len(cpus)}
         print(json.dumps(line), flush=True)
     return 0
 

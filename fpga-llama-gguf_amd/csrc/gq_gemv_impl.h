@@ -90,13 +90,10 @@ __device__ float block_norm_scale(const float * x, int n, float eps, int l2, Lds
 template <int R, int XS>  // rounds of NT items the registers hold (cols <= 16 NT R); the prologue kind
 struct XF {
     float v[R][16];
-    float w[R <= 2 ? R : 1][16];  // NORM, ACC: the norm weight (the activation again without one); GATED: the gated
+    float w[R <= 2 ? R : 1][16];  // NORM: the norm weight (the activation again without one); GATED: the gated
                                   // norm's weight (one head, item % 8)
     float z[XS == XS_GATED ? R : 1][16];  // GATED: the output gate
-    unsigned long long acc[XS == XS_ACC ? R : 1][16];  // ACC: the fused ssm_out's row sums (v holds its residual)
 };
-
-typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ void load16(const float * p, float * v) {
     const float4 * q = reinterpret_cast<const float4 *>(p);
@@ -121,21 +118,12 @@ __device__ __forceinline__ int item_of(int g, int n16) {
 template <int R, int XS>
 __device__ __forceinline__ void prologue_fetch(const GemvHot & h, const GemvArgs & a, XF<R, XS> & f) {
     const int n16 = h.cols / 16;
-    const bool normw = (XS == XS_ACC || h.xsrc == XSRC_NORM) && h.norm_w != nullptr;  // ACC instances: always a norm
+    const bool normw = h.xsrc == XSRC_NORM && h.norm_w != nullptr;
 #pragma unroll
     for (int g = 0; g < R; ++g) {
         const int i = item_of(g, n16);
         const float * xi = h.x + size_t(i) * 16;
         load16(xi, f.v[g]);
-        if constexpr (XS == XS_ACC) {
-            const u64x2 * ap = reinterpret_cast<const u64x2 *>(a.acc + size_t(i) * 16);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const u64x2 t = ap[j];
-                f.acc[g][2 * j] = t.x;
-                f.acc[g][2 * j + 1] = t.y;
-            }
-        }
         if constexpr (XS == XS_GATED) {
             load16(h.gate_z + size_t(i) * 16, f.z[g]);
             load16(h.norm_w + size_t(i & 7) * 16, f.w[g]);
@@ -224,22 +212,6 @@ __device__ __forceinline__ float norm_scale_items(const GemvArgs & a, const XF<R
 template <int R, int XS>
 __device__ __forceinline__ void prologue_finish(const GemvArgs & a, XF<R, XS> & f, Lds & s) {
     const int n16 = a.cols / 16;
-    if constexpr (XS == XS_ACC) {
-        // the fused ssm_out's output, exactly as its ADD epilog forms it (the row rounded to FP32 once, then the
-        // residual added), stored by workgroup 0 (the ssm_out command's y); then the deferred norm as below
-#pragma unroll
-        for (int g = 0; g < R; ++g) {
-            float * v = f.v[g];
-#pragma unroll
-            for (int j = 0; j < 16; ++j) v[j] = fixed_to_float((long long)f.acc[g][j]) + v[j];
-            const int i = int(threadIdx.x) + NT * g;
-            if (blockIdx.x == 0 && i < n16) {
-                float4 * o = reinterpret_cast<float4 *>(a.x_out + size_t(i) * 16);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) o[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
-            }
-        }
-    }
     if constexpr (XS == XS_GATED) {
         // the DeltaNet gated output norm (gemvqc_gdn.h:284-346): per head of 128 (8 items, 8 lanes), x =
         // silu(z) * ((y * sc) * w) with sc = 1 / sqrt(sum(y^2) / 128 + eps); workgroup 0 also stores x, which the
@@ -273,7 +245,7 @@ __device__ __forceinline__ void prologue_finish(const GemvArgs & a, XF<R, XS> & 
             quantize_half(v, i, i < n16, s);
         }
     } else {
-        const bool norm = XS == XS_ACC || a.xsrc == XSRC_NORM, normw = norm && a.norm_w != nullptr;
+        const bool norm = a.xsrc == XSRC_NORM, normw = norm && a.norm_w != nullptr;
         const float sc = norm ? norm_scale_items<R, XS>(a, f, s) : 1.0f;  // the same on every thread
 #pragma unroll
         for (int g = 0; g < R; ++g) {
@@ -914,13 +886,6 @@ __global__ __launch_bounds__(NT) void gemv_kernel(const float * x, const float *
     const int q = int(unsigned(max(len - 1 - wv, 0)) / unsigned(max(S, 1)));
     const int n = wv < S && wv < len ? q + 1 : 0;
     const int w = s_lo + wv;
-    // ACC: the fused step's new state rows, copied from the shadow rows into the state (one float4 per thread of
-    // the grid in turn); the first is requested with the activation and stored once the prologue is done
-    const int cp_i = int(blockIdx.x) * NT + int(threadIdx.x), cp_s = int(gridDim.x) * NT;
-    float4 cp_v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if constexpr (XS == XS_ACC) {
-        if (cp_i < a.cp_n) cp_v = a.cp_src[cp_i];
-    }
     Slot<TYPE, NU, PAIR> sl[DS];  // the first D rows (a wave without rows reloads the member's last row)
 #pragma unroll
     for (int j = 0; j < DS; ++j)
@@ -930,10 +895,6 @@ __global__ __launch_bounds__(NT) void gemv_kernel(const float * x, const float *
         quantize_q8_K(h.x, h.cols, h.xsrc == XSRC_NORM, h.norm_w, scale, s.xq, s.bs, s.info);
     } else {
         prologue_finish<RX, XS>(a, xf, s);
-    }
-    if constexpr (XS == XS_ACC) {
-        if (cp_i < a.cp_n) a.cp_dst[cp_i] = cp_v;
-        for (int i = cp_i + cp_s; i < a.cp_n; i += cp_s) a.cp_dst[i] = a.cp_src[i];
     }
     __syncthreads();
     XB xb[KQ ? 1 : NU];
@@ -1096,8 +1057,7 @@ hipError_t launch_slots(const GemvArgs & a, hipStream_t st) {
     return launch_typed<TYPE, NU, PAIR, XS, 1>(a, st);
 }
 
-// The gated activation prologue exists for Q4_0 / Q8_0 rows of at most 8192 columns without a SwiGLU pair; the
-// accumulator prologue for Q4_0 / Q8_0 rows of at most 4096 columns.
+// The gated activation prologue exists for Q4_0 / Q8_0 rows of at most 8192 columns without a SwiGLU pair.
 template <int TYPE, int NU>
 hipError_t launch_pair(const GemvArgs & a, hipStream_t st) {
     bool pair = false;
@@ -1106,11 +1066,6 @@ hipError_t launch_pair(const GemvArgs & a, hipStream_t st) {
         if constexpr ((TYPE == T_Q4_0 || TYPE == T_Q8_0) && NU <= 4) {
             if (!pair) return launch_slots<TYPE, NU, false, XS_GATED>(a, st);
         }
-        return hipErrorInvalidValue;
-    }
-    if (a.xsrc == XSRC_ACC) {
-        if constexpr ((TYPE == T_Q4_0 || TYPE == T_Q8_0) && NU <= 2)
-            return pair ? launch_slots<TYPE, NU, true, XS_ACC>(a, st) : launch_slots<TYPE, NU, false, XS_ACC>(a, st);
         return hipErrorInvalidValue;
     }
     return pair ? launch_slots<TYPE, NU, true, XS_PLAIN>(a, st) : launch_slots<TYPE, NU, false, XS_PLAIN>(a, st);

@@ -1067,6 +1067,9 @@ struct Emitter {
         if (!output(p.gated ? p.gated : node, y)) return false;
         const uint32_t flags = (p.l2 ? GEMVQ_GDN_L2_QK : 0u) | (p.gated ? GEMVQ_GDN_GATED : 0u) | (gates ? GEMVQ_GDN_GATES : 0u) |
                                (p.gate_silu ? GEMVQ_GDN_Z_SILU : 0u);
+        // GEMVQ_GDN_WITH_OUT, which the reference sets for the ssm_out GEMV right behind the step
+        // (ggml-xrt.cpp:2259-2270), is left clear: on this GPU the fused launch is slower in graph replays than the
+        // step and the gated GEMV as two launches
         push({GEMVQ_OP_GDN, hv | (hk << 16), qo, ko, vo, go, bo, y});
         push({uint32_t(src_row), uint32_t(dst_row), fbits(1.0f / std::sqrt(float(HEAD))), flags, fbits(p.l2_eps),
               fbits(p.rms_eps), wo, zo});

@@ -23,12 +23,10 @@ struct WeightView {
 };
 
 enum : int { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_ADD = 2, EPI_CONV = 3, EPI_SILU = 4 };
-// XSRC_GATED: gate_silu says whether z is silu(z). XSRC_ACC: the activation is the deferred norm of
-// fixed_to_float(acc) + x (a fused DeltaNet step + ssm_out left its exact row sums in acc); workgroup 0 also
-// stores that sum to x_out (the ssm_out command's residual-added output).
-enum : int { XSRC_RAW = 0, XSRC_NORM = 1, XSRC_GATED = 2, XSRC_ACC = 3 };
+// XSRC_GATED: gate_silu says whether z is silu(z).
+enum : int { XSRC_RAW = 0, XSRC_NORM = 1, XSRC_GATED = 2 };
 // Prologue kinds of the GEMV kernel instances.
-enum : int { XS_PLAIN = 0, XS_GATED = 1, XS_ACC = 2 };
+enum : int { XS_PLAIN = 0, XS_GATED = 1 };
 
 struct GemvMember {
     WeightView w;    // matrix (g of a SwiGLU pair)
@@ -64,13 +62,6 @@ struct GemvArgs {
     GemvMember m[4];
     unsigned long long * argmax_key;  // non-NULL: argmax over member 0's y
     int32_t * dbg;                    // non-NULL: integer block sums of member 0
-    // XSRC_ACC (last, so the fields every launch reads keep their places): the fused ssm_out's fixed-point row sums
-    // (LSB 2^-40; x is its residual), and the state rows the fused step left in the shadow rows, copied back into
-    // the state rows by the launch's threads (cp_n float4s; 0: none)
-    const unsigned long long * acc;
-    const float4 * cp_src;
-    float4 * cp_dst;
-    int cp_n;
     float wbound[4];  // per member (Q4_0 / Q4_1 / Q8_0): the largest block term magnitude over |d_x| * 2^40
 };
 
@@ -136,13 +127,18 @@ struct GdnArgs {
                            // dst + t * hv * 128 rows), all in one launch
 };
 
-// The DeltaNet step, its gated output norm and the ssm_out product in one launch (the reference's GDN_WITH_OUT,
-// gemvqc16.h:75-81, gemvqc16.cpp:872-903): `parts` workgroups per value head each run the head's step, normalize and
-// gate its 128 outputs, quantize them to Q8_0 and multiply them with their share of the rows of the head's 128
-// columns of ssm_out; each row's exact fixed-point terms are added into acc with integer atomics (order-free, so the
-// sums are those of one GEMV). Every workgroup of a head reads all of the head's state rows, so a workgroup stores
-// its 128 / parts rows of the new state to `shadow` (the dst layout); when shadow is the state itself (src != dst)
-// nothing more is needed, else the launch that consumes acc copies the shadow rows into dst.
+// The DeltaNet step, its gated output norm, the ssm_out product and its residual sum in one launch (the reference's
+// GDN_WITH_OUT, gemvqc16.h:75-81, gemvqc16.cpp:872-903): out = ssm_out(gated norm(step)) + res. Workgroup h < hv
+// steps value head h (its state rows read and written once, in place when src == dst), normalizes, gates and
+// quantizes the head's 128 outputs and publishes the quants in the exchange area; every workgroup holds 16 rows of
+// ssm_out in registers, waits for all heads and forms its rows (exact fixed-point sums, rounded once, plus res).
+constexpr int GDN_OUT_MAX_HEADS = 32;   // value heads (hv a multiple of 4)
+constexpr int GDN_OUT_MAX_ROWS = 16384;
+// Exchange area: two slots, each GDN_XCH_COPIES copies (one per XCD) of GDN_XCH_SLOT 64-bit words; head h's words
+// are h * 36 + j: its 32 words of quants, then its 4 block words, each as tag | word (tag zero: not yet published).
+constexpr int GDN_XCH_SLOT = 36 * GDN_OUT_MAX_HEADS;
+constexpr int GDN_XCH_COPIES = 8;
+constexpr int GDN_XCH_WORDS = 2 * GDN_XCH_COPIES * GDN_XCH_SLOT;
 struct GdnOutArgs {
     GdnArgs g;                  // one token; g.y is not used
     const float * z;            // the output gate (silu(z) when z_silu)
@@ -151,12 +147,15 @@ struct GdnOutArgs {
     int z_silu;
     float * y;                  // the gated output [hv * 128] (the GDN command's y)
     WeightView w;               // ssm_out, rows x (hv * 128), Q4_0 or Q8_0
-    int rows;
-    unsigned long long * acc;   // [rows], zero on entry
-    unsigned long long * zero;  // the other accumulator [rows], cleared for the next fused pair
-    float * shadow;             // where the new state rows go (dst, or a buffer of hv * 128 rows when src == dst)
-    int parts;                  // workgroups per head: a divisor of 128, rows / parts <= 1024
+    int rows;                   // a multiple of 16, at least 16 * hv
+    const float * res;          // residual [rows]
+    float * out;                // ssm_out + res [rows] (res itself, or apart from it)
+    unsigned long long * xch;   // exchange area (GDN_XCH_WORDS), both slots' tags zero before the list's first launch
+    int slot;                   // the exchange slot of this launch (0 or 1, in turn over a list's fused launches)
+    uint32_t * fault;           // host word set to 1 when a workgroup's wait for the heads ran out of polls
+    unsigned polls;             // the bound of that wait
 };
+bool gdn_out_fits(int hv, int rows);  // the fused launch serves hv value heads and `rows` ssm_out rows
 
 struct GatedNormArgs {    // per head of 128: y = silu(z) * ((y * s) * w), s = 1 / sqrt(mean(y^2) + eps)
     float * y;
@@ -306,7 +305,6 @@ hipError_t launch_rope(const RopeArgs & a, hipStream_t s);
 hipError_t launch_gdn(const GdnArgs & a, hipStream_t s);
 hipError_t launch_gated_norm(const GatedNormArgs & a, hipStream_t s);
 hipError_t launch_gdn_out(const GdnOutArgs & a, int type, hipStream_t s);
-int gdn_out_parts(int rows);  // workgroups per head for an ssm_out of `rows` rows
 hipError_t launch_attn(const AttnArgs & a, hipStream_t s);
 hipError_t launch_get_rows(const GetRowsArgs & a, hipStream_t s);
 hipError_t launch_argmax(const float * x, int n, unsigned long long * key, int rows, int stride, hipStream_t s);

@@ -114,8 +114,9 @@ struct gemvq_ctx {
     float * gdn_raw = nullptr;    // raw DeltaNet output when its gated norm is folded into the next GEMV
     float * dsnap = nullptr;      // a deferred norm's row, computed before a command overwrote its source
     float * xsnap = nullptr;      // a GEMV group's activation, copied before a member overwrites it
-    unsigned long long * acc[2] = {nullptr, nullptr};  // fused DeltaNet step + ssm_out row sums, used in turn
-    float * gdn_shadow = nullptr;  // the fused step's new state rows of an in-place step (GDN_MAX_HEADS * 128 rows)
+    unsigned long long * gdn_xch = nullptr;  // the fused DeltaNet step + ssm_out's exchange area (GDN_XCH_WORDS, zero)
+    uint32_t * gdn_fault = nullptr;  // host word the fused launch sets when a wait for its heads ran out of polls
+    unsigned xch_polls = 0;          // that wait's bound in polls (set at creation)
     int8_t * gemm_q = nullptr;    // a batched GEMV's quantized activation rows (GEMM_MAX_TOK x GEMV_MAXK)
     float * gemm_d = nullptr;     // and their block scales
     float * gemm_s = nullptr;     // and their Q8_1 block sums (for Q4_1 weights)
@@ -154,7 +155,15 @@ int wait_stream(gemvq_ctx * c, const char * what) {
     const auto deadline = std::chrono::steady_clock::now() + std::chrono::milliseconds(c->wait_ms);
     for (;;) {
         const hipError_t e = hipStreamQuery(c->stream);
-        if (e == hipSuccess) return 0;
+        if (e == hipSuccess) {
+            if (c->gdn_fault && __atomic_load_n(c->gdn_fault, __ATOMIC_ACQUIRE)) {
+                c->err = std::string(what) + ": a fused DeltaNet step + ssm_out launch's wait for its heads ran out "
+                         "of polls (its output was not written)";
+                c->usable = false;
+                return GEMVQ_ETIMEDOUT;
+            }
+            return 0;
+        }
         if (e != hipErrorNotReady) return fail(c, e, what);
         if (std::chrono::steady_clock::now() > deadline) {
             c->err = std::string(what) + ": the device did not finish within " + std::to_string(c->wait_ms) + " ms";
@@ -404,65 +413,33 @@ struct Compiler {
     // (written by workgroup 0 of that group), computed from the raw step output (a private buffer), z and w.
     struct Gated { bool on = false; uint32_t y, cols; const float * z; const float * w; float eps; int z_silu; } gated;
 
-    std::vector<Rng> acc_ranges() const {  // what the accumulator prologue reads and writes in the act buffer
-        std::vector<Rng> r = {{accp.y, uint64_t(accp.y) + accp.rows}, {accp.res, uint64_t(accp.res) + accp.rows}};
-        if (defer.on && !(defer.flags & GEMVQ_NORM_NO_WEIGHT)) r.push_back({defer.w, uint64_t(defer.w) + defer.n});
-        return r;
-    }
-
     std::vector<Rng> gated_ranges() const {
         const uint64_t z = uint64_t(gated.z - c->act), w = uint64_t(gated.w - c->act);
         return {{gated.y, gated.y + uint64_t(gated.cols)}, {z, z + gated.cols}, {w, w + 128}};
     }
 
-    // The fused DeltaNet step + ssm_out pending for the GEMV group whose prologue forms the ssm_out output: y =
-    // fixed_to_float(acc) + res, the deferred norm of y being that group's activation.
-    struct AccOut {
-        bool on = false;
-        uint32_t y, res, rows;
-        unsigned long long * acc;
-        const float * cp_src;  // the shadow rows of an in-place step, copied into cp_dst by the consuming launch
-        float * cp_dst;
-        int cp_n;              // float4s (0: the step wrote its state rows itself)
-    } accp;
-    int accn = 0;        // fused pairs so far: pair j accumulates into acc[j % 2] and clears the other
-    uint32_t acc_rows = 0;
-
     // The DeltaNet layer shape the fused step + ssm_out serves (the reference's GDN_WITH_OUT, gemvqc16.cpp:872-903):
     // the one-token GDN with the gated norm whose next command `next` is a Q4_0 / Q8_0 GEMV on its whole output
-    // with the ADD epilog into y apart from the residual (rows at most 4096 that the fused kernel splits into whole
-    // rounds: a multiple of 1024), followed by a deferred RMSNORM of y and a GEMV on that norm whose pass neither
-    // writes nor reads y, the residual or the norm weight.
-    // Then nothing between the GDN and that GEMV reads y, which that GEMV's prologue forms.
-    bool fuse_out(const uint32_t * cmds, unsigned n, unsigned next, uint32_t gy, uint32_t cols, uint32_t & y,
-                  uint32_t & res) const {
-        if (next + 3 >= n) return false;
+    // (hv a multiple of 4 up to 32, rows a multiple of 16 and at least 16 hv) with the ADD epilog, its ADD writing
+    // y2 = ssm_out + res. Every workgroup of the fused launch reads its rows' residuals at its start and writes y2
+    // after all heads are stepped, so y2 is res itself or apart from it, and neither meets anything the step reads
+    // or writes (q, k, v, the gates, z, the norm weight, y). y2 and res are returned.
+    bool fuse_out(const uint32_t * cmds, unsigned n, unsigned next, const std::vector<Rng> & step_io, uint32_t gy,
+                  uint32_t hv, uint32_t & y2, uint32_t & res) const {
+        if (next + 1 >= n) return false;
         const uint32_t * g = cmds + size_t(next) * GEMVQ_CMD_WORDS, * e = g + GEMVQ_CMD_WORDS;
-        const uint32_t * r = e + GEMVQ_CMD_WORDS, * u = r + GEMVQ_CMD_WORDS;
         const int t = int(g[1] & 0xffu);
         const uint32_t rows = g[2];
         const uint64_t woff = uint64_t(g[4]) | (uint64_t(g[5]) << 32);
         if (g[0] != GEMVQ_OP_GEMV || (g[1] & ~0xffu) != GEMVQ_GEMV_ADD || (t != T_Q4_0 && t != T_Q8_0) || g[6] != gy ||
-            g[3] != cols || rows > 4096 || gdn_out_parts(int(rows)) == 0 || !weight(woff, t, int(rows), int(cols)))
+            g[3] != hv * 128 || !gdn_out_fits(int(hv), int(rows)) || !weight(woff, t, int(rows), int(hv * 128)))
             return false;
-        // each fused pair clears the other accumulator's first `rows` entries for the next pair, so every pair of a
-        // list must have the same row count (else a later pair could add onto sums a wider pair left behind)
-        if (accn > 0 && rows != acc_rows) return false;
         if (e[0] != GEMVQ_OP_ADD || e[1] != rows || (e[2] != g[7] && e[3] != g[7])) return false;
         res = e[2] == g[7] ? e[3] : e[2];
-        y = e[4];
-        if (!range(res, rows) || !range(y, rows) || meet({y, uint64_t(y) + rows}, {res, uint64_t(res) + rows})) return false;
-        const uint32_t nf = r[7];
-        if (r[0] != GEMVQ_OP_RMSNORM || !(nf & GEMVQ_NORM_DEFER) || (nf & GEMVQ_NORM_L2) || r[6] > 1 || ((nf >> 8) & 0xffffu) ||
-            r[1] != rows || r[2] != y || (!(nf & GEMVQ_NORM_NO_WEIGHT) && !range(r[3], rows)))
+        y2 = e[4];
+        if (!range(res, rows) || !range(y2, rows) || (y2 != res && meet({y2, uint64_t(y2) + rows}, {res, uint64_t(res) + rows})))
             return false;
-        const int tu = int(u[1] & 0xffu);
-        if (u[0] != GEMVQ_OP_GEMV || u[6] != r[4] || u[3] != rows || (tu != T_Q4_0 && tu != T_Q8_0)) return false;
-        std::vector<Rng> wr, rd;
-        gemv_io(cmds, n, next + 3, wr, rd);
-        std::vector<Rng> pro = {{y, uint64_t(y) + rows}, {res, uint64_t(res) + rows}};
-        if (!(nf & GEMVQ_NORM_NO_WEIGHT)) pro.push_back({r[3], uint64_t(r[3]) + rows});
-        return !meet_any(wr, pro) && !meet_any(rd, pro);
+        return !meet_any({{y2, uint64_t(y2) + rows}, {res, uint64_t(res) + rows}}, step_io);
     }
 
     // The command at `next` is a Q4_0 / Q8_0 GEMV that reads exactly the GDN output y (cols = heads * 128 <= 8192)
@@ -506,6 +483,8 @@ struct Compiler {
     // on the same rows (same norm) reuses the scratch instead of quantizing again.
     struct LastQuant { bool on = false; GemmQuantArgs q; uint32_t x_off, x_len; } lastq;
 
+    int fused_out = 0;  // fused DeltaNet step + ssm_out launches so far: launch j uses exchange counter slot j % 2
+
     bool compile(const uint32_t * cmds, unsigned n) {
         for (unsigned i = 0; i < n;) {
             const size_t before = out.size();
@@ -521,9 +500,9 @@ struct Compiler {
                 if (meet_any(wr, defer_ranges())) defer.dirty = long(out.size() == before && before > 0 ? before - 1 : before);
             }
         }
-        if (accp.on) return reject(n - 1, "internal: a fused DeltaNet output was not consumed");
-        if (accn % 2) {  // the last fused pair used acc[0]: clear it for the next run of the list (acc[1] is clear)
-            EwArgs z{nullptr, nullptr, reinterpret_cast<float *>(c->acc[0]), int(2 * acc_rows), 0, 0, EW_FILL, 0.0f};
+        if (fused_out % 2) {  // the last fused launch used slot 0: clear its tags for the next list (slot 1 is clear)
+            EwArgs z{nullptr, nullptr, reinterpret_cast<float *>(c->gdn_xch), 2 * GDN_XCH_COPIES * GDN_XCH_SLOT, 0, 0,
+                     EW_FILL, 0.0f};
             out.push_back(LEw{z});
             spans.push_back({int(n) - 1, 1});
         }
@@ -669,10 +648,18 @@ struct Compiler {
                     i = next;
                     return true;
                 }
-                if ((flags & GEMVQ_GDN_GATED) && (flags & GEMVQ_GDN_WITH_OUT) && ntok == 1 && !accp.on &&
-                    fuse_out(cmds, n, next, k[7], hv * 128, fy, fres)) {
-                    // asked for with GEMVQ_GDN_WITH_OUT: the step, the gated norm and ssm_out in one launch; the GEMV
-                    // group on the norm that follows forms the ssm_out output from the accumulated row sums
+                // what the step reads and writes in the act buffer (the fused launch's rows must stay apart)
+                std::vector<Rng> step_io = {{k[2], uint64_t(k[2]) + hk * 128}, {k[3], uint64_t(k[3]) + hk * 128},
+                                            {k[4], uint64_t(k[4]) + hv * 128}, {k[5], uint64_t(k[5]) + hv},
+                                            {k[6], uint64_t(k[6]) + hv}, {k[7], uint64_t(k[7]) + hv * 128},
+                                            {k2[6], uint64_t(k2[6]) + 128}, {k2[7], uint64_t(k2[7]) + hv * 128}};
+                if (gates) {
+                    step_io.push_back({k3[0], uint64_t(k3[0]) + hv});
+                    step_io.push_back({k3[1], uint64_t(k3[1]) + hv});
+                }
+                if ((flags & GEMVQ_GDN_GATED) && (flags & GEMVQ_GDN_WITH_OUT) && ntok == 1 &&
+                    fuse_out(cmds, n, next, step_io, k[7], hv, fy, fres)) {
+                    // asked for with GEMVQ_GDN_WITH_OUT: the step, the gated norm, ssm_out and its ADD in one launch
                     const uint32_t * g = cmds + size_t(next) * GEMVQ_CMD_WORDS;
                     const int t = int(g[1] & 0xffu);
                     GdnOutArgs o{};
@@ -684,18 +671,14 @@ struct Compiler {
                     o.y = A(k[7]);
                     o.rows = int(g[2]);
                     o.w = weight_view(c->warena + (uint64_t(g[4]) | (uint64_t(g[5]) << 32)), t, o.rows, int(hv * 128));
-                    o.acc = c->acc[accn % 2];
-                    o.zero = c->acc[(accn + 1) % 2];
-                    // every workgroup of a head reads all its state rows: an in-place step writes the new rows
-                    // to the shadow rows, which the consuming launch copies into the state
-                    const bool in_place = src == dst;
-                    o.shadow = in_place ? c->gdn_shadow : a.dst;
-                    o.parts = gdn_out_parts(o.rows);
+                    o.res = A(fres);
+                    o.out = A(fy);
+                    o.xch = c->gdn_xch;
+                    o.fault = c->gdn_fault;
+                    o.polls = c->xch_polls;
+                    o.slot = fused_out++ % 2;
                     out.push_back(LGdnOut{o, t});
                     spans.push_back({int(i), int(next + 2 - i)});
-                    accp = {true, fy, fres, g[2], o.acc, c->gdn_shadow, a.dst, in_place ? int(hv * 128 * 32) : 0};
-                    ++accn;
-                    acc_rows = std::max(acc_rows, g[2]);
                     i = next + 2;
                     return true;
                 }
@@ -1180,7 +1163,6 @@ struct Compiler {
             // workgroup 0 writes the gated activation while the group runs, from z and the norm weight: no member
             // may write or read those
             if (gated.on && gemvs > 0 && (meet_any(mw, gated_ranges()) || meet_any(mr, gated_ranges()))) break;
-            if (accp.on && gemvs > 0 && (meet_any(mw, acc_ranges()) || meet_any(mr, acc_ranges()))) break;
             if (gated.on && (flags & GEMVQ_GEMV_SWIGLU)) break;
             if (gemvs == 0) {
                 type = t;
@@ -1266,20 +1248,6 @@ struct Compiler {
             a.x_out = A(gated.y);
             a.gate_silu = gated.z_silu;
             gated.on = false;
-        } else if (accp.on && defer.on && !defer.snap && defer.x == accp.y && defer.y == x_off && defer.n == cols) {
-            // the fused DeltaNet step + ssm_out left its row sums in acc: this prologue forms y = acc + res (stored
-            // by workgroup 0) and quantizes its deferred norm
-            a.xsrc = XSRC_ACC;
-            a.x = A(accp.res);
-            a.acc = accp.acc;
-            a.x_out = A(accp.y);
-            a.cp_src = reinterpret_cast<const float4 *>(accp.cp_src);
-            a.cp_dst = reinterpret_cast<float4 *>(accp.cp_dst);
-            a.cp_n = accp.cp_n;
-            a.norm_w = (defer.flags & GEMVQ_NORM_NO_WEIGHT) ? nullptr : A(defer.w);
-            a.norm_eps = defer.eps;
-            a.norm_l2 = 0;
-            accp.on = false;
         } else if (defer.on && defer.y == x_off && defer.n == cols) {
             // every workgroup reads the norm's row and weight in its prologue while others store rows: with a member
             // writing over them, or after an earlier command did, the launch reads the snapshot instead
@@ -1327,8 +1295,6 @@ std::pair<std::string, uint64_t> describe(const Launch & l, int pos) {
         const bool kq = g->type == T_Q5_K || g->type == T_Q6_K;
         const int nu = (a.cols / (kq ? 64 : 32) + 63) / 64;
         uint64_t b = uint64_t(a.cols) * 4 * (a.xsrc == XSRC_GATED ? 3 : a.xsrc == XSRC_NORM && a.norm_w ? 2 : 1);
-        if (a.xsrc == XSRC_ACC)  // acc, residual, y, weight; the shadow state rows read and written
-            b = uint64_t(a.cols) * (8 + 4 + 4 + (a.norm_w ? 4 : 0)) + uint64_t(a.cp_n) * 32;
         for (int i = 0; i < a.n_members; ++i) {
             const GemvMember & m = a.m[i];
             const uint64_t rows = uint64_t(m.rows);
@@ -1454,9 +1420,23 @@ gemvq_ctx * gemvq_ctx_create(int device, size_t act_floats, size_t weight_bytes,
         }
         wait_ms = unsigned(ms);
     }
+    // the bound of the fused DeltaNet launch's in-kernel wait for its heads, in polls of at least a microsecond: 1000
+    // per millisecond of the wait bound, at most 2^22 (seconds, against the microseconds the heads take); or
+    // GEMVQ_EXCHANGE_POLLS (0 makes every such wait fail at once, which tests use to reach the failure path)
+    unsigned polls = wait_ms >= 4194u ? 4194304u : wait_ms * 1000u;
+    if (const char * v = std::getenv("GEMVQ_EXCHANGE_POLLS")) {
+        char * end = nullptr;
+        const unsigned long p = std::strtoul(v, &end, 10);
+        if (end == v || *end != '\0' || p > 0xffffffffUL) {
+            g_create_error = "gemvq_ctx_create: GEMVQ_EXCHANGE_POLLS must be a non-negative integer";
+            return nullptr;
+        }
+        polls = unsigned(p);
+    }
     auto * c = new gemvq_ctx();
     c->device = device;
     c->wait_ms = wait_ms;
+    c->xch_polls = polls;
     hipError_t e = hipSetDevice(device);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipMalloc(&c->act, std::max<size_t>(act_floats, 16) * sizeof(float));
@@ -1466,11 +1446,10 @@ gemvq_ctx * gemvq_ctx_create(int device, size_t act_floats, size_t weight_bytes,
     if (e == hipSuccess) e = hipMalloc(&c->gdn_raw, size_t(GDN_MAX_HEADS) * 128 * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&c->dsnap, size_t(GEMV_MAXK) * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&c->xsnap, size_t(GEMV_MAXK) * sizeof(float));
-    for (int i = 0; i < 2 && e == hipSuccess; ++i) {
-        e = hipMalloc(&c->acc[i], size_t(GEMV_MAXK) * 8);
-        if (e == hipSuccess) e = hipMemset(c->acc[i], 0, size_t(GEMV_MAXK) * 8);
-    }
-    if (e == hipSuccess) e = hipMalloc(&c->gdn_shadow, size_t(GDN_MAX_HEADS) * 128 * 128 * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&c->gdn_xch, size_t(GDN_XCH_WORDS) * 8);
+    if (e == hipSuccess) e = hipMemset(c->gdn_xch, 0, size_t(GDN_XCH_WORDS) * 8);
+    if (e == hipSuccess) e = hipHostMalloc(&c->gdn_fault, sizeof(uint32_t), hipHostMallocCoherent);
+    if (e == hipSuccess) *c->gdn_fault = 0;
     if (e == hipSuccess) e = hipMalloc(&c->gemm_q, size_t(GEMM_MAX_TOK) * GEMV_MAXK);
     if (e == hipSuccess) e = hipMalloc(&c->gemm_d, size_t(GEMM_MAX_TOK) * (GEMV_MAXK / 32) * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&c->gemm_s, size_t(GEMM_MAX_TOK) * (GEMV_MAXK / 32) * sizeof(float));
@@ -1508,9 +1487,8 @@ void gemvq_ctx_destroy(gemvq_ctx * c) {
     hipFree(c->gdn_raw);
     hipFree(c->dsnap);
     hipFree(c->xsnap);
-    hipFree(c->acc[0]);
-    hipFree(c->acc[1]);
-    hipFree(c->gdn_shadow);
+    hipFree(c->gdn_xch);
+    if (c->gdn_fault) hipHostFree(c->gdn_fault);
     hipFree(c->gemm_q);
     hipFree(c->gemm_d);
     hipFree(c->gemm_s);

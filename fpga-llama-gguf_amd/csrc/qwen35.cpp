@@ -4,7 +4,8 @@
 // projections of a layer right after its norm) in the fused forms of the reference kernel (fpga/src/gemvqc16.h):
 //   DeltaNet layer: deferred RMSNORM -> GEMV group {qkv + CONV epilog, z + SiLU epilog, beta, alpha} -> GDN (L2
 //                   q/k, gates, gated output norm on silu(z)) -> ssm_out GEMV + residual ADD epilog (the runtime
-//                   applies the gated norm in that GEMV's activation prologue)
+//                   applies the gated norm in that GEMV's activation prologue; GDN_WITH_OUT, the step and ssm_out in
+//                   one launch, is not asked for: in graph replays it is slower than the two launches)
 //   attention layer: deferred RMSNORM -> GEMV group {q+gate, k, v} -> ATTN (q/k norm, RoPE, KV append, softmax,
 //                   sigmoid gate) -> attn_output GEMV + ADD
 //   both: deferred RMSNORM -> {ffn_gate, ffn_up} SwiGLU pair -> ffn_down GEMV + ADD

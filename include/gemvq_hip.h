@@ -43,12 +43,12 @@
  *             q / k / v at t * qkv_stride, its g / beta at t * gb_stride, its y and z rows packed (hv * 128 apart);
  *             the gated norm then covers every token's heads. GEMVQ_GDN_WITH_GEMV is accepted (the results are
  *             those of the commands run one by one). GEMVQ_GDN_WITH_OUT (16, as gemvqc16.h:75-81) on a one-token
- *             GDN with the gated norm asks for the step, the norm and the ssm_out GEMV that follows in one launch
- *             when the list has the shape [GDN, GEMV (Q4_0 / Q8_0, x = the step's y, rows a multiple of 1024, at
- *             most 4096) + GEMVQ_GEMV_ADD, its ADD into y2 apart from the residual, a deferred RMSNORM of y2, a
- *             GEMV group on that norm that neither reads nor writes y2, the residual or the norm weight]: the row
- *             sums are accumulated exactly and the group's prologue forms y2; other shapes run unfused. Either
- *             way the results are the bits of the commands run one by one.
+ *             GDN with the gated norm asks for the step, the norm, the ssm_out GEMV that follows and its residual
+ *             ADD in one launch when the list has the shape [GDN (H_v a multiple of 4, at most 32), GEMV (Q4_0 /
+ *             Q8_0, x = the step's y, rows a multiple of 16, at least 16 H_v, at most 16384) + GEMVQ_GEMV_ADD,
+ *             its ADD into y2], y2 being the residual itself or apart from it, and neither meeting the step's
+ *             operands or y; other shapes run unfused. Either way the results are the bits of the commands run
+ *             one by one.
  *             GEMVQ_GDN_Z_SILU (32): z_off already holds silu(z), the gated norm multiplies by it directly. A GDN with
  *             the gated norm followed by a Q4_0 / Q8_0 GEMV reading its y applies the norm in that GEMV's activation
  *             prologue (one launch less; y is still written).

@@ -1,7 +1,14 @@
-"""The fused DeltaNet step + gated norm + ssm_out that GDN_WITH_OUT asks for (one launch, exact row sums accumulated
-with integer atomics, the sum formed in the next GEMV group's prologue) against the oracle bit for bit: a whole
-DeltaNet layer at the 9B widths with a 2048-wide FFN, run twice in a row, with one and two layers per list, Q4_0 and
-Q8_0 ssm_out; without the flag, or with the sum written over its residual, the same layer runs unfused."""
+"""The fused DeltaNet step + gated norm + ssm_out + residual sum that GDN_WITH_OUT asks for (one launch: the heads'
+workgroups publish their quantized outputs, every workgroup forms its ssm_out rows from all of them) against the
+oracle bit for bit: a whole DeltaNet layer at the 9B widths with a 2048-wide FFN, run twice in a row (the exchange
+counters are clear again after each launch), with one and two layers per list, Q4_0 and Q8_0 ssm_out, the sum
+written apart from its residual or over it (as the decoder does); without the flag, or with the sum partly over its
+residual, or over the output gate the step reads, the same layer runs unfused with the same bits. A wait for the heads that runs out of polls latches the
+context."""
+import os
+import subprocess
+import sys
+
 import numpy as np
 import pytest
 
@@ -98,12 +105,12 @@ def test_fused_deltanet_layers_match_oracle(gq, orc, wtype, n_layers):
         ctx.write(X, x)
         states = [L.state for L in layers]
         csts = [L.cst for L in layers]
-        for run in range(2):  # the accumulators must be clear again after a run
+        for run in range(2):  # the exchange counters must be clear again after a launch
             print(f"[fused] {n_layers} layer(s), ssm_out type {wtype}, run {run}", flush=True)
             assert ctx.run(cmds) == 0, ctx.error()
-            # per layer: the projection group, the fused step + ssm_out, the FFN pair, the down projection; an
-            # odd number of fused pairs clears the first accumulator once more at the end
-            assert ctx.launch_count() == 4 * n_layers + (n_layers % 2)
+            # per layer: the projection group, the fused step + ssm_out, the FFN pair, the down projection; an odd
+            # number of fused launches ends with a fill of the first exchange counter slot
+            assert ctx.launch_count() == 4 * n_layers + n_layers % 2
             for i, L in enumerate(layers):
                 x, st, ns, y, h2 = L.oracle(orc, x, states[i], csts[i])
                 states[i], csts[i] = st, ns
@@ -116,29 +123,70 @@ def test_fused_deltanet_layers_match_oracle(gq, orc, wtype, n_layers):
         ctx.close()
 
 
-@pytest.mark.parametrize("case", ["no_flag", "in_place"])
-def test_unfused_forms(gq, orc, case):
-    """Without GDN_WITH_OUT, or with ssm_out's residual sum written over its own residual, the unfused path (step,
-    gated ssm_out GEMV) runs, with the same bits."""
+@pytest.mark.parametrize("case", ["no_flag", "in_place", "over_z"])
+def test_fused_and_unfused_forms(gq, orc, case):
+    """Without GDN_WITH_OUT, or with ssm_out's residual sum written over the output gate z (which the step's gated
+    norm reads), the unfused path runs; with the sum written over its own residual (the decoder's form) the fused
+    launch runs. Either way the bits are the oracle's."""
     ctx = gq.Context(act_floats=1 << 19, weight_bytes=200 << 20, state_rows=HV * 128)
     try:
-        L = Layer(gq, 30, 2, E)
+        L = Layer(gq, 30, 2, 2 * E)
         L.upload(ctx, 0)
         w = np.array(L.commands(gq, 0, with_out=case != "no_flag"), np.uint32).reshape(-1, 8)
-        if case == "in_place":
+        h2 = L.O["h2"]
+        if case != "no_flag":
+            h2 = 0 if case == "in_place" else L.O["z"]
             add = [i for i in range(len(w)) if w[i][0] == gq.OP_ADD][0]
-            w[add][4] = 0  # the ssm_out sum goes back into x (in place)
-            w[add + 1][2] = 0  # the FFN norm reads x
-            w[-1][3] = 0  # the down projection's residual is x
+            w[add][4] = h2  # the ssm_out sum over x, or over z
+            w[add + 1][2] = h2  # the FFN norm reads it
+            w[-1][3] = h2  # the down projection's residual is it
         x = gq.normal(30, 1, E)
         ctx.write(0, x)
+        print(f"[fused] form {case}", flush=True)
         assert ctx.run(w.ravel().tolist()) == 0, ctx.error()
-        assert ctx.launch_count() == 5  # group, step, gated ssm_out, FFN pair, down
-        xo, st, ns, y, h2 = L.oracle(orc, x, L.state, L.cst)
+        xo, st, ns, y, h2v = L.oracle(orc, x, L.state, L.cst)
         assert_bits(ctx.read(0, E), xo, "layer output")
         assert_bits(ctx.state_read(0, HV * 128), st, "state")
         assert_bits(ctx.read(L.O["y"], HV * S), y, "gated output")
         if case == "no_flag":
-            assert_bits(ctx.read(L.O["h2"], E), h2, "ssm_out + residual")
+            assert_bits(ctx.read(L.O["h2"], E), h2v, "ssm_out + residual")
+        # which form ran: the launches' kernels (one more pass of the list; its results are not checked)
+        names = [st_["name"] for st_ in ctx.profile(w.ravel(), 1)]
+        assert any(nm.startswith("gdn_out_kernel") for nm in names) == (case == "in_place"), names
     finally:
         ctx.close()
+
+
+_OUT_OF_POLLS = r"""
+import sys
+sys.path.insert(0, sys.argv[1])
+sys.path.insert(0, sys.argv[2])
+import numpy as np
+import gemvq as gq
+import test_gpu_fused as T
+ctx = gq.Context(act_floats=1 << 19, weight_bytes=200 << 20, state_rows=T.HV * 128)
+L = T.Layer(gq, 40, 2, T.E)
+L.upload(ctx, 0)
+ctx.write(0, gq.normal(40, 1, T.E))
+try:
+    ctx.run(L.commands(gq, 0))
+    print("no error")
+except gq.GemvqError as e:
+    print("error:", e)
+print("usable", ctx.usable())
+ctx.close()
+"""
+
+
+def test_exchange_wait_out_of_polls_latches_the_context(tmp_path):
+    """With the in-kernel wait bounded at 0 polls (GEMVQ_EXCHANGE_POLLS, read when a context is created) every
+    workgroup of the fused launch gives up at once: the launch still ends normally, the fault word makes the run
+    return GEMVQ_ETIMEDOUT and the context unusable. Run in a child process so the setting stays out of this one."""
+    here = os.path.dirname(os.path.abspath(__file__))
+    pkg = os.path.join(os.path.dirname(here), "fpga-llama-gguf_amd")
+    env = dict(os.environ, GEMVQ_EXCHANGE_POLLS="0")
+    print("[fused] exchange wait bounded at 0 polls (child process)", flush=True)
+    r = subprocess.run([sys.executable, "-c", _OUT_OF_POLLS, pkg, here], env=env, capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "ran out of polls" in r.stdout and "usable False" in r.stdout, r.stdout
