@@ -295,7 +295,11 @@ def configs(args) -> int:
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle  # noqa: E402  (the CPU baseline only)
 
-    flush = np.ones(CPU_FLUSH_BYTES // 8)
+    # evicting reads by the oracle's own thread team on the same cores (each core complex has its own last-level
+    # cache): one multithreaded GEMV over a matrix larger than the host's caches
+    fl_rows = CPU_FLUSH_BYTES // gq.row_bytes(gq.Q4_0, 4096)
+    fl_w = np.full(fl_rows * gq.row_bytes(gq.Q4_0, 4096), 0x11, np.uint8)  # blocks of d = fp16 0x1111, quants 1
+    fl_x = gq.normal(1, 98, 4096)
     for name, desc, nbytes, copies, setup, cpu in _cfg_units(len(cpus)):
         ctx = gq.Context(act_floats=1 << 21, weight_bytes=1_100_000_000, state_rows=48 * 32 * 128)
         build = setup(ctx)
@@ -318,7 +322,7 @@ def configs(args) -> int:
             fn(*fargs)
             times = []
             for _ in range(CPU_REPS):
-                flush.sum()  # untimed: evicts the unit's bytes from the host caches, as the GPU's rotated copies do
+                oracle.fast_gemv(1, gq.Q4_0, fl_w, fl_x, fl_rows, 4096, len(cpus))  # untimed: evicts the unit's bytes
                 t0 = time.perf_counter()
                 fn(*fargs)
                 times.append(time.perf_counter() - t0)
@@ -334,7 +338,8 @@ def configs(args) -> int:
                 "cpu_kind": f"port (the oracle in the reference's CPU arithmetic: GEMV rows summed sequentially in "
                             f"FP32, int8 dots in {simd_name(oracle)}; rows split over {len(cpus)} threads, one per "
                             f"physical core, CPUs {cpus[0]}..{cpus[-1]}; median of {CPU_REPS} calls, each after reading "
-                            f"{CPU_FLUSH_BYTES >> 20} MiB to evict the unit's bytes from the caches)",
+                            f"{CPU_FLUSH_BYTES >> 20} MiB (a GEMV on the same threads) to evict the unit's bytes "
+                            f"from the caches)",
                 "cpu_cores": len(cpus)}
         print(json.dumps(line), flush=True)
     return 0

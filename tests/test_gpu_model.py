@@ -153,6 +153,42 @@ def test_c5_reference_arithmetic_matches_cpu_path(gq, orc, q35, c5):
     print(f"[c5] canonical vs reference arithmetic: first differing position {int(d[0]) if d.size else None}", flush=True)
 
 
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("n_seq", [4, 8])
+def test_c5_lockstep_sequences_match_single_decodes(gq, orc, q35, c5, n_seq):
+    """Lockstep decode at C5's size (the 9B shape, 32 layers): n_seq sequences with prompts of different lengths, 12
+    steps. Every sequence's token ids and last logits equal, bit for bit, a single-sequence decode of its own prompt
+    on the GPU, and sequence 0's equal the oracle decoder's. 4 sequences run the layer projections as small-token
+    GEMVs, 8 as MFMA batched GEMVs (the paths whose rates profiles/c5_sequences_decode.md reports)."""
+    cfg, blob, _, _, _ = c5
+    steps = 12
+    rng = np.random.default_rng(40 + n_seq)
+    lens = [int(v) for v in rng.integers(1, 17, n_seq)]  # some longer than the steps: prompt positions only
+    lens[0] = 5
+    prompts = [rng.integers(0, cfg.n_vocab, L).astype(np.int32) for L in lens]
+    print(f"[c5 lockstep] {n_seq} sequences, prompts {lens}, {steps} steps", flush=True)
+    with q35.BatchModel(blob, n_seq) as bm:
+        bm.reset(prompts)
+        bm.step(steps)
+        got = [(bm.tokens(s, steps + 1), bm.logits(s)) for s in range(n_seq)]
+    print("[c5 lockstep] single-sequence decodes", flush=True)
+    with q35.Model(blob) as m:
+        for s in range(n_seq):
+            m.reset(prompts[s])
+            m.step(steps)
+            want = m.tokens(steps + 1)
+            assert np.array_equal(got[s][0], want), f"sequence {s}: {got[s][0]} vs {want}"
+            assert np.array_equal(got[s][1].view(np.uint32), m.logits().view(np.uint32)), f"sequence {s} logits"
+    print("[c5 lockstep] oracle decode of sequence 0", flush=True)
+    om = orc.Model(q35.config_c(cfg), blob.table, blob.n, blob.data)
+    lo = np.empty(cfg.n_vocab, np.float32)
+    n_gen = steps - len(prompts[0]) + 1  # positions 0 .. steps - 1 processed, as the GPU's steps
+    want = om.generate_fast(prompts[0], n_gen, lo)
+    om.close()
+    assert np.array_equal(got[0][0], want), f"{got[0][0]} vs {want}"
+    assert np.array_equal(got[0][1].view(np.uint32), lo.view(np.uint32))
+
+
 def _decode_state(m, cfg, npos):
     """DeltaNet states, the attention layers' K/V up to npos, and the device's token ids up to npos + 1."""
     gdn_layers = sum(1 for il in range(cfg.n_layer) if (il + 1) % cfg.attn_interval != 0)
