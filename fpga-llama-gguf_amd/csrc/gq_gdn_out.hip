@@ -83,6 +83,8 @@ __device__ __forceinline__ void head_step(const GdnOutArgs & a, int h, float * y
                                           uint32_t * qinfo, int row, int nb, int nbt, WB (&wr)[GX_NBT]) {
     const GdnArgs & g = a.g;
     const int t = threadIdx.x, l16 = t & 15, rg = t >> 4, lane = t & 63, kh = h % g.hk;
+    const int e = t & 127;  // the element this thread gates (threads below 128)
+    const float zv = a.z[h * 128 + e], wv = a.nw[e];  // first: the gate is formed while the state arrives
     float x[8][8];
 #pragma unroll
     for (int it = 0; it < 8; ++it) {
@@ -103,11 +105,10 @@ __device__ __forceinline__ void head_step(const GdnOutArgs & a, int h, float * y
     for (int it = 0; it < 8; ++it) v[it] = g.v[h * 128 + rg + 16 * it];
     const bool gates = g.flags & 8;
     const float gr = g.g[h], br = g.beta[h], dtv = gates ? g.dt[h] : 0.0f, av = gates ? g.a[h] : 0.0f;
-    const int e = t & 127;  // the element this thread gates (threads below 128)
-    const float zv = a.z[h * 128 + e], wv = a.nw[e];
     __builtin_amdgcn_sched_barrier(0);
     load_rows<TYPE>(a, row, nb, nbt, wr);
     __builtin_amdgcn_sched_barrier(0);
+    const float zg = a.z_silu ? zv : silu_(zv);
     // 1. the step (the arithmetic of gdn_kernel)
     if (g.flags & 2) gdn_l2_qk(q, k, g.l2_eps);
     float bt;
@@ -129,7 +130,6 @@ __device__ __forceinline__ void head_step(const GdnOutArgs & a, int h, float * y
     __syncthreads();
     if (t < 128) {
         const float sc = 1.0f / sqrtf((hsum[0] + hsum[1]) / 128.0f + a.rms_eps);
-        const float zg = a.z_silu ? zv : silu_(zv);
         const float gv = zg * ((ys[e] * sc) * wv);
         a.y[h * 128 + e] = gv;  // the gated output (the GDN command's y)
         float d;
@@ -213,23 +213,27 @@ __global__ __launch_bounds__(GX_T) void gdn_out_kernel(GdnOutArgs a) {
         for (int w = w0 + t; w < min(w0 + per, all); w += GX_T) xch_store(other + w, 0ull);
     }
     if (missing) return;
-    long long acc = 0;
+    // every block term is an integer-valued double below 2^63 in magnitude: its high and low 32-bit parts are summed
+    // in two FP64 accumulators (exact for GX_NBT terms), then joined into int64 once; blocks past hv / 4 add zero
+    double acc_hi = 0.0, acc_lo = 0.0;
 #pragma unroll
     for (int i = 0; i < GX_NBT; ++i) {
-        if (i < nbt) {
-            const int blk = l16 + 16 * i;
-            XB xb;
-            const uint4 * p = reinterpret_cast<const uint4 *>(xq + blk * 8);
-            const uint4 lo = p[0], hi = p[1];
-            xb.q[0] = lo.x; xb.q[1] = lo.y; xb.q[2] = lo.z; xb.q[3] = lo.w;
-            xb.q[4] = hi.x; xb.q[5] = hi.y; xb.q[6] = hi.z; xb.q[7] = hi.w;
-            const uint32_t inf = xinfo[blk];
-            xb.dx40 = h2f(inf & 0xffffu) * 1099511627776.0f;  // * 2^40, exact
-            xb.sum = int(int16_t(inf >> 16));
-            xb.sx40 = 0.0f;
-            acc += dint_to_i64(block_term<TYPE>(dot_block<TYPE>(wr[i], xb), wr[i].d, xb));
-        }
+        const int blk = i < nbt ? l16 + 16 * i : l16;
+        XB xb;
+        const uint4 * p = reinterpret_cast<const uint4 *>(xq + blk * 8);
+        const uint4 lo = p[0], hi = p[1];
+        xb.q[0] = lo.x; xb.q[1] = lo.y; xb.q[2] = lo.z; xb.q[3] = lo.w;
+        xb.q[4] = hi.x; xb.q[5] = hi.y; xb.q[6] = hi.z; xb.q[7] = hi.w;
+        const uint32_t inf = xinfo[blk];
+        xb.dx40 = h2f(inf & 0xffffu) * 1099511627776.0f;  // * 2^40, exact
+        xb.sum = int(int16_t(inf >> 16));
+        xb.sx40 = 0.0f;
+        const double tv = i < nbt ? block_term<TYPE>(dot_block<TYPE>(wr[i], xb), wr[i].d, xb) : 0.0;
+        const double th = floor(tv * 2.3283064365386963e-10);  // tv / 2^32
+        acc_hi += th;
+        acc_lo += __builtin_fma(-th, 4294967296.0, tv);  // 0 <= tv - th 2^32 < 2^32, exact
     }
+    long long acc = (long long)(((unsigned long long)(long long)acc_hi << 32) + (unsigned long long)(long long)acc_lo);
     acc += dpp_i64<DPP_XOR1>(acc);  // the row's 16 lanes: every lane ends with the total
     acc += dpp_i64<DPP_XOR2>(acc);
     acc += dpp_i64<DPP_HALF_MIRROR>(acc);
