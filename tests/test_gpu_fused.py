@@ -28,8 +28,10 @@ def assert_bits(got, want, what=""):
 class Layer:
     """One DeltaNet layer's tensors (seeded by `seed`) and its place in the act buffer."""
 
-    def __init__(self, gq, seed, wtype, base):
+    def __init__(self, gq, seed, wtype, base, e=E, hk=HK, hv=HV, f=F):
         self.wtype = wtype
+        self.e, self.hk, self.hv, self.f, self.ch = e, hk, hv, f, 2 * hk * S + hv * S
+        E, HK, HV, F, CH = e, hk, hv, f, self.ch  # noqa: N806 (this layer's widths)
         self.Wqkv, self.Wz = gq.matrix(2, CH, E, seed, 3), gq.matrix(2, HV * S, E, seed, 4)
         self.Wb, self.Wa = gq.matrix(2, HV, E, seed, 5), gq.matrix(2, HV, E, seed, 6)
         self.Wo = gq.matrix(wtype, E, HV * S, seed, 7)
@@ -49,6 +51,7 @@ class Layer:
         self.end = off
 
     def upload(self, ctx, row):
+        E, HK, HV, F, CH = self.e, self.hk, self.hv, self.f, self.ch  # noqa: N806
         O = self.O
         self.w = [ctx.upload(t, r, c, w) for t, r, c, w in
                   ((2, CH, E, self.Wqkv), (2, HV * S, E, self.Wz), (2, HV, E, self.Wb), (2, HV, E, self.Wa),
@@ -59,6 +62,7 @@ class Layer:
         self.row = row
 
     def commands(self, gq, x, with_out=True):
+        E, HK, HV, F, CH = self.e, self.hk, self.hv, self.f, self.ch  # noqa: N806
         O, w = self.O, self.w
         flags = gq.GDN_L2_QK | gq.GDN_GATED | gq.GDN_GATES | gq.GDN_Z_SILU | (gq.GDN_WITH_OUT if with_out else 0)
         return (gq.rmsnorm(E, x, O["nw"], O["xn"], EPS, flags=gq.NORM_DEFER) +
@@ -75,6 +79,7 @@ class Layer:
 
     def oracle(self, orc, x, state, cst):
         """The layer in the oracle: (new x, new state, new conv state, gated y, ssm_out + residual)."""
+        E, HK, HV, F, CH = self.e, self.hk, self.hv, self.f, self.ch  # noqa: N806
         flags = 2 | 4 | 8 | 32
         xn = orc.rownorm(x, self.nw, E, 1, EPS)
         yc, ns = orc.conv(cst, orc.fx_gemv(2, self.Wqkv, xn, CH, E), self.cw)
@@ -119,6 +124,34 @@ def test_fused_deltanet_layers_match_oracle(gq, orc, wtype, n_layers):
                 assert_bits(ctx.read(L.O["y"], HV * S), y, f"run {run} layer {i} gated output")
                 assert_bits(ctx.read(L.O["h2"], E), h2, f"run {run} layer {i} ssm_out + residual")
             assert_bits(ctx.read(X, E), x, f"run {run} layer output")
+    finally:
+        ctx.close()
+
+
+@pytest.mark.parametrize("hv,hk,fused", [(12, 4, True), (8, 2, True), (6, 3, False)])
+def test_fused_narrow_layers(gq, orc, hv, hk, fused):
+    """Narrower layers (hidden 2048, FFN 1024): 12 and 8 value heads run the fused launch with fewer blocks per lane
+    than its registers hold (the unused ones re-read a valid block and add nothing); 6 heads (not a multiple of 4)
+    run unfused. Two runs in a row, bit for bit against the oracle; the launches' kernels show which form ran."""
+    e, f = 2048, 1024
+    ctx = gq.Context(act_floats=1 << 18, weight_bytes=64 << 20, state_rows=hv * 128)
+    try:
+        L = Layer(gq, 50 + hv, 2, e, e=e, hk=hk, hv=hv, f=f)
+        L.upload(ctx, 0)
+        cmds = L.commands(gq, 0)
+        x = gq.normal(50, 1, e)
+        ctx.write(0, x)
+        state, cst = L.state, L.cst
+        for run in range(2):
+            print(f"[fused] narrow layer, {hv} value heads, run {run}", flush=True)
+            assert ctx.run(cmds) == 0, ctx.error()
+            x, state, cst, y, h2 = L.oracle(orc, x, state, cst)
+            assert_bits(ctx.state_read(0, hv * 128), state, f"run {run} state")
+            assert_bits(ctx.read(L.O["y"], hv * S), y, f"run {run} gated output")
+            assert_bits(ctx.read(L.O["h2"], e), h2, f"run {run} ssm_out + residual")
+            assert_bits(ctx.read(0, e), x, f"run {run} layer output")
+        names = [st_["name"] for st_ in ctx.profile(np.array(cmds, np.uint32), 1)]
+        assert any(nm.startswith("gdn_out_kernel") for nm in names) == fused, names
     finally:
         ctx.close()
 
