@@ -24,7 +24,7 @@ OP_GEMV, OP_RMSNORM, OP_ADD, OP_SILU_MUL, OP_MUL, OP_UNARY, OP_GDN, OP_CONV, OP_
 OP_ATTN, OP_GET_ROWS, OP_ARGMAX, OP_NEXT_TOKEN, OP_FILL, OP_GEMM = 12, 13, 14, 15, 16, 17
 GEMM_MAX_TOK = 32
 GEMV_SWIGLU, GEMV_CONV, GEMV_ADD, GEMV_ARGMAX, GEMV_SILU = 0x100, 0x200, 0x400, 0x800, 0x1000
-GDN_WITH_GEMV, GDN_L2_QK, GDN_GATED, GDN_GATES, GDN_WITH_OUT, GDN_Z_SILU = 1, 2, 4, 8, 16, 32
+GDN_WITH_GEMV, GDN_L2_QK, GDN_GATED, GDN_GATES, GDN_WITH_OUT, GDN_Z_SILU, GDN_SEQS = 1, 2, 4, 8, 16, 32, 64
 NORM_L2, NORM_NO_WEIGHT, NORM_DEFER = 1, 2, 4
 SILU_MUL_SIGMOID = 1
 UNARY_SILU, UNARY_SIGMOID, UNARY_SOFTPLUS, UNARY_COPY = 1, 2, 3, 4

@@ -175,6 +175,69 @@ def test_gdn_gated_norm_folded_into_gemv(gq, orc, ctx, hv, hk, wtype, z_silu):
         assert_bits(o, out_want, f"{what}: GEMV + residual")
 
 
+@pytest.mark.parametrize("hv,hk,wtype,z_silu,ntok,seqs", [
+    (32, 16, 2, False, 2, False),  # small-token GEMV
+    (32, 16, 8, True, 4, True),
+    (16, 4, 2, False, 9, False),  # quantization launch + MFMA GEMM
+    (8, 2, 8, True, 20, True),
+])
+def test_gdn_tokens_gated_norm_then_gemm(gq, orc, hv, hk, wtype, z_silu, ntok, seqs):
+    """A GDN of several tokens (one sequence in order, or one token of each of several sequences decoded in
+    lockstep, each on its own state rows) with gates, L2 q/k and the gated output norm over every token's heads,
+    followed by a GEMM + residual on its output rows: the gated rows, the state rows and the GEMM outputs equal the
+    oracle's tokens run one by one, bit for bit."""
+    S, R = 128, 160
+    cols = hv * S
+    flags = (gq.GDN_L2_QK | gq.GDN_GATED | gq.GDN_GATES | (gq.GDN_Z_SILU if z_silu else 0) |
+             (gq.GDN_SEQS if seqs else 0))
+    sq, sg = up16_(cols), up16_(hv)
+    q, k, v = gq.normal(6, 1, ntok * sq), gq.normal(6, 2, ntok * sq), gq.normal(6, 3, ntok * sq)
+    g, beta = gq.normal(6, 4, ntok * sg), gq.normal(6, 5, ntok * sg)
+    dt, a = gq.normal(6, 6, hv), -np.abs(gq.normal(6, 7, hv))
+    z, w = gq.normal(6, 8, ntok * cols), gq.uniform(6, 9, S, 0.5, 1.5)
+    if z_silu:
+        z = orc.unary(z, 1)
+    n_st = hv * S * (ntok if seqs else 1)
+    state = gq.normal(6, 10, n_st * S) * 0.1
+    res = gq.normal(6, 11, ntok * R)
+    W = gq.matrix(wtype, R, cols, 6, 12)
+    O, at = {}, 0
+    for name, size in dict(q=ntok * sq, k=ntok * sq, v=ntok * sq, g=ntok * sg, beta=ntok * sg, dt=hv, a=hv,
+                           y=ntok * cols, w=S, z=ntok * cols, res=ntok * R, out=ntok * R).items():
+        O[name], at = at, at + up16_(size)
+    ctx = gq.Context(act_floats=up16_(at), weight_bytes=1 << 26, state_rows=n_st)
+    try:
+        off = ctx.upload(wtype, R, cols, W)
+        for name, arr in dict(q=q, k=k, v=v, g=g, beta=beta, dt=dt, a=a, w=w, z=z, res=res).items():
+            ctx.write(O[name], arr)
+        ctx.state_write(0, state)
+        gdn = gq.gdn(hv, hk, O["q"], O["k"], O["v"], O["g"], O["beta"], O["y"], 0, 0, 1 / np.sqrt(S), flags,
+                     1e-6, 1e-6, O["w"], O["z"], O["dt"], O["a"])
+        gdn[16 + 2:16 + 5] = [ntok, sq, sg]  # gates slot: n_tok, q / k / v row stride, g / beta row stride
+        gemm = gq.gemm(wtype, R, cols, off, O["y"], O["out"], ntok, cols, R, gq.GEMV_ADD, O["res"], R)
+        print(f"[gdn gemm] hv {hv} fmt {wtype} tokens {ntok} seqs {seqs}", flush=True)
+        assert ctx.run(gdn + gemm) == 0, ctx.error()
+        st = state.copy()
+        y_want, out_want = [], []
+        for t in range(ntok):
+            qkv = [x[t * sq:t * sq + n] for x, n in ((q, hk * S), (k, hk * S), (v, cols))]
+            gb = [x[t * sg:t * sg + hv] for x in (g, beta)]
+            rows = slice(t * hv * S * S, (t + 1) * hv * S * S) if seqs else slice(None)
+            y_t, st[rows] = orc.gdn(st[rows], *qkv, *gb, hv, hk, float(1 / np.sqrt(S)), flags & ~gq.GDN_SEQS,
+                                    dt, a, z[t * cols:(t + 1) * cols], w)
+            y_want.append(y_t)
+            out_want.append(orc.fx_gemv(wtype, W, y_t, R, cols) + res[t * R:(t + 1) * R])
+        assert_bits(ctx.read(O["y"], ntok * cols), np.concatenate(y_want), "gated rows")
+        assert_bits(ctx.state_read(0, n_st), st, "state")
+        assert_bits(ctx.read(O["out"], ntok * R), np.concatenate(out_want), "GEMM + residual")
+    finally:
+        ctx.close()
+
+
+def up16_(n: int) -> int:
+    return (n + 15) // 16 * 16
+
+
 @pytest.mark.parametrize("nh,nkv,hd,nrot,n_ctx,npos,checks", [
     (16, 4, 256, 64, 200, 130, (0, 1, 63, 64, 65, 127, 128, 129)),  # Qwen3.5 shape, crosses two chunk boundaries
     (6, 2, 128, 128, 1100, 1041, (1023, 1024, 1040)),  # 17 chunks
