@@ -197,25 +197,42 @@ __global__ __launch_bounds__(256) void attn_ref_append_kernel(AttnArgs a, int to
     }
 }
 
-// Workgroup = q head: scores over positions 0 .. pos (a thread per position, the F16 dot summed in double), the max,
-// e^(s - max) and their sum in order (thread 0), the fp16 probabilities, then thread d sums p * v[d] over the
-// positions in order. sp: n_ctx floats per q head of scratch.
+// Workgroup = q head: scores over positions 0 .. pos (a thread per position, the F16 dot summed in double in index
+// order), the max, e^(s - max) and their sum in order (thread 0), the fp16 probabilities, then thread d sums p * v[d]
+// over the positions in order. The scores and probabilities sit in LDS up to RA_LDS positions, else in sp (n_ctx
+// floats per q head of scratch). Each row is read 16 bytes at a time and each sum's terms are requested in groups
+// ahead of the chain of additions, which keeps the order of the additions.
+constexpr int RA_LDS = 8192;
 __global__ __launch_bounds__(256) void attn_ref_kernel(AttnArgs a, int tok) {
     __shared__ float qv[256], red[4], inv;
+    __shared__ float spl[RA_LDS];
     const AttnTok t = attn_tok(a, tok);
     if (t.pos < 0 || t.pos >= a.n_ctx) return;
     const int h = blockIdx.x, hd = a.head_dim, tid = threadIdx.x, n = t.pos + 1;
     const int kvh = h / (a.n_head / a.n_head_kv);
-    float * sp = a.part + size_t(h) * a.n_ctx;
+    float * sp = n <= RA_LDS ? spl : a.part + size_t(h) * a.n_ctx;
     if (tid < hd) qv[tid] = a.qr[size_t(h) * hd + tid];
     __syncthreads();
     float mx = -__builtin_inff();
     for (int p = tid; p < n; p += 256) {
-        const uint16_t * kr = t.kc + (size_t(p) * a.n_head_kv + kvh) * hd;
+        const uint4 * kr = reinterpret_cast<const uint4 *>(t.kc + (size_t(p) * a.n_head_kv + kvh) * hd);
         double acc = 0.0;
-        for (int d = 0; d < hd; ++d) {
-            const float pr = qv[d] * h2f(kr[d]);
-            acc += double(pr);
+        for (int d0 = 0; d0 < hd; d0 += 64) {  // head_dim: a power of two from 16 (8 halves per 16 bytes)
+            uint4 w[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w[i] = d0 + 8 * i < hd ? kr[(d0 >> 3) + i] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t u[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int d = d0 + 8 * i + j;
+                    if (d < hd) {
+                        const float pr = qv[d] * h2f((u[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+                        acc += double(pr);
+                    }
+                }
+            }
         }
         const float sc = float(acc) * a.scale;
         sp[p] = sc;
@@ -230,18 +247,37 @@ __global__ __launch_bounds__(256) void attn_ref_kernel(AttnArgs a, int tok) {
     __syncthreads();
     if (tid == 0) {
         double sum = 0.0;
-        for (int p = 0; p < n; ++p) sum += double(sp[p]);
+        int p = 0;
+        for (; p + 8 <= n; p += 8) {
+            float e[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) e[i] = sp[p + i];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sum += double(e[i]);
+        }
+        for (; p < n; ++p) sum += double(sp[p]);
         inv = float(1.0 / sum);
     }
     __syncthreads();
     for (int p = tid; p < n; p += 256) sp[p] = h2f(f2h(sp[p] * inv));
     __syncthreads();
     if (tid >= hd) return;
+    const uint16_t * vcol = t.vc + size_t(kvh) * hd + tid;
+    const size_t vs = size_t(a.n_head_kv) * hd;  // between positions
     double acc = 0.0;
-    for (int p = 0; p < n; ++p) {
-        const float pv = h2f(t.vc[(size_t(p) * a.n_head_kv + kvh) * hd + tid]) * sp[p];
-        acc += double(pv);
+    int p = 0;
+    for (; p + 8 <= n; p += 8) {
+        uint16_t v[8];
+        float pp[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[i] = vcol[size_t(p + i) * vs];
+            pp[i] = sp[p + i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc += double(h2f(v[i]) * pp[i]);
     }
+    for (; p < n; ++p) acc += double(h2f(vcol[size_t(p) * vs]) * sp[p]);
     float o = float(acc);
     if (a.gate) o = cr::sigmoid(a.gate[size_t(tok) * a.n_head * a.q_stride + size_t(h) * 2 * hd + tid]) * o;
     a.y[(size_t(tok) * a.n_head + h) * hd + tid] = o;
