@@ -125,6 +125,11 @@ struct GdnArgs {
     int s_qkv, s_gb, s_y;  // row strides (floats) between tokens of q / k / v, of g / beta, of y
     int seqs;              // nonzero: the tokens belong to n_tok sequences, token t on its own state rows (src and
                            // dst + t * hv * 128 rows), all in one launch
+    // reference arithmetic with the gated output norm (GEMVQ_GDN_GATED): the step's launch also applies the norm to
+    // its token's heads (z rows hv * 128 apart per token, the norm weight [128], the RMS eps); NULL gz: not applied
+    const float * gz;
+    const float * gw;
+    float rms_eps;
 };
 
 // The DeltaNet step, its gated output norm, the ssm_out product and its residual sum in one launch (the reference's

@@ -64,8 +64,25 @@ __global__ void conv_ref_kernel(ConvArgs a, int tok) {
 
 // ---- DeltaNet step, one token (gemvq_ref.h:360-397 with ggml's L2_NORM and gate ops around it,
 // ggml-xrt.cpp:1977-2000): workgroup = value head h, thread j = state row j ----
+// Sum of squares of 128 LDS floats in index order, in double (read 16 bytes at a time, two reads ahead).
+__device__ __forceinline__ double ordered_sumsq128(const float * p) {
+    const float4 * p4 = reinterpret_cast<const float4 *>(p);
+    double sum = 0.0;
+    for (int i = 0; i < 32; i += 2) {
+        const float4 a = p4[i], b = p4[i + 1];
+        const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float sq = x[e] * x[e];
+            sum += double(sq);
+        }
+    }
+    return sum;
+}
+
 __global__ __launch_bounds__(128) void gdn_ref_kernel(GdnArgs a, int tok) {
-    __shared__ float qs[128], ks[128], sc[2];
+    __shared__ __attribute__((aligned(16))) float qs[128], ks[128], ys[128];
+    __shared__ float sc[3];
     const int h = blockIdx.x, j = threadIdx.x, kh = h % a.hk;
     const float * q = a.q + size_t(tok) * a.s_qkv + kh * 128;
     const float * k = a.k + size_t(tok) * a.s_qkv + kh * 128;
@@ -73,29 +90,7 @@ __global__ __launch_bounds__(128) void gdn_ref_kernel(GdnArgs a, int tok) {
     const size_t so = a.seqs ? size_t(tok) * a.hv * 128 * 128 : 0;
     const float * src = a.seqs ? a.src + so : tok == 0 ? a.src : a.dst;
     float * dst = a.dst + so;
-    if (a.flags & GEMVQ_GDN_L2_QK) {  // ggml_l2_norm of q and k: 1 / max(sqrt(sum of squares), eps)
-        if (j == 0 || j == 64) {
-            const float * p = j == 0 ? q : k;
-            double sum = 0.0;
-            for (int i = 0; i < 128; ++i) {
-                const float sq = p[i] * p[i];
-                sum += double(sq);
-            }
-            sc[j >> 6] = 1.0f / fmaxf(sqrtf(float(sum)), a.l2_eps);
-        }
-        __syncthreads();
-        qs[j] = q[j] * sc[0];
-        ks[j] = k[j] * sc[1];
-    } else {
-        qs[j] = q[j];
-        ks[j] = k[j];
-    }
-    float g = a.g[size_t(tok) * a.s_gb + h], beta = a.beta[size_t(tok) * a.s_gb + h];
-    if (a.flags & GEMVQ_GDN_GATES) {  // beta = sigmoid(b), g = softplus(alpha + dt) * a
-        g = cr::softplus(g + a.dt[h]) * a.a[h];
-        beta = cr::sigmoid(beta);
-    }
-    const float decay = cr::expf(g);
+    // the thread's state row is requested first: its loads overlap the norms and the gate arithmetic below
     const size_t row = (size_t(h) * 128 + j) * 128;
     float s[128];
 #pragma unroll
@@ -106,6 +101,28 @@ __global__ __launch_bounds__(128) void gdn_ref_kernel(GdnArgs a, int tok) {
         s[i + 2] = t.z;
         s[i + 3] = t.w;
     }
+    // q and k staged in LDS by all threads, so the sequential sums below read LDS
+    const float qj = q[j], kj = k[j];
+    qs[j] = qj;
+    ks[j] = kj;
+    __syncthreads();
+    if (a.flags & GEMVQ_GDN_L2_QK) {  // ggml_l2_norm of q and k: 1 / max(sqrt(sum of squares), eps)
+        if (j == 0 || j == 64) {
+            const double sum = ordered_sumsq128(j == 0 ? qs : ks);
+            sc[j >> 6] = 1.0f / fmaxf(sqrtf(float(sum)), a.l2_eps);
+        }
+        __syncthreads();
+        const float s0 = sc[0], s1 = sc[1];
+        __syncthreads();
+        qs[j] = qj * s0;
+        ks[j] = kj * s1;
+    }
+    float g = a.g[size_t(tok) * a.s_gb + h], beta = a.beta[size_t(tok) * a.s_gb + h];
+    if (a.flags & GEMVQ_GDN_GATES) {  // beta = sigmoid(b), g = softplus(alpha + dt) * a
+        g = cr::softplus(g + a.dt[h]) * a.a[h];
+        beta = cr::sigmoid(beta);
+    }
+    const float decay = cr::expf(g);
     __syncthreads();
     float dot = 0.0f;
 #pragma unroll
@@ -122,7 +139,17 @@ __global__ __launch_bounds__(128) void gdn_ref_kernel(GdnArgs a, int tok) {
     }
 #pragma unroll
     for (int i = 0; i < 128; i += 4) *reinterpret_cast<float4 *>(dst + row + i) = make_float4(s[i], s[i + 1], s[i + 2], s[i + 3]);
-    a.y[size_t(tok) * a.s_y + h * 128 + j] = out * a.scale;
+    float yv = out * a.scale;
+    if (a.gz && (a.flags & GEMVQ_GDN_GATED)) {
+        // the gated output norm of this head (gated_norm_ref_kernel's arithmetic, in the same launch)
+        ys[j] = yv;
+        __syncthreads();
+        if (j == 0) sc[2] = 1.0f / sqrtf(float(ordered_sumsq128(ys) / 128.0) + a.rms_eps);
+        __syncthreads();
+        const float z = a.gz[(size_t(tok) * a.hv + h) * 128 + j];
+        yv = ((yv * sc[2]) * a.gw[j]) * ((a.flags & GEMVQ_GDN_Z_SILU) ? z : cr::silu(z));
+    }
+    a.y[size_t(tok) * a.s_y + h * 128 + j] = yv;
 }
 
 // ---- gated output norm per head of 128 (RMS_NORM -> MUL weight -> MUL SILU(z), ggml-xrt.cpp:1952-1975) ----

@@ -20,14 +20,16 @@ constexpr int RB = 4;  // rows per batch
 // FP32 block terms of row r (Q4_0 / Q8_0: float(sumi) * (d_w * d_x); Q4_1: (d_w * d_x) * float(sumi) + m_w * s_x)
 // into t[b] for this lane's blocks.
 template <int TYPE, int NU>
-__device__ __forceinline__ void row_terms(const WeightView & w, int r, int nb, int lane, const XB * xb, const float * dx,
-                                          const float * sx, float * t) {
-    WB wb[NU];
+__device__ __forceinline__ void row_load(const WeightView & w, int r, int nb, int lane, WB * wb) {
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
         const int b = lane + 64 * k, bb = b < nb ? b : nb - 1;
         load_wb<TYPE>(w, size_t(r) * nb + bb, wb[k]);
     }
+}
+template <int TYPE, int NU>
+__device__ __forceinline__ void row_terms_wb(const WB * wb, int nb, int lane, const XB * xb, const float * dx,
+                                             const float * sx, float * t) {
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
         const int b = lane + 64 * k;
@@ -43,6 +45,25 @@ __device__ __forceinline__ void row_terms(const WeightView & w, int r, int nb, i
             t[b] = term;
         }
     }
+}
+template <int TYPE, int NU>
+__device__ __forceinline__ void row_terms(const WeightView & w, int r, int nb, int lane, const XB * xb, const float * dx,
+                                          const float * sx, float * t) {
+    WB wb[NU];
+    row_load<TYPE, NU>(w, r, nb, lane, wb);
+    row_terms_wb<TYPE, NU>(wb, nb, lane, xb, dx, sx, t);
+}
+
+// Batch bi of the members' batches in order: its member and first row.
+__device__ __forceinline__ void locate_batch(const GemvArgs & a, int bi, int & mi, int & r0) {
+    int b0 = 0;
+    mi = 0;
+    for (; mi < a.n_members - 1; ++mi) {
+        const int nbm = (a.m[mi].rows + RB - 1) / RB;
+        if (bi < b0 + nbm) break;
+        b0 += nbm;
+    }
+    r0 = (bi - b0) * RB;
 }
 
 // The per-index-class integer sums of one 64-weight unit: aux[l] = sum over its weights i with i % 8 == l of sc *
@@ -140,12 +161,33 @@ template <int TYPE, int NU, bool PAIR>
 __global__ __launch_bounds__(NT) void gemv_ref_kernel(GemvArgs a, int total_batches) {
     constexpr bool KQ = TYPE == T_Q5_K || TYPE == T_Q6_K;
     constexpr int TPR = KQ ? 16 * NU * 9 : 64 * NU;  // terms per row at most
-    constexpr int STR = TPR + 1;                     // a row of terms (padded against bank conflicts)
+    // a row of terms, padded against bank conflicts (K-quants: one float; Q4_0 / Q4_1 / Q8_0: four, so that each
+    // row's chain reads its terms 16 bytes at a time)
+    constexpr int STR = KQ ? TPR + 1 : TPR + 4;
     __shared__ Lds s;
-    __shared__ float tm[NWAVES][PAIR ? 2 : 1][RB][STR];
+    __shared__ __attribute__((aligned(16))) float tm[NWAVES][PAIR ? 2 : 1][RB][STR];
     __shared__ double red[NWAVES];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int cols = a.cols, nb = cols / 32, nu = cols / 64, nsb = cols / 256;
+    // ---- the wave's first batch of rows (Q4_0 / Q4_1 / Q8_0 up to 4096 columns) is requested before the
+    // prologue, so its weights stream while the activation is quantized
+    constexpr bool PRE = !KQ && NU <= 2;
+    const int bi0 = blockIdx.x * NWAVES + wave;
+    WB pre[PRE ? RB : 1][PRE ? NU : 1], pre2[PRE && PAIR ? RB : 1][PRE && PAIR ? NU : 1];
+    if constexpr (PRE) {
+        int mi = 0, r0 = 0;
+        locate_batch(a, bi0 < total_batches ? bi0 : 0, mi, r0);
+        const GemvMember & m = a.m[mi];
+        const int n = min(RB, m.rows - r0);
+        // a pair kernel's members other than the SwiGLU pair have no second matrix (w2 is not set for them here):
+        // they read their own matrix again, whose terms are not used
+        const WeightView & w2 = m.epi == EPI_SWIGLU ? m.w2 : m.w;
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            row_load<TYPE, NU>(m.w, r0 + min(j, n - 1), nb, lane, pre[j]);
+            if constexpr (PAIR) row_load<TYPE, NU>(w2, r0 + min(j, n - 1), nb, lane, pre2[j]);
+        }
+    }
     // ---- prologue: the activation, with the folded norm in the reference's arithmetic, quantized into LDS
     const bool norm = a.xsrc == XSRC_NORM;
     float scale = 1.0f;
@@ -195,24 +237,28 @@ __global__ __launch_bounds__(NT) void gemv_ref_kernel(GemvArgs a, int total_batc
     // ---- batches of RB rows of one member: batch bi of the members' batches in order
     unsigned long long best = 0;
     const bool argmax = a.argmax_key != nullptr;
-    for (int bi = blockIdx.x * NWAVES + wave; bi < total_batches; bi += gridDim.x * NWAVES) {
-        int mi = 0, b0 = 0;
-        for (; mi < a.n_members - 1; ++mi) {
-            const int nbm = (a.m[mi].rows + RB - 1) / RB;
-            if (bi < b0 + nbm) break;
-            b0 += nbm;
-        }
+    for (int bi = bi0; bi < total_batches; bi += gridDim.x * NWAVES) {
+        int mi = 0, r0 = 0;
+        locate_batch(a, bi, mi, r0);
         const GemvMember & m = a.m[mi];
-        const int r0 = (bi - b0) * RB, n = min(RB, m.rows - r0);
+        const int n = min(RB, m.rows - r0);
         const bool pair = PAIR && m.epi == EPI_SWIGLU;
+        if (PRE && bi == bi0) {  // the rows requested before the prologue
 #pragma unroll
-        for (int j = 0; j < RB; ++j) {
-            const int r = r0 + min(j, n - 1);
-            if constexpr (KQ) {
-                row_terms_kq<TYPE, NU>(m.w, r, nu, lane, xk, s.info, tm[wave][0][j]);
-            } else {
-                row_terms<TYPE, NU>(m.w, r, nb, lane, xb, dx, sx, tm[wave][0][j]);
-                if (pair) row_terms<TYPE, NU>(m.w2, r, nb, lane, xb, dx, sx, tm[wave][PAIR ? 1 : 0][j]);
+            for (int j = 0; j < RB; ++j) {
+                row_terms_wb<TYPE, NU>(pre[j], nb, lane, xb, dx, sx, tm[wave][0][j]);
+                if (pair) row_terms_wb<TYPE, NU>(pre2[PAIR ? j : 0], nb, lane, xb, dx, sx, tm[wave][PAIR ? 1 : 0][j]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < RB; ++j) {
+                const int r = r0 + min(j, n - 1);
+                if constexpr (KQ) {
+                    row_terms_kq<TYPE, NU>(m.w, r, nu, lane, xk, s.info, tm[wave][0][j]);
+                } else {
+                    row_terms<TYPE, NU>(m.w, r, nb, lane, xb, dx, sx, tm[wave][0][j]);
+                    if (pair) row_terms<TYPE, NU>(m.w2, r, nb, lane, xb, dx, sx, tm[wave][PAIR ? 1 : 0][j]);
+                }
             }
         }
         wave_lds_order();
@@ -237,8 +283,30 @@ __global__ __launch_bounds__(NT) void gemv_ref_kernel(GemvArgs a, int total_batc
             const int j = lane & (RB - 1), w2 = lane / RB;
             float acc = 0.0f;
             if (lane < (pair ? 2 * RB : RB)) {
-                const float * t = tm[wave][PAIR ? w2 : 0][j];
-                for (int b = 0; b < nb; ++b) acc += t[b];
+                // the row's terms in block order, read 16 bytes at a time, two reads ahead of their additions
+                const float * tf = tm[wave][PAIR ? w2 : 0][j];
+                const float4 * t = reinterpret_cast<const float4 *>(tf);
+                const int n4 = nb >> 2;
+                int b = 0;
+                for (; b + 2 <= n4; b += 2) {
+                    const float4 x0 = t[b], x1 = t[b + 1];
+                    acc += x0.x;
+                    acc += x0.y;
+                    acc += x0.z;
+                    acc += x0.w;
+                    acc += x1.x;
+                    acc += x1.y;
+                    acc += x1.z;
+                    acc += x1.w;
+                }
+                if (b < n4) {
+                    const float4 x0 = t[b];
+                    acc += x0.x;
+                    acc += x0.y;
+                    acc += x0.z;
+                    acc += x0.w;
+                }
+                for (int e = n4 * 4; e < nb; ++e) acc += tf[e];
             }
             v = __shfl(acc, j, WAVE);
             u = __shfl(acc, RB + j, WAVE);

@@ -634,15 +634,14 @@ struct Compiler {
                 a.seqs = int(seqs && ntok > 1);
                 const unsigned next = i + (gates ? 3 : 2);
                 uint32_t fy = 0, fres = 0;
-                if (ref()) {  // the tokens one launch each, in order; then the gated norm of all of them
+                if (ref()) {  // the tokens one launch each, in order, each with the gated norm of its heads
+                    if (flags & GEMVQ_GDN_GATED) {
+                        a.gz = A(k2[7]);
+                        a.gw = A(k2[6]);
+                        a.rms_eps = bits_f(k2[5]);
+                    }
                     for (uint32_t t = 0; t < ntok; ++t) {
                         out.push_back(LGdn{a, 1, int(t)});
-                        spans.push_back({int(i), gates ? 3 : 2});
-                    }
-                    if (flags & GEMVQ_GDN_GATED) {
-                        GatedNormArgs g{A(k[7]), A(k2[7]), A(k2[6]), int(hv * ntok), bits_f(k2[5]),
-                                        int(bool(flags & GEMVQ_GDN_Z_SILU))};
-                        out.push_back(LGated{g, 1});
                         spans.push_back({int(i), gates ? 3 : 2});
                     }
                     i = next;
