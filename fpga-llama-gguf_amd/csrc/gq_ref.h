@@ -67,7 +67,6 @@ hipError_t launch_ew_ref(const EwArgs & a, hipStream_t s);
 // order; the sequences forms take token tok's own state, window, KV region and position).
 hipError_t launch_conv_ref(const ConvArgs & a, int tok, hipStream_t s);
 hipError_t launch_gdn_ref(const GdnArgs & a, int tok, hipStream_t s);
-hipError_t launch_gated_norm_ref(const GatedNormArgs & a, hipStream_t s);
 hipError_t launch_attn_ref(const AttnArgs & a, int tok, hipStream_t s);
 // hashes[b] (b < 4096): sum mod 2^64 over i < 2^20 of bits(f(x)) (2 i + 1), x the binary32 with bits b 2^20 + i,
 // f the correctly rounded exp (fn 0) or log (fn 1), NaN results as 0x7fc00000.

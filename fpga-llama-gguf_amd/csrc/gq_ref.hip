@@ -141,7 +141,8 @@ __global__ __launch_bounds__(128) void gdn_ref_kernel(GdnArgs a, int tok) {
     for (int i = 0; i < 128; i += 4) *reinterpret_cast<float4 *>(dst + row + i) = make_float4(s[i], s[i + 1], s[i + 2], s[i + 3]);
     float yv = out * a.scale;
     if (a.gz && (a.flags & GEMVQ_GDN_GATED)) {
-        // the gated output norm of this head (gated_norm_ref_kernel's arithmetic, in the same launch)
+        // the gated output norm of this head (RMS_NORM -> MUL weight -> MUL SILU(z), ggml-xrt.cpp:1952-1975): the sum
+        // of the squares in order in double, then ((y * sc) * w) * silu(z)
         ys[j] = yv;
         __syncthreads();
         if (j == 0) sc[2] = 1.0f / sqrtf(float(ordered_sumsq128(ys) / 128.0) + a.rms_eps);
@@ -150,25 +151,6 @@ __global__ __launch_bounds__(128) void gdn_ref_kernel(GdnArgs a, int tok) {
         yv = ((yv * sc[2]) * a.gw[j]) * ((a.flags & GEMVQ_GDN_Z_SILU) ? z : cr::silu(z));
     }
     a.y[size_t(tok) * a.s_y + h * 128 + j] = yv;
-}
-
-// ---- gated output norm per head of 128 (RMS_NORM -> MUL weight -> MUL SILU(z), ggml-xrt.cpp:1952-1975) ----
-__global__ __launch_bounds__(128) void gated_norm_ref_kernel(GatedNormArgs a) {
-    __shared__ float sc;
-    const int h = blockIdx.x, j = threadIdx.x;
-    float * y = a.y + size_t(h) * 128;
-    const float yv = y[j];
-    if (j == 0) {
-        double sum = 0.0;
-        for (int i = 0; i < 128; ++i) {
-            const float sq = y[i] * y[i];
-            sum += double(sq);
-        }
-        sc = 1.0f / sqrtf(float(sum / 128.0) + a.eps);
-    }
-    __syncthreads();
-    const float z = a.z[size_t(h) * 128 + j];
-    y[j] = ((yv * sc) * a.w[j]) * (a.z_silu ? z : cr::silu(z));
 }
 
 // ---- attention, one token ----
@@ -352,10 +334,6 @@ hipError_t launch_gdn_ref(const GdnArgs & a, int tok, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_gated_norm_ref(const GatedNormArgs & a, hipStream_t s) {
-    GQ_LAUNCH(gated_norm_ref_kernel, dim3(a.heads), dim3(128), 0, s, a);
-    return hipGetLastError();
-}
 
 hipError_t launch_attn_ref(const AttnArgs & a, int tok, hipStream_t s) {
     if (a.head_dim > 256 || a.n_head % a.n_head_kv) return hipErrorInvalidValue;

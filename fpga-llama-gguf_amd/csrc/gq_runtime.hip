@@ -81,7 +81,7 @@ struct LConv { ConvArgs a; int ref = 0, tok = 0; };
 struct LRope { RopeArgs a; };
 struct LGdn { GdnArgs a; int ref = 0, tok = 0; };
 struct LGdnOut { GdnOutArgs a; int type; };
-struct LGated { GatedNormArgs a; int ref = 0; };
+struct LGated { GatedNormArgs a; };
 struct LAttn { AttnArgs a; int ref = 0, tok = 0; };
 struct LRows { GetRowsArgs a; };
 struct LArgmax { const float * x; int n; unsigned long long * key; int rows, stride; };
@@ -1317,7 +1317,7 @@ std::pair<std::string, uint64_t> describe(const Launch & l, int pos) {
                 2 * hv * 128 * 128 * 4 + ((2 * hk + 2 * hv) * 128 * 4 + hv * 16) * uint64_t(x->ref ? 1 : x->a.n_tok)};
     }
     if (auto * x = std::get_if<LGated>(&l))
-        return {x->ref ? "gated_norm_ref_kernel" : "gated_norm_kernel", uint64_t(x->a.heads) * 128 * 12 + 512};
+        return {"gated_norm_kernel", uint64_t(x->a.heads) * 128 * 12 + 512};
     if (auto * x = std::get_if<LGdnOut>(&l)) {
         const GdnOutArgs & o = x->a;
         const uint64_t hv = uint64_t(o.g.hv), hk = uint64_t(o.g.hk), rows = uint64_t(o.rows);
@@ -1373,7 +1373,7 @@ hipError_t issue(const std::vector<Launch> & ls, hipStream_t s) {
         else if (auto * x = std::get_if<LConv>(&l)) e = x->ref ? launch_conv_ref(x->a, x->tok, s) : launch_conv(x->a, s);
         else if (auto * x = std::get_if<LRope>(&l)) e = launch_rope(x->a, s);
         else if (auto * x = std::get_if<LGdn>(&l)) e = x->ref ? launch_gdn_ref(x->a, x->tok, s) : launch_gdn(x->a, s);
-        else if (auto * x = std::get_if<LGated>(&l)) e = x->ref ? launch_gated_norm_ref(x->a, s) : launch_gated_norm(x->a, s);
+        else if (auto * x = std::get_if<LGated>(&l)) e = launch_gated_norm(x->a, s);
         else if (auto * x = std::get_if<LAttn>(&l)) e = x->ref ? launch_attn_ref(x->a, x->tok, s) : launch_attn(x->a, s);
         else if (auto * x = std::get_if<LRows>(&l)) e = launch_get_rows(x->a, s);
         else if (auto * x = std::get_if<LArgmax>(&l)) e = launch_argmax(x->x, x->n, x->key, x->rows, x->stride, s);
