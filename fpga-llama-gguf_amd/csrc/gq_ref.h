@@ -18,22 +18,29 @@
 
 namespace gq {
 
-// The reference's norm value of one row of n floats, computed by the whole workgroup (blockDim.x a multiple of 64,
-// at most 1024; red: shared memory of blockDim.x / 64 doubles): S = sum over i of double(x_i * x_i) (FP32 squares)
-// in index order, then float(S / n) (RMS) or float(S) (L2) (gemvq_ref.h:309-324). S is first formed as a tree sum
-// T. The sequential sum is within (n - 1) 2^-53 S of the exact one (non-negative terms) and the tree within
-// ceil(log2 n) 2^-53 S, so it lies in [T - E, T + E] with E = (n + 64) 2^-52 T (a factor 2 of margin); rounding is
-// monotone, so when both ends give the same float the sequential sum gives it too. Otherwise (about one row in 10^5
-// at n = 4096) thread 0 adds the squares in order. Every thread returns the value.
-__device__ inline float ref_norm_value(const float * x, int n, int l2, double * red) {
+// The reference's norm value of one row of n floats (n a multiple of 4, x 16-byte aligned), computed by the whole
+// workgroup (blockDim.x a multiple of 64, at most 1024; red: shared memory of blockDim.x / 64 doubles): S = sum over
+// i of double(x_i * x_i) (FP32 squares) in index order, then float(S / n) (RMS) or float(S) (L2)
+// (gemvq_ref.h:309-324). S is first formed as T, the workgroup's sum in its own order (each thread's 4-float pieces,
+// then across the lanes and the waves). Any order of adding n non-negative terms in double is within (n - 1) 2^-53 S
+// of the exact sum, so the sequential sum lies in [T - E, T + E] with E = (n + 64) 2^-52 T (a factor 2 of margin);
+// rounding is monotone, so when both ends give the same float the sequential sum gives it too. Otherwise (about one
+// row in 10^5 at n = 4096) thread 0 adds the squares in order. Every thread returns the value.
+template <int CTRL>
+__device__ inline double dpp_f64(double v) {
+    return __builtin_bit_cast(double, dpp_i64<CTRL>(__builtin_bit_cast(long long, v)));
+}
+// The second half of ref_norm_value: each thread's partial p of T (the double squares of its share of the row, in
+// any order; the shares together cover the row once), then the workgroup's sum, the check and the fallback.
+__device__ inline float ref_norm_reduce(double p, const float * x, int n, int l2, double * red) {
     const int tid = threadIdx.x, nt = blockDim.x;
-    double p = 0.0;
-    for (int i = tid; i < n; i += nt) {
-        const float q = x[i] * x[i];
-        p += double(q);
-    }
-#pragma unroll
-    for (int st = 32; st >= 1; st >>= 1) p += __shfl_xor(p, st, 64);
+    // across the wave: within rows of 16 lanes by DPP, then across the rows
+    p += dpp_f64<DPP_XOR1>(p);
+    p += dpp_f64<DPP_XOR2>(p);
+    p += dpp_f64<DPP_HALF_MIRROR>(p);
+    p += dpp_f64<DPP_MIRROR>(p);
+    p += __shfl_xor(p, 16, 64);
+    p += __shfl_xor(p, 32, 64);
     if ((tid & 63) == 0) red[tid >> 6] = p;
     __syncthreads();
     double t = 0.0;
@@ -58,6 +65,18 @@ __device__ inline float ref_norm_value(const float * x, int n, int l2, double * 
     }
     __syncthreads();
     return v;
+}
+__device__ inline float ref_norm_value(const float * x, int n, int l2, double * red) {
+    double p = 0.0;
+    for (int i = 4 * int(threadIdx.x); i < n; i += 4 * int(blockDim.x)) {
+        const float4 q = *reinterpret_cast<const float4 *>(x + i);
+        const float s0 = q.x * q.x, s1 = q.y * q.y, s2 = q.z * q.z, s3 = q.w * q.w;
+        p += double(s0);
+        p += double(s1);
+        p += double(s2);
+        p += double(s3);
+    }
+    return ref_norm_reduce(p, x, n, l2, red);
 }
 
 hipError_t launch_gemv_ref(const GemvArgs & a, int type, hipStream_t s);

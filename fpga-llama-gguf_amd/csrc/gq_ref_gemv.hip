@@ -191,24 +191,46 @@ __global__ __launch_bounds__(NT) void gemv_ref_kernel(GemvArgs a, int total_batc
     // ---- prologue: the activation, with the folded norm in the reference's arithmetic, quantized into LDS
     const bool norm = a.xsrc == XSRC_NORM;
     float scale = 1.0f;
-    if (norm) {
-        const float v = ref_norm_value(a.x, cols, a.norm_l2, red);
-        scale = a.norm_l2 ? 1.0f / fmaxf(sqrtf(v), a.norm_eps) : 1.0f / sqrtf(v + a.norm_eps);
-    }
     if constexpr (KQ) {
+        if (norm) {
+            const float v = ref_norm_value(a.x, cols, a.norm_l2, red);
+            scale = a.norm_l2 ? 1.0f / fmaxf(sqrtf(v), a.norm_eps) : 1.0f / sqrtf(v + a.norm_eps);
+        }
         quantize_q8_K(a.x, cols, norm, a.norm_w, scale, s.xq, s.bs, s.info);
     } else {
+        // thread t's items t + NT g (16 floats each) are loaded once, for the norm's share and the quantization
+        constexpr int R = (NU + 1) / 2;  // rounds: cols <= 2048 NU = 16 NT R
         const int n16 = cols / 16;
-        for (int g = 0; g * NT < n16; ++g) {
-            const int i = item_of(g, n16);
-            float v[16];
-            load16(a.x + size_t(i) * 16, v);
-            if (norm) {
-                if (a.norm_w) {
-                    float w[16];
-                    load16(a.norm_w + size_t(i) * 16, w);
+        float xv[R][16], wv[R][16];
+        const bool normw = norm && a.norm_w;
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) v[j] = (v[j] * scale) * w[j];
+        for (int g = 0; g < R; ++g) {
+            const int i = item_of(g, n16);
+            load16(a.x + size_t(i) * 16, xv[g]);
+            load16(normw ? a.norm_w + size_t(i) * 16 : a.x + size_t(i) * 16, wv[g]);
+        }
+        if (norm) {
+            double p = 0.0;
+#pragma unroll
+            for (int g = 0; g < R; ++g) {
+                if (tid + NT * g < n16) {
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+                        const float sq = xv[g][j] * xv[g][j];
+                        p += double(sq);
+                    }
+                }
+            }
+            const float v = ref_norm_reduce(p, a.x, cols, a.norm_l2, red);
+            scale = a.norm_l2 ? 1.0f / fmaxf(sqrtf(v), a.norm_eps) : 1.0f / sqrtf(v + a.norm_eps);
+        }
+#pragma unroll
+        for (int g = 0; g < R; ++g) {
+            float * v = xv[g];
+            if (norm) {
+                if (normw) {
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) v[j] = (v[j] * scale) * wv[g][j];
                 } else {
 #pragma unroll
                     for (int j = 0; j < 16; ++j) v[j] = v[j] * scale;
