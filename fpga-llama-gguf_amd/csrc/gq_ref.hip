@@ -226,12 +226,12 @@ __global__ __launch_bounds__(256) void attn_ref_kernel(AttnArgs a, int tok) {
     for (int p = tid; p < n; p += 256) {
         const uint4 * kr = reinterpret_cast<const uint4 *>(t.kc + (size_t(p) * a.n_head_kv + kvh) * hd);
         double acc = 0.0;
-        for (int d0 = 0; d0 < hd; d0 += 64) {  // head_dim: a power of two from 16 (8 halves per 16 bytes)
-            uint4 w[8];
+        for (int d0 = 0; d0 < hd; d0 += 128) {  // head_dim: a power of two from 16 (8 halves per 16 bytes)
+            uint4 w[16];  // up to 128 halves of the row requested together
 #pragma unroll
-            for (int i = 0; i < 8; ++i) w[i] = d0 + 8 * i < hd ? kr[(d0 >> 3) + i] : make_uint4(0u, 0u, 0u, 0u);
+            for (int i = 0; i < 16; ++i) w[i] = d0 + 8 * i < hd ? kr[(d0 >> 3) + i] : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < 16; ++i) {
                 const uint32_t u[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
@@ -275,16 +275,12 @@ __global__ __launch_bounds__(256) void attn_ref_kernel(AttnArgs a, int tok) {
     const size_t vs = size_t(a.n_head_kv) * hd;  // between positions
     double acc = 0.0;
     int p = 0;
-    for (; p + 8 <= n; p += 8) {
-        uint16_t v[8];
-        float pp[8];
+    for (; p + 32 <= n; p += 32) {  // 32 positions' values requested together, then added in order
+        uint16_t v[32];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            v[i] = vcol[size_t(p + i) * vs];
-            pp[i] = sp[p + i];
-        }
+        for (int i = 0; i < 32; ++i) v[i] = vcol[size_t(p + i) * vs];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc += double(h2f(v[i]) * pp[i]);
+        for (int i = 0; i < 32; ++i) acc += double(h2f(v[i]) * sp[p + i]);
     }
     for (; p < n; ++p) acc += double(h2f(vcol[size_t(p) * vs]) * sp[p]);
     float o = float(acc);
