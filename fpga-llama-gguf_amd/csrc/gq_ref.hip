@@ -209,24 +209,38 @@ __global__ __launch_bounds__(256) void attn_ref_append_kernel(AttnArgs a, int to
 // Workgroup = q head: scores over positions 0 .. pos (a thread per position, the F16 dot summed in double in index
 // order), the max, e^(s - max) and their sum in order (thread 0), the fp16 probabilities, then thread d sums p * v[d]
 // over the positions in order. The scores and probabilities sit in LDS up to RA_LDS positions, else in sp (n_ctx
-// floats per q head of scratch). Each row is read 16 bytes at a time and each sum's terms are requested in groups
-// ahead of the chain of additions, which keeps the order of the additions.
-constexpr int RA_LDS = 8192;
+// floats per q head of scratch). A key row is read 16 bytes at a time, 128 halves requested together. The values
+// are staged in LDS in chunks of RA_CP positions by LDS DMA (each wave requests its share of a chunk's rows at once,
+// the workgroup waits for the chunk once), and thread d adds the chunk's p * v[d] from LDS in position order.
+constexpr int RA_LDS = 6144;
+constexpr int RA_CP = 256;  // positions per staged chunk of values: RA_CP * 2 * head_dim bytes of dynamic LDS
+template <int HD>  // head_dim: a power of two from 16 to 256
 __global__ __launch_bounds__(256) void attn_ref_kernel(AttnArgs a, int tok) {
     __shared__ float qv[256], red[4], inv;
     __shared__ float spl[RA_LDS];
     const AttnTok t = attn_tok(a, tok);
     if (t.pos < 0 || t.pos >= a.n_ctx) return;
-    const int h = blockIdx.x, hd = a.head_dim, tid = threadIdx.x, n = t.pos + 1;
+    constexpr int hd = HD;
+    const int h = blockIdx.x, tid = threadIdx.x, n = t.pos + 1;
     const int kvh = h / (a.n_head / a.n_head_kv);
     float * sp = n <= RA_LDS ? spl : a.part + size_t(h) * a.n_ctx;
     if (tid < hd) qv[tid] = a.qr[size_t(h) * hd + tid];
     __syncthreads();
+    // the query in registers, element d in lane d % 64 of word d / 64, read back as a scalar (readlane) at each step
+    // of the in-order sums
+    // (formed here, where every lane is active: readlane reads lanes that the loop below may leave inactive)
+    float qreg[(HD + 63) / 64];
+#pragma unroll
+    for (int k = 0; k < (HD + 63) / 64; ++k) {
+        qreg[k] = (tid & 63) + 64 * k < hd ? qv[(tid & 63) + 64 * k] : 0.0f;
+        asm volatile("" : "+v"(qreg[k]));
+    }
     float mx = -__builtin_inff();
     for (int p = tid; p < n; p += 256) {
         const uint4 * kr = reinterpret_cast<const uint4 *>(t.kc + (size_t(p) * a.n_head_kv + kvh) * hd);
         double acc = 0.0;
-        for (int d0 = 0; d0 < hd; d0 += 128) {  // head_dim: a power of two from 16 (8 halves per 16 bytes)
+#pragma unroll
+        for (int d0 = 0; d0 < hd; d0 += 128) {  // 8 halves per 16 bytes
             uint4 w[16];  // up to 128 halves of the row requested together
 #pragma unroll
             for (int i = 0; i < 16; ++i) w[i] = d0 + 8 * i < hd ? kr[(d0 >> 3) + i] : make_uint4(0u, 0u, 0u, 0u);
@@ -237,7 +251,8 @@ __global__ __launch_bounds__(256) void attn_ref_kernel(AttnArgs a, int tok) {
                 for (int j = 0; j < 8; ++j) {
                     const int d = d0 + 8 * i + j;
                     if (d < hd) {
-                        const float pr = qv[d] * h2f((u[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+                        const float qd = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qreg[d >> 6]), d & 63));
+                        const float pr = qd * h2f((u[j >> 1] >> (16 * (j & 1))) & 0xffffu);
                         acc += double(pr);
                     }
                 }
@@ -269,20 +284,43 @@ __global__ __launch_bounds__(256) void attn_ref_kernel(AttnArgs a, int tok) {
     }
     __syncthreads();
     for (int p = tid; p < n; p += 256) sp[p] = h2f(f2h(sp[p] * inv));
-    __syncthreads();
-    if (tid >= hd) return;
-    const uint16_t * vcol = t.vc + size_t(kvh) * hd + tid;
-    const size_t vs = size_t(a.n_head_kv) * hd;  // between positions
+    // values: chunks of RA_CP positions staged in LDS as rows of head_dim halves (a 1 KiB DMA instruction holds
+    // rpi = 512 / head_dim rows; lane l takes 16 bytes of row l / (head_dim / 8)); rows past pos read row pos
+    extern __shared__ __attribute__((aligned(16))) uint16_t vst[];
+    const unsigned vst_lds = unsigned(reinterpret_cast<uintptr_t>(vst));
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int lpr = hd / 8, rpi = 64 / lpr;  // lanes per row, rows per instruction
     double acc = 0.0;
-    int p = 0;
-    for (; p + 32 <= n; p += 32) {  // 32 positions' values requested together, then added in order
-        uint16_t v[32];
+    for (int c0 = 0; c0 < n; c0 += RA_CP) {
+        const int cp = min(RA_CP, n - c0), ninst = (cp + rpi - 1) / rpi;
+        __syncthreads();  // the probabilities are written, and the previous chunk's values are read
+        for (int i = wave; i < ninst; i += 4) {
+            const int r = min(c0 + i * rpi + lane / lpr, n - 1);
+            const uint16_t * src = t.vc + (size_t(r) * a.n_head_kv + kvh) * hd + (lane % lpr) * 8;
+            asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(vst_lds + unsigned(i) * 1024u),
+                         "v"(src)
+                         : "memory", "m0");
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid < hd) {
+            const uint16_t * vc = vst + tid;
+            int q = 0;
+            for (; q + 8 <= cp; q += 8) {
+                uint16_t v[8];
+                float pp[8];
 #pragma unroll
-        for (int i = 0; i < 32; ++i) v[i] = vcol[size_t(p + i) * vs];
+                for (int i = 0; i < 8; ++i) {
+                    v[i] = vc[(q + i) * hd];
+                    pp[i] = sp[c0 + q + i];
+                }
 #pragma unroll
-        for (int i = 0; i < 32; ++i) acc += double(h2f(v[i]) * sp[p + i]);
+                for (int i = 0; i < 8; ++i) acc += double(h2f(v[i]) * pp[i]);
+            }
+            for (; q < cp; ++q) acc += double(h2f(vc[q * hd]) * sp[c0 + q]);
+        }
     }
-    for (; p < n; ++p) acc += double(h2f(vcol[size_t(p) * vs]) * sp[p]);
+    if (tid >= hd) return;
     float o = float(acc);
     if (a.gate) o = cr::sigmoid(a.gate[size_t(tok) * a.n_head * a.q_stride + size_t(h) * 2 * hd + tid]) * o;
     a.y[(size_t(tok) * a.n_head + h) * hd + tid] = o;
@@ -331,11 +369,26 @@ hipError_t launch_gdn_ref(const GdnArgs & a, int tok, hipStream_t s) {
 }
 
 
+template <int HD>
+hipError_t launch_attn_ref_hd(const AttnArgs & a, int tok, hipStream_t s) {
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_ref_kernel<HD>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, RA_CP * 2 * HD);
+    if (attr != hipSuccess) return attr;
+    GQ_LAUNCH(attn_ref_kernel<HD>, dim3(a.n_head), dim3(256), size_t(RA_CP) * 2 * HD, s, a, tok);
+    return hipGetLastError();
+}
+
 hipError_t launch_attn_ref(const AttnArgs & a, int tok, hipStream_t s) {
     if (a.head_dim > 256 || a.n_head % a.n_head_kv) return hipErrorInvalidValue;
     GQ_LAUNCH(attn_ref_append_kernel, dim3(a.n_head + a.n_head_kv), dim3(256), 0, s, a, tok);
-    GQ_LAUNCH(attn_ref_kernel, dim3(a.n_head), dim3(256), 0, s, a, tok);
-    return hipGetLastError();
+    switch (a.head_dim) {
+    case 16: return launch_attn_ref_hd<16>(a, tok, s);
+    case 32: return launch_attn_ref_hd<32>(a, tok, s);
+    case 64: return launch_attn_ref_hd<64>(a, tok, s);
+    case 128: return launch_attn_ref_hd<128>(a, tok, s);
+    case 256: return launch_attn_ref_hd<256>(a, tok, s);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_crmath_hash(int fn, unsigned long long * hashes, hipStream_t s) {
