@@ -81,8 +81,8 @@ __device__ __forceinline__ double ordered_sumsq128(const float * p) {
 }
 
 __global__ __launch_bounds__(128) void gdn_ref_kernel(GdnArgs a, int tok) {
-    __shared__ __attribute__((aligned(16))) float qs[128], ks[128], ys[128];
-    __shared__ float sc[3];
+    __shared__ __attribute__((aligned(16))) float ys[128];
+    __shared__ float sc[3], gt[2];
     const int h = blockIdx.x, j = threadIdx.x, kh = h % a.hk;
     const float * q = a.q + size_t(tok) * a.s_qkv + kh * 128;
     const float * k = a.k + size_t(tok) * a.s_qkv + kh * 128;
@@ -101,54 +101,76 @@ __global__ __launch_bounds__(128) void gdn_ref_kernel(GdnArgs a, int tok) {
         s[i + 2] = t.z;
         s[i + 3] = t.w;
     }
-    // q and k staged in LDS by all threads, so the sequential sums below read LDS
-    const float qj = q[j], kj = k[j];
-    qs[j] = qj;
-    ks[j] = kj;
-    __syncthreads();
-    if (a.flags & GEMVQ_GDN_L2_QK) {  // ggml_l2_norm of q and k: 1 / max(sqrt(sum of squares), eps)
-        if (j == 0 || j == 64) {
-            const double sum = ordered_sumsq128(j == 0 ? qs : ks);
-            sc[j >> 6] = 1.0f / fmaxf(sqrtf(float(sum)), a.l2_eps);
+    // q and k in registers of both waves (element i in lane i % 64 of word i / 64), read back by readlane in the
+    // in-order sums and dots below (instead of an LDS read per step); the gate parameters and z requested now
+    const auto lane_of = [](float x, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)); };
+    const int l = j & 63;
+    float qr[2] = {q[l], q[l + 64]}, kr[2] = {k[l], k[l + 64]};
+    const float vj = v[j];
+    const float g_in = a.g[size_t(tok) * a.s_gb + h], b_in = a.beta[size_t(tok) * a.s_gb + h];
+    const bool gated = a.gz && (a.flags & GEMVQ_GDN_GATED);
+    const float zj = gated ? a.gz[(size_t(tok) * a.hv + h) * 128 + j] : 0.0f;
+    // wave 0: the L2 norms' in-order sums (lane 0); wave 1: the gates, at the same time
+    if (j < 64) {
+        if (a.flags & GEMVQ_GDN_L2_QK) {  // ggml_l2_norm of q and k: 1 / max(sqrt(sum of squares), eps)
+            double sq = 0.0, sk = 0.0;
+#pragma unroll
+            for (int i = 0; i < 128; ++i) {
+                const float x = lane_of(qr[i >> 6], i & 63), y = lane_of(kr[i >> 6], i & 63);
+                const float x2 = x * x, y2 = y * y;
+                sq += double(x2);
+                sk += double(y2);
+            }
+            if (j == 0) {
+                sc[0] = 1.0f / fmaxf(sqrtf(float(sq)), a.l2_eps);
+                sc[1] = 1.0f / fmaxf(sqrtf(float(sk)), a.l2_eps);
+            }
         }
-        __syncthreads();
-        const float s0 = sc[0], s1 = sc[1];
-        __syncthreads();
-        qs[j] = qj * s0;
-        ks[j] = kj * s1;
+    } else {
+        float g = g_in, beta = b_in;
+        if (a.flags & GEMVQ_GDN_GATES) {  // beta = sigmoid(b), g = softplus(alpha + dt) * a
+            g = cr::softplus(g + a.dt[h]) * a.a[h];
+            beta = cr::sigmoid(beta);
+        }
+        if (j == 64) {
+            gt[0] = beta;
+            gt[1] = cr::expf(g);
+        }
     }
-    float g = a.g[size_t(tok) * a.s_gb + h], beta = a.beta[size_t(tok) * a.s_gb + h];
-    if (a.flags & GEMVQ_GDN_GATES) {  // beta = sigmoid(b), g = softplus(alpha + dt) * a
-        g = cr::softplus(g + a.dt[h]) * a.a[h];
-        beta = cr::sigmoid(beta);
-    }
-    const float decay = cr::expf(g);
     __syncthreads();
+    const float beta = gt[0], decay = gt[1];
+    if (a.flags & GEMVQ_GDN_L2_QK) {
+        const float s0 = sc[0], s1 = sc[1];
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            qr[w] = qr[w] * s0;
+            kr[w] = kr[w] * s1;
+        }
+    }
     float dot = 0.0f;
 #pragma unroll
     for (int i = 0; i < 128; ++i) {
         s[i] = s[i] * decay;
-        dot += s[i] * ks[i];
+        dot += s[i] * lane_of(kr[i >> 6], i & 63);
     }
-    const float delta = (v[j] - dot) * beta;
+    const float delta = (vj - dot) * beta;
     float out = 0.0f;
 #pragma unroll
     for (int i = 0; i < 128; ++i) {
-        s[i] += ks[i] * delta;
-        out += s[i] * qs[i];
+        s[i] += lane_of(kr[i >> 6], i & 63) * delta;
+        out += s[i] * lane_of(qr[i >> 6], i & 63);
     }
 #pragma unroll
     for (int i = 0; i < 128; i += 4) *reinterpret_cast<float4 *>(dst + row + i) = make_float4(s[i], s[i + 1], s[i + 2], s[i + 3]);
     float yv = out * a.scale;
-    if (a.gz && (a.flags & GEMVQ_GDN_GATED)) {
+    if (gated) {
         // the gated output norm of this head (RMS_NORM -> MUL weight -> MUL SILU(z), ggml-xrt.cpp:1952-1975): the sum
         // of the squares in order in double, then ((y * sc) * w) * silu(z)
         ys[j] = yv;
         __syncthreads();
         if (j == 0) sc[2] = 1.0f / sqrtf(float(ordered_sumsq128(ys) / 128.0) + a.rms_eps);
         __syncthreads();
-        const float z = a.gz[(size_t(tok) * a.hv + h) * 128 + j];
-        yv = ((yv * sc[2]) * a.gw[j]) * ((a.flags & GEMVQ_GDN_Z_SILU) ? z : cr::silu(z));
+        yv = ((yv * sc[2]) * a.gw[j]) * ((a.flags & GEMVQ_GDN_Z_SILU) ? zj : cr::silu(zj));
     }
     a.y[size_t(tok) * a.s_y + h * 128 + j] = yv;
 }
