@@ -253,8 +253,9 @@ int gemvq_profile(gemvq_ctx * ctx, const uint32_t * cmds, unsigned n_cmds, int r
  * K-quants' eight FP32 partial sums), norm sums of FP32 squares in double in index order, the DeltaNet step's dots in
  * order, attention with double sums (ggml's CPU path), and correctly rounded exp / log (gemvq_cr_expf / _logf) where
  * the reference calls libm. Every command keeps its meaning; the fused forms whose arithmetic differs (the gated norm
- * in the next GEMV's prologue, GEMVQ_GDN_WITH_OUT) run unfused, a GEMM runs token by token as GEMV commands, and
- * CONV, GDN and ATTN with several tokens run token by token. Debug block sums are not written in this mode.
+ * in the next GEMV's prologue, GEMVQ_GDN_WITH_OUT) run unfused (the gated norm, in the reference's order, in the
+ * DeltaNet step's own launch), a GEMM runs token by token as GEMV commands, and CONV, GDN and ATTN with several
+ * tokens run token by token. Debug block sums are not written in this mode.
  * Returns 0 or GEMVQ_EINVAL. */
 #define GEMVQ_ARITH_CANONICAL 0
 #define GEMVQ_ARITH_REFERENCE 1
