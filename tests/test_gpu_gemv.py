@@ -41,6 +41,8 @@ def run_gemv(gq, t, rows, cols, w, x, blocksums=False):
     (8, 64, 256), (8, 100, 2560), (8, 40, 9728), (8, 31, 4096),
     (13, 64, 256), (13, 50, 4096), (13, 20, 12288),
     (14, 64, 256), (14, 50, 4096), (14, 20, 12288), (14, 7, 16384),
+    # Q4_0 / Q4_1 / Q8_0 rows of an odd number of 32-column blocks (one block, three, five, 81, 129)
+    (2, 37, 32), (3, 9, 96), (8, 70, 160), (2, 33, 2592), (8, 5, 4128), (3, 21, 800),
 ])
 def test_gemv_formats_bitexact(gq, orc, t, rows, cols):
     w = gq.matrix(t, rows, cols, SEED, 1 + t, std=0.02)

@@ -33,6 +33,7 @@ def test_correctly_rounded_math_on_every_input(gq, orc, ctx, fn):
 @pytest.mark.parametrize("t,rows,cols", [
     (2, 300, 2560), (2, 64, 12288), (2, 129, 512), (8, 257, 2560), (8, 40, 16384), (3, 200, 4096),
     (14, 301, 4096), (14, 33, 12288), (13, 130, 4096), (13, 50, 2048),
+    (2, 37, 96), (8, 70, 2592), (3, 11, 160), (8, 9, 32),  # odd numbers of 32-column blocks
 ])
 def test_gemv_rows(gq, orc, ctx, t, rows, cols):
     """GEMV rows in every weight format equal gemvq_ref.h's sequential FP32 rows (orc_ref_gemv, itself pinned to
@@ -202,11 +203,14 @@ def test_gdn_layer_step(gq, orc, ctx, hv, hk, ntok, z_silu):
     assert_bits(ctx.state_read(0, hv * S), st, "state")
 
 
-@pytest.mark.parametrize("nh,nkv,hd,nrot,npos", [(16, 4, 256, 64, 70), (6, 2, 128, 128, 3)])
+@pytest.mark.parametrize("nh,nkv,hd,nrot,npos", [
+    (16, 4, 256, 64, 70), (6, 2, 128, 128, 3),
+    (8, 2, 64, 64, 300), (4, 1, 32, 32, 20), (2, 2, 16, 16, 9),  # values staged in 256-position chunks
+])
 def test_attention(gq, orc, ctx, nh, nkv, hd, nrot, npos):
     """Attention token by token (q / k RMS norm, RoPE, fp16 cache, softmax, sigmoid gate) against the reference
     decoder's attention (the reference's norms, ggml's CPU softmax with double sums)."""
-    n_ctx = 128
+    n_ctx = 128 if npos <= 128 else 320
     kv = ctx.kv_create(n_ctx, nkv, hd)
     qn = gq.uniform(9, 1, hd, 0.5, 1.5)
     kn = gq.uniform(9, 2, hd, 0.5, 1.5)
@@ -234,7 +238,7 @@ def test_attention(gq, orc, ctx, nh, nkv, hd, nrot, npos):
         kh = orc.rope(orc.ref_rownorm(k, kn, hd, nkv, EPS), cs, nrot, hd, nkv)
         kc[pos] = orc.f2h(kh).reshape(nkv, hd)
         vc[pos] = orc.f2h(v).reshape(nkv, hd)
-        if pos in (0, 1, npos - 1, 63, 64):
+        if pos in (0, 1, npos - 1, 63, 64, 255, 256, 257):
             att = orc.ref_attn_cr(qh, kc, vc, nh, nkv, hd, pos + 1, 1 / 16)
             gate = qg.reshape(nh, 2 * hd)[:, hd:].ravel()
             assert_bits(ctx.read(O["y"], nh * hd), orc.ref_unary_cr(gate, 2) * att, f"attention at {pos}")
