@@ -32,7 +32,9 @@ __device__ inline double dpp_f64(double v) {
 }
 // The second half of ref_norm_value: each thread's partial p of T (the double squares of its share of the row, in
 // any order; the shares together cover the row once), then the workgroup's sum, the check and the fallback.
-__device__ inline float ref_norm_reduce(double p, const float * x, int n, int l2, double * red) {
+// The workgroup's sum of the threads' doubles p (in no particular order), on every thread; red holds a double per
+// wave. Ends with the threads' reads of red pending: a following use of red needs a barrier first.
+__device__ inline double ref_block_sum(double p, double * red) {
     const int tid = threadIdx.x, nt = blockDim.x;
     // across the wave: within rows of 16 lanes by DPP, then across the rows
     p += dpp_f64<DPP_XOR1>(p);
@@ -45,6 +47,11 @@ __device__ inline float ref_norm_reduce(double p, const float * x, int n, int l2
     __syncthreads();
     double t = 0.0;
     for (int w = 0; w < nt / 64; ++w) t += red[w];
+    return t;
+}
+__device__ inline float ref_norm_reduce(double p, const float * x, int n, int l2, double * red) {
+    const int tid = threadIdx.x;
+    const double t = ref_block_sum(p, red);
     const double e = double(n + 64) * 2.220446049250313080847e-16 * t;
     const double lo = t - e, hi = t + e;
     const float vlo = l2 ? float(lo) : float(lo / double(n));

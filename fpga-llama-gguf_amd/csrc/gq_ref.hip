@@ -64,25 +64,9 @@ __global__ void conv_ref_kernel(ConvArgs a, int tok) {
 
 // ---- DeltaNet step, one token (gemvq_ref.h:360-397 with ggml's L2_NORM and gate ops around it,
 // ggml-xrt.cpp:1977-2000): workgroup = value head h, thread j = state row j ----
-// Sum of squares of 128 LDS floats in index order, in double (read 16 bytes at a time, two reads ahead).
-__device__ __forceinline__ double ordered_sumsq128(const float * p) {
-    const float4 * p4 = reinterpret_cast<const float4 *>(p);
-    double sum = 0.0;
-    for (int i = 0; i < 32; i += 2) {
-        const float4 a = p4[i], b = p4[i + 1];
-        const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float sq = x[e] * x[e];
-            sum += double(sq);
-        }
-    }
-    return sum;
-}
-
 __global__ __launch_bounds__(128) void gdn_ref_kernel(GdnArgs a, int tok) {
-    __shared__ __attribute__((aligned(16))) float ys[128];
-    __shared__ float sc[3], gt[2];
+    __shared__ float ys[128];
+    __shared__ double red[2];
     const int h = blockIdx.x, j = threadIdx.x, kh = h % a.hk;
     const float * q = a.q + size_t(tok) * a.s_qkv + kh * 128;
     const float * k = a.k + size_t(tok) * a.s_qkv + kh * 128;
@@ -102,7 +86,7 @@ __global__ __launch_bounds__(128) void gdn_ref_kernel(GdnArgs a, int tok) {
         s[i + 3] = t.w;
     }
     // q and k in registers of both waves (element i in lane i % 64 of word i / 64), read back by readlane in the
-    // in-order sums and dots below (instead of an LDS read per step); the gate parameters and z requested now
+    // in-order dots below (instead of an LDS read per step); the gate parameters and z requested now
     const auto lane_of = [](float x, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)); };
     const int l = j & 63;
     float qr[2] = {q[l], q[l + 64]}, kr[2] = {k[l], k[l + 64]};
@@ -110,37 +94,21 @@ __global__ __launch_bounds__(128) void gdn_ref_kernel(GdnArgs a, int tok) {
     const float g_in = a.g[size_t(tok) * a.s_gb + h], b_in = a.beta[size_t(tok) * a.s_gb + h];
     const bool gated = a.gz && (a.flags & GEMVQ_GDN_GATED);
     const float zj = gated ? a.gz[(size_t(tok) * a.hv + h) * 128 + j] : 0.0f;
-    // wave 0: the L2 norms' in-order sums (lane 0); wave 1: the gates, at the same time
-    if (j < 64) {
-        if (a.flags & GEMVQ_GDN_L2_QK) {  // ggml_l2_norm of q and k: 1 / max(sqrt(sum of squares), eps)
-            double sq = 0.0, sk = 0.0;
-#pragma unroll
-            for (int i = 0; i < 128; ++i) {
-                const float x = lane_of(qr[i >> 6], i & 63), y = lane_of(kr[i >> 6], i & 63);
-                const float x2 = x * x, y2 = y * y;
-                sq += double(x2);
-                sk += double(y2);
-            }
-            if (j == 0) {
-                sc[0] = 1.0f / fmaxf(sqrtf(float(sq)), a.l2_eps);
-                sc[1] = 1.0f / fmaxf(sqrtf(float(sk)), a.l2_eps);
-            }
-        }
-    } else {
-        float g = g_in, beta = b_in;
-        if (a.flags & GEMVQ_GDN_GATES) {  // beta = sigmoid(b), g = softplus(alpha + dt) * a
-            g = cr::softplus(g + a.dt[h]) * a.a[h];
-            beta = cr::sigmoid(beta);
-        }
-        if (j == 64) {
-            gt[0] = beta;
-            gt[1] = cr::expf(g);
-        }
+    // the gates (every thread alike): beta = sigmoid(b), g = softplus(alpha + dt) * a
+    float beta = b_in, decay = g_in;
+    if (a.flags & GEMVQ_GDN_GATES) {
+        decay = cr::softplus(decay + a.dt[h]) * a.a[h];
+        beta = cr::sigmoid(beta);
     }
-    __syncthreads();
-    const float beta = gt[0], decay = gt[1];
+    decay = cr::expf(decay);
     if (a.flags & GEMVQ_GDN_L2_QK) {
-        const float s0 = sc[0], s1 = sc[1];
+        // ggml_l2_norm of q and k, 1 / max(sqrt(sum of squares), eps): each double sum of squares formed across the
+        // workgroup (thread j: element j) and checked against its rounding bound (the in-order sum where the bound
+        // does not fix its FP32 rounding)
+        const float xq = j < 64 ? qr[0] : qr[1], xk = j < 64 ? kr[0] : kr[1];
+        const float sq = xq * xq, sk = xk * xk;
+        const float s0 = 1.0f / fmaxf(sqrtf(ref_norm_reduce(double(sq), q, 128, 1, red)), a.l2_eps);
+        const float s1 = 1.0f / fmaxf(sqrtf(ref_norm_reduce(double(sk), k, 128, 1, red)), a.l2_eps);
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
             qr[w] = qr[w] * s0;
@@ -164,13 +132,13 @@ __global__ __launch_bounds__(128) void gdn_ref_kernel(GdnArgs a, int tok) {
     for (int i = 0; i < 128; i += 4) *reinterpret_cast<float4 *>(dst + row + i) = make_float4(s[i], s[i + 1], s[i + 2], s[i + 3]);
     float yv = out * a.scale;
     if (gated) {
-        // the gated output norm of this head (RMS_NORM -> MUL weight -> MUL SILU(z), ggml-xrt.cpp:1952-1975): the sum
-        // of the squares in order in double, then ((y * sc) * w) * silu(z)
+        // the gated output norm of this head (RMS_NORM -> MUL weight -> MUL SILU(z), ggml-xrt.cpp:1952-1975): the
+        // double sum of the squares (formed across the workgroup, checked against its rounding bound), then
+        // ((y * sc) * w) * silu(z)
         ys[j] = yv;
-        __syncthreads();
-        if (j == 0) sc[2] = 1.0f / sqrtf(float(ordered_sumsq128(ys) / 128.0) + a.rms_eps);
-        __syncthreads();
-        yv = ((yv * sc[2]) * a.gw[j]) * ((a.flags & GEMVQ_GDN_Z_SILU) ? zj : cr::silu(zj));
+        const float y2 = yv * yv;
+        const float sn = 1.0f / sqrtf(ref_norm_reduce(double(y2), ys, 128, 0, red) + a.rms_eps);
+        yv = ((yv * sn) * a.gw[j]) * ((a.flags & GEMVQ_GDN_Z_SILU) ? zj : cr::silu(zj));
     }
     a.y[size_t(tok) * a.s_y + h * 128 + j] = yv;
 }
@@ -194,7 +162,8 @@ __device__ inline AttnTok attn_tok(const AttnArgs & a, int tok) {
 // Workgroup s < n_head: q head s, normalized (RMS, weight), rotated (NEOX) and rounded to fp16 into qr; the others:
 // the new key of KV head s - n_head, normalized and rotated, and the value, stored as fp16 at the position.
 __global__ __launch_bounds__(256) void attn_ref_append_kernel(AttnArgs a, int tok) {
-    __shared__ float xs[256], scs;
+    __shared__ float xs[256];
+    __shared__ double red[4];
     const AttnTok t = attn_tok(a, tok);
     if (t.pos < 0 || t.pos >= a.n_ctx) return;  // positions past the KV capacity are not stored
     const int s = blockIdx.x, hd = a.head_dim, e = threadIdx.x, half = a.n_rot / 2;
@@ -202,16 +171,12 @@ __global__ __launch_bounds__(256) void attn_ref_append_kernel(AttnArgs a, int to
     const int h = isq ? s : s - a.n_head;
     const float * x = isq ? a.q + size_t(tok) * a.n_head * a.q_stride + size_t(h) * a.q_stride
                           : a.k + (size_t(tok) * a.n_head_kv + h) * hd;
-    if (e == 0) {
-        double sum = 0.0;
-        for (int i = 0; i < hd; ++i) {
-            const float sq = x[i] * x[i];
-            sum += double(sq);
-        }
-        scs = 1.0f / sqrtf(float(sum / double(hd)) + a.eps);
-    }
-    __syncthreads();
-    if (e < hd) xs[e] = (x[e] * scs) * (isq ? a.qn[e] : a.kn[e]);
+    // the row's double sum of squares formed across the workgroup and checked against its rounding bound (the
+    // in-order sum where the bound does not fix the mean's rounding)
+    const float xe = e < hd ? x[e] : 0.0f;
+    const float sq = xe * xe;
+    const float scs = 1.0f / sqrtf(ref_norm_reduce(double(sq), x, hd, 0, red) + a.eps);
+    if (e < hd) xs[e] = (xe * scs) * (isq ? a.qn[e] : a.kn[e]);
     __syncthreads();
     if (e >= hd) return;
     const float * cs = a.cs + size_t(t.pos) * a.n_rot;
@@ -228,29 +193,99 @@ __global__ __launch_bounds__(256) void attn_ref_append_kernel(AttnArgs a, int to
     }
 }
 
-// Workgroup = q head: scores over positions 0 .. pos (a thread per position, the F16 dot summed in double in index
-// order), the max, e^(s - max) and their sum in order (thread 0), the fp16 probabilities, then thread d sums p * v[d]
-// over the positions in order. The scores and probabilities sit in LDS up to RA_LDS positions, else in sp (n_ctx
-// floats per q head of scratch). A key row is read 16 bytes at a time, 128 halves requested together. The values
-// are staged in LDS in chunks of RA_CP positions by LDS DMA (each wave requests its share of a chunk's rows at once,
-// the workgroup waits for the chunk once), and thread d adds the chunk's p * v[d] from LDS in position order.
+// Workgroup = q head, for the positions 0 .. pos:
+// - scores: a thread per position, the F16 dot summed in double in index order (the products q * k are exact in
+//   FP32); a thread keeps up to three positions' sums (256 apart) interleaved, its key rows read 32 halves at a time
+//   with the next 32 requested before the current ones are summed;
+// - the max, e^(s - max), their double sum and the fp16 probabilities;
+// - values: thread d sums p * v[d] over the positions in order, the values staged in LDS in chunks of RA_CP
+//   positions by LDS DMA (each wave requests its share of a chunk's rows at once, the workgroup waits for the chunk
+//   once).
+// The scores and probabilities sit in LDS up to RA_LDS positions, else in sp (n_ctx floats per q head of scratch).
 constexpr int RA_LDS = 6144;
 constexpr int RA_CP = 256;  // positions per staged chunk of values: RA_CP * 2 * head_dim bytes of dynamic LDS
+// x times the fp16 value in the low (HI = 0) or high half of h, in one instruction (v_fma_mix_f32 with a zero
+// addend). The product of an fp16 value and an fp16-valued float is exact in FP32 (22 significant bits, at least
+// 2^-48), so for finite values this is the FP32 product h2f(half) * x, but for the sign of a zero product (+0 where
+// the product is -0), which no double sum starting at +0 can tell apart.
+template <int HI>
+__device__ __forceinline__ float mul_f16(float x, uint32_t h) {
+    float r;
+    if constexpr (HI) asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(x), "v"(h));
+    else asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(x), "v"(h));
+    return r;
+}
+
+// The scores of positions p0 + 256 g (g < G; positions at or past n read row n - 1 and store nothing).
+template <int HD, int G>
+__device__ __forceinline__ void attn_ref_scores(const AttnArgs & a, const AttnTok & t, int kvh, int p0, int n,
+                                                const float * qreg, float * sp, float & mx) {
+    constexpr int NS = (HD + 31) / 32, NL = HD < 32 ? HD / 8 : 4;  // steps of 32 halves, 16-byte loads per step
+    const uint4 * kr[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int p = min(p0 + 256 * g, n - 1);
+        kr[g] = reinterpret_cast<const uint4 *>(t.kc + (size_t(p) * a.n_head_kv + kvh) * HD);
+    }
+    double acc[G];
+    uint4 w[2][G][NL];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        acc[g] = 0.0;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) w[0][g][i] = kr[g][i];
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        if (s + 1 < NS) {
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int i = 0; i < NL; ++i) w[(s + 1) & 1][g][i] = kr[g][4 * (s + 1) + i];
+        }
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int d = 32 * s + 8 * i + j;
+                const float qd = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qreg[d >> 6]), d & 63));
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const uint4 & x = w[s & 1][g][i];
+                    const uint32_t u = (j >> 1) == 0 ? x.x : (j >> 1) == 1 ? x.y : (j >> 1) == 2 ? x.z : x.w;
+                    const float pr = (j & 1) ? mul_f16<1>(qd, u) : mul_f16<0>(qd, u);  // q * k, exact
+                    acc[g] += double(pr);
+                }
+            }
+        }
+        // this step's sums complete before the loads of the step after next are issued
+#pragma unroll
+        for (int g = 0; g < G; ++g) asm volatile("" : "+v"(acc[g])::"memory");
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int p = p0 + 256 * g;
+        if (p < n) {
+            const float sc = float(acc[g]) * a.scale;
+            sp[p] = sc;
+            mx = fmaxf(mx, sc);
+        }
+    }
+}
+
+// q head blockIdx.x over positions 0 .. n - 1, its scores and probabilities in sp
 template <int HD>  // head_dim: a power of two from 16 to 256
-__global__ __launch_bounds__(256) void attn_ref_kernel(AttnArgs a, int tok) {
-    __shared__ float qv[256], red[4], inv;
-    __shared__ float spl[RA_LDS];
-    const AttnTok t = attn_tok(a, tok);
-    if (t.pos < 0 || t.pos >= a.n_ctx) return;
+__device__ __forceinline__ void attn_ref_head(const AttnArgs & a, int tok, const AttnTok & t, int n, float * sp) {
+    __shared__ float qv[256], red[4];
+    __shared__ double dred[4];
     constexpr int hd = HD;
-    const int h = blockIdx.x, tid = threadIdx.x, n = t.pos + 1;
+    const int h = blockIdx.x, tid = threadIdx.x;
     const int kvh = h / (a.n_head / a.n_head_kv);
-    float * sp = n <= RA_LDS ? spl : a.part + size_t(h) * a.n_ctx;
     if (tid < hd) qv[tid] = a.qr[size_t(h) * hd + tid];
     __syncthreads();
     // the query in registers, element d in lane d % 64 of word d / 64, read back as a scalar (readlane) at each step
     // of the in-order sums
-    // (formed here, where every lane is active: readlane reads lanes that the loop below may leave inactive)
+    // (formed here, where every lane is active: readlane reads lanes that the sums may leave inactive)
     float qreg[(HD + 63) / 64];
 #pragma unroll
     for (int k = 0; k < (HD + 63) / 64; ++k) {
@@ -258,53 +293,46 @@ __global__ __launch_bounds__(256) void attn_ref_kernel(AttnArgs a, int tok) {
         asm volatile("" : "+v"(qreg[k]));
     }
     float mx = -__builtin_inff();
-    for (int p = tid; p < n; p += 256) {
-        const uint4 * kr = reinterpret_cast<const uint4 *>(t.kc + (size_t(p) * a.n_head_kv + kvh) * hd);
-        double acc = 0.0;
-#pragma unroll
-        for (int d0 = 0; d0 < hd; d0 += 128) {  // 8 halves per 16 bytes
-            uint4 w[16];  // up to 128 halves of the row requested together
-#pragma unroll
-            for (int i = 0; i < 16; ++i) w[i] = d0 + 8 * i < hd ? kr[(d0 >> 3) + i] : make_uint4(0u, 0u, 0u, 0u);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const uint32_t u[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int d = d0 + 8 * i + j;
-                    if (d < hd) {
-                        const float qd = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qreg[d >> 6]), d & 63));
-                        const float pr = qd * h2f((u[j >> 1] >> (16 * (j & 1))) & 0xffffu);
-                        acc += double(pr);
-                    }
-                }
-            }
-        }
-        const float sc = float(acc) * a.scale;
-        sp[p] = sc;
-        mx = fmaxf(mx, sc);
-    }
+    const int rounds = (n + 255) / 256;
+    int r = 0;
+    for (; r + 3 <= rounds; r += 3) attn_ref_scores<HD, 3>(a, t, kvh, tid + 256 * r, n, qreg, sp, mx);
+    if (rounds - r == 2) attn_ref_scores<HD, 2>(a, t, kvh, tid + 256 * r, n, qreg, sp, mx);
+    else if (rounds - r == 1) attn_ref_scores<HD, 1>(a, t, kvh, tid + 256 * r, n, qreg, sp, mx);
 #pragma unroll
     for (int st = 32; st >= 1; st >>= 1) mx = fmaxf(mx, __shfl_xor(mx, st, 64));
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int p = tid; p < n; p += 256) sp[p] = cr::expf(sp[p] - mx);
-    __syncthreads();
-    if (tid == 0) {
-        double sum = 0.0;
-        int p = 0;
-        for (; p + 8 <= n; p += 8) {
-            float e[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) e[i] = sp[p + i];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) sum += double(e[i]);
-        }
-        for (; p < n; ++p) sum += double(sp[p]);
-        inv = float(1.0 / sum);
+    // e^(s - max) and their double sum, formed across the workgroup; the in-order sum fixes 1 / sum rounded to FP32
+    // whenever the tree sum's error bound leaves that rounding open
+    double pe = 0.0;
+    for (int p = tid; p < n; p += 256) {
+        const float e = cr::expf(sp[p] - mx);
+        sp[p] = e;
+        pe += double(e);
     }
-    __syncthreads();
+    const double ts = ref_block_sum(pe, dred);  // also the barrier after every e is stored
+    const double es = double(n + 64) * 2.220446049250313080847e-16 * ts;
+    const float ilo = float(1.0 / (ts + es)), ihi = float(1.0 / (ts - es));
+    float inv = ilo;
+    if (!(ilo == ihi)) {  // the same on every thread
+        __syncthreads();
+        if (tid == 0) {
+            double sum = 0.0;
+            int p = 0;
+            for (; p + 8 <= n; p += 8) {
+                float e[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) e[i] = sp[p + i];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) sum += double(e[i]);
+            }
+            for (; p < n; ++p) sum += double(sp[p]);
+            dred[0] = sum;
+        }
+        __syncthreads();
+        inv = float(1.0 / dred[0]);
+    }
     for (int p = tid; p < n; p += 256) sp[p] = h2f(f2h(sp[p] * inv));
     // values: chunks of RA_CP positions staged in LDS as rows of head_dim halves (a 1 KiB DMA instruction holds
     // rpi = 512 / head_dim rows; lane l takes 16 bytes of row l / (head_dim / 8)); rows past pos read row pos
@@ -326,26 +354,52 @@ __global__ __launch_bounds__(256) void attn_ref_kernel(AttnArgs a, int tok) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (tid < hd) {
+            // in position order, the next 16 positions' values and probabilities read from LDS while the current
+            // 16 are added
             const uint16_t * vc = vst + tid;
-            int q = 0;
-            for (; q + 8 <= cp; q += 8) {
-                uint16_t v[8];
-                float pp[8];
+            const float * pc = sp + c0;
+            const int ng = cp / 16;
+            uint16_t v0[16], v1[16];
+            float p0[16], p1[16];
+            const auto load = [&](int q0, uint16_t * v, float * pp) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    v[i] = vc[(q + i) * hd];
-                    pp[i] = sp[c0 + q + i];
+                for (int i = 0; i < 16; ++i) {
+                    v[i] = vc[(q0 + i) * hd];
+                    pp[i] = pc[q0 + i];
                 }
+            };
+            const auto add = [&](const uint16_t * v, const float * pp) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) acc += double(h2f(v[i]) * pp[i]);
+                for (int i = 0; i < 16; ++i) acc += double(mul_f16<0>(pp[i], v[i]));  // p * v, exact
+                asm volatile("" : "+v"(acc)::"memory");  // these sums complete before the loads after them
+            };
+            if (ng > 0) load(0, v0, p0);
+            for (int g = 0; g < ng; g += 2) {
+                if (g + 1 < ng) load(16 * (g + 1), v1, p1);
+                add(v0, p0);
+                if (g + 1 < ng) {
+                    if (g + 2 < ng) load(16 * (g + 2), v0, p0);
+                    add(v1, p1);
+                }
             }
-            for (; q < cp; ++q) acc += double(h2f(vc[q * hd]) * sp[c0 + q]);
+            for (int q = 16 * ng; q < cp; ++q) acc += double(h2f(vc[q * hd]) * pc[q]);
         }
     }
     if (tid >= hd) return;
     float o = float(acc);
     if (a.gate) o = cr::sigmoid(a.gate[size_t(tok) * a.n_head * a.q_stride + size_t(h) * 2 * hd + tid]) * o;
     a.y[(size_t(tok) * a.n_head + h) * hd + tid] = o;
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_ref_kernel(AttnArgs a, int tok) {
+    __shared__ float spl[RA_LDS];
+    const AttnTok t = attn_tok(a, tok);
+    if (t.pos < 0 || t.pos >= a.n_ctx) return;
+    const int n = t.pos + 1;
+    // the scores in LDS (read and written by LDS instructions) or, past RA_LDS positions, in the head's scratch row
+    if (n <= RA_LDS) attn_ref_head<HD>(a, tok, t, n, spl);
+    else attn_ref_head<HD>(a, tok, t, n, a.part + size_t(blockIdx.x) * a.n_ctx);
 }
 
 // ---- exhaustive hash of the correctly rounded exp / log (block b: inputs b 2^20 .. b 2^20 + 2^20 - 1) ----

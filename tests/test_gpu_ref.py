@@ -172,13 +172,29 @@ def _gdn_reference(orc, state, q, k, v, ar, br, dt, a, z, wn, hv, hk, z_silu):
     return yt * (z if z_silu else orc.ref_unary_cr(z, 1)), st
 
 
-@pytest.mark.parametrize("hv,hk,ntok,z_silu", [(32, 16, 1, True), (16, 4, 1, False), (32, 16, 3, True)])
-def test_gdn_layer_step(gq, orc, ctx, hv, hk, ntok, z_silu):
+def boundary_row(n, i):
+    """Ones but element i, whose FP32 square is 1 + n 2^-24: the row's sum of squares, n + n 2^-24, lies halfway
+    between two floats, and so does its mean over n, 1 + 2^-24 (n a power of two up to 256): no tree sum with an
+    error bound decides either rounding, the in-order sum does (ties to even)."""
+    x = np.ones(n, np.float32)
+    x[i] = np.float32(1.0 + 2.0 ** (-25 + int(np.log2(n))))
+    assert np.float32(x[i] * x[i]) == np.float32(1.0 + n * 2.0 ** -24)
+    return x
+
+
+@pytest.mark.parametrize("hv,hk,ntok,z_silu,edge", [(32, 16, 1, True, False), (16, 4, 1, False, False),
+                                                    (32, 16, 3, True, False), (16, 4, 2, True, True)])
+def test_gdn_layer_step(gq, orc, ctx, hv, hk, ntok, z_silu, edge):
     """The DeltaNet GDN command as the model uses it (L2 q/k, gates from the raw projections, gated output norm),
-    for one token and for several in order."""
+    for one token and for several in order; edge: the first token's q and k rows of key head 0 with sums of squares
+    on a rounding boundary."""
     S = 128
     st0 = gq.normal(8, 1, hv * S * S, std=0.1)
     qkv = gq.normal(8, 2, ntok * (2 * hk + hv) * S)
+    if edge:
+        qkv[:S] = boundary_row(S, 5)
+        qkv[hk * S:hk * S + S] = boundary_row(S, 77)
+        assert np.float32(np.sum((qkv[:S] * qkv[:S]).astype(np.float64))) == np.float32(128.0)  # the tie, to even
     ab = gq.normal(8, 3, ntok * 2 * 64)
     dt = gq.normal(8, 4, hv)
     a = -np.abs(gq.normal(8, 5, hv))
@@ -203,13 +219,15 @@ def test_gdn_layer_step(gq, orc, ctx, hv, hk, ntok, z_silu):
     assert_bits(ctx.state_read(0, hv * S), st, "state")
 
 
-@pytest.mark.parametrize("nh,nkv,hd,nrot,npos", [
-    (16, 4, 256, 64, 70), (6, 2, 128, 128, 3),
-    (8, 2, 64, 64, 300), (4, 1, 32, 32, 20), (2, 2, 16, 16, 9),  # values staged in 256-position chunks
+@pytest.mark.parametrize("nh,nkv,hd,nrot,npos,edge", [
+    (16, 4, 256, 64, 70, False), (6, 2, 128, 128, 3, False),
+    (8, 2, 64, 64, 300, False), (4, 1, 32, 32, 20, False), (2, 2, 16, 16, 9, False),  # values staged in 256-position chunks
+    (16, 4, 256, 64, 4, True), (6, 2, 128, 128, 3, True),
 ])
-def test_attention(gq, orc, ctx, nh, nkv, hd, nrot, npos):
+def test_attention(gq, orc, ctx, nh, nkv, hd, nrot, npos, edge):
     """Attention token by token (q / k RMS norm, RoPE, fp16 cache, softmax, sigmoid gate) against the reference
-    decoder's attention (the reference's norms, ggml's CPU softmax with double sums)."""
+    decoder's attention (the reference's norms, ggml's CPU softmax with double sums); edge: q head 0 and KV head 0
+    rows whose mean squares lie on a rounding boundary at every position."""
     n_ctx = 128 if npos <= 128 else 320
     kv = ctx.kv_create(n_ctx, nkv, hd)
     qn = gq.uniform(9, 1, hd, 0.5, 1.5)
@@ -225,6 +243,9 @@ def test_attention(gq, orc, ctx, nh, nkv, hd, nrot, npos):
         qg = gq.normal(9, 100 + pos, 2 * nh * hd)
         k = gq.normal(9, 300 + pos, nkv * hd)
         v = gq.normal(9, 500 + pos, nkv * hd)
+        if edge:
+            qg[:hd] = boundary_row(hd, 3 + pos)
+            k[:hd] = boundary_row(hd, 2 * pos + 1)
         ctx.write(O["qg"], qg)
         ctx.write(O["k"], k)
         ctx.write(O["v"], v)
