@@ -118,15 +118,17 @@ __device__ __forceinline__ void unit_aux(const WK & w, const XK & x, int part, i
 // K-quant terms of row r: per super-block sb, t[9 sb + l] = d * float(aux[l]) (d = fp16 d_w * the Q8_K d) and for
 // Q5_K t[9 sb + 8] = dmin * float(sumi).
 template <int TYPE, int NU>
-__device__ __forceinline__ void row_terms_kq(const WeightView & w, int r, int nu, int lane, const XK * xk,
-                                             const uint32_t * info, float * t) {
+__device__ __forceinline__ void row_load_kq(const WeightView & w, int r, int nu, int lane, WK * wk) {
     const int nsb = nu >> 2;
-    WK wk[NU];
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
         const int u0 = lane + 64 * k, u = u0 < nu ? u0 : nu - 1;
         load_wk<TYPE>(w, size_t(r) * nsb + (u >> 2), u & 3, wk[k]);
     }
+}
+template <int TYPE, int NU>
+__device__ __forceinline__ void row_terms_kq_wk(const WK * wk, int nu, int lane, const XK * xk, const uint32_t * info,
+                                                float * t) {
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
         const int u = lane + 64 * k;
@@ -148,6 +150,13 @@ __device__ __forceinline__ void row_terms_kq(const WeightView & w, int r, int nu
             }
         }
     }
+}
+template <int TYPE, int NU>
+__device__ __forceinline__ void row_terms_kq(const WeightView & w, int r, int nu, int lane, const XK * xk,
+                                             const uint32_t * info, float * t) {
+    WK wk[NU];
+    row_load_kq<TYPE, NU>(w, r, nu, lane, wk);
+    row_terms_kq_wk<TYPE, NU>(wk, nu, lane, xk, info, t);
 }
 
 // Orders this wave's LDS writes before its later LDS reads (another lane's data); LDS keeps a wave's accesses in
@@ -186,6 +195,22 @@ __global__ __launch_bounds__(NT) void gemv_ref_kernel(GemvArgs a, int total_batc
         for (int j = 0; j < RB; ++j) {
             row_load<TYPE, NU>(m.w, r0 + min(j, n - 1), nb, lane, pre[j]);
             if constexpr (PAIR) row_load<TYPE, NU>(w2, r0 + min(j, n - 1), nb, lane, pre2[j]);
+        }
+    }
+    // ---- Q6_K of one unit per lane (up to 4096 columns; the output head's shape): each batch's rows are requested
+    // before the previous batch's terms are formed (the first batch's before the prologue), the registers holding
+    // two batches (head 166 -> 158 us at 151936 x 4096)
+    constexpr bool KPRE = TYPE == T_Q6_K && NU == 1;
+    const int bstride = gridDim.x * NWAVES;
+    WK kcur[KPRE ? RB : 1][1], knext[KPRE ? RB : 1][1];
+    if constexpr (KPRE) {
+        if (bi0 < total_batches) {
+            int mi = 0, r0 = 0;
+            locate_batch(a, bi0, mi, r0);
+            const GemvMember & m = a.m[mi];
+            const int n = min(RB, m.rows - r0);
+#pragma unroll
+            for (int j = 0; j < RB; ++j) row_load_kq<TYPE, 1>(m.w, r0 + min(j, n - 1), cols / 64, lane, kcur[j]);
         }
     }
     // ---- prologue: the activation, with the folded norm in the reference's arithmetic, quantized into LDS
@@ -270,6 +295,22 @@ __global__ __launch_bounds__(NT) void gemv_ref_kernel(GemvArgs a, int total_batc
             for (int j = 0; j < RB; ++j) {
                 row_terms_wb<TYPE, NU>(pre[j], nb, lane, xb, dx, sx, tm[wave][0][j]);
                 if (pair) row_terms_wb<TYPE, NU>(pre2[PAIR ? j : 0], nb, lane, xb, dx, sx, tm[wave][PAIR ? 1 : 0][j]);
+            }
+        } else if constexpr (KPRE) {
+            const int bn = bi + bstride;
+            if (bn < total_batches) {
+                int mn = 0, rn = 0;
+                locate_batch(a, bn, mn, rn);
+                const GemvMember & mb = a.m[mn];
+                const int nn = min(RB, mb.rows - rn);
+#pragma unroll
+                for (int j = 0; j < RB; ++j) row_load_kq<TYPE, 1>(mb.w, rn + min(j, nn - 1), nu, lane, knext[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < RB; ++j) row_terms_kq_wk<TYPE, 1>(kcur[j], nu, lane, xk, s.info, tm[wave][0][j]);
+            if (bn < total_batches) {
+#pragma unroll
+                for (int j = 0; j < RB; ++j) kcur[j][0] = knext[j][0];
             }
         } else {
 #pragma unroll
