@@ -449,6 +449,9 @@ def main() -> int:
     ap.add_argument("--ref-steps", type=int, default=32,
                     help="decode steps timed in the reference arithmetic after the profile (0: skip)")
     ap.add_argument("--layers", type=int, default=32, help="(testing) fewer layers; the reported line is then invalid")
+    ap.add_argument("--reference", action="store_true",
+                    help="(profiling) run the prompt, the timed steps and the per-kernel pass in the reference "
+                         "arithmetic (gemvq_set_arith); the line then reports that mode's rate, not the headline one")
     ap.add_argument("--direct", action="store_true",
                     help="plain stream launches instead of graph replays (for tracing tools); slower per step")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -484,6 +487,8 @@ def main() -> int:
 
     t = time.perf_counter()
     m = Q.Model(blob)
+    if args.reference:
+        m.set_arith(gq.ARITH_REFERENCE)
     log(f"uploaded and captured the per-token graph in {time.perf_counter() - t:.1f} s "
         f"({len(m.commands())} commands, weight bytes per token {wbytes})")
     m.reset(prompt[:args.prompt])
@@ -552,7 +557,7 @@ def main() -> int:
     achieved = dom["bytes"] / dom["us"] / 1e3  # GB/s
     traffic, traffic_src = measured_traffic(dom_name)
     ref = None
-    if args.ref_steps > 0 and not args.direct:
+    if args.ref_steps > 0 and not args.direct and not args.reference:
         # the same model continuing in the reference arithmetic (gemvq_set_arith): bit-identical to the reference's
         # CPU path, not the timed workload
         m.set_arith(gq.ARITH_REFERENCE)
@@ -604,6 +609,7 @@ def main() -> int:
             "launches_per_token": len(stats),
             "prompt_prefill": prefill,
             "reference_arithmetic": ref,
+            "arithmetic": "reference (gemvq_set_arith)" if args.reference else "canonical",
         },
         "roofline": {
             "bound": "hbm",
