@@ -74,3 +74,59 @@ def test_attention_8320_positions(gq, orc):
             assert_bits(y_one[t * arow:(t + 1) * arow], want, f"oracle at position {pos}")
     finally:
         ctx.close()
+
+
+def test_reference_attention_past_the_lds_scores(gq, orc):
+    """The reference-arithmetic attention past 6144 positions, where a head's scores and probabilities leave LDS for
+    its scratch row: a 6400-position cache whose history is written by batched canonical commands, then one-token
+    commands in the reference arithmetic at its last positions against the reference decoder's attention (the
+    reference's norms, double sums in order) on the cache as read back, bit for bit."""
+    nh, nkv, hd, nrot, n_ctx = 16, 4, 256, 64, 6400
+    qrow, kvrow, arow = 2 * nh * hd, nkv * hd, nh * hd
+    ctx = gq.Context(act_floats=1 << 22, weight_bytes=1 << 20, state_rows=0)
+    try:
+        O = dict(q=0, k=262144, v=294912, qn=327680, kn=327936, pos=328192, y=328704, cs=1 << 21)
+        qn = gq.uniform(3, 71, hd, 0.5, 1.5)
+        kn = gq.uniform(3, 72, hd, 0.5, 1.5)
+        table = np.concatenate([orc.rope_cache(p, nrot, 1e7) for p in range(n_ctx)])
+        ctx.write(O["qn"], qn)
+        ctx.write(O["kn"], kn)
+        ctx.write(O["cs"], table)
+        kv = ctx.kv_create(n_ctx, nkv, hd)
+
+        def attn(n_tok=1):
+            return gq.attn(nh, nkv, O["q"], kv, O["y"], hd, nrot, O["pos"], O["k"], O["v"], 1 / 16, 1e-6, O["qn"],
+                           O["kn"], O["cs"], gate=O["q"] + hd, n_tok=n_tok)
+
+        def tokens(first, n, seed):
+            qg, k, v = gq.normal(7, seed, n * qrow), gq.normal(7, seed + 1, n * kvrow), gq.normal(7, seed + 2, n * kvrow)
+            ctx.write(O["q"], qg)
+            ctx.write(O["k"], k)
+            ctx.write(O["v"], v)
+            slots = np.zeros(16 * 32, np.int32)
+            slots[0:16 * n:16] = np.arange(first, first + n)
+            ctx.write(O["pos"], slots)
+            return qg, k, v
+
+        p_end = n_ctx - 32
+        for b0 in range(0, p_end, 32):
+            if b0 % 2048 == 0:
+                print(f"[ref attn long] history at {b0}", flush=True)
+            tokens(b0, 32, 2000 + b0)
+            assert ctx.run(attn(32)) == 0, ctx.error()
+        ctx.set_arith(gq.ARITH_REFERENCE)
+        for pos in (p_end, p_end + 1, n_ctx - 1):
+            print(f"[ref attn long] reference arithmetic at {pos}", flush=True)
+            qg, k, v = tokens(pos, 1, 99 + pos)
+            assert ctx.run(attn()) == 0, ctx.error()
+            kc, vc = ctx.kv_read(kv, 0, pos + 1, kvrow)
+            kc, vc = kc.reshape(pos + 1, nkv, hd), vc.reshape(pos + 1, nkv, hd)
+            cs = table[pos * nrot:(pos + 1) * nrot]
+            kh = orc.rope(orc.ref_rownorm(k, kn, hd, nkv, 1e-6), cs, nrot, hd, nkv)
+            assert np.array_equal(kc[pos], orc.f2h(kh).reshape(nkv, hd)), f"stored key at {pos}"
+            qh = orc.rope(orc.ref_rownorm(qg.reshape(nh, 2 * hd)[:, :hd].ravel(), qn, hd, nh, 1e-6), cs, nrot, hd, nh)
+            att = orc.ref_attn_cr(qh, kc, vc, nh, nkv, hd, pos + 1, 1 / 16)
+            gate = qg.reshape(nh, 2 * hd)[:, hd:].ravel()
+            assert_bits(ctx.read(O["y"], arow), orc.ref_unary_cr(gate, 2) * att, f"reference attention at {pos}")
+    finally:
+        ctx.close()
