@@ -347,6 +347,10 @@ class BatchModel:
     def step(self, n: int = 1) -> None:
         self._ok(self.lib.gemvq_qwen35_step(self.h, n), "batch step")
 
+    def set_arith(self, arith: int) -> None:
+        """gq.ARITH_REFERENCE: the following steps in the reference's CPU arithmetic (gemvq_qwen35_set_arith)."""
+        self._ok(self.lib.gemvq_qwen35_set_arith(self.h, arith), "batch set arith")
+
     def sync(self) -> None:
         self.ctx.sync()
 

@@ -74,8 +74,10 @@ int gemvq_qwen35_set_arith(gemvq_qwen35 * m, int arith);
  * logits are those of a single-sequence model decoding its prompt, bit for bit. Prompts are consumed by the same
  * steps (a sequence takes its next prompt token while it has one, then its argmax). Layer projections must have a
  * batched form (Q4_0 / Q4_1 / Q8_0, columns a multiple of 512); a head of another type runs one GEMV per sequence.
- * gemvq_qwen35_batch_sizes gives the context sizes; gemvq_qwen35_step, _commands, _graph and _destroy apply to the
- * batch model, the single-sequence _reset, _prefill, _tokens, _logits and _hidden return GEMVQ_EINVAL for it
+ * gemvq_qwen35_batch_sizes gives the context sizes; gemvq_qwen35_step, _set_arith, _commands, _graph and _destroy
+ * apply to the batch model (in the reference arithmetic each sequence's ids and logits are those of a
+ * single-sequence model decoding in it), the single-sequence _reset, _prefill, _tokens, _logits and _hidden return
+ * GEMVQ_EINVAL for it
  * (gemvq_qwen35_batch_create with n_seq 1 is gemvq_qwen35_create). */
 int gemvq_qwen35_batch_sizes(const gemvq_qw_config * cfg, const gemvq_tensor_desc * table, int n_tensors, int n_seq,
                              size_t * act_floats, size_t * weight_bytes, size_t * state_rows);

@@ -55,6 +55,38 @@ def test_lockstep_sequences_equal_single_decodes(gq, q35, n_seq, head, steps):
             assert np.array_equal(want[:min(lens[s], steps + 1)], prompts[s][:min(lens[s], steps + 1)])
 
 
+@pytest.mark.parametrize("n_seq,head", [(3, "q8_0"), (5, "q6_k")])
+def test_lockstep_sequences_in_reference_arithmetic(gq, q35, n_seq, head):
+    """The batch model in the reference arithmetic (its GEMMs as token GEMVs, the sequences forms of CONV, the
+    DeltaNet step and attention token by token): every sequence's ids and last logits equal a single-sequence model's
+    decode of its prompt in the reference arithmetic, bit for bit."""
+    cfg = small()
+    types = {"output.weight": gq.Q8_0} if head == "q8_0" else None
+    blob = q35.generate(cfg, seed=21, types=types)
+    rng = np.random.default_rng(30 + n_seq)
+    lens = [int(v) for v in rng.integers(1, 10, n_seq)]
+    prompts = [rng.integers(0, cfg.n_vocab, L).astype(np.int32) for L in lens]
+    steps = 12
+    print(f"[batch ref] {n_seq} sequences, prompts {lens}, {steps} steps, {head} head", flush=True)
+    with q35.BatchModel(blob, n_seq) as bm:
+        bm.reset(prompts)
+        bm.step(steps)
+        canonical = [bm.logits(s) for s in range(n_seq)]
+        bm.set_arith(gq.ARITH_REFERENCE)
+        bm.reset(prompts)
+        bm.step(steps)
+        got = [(bm.tokens(s, steps + 1), bm.logits(s)) for s in range(n_seq)]
+    # the mode took effect: the two arithmetics' logits differ in their low bits
+    assert any(not np.array_equal(c.view(np.uint32), g[1].view(np.uint32)) for c, g in zip(canonical, got))
+    with q35.Model(blob) as m:
+        m.set_arith(gq.ARITH_REFERENCE)
+        for s in range(n_seq):
+            m.reset(prompts[s])
+            m.step(steps)
+            assert np.array_equal(got[s][0], m.tokens(steps + 1)), f"sequence {s}"
+            assert np.array_equal(got[s][1].view(np.uint32), m.logits().view(np.uint32)), f"sequence {s} logits"
+
+
 def test_batch_model_rejects_single_sequence_calls(gq, q35):
     cfg = small(n_layer=4, n_ctx=32)
     blob = q35.generate(cfg, seed=13)
