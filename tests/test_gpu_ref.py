@@ -34,6 +34,7 @@ def test_correctly_rounded_math_on_every_input(gq, orc, ctx, fn):
     (2, 300, 2560), (2, 64, 12288), (2, 129, 512), (8, 257, 2560), (8, 40, 16384), (3, 200, 4096),
     (14, 301, 4096), (14, 33, 12288), (13, 130, 4096), (13, 50, 2048),
     (2, 37, 96), (8, 70, 2592), (3, 11, 160), (8, 9, 32),  # odd numbers of 32-column blocks
+    (14, 36000, 4096),  # Q6_K rows enough for several batches per wave (each requested before the one before is added)
 ])
 def test_gemv_rows(gq, orc, ctx, t, rows, cols):
     """GEMV rows in every weight format equal gemvq_ref.h's sequential FP32 rows (orc_ref_gemv, itself pinned to
