@@ -215,14 +215,6 @@ __device__ __forceinline__ float mul_f16(float x, uint32_t h) {
     else asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(x), "v"(h));
     return r;
 }
-// The same with x a wave-uniform value in a scalar register (no copy into a vector register first).
-template <int HI>
-__device__ __forceinline__ float mul_f16_s(float x, uint32_t h) {
-    float r;
-    if constexpr (HI) asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "s"(x), "v"(h));
-    else asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(r) : "s"(x), "v"(h));
-    return r;
-}
 
 // The scores of positions p0 + 256 g (g < G; positions at or past n read row n - 1 and store nothing).
 template <int HD, int G>
@@ -261,7 +253,7 @@ __device__ __forceinline__ void attn_ref_scores(const AttnArgs & a, const AttnTo
                 for (int g = 0; g < G; ++g) {
                     const uint4 & x = w[s & 1][g][i];
                     const uint32_t u = (j >> 1) == 0 ? x.x : (j >> 1) == 1 ? x.y : (j >> 1) == 2 ? x.z : x.w;
-                    const float pr = (j & 1) ? mul_f16_s<1>(qd, u) : mul_f16_s<0>(qd, u);  // q * k, exact
+                    const float pr = (j & 1) ? mul_f16<1>(qd, u) : mul_f16<0>(qd, u);  // q * k, exact
                     acc[g] += double(pr);
                 }
             }
